@@ -1,0 +1,181 @@
+/*
+ * kfhip.h — C ABI of the MI355X (gfx950) fused KAN basis kernels.
+ *
+ * One shared library, libkfhip.so, built from kanforge_amd/csrc/*.hip. The
+ * entry points below replace the reference's raw launcher
+ *   kanforge/torch/kernels.py:39-55   _raw(op, plan, m, x, a, b, grid, n_out, nf)
+ *   kanforge/kernels/triton_kernels.py:225-242   launch(op, ...)
+ * op "F" -> kf_F, "G" -> kf_G, "P" -> kf_P, plus entry points for what the
+ * reference computes with plain ops on this path (basis evaluation,
+ * edge_derivative, the group-rational parameter gradients).
+ *
+ * Conventions
+ *  - All array arguments are DEVICE pointers to dense row-major arrays
+ *    (no strides); the caller owns every buffer. The library never
+ *    allocates, frees or synchronises.
+ *  - Work that needs scratch memory takes a caller-provided workspace of at
+ *    least kf_workspace_bytes(...) bytes (256-byte aligned).
+ *  - `stream` is a hipStream_t (passed as void*); every launch is ordered on it.
+ *  - Return value: 0 on success, a negative KF_E* code otherwise; the text
+ *    of the last error of the calling thread is kf_last_error().
+ *  - x, w, coefficients, upstream gradients and outputs of one call share
+ *    one dtype (kf_dtype). Accumulation is float32.
+ */
+#ifndef KFHIP_H
+#define KFHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define KF_OK 0
+#define KF_EINVAL -1     /* bad argument (shape, null pointer, unsupported combination) */
+#define KF_EWORKSPACE -2 /* workspace missing or too small */
+#define KF_ELAUNCH -3    /* a HIP launch failed */
+#define KF_EUNSUPPORTED -4
+
+/* element types */
+#define KF_F32 0
+#define KF_BF16 1
+
+/* basis kinds (kanforge/kernels/plan.py:39-45 KernelPlan.kind, plus rational) */
+#define KF_KIND_CHEB 0     /* T_j(g(x)) features, g = tanh or identity; derivatives folded */
+#define KF_KIND_BSPLINE 1  /* B-splines on a per-input knot vector; derivative order native */
+#define KF_KIND_RATIONAL 2 /* P(x)/(1+|Q(x)|), parameters shared by groups of inputs */
+
+/* input maps of the Chebyshev family (kanforge/bases/polynomial.py:66-85) */
+#define KF_MAP_IDENTITY 0
+#define KF_MAP_TANH 1
+
+#define KF_MAX_K 16   /* basis functions per edge */
+#define KF_MAX_NT 24  /* kernel features per edge (K + derivative order for tanh maps) */
+
+/*
+ * What one input's kernel features are. Mirrors KernelPlan
+ * (kanforge/kernels/plan.py:39-72): kind, consts, size, and the fold matrix
+ * R_m (plan.py:75-101) that maps kernel features to the m-th derivative of
+ * the basis functions.
+ *
+ *  cheb:     features T_0..T_{n_t-1}(g(x)); `fold` is R_m (size x n_t,
+ *            row-major, HOST pointer, copied into the launch) so that
+ *            phi_k^(m) = sum_j fold[k][j] T_j.  n_t = size + m (tanh) or size.
+ *  bspline:  features are the m-th derivatives of the `size` = G + k
+ *            B-splines of degree `spline_k` on per-input knots.
+ *            knots:     (n_in, n_knots + 2*spline_k) float32, the real knots
+ *                       padded by spline_k strictly increasing knots per side.
+ *            knots_cmp: (n_in, n_knots) float32, each real float64 knot
+ *                       rounded toward +inf; x >= t64 <=> x >= ceil32(t64) for
+ *                       every float32 x, so interval search is exact.
+ *  rational: one feature, the m-th derivative of P/(1+|Q|),
+ *            P = sum_{j<=num_deg} num[g][j] x^j, Q = sum_{1<=j<=den_deg} den[g][j-1] x^j,
+ *            g = input / group_size. num (groups, num_deg+1), den (groups, den_deg),
+ *            float32 device arrays.
+ */
+typedef struct kf_basis {
+  int32_t kind;
+  int32_t size;      /* K: basis functions per input */
+  int32_t order;     /* m: derivative order of the features */
+  int32_t n_t;       /* kernel features per input (n_t == size unless cheb+tanh) */
+  int32_t input_map; /* cheb */
+  int32_t spline_k;  /* bspline degree */
+  int32_t n_knots;   /* bspline real knots per input (G + 2k + 1) */
+  int32_t num_deg;   /* rational */
+  int32_t den_deg;
+  int32_t group_size;
+  const float *fold;      /* cheb, host */
+  const float *knots;     /* bspline, device */
+  const float *knots_cmp; /* bspline, device */
+  const float *num;       /* rational, device */
+  const float *den;       /* rational, device */
+} kf_basis;
+
+/* operation ids for kf_workspace_bytes */
+#define KF_OP_F 0
+#define KF_OP_G 1
+#define KF_OP_P 2
+
+/*
+ * Scratch bytes kf_F / kf_G / kf_P need for these shapes (0 is possible).
+ * Replaces nothing in the reference (Triton allocates implicitly).
+ */
+size_t kf_workspace_bytes(int op, const kf_basis *basis, int dtype, int64_t batch, int64_t n_in, int64_t n_out);
+
+/*
+ * y[b,o] = sum_{i,k} w[b,i] c[o,i,k] phi_k^(m)(x[b,i])          (op "F")
+ * x (batch, n_in); w (batch, n_in) or NULL for ones; c (n_out, n_in, size);
+ * y (batch, n_out).  Replaces _raw("F", ...) (kanforge/torch/kernels.py:77)
+ * together with the fold c @ R_m (kanforge/torch/kernels.py:75-76).
+ */
+int kf_F(const kf_basis *basis, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void *x,
+         const void *w, const void *c, void *y, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * dc[o,i,k] = sum_b w[b,i] g[b,o] phi_k^(m)(x[b,i])              (op "G")
+ * g (batch, n_out); dc (n_out, n_in, size). Replaces _raw("G", ...) and the
+ * fold gt @ R_m^T (kanforge/torch/kernels.py:95-98).
+ */
+int kf_G(const kf_basis *basis, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void *x,
+         const void *g, const void *w, void *dc, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * p[b,i] = sum_{o,k} g[b,o] c[o,i,k] phi_k^(m)(x[b,i])            (op "P")
+ * Replaces _raw("P", ...) (kanforge/torch/kernels.py:118). If h is not NULL,
+ * also writes h[b,i] = sum_o g[b,o] c[o,i,0] as float32 (rational kind,
+ * size 1: the input of kf_rational_param_grad).
+ */
+int kf_P(const kf_basis *basis, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void *x,
+         const void *g, const void *c, void *p, float *h, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * phi[b,i,k] = phi_k^(m)(x[b,i]), out (batch, n_in, size) in dtype.
+ * Replaces Basis.derivative (kanforge/bases/base.py:79-85) for the kinds above.
+ */
+int kf_features(const kf_basis *basis, int dtype, int64_t batch, int64_t n_in, const void *x, void *out,
+                void *stream);
+
+/*
+ * d[b,o,i] = sum_k c[o,i,k] phi_k^(m)(x[b,i]) + base_w[o,i] silu^(m)(x[b,i])
+ * out (batch, n_out, n_in); base_w may be NULL (no base branch).
+ * Replaces KANLinear.edge_derivative (kanforge/torch/layers.py:206-226).
+ * `c` holds the basis coefficients (n_out, n_in, size), not a folded copy.
+ */
+int kf_edge_derivative(const kf_basis *basis, int dtype, int64_t batch, int64_t n_in, int64_t n_out,
+                       const void *x, const void *c, const void *base_w, void *out, void *stream);
+
+/*
+ * Interval index j with knots[i][j] <= x[b,i] < knots[i][j+1] (float64
+ * knots, compared exactly through the ceil32 table), -1 outside.
+ * x float32 (batch, n_in); idx int32 (batch, n_in). This is the level-0
+ * indicator of kanforge/bases/spline.py:80.
+ */
+int kf_bspline_interval(int64_t batch, int64_t n_in, const float *x, const float *knots_cmp, int32_t n_knots,
+                        int32_t *idx, void *stream);
+
+/*
+ * Gradients of sum_{b,i} h[b,i] w[b,i] phi(x[b,i]) with respect to the
+ * rational parameters: dnum (groups, num_deg+1), dden (groups, den_deg),
+ * float32, overwritten. h float32 (batch, n_in) from kf_P; w may be NULL.
+ * What autograd computes through Rational._eval (kanforge/bases/rational.py:84-101).
+ * Needs kf_workspace_bytes-independent scratch: workspace of
+ * kf_rational_workspace_bytes(...) bytes.
+ */
+size_t kf_rational_workspace_bytes(const kf_basis *basis, int64_t batch, int64_t n_in);
+int kf_rational_param_grad(const kf_basis *basis, int dtype, int64_t batch, int64_t n_in, const void *x,
+                           const float *h, const void *w, float *dnum, float *dden, void *workspace,
+                           size_t workspace_bytes, void *stream);
+
+/* Text of the last error on the calling thread ("" if none). */
+const char *kf_last_error(void);
+
+/* Library version string, e.g. "kfhip 0.1.0 gfx950". */
+const char *kf_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KFHIP_H */

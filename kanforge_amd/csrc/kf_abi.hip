@@ -1,0 +1,522 @@
+// extern "C" entry points of libkfhip.so (declared in include/kfhip.h):
+// argument validation, workspace carving and kernel dispatch.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "kf_kernels.h"
+
+using namespace kf;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(KF_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
+  return KF_OK;
+}
+
+inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+inline int elt_size(int dtype) { return dtype == KF_BF16 ? 2 : 4; }
+
+// tile constants shared by workspace sizing and launches
+constexpr int F_BM = 128, F_BN = 128;
+constexpr int P_BM = 128;
+constexpr int G_BM = 128, G_BC = 64;
+constexpr int CHUNK = 32;
+
+int validate_basis(const kf_basis* b) {
+  if (!b) return fail(KF_EINVAL, "basis descriptor is NULL");
+  if (b->size < 1 || b->size > KF_MAX_K) return fail(KF_EINVAL, "basis size %d outside [1, %d]", b->size, KF_MAX_K);
+  if (b->order < 0 || b->order > 8) return fail(KF_EUNSUPPORTED, "derivative order %d outside [0, 8]", b->order);
+  if (b->n_t < 1 || b->n_t > KF_MAX_NT) return fail(KF_EINVAL, "n_t %d outside [1, %d]", b->n_t, KF_MAX_NT);
+  switch (b->kind) {
+    case KF_KIND_CHEB:
+      if (!b->fold) return fail(KF_EINVAL, "cheb basis needs the fold matrix");
+      if (b->input_map != KF_MAP_TANH && b->input_map != KF_MAP_IDENTITY)
+        return fail(KF_EINVAL, "unknown input map %d", b->input_map);
+      break;
+    case KF_KIND_BSPLINE:
+      if (b->spline_k < 0 || b->spline_k > 5) return fail(KF_EUNSUPPORTED, "B-spline degree %d outside [0, 5]", b->spline_k);
+      if (b->n_knots != b->size + b->spline_k + 1)
+        return fail(KF_EINVAL, "n_knots %d != size + degree + 1 = %d", b->n_knots, b->size + b->spline_k + 1);
+      if (b->n_t != b->size) return fail(KF_EINVAL, "bspline n_t must equal size");
+      if (!b->knots || !b->knots_cmp) return fail(KF_EINVAL, "bspline basis needs knot tables");
+      break;
+    case KF_KIND_RATIONAL:
+      if (b->size != 1 || b->n_t != 1) return fail(KF_EINVAL, "rational basis has size 1");
+      if (b->num_deg < 0 || b->den_deg < 1 || b->num_deg + 1 + b->den_deg > kRatMaxParams)
+        return fail(KF_EUNSUPPORTED, "rational degrees (%d, %d) unsupported", b->num_deg, b->den_deg);
+      if (!b->num || !b->den) return fail(KF_EINVAL, "rational basis needs num/den");
+      if (b->group_size < 1) return fail(KF_EINVAL, "group_size must be >= 1");
+      break;
+    default:
+      return fail(KF_EINVAL, "unknown basis kind %d", b->kind);
+  }
+  return KF_OK;
+}
+
+int validate_common(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out) {
+  int rc = validate_basis(b);
+  if (rc) return rc;
+  if (dtype != KF_F32 && dtype != KF_BF16) return fail(KF_EINVAL, "unsupported dtype %d", dtype);
+  if (batch < 0 || n_in < 0 || n_out < 0) return fail(KF_EINVAL, "negative dimension");
+  if (batch > (1LL << 31) - 1024 || n_in > (1 << 24) || n_out > (1 << 24))
+    return fail(KF_EINVAL, "dimension too large");
+  if (b->kind == KF_KIND_RATIONAL && n_in % b->group_size)
+    return fail(KF_EINVAL, "group_size %d does not divide n_in %lld", b->group_size, (long long)n_in);
+  return KF_OK;
+}
+
+KBasis to_kbasis(const kf_basis* b) {
+  KBasis k;
+  memset(&k, 0, sizeof(k));
+  k.kind = b->kind;
+  k.K = b->size;
+  k.n_t = b->n_t;
+  k.order = b->order;
+  k.input_map = b->input_map;
+  k.spline_k = b->spline_k;
+  k.n_knots = b->n_knots;
+  k.num_deg = b->num_deg;
+  k.den_deg = b->den_deg;
+  k.group_size = b->group_size > 0 ? b->group_size : 1;
+  k.knots = b->knots;
+  k.knots_cmp = b->knots_cmp;
+  k.num = b->num;
+  k.den = b->den;
+  if (b->kind == KF_KIND_CHEB) {
+    for (int r = 0; r < b->size; ++r)
+      for (int c = 0; c < b->n_t; ++c) k.fold[r * KF_MAX_NT + c] = b->fold[r * b->n_t + c];
+  } else {
+    for (int r = 0; r < b->size; ++r) k.fold[r * KF_MAX_NT + r] = 1.f;  // identity
+  }
+  return k;
+}
+
+int nt_bucket(int n) { return n <= 4 ? 4 : n <= 8 ? 8 : n <= 12 ? 12 : n <= 16 ? 16 : 24; }
+
+struct WsF {
+  int64_t INP, OUTP, BP;
+  size_t cfm, phi, total;
+};
+WsF ws_f(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out) {
+  WsF w;
+  w.INP = round_up(n_in, CHUNK);
+  w.OUTP = round_up(n_out, F_BN);
+  w.BP = round_up(batch, F_BM);
+  const int es = elt_size(dtype);
+  w.cfm = align256((size_t)b->n_t * w.OUTP * w.INP * es);
+  w.phi = b->kind == KF_KIND_CHEB ? 0 : align256((size_t)w.BP * b->n_t * w.INP * es);
+  w.total = w.cfm + w.phi;
+  return w;
+}
+struct WsP {
+  int64_t INP, OUTP;
+  size_t cfmt, total;
+};
+WsP ws_p(const kf_basis* b, int dtype, int64_t n_in, int64_t n_out) {
+  WsP w;
+  w.INP = round_up(n_in, 16);
+  w.OUTP = round_up(n_out, 32);
+  w.cfmt = align256((size_t)b->n_t * w.INP * w.OUTP * elt_size(dtype));
+  w.total = w.cfmt;
+  return w;
+}
+struct WsG {
+  int64_t OUTP, BP;
+  size_t gt, total;
+};
+WsG ws_g(int dtype, int64_t batch, int64_t n_out) {
+  WsG w;
+  w.OUTP = round_up(n_out, G_BM);
+  w.BP = round_up(batch, G_BC);
+  w.gt = align256((size_t)w.OUTP * w.BP * elt_size(dtype));
+  w.total = w.gt;
+  return w;
+}
+
+template <typename T>
+__global__ void fill_zero_kernel(T* p, long n) {
+  for (long e = blockIdx.x * (long)blockDim.x + threadIdx.x; e < n; e += (long)gridDim.x * blockDim.x) p[e] = T(0.f);
+}
+
+template <typename T>
+int zero_fill(void* p, long n, hipStream_t s) {
+  if (n <= 0) return KF_OK;
+  long blocks = (n + 255) / 256;
+  if (blocks > 65535) blocks = 65535;
+  hipLaunchKernelGGL(fill_zero_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, s, (T*)p, n);
+  return check_launch("fill");
+}
+
+// permute (and fold) coefficients into a feature-major workspace layout
+template <typename T>
+int launch_permute(const KBasis& kb, int64_t n_out, int64_t n_in, int64_t OUTP, int64_t INP, const void* c, void* out,
+                   bool fmt, hipStream_t s) {
+  dim3 grid((unsigned)((OUTP + 31) / 32), (unsigned)((INP + 15) / 16));
+  size_t lds = (size_t)kb.n_t * 16 * 33 * sizeof(float);
+  if (fmt)
+    hipLaunchKernelGGL((permute_coef_kernel<T, true>), grid, dim3(kThreads), lds, s, kb, (int)n_out, (int)n_in,
+                       (int)OUTP, (int)INP, (const T*)c, (T*)out);
+  else
+    hipLaunchKernelGGL((permute_coef_kernel<T, false>), grid, dim3(kThreads), lds, s, kb, (int)n_out, (int)n_in,
+                       (int)OUTP, (int)INP, (const T*)c, (T*)out);
+  return check_launch("permute_coef");
+}
+
+template <typename T, int NTB, bool FOLDED>
+void launch_features_t(const KBasis& kb, int64_t batch, int64_t n_in, int64_t brows, int64_t icols, const void* x,
+                       void* out, long sb, long sj, long si, bool b_fastest, hipStream_t s) {
+  long n = (long)brows * icols;
+  long blocks = (n + kThreads - 1) / kThreads;
+  if (blocks > 65535 * 4) blocks = 65535 * 4;
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL((features_kernel<T, NTB, FOLDED>), dim3((unsigned)blocks), dim3(kThreads), 0, s, kb, (int)batch,
+                     (int)n_in, (int)brows, (int)icols, (const T*)x, (T*)out, sb, sj, si, b_fastest);
+}
+
+template <typename T, bool FOLDED>
+int launch_features(const KBasis& kb, int64_t batch, int64_t n_in, int64_t brows, int64_t icols, const void* x,
+                    void* out, long sb, long sj, long si, bool b_fastest, hipStream_t s) {
+  const int nb = nt_bucket(FOLDED ? (kb.kind == KF_KIND_CHEB ? kb.n_t : kb.K) : kb.n_t);
+  switch (nb) {
+    case 4: launch_features_t<T, 4, FOLDED>(kb, batch, n_in, brows, icols, x, out, sb, sj, si, b_fastest, s); break;
+    case 8: launch_features_t<T, 8, FOLDED>(kb, batch, n_in, brows, icols, x, out, sb, sj, si, b_fastest, s); break;
+    case 12: launch_features_t<T, 12, FOLDED>(kb, batch, n_in, brows, icols, x, out, sb, sj, si, b_fastest, s); break;
+    case 16: launch_features_t<T, 16, FOLDED>(kb, batch, n_in, brows, icols, x, out, sb, sj, si, b_fastest, s); break;
+    default: launch_features_t<T, 24, FOLDED>(kb, batch, n_in, brows, icols, x, out, sb, sj, si, b_fastest, s); break;
+  }
+  return check_launch("features");
+}
+
+template <typename T>
+int run_F(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
+          const void* w, const void* c, void* y, void* ws, hipStream_t s) {
+  WsF L = ws_f(b, dtype, batch, n_in, n_out);
+  char* base = (char*)ws;
+  void* cfm = base;
+  void* phi = base + L.cfm;
+  int rc = launch_permute<T>(kb, n_out, n_in, L.OUTP, L.INP, c, cfm, false, s);
+  if (rc) return rc;
+  dim3 grid((unsigned)(L.OUTP / F_BN), (unsigned)(L.BP / F_BM));
+  if (kb.kind == KF_KIND_CHEB) {
+    if (w) return fail(KF_EUNSUPPORTED, "internal: weighted cheb F handled by the generator");
+    hipLaunchKernelGGL((f_kernel<T, F_BM, F_BN, 2, 2, true>), grid, dim3(kThreads), 0, s, kb, (int)batch, (int)n_in,
+                       (int)n_out, (int)L.INP, (int)L.OUTP, (const T*)x, (const T*)nullptr, (const T*)cfm,
+                       (const T*)nullptr, (T*)y);
+  } else {
+    // phi_fm[b][j][i] (BP, n_t, INP), features already multiplied by w when given
+    rc = launch_features<T, false>(kb, batch, n_in, L.BP, L.INP, x, phi, (long)kb.n_t * L.INP, (long)L.INP, 1L,
+                                   false, s);
+    if (rc) return rc;
+    hipLaunchKernelGGL((f_kernel<T, F_BM, F_BN, 2, 2, false>), grid, dim3(kThreads), 0, s, kb, (int)batch,
+                       (int)n_in, (int)n_out, (int)L.INP, (int)L.OUTP, (const T*)x, (const T*)nullptr,
+                       (const T*)cfm, (const T*)phi, (T*)y);
+  }
+  return check_launch("F");
+}
+
+}  // namespace
+
+// weighted F: the generator multiplies by w; non-cheb kinds multiply the
+// precomputed features (a separate small kernel).
+namespace kf {
+template <typename T>
+__global__ __launch_bounds__(kThreads) void scale_phi_kernel(int B, int IN, int n_t, int INP, const T* __restrict__ w,
+                                                             T* __restrict__ phi) {
+  const long n = (long)B * n_t * INP;
+  for (long e = blockIdx.x * (long)kThreads + threadIdx.x; e < n; e += (long)gridDim.x * kThreads) {
+    const int i = (int)(e % INP);
+    const int b = (int)(e / ((long)n_t * INP));
+    if (i < IN) phi[e] = from_f32<T>(to_f32(phi[e]) * to_f32(w[(size_t)b * IN + i]));
+  }
+}
+}  // namespace kf
+
+namespace {
+template <typename T>
+int run_F_weighted(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out,
+                   const void* x, const void* w, const void* c, void* y, void* ws, hipStream_t s) {
+  WsF L = ws_f(b, dtype, batch, n_in, n_out);
+  char* base = (char*)ws;
+  void* cfm = base;
+  int rc = launch_permute<T>(kb, n_out, n_in, L.OUTP, L.INP, c, cfm, false, s);
+  if (rc) return rc;
+  dim3 grid((unsigned)(L.OUTP / F_BN), (unsigned)(L.BP / F_BM));
+  if (kb.kind == KF_KIND_CHEB) {
+    hipLaunchKernelGGL((f_kernel<T, F_BM, F_BN, 2, 2, true>), grid, dim3(kThreads), 0, s, kb, (int)batch, (int)n_in,
+                       (int)n_out, (int)L.INP, (int)L.OUTP, (const T*)x, (const T*)w, (const T*)cfm,
+                       (const T*)nullptr, (T*)y);
+  } else {
+    void* phi = base + L.cfm;
+    rc = launch_features<T, false>(kb, batch, n_in, L.BP, L.INP, x, phi, (long)kb.n_t * L.INP, (long)L.INP, 1L,
+                                   false, s);
+    if (rc) return rc;
+    long n = (long)batch * kb.n_t * L.INP;
+    long blocks = (n + kThreads - 1) / kThreads;
+    if (blocks > 65535 * 4) blocks = 65535 * 4;
+    if (blocks > 0)
+      hipLaunchKernelGGL(scale_phi_kernel<T>, dim3((unsigned)blocks), dim3(kThreads), 0, s, (int)batch, (int)n_in,
+                         kb.n_t, (int)L.INP, (const T*)w, (T*)phi);
+    rc = check_launch("scale_phi");
+    if (rc) return rc;
+    hipLaunchKernelGGL((f_kernel<T, F_BM, F_BN, 2, 2, false>), grid, dim3(kThreads), 0, s, kb, (int)batch,
+                       (int)n_in, (int)n_out, (int)L.INP, (int)L.OUTP, (const T*)x, (const T*)nullptr,
+                       (const T*)cfm, (const T*)phi, (T*)y);
+  }
+  return check_launch("F");
+}
+
+template <typename T, int NTB>
+void launch_p_t(const KBasis& kb, dim3 grid, hipStream_t s, int64_t batch, int64_t n_in, int64_t n_out, int64_t INP,
+                int64_t OUTP, const void* x, const void* g, const void* cfmt, void* p, float* h) {
+  hipLaunchKernelGGL((p_kernel<T, NTB, P_BM>), grid, dim3(kThreads), 0, s, kb, (int)batch, (int)n_in, (int)n_out,
+                     (int)INP, (int)OUTP, (const T*)x, (const T*)g, (const T*)cfmt, (T*)p, h);
+}
+
+template <typename T>
+int run_P(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
+          const void* g, const void* c, void* p, float* h, void* ws, hipStream_t s) {
+  WsP L = ws_p(b, dtype, n_in, n_out);
+  void* cfmt = ws;
+  int rc = launch_permute<T>(kb, n_out, n_in, L.OUTP, L.INP, c, cfmt, true, s);
+  if (rc) return rc;
+  dim3 grid((unsigned)(L.INP / 16), (unsigned)((batch + P_BM - 1) / P_BM));
+  switch (nt_bucket(kb.n_t)) {
+    case 4: launch_p_t<T, 4>(kb, grid, s, batch, n_in, n_out, L.INP, L.OUTP, x, g, cfmt, p, h); break;
+    case 8: launch_p_t<T, 8>(kb, grid, s, batch, n_in, n_out, L.INP, L.OUTP, x, g, cfmt, p, h); break;
+    case 12: launch_p_t<T, 12>(kb, grid, s, batch, n_in, n_out, L.INP, L.OUTP, x, g, cfmt, p, h); break;
+    case 16: launch_p_t<T, 16>(kb, grid, s, batch, n_in, n_out, L.INP, L.OUTP, x, g, cfmt, p, h); break;
+    default: launch_p_t<T, 24>(kb, grid, s, batch, n_in, n_out, L.INP, L.OUTP, x, g, cfmt, p, h); break;
+  }
+  return check_launch("P");
+}
+
+template <typename T, int NTB>
+void launch_g_t(const KBasis& kb, dim3 grid, hipStream_t s, int64_t batch, int64_t n_in, int64_t n_out, int64_t BP,
+                int64_t OUTP, const void* x, const void* w, const void* gt, void* dc) {
+  hipLaunchKernelGGL((g_kernel<T, NTB, G_BM>), grid, dim3(kThreads), 0, s, kb, (int)batch, (int)n_in, (int)n_out,
+                     (int)BP, (int)OUTP, (const T*)x, (const T*)w, (const T*)gt, (T*)dc);
+}
+
+template <typename T>
+int run_G(const KBasis& kb, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* g,
+          const void* w, void* dc, void* ws, hipStream_t s) {
+  WsG L = ws_g(dtype, batch, n_out);
+  void* gt = ws;
+  dim3 tg((unsigned)((L.OUTP + 63) / 64), (unsigned)((L.BP + 63) / 64));
+  hipLaunchKernelGGL(transpose_kernel<T>, tg, dim3(kThreads), 0, s, (int)batch, (int)n_out, (int)L.BP, (int)L.OUTP,
+                     (const T*)g, (T*)gt);
+  int rc = check_launch("transpose");
+  if (rc) return rc;
+  dim3 grid((unsigned)((n_in + 15) / 16), (unsigned)(L.OUTP / G_BM));
+  switch (nt_bucket(kb.n_t)) {
+    case 4: launch_g_t<T, 4>(kb, grid, s, batch, n_in, n_out, L.BP, L.OUTP, x, w, gt, dc); break;
+    case 8: launch_g_t<T, 8>(kb, grid, s, batch, n_in, n_out, L.BP, L.OUTP, x, w, gt, dc); break;
+    case 12: launch_g_t<T, 12>(kb, grid, s, batch, n_in, n_out, L.BP, L.OUTP, x, w, gt, dc); break;
+    case 16: launch_g_t<T, 16>(kb, grid, s, batch, n_in, n_out, L.BP, L.OUTP, x, w, gt, dc); break;
+    default: launch_g_t<T, 24>(kb, grid, s, batch, n_in, n_out, L.BP, L.OUTP, x, w, gt, dc); break;
+  }
+  return check_launch("G");
+}
+
+template <typename T, int KM>
+void launch_edge_t(const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* c,
+                   const void* bw, void* out, hipStream_t s) {
+  dim3 grid((unsigned)((n_in + 63) / 64), (unsigned)((batch + 7) / 8));
+  hipLaunchKernelGGL((edge_kernel<T, KM>), grid, dim3(kThreads), 0, s, kb, (int)batch, (int)n_in, (int)n_out,
+                     (const T*)x, (const T*)c, (const T*)bw, (T*)out);
+}
+
+template <typename T>
+int run_edge(const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* c,
+             const void* bw, void* out, hipStream_t s) {
+  switch (nt_bucket(kb.K)) {
+    case 4: launch_edge_t<T, 4>(kb, batch, n_in, n_out, x, c, bw, out, s); break;
+    case 8: launch_edge_t<T, 8>(kb, batch, n_in, n_out, x, c, bw, out, s); break;
+    case 12: launch_edge_t<T, 12>(kb, batch, n_in, n_out, x, c, bw, out, s); break;
+    default: launch_edge_t<T, 16>(kb, batch, n_in, n_out, x, c, bw, out, s); break;
+  }
+  return check_launch("edge_derivative");
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* kf_last_error(void) { return g_err.c_str(); }
+
+const char* kf_version(void) { return "kfhip 0.1.0 gfx950"; }
+
+size_t kf_workspace_bytes(int op, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out) {
+  if (validate_common(b, dtype, batch, n_in, n_out)) return 0;
+  switch (op) {
+    case KF_OP_F: return ws_f(b, dtype, batch, n_in, n_out).total;
+    case KF_OP_P: return ws_p(b, dtype, n_in, n_out).total;
+    case KF_OP_G: return ws_g(dtype, batch, n_out).total;
+    default: return 0;
+  }
+}
+
+int kf_F(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* w,
+         const void* c, void* y, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err.clear();
+  int rc = validate_common(b, dtype, batch, n_in, n_out);
+  if (rc) return rc;
+  if (batch == 0 || n_out == 0) return KF_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (n_in == 0) return dtype == KF_BF16 ? zero_fill<bf16>(y, (long)batch * n_out, s) : zero_fill<float>(y, (long)batch * n_out, s);
+  if (!x || !c || !y) return fail(KF_EINVAL, "kf_F: NULL array");
+  size_t need = ws_f(b, dtype, batch, n_in, n_out).total;
+  if (!workspace || workspace_bytes < need)
+    return fail(KF_EWORKSPACE, "kf_F: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  KBasis kb = to_kbasis(b);
+  if (dtype == KF_BF16)
+    return w ? run_F_weighted<bf16>(kb, b, dtype, batch, n_in, n_out, x, w, c, y, workspace, s)
+             : run_F<bf16>(kb, b, dtype, batch, n_in, n_out, x, w, c, y, workspace, s);
+  return w ? run_F_weighted<float>(kb, b, dtype, batch, n_in, n_out, x, w, c, y, workspace, s)
+           : run_F<float>(kb, b, dtype, batch, n_in, n_out, x, w, c, y, workspace, s);
+}
+
+int kf_G(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* g,
+         const void* w, void* dc, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err.clear();
+  int rc = validate_common(b, dtype, batch, n_in, n_out);
+  if (rc) return rc;
+  if (n_in == 0 || n_out == 0) return KF_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const long n = (long)n_out * n_in * b->size;
+  if (batch == 0) return dtype == KF_BF16 ? zero_fill<bf16>(dc, n, s) : zero_fill<float>(dc, n, s);
+  if (!x || !g || !dc) return fail(KF_EINVAL, "kf_G: NULL array");
+  size_t need = ws_g(dtype, batch, n_out).total;
+  if (!workspace || workspace_bytes < need)
+    return fail(KF_EWORKSPACE, "kf_G: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  KBasis kb = to_kbasis(b);
+  if (dtype == KF_BF16) return run_G<bf16>(kb, dtype, batch, n_in, n_out, x, g, w, dc, workspace, s);
+  return run_G<float>(kb, dtype, batch, n_in, n_out, x, g, w, dc, workspace, s);
+}
+
+int kf_P(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* g,
+         const void* c, void* p, float* h, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err.clear();
+  int rc = validate_common(b, dtype, batch, n_in, n_out);
+  if (rc) return rc;
+  if (batch == 0 || n_in == 0) return KF_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (n_out == 0) {
+    rc = dtype == KF_BF16 ? zero_fill<bf16>(p, (long)batch * n_in, s) : zero_fill<float>(p, (long)batch * n_in, s);
+    if (rc == KF_OK && h) rc = zero_fill<float>(h, (long)batch * n_in, s);
+    return rc;
+  }
+  if (!x || !g || !c || !p) return fail(KF_EINVAL, "kf_P: NULL array");
+  if (h && b->kind != KF_KIND_RATIONAL) return fail(KF_EINVAL, "kf_P: h output is for the rational kind");
+  size_t need = ws_p(b, dtype, n_in, n_out).total;
+  if (!workspace || workspace_bytes < need)
+    return fail(KF_EWORKSPACE, "kf_P: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  KBasis kb = to_kbasis(b);
+  if (dtype == KF_BF16) return run_P<bf16>(kb, b, dtype, batch, n_in, n_out, x, g, c, p, h, workspace, s);
+  return run_P<float>(kb, b, dtype, batch, n_in, n_out, x, g, c, p, h, workspace, s);
+}
+
+int kf_features(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, const void* x, void* out, void* stream) {
+  g_err.clear();
+  int rc = validate_common(b, dtype, batch, n_in, 0);
+  if (rc) return rc;
+  if (batch == 0 || n_in == 0) return KF_OK;
+  if (!x || !out) return fail(KF_EINVAL, "kf_features: NULL array");
+  KBasis kb = to_kbasis(b);
+  hipStream_t s = (hipStream_t)stream;
+  const long K = b->size;
+  if (dtype == KF_BF16)
+    return launch_features<bf16, true>(kb, batch, n_in, batch, n_in, x, out, (long)n_in * K, 1L, K, false, s);
+  return launch_features<float, true>(kb, batch, n_in, batch, n_in, x, out, (long)n_in * K, 1L, K, false, s);
+}
+
+int kf_edge_derivative(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
+                       const void* c, const void* base_w, void* out, void* stream) {
+  g_err.clear();
+  int rc = validate_common(b, dtype, batch, n_in, n_out);
+  if (rc) return rc;
+  if (batch == 0 || n_in == 0 || n_out == 0) return KF_OK;
+  if (!x || !c || !out) return fail(KF_EINVAL, "kf_edge_derivative: NULL array");
+  KBasis kb = to_kbasis(b);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == KF_BF16) return run_edge<bf16>(kb, batch, n_in, n_out, x, c, base_w, out, s);
+  return run_edge<float>(kb, batch, n_in, n_out, x, c, base_w, out, s);
+}
+
+int kf_bspline_interval(int64_t batch, int64_t n_in, const float* x, const float* knots_cmp, int32_t n_knots,
+                        int32_t* idx, void* stream) {
+  g_err.clear();
+  if (batch < 0 || n_in < 0) return fail(KF_EINVAL, "negative dimension");
+  if (n_knots < 2) return fail(KF_EINVAL, "need at least 2 knots");
+  if (batch == 0 || n_in == 0) return KF_OK;
+  if (!x || !knots_cmp || !idx) return fail(KF_EINVAL, "kf_bspline_interval: NULL array");
+  long n = (long)batch * n_in;
+  long blocks = (n + kThreads - 1) / kThreads;
+  if (blocks > 65535 * 4) blocks = 65535 * 4;
+  hipLaunchKernelGGL(interval_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, (hipStream_t)stream, n, (int)n_in, x,
+                     knots_cmp, n_knots, idx);
+  return check_launch("bspline_interval");
+}
+
+size_t kf_rational_workspace_bytes(const kf_basis* b, int64_t batch, int64_t n_in) {
+  if (!b || b->kind != KF_KIND_RATIONAL || b->group_size < 1) return 0;
+  const int64_t groups = n_in / b->group_size;
+  const int64_t chunks = (batch + kRatRows - 1) / kRatRows;
+  return align256((size_t)chunks * groups * (b->num_deg + 1 + b->den_deg) * sizeof(float));
+}
+
+int kf_rational_param_grad(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, const void* x, const float* h,
+                           const void* w, float* dnum, float* dden, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  g_err.clear();
+  int rc = validate_common(b, dtype, batch, n_in, 0);
+  if (rc) return rc;
+  if (b->kind != KF_KIND_RATIONAL) return fail(KF_EINVAL, "kf_rational_param_grad needs the rational kind");
+  if (!dnum || !dden) return fail(KF_EINVAL, "kf_rational_param_grad: NULL output");
+  hipStream_t s = (hipStream_t)stream;
+  const int groups = (int)(n_in / b->group_size);
+  const int nP = b->num_deg + 1, nQ = b->den_deg;
+  if (batch == 0 || n_in == 0) {
+    rc = zero_fill<float>(dnum, (long)groups * nP, s);
+    if (rc == KF_OK) rc = zero_fill<float>(dden, (long)groups * nQ, s);
+    return rc;
+  }
+  if (!x || !h) return fail(KF_EINVAL, "kf_rational_param_grad: NULL array");
+  size_t need = kf_rational_workspace_bytes(b, batch, n_in);
+  if (!workspace || workspace_bytes < need)
+    return fail(KF_EWORKSPACE, "kf_rational_param_grad: workspace of %zu bytes needed, %zu given", need,
+                workspace_bytes);
+  KBasis kb = to_kbasis(b);
+  const int chunks = (int)((batch + kRatRows - 1) / kRatRows);
+  dim3 grid((unsigned)groups, (unsigned)chunks);
+  if (dtype == KF_BF16)
+    hipLaunchKernelGGL(rational_grad_partial<bf16>, grid, dim3(kThreads), 0, s, kb, (int)batch, (int)n_in,
+                       (const bf16*)x, h, (const bf16*)w, (float*)workspace);
+  else
+    hipLaunchKernelGGL(rational_grad_partial<float>, grid, dim3(kThreads), 0, s, kb, (int)batch, (int)n_in,
+                       (const float*)x, h, (const float*)w, (float*)workspace);
+  rc = check_launch("rational_grad_partial");
+  if (rc) return rc;
+  hipLaunchKernelGGL(rational_grad_final, dim3(1), dim3(256), 0, s, groups, nP, nQ, chunks,
+                     (const float*)workspace, dnum, dden);
+  return check_launch("rational_grad_final");
+}
+
+}  // extern "C"

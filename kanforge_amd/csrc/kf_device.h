@@ -1,0 +1,282 @@
+// Device-side building blocks of the fused KAN kernels for gfx950 (CDNA4):
+// element types, MFMA wrappers, and the per-input basis feature generators.
+//
+// Feature generators evaluate, in float32 registers, what the reference's
+// bases compute in float64:
+//   Chebyshev features T_j(g(x)), g = tanh | identity   kanforge/bases/polynomial.py:87-106
+//   B-splines and their derivatives                     kanforge/bases/spline.py:74-92
+//   rational P/(1+|Q|) and its derivatives              kanforge/bases/rational.py:84-101
+//   d^m silu                                            kanforge/_calculus.py:90-96
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/kfhip.h"
+
+namespace kf {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Launch-time copy of kf_basis; passed by value as a kernel argument.
+struct KBasis {
+  int kind, K, n_t, order, input_map;
+  int spline_k, n_knots;
+  int num_deg, den_deg, group_size;
+  const float* knots;
+  const float* knots_cmp;
+  const float* num;
+  const float* den;
+  float fold[KF_MAX_K * KF_MAX_NT];  // R_m, K x n_t row-major (cheb)
+};
+
+// ---------------------------------------------------------------------------
+// element conversion
+
+template <typename T>
+__device__ __forceinline__ float to_f32(T v);
+template <>
+__device__ __forceinline__ float to_f32<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ float to_f32<bf16>(bf16 v) { return (float)v; }
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float v);
+template <>
+__device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ bf16 from_f32<bf16>(float v) { return (bf16)v; }  // round to nearest even
+
+// ---------------------------------------------------------------------------
+// scalar math
+
+// tanh(x) = sign(x) (1 - e^{-2|x|}) / (1 + e^{-2|x|}); absolute error a few
+// float32 ulps of 1, the quantity the features need (T_j(z) is bounded by 1).
+__device__ __forceinline__ float fast_tanh(float x) {
+  float t = __expf(-2.0f * fabsf(x));
+  float r = (1.0f - t) * __frcp_rn(1.0f + t);
+  return copysignf(r, x);
+}
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+// d^m/dx^m silu(x) = x p_m(s) + m p_{m-1}(s), s = sigmoid(x), where
+// p_0 = s and p_{j+1} = p_j'(s) (s - s^2). The polynomial coefficients are
+// generated on the fly (m <= 8).
+__device__ inline float silu_derivative(float x, int m) {
+  float s = sigmoidf_(x);
+  if (m == 0) return x * s;
+  // coefficients of p_j in powers of s, degree j+1
+  float p[11], q[11];
+  for (int a = 0; a < 11; ++a) p[a] = 0.f;
+  p[1] = 1.f;  // p_0 = s
+  float prev_val = 0.f, cur_val = s;
+  for (int j = 1; j <= m; ++j) {
+    // q = p' * (s - s^2): p' has coefficients (a+1) p[a+1]
+    for (int a = 0; a < 11; ++a) q[a] = 0.f;
+    for (int a = 0; a + 1 < 11; ++a) {
+      float d = (a + 1) * p[a + 1];  // coefficient of s^a in p'
+      if (a + 1 < 11) q[a + 1] += d;
+      if (a + 2 < 11) q[a + 2] -= d;
+    }
+    for (int a = 0; a < 11; ++a) p[a] = q[a];
+    prev_val = cur_val;
+    float v = 0.f;
+    for (int a = 10; a >= 0; --a) v = v * s + p[a];
+    cur_val = v;
+  }
+  return x * cur_val + (float)m * prev_val;
+}
+
+// ---------------------------------------------------------------------------
+// Chebyshev features: T[j] = w * T_j(g(x)), j < n_t (n_t <= NT).
+// The three-term recurrence is linear, so scaling T_0 and T_1 by w scales
+// every feature by w.
+
+__device__ __forceinline__ float cheb_map(float x, int input_map) {
+  return input_map == KF_MAP_TANH ? fast_tanh(x) : x;
+}
+
+template <int NT>
+__device__ __forceinline__ void cheb_features(float z, float w, int n_t, float* T) {
+  float z2 = 2.0f * z;
+  T[0] = w;
+  if (NT > 1) T[1] = w * z;
+#pragma unroll
+  for (int j = 2; j < NT; ++j) T[j] = j < n_t ? fmaf(z2, T[j - 1], -T[j - 2]) : 0.f;
+}
+
+// phi_k^(m) = sum_j fold[k][j] T_j  (fold = R_m of the plan)
+template <int KM, int NT>
+__device__ __forceinline__ void cheb_folded(const KBasis& b, const float* T, float* phi) {
+#pragma unroll
+  for (int k = 0; k < KM; ++k) {
+    float acc = 0.f;
+    if (k < b.K) {
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+        if (j < b.n_t) acc = fmaf(b.fold[k * KF_MAX_NT + j], T[j], acc);
+    }
+    phi[k] = acc;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// B-splines. Knot vector of input i: t_0 .. t_{n_knots-1} (real), stored with
+// spline_k padding knots per side: kp[r] = t_{r - spline_k}.
+
+// Interval j with t_j <= x < t_{j+1}, or -1: count of comparison knots <= x, minus one.
+__device__ __forceinline__ int bspline_interval(float x, const float* kc, int n_knots) {
+  int cnt = 0;
+  for (int r = 0; r < n_knots; ++r) cnt += (x >= kc[r]) ? 1 : 0;
+  int j = cnt - 1;
+  return (j >= 0 && j <= n_knots - 2) ? j : -1;
+}
+
+// phi[s] = w * d^m/dx^m B_{k,s}(x), s < K = n_knots - 1 - k, for k == KD.
+// Local de Boor on the k+1 splines that can be non-zero in interval j, then
+// m derivative steps (m > k gives zeros). KM >= K.
+template <int KM, int KD>
+__device__ inline void bspline_features(float x, float w, int i, const KBasis& b, float* phi) {
+#pragma unroll
+  for (int s = 0; s < KM; ++s) phi[s] = 0.f;
+  const int nk = b.n_knots, m = b.order;
+  if (m > KD) return;
+  const int j = bspline_interval(x, b.knots_cmp + (size_t)i * nk, nk);
+  if (j < 0) return;
+  // L[r] = t_{j-KD+r}, r = 0..2KD+1 (kp[r'] = t_{r'-KD}, so t_{j-KD+r} = kp[j+r])
+  const float* kp = b.knots + (size_t)i * (nk + 2 * KD) + j;
+  float L[2 * KD + 2];
+#pragma unroll
+  for (int r = 0; r < 2 * KD + 2; ++r) L[r] = kp[r];
+  // N[r] = B_{q, j-q+r}, r = 0..q. With s = j-q+r:
+  //   t_s = L[KD-q+r], t_{s+1} = L[KD-q+r+1], t_{s+q} = L[KD+r], t_{s+q+1} = L[KD+r+1]
+  float N[KD + 1];
+  N[0] = 1.f;
+#pragma unroll
+  for (int r = 1; r <= KD; ++r) N[r] = 0.f;
+  const int deg = KD - m;
+#pragma unroll
+  for (int q = 1; q <= KD; ++q) {
+    float nn[KD + 1];
+#pragma unroll
+    for (int r = 0; r <= KD; ++r) nn[r] = 0.f;
+#pragma unroll
+    for (int r = 0; r <= q; ++r) {
+      const float ts = L[KD - q + r], ts1 = L[KD - q + r + 1], tsq = L[KD + r], tsq1 = L[KD + r + 1];
+      const float left = (r >= 1) ? N[r - 1] : 0.f;   // B_{q-1,s}
+      const float right = (r <= q - 1) ? N[r] : 0.f;  // B_{q-1,s+1}
+      if (q <= deg)  // Cox-de Boor
+        nn[r] = (x - ts) / (tsq - ts) * left + (tsq1 - x) / (tsq1 - ts1) * right;
+      else  // derivative step
+        nn[r] = (float)q * (left / (tsq - ts) - right / (tsq1 - ts1));
+    }
+#pragma unroll
+    for (int r = 0; r <= KD; ++r) N[r] = nn[r];
+  }
+  // N[r] = B^(m)_{KD, j-KD+r}
+  const int base = j - KD;
+#pragma unroll
+  for (int s = 0; s < KM; ++s) {
+    const int r = s - base;
+    float v = 0.f;
+#pragma unroll
+    for (int rr = 0; rr <= KD; ++rr) v = (rr == r) ? N[rr] : v;
+    phi[s] = (s < b.K) ? w * v : 0.f;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Rational P/(1+|Q|) and derivatives by the quotient rule
+//   out_n = (P^(n) - sum_{k=1..n} C(n,k) D^(k) out_{n-k}) / D,  D^(k) = sign(Q) Q^(k) for k >= 1.
+
+// Evaluates sum_{p >= j} c_p p!/(p-j)! x^(p-j) for the polynomial with coefficients
+// c_p = coef[p - first] (p = first .. first+n-1).
+__device__ inline float poly_dj(const float* coef, int n, int first, int j, float x) {
+  int hi = first + n - 1;  // highest power
+  if (hi < j) return 0.f;
+  float acc = 0.f;
+  for (int p = hi; p >= j; --p) {
+    float c = (p >= first) ? coef[p - first] : 0.f;
+    float f = c;
+    for (int t = 0; t < j; ++t) f *= (float)(p - t);
+    acc = fmaf(acc, x, f);
+  }
+  return acc;
+}
+
+__device__ inline float binom(int n, int k) {
+  float r = 1.f;
+  for (int t = 1; t <= k; ++t) r = r * (float)(n - k + t) / (float)t;
+  return r;
+}
+
+// d^m/dx^m of P/(1+|Q|), m <= 8
+__device__ inline float rational_feature(float x, int i, const KBasis& b, int m) {
+  const int g = i / b.group_size;
+  const float* a = b.num + (size_t)g * (b.num_deg + 1);
+  const float* c = b.den + (size_t)g * b.den_deg;
+  float out[9];
+  float Q0 = poly_dj(c, b.den_deg, 1, 0, x);
+  float sgn = (Q0 > 0.f) ? 1.f : ((Q0 < 0.f) ? -1.f : 0.f);
+  float D0 = 1.f + fabsf(Q0);
+  float invD = 1.f / D0;
+  out[0] = poly_dj(a, b.num_deg + 1, 0, 0, x) * invD;
+  for (int n = 1; n <= m && n <= 8; ++n) {
+    float acc = poly_dj(a, b.num_deg + 1, 0, n, x);
+    for (int k = 1; k <= n; ++k) acc -= binom(n, k) * sgn * poly_dj(c, b.den_deg, 1, k, x) * out[n - k];
+    out[n] = acc * invD;
+  }
+  return out[m < 8 ? m : 8];
+}
+
+// Degree dispatch (degrees 0..5 are compiled).
+template <int KM>
+__device__ inline void bspline_dispatch(float x, float w, int i, const KBasis& b, float* phi) {
+  switch (b.spline_k) {
+    case 0: bspline_features<KM, 0>(x, w, i, b, phi); break;
+    case 1: bspline_features<KM, 1>(x, w, i, b, phi); break;
+    case 2: bspline_features<KM, 2>(x, w, i, b, phi); break;
+    case 3: bspline_features<KM, 3>(x, w, i, b, phi); break;
+    case 4: bspline_features<KM, 4>(x, w, i, b, phi); break;
+    default: bspline_features<KM, 5>(x, w, i, b, phi); break;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// All K features of order b.order (fold applied for cheb): the generic
+// generator used where every feature of one element is needed at once.
+template <int KM, int NT>
+__device__ inline void basis_features(float x, float w, int i, const KBasis& b, float* phi) {
+  if (b.kind == KF_KIND_CHEB) {
+    float T[NT];
+    cheb_features<NT>(cheb_map(x, b.input_map), w, b.n_t, T);
+    cheb_folded<KM, NT>(b, T, phi);
+  } else if (b.kind == KF_KIND_BSPLINE) {
+    bspline_dispatch<KM>(x, w, i, b, phi);
+  } else {
+#pragma unroll
+    for (int s = 0; s < KM; ++s) phi[s] = 0.f;
+    phi[0] = w * rational_feature(x, i, b, b.order);
+  }
+}
+
+// Kernel features (what the F and G contractions consume): for cheb the
+// unfolded T_j (n_t of them), otherwise the K basis derivatives.
+template <int NT>
+__device__ inline void kernel_features(float x, float w, int i, const KBasis& b, float* f) {
+  if (b.kind == KF_KIND_CHEB) {
+    cheb_features<NT>(cheb_map(x, b.input_map), w, b.n_t, f);
+  } else if (b.kind == KF_KIND_BSPLINE) {
+    bspline_dispatch<NT>(x, w, i, b, f);
+  } else {
+#pragma unroll
+    for (int s = 0; s < NT; ++s) f[s] = 0.f;
+    f[0] = w * rational_feature(x, i, b, b.order);
+  }
+}
+
+}  // namespace kf

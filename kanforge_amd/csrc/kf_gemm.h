@@ -1,0 +1,70 @@
+// MFMA tile primitives shared by the F, G and P contractions (gfx950).
+//
+// Every contraction is staged as "k-groups" of 64 bytes of the reduction
+// dimension: 32 bf16 or 16 float32 values. Operand tiles live in LDS with the
+// reduction dimension contiguous; each lane reads 16 bytes per fragment:
+//   lane l supplies row (l % 16) and reduction elements [h*E, h*E+E) of the
+//   k-group, h = l / 16, E = 16 / sizeof(T).
+// bf16: one v_mfma_f32_16x16x32_bf16 per k-group and 16x16 tile.
+// f32 : four v_mfma_f32_16x16x4_f32; instruction q takes element q of each
+//       lane's four, so lanes h = 0..3 contribute reduction elements 4h+q.
+// A and B use the same element-to-lane assignment, so the sum runs over the
+// whole k-group. The accumulator of a 16x16 tile holds, in lane l,
+// D[4*(l/16) + r][l % 16], r = 0..3 (checked on gfx950 hardware).
+#pragma once
+
+#include "kf_device.h"
+
+namespace kf {
+
+template <typename T>
+struct KG {
+  static constexpr int elems = 64 / sizeof(T);  // reduction elements per k-group
+  static constexpr int per_lane = 16 / sizeof(T);
+};
+
+template <typename T>
+__device__ __forceinline__ void mma(f32x4& acc, const u32x4& a, const u32x4& b);
+
+template <>
+__device__ __forceinline__ void mma<bf16>(f32x4& acc, const u32x4& a, const u32x4& b) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), acc, 0,
+                                                 0, 0);
+}
+
+template <>
+__device__ __forceinline__ void mma<float>(f32x4& acc, const u32x4& a, const u32x4& b) {
+  const f32x4 af = __builtin_bit_cast(f32x4, a);
+  const f32x4 bf = __builtin_bit_cast(f32x4, b);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af[0], bf[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af[1], bf[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af[2], bf[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af[3], bf[3], acc, 0, 0, 0);
+}
+
+__device__ __forceinline__ u32x4 lds_read16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ void lds_write16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+// Pack 16 bytes worth of float values into T elements.
+template <typename T>
+__device__ __forceinline__ u32x4 pack16(const float* v);
+template <>
+__device__ __forceinline__ u32x4 pack16<bf16>(const float* v) {
+  bf16x8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = (bf16)v[e];
+  return __builtin_bit_cast(u32x4, r);
+}
+template <>
+__device__ __forceinline__ u32x4 pack16<float>(const float* v) {
+  f32x4 r = {v[0], v[1], v[2], v[3]};
+  return __builtin_bit_cast(u32x4, r);
+}
+
+// Load 16 bytes from global memory; `ok` false gives zeros.
+__device__ __forceinline__ u32x4 gload16(const void* p, bool ok) {
+  u32x4 z = {0u, 0u, 0u, 0u};
+  return ok ? *reinterpret_cast<const u32x4*>(p) : z;
+}
+
+}  // namespace kf

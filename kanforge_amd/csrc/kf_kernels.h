@@ -1,0 +1,563 @@
+// HIP kernels of the fused KAN hot path for gfx950.
+//
+// The three primitives of kanforge/kernels/__init__.py:1-13,
+//   F_m(x, c, w)[b,o]   = sum_{i,k} w[b,i] c[o,i,k] phi_k^(m)(x[b,i])
+//   G_m(x, g, w)[o,i,k] = sum_b     w[b,i] g[b,o]   phi_k^(m)(x[b,i])
+//   P_m(x, g, c)[b,i]   = sum_{o,k} g[b,o] c[o,i,k] phi_k^(m)(x[b,i])
+// run as MFMA contractions over "kernel features" f_j(x[b,i]), j < n_t:
+// Chebyshev T_j(g(x)) with the fold R_m applied to the coefficients
+// (kanforge/kernels/plan.py:75-101), or the K basis derivatives themselves
+// for B-splines and rationals. Reduction order inside an input chunk is
+// feature-major (feature j, then 32 inputs), which lets the Chebyshev
+// recurrence emit one feature per k-group.
+#pragma once
+#include "kf_gemm.h"
+
+namespace kf {
+
+constexpr int kThreads = 256;
+
+// ---------------------------------------------------------------------------
+// Coefficients c (n_out, n_in, K) -> folded, feature-major, zero-padded copy:
+//   FM : out[j][o][i]  (n_t, OUTP, INP)   B operand of F
+//   FMT: out[j][i][o]  (n_t, INP, OUTP)   B operand of P
+// out[j] = sum_k c[o,i,k] fold[k][j]. Tile 32 o x 16 i through LDS.
+template <typename T, bool FMT>
+__global__ __launch_bounds__(kThreads) void permute_coef_kernel(KBasis bs, int OUT, int IN, int OUTP, int INP,
+                                                                const T* __restrict__ c, T* __restrict__ out) {
+  extern __shared__ float tile[];  // [n_t][16][33]
+  const int K = bs.K, n_t = bs.n_t;
+  const int o0 = blockIdx.x * 32, i0 = blockIdx.y * 16;
+  const int t = threadIdx.x;
+  // phase 1: thread (ol = t / 16 .. +16, il = t % 16) covers 2 o rows
+  for (int rep = 0; rep < 2; ++rep) {
+    const int ol = t / 16 + rep * 16, il = t % 16;
+    const int o = o0 + ol, i = i0 + il;
+    float cv[KF_MAX_K];
+#pragma unroll
+    for (int k = 0; k < KF_MAX_K; ++k)
+      cv[k] = (k < K && o < OUT && i < IN) ? to_f32(c[((size_t)o * IN + i) * K + k]) : 0.f;
+    for (int j = 0; j < n_t; ++j) {
+      float acc = 0.f;
+#pragma unroll
+      for (int k = 0; k < KF_MAX_K; ++k)
+        if (k < K) acc = fmaf(cv[k], bs.fold[k * KF_MAX_NT + j], acc);
+      tile[(j * 16 + il) * 33 + ol] = acc;
+    }
+  }
+  __syncthreads();
+  if (!FMT) {
+    // out[j][o][i]: consecutive threads along i
+    for (int e = t; e < n_t * 32 * 16; e += kThreads) {
+      const int il = e % 16, ol = (e / 16) % 32, j = e / (16 * 32);
+      const int o = o0 + ol, i = i0 + il;
+      if (o < OUTP && i < INP) out[((size_t)j * OUTP + o) * INP + i] = from_f32<T>(tile[(j * 16 + il) * 33 + ol]);
+    }
+  } else {
+    // out[j][i][o]: consecutive threads along o
+    for (int e = t; e < n_t * 32 * 16; e += kThreads) {
+      const int ol = e % 32, il = (e / 32) % 16, j = e / (16 * 32);
+      const int o = o0 + ol, i = i0 + il;
+      if (o < OUTP && i < INP) out[((size_t)j * INP + i) * OUTP + o] = from_f32<T>(tile[(j * 16 + il) * 33 + ol]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// g (B, OUT) -> gT (OUTP, BP), zero padded. 64x64 tiles through LDS.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void transpose_kernel(int B, int OUT, int BP, int OUTP, const T* __restrict__ g,
+                                                             T* __restrict__ gt) {
+  __shared__ float tile[64][65];
+  const int b0 = blockIdx.y * 64, o0 = blockIdx.x * 64;
+  const int tx = threadIdx.x % 64, ty = threadIdx.x / 64;
+  for (int r = ty; r < 64; r += 4) {
+    const int b = b0 + r, o = o0 + tx;
+    tile[r][tx] = (b < B && o < OUT) ? to_f32(g[(size_t)b * OUT + o]) : 0.f;
+  }
+  __syncthreads();
+  for (int r = ty; r < 64; r += 4) {
+    const int o = o0 + r, b = b0 + tx;
+    if (o < OUTP && b < BP) gt[(size_t)o * BP + b] = from_f32<T>(tile[tx][r]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Features: out[b*sb + j*sj + i*si] for b < BROWS, i < ICOLS, j < count,
+// zero where b >= B or i >= IN. FOLDED: the K basis derivatives (fold
+// applied for cheb), else the n_t kernel features.
+template <typename T, int NTB, bool FOLDED>
+__global__ __launch_bounds__(kThreads) void features_kernel(KBasis bs, int B, int IN, int BROWS, int ICOLS,
+                                                            const T* __restrict__ x, T* __restrict__ out, long sb,
+                                                            long sj, long si, bool b_fastest) {
+  const long n = (long)BROWS * ICOLS;
+  for (long e = blockIdx.x * (long)kThreads + threadIdx.x; e < n; e += (long)gridDim.x * kThreads) {
+    int b, i;
+    if (b_fastest) {
+      b = (int)(e % BROWS);
+      i = (int)(e / BROWS);
+    } else {
+      i = (int)(e % ICOLS);
+      b = (int)(e / ICOLS);
+    }
+    float f[NTB];
+    const bool ok = b < B && i < IN;
+    const float xv = ok ? to_f32(x[(size_t)b * IN + i]) : 0.f;
+    if (FOLDED)
+      basis_features<NTB, NTB>(xv, 1.f, ok ? i : 0, bs, f);
+    else
+      kernel_features<NTB>(xv, 1.f, ok ? i : 0, bs, f);
+    const int cnt = FOLDED ? bs.K : bs.n_t;
+#pragma unroll
+    for (int j = 0; j < NTB; ++j)
+      if (j < cnt) out[b * sb + j * sj + i * si] = from_f32<T>(ok ? f[j] : 0.f);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// F: y[b,o] = sum over chunks of 32 inputs, features j:  A_j[b][i] * Cfm[j][o][i]
+// A_j is generated in LDS from x (Chebyshev recurrence, CHEB) or copied from
+// the precomputed feature tensor phi_fm[b][j][i] (other kinds).
+template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, bool CHEB>
+__global__ __launch_bounds__(kThreads) void f_kernel(KBasis bs, int B, int IN, int OUT, int INP, int OUTP,
+                                                     const T* __restrict__ x, const T* __restrict__ w,
+                                                     const T* __restrict__ cfm, const T* __restrict__ phi_fm,
+                                                     T* __restrict__ y) {
+  constexpr int KGE = KG<T>::elems, PL = KG<T>::per_lane;
+  constexpr int IC = 32;
+  constexpr int STR = IC + 16 / (int)sizeof(T);  // row stride (elements), +16 bytes against bank conflicts
+  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N, TM = WM / 16, TN = WN / 16;
+  constexpr int TPR = kThreads / BM;  // generator threads per A row
+  constexpr int EPT = IC / TPR;       // elements per generator thread
+  static_assert(WAVES_M * WAVES_N * 64 == kThreads, "4 waves");
+  static_assert(EPT * sizeof(T) % 16 == 0, "generator writes 16-byte chunks");
+
+  __shared__ __attribute__((aligned(16))) T As[BM * STR];
+  __shared__ __attribute__((aligned(16))) T Bs[BN * STR];
+
+  const int b0 = blockIdx.y * BM, o0 = blockIdx.x * BN;
+  const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  const int h = lane / 16, l16 = lane % 16;
+  const int n_t = bs.n_t;
+
+  f32x4 acc[TM][TN];
+#pragma unroll
+  for (int a = 0; a < TM; ++a)
+#pragma unroll
+    for (int c = 0; c < TN; ++c) acc[a][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // generator state (CHEB): row gr, inputs gc*EPT .. +EPT of the chunk
+  const int gr = tid / TPR, gc = tid % TPR;
+  const int gb = b0 + gr;
+  float z2[EPT], tp[EPT], tc[EPT];
+
+  const int n_chunks = INP / IC;
+  for (int ch = 0; ch < n_chunks; ++ch) {
+    const int i0 = ch * IC;
+    if (CHEB) {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        const int i = i0 + gc * EPT + e;
+        const bool ok = gb < B && i < IN;
+        const float xv = ok ? to_f32(x[(size_t)gb * IN + i]) : 0.f;
+        const float wv = ok ? (w ? to_f32(w[(size_t)gb * IN + i]) : 1.f) : 0.f;
+        const float z = cheb_map(xv, bs.input_map);
+        z2[e] = 2.f * z;
+        tp[e] = wv;      // T_0 * w
+        tc[e] = wv * z;  // T_1 * w
+      }
+    }
+    for (int j = 0; j < n_t; ++j) {
+      __syncthreads();  // previous step's MFMAs are done with As/Bs
+      // --- A tile
+      if (CHEB) {
+        float f[EPT];
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) {
+          if (j == 0) {
+            f[e] = tp[e];
+          } else if (j == 1) {
+            f[e] = tc[e];
+          } else {
+            const float nt = fmaf(z2[e], tc[e], -tp[e]);
+            tp[e] = tc[e];
+            tc[e] = nt;
+            f[e] = nt;
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < EPT / PL; ++q) lds_write16(&As[gr * STR + gc * EPT + q * PL], pack16<T>(&f[q * PL]));
+      } else {
+        // copy phi_fm[b][j][i0 .. i0+32] rows
+        constexpr int CPR = IC / PL;  // 16-byte chunks per row
+        for (int e = tid; e < BM * CPR; e += kThreads) {
+          const int r = e / CPR, q = e % CPR;
+          const T* src = phi_fm + ((size_t)(b0 + r) * n_t + j) * INP + i0 + q * PL;
+          lds_write16(&As[r * STR + q * PL], gload16(src, true));
+        }
+      }
+      // --- B tile: cfm[j][o0 + n][i0 .. i0+32]
+      {
+        constexpr int CPR = IC / PL;
+        for (int e = tid; e < BN * CPR; e += kThreads) {
+          const int r = e / CPR, q = e % CPR;
+          const T* src = cfm + ((size_t)j * OUTP + o0 + r) * INP + i0 + q * PL;
+          lds_write16(&Bs[r * STR + q * PL], gload16(src, true));
+        }
+      }
+      __syncthreads();
+      // --- MFMA
+#pragma unroll
+      for (int kg = 0; kg < IC / KGE; ++kg) {
+        u32x4 af[TM], bfr[TN];
+#pragma unroll
+        for (int a = 0; a < TM; ++a) af[a] = lds_read16(&As[(wm * WM + a * 16 + l16) * STR + kg * KGE + h * PL]);
+#pragma unroll
+        for (int c = 0; c < TN; ++c) bfr[c] = lds_read16(&Bs[(wn * WN + c * 16 + l16) * STR + kg * KGE + h * PL]);
+#pragma unroll
+        for (int a = 0; a < TM; ++a)
+#pragma unroll
+          for (int c = 0; c < TN; ++c) mma<T>(acc[a][c], af[a], bfr[c]);
+      }
+    }
+  }
+  // --- epilogue
+#pragma unroll
+  for (int a = 0; a < TM; ++a)
+#pragma unroll
+    for (int c = 0; c < TN; ++c) {
+      const int o = o0 + wn * WN + c * 16 + l16;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int b = b0 + wm * WM + a * 16 + 4 * h + r;
+        if (b < B && o < OUT) y[(size_t)b * OUT + o] = from_f32<T>(acc[a][c][r]);
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// P: p[b,i] = sum_j f_j(x[b,i]) * sum_o g[b,o] CfmT[j][i][o]
+// N tile = 16 inputs x n_t features (column j*16 + input), all waves along M;
+// each lane ends with every feature of its (b, i) positions and finishes the
+// feature sum in registers.
+template <typename T, int NTB, int BM>
+__global__ __launch_bounds__(kThreads) void p_kernel(KBasis bs, int B, int IN, int OUT, int INP, int OUTP,
+                                                     const T* __restrict__ x, const T* __restrict__ g,
+                                                     const T* __restrict__ cfmt, T* __restrict__ p,
+                                                     float* __restrict__ hout) {
+  constexpr int KGE = KG<T>::elems, PL = KG<T>::per_lane;
+  constexpr int OC = 32;  // reduction elements (outputs o) per step
+  constexpr int STR = OC + 16 / (int)sizeof(T);
+  constexpr int WM = BM / 4, TM = WM / 16;
+  __shared__ __attribute__((aligned(16))) T As[BM * STR];
+  __shared__ __attribute__((aligned(16))) T Bs[NTB * 16 * STR];
+
+  const int b0 = blockIdx.y * BM, i0 = blockIdx.x * 16;
+  const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+  const int h = lane / 16, l16 = lane % 16;
+  const int n_t = bs.n_t;
+  const bool g_vec = (OUT % PL) == 0;
+
+  f32x4 acc[TM][NTB];
+#pragma unroll
+  for (int a = 0; a < TM; ++a)
+#pragma unroll
+    for (int c = 0; c < NTB; ++c) acc[a][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int oc0 = 0; oc0 < OUTP; oc0 += OC) {
+    __syncthreads();
+    constexpr int CPR = OC / PL;
+    // A tile: g[b0 + r][oc0 .. oc0+32] (bounds-checked)
+    for (int e = tid; e < BM * CPR; e += kThreads) {
+      const int r = e / CPR, q = e % CPR;
+      const int b = b0 + r, o = oc0 + q * PL;
+      u32x4 v;
+      if (g_vec) {
+        v = gload16(g + (size_t)b * OUT + o, b < B && o < OUT);
+      } else {
+        float tmp[PL];
+#pragma unroll
+        for (int u = 0; u < PL; ++u) tmp[u] = (b < B && o + u < OUT) ? to_f32(g[(size_t)b * OUT + o + u]) : 0.f;
+        v = pack16<T>(tmp);
+      }
+      lds_write16(&As[r * STR + q * PL], v);
+    }
+    // B tile: cfmt[j][i0 + il][oc0 .. oc0+32], row j*16 + il
+    for (int e = tid; e < n_t * 16 * CPR; e += kThreads) {
+      const int r = e / CPR, q = e % CPR;
+      const int j = r / 16, il = r % 16;
+      const T* src = cfmt + ((size_t)j * INP + i0 + il) * OUTP + oc0 + q * PL;
+      lds_write16(&Bs[r * STR + q * PL], gload16(src, true));
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kg = 0; kg < OC / KGE; ++kg) {
+      u32x4 af[TM];
+#pragma unroll
+      for (int a = 0; a < TM; ++a) af[a] = lds_read16(&As[(wave * WM + a * 16 + l16) * STR + kg * KGE + h * PL]);
+#pragma unroll
+      for (int c = 0; c < NTB; ++c) {
+        if (c < n_t) {
+          const u32x4 bf = lds_read16(&Bs[(c * 16 + l16) * STR + kg * KGE + h * PL]);
+#pragma unroll
+          for (int a = 0; a < TM; ++a) mma<T>(acc[a][c], af[a], bf);
+        }
+      }
+    }
+  }
+  // epilogue: feature sum per (b, i)
+  const int i = i0 + l16;
+#pragma unroll
+  for (int a = 0; a < TM; ++a)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int b = b0 + wave * WM + a * 16 + 4 * h + r;
+      if (b < B && i < IN) {
+        float f[NTB];
+        kernel_features<NTB>(to_f32(x[(size_t)b * IN + i]), 1.f, i, bs, f);
+        float s = 0.f;
+#pragma unroll
+        for (int c = 0; c < NTB; ++c)
+          if (c < n_t) s = fmaf(acc[a][c][r], f[c], s);
+        p[(size_t)b * IN + i] = from_f32<T>(s);
+        if (hout) hout[(size_t)b * IN + i] = acc[a][0][r];
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// G: dc[o,i,k] = sum_j fold[k][j] sum_b gT[o][b] w[b,i] f_j(x[b,i])
+// N tile = 16 inputs x n_t features; features generated into LDS with b
+// contiguous (the reduction dimension), shared by all four waves.
+template <typename T, int NTB, int BM>
+__global__ __launch_bounds__(kThreads) void g_kernel(KBasis bs, int B, int IN, int OUT, int BP, int OUTP,
+                                                     const T* __restrict__ x, const T* __restrict__ w,
+                                                     const T* __restrict__ gt, T* __restrict__ dc) {
+  constexpr int KGE = KG<T>::elems, PL = KG<T>::per_lane;
+  constexpr int BC = 64;  // batch rows per step
+  constexpr int STR = BC + 16 / (int)sizeof(T);
+  constexpr int WM = BM / 4, TM = WM / 16;
+  __shared__ __attribute__((aligned(16))) T As[BM * STR];
+  __shared__ __attribute__((aligned(16))) T Bs[NTB * 16 * STR];
+
+  const int o0 = blockIdx.y * BM, i0 = blockIdx.x * 16;
+  const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+  const int h = lane / 16, l16 = lane % 16;
+  const int n_t = bs.n_t, K = bs.K;
+
+  f32x4 acc[TM][NTB];
+#pragma unroll
+  for (int a = 0; a < TM; ++a)
+#pragma unroll
+    for (int c = 0; c < NTB; ++c) acc[a][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // generator task: input gi (of 16), 4 consecutive batch rows gq*4 .. +4
+  const int gi = tid % 16, gq = tid / 16;
+  const int gin = i0 + gi;
+
+  for (int bc0 = 0; bc0 < BP; bc0 += BC) {
+    __syncthreads();
+    // A tile: gT[o0 + r][bc0 .. bc0+64]
+    constexpr int CPR = BC / PL;
+    for (int e = tid; e < BM * CPR; e += kThreads) {
+      const int r = e / CPR, q = e % CPR;
+      const T* src = gt + (size_t)(o0 + r) * BP + bc0 + q * PL;
+      lds_write16(&As[r * STR + q * PL], gload16(src, true));
+    }
+    // B tile: features of x[bc0 + gq*4 + u][gin], u < 4, row j*16 + gi
+    {
+      float f[4][NTB];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int b = bc0 + gq * 4 + u;
+        const bool ok = b < B && gin < IN;
+        const float xv = ok ? to_f32(x[(size_t)b * IN + gin]) : 0.f;
+        const float wv = ok ? (w ? to_f32(w[(size_t)b * IN + gin]) : 1.f) : 0.f;
+        kernel_features<NTB>(xv, wv, ok ? gin : 0, bs, f[u]);
+      }
+#pragma unroll
+      for (int c = 0; c < NTB; ++c) {
+        if (c < n_t) {
+          T* dst = &Bs[(c * 16 + gi) * STR + gq * 4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) dst[u] = from_f32<T>(f[u][c]);
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kg = 0; kg < BC / KGE; ++kg) {
+      u32x4 af[TM];
+#pragma unroll
+      for (int a = 0; a < TM; ++a) af[a] = lds_read16(&As[(wave * WM + a * 16 + l16) * STR + kg * KGE + h * PL]);
+#pragma unroll
+      for (int c = 0; c < NTB; ++c) {
+        if (c < n_t) {
+          const u32x4 bf = lds_read16(&Bs[(c * 16 + l16) * STR + kg * KGE + h * PL]);
+#pragma unroll
+          for (int a = 0; a < TM; ++a) mma<T>(acc[a][c], af[a], bf);
+        }
+      }
+    }
+  }
+  // epilogue: apply the fold, store dc[o][i][0..K)
+  const int i = i0 + l16;
+#pragma unroll
+  for (int a = 0; a < TM; ++a)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int o = o0 + wave * WM + a * 16 + 4 * h + r;
+      if (o < OUT && i < IN) {
+        T* dst = dc + ((size_t)o * IN + i) * K;
+        for (int k = 0; k < K; ++k) {
+          float s = 0.f;
+#pragma unroll
+          for (int c = 0; c < NTB; ++c)
+            if (c < n_t) s = fmaf(acc[a][c][r], bs.fold[k * KF_MAX_NT + c], s);
+          dst[k] = from_f32<T>(s);
+        }
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// edge_derivative: out[b,o,i] = sum_k c[o,i,k] phi_k^(m)(x[b,i]) + W[o,i] silu^(m)(x[b,i])
+// Block: ROWS batch rows x 64 inputs, all outputs. Phase 1 evaluates the
+// features into LDS; phase 2 streams the outputs, i fastest (coalesced).
+template <typename T, int KM>
+__global__ __launch_bounds__(kThreads) void edge_kernel(KBasis bs, int B, int IN, int OUT, const T* __restrict__ x,
+                                                        const T* __restrict__ c, const T* __restrict__ bw,
+                                                        T* __restrict__ out) {
+  constexpr int ROWS = 8, IT = 64, OG = 4;
+  constexpr int FS = KM + 1;  // features + silu slot
+  __shared__ float feat[ROWS][IT][FS + 1];
+  const int b0 = blockIdx.y * ROWS, i0 = blockIdx.x * IT;
+  const int tid = threadIdx.x;
+  const int K = bs.K, m = bs.order;
+  for (int e = tid; e < ROWS * IT; e += kThreads) {
+    const int r = e / IT, il = e % IT;
+    const int b = b0 + r, i = i0 + il;
+    const bool ok = b < B && i < IN;
+    const float xv = ok ? to_f32(x[(size_t)b * IN + i]) : 0.f;
+    float phi[KM];
+    basis_features<KM, (KM + 8 < KF_MAX_NT ? KM + 8 : KF_MAX_NT)>(xv, 1.f, ok ? i : 0, bs, phi);
+#pragma unroll
+    for (int k = 0; k < KM; ++k) feat[r][il][k] = ok ? phi[k] : 0.f;
+    feat[r][il][KM] = (ok && bw) ? silu_derivative(xv, m) : 0.f;
+  }
+  __syncthreads();
+  const int il = tid % IT, og0 = tid / IT;  // 4 groups of outputs in parallel
+  const int i = i0 + il;
+  if (i >= IN) return;
+  const int n_groups = (OUT + OG - 1) / OG;
+  for (int og = og0; og < n_groups; og += kThreads / IT) {
+    float cv[OG][KM], wv[OG];
+#pragma unroll
+    for (int u = 0; u < OG; ++u) {
+      const int o = og * OG + u;
+#pragma unroll
+      for (int k = 0; k < KM; ++k) cv[u][k] = (o < OUT && k < K) ? to_f32(c[((size_t)o * IN + i) * K + k]) : 0.f;
+      wv[u] = (o < OUT && bw) ? to_f32(bw[(size_t)o * IN + i]) : 0.f;
+    }
+    for (int r = 0; r < ROWS; ++r) {
+      const int b = b0 + r;
+      if (b >= B) break;
+      float fv[KM + 1];
+#pragma unroll
+      for (int k = 0; k <= KM; ++k) fv[k] = feat[r][il][k];
+#pragma unroll
+      for (int u = 0; u < OG; ++u) {
+        const int o = og * OG + u;
+        if (o < OUT) {
+          float s = wv[u] * fv[KM];
+#pragma unroll
+          for (int k = 0; k < KM; ++k) s = fmaf(cv[u][k], fv[k], s);
+          out[((size_t)b * OUT + o) * IN + i] = from_f32<T>(s);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void interval_kernel(long n, int IN, const float* __restrict__ x,
+                                                            const float* __restrict__ kc, int nk,
+                                                            int32_t* __restrict__ idx) {
+  for (long e = blockIdx.x * (long)kThreads + threadIdx.x; e < n; e += (long)gridDim.x * kThreads) {
+    const int i = (int)(e % IN);
+    idx[e] = bspline_interval(x[e], kc + (size_t)i * nk, nk);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Rational parameter gradients. Stage 1: block (group g, row chunk) sums
+// h * w * dphi/dtheta over its rows and the group's inputs; stage 2 adds the
+// row-chunk partials (fixed order: deterministic).
+constexpr int kRatRows = 256;
+constexpr int kRatMaxParams = 16;
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void rational_grad_partial(KBasis bs, int B, int IN, const T* __restrict__ x,
+                                                                  const float* __restrict__ hbuf,
+                                                                  const T* __restrict__ w, float* __restrict__ part) {
+  const int g = blockIdx.x, chunk = blockIdx.y;
+  const int nP = bs.num_deg + 1, nQ = bs.den_deg, np = nP + nQ;
+  const float* a = bs.num + (size_t)g * nP;
+  const float* c = bs.den + (size_t)g * nQ;
+  float accp[kRatMaxParams];
+#pragma unroll
+  for (int q = 0; q < kRatMaxParams; ++q) accp[q] = 0.f;
+  const int gs = bs.group_size;
+  const long n = (long)kRatRows * gs;
+  for (long e = threadIdx.x; e < n; e += kThreads) {
+    const int r = (int)(e / gs), il = (int)(e % gs);
+    const int b = chunk * kRatRows + r, i = g * gs + il;
+    if (b >= B) continue;
+    const size_t off = (size_t)b * IN + i;
+    const float xv = to_f32(x[off]);
+    const float hv = hbuf[off] * (w ? to_f32(w[off]) : 1.f);
+    const float P = poly_dj(a, nP, 0, 0, xv);
+    const float Q = poly_dj(c, nQ, 1, 0, xv);
+    const float sgn = (Q > 0.f) ? 1.f : ((Q < 0.f) ? -1.f : 0.f);
+    const float invD = 1.f / (1.f + fabsf(Q));
+    float xp = 1.f;
+    for (int q = 0; q < nP; ++q) {
+      accp[q] += hv * xp * invD;
+      xp *= xv;
+    }
+    xp = xv;
+    const float coef = -hv * P * sgn * invD * invD;
+    for (int q = 0; q < nQ; ++q) {
+      accp[nP + q] += coef * xp;
+      xp *= xv;
+    }
+  }
+  __shared__ float red[kThreads];
+  for (int q = 0; q < np; ++q) {
+    red[threadIdx.x] = accp[q];
+    __syncthreads();
+    for (int s = kThreads / 2; s > 0; s >>= 1) {
+      if ((int)threadIdx.x < s) red[threadIdx.x] += red[threadIdx.x + s];
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) part[((size_t)chunk * gridDim.x + g) * np + q] = red[0];
+    __syncthreads();
+  }
+}
+
+__global__ void rational_grad_final(int groups, int nP, int nQ, int n_chunks, const float* __restrict__ part,
+                                    float* __restrict__ dnum, float* __restrict__ dden) {
+  const int np = nP + nQ;
+  for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < groups * np; e += gridDim.x * blockDim.x) {
+    const int g = e / np, q = e % np;
+    float s = 0.f;
+    for (int ch = 0; ch < n_chunks; ++ch) s += part[((size_t)ch * groups + g) * np + q];
+    if (q < nP)
+      dnum[(size_t)g * nP + q] = s;
+    else
+      dden[(size_t)g * nQ + (q - nP)] = s;
+  }
+}
+
+}  // namespace kf

@@ -1,0 +1,106 @@
+"""ctypes binding of libkfhip.so (include/kfhip.h).
+
+The library is loaded once; a missing library is an error, never a silent
+fallback: every op of this package runs on the HIP kernels or raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from ctypes import c_char_p, c_int, c_int32, c_int64, c_size_t, c_void_p
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent.parent / "libkfhip.so"
+
+# status codes / enums of include/kfhip.h
+KF_OK = 0
+KF_F32, KF_BF16 = 0, 1
+KF_KIND_CHEB, KF_KIND_BSPLINE, KF_KIND_RATIONAL = 0, 1, 2
+KF_MAP_IDENTITY, KF_MAP_TANH = 0, 1
+KF_OP_F, KF_OP_G, KF_OP_P = 0, 1, 2
+KF_MAX_K, KF_MAX_NT = 16, 24
+
+EXPORTS = (
+    "kf_workspace_bytes",
+    "kf_F",
+    "kf_G",
+    "kf_P",
+    "kf_features",
+    "kf_edge_derivative",
+    "kf_bspline_interval",
+    "kf_rational_workspace_bytes",
+    "kf_rational_param_grad",
+    "kf_last_error",
+    "kf_version",
+)
+
+
+class KfBasis(ctypes.Structure):
+    _fields_ = [
+        ("kind", c_int32),
+        ("size", c_int32),
+        ("order", c_int32),
+        ("n_t", c_int32),
+        ("input_map", c_int32),
+        ("spline_k", c_int32),
+        ("n_knots", c_int32),
+        ("num_deg", c_int32),
+        ("den_deg", c_int32),
+        ("group_size", c_int32),
+        ("fold", c_void_p),
+        ("knots", c_void_p),
+        ("knots_cmp", c_void_p),
+        ("num", c_void_p),
+        ("den", c_void_p),
+    ]
+
+
+_lock = threading.Lock()
+_lib = None
+
+
+def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
+    """The loaded library (raises if it is missing or incomplete)."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    with _lock:
+        if _lib is not None and path is None:
+            return _lib
+        p = Path(path) if path is not None else LIB_PATH
+        if not p.exists():
+            raise RuntimeError(f"{p} is missing: build it with `python -m kanforge_amd.build` (needs hipcc)")
+        lib = ctypes.CDLL(str(p))
+        for name in EXPORTS:
+            if not hasattr(lib, name):
+                raise RuntimeError(f"{p} does not export {name}")
+        P = ctypes.POINTER(KfBasis)
+        lib.kf_workspace_bytes.argtypes = [c_int, P, c_int, c_int64, c_int64, c_int64]
+        lib.kf_workspace_bytes.restype = c_size_t
+        lib.kf_F.argtypes = [P, c_int, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]
+        lib.kf_G.argtypes = [P, c_int, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]
+        lib.kf_P.argtypes = [P, c_int, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]
+        lib.kf_features.argtypes = [P, c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p]
+        lib.kf_edge_derivative.argtypes = [P, c_int, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]
+        lib.kf_bspline_interval.argtypes = [c_int64, c_int64, c_void_p, c_void_p, c_int32, c_void_p, c_void_p]
+        lib.kf_rational_workspace_bytes.argtypes = [P, c_int64, c_int64]
+        lib.kf_rational_workspace_bytes.restype = c_size_t
+        lib.kf_rational_param_grad.argtypes = [P, c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]
+        for name in ("kf_F", "kf_G", "kf_P", "kf_features", "kf_edge_derivative", "kf_bspline_interval", "kf_rational_param_grad"):
+            getattr(lib, name).restype = c_int
+        lib.kf_last_error.argtypes = []
+        lib.kf_last_error.restype = c_char_p
+        lib.kf_version.argtypes = []
+        lib.kf_version.restype = c_char_p
+        if path is None:
+            _lib = lib
+        return lib
+
+
+def check(rc: int, what: str) -> None:
+    """Raise RuntimeError with the library's message when rc != 0."""
+    if rc != KF_OK:
+        msg = load().kf_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed ({rc}): {msg}")

@@ -1,0 +1,464 @@
+"""PyTorch side of the HIP kernels: launchers and differentiable primitives.
+
+Mirrors kanforge/torch/kernels.py: ``available``, the raw launcher ``_raw``
+(kernels.py:39-55), the autograd Functions ``_F``, ``_G``, ``_P`` that close
+F/G/P under differentiation (kernels.py:70-128), ``prim_F/prim_G/prim_P``
+and ``spline_forward`` (kernels.py:131-150). Every launch goes through the
+C ABI of libkfhip.so (include/kfhip.h) on the current HIP stream; there is
+no other execution path.
+
+Differences from the reference, by design:
+* bfloat16 and float32 run natively (no upcast); accumulation is float32;
+* ``w=None`` means ones (no ones tensor is materialised);
+* the fold R_m of Chebyshev plans is applied inside the library;
+* the rational basis has a plan; its trainable parameters receive
+  gradients through ``_F`` (first order).
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from ..kernels.plan import MAX_ORDER, KernelPlan
+from . import _lib
+
+_DTYPES = {torch.float32: _lib.KF_F32, torch.bfloat16: _lib.KF_BF16}
+_KINDS = {"cheb": _lib.KF_KIND_CHEB, "bspline": _lib.KF_KIND_BSPLINE, "rational": _lib.KF_KIND_RATIONAL}
+
+
+def available(device: torch.device) -> bool:
+    """True on a ROCm (HIP) device with libkfhip.so loadable."""
+    device = torch.device(device)
+    if device.type != "cuda" or torch.version.hip is None or not torch.cuda.is_available():
+        return False
+    try:
+        _lib.load()
+    except (RuntimeError, OSError):
+        return False
+    return True
+
+
+def _require_device(t: torch.Tensor) -> None:
+    if t.device.type != "cuda" or torch.version.hip is None:
+        raise RuntimeError(f"the HIP kernels need a ROCm GPU tensor, got a tensor on {t.device}")
+
+
+def _dtype_code(dtype: torch.dtype) -> int:
+    code = _DTYPES.get(dtype)
+    if code is None:
+        raise TypeError(f"the HIP kernels compute in float32 or bfloat16, not {dtype}")
+    return code
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+# --- basis state ---------------------------------------------------------------
+
+
+class BasisState:
+    """Device tables a plan needs besides x and the coefficients.
+
+    bspline: ``knots`` (in, nk + 2k) and ``knots_cmp`` (in, nk) float32;
+    rational: ``num`` (groups, p+1), ``den`` (groups, q) float32 and the group size.
+    """
+
+    __slots__ = ("knots", "knots_cmp", "num", "den", "group_size")
+
+    def __init__(self, knots=None, knots_cmp=None, num=None, den=None, group_size=1):
+        self.knots, self.knots_cmp = knots, knots_cmp
+        self.num, self.den, self.group_size = num, den, int(group_size)
+
+    def with_params(self, num, den) -> "BasisState":
+        return BasisState(self.knots, self.knots_cmp, num, den, self.group_size)
+
+
+def bspline_state(grid: torch.Tensor, order: int) -> BasisState:
+    """Knot tables of a per-input grid buffer (host float64 preparation)."""
+    from ..bases.spline import knot_tables
+
+    pad, cmp_ = knot_tables(grid.detach().double().cpu().numpy(), order)
+    dev = grid.device
+    return BasisState(knots=torch.from_numpy(pad).to(dev), knots_cmp=torch.from_numpy(cmp_).to(dev))
+
+
+def rational_state(num: torch.Tensor, den: torch.Tensor, group_size: int) -> BasisState:
+    return BasisState(num=num.detach().float().contiguous(), den=den.detach().float().contiguous(), group_size=group_size)
+
+
+def _desc(plan: KernelPlan, m: int, st: BasisState | None):
+    """(kf_basis struct, keep-alive objects) for derivative order m."""
+    if m > MAX_ORDER:
+        raise NotImplementedError(f"derivative order {m} > {MAX_ORDER} is not compiled into the HIP kernels")
+    d = _lib.KfBasis()
+    d.kind = _KINDS[plan.kind]
+    d.size = plan.size
+    keep = []
+    if plan.kind == "cheb":
+        degree, input_map = plan.consts
+        r = np.ascontiguousarray(plan.fold(m), dtype=np.float32)
+        keep.append(r)
+        d.order = m
+        d.n_t = r.shape[1]
+        d.input_map = _lib.KF_MAP_TANH if input_map == "tanh" else _lib.KF_MAP_IDENTITY
+        d.fold = r.ctypes.data_as(ctypes.c_void_p)
+    elif plan.kind == "bspline":
+        g, k = plan.consts
+        d.order = m
+        d.n_t = plan.size
+        d.spline_k = k
+        d.n_knots = g + 2 * k + 1
+        d.knots = st.knots.data_ptr()
+        d.knots_cmp = st.knots_cmp.data_ptr()
+    else:
+        p, q = plan.consts
+        d.order = m
+        d.n_t = 1
+        d.num_deg, d.den_deg = p, q
+        d.group_size = st.group_size
+        d.num = st.num.data_ptr()
+        d.den = st.den.data_ptr()
+    return d, keep
+
+
+# --- raw launches (no autograd) ----------------------------------------------------
+
+
+def _workspace(op: int, desc, dt: int, batch: int, n_in: int, n_out: int, device) -> torch.Tensor | None:
+    nbytes = _lib.load().kf_workspace_bytes(op, ctypes.byref(desc), dt, batch, n_in, n_out)
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def _raw(op: str, plan: KernelPlan, m: int, x, a, b, st: BasisState | None, n_out: int, h=None):
+    """op F: (x, w, c) -> y (B, out); G: (x, w, g) -> dc (out, in, K); P: (x, g, c) -> p (B, in).
+
+    ``x`` (B, in) and every other array share the dtype of ``x``; ``w`` may be None.
+    """
+    _require_device(x)
+    lib = _lib.load()
+    dt = _dtype_code(x.dtype)
+    batch, n_in = x.shape
+    desc, keep = _desc(plan, m, st)
+    dev = x.device
+    stream = _stream(dev)
+    x = x.contiguous()
+    with torch.cuda.device(dev):
+        if op == "F":
+            w, c = a, b
+            w = None if w is None else w.contiguous()
+            c = c.contiguous()
+            y = torch.empty(batch, n_out, dtype=x.dtype, device=dev)
+            ws = _workspace(_lib.KF_OP_F, desc, dt, batch, n_in, n_out, dev)
+            rc = lib.kf_F(ctypes.byref(desc), dt, batch, n_in, n_out, _ptr(x), _ptr(w), _ptr(c), _ptr(y), _ptr(ws), ws.numel(), stream)
+            _lib.check(rc, "kf_F")
+            return y
+        if op == "G":
+            w, g = a, b
+            w = None if w is None else w.contiguous()
+            g = g.contiguous()
+            dc = torch.empty(n_out, n_in, plan.size, dtype=x.dtype, device=dev)
+            ws = _workspace(_lib.KF_OP_G, desc, dt, batch, n_in, n_out, dev)
+            rc = lib.kf_G(ctypes.byref(desc), dt, batch, n_in, n_out, _ptr(x), _ptr(g), _ptr(w), _ptr(dc), _ptr(ws), ws.numel(), stream)
+            _lib.check(rc, "kf_G")
+            return dc
+        g, c = a, b
+        g, c = g.contiguous(), c.contiguous()
+        p = torch.empty(batch, n_in, dtype=x.dtype, device=dev)
+        ws = _workspace(_lib.KF_OP_P, desc, dt, batch, n_in, n_out, dev)
+        rc = lib.kf_P(ctypes.byref(desc), dt, batch, n_in, n_out, _ptr(x), _ptr(g), _ptr(c), _ptr(p), _ptr(h), _ptr(ws), ws.numel(), stream)
+        _lib.check(rc, "kf_P")
+        del keep
+        return p
+
+
+def _rational_param_grad(plan, st: BasisState, x, h, w):
+    """(d num, d den) float32 of sum_{b,i} h w phi(x) for the rational plan."""
+    lib = _lib.load()
+    desc, keep = _desc(plan, 0, st)
+    batch, n_in = x.shape
+    dev = x.device
+    dnum = torch.empty_like(st.num)
+    dden = torch.empty_like(st.den)
+    nbytes = lib.kf_rational_workspace_bytes(ctypes.byref(desc), batch, n_in)
+    ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        rc = lib.kf_rational_param_grad(
+            ctypes.byref(desc), _dtype_code(x.dtype), batch, n_in, _ptr(x.contiguous()), _ptr(h), _ptr(None if w is None else w.contiguous()),
+            _ptr(dnum), _ptr(dden), _ptr(ws), ws.numel(), _stream(dev),
+        )
+    _lib.check(rc, "kf_rational_param_grad")
+    return dnum, dden
+
+
+# --- differentiable primitives ------------------------------------------------------
+
+
+def _mul(w, t):
+    return t if w is None else w * t
+
+
+class _F(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, c, w, num, den, st, plan, m):
+        ctx.save_for_backward(x, c, w, num, den)
+        ctx.st, ctx.plan, ctx.m = st, plan, m
+        return _raw("F", plan, m, x, w, c, st, c.shape[0])
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, c, w, num, den = ctx.saved_tensors
+        st, plan, m = ctx.st, ctx.plan, ctx.m
+        need = ctx.needs_input_grad
+        gx = gc = gw = gnum = gden = None
+        gy = gy.contiguous()
+        need_theta = plan.kind == "rational" and (need[3] or need[4])
+        if need_theta:
+            if m != 0 or torch.is_grad_enabled():
+                raise NotImplementedError("rational parameter gradients are first order only on the HIP path")
+            h = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+            p1 = _raw("P", plan, m + 1, x, gy, c, st, c.shape[0], h=h)
+            if need[0]:
+                gx = _mul(w, p1)
+            dnum, dden = _rational_param_grad(plan, st, x, h, w)
+            gnum = dnum.to(num.dtype) if need[3] else None
+            gden = dden.to(den.dtype) if need[4] else None
+        elif need[0]:
+            gx = _mul(w, prim_P(x, gy, c, st, plan, m + 1))
+        if need[1]:
+            gc = prim_G(x, gy, w, st, plan, m)
+        if need[2]:
+            gw = prim_P(x, gy, c, st, plan, m)
+        return gx, gc, gw, gnum, gden, None, None, None
+
+
+class _G(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, g, w, st, plan, m):
+        ctx.save_for_backward(x, g, w)
+        ctx.st, ctx.plan, ctx.m = st, plan, m
+        return _raw("G", plan, m, x, w, g, st, g.shape[1])
+
+    @staticmethod
+    def backward(ctx, gg_out):
+        x, g, w = ctx.saved_tensors
+        st, plan, m = ctx.st, ctx.plan, ctx.m
+        need = ctx.needs_input_grad
+        gg_out = gg_out.contiguous()
+        gx = _mul(w, prim_P(x, g, gg_out, st, plan, m + 1)) if need[0] else None
+        gg = prim_F(x, gg_out, w, st, plan, m) if need[1] else None
+        gw = prim_P(x, g, gg_out, st, plan, m) if need[2] else None
+        return gx, gg, gw, None, None, None
+
+
+class _P(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, g, c, st, plan, m):
+        ctx.save_for_backward(x, g, c)
+        ctx.st, ctx.plan, ctx.m = st, plan, m
+        return _raw("P", plan, m, x, g, c, st, c.shape[0])
+
+    @staticmethod
+    def backward(ctx, gp):
+        x, g, c = ctx.saved_tensors
+        st, plan, m = ctx.st, ctx.plan, ctx.m
+        need = ctx.needs_input_grad
+        gp = gp.contiguous()
+        gx = gp * prim_P(x, g, c, st, plan, m + 1) if need[0] else None
+        gg = prim_F(x, c, gp, st, plan, m) if need[1] else None
+        gc = prim_G(x, g, gp, st, plan, m) if need[2] else None
+        return gx, gg, gc, None, None, None
+
+
+def prim_F(x, c, w, st, plan, m=0, num=None, den=None):
+    return _F.apply(x, c, w, num, den, st, plan, m)
+
+
+def prim_G(x, g, w, st, plan, m=0):
+    return _G.apply(x, g, w, st, plan, m)
+
+
+def prim_P(x, g, c, st, plan, m=0):
+    return _P.apply(x, g, c, st, plan, m)
+
+
+def spline_forward(x: torch.Tensor, coef: torch.Tensor, st: BasisState | None, plan: KernelPlan, num=None, den=None) -> torch.Tensor:
+    """sum_{i,k} coef[o,i,k] phi_k(x[..., i]) through the HIP F kernel.
+
+    Computes in the coefficients' dtype (float32 or bfloat16) and returns
+    ``x.dtype``.
+    """
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.dtype != coef.dtype:
+        x2 = x2.to(coef.dtype)
+    y = prim_F(x2, coef, None, st, plan, 0, num, den)
+    return y.to(x.dtype).reshape(*lead, coef.shape[0])
+
+
+# --- basis values and edge derivatives ---------------------------------------------
+
+
+def _features_raw(plan, m, st, x2: torch.Tensor) -> torch.Tensor:
+    _require_device(x2)
+    lib = _lib.load()
+    desc, keep = _desc(plan, m, st)
+    batch, n_in = x2.shape
+    out = torch.empty(batch, n_in, plan.size, dtype=x2.dtype, device=x2.device)
+    with torch.cuda.device(x2.device):
+        rc = lib.kf_features(ctypes.byref(desc), _dtype_code(x2.dtype), batch, n_in, _ptr(x2), _ptr(out), _stream(x2.device))
+    _lib.check(rc, "kf_features")
+    return out
+
+
+class _Features(torch.autograd.Function):
+    """phi^(m)(x) (B, in, K); d/dx is phi^(m+1)."""
+
+    @staticmethod
+    def forward(ctx, x2, st, plan, m):
+        ctx.save_for_backward(x2)
+        ctx.st, ctx.plan, ctx.m = st, plan, m
+        return _features_raw(plan, m, st, x2.contiguous())
+
+    @staticmethod
+    def backward(ctx, gphi):
+        (x2,) = ctx.saved_tensors
+        d = _Features.apply(x2, ctx.st, ctx.plan, ctx.m + 1)
+        return (gphi * d).sum(-1), None, None, None
+
+
+def basis_derivative(basis, x: torch.Tensor, m: int, params: dict | None) -> torch.Tensor:
+    """Basis.derivative on a device tensor: ``(..., in, K)`` through kf_features."""
+    from ..kernels.plan import plan_for
+
+    if not isinstance(x, torch.Tensor):
+        raise TypeError("basis evaluation runs on the GPU: pass a torch tensor on a ROCm device")
+    _require_device(x)
+    plan = plan_for(basis)
+    if plan is None:
+        raise RuntimeError(f"no HIP kernel for {basis!r}")
+    st = state_from_params(plan, basis, params, x)
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.dtype not in _DTYPES:
+        x2 = x2.float()
+    out = _Features.apply(x2, st, plan, m)
+    return out.to(x.dtype).reshape(*lead, x.shape[-1], plan.size)
+
+
+def state_from_params(plan, basis, params: dict | None, like: torch.Tensor) -> BasisState | None:
+    """BasisState from per-input parameters ``{name: (in or groups, *shape)}`` (or defaults)."""
+    n_in = like.shape[-1]
+    if plan.kind == "cheb":
+        return None
+    if plan.kind == "bspline":
+        if params is None or "grid" not in params:
+            grid = torch.as_tensor(np.broadcast_to(basis.param_specs()["grid"].value, (n_in, basis.grid_size + 1)).copy(), device=like.device)
+        else:
+            grid = torch.as_tensor(params["grid"], device=like.device)
+            grid = grid.expand(n_in, grid.shape[-1]) if grid.dim() == 1 or grid.shape[0] == 1 else grid
+        return bspline_state(grid, basis.order)
+    if params is None:
+        specs = basis.param_specs()
+        num = torch.as_tensor(specs["numerator"].value, device=like.device)[None]
+        den = torch.as_tensor(specs["denominator"].value, device=like.device)[None]
+    else:
+        num = torch.as_tensor(params["numerator"], device=like.device)
+        den = torch.as_tensor(params["denominator"], device=like.device)
+        if num.dim() == 1:
+            num, den = num[None], den[None]
+    rows = num.shape[0]
+    if n_in % rows:
+        raise ValueError(f"rational parameters have {rows} rows, which does not divide {n_in} inputs")
+    return rational_state(num, den, n_in // rows)
+
+
+def _edge_raw(plan, m, st, x2, c, base_w):
+    lib = _lib.load()
+    desc, keep = _desc(plan, m, st)
+    batch, n_in = x2.shape
+    n_out = c.shape[0]
+    out = torch.empty(batch, n_out, n_in, dtype=x2.dtype, device=x2.device)
+    with torch.cuda.device(x2.device):
+        rc = lib.kf_edge_derivative(
+            ctypes.byref(desc), _dtype_code(x2.dtype), batch, n_in, n_out, _ptr(x2), _ptr(c.contiguous()),
+            _ptr(None if base_w is None else base_w.contiguous()), _ptr(out), _stream(x2.device),
+        )
+    _lib.check(rc, "kf_edge_derivative")
+    return out
+
+
+class _Edge(torch.autograd.Function):
+    """d[b,o,i] = sum_k c[o,i,k] phi_k^(m)(x[b,i]) + W[o,i] silu^(m)(x[b,i])."""
+
+    @staticmethod
+    def forward(ctx, x2, c, base_w, st, plan, m):
+        ctx.save_for_backward(x2, c, base_w)
+        ctx.st, ctx.plan, ctx.m = st, plan, m
+        return _edge_raw(plan, m, st, x2.contiguous(), c, base_w)
+
+    @staticmethod
+    def backward(ctx, gd):
+        x2, c, base_w = ctx.saved_tensors
+        st, plan, m = ctx.st, ctx.plan, ctx.m
+        need = ctx.needs_input_grad
+        gx = gc = gw = None
+        if need[0]:
+            # d/dx of the edge is the edge derivative of order m+1
+            gx = (gd * _Edge.apply(x2, c, base_w, st, plan, m + 1)).sum(1)
+        if need[1]:
+            phi = _Features.apply(x2, st, plan, m)  # (B, in, K)
+            gc = torch.einsum("boi,bik->oik", gd, phi)
+        if need[2] and base_w is not None:
+            s = silu_derivative_t(x2, m)
+            gw = torch.einsum("boi,bi->oi", gd, s)
+        return gx, gc, gw, None, None, None
+
+
+def silu_derivative_t(x: torch.Tensor, m: int) -> torch.Tensor:
+    """d^m/dx^m silu(x) with torch ops (x p_m(s) + m p_{m-1}(s), s = sigmoid(x))."""
+    from .._calculus import SIGMOID_FACTOR, chain_polys
+
+    s = torch.sigmoid(x)
+    if m == 0:
+        return x * s
+    polys = chain_polys([0.0, 1.0], SIGMOID_FACTOR, m)
+
+    def hp(c):
+        y = torch.zeros_like(s) + float(c[-1])
+        for v in reversed(c[:-1]):
+            y = y * s + float(v)
+        return y
+
+    return x * hp(polys[m]) + m * hp(polys[m - 1])
+
+
+def edge_derivative(x: torch.Tensor, coef_eff: torch.Tensor, base_w: torch.Tensor | None, st, plan, m: int) -> torch.Tensor:
+    """(..., out, in) edge derivatives through kf_edge_derivative."""
+    _require_device(x)
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.dtype != coef_eff.dtype:
+        x2 = x2.to(coef_eff.dtype)
+    d = _Edge.apply(x2, coef_eff, base_w, st, plan, m)
+    return d.to(x.dtype).reshape(*lead, coef_eff.shape[0], x.shape[-1])
+
+
+def bspline_interval(x: torch.Tensor, knots_cmp: torch.Tensor) -> torch.Tensor:
+    """int32 interval index of float32 x (B, in) on the comparison knots (in, nk); -1 outside."""
+    _require_device(x)
+    lib = _lib.load()
+    x = x.contiguous().float()
+    kc = knots_cmp.contiguous().float()
+    out = torch.empty(x.shape, dtype=torch.int32, device=x.device)
+    with torch.cuda.device(x.device):
+        rc = lib.kf_bspline_interval(x.shape[0], x.shape[1], _ptr(x), _ptr(kc), kc.shape[1], _ptr(out), _stream(x.device))
+    _lib.check(rc, "kf_bspline_interval")
+    return out

@@ -1,0 +1,348 @@
+"""KAN layers whose spline part runs on the HIP kernels.
+
+Same constructor, parameter names, shapes and ``state_dict`` layout as
+kanforge/torch/layers.py (KANLinear :28-116, GRKAN :335-363, KAN :366-398),
+so checkpoints and ``kanforge.save`` files move between the two unchanged.
+The spline branch always takes the fused HIP path (libkfhip.so); the base
+branch F.linear(silu(x), W * mask) and the bias are torch ops on the same
+device.
+"""
+
+from __future__ import annotations
+
+import math
+from collections.abc import Callable, Sequence
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from .._layer import basis_param_values, init_stds, resolve_groups
+from ..bases import Basis, Rational, make_basis
+from ..kernels import plan_for
+from ..kernels.plan import AUTO_KINDS
+from . import kernels as _kernels
+
+BACKENDS = ("auto", "ops", "kernel")
+
+
+class KANLinear(nn.Module):
+    """One KAN layer: y_o = sum_i s_oi * phi_oi(x_i) + sum_i w_oi * act(x_i) + b_o.
+
+    Parameters (as in the reference):
+      ``coef``           ``(out, in, basis.size)``
+      ``base_weight``    ``(out, in)``, absent if ``base_activation`` is None
+      ``bias``           ``(out,)``, absent if ``bias=False``
+      ``edge_scale``     ``(out, in)``, only with ``edge_scale=True``
+      ``basis_<name>``   trainable basis parameters ``(groups, *shape)``
+    Buffers: ``basis_<name>`` grids ``(in, *shape)``; ``edge_mask``,
+    ``sym_code``, ``sym_params``.
+
+    ``backend``: ``"auto"`` and ``"kernel"`` run the HIP kernels; the
+    plain-ops route (``"ops"``) is not part of this build and raises.
+    """
+
+    def __init__(
+        self,
+        in_features: int,
+        out_features: int,
+        basis: str | dict | Basis = "bspline",
+        *,
+        bias: bool = True,
+        base_activation: Callable[[torch.Tensor], torch.Tensor] | None = F.silu,
+        groups: int | None = None,
+        edge_scale: bool = False,
+        grid_ranges=None,
+        coef_init: str = "normal",
+        coef_init_std: float = 0.1,
+        edge_dropout: float = 0.0,
+        backend: str = "auto",
+        device=None,
+        dtype=None,
+    ):
+        super().__init__()
+        if not 0 <= edge_dropout < 1:
+            raise ValueError("edge_dropout must be in [0, 1)")
+        factory = {"device": device, "dtype": dtype}
+        self.in_features = in_features
+        self.out_features = out_features
+        self.basis = make_basis(basis)
+        self.base_activation = base_activation
+        self.groups = resolve_groups(in_features, groups)
+        self.coef_init = coef_init
+        self.coef_init_std = coef_init_std
+        self.edge_dropout = edge_dropout
+        if backend not in BACKENDS:
+            raise ValueError(f"backend must be one of {BACKENDS}")
+        self.backend = backend
+        self._grid_ranges = grid_ranges
+        self._init_kwargs = {
+            "basis": self.basis,
+            "bias": bias,
+            "base_activation": base_activation,
+            "groups": groups,
+            "edge_scale": edge_scale,
+            "coef_init": coef_init,
+            "coef_init_std": coef_init_std,
+            "edge_dropout": edge_dropout,
+            "backend": backend,
+        }
+        init_stds(self.basis, in_features, out_features, coef_init, coef_init_std, base_activation is not None)
+        self.coef = nn.Parameter(torch.empty(out_features, in_features, self.basis.size, **factory))
+        if base_activation is not None:
+            self.base_weight = nn.Parameter(torch.empty(out_features, in_features, **factory))
+        else:
+            self.register_parameter("base_weight", None)
+        if bias:
+            self.bias = nn.Parameter(torch.empty(out_features, **factory))
+        else:
+            self.register_parameter("bias", None)
+        if edge_scale:
+            self.edge_scale = nn.Parameter(torch.empty(out_features, in_features, **factory))
+        else:
+            self.register_parameter("edge_scale", None)
+        self.register_buffer("edge_mask", torch.empty(out_features, in_features, **factory))
+        self.register_buffer("sym_code", torch.empty(out_features, in_features, dtype=torch.int32, device=device))
+        self.register_buffer("sym_params", torch.empty(out_features, in_features, 4, **factory))
+        self._trainable_names: list[str] = []
+        self._buffer_names: list[str] = []
+        self._state_cache = None
+        self._mask_cache = None
+        self.reset_parameters()
+
+    # --- parameters -------------------------------------------------------------
+
+    def _set_basis_state(self, trainable: dict, buffers: dict) -> None:
+        for name in self._trainable_names + self._buffer_names:
+            delattr(self, f"basis_{name}")
+        like = {"dtype": self.coef.dtype, "device": self.coef.device}
+        for name, value in trainable.items():
+            self.register_parameter(f"basis_{name}", nn.Parameter(torch.as_tensor(np.ascontiguousarray(value), **like)))
+        for name, value in buffers.items():
+            self.register_buffer(f"basis_{name}", torch.as_tensor(np.ascontiguousarray(value), **like))
+        self._trainable_names, self._buffer_names = list(trainable), list(buffers)
+        self._plan = plan_for(self.basis)
+        self._state_cache = None
+
+    def reset_parameters(self) -> None:
+        coef_std, base_std = init_stds(
+            self.basis, self.in_features, self.out_features, self.coef_init, self.coef_init_std, self.base_weight is not None
+        )
+        nn.init.normal_(self.coef, std=coef_std) if coef_std else nn.init.zeros_(self.coef)
+        if self.base_weight is not None:
+            if base_std is None:
+                nn.init.kaiming_uniform_(self.base_weight, a=math.sqrt(5))
+            else:
+                nn.init.normal_(self.base_weight, std=base_std)
+        if self.bias is not None:
+            nn.init.zeros_(self.bias)
+        if self.edge_scale is not None:
+            nn.init.ones_(self.edge_scale)
+        self.edge_mask.fill_(1.0)
+        self.sym_code.fill_(-1)
+        self.sym_params.zero_()
+        self._sym_codes = ()
+        self._set_basis_state(*basis_param_values(self.basis, self.groups, self.in_features, self._grid_ranges))
+
+    def basis_params(self) -> dict[str, torch.Tensor]:
+        """Basis parameters and buffers expanded to ``(in, *shape)`` (or ``(1, *shape)``)."""
+        rep = self.in_features // self.groups
+        out = {}
+        for name in self._trainable_names:
+            p = getattr(self, f"basis_{name}")
+            out[name] = p if self.groups in (1, self.in_features) else p.repeat_interleave(rep, dim=0)
+        for name in self._buffer_names:
+            out[name] = getattr(self, f"basis_{name}")
+        return out
+
+    def _mask_is_ones(self) -> bool:
+        m = self.edge_mask
+        key = (m.data_ptr(), m._version, m.device)
+        if self._mask_cache is None or self._mask_cache[0] != key:
+            self._mask_cache = (key, bool((m == 1).all()))
+        return self._mask_cache[1]
+
+    def effective_coef(self) -> torch.Tensor:
+        if self.edge_scale is None and self._mask_is_ones():
+            return self.coef
+        scale = self.edge_mask if self.edge_scale is None else self.edge_scale * self.edge_mask
+        return self.coef * scale[..., None]
+
+    def effective_base_weight(self) -> torch.Tensor | None:
+        if self.base_weight is None:
+            return None
+        return self.base_weight if self._mask_is_ones() else self.base_weight * self.edge_mask
+
+    # --- computation ------------------------------------------------------------
+
+    def _basis_state(self):
+        """Device tables of the plan (cached per grid version for B-splines)."""
+        plan = self._plan
+        if plan.kind == "cheb":
+            return None
+        if plan.kind == "bspline":
+            grid = self.basis_grid
+            key = (grid.data_ptr(), grid._version, grid.device, grid.dtype)
+            if self._state_cache is None or self._state_cache[0] != key:
+                self._state_cache = (key, _kernels.bspline_state(grid, self.basis.order))
+            return self._state_cache[1]
+        num, den = self.basis_numerator, self.basis_denominator
+        return _kernels.rational_state(num, den, self.in_features // num.shape[0])
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.training and self.edge_dropout > 0:
+            edges = self.edge_derivative(x, 0)
+            keep = torch.rand_like(edges) >= self.edge_dropout
+            y = (edges * keep).sum(-1) / (1 - self.edge_dropout)
+            return y if self.bias is None else y + self.bias
+        self.uses_kernel(x.device)  # raises when the HIP path cannot run
+        st = self._basis_state()
+        if self._plan.kind == "rational":
+            y = _kernels.spline_forward(x, self.effective_coef(), st, self._plan, self.basis_numerator, self.basis_denominator)
+        else:
+            y = _kernels.spline_forward(x, self.effective_coef(), st, self._plan)
+        if self.base_weight is not None:
+            y = y + F.linear(self.base_activation(x), self.effective_base_weight())
+        if self._sym_codes:
+            raise NotImplementedError("symbolic edges are not part of the HIP path")
+        if self.bias is not None:
+            y = y + self.bias
+        return y
+
+    def uses_kernel(self, device: torch.device) -> bool:
+        """Whether forward runs the fused kernel on ``device`` (always, or an error)."""
+        if self.backend == "ops":
+            raise RuntimeError("backend='ops' (plain torch ops) is not part of the HIP build; use 'auto' or 'kernel'")
+        if self._plan is None:
+            raise RuntimeError(f"no fused kernel for this basis: {self.basis!r}")
+        if not _kernels.available(device):
+            raise RuntimeError(f"no fused kernel for device {device}: the HIP kernels need a ROCm GPU and libkfhip.so")
+        if self.backend == "auto" and self._plan.kind not in AUTO_KINDS.get(torch.device(device).type, ()):
+            raise RuntimeError(f"no fused kernel for plan kind {self._plan.kind} on {device}")
+        return True
+
+    def edge_derivative(self, x: torch.Tensor, order: int = 1) -> torch.Tensor:
+        """d^order phi_oi / dx_i^order for every edge, shape ``(..., out, in)``
+        (kanforge/torch/layers.py:206-226), through kf_edge_derivative."""
+        if order < 0:
+            raise ValueError("order must be >= 0")
+        self.uses_kernel(x.device)
+        bw = self.effective_base_weight()
+        if bw is not None and order > 0 and self.base_activation is not F.silu:
+            raise NotImplementedError("analytic derivatives need base_activation=F.silu or None")
+        if bw is not None and order == 0 and self.base_activation is not F.silu:
+            raise NotImplementedError("the HIP edge kernel evaluates the SiLU base branch only")
+        if self._sym_codes:
+            raise NotImplementedError("symbolic edges are not part of the HIP path")
+        return _kernels.edge_derivative(x, self.effective_coef(), bw, self._basis_state(), self._plan, int(order))
+
+    # --- state import / export (kanforge.save format) ------------------------------
+
+    @staticmethod
+    def _to_numpy(x) -> np.ndarray:
+        return x.detach().cpu().double().numpy() if isinstance(x, torch.Tensor) else np.asarray(x)
+
+    def _export_full(self) -> dict:
+        named = {**dict(self.named_parameters(recurse=False)), **dict(self.named_buffers(recurse=False))}
+        out = {k: self._to_numpy(v) for k, v in named.items()}
+        out.update({k: None for k in ("base_weight", "bias", "edge_scale") if getattr(self, k) is None})
+        return out
+
+    @torch.no_grad()
+    def _import_full(self, state: dict) -> None:
+        for name, value in state.items():
+            t = getattr(self, name, None)
+            if value is None or t is None:
+                continue
+            if tuple(t.shape) != tuple(np.shape(value)):
+                raise ValueError(f"{name}: shape {np.shape(value)} does not fit {tuple(t.shape)}")
+            t.copy_(torch.as_tensor(value, dtype=t.dtype, device=t.device))
+        self._refresh_symbolic()
+
+    def _refresh_symbolic(self) -> None:
+        codes = np.unique(self.sym_code.detach().cpu().numpy().astype(int))
+        self._sym_codes = tuple(int(c) for c in codes if c >= 0)
+
+    def _load_from_state_dict(self, *args, **kwargs):
+        super()._load_from_state_dict(*args, **kwargs)
+        self._refresh_symbolic()
+
+    def extra_repr(self) -> str:
+        groups = "" if self.groups == self.in_features else f", groups={self.groups}"
+        return f"in_features={self.in_features}, out_features={self.out_features}, basis={self.basis!r}{groups}"
+
+
+class GRKAN(KANLinear):
+    """Group-rational KAN layer of KAT (kanforge/torch/layers.py:335-363)."""
+
+    def __init__(
+        self,
+        in_features: int,
+        out_features: int,
+        *,
+        groups: int = 8,
+        num_degree: int = 5,
+        den_degree: int = 4,
+        init: str = "gelu",
+        bias: bool = True,
+        device=None,
+        dtype=None,
+    ):
+        super().__init__(
+            in_features,
+            out_features,
+            Rational(num_degree, den_degree, init),
+            bias=bias,
+            base_activation=None,
+            groups=groups,
+            coef_init="variance",
+            device=device,
+            dtype=dtype,
+        )
+
+
+class KAN(nn.Sequential):
+    """Stack of ``KANLinear`` layers (kanforge/torch/layers.py:366-398)."""
+
+    def __init__(self, widths: Sequence[int], basis: str | dict | Basis = "bspline", grid_ranges=None, **layer_kwargs):
+        if len(widths) < 2:
+            raise ValueError("widths needs at least input and output size")
+        super().__init__(
+            *(
+                KANLinear(a, b, basis, grid_ranges=grid_ranges if k == 0 else None, **layer_kwargs)
+                for k, (a, b) in enumerate(zip(widths[:-1], widths[1:]))
+            )
+        )
+        self.widths = list(widths)
+
+    def edge_derivative(self, x: torch.Tensor, order: int = 1) -> list[torch.Tensor]:
+        """Per-layer edge derivatives at the activations each layer receives."""
+        return [layer.edge_derivative(h, order) for layer, h in layer_inputs(self, x)]
+
+
+def rebuild_kan(layers: Sequence[KANLinear]) -> KAN:
+    """A ``KAN`` made of existing layers."""
+    model = KAN.__new__(KAN)
+    nn.Sequential.__init__(model, *layers)
+    model.widths = [layers[0].in_features] + [layer.out_features for layer in layers]
+    return model
+
+
+def layer_inputs(model: nn.Module, x: torch.Tensor) -> list[tuple[KANLinear, torch.Tensor]]:
+    """(KANLinear, the input it receives) for every KAN layer of ``model``
+    (kanforge/torch/layers.py:446-467)."""
+    out = []
+
+    def walk(m, h):
+        if isinstance(m, KANLinear):
+            out.append((m, h))
+            return m(h)
+        if isinstance(m, nn.Sequential):
+            for sub in m:
+                h = walk(sub, h)
+            return h
+        return m(h)
+
+    walk(model, x)
+    return out

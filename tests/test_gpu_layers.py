@@ -1,0 +1,194 @@
+"""KANLinear / GRKAN / KAN on the HIP path against the float64 oracle:
+values, every first-order gradient, higher input derivatives through the
+F/G/P closure, the gradient penalty (double backward into coef), and the
+chained PINN Laplacian."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import kanforge_amd as kf
+from cases import BASES, oracle_basis, rounded
+from kanforge_amd.torch import GRKAN, KAN, KANLinear, laplacian
+from oracle import kan64 as o
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2}
+
+
+def np64(t):
+    return t.detach().float().cpu().double().numpy()
+
+
+def make_layer(name, IN, OUT, dtype, seed=0, edge_scale=True, base=True):
+    torch.manual_seed(seed)
+    layer = KANLinear(IN, OUT, BASES[name], edge_scale=edge_scale, base_activation=torch.nn.functional.silu if base else None)
+    with torch.no_grad():
+        layer.coef.normal_(0, 0.5 / math.sqrt(IN))
+        if edge_scale:
+            layer.edge_scale.uniform_(0.5, 1.5)
+        if layer.bias is not None:
+            layer.bias.normal_()
+        if name.startswith("bspline"):
+            rng = np.random.default_rng(seed)
+            from cases import random_grid
+
+            layer.basis_grid.copy_(torch.as_tensor(random_grid(IN, BASES[name].grid_size + 1, rng)))
+    return layer.to(device=DEV, dtype=dtype)
+
+
+def oracle_of(layer):
+    params = None
+    if layer._plan.kind == "bspline":
+        params = {"grid": np64(layer.basis_grid)}
+    elif layer._plan.kind == "rational":
+        params = {"num": np64(layer.basis_numerator), "den": np64(layer.basis_denominator)}
+    return oracle_basis(layer.basis, layer.in_features, params)
+
+
+LAYER_CASES = ["chebyshev8", "jacobi6", "legendre_identity", "bspline53", "bspline41"]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("name", LAYER_CASES)
+def test_layer_forward_and_gradients(name, dtype):
+    B, IN, OUT = 77, 24, 19
+    layer = make_layer(name, IN, OUT, dtype)
+    ob = oracle_of(layer)
+    rng = np.random.default_rng(1)
+    x0 = rng.uniform(-0.95, 0.95, (B, IN))
+    gy0 = rng.normal(0, 1, (B, OUT))
+    x = torch.as_tensor(x0, dtype=torch.float32).to(DEV, dtype).requires_grad_()
+    gy = torch.as_tensor(gy0, dtype=torch.float32).to(DEV, dtype)
+    y = layer(x)
+    assert y.dtype == dtype and y.shape == (B, OUT)
+    y.backward(gy)
+
+    xr, gyr = rounded(x0, dtype), rounded(gy0, dtype)
+    c, s, W, b = np64(layer.coef), np64(layer.edge_scale), np64(layer.base_weight), np64(layer.bias)
+    want_y = o.kan_linear(xr, c, ob, W, b, s)
+    assert o.normwise_err(np64(y), want_y) <= TOL[dtype]
+    ceff = c * s[..., None]
+    want_gx = o.prim_P(xr, gyr, ceff, ob, 1) + (gyr @ W) * o.silu_derivative(xr, 1)
+    G0 = o.prim_G(xr, gyr, None, ob, 0)
+    checks = {
+        "x": (x.grad, want_gx),
+        "coef": (layer.coef.grad, G0 * s[..., None]),
+        "edge_scale": (layer.edge_scale.grad, (G0 * c).sum(-1)),
+        "base_weight": (layer.base_weight.grad, gyr.T @ o.silu_derivative(xr, 0)),
+        "bias": (layer.bias.grad, gyr.sum(0)),
+    }
+    tol = TOL[dtype] if dtype == torch.float32 else 3e-2  # bf16 grads round the upstream chain twice
+    for key, (got, want) in checks.items():
+        assert o.normwise_err(np64(got), want) <= tol, key
+
+
+@pytest.mark.parametrize("name", ["chebyshev5", "jacobi_ab", "bspline53", "taylor"])
+def test_higher_input_derivatives_and_gradient_penalty(name):
+    # what tests/test_kernels.py:102-121 checks, here against float64
+    B, IN, OUT = 37, 4, 5
+    layer = make_layer(name, IN, OUT, torch.float32, edge_scale=False)
+    ob = oracle_of(layer)
+    rng = np.random.default_rng(2)
+    x0 = rng.uniform(-0.9, 0.9, (B, IN))
+    x = torch.as_tensor(x0, dtype=torch.float32, device=DEV).requires_grad_()
+    wts = torch.linspace(-1, 1, OUT, device=DEV)
+    loss = (layer(x) * wts).sum()
+    (gx,) = torch.autograd.grad(loss, x, create_graph=True)
+    (gxx,) = torch.autograd.grad(gx.sum(), x, create_graph=True)
+    (gxxx,) = torch.autograd.grad(gxx.sum(), x, create_graph=True)
+    (gc,) = torch.autograd.grad((gx**2).sum(), layer.coef)
+    xr = rounded(x0, torch.float32)
+    gyr = np.broadcast_to(np64(wts), (B, OUT))
+    c, W = np64(layer.coef), np64(layer.base_weight)
+    for m, got in ((1, gx), (2, gxx), (3, gxxx)):
+        want = o.prim_P(xr, gyr, c, ob, m) + (gyr @ W) * o.silu_derivative(xr, m)
+        assert o.normwise_err(np64(got), want) <= 2e-5, m
+    gx64 = o.prim_P(xr, gyr, c, ob, 1) + (gyr @ W) * o.silu_derivative(xr, 1)
+    want_gc = 2 * o.prim_G(xr, gyr, gx64, ob, 1)
+    assert o.normwise_err(np64(gc), want_gc) <= 2e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("name,order", [("chebyshev8", 0), ("chebyshev8", 2), ("bspline53", 1), ("jacobi6", 2)])
+def test_layer_edge_derivative(name, order, dtype):
+    B, IN, OUT = 50, 12, 7
+    layer = make_layer(name, IN, OUT, dtype)
+    ob = oracle_of(layer)
+    x0 = np.random.default_rng(3).uniform(-0.9, 0.9, (B, IN))
+    x = torch.as_tensor(x0, dtype=torch.float32).to(DEV, dtype)
+    d = layer.edge_derivative(x, order)
+    assert d.shape == (B, OUT, IN)
+    ceff = np64(layer.coef) * np64(layer.edge_scale)[..., None]
+    want = o.edge_derivative(rounded(x0, dtype), ceff, ob, order, np64(layer.base_weight))
+    assert o.normwise_err(np64(d), want) <= TOL[dtype]
+    if order == 0 and dtype == torch.float32:
+        # sum over inputs plus bias is the layer output (tests/test_layers.py:62-63)
+        np.testing.assert_allclose(np64(d.sum(-1) + layer.bias), np64(layer(x)), atol=2e-5)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_grkan_forward_and_all_gradients(dtype):
+    B, IN, OUT = 96, 32, 40
+    torch.manual_seed(0)
+    layer = GRKAN(IN, OUT, groups=8)
+    with torch.no_grad():
+        layer.basis_numerator.add_(0.05 * torch.randn_like(layer.basis_numerator))
+        layer.basis_denominator.add_(0.05 * torch.randn_like(layer.basis_denominator))
+        layer.bias.normal_()
+    layer = layer.to(DEV, dtype)
+    rng = np.random.default_rng(4)
+    x0, gy0 = rng.normal(0, 1, (B, IN)), rng.normal(0, 1, (B, OUT))
+    x = torch.as_tensor(x0, dtype=torch.float32).to(DEV, dtype).requires_grad_()
+    y = layer(x)
+    y.backward(torch.as_tensor(gy0, dtype=torch.float32).to(DEV, dtype))
+    num, den = np64(layer.basis_numerator), np64(layer.basis_denominator)
+    ob = o.Basis64("rational", num=np.repeat(num, IN // 8, 0), den=np.repeat(den, IN // 8, 0))
+    xr, gyr = rounded(x0, dtype), rounded(gy0, dtype)
+    c = np64(layer.coef)
+    tol = TOL[dtype] if dtype == torch.float32 else 3e-2
+    assert o.normwise_err(np64(y), o.kan_linear(xr, c, ob, None, np64(layer.bias))) <= TOL[dtype]
+    assert o.normwise_err(np64(x.grad), o.prim_P(xr, gyr, c, ob, 1)) <= tol
+    assert o.normwise_err(np64(layer.coef.grad), o.prim_G(xr, gyr, None, ob, 0)) <= tol
+    h = gyr @ c[..., 0]  # (B, IN)
+    dn, dd = o.rational_param_grads(xr, ob.kw["num"], ob.kw["den"])
+    want_n = np.einsum("bi,bij->ij", h, dn).reshape(8, -1, 6).sum(1)
+    want_d = np.einsum("bi,bij->ij", h, dd).reshape(8, -1, 4).sum(1)
+    assert o.normwise_err(np64(layer.basis_numerator.grad), want_n) <= tol
+    assert o.normwise_err(np64(layer.basis_denominator.grad), want_d) <= tol
+
+
+def _chained_second_derivative(layers, x, dim):
+    """Forward-mode (h, h', h'') through KAN layers in float64."""
+    h = x
+    hp = np.zeros_like(x)
+    hp[:, dim] = 1.0
+    hpp = np.zeros_like(x)
+    for lay in layers:
+        ob, ceff, W, b = lay
+        e0 = o.edge_derivative(h, ceff, ob, 0, W)
+        e1 = o.edge_derivative(h, ceff, ob, 1, W)
+        e2 = o.edge_derivative(h, ceff, ob, 2, W)
+        h_new = e0.sum(-1) + b
+        hp_new = np.einsum("boi,bi->bo", e1, hp)
+        hpp_new = np.einsum("boi,bi->bo", e2, hp**2) + np.einsum("boi,bi->bo", e1, hpp)
+        h, hp, hpp = h_new, hp_new, hpp_new
+    return hpp[:, 0]
+
+
+def test_pinn_laplacian_matches_forward_mode_oracle():
+    torch.manual_seed(0)
+    model = KAN([2, 16, 16, 1], kf.Jacobi(6, 0.5, 0.5)).to(DEV)
+    rng = np.random.default_rng(5)
+    x0 = rng.uniform(-1, 1, (300, 2))
+    x = torch.as_tensor(x0, dtype=torch.float32, device=DEV)
+    lap = laplacian(model, x)
+    layers = []
+    for lay in model:
+        layers.append((oracle_of(lay), np64(lay.coef), np64(lay.base_weight), np64(lay.bias)))
+    xr = rounded(x0, torch.float32)
+    want = sum(_chained_second_derivative(layers, xr, d) for d in range(2))
+    assert o.normwise_err(np64(lap), want) <= 5e-5

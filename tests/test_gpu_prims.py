@@ -1,0 +1,188 @@
+"""Parity of the HIP primitives (through the C ABI) with the float64 oracle.
+
+Every case feeds the device and the oracle the same seeded, dtype-rounded
+inputs. Tolerances (normwise max|d|/max|ref|): float32 1e-5, bfloat16 2e-2;
+B-spline interval indices bit-exact.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from cases import BASES, oracle_basis, random_grid, rounded, to_dev
+from kanforge_amd.kernels import plan_for
+from kanforge_amd.torch import kernels as K
+from oracle import kan64 as o
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2}
+DTYPES = [torch.float32, torch.bfloat16]
+SHAPES = [(150, 45, 70), (256, 64, 128)]
+
+
+def setup(name, B, IN, seed=0):
+    rng = np.random.default_rng(seed)
+    basis = BASES[name]
+    plan = plan_for(basis)
+    params, st = None, None
+    if plan.kind == "bspline":
+        grid = random_grid(IN, basis.grid_size + 1, rng)
+        params = {"grid": grid}
+        st = K.bspline_state(torch.as_tensor(grid, device="cuda"), basis.order)
+        x = rng.uniform(-1.15, 1.15, (B, IN))
+    elif plan.kind == "rational":
+        groups = math.gcd(IN, 5) if IN % 5 == 0 else 1
+        num = rounded(rng.normal(0, math.sqrt(0.1), (groups, 6)), torch.float32)
+        den = rounded(rng.normal(0, math.sqrt(0.1), (groups, 4)), torch.float32)
+        params = {"num": num, "den": den}
+        st = K.rational_state(torch.as_tensor(num, device="cuda"), torch.as_tensor(den, device="cuda"), IN // groups)
+        x = rng.normal(0, 1, (B, IN))
+    else:
+        x = rng.normal(0, 1, (B, IN)) * (0.6 if basis.input_map == "identity" else 1.0)
+    return basis, plan, st, oracle_basis(basis, IN, params), x, rng
+
+
+def err(got, want):
+    return o.normwise_err(got.detach().float().cpu().double().numpy(), want)
+
+
+PRIM_CASES = [
+    ("chebyshev8", 0), ("chebyshev8", 1), ("chebyshev8", 2),
+    ("legendre_identity", 0), ("legendre_identity", 1),
+    ("jacobi6", 0), ("jacobi6", 2),
+    ("gram", 1),
+    ("bspline53", 0), ("bspline53", 1), ("bspline53", 3), ("bspline53", 4),
+    ("bspline41", 0), ("bspline20", 0),
+    ("rational", 0), ("rational", 1), ("rational", 2),
+]  # fmt: skip
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16"])
+@pytest.mark.parametrize("shape", SHAPES, ids=["ragged", "aligned"])
+@pytest.mark.parametrize("name,m", PRIM_CASES)
+def test_F_matches_oracle(name, m, shape, dtype):
+    B, IN, OUT = shape
+    basis, plan, st, ob, x, rng = setup(name, B, IN)
+    Kb = basis.size
+    c = rng.normal(0, 1 / math.sqrt(IN * Kb), (OUT, IN, Kb))
+    for weighted in (False, True):
+        w = rng.uniform(0.5, 1.5, (B, IN)) if weighted else None
+        y = K._raw("F", plan, m, to_dev(x, dtype), None if w is None else to_dev(w, dtype), to_dev(c, dtype), st, OUT)
+        want = o.prim_F(rounded(x, dtype), rounded(c, dtype), None if w is None else rounded(w, dtype), ob, m)
+        e = err(y, want)
+        assert e <= TOL[dtype], (name, m, weighted, e)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16"])
+@pytest.mark.parametrize("shape", SHAPES, ids=["ragged", "aligned"])
+@pytest.mark.parametrize("name,m", PRIM_CASES)
+def test_G_matches_oracle(name, m, shape, dtype):
+    B, IN, OUT = shape
+    basis, plan, st, ob, x, rng = setup(name, B, IN, seed=1)
+    g = rng.normal(0, 1, (B, OUT))
+    for weighted in (False, True):
+        w = rng.uniform(0.5, 1.5, (B, IN)) if weighted else None
+        dc = K._raw("G", plan, m, to_dev(x, dtype), None if w is None else to_dev(w, dtype), to_dev(g, dtype), st, OUT)
+        want = o.prim_G(rounded(x, dtype), rounded(g, dtype), None if w is None else rounded(w, dtype), ob, m)
+        assert dc.shape == want.shape
+        e = err(dc, want)
+        assert e <= TOL[dtype], (name, m, weighted, e)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16"])
+@pytest.mark.parametrize("shape", SHAPES, ids=["ragged", "aligned"])
+@pytest.mark.parametrize("name,m", PRIM_CASES)
+def test_P_matches_oracle(name, m, shape, dtype):
+    B, IN, OUT = shape
+    basis, plan, st, ob, x, rng = setup(name, B, IN, seed=2)
+    Kb = basis.size
+    c = rng.normal(0, 1 / math.sqrt(IN * Kb), (OUT, IN, Kb))
+    g = rng.normal(0, 1, (B, OUT))
+    p = K._raw("P", plan, m, to_dev(x, dtype), to_dev(g, dtype), to_dev(c, dtype), st, OUT)
+    want = o.prim_P(rounded(x, dtype), rounded(g, dtype), rounded(c, dtype), ob, m)
+    e = err(p, want)
+    assert e <= TOL[dtype], (name, m, e)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16"])
+@pytest.mark.parametrize("name,m", PRIM_CASES + [("chebyshev8", 5), ("bspline83", 2)])
+def test_features_match_oracle(name, m, dtype):
+    basis, plan, st, ob, x, rng = setup(name, 97, 13, seed=3)
+    phi = K._features_raw(plan, m, st, to_dev(x, dtype))
+    want = ob(rounded(x, dtype), m)
+    assert phi.shape == want.shape
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert err(phi, want) <= tol
+
+
+@pytest.mark.parametrize("name", ["bspline53", "bspline83", "bspline41", "bspline20"])
+def test_bspline_interval_bit_exact(name):
+    rng = np.random.default_rng(4)
+    basis = BASES[name]
+    IN = 7
+    grid = random_grid(IN, basis.grid_size + 1, rng, -0.8, 1.3)
+    t = o.extend_grid(grid, basis.order)  # float64 knots (IN, nk)
+    # points on, one float32 ulp around, and between every knot, plus far outside and NaN
+    t32 = t.astype(np.float32)
+    cols = [t32, np.nextafter(t32, np.float32(-np.inf)), np.nextafter(t32, np.float32(np.inf))]
+    mids = ((t[:, 1:] + t[:, :-1]) / 2).astype(np.float32)
+    far = np.tile(np.array([-1e6, 1e6, np.nan], np.float32), (IN, 1))
+    xt = np.concatenate(cols + [mids, far], 1)  # (IN, n)
+    x = np.ascontiguousarray(xt.T)  # (n, IN)
+    st = K.bspline_state(torch.as_tensor(grid, device="cuda"), basis.order)
+    got = K.bspline_interval(torch.as_tensor(x, device="cuda"), st.knots_cmp).cpu().numpy()
+    want = np.stack([o.bspline_interval(x[:, i].astype(np.float64), t[i]) for i in range(IN)], 1)
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16"])
+@pytest.mark.parametrize("name,m", [("chebyshev8", 0), ("chebyshev8", 2), ("jacobi6", 2), ("bspline53", 1), ("rational", 1), ("legendre_identity", 2)])
+@pytest.mark.parametrize("base", [False, True])
+def test_edge_derivative_matches_oracle(name, m, base, dtype):
+    B, IN, OUT = 83, 70, 9
+    basis, plan, st, ob, x, rng = setup(name, B, IN, seed=5)
+    c = rng.normal(0, 0.5, (OUT, IN, basis.size))
+    bw = rng.normal(0, 0.5, (OUT, IN)) if base else None
+    d = K._edge_raw(plan, m, st, to_dev(x, dtype), to_dev(c, dtype), None if bw is None else to_dev(bw, dtype))
+    want = o.edge_derivative(rounded(x, dtype), rounded(c, dtype), ob, m, None if bw is None else rounded(bw, dtype))
+    assert d.shape == want.shape
+    assert err(d, want) <= TOL[dtype]
+
+
+def test_rational_param_grad_matches_oracle():
+    B, IN, OUT = 300, 40, 24
+    basis, plan, st, ob, x, rng = setup("rational", B, IN, seed=6)
+    c = rng.normal(0, 0.3, (OUT, IN, 1))
+    g = rng.normal(0, 1, (B, OUT))
+    w = rng.uniform(0.5, 1.5, (B, IN))
+    xd = to_dev(x, torch.float32)
+    h = torch.empty(B, IN, dtype=torch.float32, device="cuda")
+    K._raw("P", plan, 1, xd, to_dev(g, torch.float32), to_dev(c, torch.float32), st, OUT, h=h)
+    hw = np.einsum("bo,oi->bi", rounded(g, torch.float32), rounded(c, torch.float32)[..., 0])
+    assert o.normwise_err(h.cpu().double().numpy(), hw) <= 1e-5
+    dnum, dden = K._rational_param_grad(plan, st, xd, h, to_dev(w, torch.float32))
+    xr = rounded(x, torch.float32)
+    gn, gd = o.rational_param_grads(xr, ob.kw["num"], ob.kw["den"])
+    wr = rounded(w, torch.float32)
+    groups = st.num.shape[0]
+    want_n = np.einsum("bi,bij->ij", hw * wr, gn).reshape(groups, -1, gn.shape[-1]).sum(1)
+    want_d = np.einsum("bi,bij->ij", hw * wr, gd).reshape(groups, -1, gd.shape[-1]).sum(1)
+    assert o.normwise_err(dnum.cpu().double().numpy(), want_n) <= 1e-5
+    assert o.normwise_err(dden.cpu().double().numpy(), want_d) <= 1e-5
+
+
+def test_zero_batch_and_errors():
+    basis, plan, st, ob, x, rng = setup("chebyshev8", 4, 8)
+    xd = torch.zeros(0, 8, device="cuda")
+    c = torch.randn(5, 8, 9, device="cuda")
+    y = K._raw("F", plan, 0, xd, None, c, st, 5)
+    assert y.shape == (0, 5)
+    dc = K._raw("G", plan, 0, xd, None, torch.zeros(0, 5, device="cuda"), st, 5)
+    assert dc.shape == (5, 8, 9) and float(dc.abs().max()) == 0.0
+    with pytest.raises(TypeError):
+        K._raw("F", plan, 0, torch.zeros(3, 8, device="cuda", dtype=torch.float16), None, c.half(), st, 5)
+    with pytest.raises(NotImplementedError):
+        K._raw("F", plan, 9, torch.zeros(3, 8, device="cuda"), None, c, st, 5)
