@@ -110,19 +110,50 @@ KBasis to_kbasis(const kf_basis* b) {
 
 int nt_bucket(int n) { return n <= 4 ? 4 : n <= 8 ? 8 : n <= 12 ? 12 : n <= 16 ? 16 : 24; }
 
-struct WsF {
-  int64_t INP, OUTP, BP;
-  size_t cfm, phi, total;
+// F tile configurations: (BM, BN, waves along M, waves along N), 512 threads.
+struct FCfg {
+  int bm, bn, wm, wn;
 };
-WsF ws_f(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out) {
+constexpr FCfg F_CFGS[] = {{256, 192, 4, 2}, {256, 256, 2, 4}, {256, 128, 4, 2}};
+constexpr int N_CUS = 256;
+
+// The configuration with the fewest tile-area x dispatch rounds (whole-GPU
+// waves of 256 workgroups); ties keep the larger tile.
+int pick_f_cfg(int64_t batch, int64_t n_out) {
+  int best = 0;
+  double best_cost = 1e300;
+  for (int k = 0; k < 3; ++k) {
+    const FCfg& c = F_CFGS[k];
+    int64_t tiles = ((batch + c.bm - 1) / c.bm) * ((n_out + c.bn - 1) / c.bn);
+    int64_t rounds = (tiles + N_CUS - 1) / N_CUS;
+    double cost = (double)rounds * c.bm * c.bn;
+    if (cost < best_cost * 0.999) {
+      best = k;
+      best_cost = cost;
+    }
+  }
+  return best;
+}
+
+struct WsF {
+  int cfg;
+  int64_t INP, OUTP, BP;
+  size_t cfm, z, wz, phi, total;
+};
+WsF ws_f(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, bool has_w) {
   WsF w;
+  w.cfg = pick_f_cfg(batch, n_out);
+  const FCfg& c = F_CFGS[w.cfg];
   w.INP = round_up(n_in, CHUNK);
-  w.OUTP = round_up(n_out, F_BN);
-  w.BP = round_up(batch, F_BM);
+  w.OUTP = round_up(n_out, c.bn);
+  w.BP = round_up(batch, c.bm);
   const int es = elt_size(dtype);
+  const bool cheb = b->kind == KF_KIND_CHEB;
   w.cfm = align256((size_t)b->n_t * w.OUTP * w.INP * es);
-  w.phi = b->kind == KF_KIND_CHEB ? 0 : align256((size_t)w.BP * b->n_t * w.INP * es);
-  w.total = w.cfm + w.phi;
+  w.z = cheb ? align256((size_t)w.BP * w.INP * sizeof(float)) : 0;
+  w.wz = cheb && has_w ? align256((size_t)w.BP * w.INP * sizeof(float)) : 0;
+  w.phi = cheb ? 0 : align256((size_t)w.BP * b->n_t * w.INP * es);
+  w.total = w.cfm + w.z + w.wz + w.phi;
   return w;
 }
 struct WsP {
@@ -204,38 +235,10 @@ int launch_features(const KBasis& kb, int64_t batch, int64_t n_in, int64_t brows
   return check_launch("features");
 }
 
-template <typename T>
-int run_F(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
-          const void* w, const void* c, void* y, void* ws, hipStream_t s) {
-  WsF L = ws_f(b, dtype, batch, n_in, n_out);
-  char* base = (char*)ws;
-  void* cfm = base;
-  void* phi = base + L.cfm;
-  int rc = launch_permute<T>(kb, n_out, n_in, L.OUTP, L.INP, c, cfm, false, s);
-  if (rc) return rc;
-  dim3 grid((unsigned)(L.OUTP / F_BN), (unsigned)(L.BP / F_BM));
-  if (kb.kind == KF_KIND_CHEB) {
-    if (w) return fail(KF_EUNSUPPORTED, "internal: weighted cheb F handled by the generator");
-    hipLaunchKernelGGL((f_kernel<T, F_BM, F_BN, 2, 2, true>), grid, dim3(kThreads), 0, s, kb, (int)batch, (int)n_in,
-                       (int)n_out, (int)L.INP, (int)L.OUTP, (const T*)x, (const T*)nullptr, (const T*)cfm,
-                       (const T*)nullptr, (T*)y);
-  } else {
-    // phi_fm[b][j][i] (BP, n_t, INP), features already multiplied by w when given
-    rc = launch_features<T, false>(kb, batch, n_in, L.BP, L.INP, x, phi, (long)kb.n_t * L.INP, (long)L.INP, 1L,
-                                   false, s);
-    if (rc) return rc;
-    hipLaunchKernelGGL((f_kernel<T, F_BM, F_BN, 2, 2, false>), grid, dim3(kThreads), 0, s, kb, (int)batch,
-                       (int)n_in, (int)n_out, (int)L.INP, (int)L.OUTP, (const T*)x, (const T*)nullptr,
-                       (const T*)cfm, (const T*)phi, (T*)y);
-  }
-  return check_launch("F");
-}
-
 }  // namespace
 
-// weighted F: the generator multiplies by w; non-cheb kinds multiply the
-// precomputed features (a separate small kernel).
 namespace kf {
+// Multiplies precomputed features phi[b][j][i] by w[b][i] (weighted F, non-Chebyshev kinds).
 template <typename T>
 __global__ __launch_bounds__(kThreads) void scale_phi_kernel(int B, int IN, int n_t, int INP, const T* __restrict__ w,
                                                              T* __restrict__ phi) {
@@ -249,24 +252,60 @@ __global__ __launch_bounds__(kThreads) void scale_phi_kernel(int B, int IN, int 
 }  // namespace kf
 
 namespace {
+
+template <typename T, int BM, int BN, int WMW, int WNW, bool CHEB, bool HAS_W>
+int launch_f_t(const WsF& L, int64_t batch, int64_t n_out, int n_t, const float* z, const float* wz, const void* cfm,
+               const void* phi, void* y, hipStream_t s) {
+  const int n_m = (int)(L.BP / BM), n_n = (int)(L.OUTP / BN);
+  const int rs = 32 * (int)sizeof(T) + 16;
+  const size_t lds = (size_t)2 * (BM + BN) * rs;
+  auto kern = f_kernel<T, BM, BN, WMW, WNW, CHEB, HAS_W>;
+  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+    return fail(KF_ELAUNCH, "F: cannot reserve %zu bytes of LDS", lds);
+  hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(WMW * WNW * 64), lds, s, (int)batch, (int)n_out, (int)L.INP,
+                     (int)L.OUTP, n_t, z, wz, (const T*)cfm, (const T*)phi, (T*)y);
+  return check_launch("F");
+}
+
+template <typename T, bool CHEB, bool HAS_W>
+int launch_f_cfg(const WsF& L, int64_t batch, int64_t n_out, int n_t, const float* z, const float* wz, const void* cfm,
+                 const void* phi, void* y, hipStream_t s) {
+  switch (L.cfg) {
+    case 0: return launch_f_t<T, 256, 192, 4, 2, CHEB, HAS_W>(L, batch, n_out, n_t, z, wz, cfm, phi, y, s);
+    case 1: return launch_f_t<T, 256, 256, 2, 4, CHEB, HAS_W>(L, batch, n_out, n_t, z, wz, cfm, phi, y, s);
+    default: return launch_f_t<T, 256, 128, 4, 2, CHEB, HAS_W>(L, batch, n_out, n_t, z, wz, cfm, phi, y, s);
+  }
+}
+
 template <typename T>
-int run_F_weighted(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out,
-                   const void* x, const void* w, const void* c, void* y, void* ws, hipStream_t s) {
-  WsF L = ws_f(b, dtype, batch, n_in, n_out);
+int run_F(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
+          const void* w, const void* c, void* y, void* ws, hipStream_t s) {
+  const bool has_w = w != nullptr;
+  const bool cheb = kb.kind == KF_KIND_CHEB;
+  WsF L = ws_f(b, dtype, batch, n_in, n_out, has_w);
   char* base = (char*)ws;
   void* cfm = base;
+  float* z = (float*)(base + L.cfm);
+  float* wz = has_w && cheb ? (float*)(base + L.cfm + L.z) : nullptr;
+  void* phi = base + L.cfm + L.z + L.wz;
   int rc = launch_permute<T>(kb, n_out, n_in, L.OUTP, L.INP, c, cfm, false, s);
   if (rc) return rc;
-  dim3 grid((unsigned)(L.OUTP / F_BN), (unsigned)(L.BP / F_BM));
-  if (kb.kind == KF_KIND_CHEB) {
-    hipLaunchKernelGGL((f_kernel<T, F_BM, F_BN, 2, 2, true>), grid, dim3(kThreads), 0, s, kb, (int)batch, (int)n_in,
-                       (int)n_out, (int)L.INP, (int)L.OUTP, (const T*)x, (const T*)w, (const T*)cfm,
-                       (const T*)nullptr, (T*)y);
-  } else {
-    void* phi = base + L.cfm;
-    rc = launch_features<T, false>(kb, batch, n_in, L.BP, L.INP, x, phi, (long)kb.n_t * L.INP, (long)L.INP, 1L,
-                                   false, s);
+  if (cheb) {
+    long n = (long)L.BP * L.INP;
+    long blocks = (n + kThreads - 1) / kThreads;
+    if (blocks > 65535 * 4) blocks = 65535 * 4;
+    hipLaunchKernelGGL(zmap_kernel<T>, dim3((unsigned)blocks), dim3(kThreads), 0, s, (int)batch, (int)n_in, (int)L.BP,
+                       (int)L.INP, kb.input_map, (const T*)x, (const T*)w, z, wz);
+    rc = check_launch("zmap");
     if (rc) return rc;
+    if (has_w) return launch_f_cfg<T, true, true>(L, batch, n_out, kb.n_t, z, wz, cfm, nullptr, y, s);
+    return launch_f_cfg<T, true, false>(L, batch, n_out, kb.n_t, z, nullptr, cfm, nullptr, y, s);
+  }
+  // precomputed features phi_fm[b][j][i] (BP, n_t, INP)
+  rc = launch_features<T, false>(kb, batch, n_in, L.BP, L.INP, x, phi, (long)kb.n_t * L.INP, (long)L.INP, 1L, false,
+                                 s);
+  if (rc) return rc;
+  if (has_w) {
     long n = (long)batch * kb.n_t * L.INP;
     long blocks = (n + kThreads - 1) / kThreads;
     if (blocks > 65535 * 4) blocks = 65535 * 4;
@@ -275,11 +314,8 @@ int run_F_weighted(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch
                          kb.n_t, (int)L.INP, (const T*)w, (T*)phi);
     rc = check_launch("scale_phi");
     if (rc) return rc;
-    hipLaunchKernelGGL((f_kernel<T, F_BM, F_BN, 2, 2, false>), grid, dim3(kThreads), 0, s, kb, (int)batch,
-                       (int)n_in, (int)n_out, (int)L.INP, (int)L.OUTP, (const T*)x, (const T*)nullptr,
-                       (const T*)cfm, (const T*)phi, (T*)y);
   }
-  return check_launch("F");
+  return launch_f_cfg<T, false, false>(L, batch, n_out, kb.n_t, nullptr, nullptr, cfm, phi, y, s);
 }
 
 template <typename T, int NTB>
@@ -366,7 +402,7 @@ const char* kf_version(void) { return "kfhip 0.1.0 gfx950"; }
 size_t kf_workspace_bytes(int op, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out) {
   if (validate_common(b, dtype, batch, n_in, n_out)) return 0;
   switch (op) {
-    case KF_OP_F: return ws_f(b, dtype, batch, n_in, n_out).total;
+    case KF_OP_F: return ws_f(b, dtype, batch, n_in, n_out, true).total;
     case KF_OP_P: return ws_p(b, dtype, n_in, n_out).total;
     case KF_OP_G: return ws_g(dtype, batch, n_out).total;
     default: return 0;
@@ -382,15 +418,12 @@ int kf_F(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
   hipStream_t s = (hipStream_t)stream;
   if (n_in == 0) return dtype == KF_BF16 ? zero_fill<bf16>(y, (long)batch * n_out, s) : zero_fill<float>(y, (long)batch * n_out, s);
   if (!x || !c || !y) return fail(KF_EINVAL, "kf_F: NULL array");
-  size_t need = ws_f(b, dtype, batch, n_in, n_out).total;
+  size_t need = ws_f(b, dtype, batch, n_in, n_out, w != nullptr).total;
   if (!workspace || workspace_bytes < need)
     return fail(KF_EWORKSPACE, "kf_F: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
   KBasis kb = to_kbasis(b);
-  if (dtype == KF_BF16)
-    return w ? run_F_weighted<bf16>(kb, b, dtype, batch, n_in, n_out, x, w, c, y, workspace, s)
-             : run_F<bf16>(kb, b, dtype, batch, n_in, n_out, x, w, c, y, workspace, s);
-  return w ? run_F_weighted<float>(kb, b, dtype, batch, n_in, n_out, x, w, c, y, workspace, s)
-           : run_F<float>(kb, b, dtype, batch, n_in, n_out, x, w, c, y, workspace, s);
+  if (dtype == KF_BF16) return run_F<bf16>(kb, b, dtype, batch, n_in, n_out, x, w, c, y, workspace, s);
+  return run_F<float>(kb, b, dtype, batch, n_in, n_out, x, w, c, y, workspace, s);
 }
 
 int kf_G(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* g,

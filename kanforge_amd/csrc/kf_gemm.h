@@ -68,3 +68,48 @@ __device__ __forceinline__ u32x4 gload16(const void* p, bool ok) {
 }
 
 }  // namespace kf
+
+namespace kf {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// 32x32 tiles. A 16-byte lane fragment covers 32 bytes of the reduction
+// dimension across the two lane halves h = lane / 32:
+//   bf16: one v_mfma_f32_32x32x16_bf16 (lane supplies 8 consecutive elements);
+//   f32 : four v_mfma_f32_32x32x2_f32; instruction q takes element q of each
+//         lane, so lane halves contribute elements q and 4 + q.
+// Accumulator element r of lane l is D[(r%4) + 8*(r/4) + 4*(l/32)][l % 32].
+template <typename T>
+__device__ __forceinline__ void mma32(f32x16& acc, const u32x4& a, const u32x4& b);
+
+template <>
+__device__ __forceinline__ void mma32<bf16>(f32x16& acc, const u32x4& a, const u32x4& b) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), acc, 0,
+                                                 0, 0);
+}
+
+template <>
+__device__ __forceinline__ void mma32<float>(f32x16& acc, const u32x4& a, const u32x4& b) {
+  const f32x4 af = __builtin_bit_cast(f32x4, a);
+  const f32x4 bf = __builtin_bit_cast(f32x4, b);
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[0], bf[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[1], bf[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[2], bf[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[3], bf[3], acc, 0, 0, 0);
+}
+
+__device__ __forceinline__ int acc_row(int r, int lane) { return (r & 3) + 8 * (r >> 2) + 4 * (lane >> 5); }
+
+// Workgroup index -> (m tile, n tile), XCD aware: hardware dispatches
+// consecutive workgroups round-robin over the 8 XCDs, so workgroup g runs
+// on XCD g % 8. Each XCD is given a contiguous range of the row-major tile
+// order, so the tiles sharing operand panels meet in the same L2.
+__device__ __forceinline__ void xcd_tile(int g, int n_m, int n_n, int& tm, int& tn) {
+  const int total = n_m * n_n;
+  int logical = g;
+  if (total % 8 == 0) logical = (g % 8) * (total / 8) + g / 8;
+  tm = logical / n_n;
+  tn = logical % n_n;
+}
+
+}  // namespace kf

@@ -115,122 +115,216 @@ __global__ __launch_bounds__(kThreads) void features_kernel(KBasis bs, int B, in
 }
 
 // ---------------------------------------------------------------------------
-// F: y[b,o] = sum over chunks of 32 inputs, features j:  A_j[b][i] * Cfm[j][o][i]
-// A_j is generated in LDS from x (Chebyshev recurrence, CHEB) or copied from
-// the precomputed feature tensor phi_fm[b][j][i] (other kinds).
-template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, bool CHEB>
-__global__ __launch_bounds__(kThreads) void f_kernel(KBasis bs, int B, int IN, int OUT, int INP, int OUTP,
-                                                     const T* __restrict__ x, const T* __restrict__ w,
-                                                     const T* __restrict__ cfm, const T* __restrict__ phi_fm,
-                                                     T* __restrict__ y) {
-  constexpr int KGE = KG<T>::elems, PL = KG<T>::per_lane;
+// Input map prepass: z[b][i] = g(x[b][i]) (tanh or identity) and, when w is
+// given, wz[b][i] = w[b][i], both float32, zero-padded to (BP, INP). The
+// contraction kernels read z instead of re-evaluating tanh for every output
+// tile that shares the row.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void zmap_kernel(int B, int IN, int BP, int INP, int input_map,
+                                                        const T* __restrict__ x, const T* __restrict__ w,
+                                                        float* __restrict__ z, float* __restrict__ wz) {
+  const long n = (long)BP * INP;
+  for (long e = blockIdx.x * (long)kThreads + threadIdx.x; e < n; e += (long)gridDim.x * kThreads) {
+    const int i = (int)(e % INP), b = (int)(e / INP);
+    const bool ok = b < B && i < IN;
+    const size_t off = (size_t)b * IN + i;
+    z[e] = ok ? cheb_map(to_f32(x[off]), input_map) : 0.f;
+    if (wz) wz[e] = ok ? to_f32(w[off]) : 0.f;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// F: y[b,o] = sum over input chunks of 32 and kernel features j of
+//            A_j[b][i] * Cfm[j][o][i],  A_j[b][i] = w[b,i] f_j(x[b,i]).
+// One stage = one feature of one chunk (32 reduction elements). A_j is
+// produced in LDS by every thread for the stage after the one the MFMAs
+// consume (double buffer, one barrier per stage):
+//   CHEB : Chebyshev recurrence T_j = 2 z T_{j-1} - T_{j-2} from z = g(x),
+//          one feature per stage, state (2z, T_{j-1}, T_{j-2}) in registers;
+//   else : rows of the precomputed features phi_fm[b][j][i].
+// WG tile BM x BN, WAVES_M x WAVES_N waves, 32x32 MFMA tiles.
+template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, bool CHEB, bool HAS_W>
+__global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void f_kernel(int B, int OUT, int INP, int OUTP, int n_t,
+                                                                 const float* __restrict__ z,
+                                                                 const float* __restrict__ wz,
+                                                                 const T* __restrict__ cfm,
+                                                                 const T* __restrict__ phi_fm, T* __restrict__ y) {
+  constexpr int NTH = WAVES_M * WAVES_N * 64;
   constexpr int IC = 32;
-  constexpr int STR = IC + 16 / (int)sizeof(T);  // row stride (elements), +16 bytes against bank conflicts
-  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N, TM = WM / 16, TN = WN / 16;
-  constexpr int TPR = kThreads / BM;  // generator threads per A row
-  constexpr int EPT = IC / TPR;       // elements per generator thread
-  static_assert(WAVES_M * WAVES_N * 64 == kThreads, "4 waves");
-  static_assert(EPT * sizeof(T) % 16 == 0, "generator writes 16-byte chunks");
+  constexpr int RB = IC * (int)sizeof(T);  // bytes of one stage row
+  constexpr int RS = RB + 16;              // LDS row stride in bytes (+16: conflict-free 16-byte reads)
+  constexpr int FS = RB / 32;              // fragment steps per stage
+  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N, TM = WM / 32, TN = WN / 32;
+  constexpr int TPR = NTH / BM;  // generator threads per A row
+  constexpr int EPT = IC / TPR;  // A elements per generator thread
+  constexpr int PL = 16 / (int)sizeof(T);
+  constexpr int BCH = BN * (RB / 16);  // 16-byte chunks of one B stage
+  constexpr int BPT = (BCH + NTH - 1) / NTH;
+  static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile is a multiple of 32");
+  static_assert(NTH % BM == 0 && EPT % PL == 0, "generator mapping");
 
-  __shared__ __attribute__((aligned(16))) T As[BM * STR];
-  __shared__ __attribute__((aligned(16))) T Bs[BN * STR];
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  unsigned char* As = smem;                  // [2][BM][RS]
+  unsigned char* Bs = smem + 2 * BM * RS;    // [2][BN][RS]
 
-  const int b0 = blockIdx.y * BM, o0 = blockIdx.x * BN;
-  const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+  const int n_m = (B + BM - 1) / BM, n_n = OUTP / BN;
+  int tm_, tn_;
+  xcd_tile(blockIdx.x, n_m, n_n, tm_, tn_);
+  const int b0 = tm_ * BM, o0 = tn_ * BN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
-  const int h = lane / 16, l16 = lane % 16;
-  const int n_t = bs.n_t;
+  const int h = lane >> 5, l32 = lane & 31;
 
-  f32x4 acc[TM][TN];
+  f32x16 acc[TM][TN];
 #pragma unroll
   for (int a = 0; a < TM; ++a)
 #pragma unroll
-    for (int c = 0; c < TN; ++c) acc[a][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < TN; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[a][c][r] = 0.f;
 
-  // generator state (CHEB): row gr, inputs gc*EPT .. +EPT of the chunk
+  // generator: row gr, inputs gc*EPT .. +EPT of the chunk
   const int gr = tid / TPR, gc = tid % TPR;
-  const int gb = b0 + gr;
-  float z2[EPT], tp[EPT], tc[EPT];
+  const float* zrow = z + (size_t)(b0 + gr) * INP + gc * EPT;
+  const float* wrow = HAS_W ? wz + (size_t)(b0 + gr) * INP + gc * EPT : nullptr;
+  float z2[EPT], tp[EPT], tc[EPT], zn[EPT], wn_[HAS_W ? EPT : 1];
 
   const int n_chunks = INP / IC;
-  for (int ch = 0; ch < n_chunks; ++ch) {
-    const int i0 = ch * IC;
+  const int S = n_chunks * n_t;
+
+  auto load_chunk = [&](int ch) {
     if (CHEB) {
 #pragma unroll
-      for (int e = 0; e < EPT; ++e) {
-        const int i = i0 + gc * EPT + e;
-        const bool ok = gb < B && i < IN;
-        const float xv = ok ? to_f32(x[(size_t)gb * IN + i]) : 0.f;
-        const float wv = ok ? (w ? to_f32(w[(size_t)gb * IN + i]) : 1.f) : 0.f;
-        const float z = cheb_map(xv, bs.input_map);
-        z2[e] = 2.f * z;
-        tp[e] = wv;      // T_0 * w
-        tc[e] = wv * z;  // T_1 * w
+      for (int q = 0; q < EPT / 4; ++q) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(zrow + ch * IC + 4 * q);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) zn[4 * q + u] = v[u];
+        if (HAS_W) {
+          const f32x4 wv = *reinterpret_cast<const f32x4*>(wrow + ch * IC + 4 * q);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) wn_[4 * q + u] = wv[u];
+        }
       }
     }
-    for (int j = 0; j < n_t; ++j) {
-      __syncthreads();  // previous step's MFMAs are done with As/Bs
-      // --- A tile
+  };
+  // feature j of the current chunk into f (advances the recurrence state)
+  auto gen = [&](int j, float* f) {
+    if (j == 0) {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        const float wv = HAS_W ? wn_[e] : 1.f;
+        z2[e] = 2.f * zn[e];
+        tp[e] = wv;
+        tc[e] = wv * zn[e];
+        f[e] = tp[e];
+      }
+    } else if (j == 1) {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) f[e] = tc[e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        const float nt = fmaf(z2[e], tc[e], -tp[e]);
+        tp[e] = tc[e];
+        tc[e] = nt;
+        f[e] = nt;
+      }
+    }
+  };
+  auto store_a = [&](int buf, const float* f) {
+    unsigned char* dst = As + (size_t)(buf * BM + gr) * RS + gc * EPT * (int)sizeof(T);
+#pragma unroll
+    for (int q = 0; q < EPT / PL; ++q) lds_write16(dst + 16 * q, pack16<T>(&f[q * PL]));
+  };
+  auto copy_a = [&](int buf, int ch, int j) {  // precomputed features
+    for (int e = tid; e < BM * (RB / 16); e += NTH) {
+      const int r = e / (RB / 16), q = e % (RB / 16);
+      const T* src = phi_fm + ((size_t)(b0 + r) * n_t + j) * INP + ch * IC + q * PL;
+      lds_write16(As + (size_t)(buf * BM + r) * RS + 16 * q, gload16(src, true));
+    }
+  };
+  u32x4 bst[BPT];
+  auto load_b = [&](int ch, int j) {
+#pragma unroll
+    for (int u = 0; u < BPT; ++u) {
+      const int e = tid + u * NTH;
+      const int ec = e < BCH ? e : BCH - 1;
+      const int r = ec / (RB / 16), q = ec % (RB / 16);
+      const T* src = cfm + ((size_t)j * OUTP + o0 + r) * INP + ch * IC + q * PL;
+      bst[u] = gload16(src, e < BCH);
+    }
+  };
+  auto store_b = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < BPT; ++u) {
+      const int e = tid + u * NTH;
+      const int r = e / (RB / 16), q = e % (RB / 16);
+      if (e < BCH) lds_write16(Bs + (size_t)(buf * BN + r) * RS + 16 * q, bst[u]);
+    }
+  };
+
+  // prologue: stage 0 into buffer 0
+  {
+    load_chunk(0);
+    load_b(0, 0);
+    if (CHEB) {
+      float f[EPT];
+      gen(0, f);
+      store_a(0, f);
+    } else {
+      copy_a(0, 0, 0);
+    }
+    store_b(0);
+  }
+  __syncthreads();
+
+  for (int s = 0; s < S; ++s) {
+    const int buf = s & 1;
+    const int ch = s / n_t, j = s - ch * n_t;
+    const bool more = s + 1 < S;
+    const int ch1 = (j + 1 == n_t) ? ch + 1 : ch, j1 = (j + 1 == n_t) ? 0 : j + 1;
+    if (more) {
+      load_b(ch1, j1);
+      if (CHEB && j == 0 && ch + 1 < n_chunks) load_chunk(ch + 1);
+    }
+    // MFMAs on this stage
+#pragma unroll
+    for (int fs = 0; fs < FS; ++fs) {
+      u32x4 af[TM], bfr[TN];
+#pragma unroll
+      for (int a = 0; a < TM; ++a)
+        af[a] = lds_read16(As + (size_t)(buf * BM + wm * WM + a * 32 + l32) * RS + fs * 32 + h * 16);
+#pragma unroll
+      for (int c = 0; c < TN; ++c)
+        bfr[c] = lds_read16(Bs + (size_t)(buf * BN + wn * WN + c * 32 + l32) * RS + fs * 32 + h * 16);
+#pragma unroll
+      for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int c = 0; c < TN; ++c) mma32<T>(acc[a][c], af[a], bfr[c]);
+    }
+    // next stage's operands into the other buffer
+    if (more) {
       if (CHEB) {
         float f[EPT];
-#pragma unroll
-        for (int e = 0; e < EPT; ++e) {
-          if (j == 0) {
-            f[e] = tp[e];
-          } else if (j == 1) {
-            f[e] = tc[e];
-          } else {
-            const float nt = fmaf(z2[e], tc[e], -tp[e]);
-            tp[e] = tc[e];
-            tc[e] = nt;
-            f[e] = nt;
-          }
-        }
-#pragma unroll
-        for (int q = 0; q < EPT / PL; ++q) lds_write16(&As[gr * STR + gc * EPT + q * PL], pack16<T>(&f[q * PL]));
+        gen(j1, f);
+        store_a(buf ^ 1, f);
       } else {
-        // copy phi_fm[b][j][i0 .. i0+32] rows
-        constexpr int CPR = IC / PL;  // 16-byte chunks per row
-        for (int e = tid; e < BM * CPR; e += kThreads) {
-          const int r = e / CPR, q = e % CPR;
-          const T* src = phi_fm + ((size_t)(b0 + r) * n_t + j) * INP + i0 + q * PL;
-          lds_write16(&As[r * STR + q * PL], gload16(src, true));
-        }
+        copy_a(buf ^ 1, ch1, j1);
       }
-      // --- B tile: cfm[j][o0 + n][i0 .. i0+32]
-      {
-        constexpr int CPR = IC / PL;
-        for (int e = tid; e < BN * CPR; e += kThreads) {
-          const int r = e / CPR, q = e % CPR;
-          const T* src = cfm + ((size_t)j * OUTP + o0 + r) * INP + i0 + q * PL;
-          lds_write16(&Bs[r * STR + q * PL], gload16(src, true));
-        }
-      }
-      __syncthreads();
-      // --- MFMA
-#pragma unroll
-      for (int kg = 0; kg < IC / KGE; ++kg) {
-        u32x4 af[TM], bfr[TN];
-#pragma unroll
-        for (int a = 0; a < TM; ++a) af[a] = lds_read16(&As[(wm * WM + a * 16 + l16) * STR + kg * KGE + h * PL]);
-#pragma unroll
-        for (int c = 0; c < TN; ++c) bfr[c] = lds_read16(&Bs[(wn * WN + c * 16 + l16) * STR + kg * KGE + h * PL]);
-#pragma unroll
-        for (int a = 0; a < TM; ++a)
-#pragma unroll
-          for (int c = 0; c < TN; ++c) mma<T>(acc[a][c], af[a], bfr[c]);
-      }
+      store_b(buf ^ 1);
     }
+    __syncthreads();
   }
-  // --- epilogue
+
+  // epilogue
 #pragma unroll
   for (int a = 0; a < TM; ++a)
 #pragma unroll
     for (int c = 0; c < TN; ++c) {
-      const int o = o0 + wn * WN + c * 16 + l16;
+      const int o = o0 + wn * WN + c * 32 + l32;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int b = b0 + wm * WM + a * 16 + 4 * h + r;
+      for (int r = 0; r < 16; ++r) {
+        const int b = b0 + wm * WM + a * 32 + acc_row(r, lane);
         if (b < B && o < OUT) y[(size_t)b * OUT + o] = from_f32<T>(acc[a][c][r]);
       }
     }
