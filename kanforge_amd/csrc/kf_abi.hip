@@ -34,9 +34,6 @@ inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 inline int elt_size(int dtype) { return dtype == KF_BF16 ? 2 : 4; }
 
 // tile constants shared by workspace sizing and launches
-constexpr int F_BM = 128, F_BN = 128;
-constexpr int P_BM = 128;
-constexpr int G_BM = 128, G_BC = 64;
 constexpr int CHUNK = 32;
 
 int validate_basis(const kf_basis* b) {
@@ -156,28 +153,54 @@ WsF ws_f(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
   w.total = w.cfm + w.z + w.wz + w.phi;
   return w;
 }
+// P / G configurations. The waves split the features in two groups of
+// FW = ceil(n_t / 2) (FW in {2,3,4,5,6,8,12}); TM 32-row tiles per wave keep
+// the accumulators at <= 192 registers. P: 4x2 waves (512 threads, 64-byte
+// stages); G: 2x2 waves (256 threads, 128-byte stages, 64 from FW = 8).
+constexpr int FW_LIST[] = {2, 3, 4, 5, 6, 8, 12};
+int fw_index(int n_t) {
+  const int need = (n_t + 1) / 2;
+  for (int k = 0; k < 7; ++k)
+    if (FW_LIST[k] >= need) return k;
+  return 6;
+}
+int p_tm(int fw) { return fw <= 5 ? 2 : 1; }
+int g_tm(int fw) { return fw <= 6 ? 2 : 1; }
+int g_rb(int fw) { return fw <= 6 ? 128 : 64; }
+
 struct WsP {
+  int cfg;
   int64_t INP, OUTP;
   size_t cfmt, total;
 };
 WsP ws_p(const kf_basis* b, int dtype, int64_t n_in, int64_t n_out) {
   WsP w;
-  w.INP = round_up(n_in, 16);
+  w.cfg = fw_index(b->n_t);
+  w.INP = round_up(n_in, 32);
   w.OUTP = round_up(n_out, 32);
   w.cfmt = align256((size_t)b->n_t * w.INP * w.OUTP * elt_size(dtype));
   w.total = w.cfmt;
   return w;
 }
 struct WsG {
-  int64_t OUTP, BP;
-  size_t gt, total;
+  int cfg;
+  int64_t OUTP, BP, INP;
+  size_t gt, zt, wt, total;
 };
-WsG ws_g(int dtype, int64_t batch, int64_t n_out) {
+WsG ws_g(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, bool has_w) {
   WsG w;
-  w.OUTP = round_up(n_out, G_BM);
-  w.BP = round_up(batch, G_BC);
+  w.cfg = fw_index(b->n_t);
+  const int fw = FW_LIST[w.cfg];
+  const int bm = 2 * g_tm(fw) * 32;
+  const int eps = g_rb(fw) / elt_size(dtype);
+  w.OUTP = round_up(n_out, bm);
+  w.BP = round_up(batch, eps);
+  w.INP = round_up(n_in, 32);
+  const bool cheb = b->kind == KF_KIND_CHEB;
   w.gt = align256((size_t)w.OUTP * w.BP * elt_size(dtype));
-  w.total = w.gt;
+  w.zt = cheb ? align256((size_t)w.INP * w.BP * sizeof(float)) : 0;
+  w.wt = cheb && has_w ? align256((size_t)w.INP * w.BP * sizeof(float)) : 0;
+  w.total = w.gt + w.zt + w.wt;
   return w;
 }
 
@@ -318,11 +341,19 @@ int run_F(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
   return launch_f_cfg<T, false, false>(L, batch, n_out, kb.n_t, nullptr, nullptr, cfm, phi, y, s);
 }
 
-template <typename T, int NTB>
-void launch_p_t(const KBasis& kb, dim3 grid, hipStream_t s, int64_t batch, int64_t n_in, int64_t n_out, int64_t INP,
-                int64_t OUTP, const void* x, const void* g, const void* cfmt, void* p, float* h) {
-  hipLaunchKernelGGL((p_kernel<T, NTB, P_BM>), grid, dim3(kThreads), 0, s, kb, (int)batch, (int)n_in, (int)n_out,
-                     (int)INP, (int)OUTP, (const T*)x, (const T*)g, (const T*)cfmt, (T*)p, h);
+template <typename T, int WMW, int WJW, int TM, int FW>
+int launch_p_t(const WsP& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out,
+               const void* x, const void* g, const void* cfmt, void* p, float* h) {
+  constexpr int BM = WMW * TM * 32, NMAX = WJW * FW * 32, RS = 64 + 16;
+  const size_t lds_ops = (size_t)2 * (BM + NMAX) * RS, lds_red = (size_t)WJW * BM * 33 * 4;
+  const size_t lds = lds_ops > lds_red ? lds_ops : lds_red;
+  auto kern = p_kernel<T, WMW, WJW, TM, FW>;
+  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+    return fail(KF_ELAUNCH, "P: cannot reserve %zu bytes of LDS", lds);
+  const int n_m = (int)((batch + BM - 1) / BM), n_n = (int)(L.INP / 32);
+  hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(WMW * WJW * 64), lds, s, kb, (int)batch, (int)n_in, (int)n_out,
+                     (int)L.INP, (int)L.OUTP, (const T*)x, (const T*)g, (const T*)cfmt, (T*)p, h);
+  return check_launch("P");
 }
 
 template <typename T>
@@ -332,43 +363,69 @@ int run_P(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
   void* cfmt = ws;
   int rc = launch_permute<T>(kb, n_out, n_in, L.OUTP, L.INP, c, cfmt, true, s);
   if (rc) return rc;
-  dim3 grid((unsigned)(L.INP / 16), (unsigned)((batch + P_BM - 1) / P_BM));
-  switch (nt_bucket(kb.n_t)) {
-    case 4: launch_p_t<T, 4>(kb, grid, s, batch, n_in, n_out, L.INP, L.OUTP, x, g, cfmt, p, h); break;
-    case 8: launch_p_t<T, 8>(kb, grid, s, batch, n_in, n_out, L.INP, L.OUTP, x, g, cfmt, p, h); break;
-    case 12: launch_p_t<T, 12>(kb, grid, s, batch, n_in, n_out, L.INP, L.OUTP, x, g, cfmt, p, h); break;
-    case 16: launch_p_t<T, 16>(kb, grid, s, batch, n_in, n_out, L.INP, L.OUTP, x, g, cfmt, p, h); break;
-    default: launch_p_t<T, 24>(kb, grid, s, batch, n_in, n_out, L.INP, L.OUTP, x, g, cfmt, p, h); break;
+  switch (L.cfg) {
+    case 0: return launch_p_t<T, 4, 2, 2, 2>(L, s, kb, batch, n_in, n_out, x, g, cfmt, p, h);
+    case 1: return launch_p_t<T, 4, 2, 2, 3>(L, s, kb, batch, n_in, n_out, x, g, cfmt, p, h);
+    case 2: return launch_p_t<T, 4, 2, 2, 4>(L, s, kb, batch, n_in, n_out, x, g, cfmt, p, h);
+    case 3: return launch_p_t<T, 4, 2, 2, 5>(L, s, kb, batch, n_in, n_out, x, g, cfmt, p, h);
+    case 4: return launch_p_t<T, 4, 2, 1, 6>(L, s, kb, batch, n_in, n_out, x, g, cfmt, p, h);
+    case 5: return launch_p_t<T, 4, 2, 1, 8>(L, s, kb, batch, n_in, n_out, x, g, cfmt, p, h);
+    default: return launch_p_t<T, 4, 2, 1, 12>(L, s, kb, batch, n_in, n_out, x, g, cfmt, p, h);
   }
-  return check_launch("P");
 }
 
-template <typename T, int NTB>
-void launch_g_t(const KBasis& kb, dim3 grid, hipStream_t s, int64_t batch, int64_t n_in, int64_t n_out, int64_t BP,
-                int64_t OUTP, const void* x, const void* w, const void* gt, void* dc) {
-  hipLaunchKernelGGL((g_kernel<T, NTB, G_BM>), grid, dim3(kThreads), 0, s, kb, (int)batch, (int)n_in, (int)n_out,
-                     (int)BP, (int)OUTP, (const T*)x, (const T*)w, (const T*)gt, (T*)dc);
+template <typename T, int WMW, int WJW, int TM, int FW, int RB, bool CHEB>
+int launch_g_t(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out,
+               const void* x, const void* w, const float* zt, const float* wt, const void* gt, void* dc) {
+  constexpr int BM = WMW * TM * 32, NMAX = WJW * FW * 32, RS = RB + 16;
+  const size_t lds_ops = (size_t)2 * (BM + NMAX) * RS, lds_red = (size_t)kb.n_t * (BM / 2) * 33 * 4;
+  const size_t lds = lds_ops > lds_red ? lds_ops : lds_red;
+  auto kern = g_kernel<T, WMW, WJW, TM, FW, RB, CHEB>;
+  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+    return fail(KF_ELAUNCH, "G: cannot reserve %zu bytes of LDS", lds);
+  const int n_m = (int)(L.OUTP / BM), n_n = (int)((n_in + 31) / 32);
+  hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(WMW * WJW * 64), lds, s, kb, (int)batch, (int)n_in, (int)n_out,
+                     (int)L.BP, (int)L.OUTP, (const T*)x, (const T*)w, zt, wt, (const T*)gt, (T*)dc);
+  return check_launch("G");
+}
+
+template <typename T, bool CHEB>
+int launch_g_cfg(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out,
+                 const void* x, const void* w, const float* zt, const float* wt, const void* gt, void* dc) {
+  switch (L.cfg) {
+    case 0: return launch_g_t<T, 2, 2, 2, 2, 128, CHEB>(L, s, kb, batch, n_in, n_out, x, w, zt, wt, gt, dc);
+    case 1: return launch_g_t<T, 2, 2, 2, 3, 128, CHEB>(L, s, kb, batch, n_in, n_out, x, w, zt, wt, gt, dc);
+    case 2: return launch_g_t<T, 2, 2, 2, 4, 128, CHEB>(L, s, kb, batch, n_in, n_out, x, w, zt, wt, gt, dc);
+    case 3: return launch_g_t<T, 2, 2, 2, 5, 128, CHEB>(L, s, kb, batch, n_in, n_out, x, w, zt, wt, gt, dc);
+    case 4: return launch_g_t<T, 2, 2, 2, 6, 128, CHEB>(L, s, kb, batch, n_in, n_out, x, w, zt, wt, gt, dc);
+    case 5: return launch_g_t<T, 2, 2, 1, 8, 64, CHEB>(L, s, kb, batch, n_in, n_out, x, w, zt, wt, gt, dc);
+    default: return launch_g_t<T, 2, 2, 1, 12, 64, CHEB>(L, s, kb, batch, n_in, n_out, x, w, zt, wt, gt, dc);
+  }
 }
 
 template <typename T>
-int run_G(const KBasis& kb, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* g,
-          const void* w, void* dc, void* ws, hipStream_t s) {
-  WsG L = ws_g(dtype, batch, n_out);
-  void* gt = ws;
+int run_G(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
+          const void* g, const void* w, void* dc, void* ws, hipStream_t s) {
+  const bool cheb = kb.kind == KF_KIND_CHEB;
+  WsG L = ws_g(b, dtype, batch, n_in, n_out, w != nullptr);
+  char* base = (char*)ws;
+  void* gt = base;
+  float* zt = cheb ? (float*)(base + L.gt) : nullptr;
+  float* wt = cheb && w ? (float*)(base + L.gt + L.zt) : nullptr;
   dim3 tg((unsigned)((L.OUTP + 63) / 64), (unsigned)((L.BP + 63) / 64));
   hipLaunchKernelGGL(transpose_kernel<T>, tg, dim3(kThreads), 0, s, (int)batch, (int)n_out, (int)L.BP, (int)L.OUTP,
                      (const T*)g, (T*)gt);
   int rc = check_launch("transpose");
   if (rc) return rc;
-  dim3 grid((unsigned)((n_in + 15) / 16), (unsigned)(L.OUTP / G_BM));
-  switch (nt_bucket(kb.n_t)) {
-    case 4: launch_g_t<T, 4>(kb, grid, s, batch, n_in, n_out, L.BP, L.OUTP, x, w, gt, dc); break;
-    case 8: launch_g_t<T, 8>(kb, grid, s, batch, n_in, n_out, L.BP, L.OUTP, x, w, gt, dc); break;
-    case 12: launch_g_t<T, 12>(kb, grid, s, batch, n_in, n_out, L.BP, L.OUTP, x, w, gt, dc); break;
-    case 16: launch_g_t<T, 16>(kb, grid, s, batch, n_in, n_out, L.BP, L.OUTP, x, w, gt, dc); break;
-    default: launch_g_t<T, 24>(kb, grid, s, batch, n_in, n_out, L.BP, L.OUTP, x, w, gt, dc); break;
+  if (cheb) {
+    dim3 zg((unsigned)((L.INP + 63) / 64), (unsigned)((L.BP + 63) / 64));
+    hipLaunchKernelGGL(zmapT_kernel<T>, zg, dim3(kThreads), 0, s, (int)batch, (int)n_in, (int)L.BP, (int)L.INP,
+                       kb.input_map, (const T*)x, (const T*)w, zt, wt);
+    rc = check_launch("zmapT");
+    if (rc) return rc;
+    return launch_g_cfg<T, true>(L, s, kb, batch, n_in, n_out, x, w, zt, wt, gt, dc);
   }
-  return check_launch("G");
+  return launch_g_cfg<T, false>(L, s, kb, batch, n_in, n_out, x, w, nullptr, nullptr, gt, dc);
 }
 
 template <typename T, int KM>
@@ -404,7 +461,7 @@ size_t kf_workspace_bytes(int op, const kf_basis* b, int dtype, int64_t batch, i
   switch (op) {
     case KF_OP_F: return ws_f(b, dtype, batch, n_in, n_out, true).total;
     case KF_OP_P: return ws_p(b, dtype, n_in, n_out).total;
-    case KF_OP_G: return ws_g(dtype, batch, n_out).total;
+    case KF_OP_G: return ws_g(b, dtype, batch, n_in, n_out, true).total;
     default: return 0;
   }
 }
@@ -436,12 +493,12 @@ int kf_G(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
   const long n = (long)n_out * n_in * b->size;
   if (batch == 0) return dtype == KF_BF16 ? zero_fill<bf16>(dc, n, s) : zero_fill<float>(dc, n, s);
   if (!x || !g || !dc) return fail(KF_EINVAL, "kf_G: NULL array");
-  size_t need = ws_g(dtype, batch, n_out).total;
+  size_t need = ws_g(b, dtype, batch, n_in, n_out, w != nullptr).total;
   if (!workspace || workspace_bytes < need)
     return fail(KF_EWORKSPACE, "kf_G: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
   KBasis kb = to_kbasis(b);
-  if (dtype == KF_BF16) return run_G<bf16>(kb, dtype, batch, n_in, n_out, x, g, w, dc, workspace, s);
-  return run_G<float>(kb, dtype, batch, n_in, n_out, x, g, w, dc, workspace, s);
+  if (dtype == KF_BF16) return run_G<bf16>(kb, b, dtype, batch, n_in, n_out, x, g, w, dc, workspace, s);
+  return run_G<float>(kb, b, dtype, batch, n_in, n_out, x, g, w, dc, workspace, s);
 }
 
 int kf_P(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* g,

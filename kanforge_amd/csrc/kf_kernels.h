@@ -331,188 +331,355 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void f_kernel(int B, int OUT
 }
 
 // ---------------------------------------------------------------------------
-// P: p[b,i] = sum_j f_j(x[b,i]) * sum_o g[b,o] CfmT[j][i][o]
-// N tile = 16 inputs x n_t features (column j*16 + input), all waves along M;
-// each lane ends with every feature of its (b, i) positions and finishes the
-// feature sum in registers.
-template <typename T, int NTB, int BM>
-__global__ __launch_bounds__(kThreads) void p_kernel(KBasis bs, int B, int IN, int OUT, int INP, int OUTP,
-                                                     const T* __restrict__ x, const T* __restrict__ g,
-                                                     const T* __restrict__ cfmt, T* __restrict__ p,
-                                                     float* __restrict__ hout) {
-  constexpr int KGE = KG<T>::elems, PL = KG<T>::per_lane;
-  constexpr int OC = 32;  // reduction elements (outputs o) per step
-  constexpr int STR = OC + 16 / (int)sizeof(T);
-  constexpr int WM = BM / 4, TM = WM / 16;
-  __shared__ __attribute__((aligned(16))) T As[BM * STR];
-  __shared__ __attribute__((aligned(16))) T Bs[NTB * 16 * STR];
+// z^T[i][b] = g(x[b][i]) (float32, zero-padded to (INP, BP)) and, when w is
+// given, w^T the same way: the G kernel generates features with the batch
+// (its reduction dimension) contiguous. 64x64 tiles through LDS.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void zmapT_kernel(int B, int IN, int BP, int INP, int input_map,
+                                                         const T* __restrict__ x, const T* __restrict__ w,
+                                                         float* __restrict__ zt, float* __restrict__ wt) {
+  __shared__ float tz[64][65], tw[64][65];
+  const int b0 = blockIdx.y * 64, i0 = blockIdx.x * 64;
+  const int tx = threadIdx.x % 64, ty = threadIdx.x / 64;
+  for (int r = ty; r < 64; r += 4) {
+    const int b = b0 + r, i = i0 + tx;
+    const bool ok = b < B && i < IN;
+    tz[r][tx] = ok ? cheb_map(to_f32(x[(size_t)b * IN + i]), input_map) : 0.f;
+    if (wt) tw[r][tx] = ok ? to_f32(w[(size_t)b * IN + i]) : 0.f;
+  }
+  __syncthreads();
+  for (int r = ty; r < 64; r += 4) {
+    const int i = i0 + r, b = b0 + tx;
+    if (i < INP && b < BP) {
+      zt[(size_t)i * BP + b] = tz[tx][r];
+      if (wt) wt[(size_t)i * BP + b] = tw[tx][r];
+    }
+  }
+}
 
-  const int b0 = blockIdx.y * BM, i0 = blockIdx.x * 16;
-  const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
-  const int h = lane / 16, l16 = lane % 16;
+// Shared shape of P and G: the N dimension of a workgroup is 32 inputs x n_t
+// kernel features, column n = j*32 + input (feature-major), and the waves
+// split it into WAVES_J groups of FW features, so one lane holds consecutive
+// features of one (row, input) position. Stages cover 64 bytes (P) or 128
+// bytes (G) of the reduction dimension; operands are double-buffered in LDS
+// with one barrier per stage.
+
+// P: p[b,i] = sum_j f_j(x[b,i]) * sum_o g[b,o] CfmT[j][i][o]
+// M = batch rows (A = g, natural layout), reduction over outputs o.
+template <typename T, int WAVES_M, int WAVES_J, int TM, int FW>
+__global__ __launch_bounds__(WAVES_M* WAVES_J * 64) void p_kernel(KBasis bs, int B, int IN, int OUT, int INP, int OUTP,
+                                                                 const T* __restrict__ x, const T* __restrict__ g,
+                                                                 const T* __restrict__ cfmt, T* __restrict__ p,
+                                                                 float* __restrict__ hout) {
+  constexpr int NTH = WAVES_M * WAVES_J * 64;
+  constexpr int BM = WAVES_M * TM * 32;
+  constexpr int RB = 64, RS = RB + 16, FS = RB / 32;
+  constexpr int EPS = RB / (int)sizeof(T);  // outputs o per stage
+  constexpr int PL = 16 / (int)sizeof(T);
+  constexpr int NMAX = WAVES_J * FW * 32;  // N rows of the B tile
+  constexpr int ACH = BM * (RB / 16), APT = (ACH + NTH - 1) / NTH;
+  constexpr int BCH = NMAX * (RB / 16), BPT = (BCH + NTH - 1) / NTH;
+  constexpr int NTB = WAVES_J * FW;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  unsigned char* As = smem;                // [2][BM][RS]
+  unsigned char* Bs = smem + 2 * BM * RS;  // [2][NMAX][RS]
+
+  const int n_m = (B + BM - 1) / BM, n_n = INP / 32;
+  int tm_, tn_;
+  xcd_tile(blockIdx.x, n_m, n_n, tm_, tn_);
+  const int b0 = tm_ * BM, i0 = tn_ * 32;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WAVES_J, wj = wave % WAVES_J;
+  const int h = lane >> 5, l32 = lane & 31;
   const int n_t = bs.n_t;
+  const int nrows = n_t * 32;
   const bool g_vec = (OUT % PL) == 0;
 
-  f32x4 acc[TM][NTB];
+  f32x16 acc[TM][FW];
 #pragma unroll
   for (int a = 0; a < TM; ++a)
 #pragma unroll
-    for (int c = 0; c < NTB; ++c) acc[a][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int f = 0; f < FW; ++f)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[a][f][r] = 0.f;
 
-  for (int oc0 = 0; oc0 < OUTP; oc0 += OC) {
-    __syncthreads();
-    constexpr int CPR = OC / PL;
-    // A tile: g[b0 + r][oc0 .. oc0+32] (bounds-checked)
-    for (int e = tid; e < BM * CPR; e += kThreads) {
-      const int r = e / CPR, q = e % CPR;
+  u32x4 ast[APT], bst[BPT];
+  auto load = [&](int oc0) {
+#pragma unroll
+    for (int u = 0; u < APT; ++u) {
+      const int e = tid + u * NTH;
+      const int r = e / (RB / 16), q = e % (RB / 16);
       const int b = b0 + r, o = oc0 + q * PL;
-      u32x4 v;
+      const bool ok = e < ACH && b < B;
       if (g_vec) {
-        v = gload16(g + (size_t)b * OUT + o, b < B && o < OUT);
+        ast[u] = gload16(g + (size_t)(ok ? b : 0) * OUT + (o < OUT ? o : 0), ok && o < OUT);
       } else {
         float tmp[PL];
 #pragma unroll
-        for (int u = 0; u < PL; ++u) tmp[u] = (b < B && o + u < OUT) ? to_f32(g[(size_t)b * OUT + o + u]) : 0.f;
-        v = pack16<T>(tmp);
+        for (int v = 0; v < PL; ++v) tmp[v] = (ok && o + v < OUT) ? to_f32(g[(size_t)b * OUT + o + v]) : 0.f;
+        ast[u] = pack16<T>(tmp);
       }
-      lds_write16(&As[r * STR + q * PL], v);
     }
-    // B tile: cfmt[j][i0 + il][oc0 .. oc0+32], row j*16 + il
-    for (int e = tid; e < n_t * 16 * CPR; e += kThreads) {
-      const int r = e / CPR, q = e % CPR;
-      const int j = r / 16, il = r % 16;
-      const T* src = cfmt + ((size_t)j * INP + i0 + il) * OUTP + oc0 + q * PL;
-      lds_write16(&Bs[r * STR + q * PL], gload16(src, true));
-    }
-    __syncthreads();
 #pragma unroll
-    for (int kg = 0; kg < OC / KGE; ++kg) {
+    for (int u = 0; u < BPT; ++u) {
+      const int e = tid + u * NTH;
+      const int r = e / (RB / 16), q = e % (RB / 16);
+      const bool ok = e < BCH && r < nrows;
+      const int j = ok ? r / 32 : 0, il = r % 32;
+      bst[u] = gload16(cfmt + ((size_t)j * INP + i0 + il) * OUTP + oc0 + q * PL, ok);
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < APT; ++u) {
+      const int e = tid + u * NTH;
+      if (e < ACH) lds_write16(As + (size_t)(buf * BM + e / (RB / 16)) * RS + 16 * (e % (RB / 16)), ast[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < BPT; ++u) {
+      const int e = tid + u * NTH;
+      if (e < BCH) lds_write16(Bs + (size_t)(buf * NMAX + e / (RB / 16)) * RS + 16 * (e % (RB / 16)), bst[u]);
+    }
+  };
+
+  const int S = OUTP / EPS;
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int s = 0; s < S; ++s) {
+    const int buf = s & 1;
+    if (s + 1 < S) load((s + 1) * EPS);
+#pragma unroll
+    for (int fs = 0; fs < FS; ++fs) {
       u32x4 af[TM];
 #pragma unroll
-      for (int a = 0; a < TM; ++a) af[a] = lds_read16(&As[(wave * WM + a * 16 + l16) * STR + kg * KGE + h * PL]);
+      for (int a = 0; a < TM; ++a)
+        af[a] = lds_read16(As + (size_t)(buf * BM + (wm * TM + a) * 32 + l32) * RS + fs * 32 + h * 16);
 #pragma unroll
-      for (int c = 0; c < NTB; ++c) {
-        if (c < n_t) {
-          const u32x4 bf = lds_read16(&Bs[(c * 16 + l16) * STR + kg * KGE + h * PL]);
+      for (int f = 0; f < FW; ++f) {
+        const int j = wj * FW + f;
+        if (j < n_t) {
+          const u32x4 bf = lds_read16(Bs + (size_t)(buf * NMAX + j * 32 + l32) * RS + fs * 32 + h * 16);
 #pragma unroll
-          for (int a = 0; a < TM; ++a) mma<T>(acc[a][c], af[a], bf);
+          for (int a = 0; a < TM; ++a) mma32<T>(acc[a][f], af[a], bf);
         }
       }
     }
+    if (s + 1 < S) store(buf ^ 1);
+    __syncthreads();
   }
-  // epilogue: feature sum per (b, i)
-  const int i = i0 + l16;
+
+  // epilogue: feature sum, then across the feature groups through LDS
+  float* red = reinterpret_cast<float*>(smem);  // [WAVES_J][BM][33]
+  const int i = i0 + l32;
 #pragma unroll
   for (int a = 0; a < TM; ++a)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int b = b0 + wave * WM + a * 16 + 4 * h + r;
+    for (int r = 0; r < 16; ++r) {
+      const int row = (wm * TM + a) * 32 + acc_row(r, lane);
+      const int b = b0 + row;
+      float sum = 0.f;
       if (b < B && i < IN) {
         float f[NTB];
         kernel_features<NTB>(to_f32(x[(size_t)b * IN + i]), 1.f, i, bs, f);
-        float s = 0.f;
 #pragma unroll
-        for (int c = 0; c < NTB; ++c)
-          if (c < n_t) s = fmaf(acc[a][c][r], f[c], s);
-        p[(size_t)b * IN + i] = from_f32<T>(s);
-        if (hout) hout[(size_t)b * IN + i] = acc[a][0][r];
+        for (int q = 0; q < FW; ++q) sum = fmaf(acc[a][q][r], f[wj * FW + q], sum);
+        if (hout && wj == 0) hout[(size_t)b * IN + i] = acc[a][0][r];
       }
+      red[(wj * BM + row) * 33 + l32] = sum;
     }
-}
-
-// ---------------------------------------------------------------------------
-// G: dc[o,i,k] = sum_j fold[k][j] sum_b gT[o][b] w[b,i] f_j(x[b,i])
-// N tile = 16 inputs x n_t features; features generated into LDS with b
-// contiguous (the reduction dimension), shared by all four waves.
-template <typename T, int NTB, int BM>
-__global__ __launch_bounds__(kThreads) void g_kernel(KBasis bs, int B, int IN, int OUT, int BP, int OUTP,
-                                                     const T* __restrict__ x, const T* __restrict__ w,
-                                                     const T* __restrict__ gt, T* __restrict__ dc) {
-  constexpr int KGE = KG<T>::elems, PL = KG<T>::per_lane;
-  constexpr int BC = 64;  // batch rows per step
-  constexpr int STR = BC + 16 / (int)sizeof(T);
-  constexpr int WM = BM / 4, TM = WM / 16;
-  __shared__ __attribute__((aligned(16))) T As[BM * STR];
-  __shared__ __attribute__((aligned(16))) T Bs[NTB * 16 * STR];
-
-  const int o0 = blockIdx.y * BM, i0 = blockIdx.x * 16;
-  const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
-  const int h = lane / 16, l16 = lane % 16;
-  const int n_t = bs.n_t, K = bs.K;
-
-  f32x4 acc[TM][NTB];
+  __syncthreads();
+  for (int e = tid; e < BM * 32; e += NTH) {
+    const int row = e / 32, il = e % 32;
+    const int b = b0 + row, ii = i0 + il;
+    if (b < B && ii < IN) {
+      float sum = 0.f;
 #pragma unroll
-  for (int a = 0; a < TM; ++a)
-#pragma unroll
-    for (int c = 0; c < NTB; ++c) acc[a][c] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  // generator task: input gi (of 16), 4 consecutive batch rows gq*4 .. +4
-  const int gi = tid % 16, gq = tid / 16;
-  const int gin = i0 + gi;
-
-  for (int bc0 = 0; bc0 < BP; bc0 += BC) {
-    __syncthreads();
-    // A tile: gT[o0 + r][bc0 .. bc0+64]
-    constexpr int CPR = BC / PL;
-    for (int e = tid; e < BM * CPR; e += kThreads) {
-      const int r = e / CPR, q = e % CPR;
-      const T* src = gt + (size_t)(o0 + r) * BP + bc0 + q * PL;
-      lds_write16(&As[r * STR + q * PL], gload16(src, true));
-    }
-    // B tile: features of x[bc0 + gq*4 + u][gin], u < 4, row j*16 + gi
-    {
-      float f[4][NTB];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int b = bc0 + gq * 4 + u;
-        const bool ok = b < B && gin < IN;
-        const float xv = ok ? to_f32(x[(size_t)b * IN + gin]) : 0.f;
-        const float wv = ok ? (w ? to_f32(w[(size_t)b * IN + gin]) : 1.f) : 0.f;
-        kernel_features<NTB>(xv, wv, ok ? gin : 0, bs, f[u]);
-      }
-#pragma unroll
-      for (int c = 0; c < NTB; ++c) {
-        if (c < n_t) {
-          T* dst = &Bs[(c * 16 + gi) * STR + gq * 4];
-#pragma unroll
-          for (int u = 0; u < 4; ++u) dst[u] = from_f32<T>(f[u][c]);
-        }
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int kg = 0; kg < BC / KGE; ++kg) {
-      u32x4 af[TM];
-#pragma unroll
-      for (int a = 0; a < TM; ++a) af[a] = lds_read16(&As[(wave * WM + a * 16 + l16) * STR + kg * KGE + h * PL]);
-#pragma unroll
-      for (int c = 0; c < NTB; ++c) {
-        if (c < n_t) {
-          const u32x4 bf = lds_read16(&Bs[(c * 16 + l16) * STR + kg * KGE + h * PL]);
-#pragma unroll
-          for (int a = 0; a < TM; ++a) mma<T>(acc[a][c], af[a], bf);
-        }
-      }
+      for (int q = 0; q < WAVES_J; ++q) sum += red[(q * BM + row) * 33 + il];
+      p[(size_t)b * IN + ii] = from_f32<T>(sum);
     }
   }
-  // epilogue: apply the fold, store dc[o][i][0..K)
-  const int i = i0 + l16;
+}
+
+// G: dc[o,i,k] = sum_j fold[k][j] sum_b gT[o][b] w[b,i] f_j(x[b,i])
+// M = outputs o (A = gT from the transpose prepass), reduction over batch
+// rows. The B tile (features, batch contiguous) is generated per stage by
+// every thread: input gi, 8 (bf16) or 4 (f32) consecutive rows; Chebyshev
+// features come from z^T by the recurrence, other kinds from x.
+template <typename T, int WAVES_M, int WAVES_J, int TM, int FW, int RB, bool CHEB>
+__global__ __launch_bounds__(WAVES_M* WAVES_J * 64) void g_kernel(KBasis bs, int B, int IN, int OUT, int BP, int OUTP,
+                                                                 const T* __restrict__ x, const T* __restrict__ w,
+                                                                 const float* __restrict__ zt,
+                                                                 const float* __restrict__ wt,
+                                                                 const T* __restrict__ gt, T* __restrict__ dc) {
+  constexpr int NTH = WAVES_M * WAVES_J * 64;
+  constexpr int BM = WAVES_M * TM * 32;
+  constexpr int RS = RB + 16, FS = RB / 32;
+  constexpr int EPS = RB / (int)sizeof(T);  // batch rows per stage
+  constexpr int PL = 16 / (int)sizeof(T);   // rows per generator write
+  constexpr int NTB = WAVES_J * FW;
+  constexpr int NMAX = NTB * 32;
+  constexpr int ACH = BM * (RB / 16), APT = (ACH + NTH - 1) / NTH;
+  constexpr int GTASK = 32 * (EPS / PL);  // generator tasks per stage
+  static_assert(GTASK <= NTH, "one generator task per thread");
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  unsigned char* As = smem;                // [2][BM][RS]
+  unsigned char* Bs = smem + 2 * BM * RS;  // [2][NMAX][RS]
+
+  const int n_m = OUTP / BM, n_n = (IN + 31) / 32;
+  int tm_, tn_;
+  xcd_tile(blockIdx.x, n_m, n_n, tm_, tn_);
+  const int o0 = tm_ * BM, i0 = tn_ * 32;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WAVES_J, wj = wave % WAVES_J;
+  const int h = lane >> 5, l32 = lane & 31;
+  const int n_t = bs.n_t, K = bs.K;
+
+  f32x16 acc[TM][FW];
 #pragma unroll
   for (int a = 0; a < TM; ++a)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int o = o0 + wave * WM + a * 16 + 4 * h + r;
-      if (o < OUT && i < IN) {
-        T* dst = dc + ((size_t)o * IN + i) * K;
-        for (int k = 0; k < K; ++k) {
-          float s = 0.f;
+    for (int f = 0; f < FW; ++f)
 #pragma unroll
-          for (int c = 0; c < NTB; ++c)
-            if (c < n_t) s = fmaf(acc[a][c][r], bs.fold[k * KF_MAX_NT + c], s);
-          dst[k] = from_f32<T>(s);
+      for (int r = 0; r < 16; ++r) acc[a][f][r] = 0.f;
+
+  const int gi = tid % 32, gq = tid / 32;  // generator: input gi, rows gq*PL .. +PL of the stage
+  const bool gen_on = tid < GTASK;
+  const int gin = i0 + gi;
+  u32x4 ast[APT];
+  float fz[PL], fw[PL];
+  auto load = [&](int bc0) {
+#pragma unroll
+    for (int u = 0; u < APT; ++u) {
+      const int e = tid + u * NTH;
+      const int r = e / (RB / 16), q = e % (RB / 16);
+      ast[u] = gload16(gt + (size_t)(o0 + (e < ACH ? r : 0)) * BP + bc0 + q * PL, e < ACH);
+    }
+    if (gen_on) {
+      const int b = bc0 + gq * PL;
+      if (CHEB) {
+        const float* zp = zt + (size_t)gin * BP + b;
+#pragma unroll
+        for (int q = 0; q < PL / 4; ++q) {
+          const f32x4 v = (gin < IN) ? *reinterpret_cast<const f32x4*>(zp + 4 * q) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int u = 0; u < 4; ++u) fz[4 * q + u] = v[u];
+          if (wt) {
+            const f32x4 v2 = (gin < IN) ? *reinterpret_cast<const f32x4*>(wt + (size_t)gin * BP + b + 4 * q)
+                                        : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) fw[4 * q + u] = v2[u];
+          }
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < PL; ++u) {
+          const bool ok = b + u < B && gin < IN;
+          fz[u] = ok ? to_f32(x[(size_t)(b + u) * IN + gin]) : 0.f;
+          fw[u] = ok ? (w ? to_f32(w[(size_t)(b + u) * IN + gin]) : 1.f) : 0.f;
         }
       }
     }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < APT; ++u) {
+      const int e = tid + u * NTH;
+      if (e < ACH) lds_write16(As + (size_t)(buf * BM + e / (RB / 16)) * RS + 16 * (e % (RB / 16)), ast[u]);
+    }
+    if (gen_on) {
+      unsigned char* dst = Bs + (size_t)(buf * NMAX + gi) * RS + gq * 16;
+      if (CHEB) {
+        float z2[PL], tp[PL], tc[PL];
+#pragma unroll
+        for (int u = 0; u < PL; ++u) {
+          const float wv = wt ? fw[u] : (gin < IN ? 1.f : 0.f);
+          z2[u] = 2.f * fz[u];
+          tp[u] = wv;
+          tc[u] = wv * fz[u];
+        }
+        lds_write16(dst, pack16<T>(tp));
+        if (n_t > 1) lds_write16(dst + 32 * RS, pack16<T>(tc));
+        for (int j = 2; j < n_t; ++j) {
+#pragma unroll
+          for (int u = 0; u < PL; ++u) {
+            const float nt = fmaf(z2[u], tc[u], -tp[u]);
+            tp[u] = tc[u];
+            tc[u] = nt;
+          }
+          lds_write16(dst + (size_t)j * 32 * RS, pack16<T>(tc));
+        }
+      } else {
+        // one element at a time: all its features, scattered as single elements
+        T* dst_t = reinterpret_cast<T*>(dst);
+        for (int u = 0; u < PL; ++u) {
+          float f[NTB];
+          kernel_features<NTB>(fz[u], fw[u], gin < IN ? gin : 0, bs, f);
+#pragma unroll
+          for (int j = 0; j < NTB; ++j)
+            if (j < n_t) dst_t[(size_t)j * 32 * RS / sizeof(T) + u] = from_f32<T>(f[j]);
+        }
+      }
+    }
+  };
+
+  const int S = BP / EPS;
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int s = 0; s < S; ++s) {
+    const int buf = s & 1;
+    if (s + 1 < S) load((s + 1) * EPS);
+#pragma unroll
+    for (int fs = 0; fs < FS; ++fs) {
+      u32x4 af[TM];
+#pragma unroll
+      for (int a = 0; a < TM; ++a)
+        af[a] = lds_read16(As + (size_t)(buf * BM + (wm * TM + a) * 32 + l32) * RS + fs * 32 + h * 16);
+#pragma unroll
+      for (int f = 0; f < FW; ++f) {
+        const int j = wj * FW + f;
+        if (j < n_t) {
+          const u32x4 bf = lds_read16(Bs + (size_t)(buf * NMAX + j * 32 + l32) * RS + fs * 32 + h * 16);
+#pragma unroll
+          for (int a = 0; a < TM; ++a) mma32<T>(acc[a][f], af[a], bf);
+        }
+      }
+    }
+    if (s + 1 < S) store(buf ^ 1);
+    __syncthreads();
+  }
+
+  // epilogue: raw feature sums to LDS in halves of the M tile, then the fold
+  // dc[o][i][k] = sum_j fold[k][j] GT[o][i][j], written k-fastest (coalesced).
+  float* red = reinterpret_cast<float*>(smem);  // [n_t][BM/2][33]
+  constexpr int HM = BM / 2;
+  for (int half = 0; half < 2; ++half) {
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = (wm * TM + a) * 32 + acc_row(r, lane);
+        if (row / HM == half) {
+#pragma unroll
+          for (int f = 0; f < FW; ++f) {
+            const int j = wj * FW + f;
+            if (j < n_t) red[(j * HM + row % HM) * 33 + l32] = acc[a][f][r];
+          }
+        }
+      }
+    __syncthreads();
+    for (int e = tid; e < HM * 32 * K; e += NTH) {
+      const int k = e % K, il = (e / K) % 32, row = e / (K * 32);
+      const int o = o0 + half * HM + row, i = i0 + il;
+      if (o < OUT && i < IN) {
+        float sum = 0.f;
+        for (int j = 0; j < n_t; ++j) sum = fmaf(bs.fold[k * KF_MAX_NT + j], red[(j * HM + row) * 33 + il], sum);
+        dc[((size_t)o * IN + i) * K + k] = from_f32<T>(sum);
+      }
+    }
+    __syncthreads();
+  }
 }
 
 // ---------------------------------------------------------------------------
