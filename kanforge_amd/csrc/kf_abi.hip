@@ -133,7 +133,7 @@ int pick_f_cfg(int64_t batch, int64_t n_out) {
 }
 
 struct WsF {
-  int cfg;
+  int cfg, n_tp;
   int64_t INP, OUTP, BP;
   size_t cfm, z, wz, phi, total;
 };
@@ -146,10 +146,12 @@ WsF ws_f(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
   w.BP = round_up(batch, c.bm);
   const int es = elt_size(dtype);
   const bool cheb = b->kind == KF_KIND_CHEB;
-  w.cfm = align256((size_t)b->n_t * w.OUTP * w.INP * es);
+  const int fps = dtype == KF_BF16 ? 2 : 1;
+  w.n_tp = (b->n_t + fps - 1) / fps * fps;
+  w.cfm = align256((size_t)w.n_tp * w.OUTP * w.INP * es);
   w.z = cheb ? align256((size_t)w.BP * w.INP * sizeof(float)) : 0;
   w.wz = cheb && has_w ? align256((size_t)w.BP * w.INP * sizeof(float)) : 0;
-  w.phi = cheb ? 0 : align256((size_t)w.BP * b->n_t * w.INP * es);
+  w.phi = cheb ? 0 : align256((size_t)w.BP * w.n_tp * w.INP * es);
   w.total = w.cfm + w.z + w.wz + w.phi;
   return w;
 }
@@ -169,16 +171,17 @@ int g_tm(int fw) { return fw <= 6 ? 2 : 1; }
 int g_rb(int fw) { return fw <= 6 ? 128 : 64; }
 
 struct WsP {
-  int cfg;
+  int cfg, ntb;
   int64_t INP, OUTP;
   size_t cfmt, total;
 };
 WsP ws_p(const kf_basis* b, int dtype, int64_t n_in, int64_t n_out) {
   WsP w;
   w.cfg = fw_index(b->n_t);
+  w.ntb = 2 * FW_LIST[w.cfg];
   w.INP = round_up(n_in, 32);
   w.OUTP = round_up(n_out, 32);
-  w.cfmt = align256((size_t)b->n_t * w.INP * w.OUTP * elt_size(dtype));
+  w.cfmt = align256((size_t)w.ntb * w.INP * w.OUTP * elt_size(dtype));
   w.total = w.cfmt;
   return w;
 }
@@ -218,18 +221,19 @@ int zero_fill(void* p, long n, hipStream_t s) {
   return check_launch("fill");
 }
 
-// permute (and fold) coefficients into a feature-major workspace layout
+// permute (and fold) coefficients into a feature-major workspace layout with
+// n_feat >= n_t features (zeros past n_t)
 template <typename T>
-int launch_permute(const KBasis& kb, int64_t n_out, int64_t n_in, int64_t OUTP, int64_t INP, const void* c, void* out,
-                   bool fmt, hipStream_t s) {
+int launch_permute(const KBasis& kb, int64_t n_out, int64_t n_in, int64_t OUTP, int64_t INP, int n_feat, const void* c,
+                   void* out, bool fmt, hipStream_t s) {
   dim3 grid((unsigned)((OUTP + 31) / 32), (unsigned)((INP + 15) / 16));
-  size_t lds = (size_t)kb.n_t * 16 * 33 * sizeof(float);
+  size_t lds = (size_t)n_feat * 16 * 33 * sizeof(float);
   if (fmt)
     hipLaunchKernelGGL((permute_coef_kernel<T, true>), grid, dim3(kThreads), lds, s, kb, (int)n_out, (int)n_in,
-                       (int)OUTP, (int)INP, (const T*)c, (T*)out);
+                       (int)OUTP, (int)INP, n_feat, (const T*)c, (T*)out);
   else
     hipLaunchKernelGGL((permute_coef_kernel<T, false>), grid, dim3(kThreads), lds, s, kb, (int)n_out, (int)n_in,
-                       (int)OUTP, (int)INP, (const T*)c, (T*)out);
+                       (int)OUTP, (int)INP, n_feat, (const T*)c, (T*)out);
   return check_launch("permute_coef");
 }
 
@@ -279,14 +283,15 @@ namespace {
 template <typename T, int BM, int BN, int WMW, int WNW, bool CHEB, bool HAS_W>
 int launch_f_t(const WsF& L, int64_t batch, int64_t n_out, int n_t, const float* z, const float* wz, const void* cfm,
                const void* phi, void* y, hipStream_t s) {
+  constexpr int FPS = sizeof(T) == 2 ? 2 : 1;
   const int n_m = (int)(L.BP / BM), n_n = (int)(L.OUTP / BN);
   const int rs = 32 * (int)sizeof(T) + 16;
-  const size_t lds = (size_t)2 * (BM + BN) * rs;
-  auto kern = f_kernel<T, BM, BN, WMW, WNW, CHEB, HAS_W>;
+  const size_t lds = (size_t)2 * FPS * (BM + BN) * rs;
+  auto kern = f_kernel<T, BM, BN, WMW, WNW, FPS, CHEB, HAS_W>;
   if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return fail(KF_ELAUNCH, "F: cannot reserve %zu bytes of LDS", lds);
   hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(WMW * WNW * 64), lds, s, (int)batch, (int)n_out, (int)L.INP,
-                     (int)L.OUTP, n_t, z, wz, (const T*)cfm, (const T*)phi, (T*)y);
+                     (int)L.OUTP, n_t, L.n_tp, z, wz, (const T*)cfm, (const T*)phi, (T*)y);
   return check_launch("F");
 }
 
@@ -311,7 +316,7 @@ int run_F(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
   float* z = (float*)(base + L.cfm);
   float* wz = has_w && cheb ? (float*)(base + L.cfm + L.z) : nullptr;
   void* phi = base + L.cfm + L.z + L.wz;
-  int rc = launch_permute<T>(kb, n_out, n_in, L.OUTP, L.INP, c, cfm, false, s);
+  int rc = launch_permute<T>(kb, n_out, n_in, L.OUTP, L.INP, L.n_tp, c, cfm, false, s);
   if (rc) return rc;
   if (cheb) {
     long n = (long)L.BP * L.INP;
@@ -325,16 +330,16 @@ int run_F(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
     return launch_f_cfg<T, true, false>(L, batch, n_out, kb.n_t, z, nullptr, cfm, nullptr, y, s);
   }
   // precomputed features phi_fm[b][j][i] (BP, n_t, INP)
-  rc = launch_features<T, false>(kb, batch, n_in, L.BP, L.INP, x, phi, (long)kb.n_t * L.INP, (long)L.INP, 1L, false,
+  rc = launch_features<T, false>(kb, batch, n_in, L.BP, L.INP, x, phi, (long)L.n_tp * L.INP, (long)L.INP, 1L, false,
                                  s);
   if (rc) return rc;
   if (has_w) {
-    long n = (long)batch * kb.n_t * L.INP;
+    long n = (long)batch * L.n_tp * L.INP;
     long blocks = (n + kThreads - 1) / kThreads;
     if (blocks > 65535 * 4) blocks = 65535 * 4;
     if (blocks > 0)
       hipLaunchKernelGGL(scale_phi_kernel<T>, dim3((unsigned)blocks), dim3(kThreads), 0, s, (int)batch, (int)n_in,
-                         kb.n_t, (int)L.INP, (const T*)w, (T*)phi);
+                         L.n_tp, (int)L.INP, (const T*)w, (T*)phi);
     rc = check_launch("scale_phi");
     if (rc) return rc;
   }
@@ -361,7 +366,7 @@ int run_P(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
           const void* g, const void* c, void* p, float* h, void* ws, hipStream_t s) {
   WsP L = ws_p(b, dtype, n_in, n_out);
   void* cfmt = ws;
-  int rc = launch_permute<T>(kb, n_out, n_in, L.OUTP, L.INP, c, cfmt, true, s);
+  int rc = launch_permute<T>(kb, n_out, n_in, L.OUTP, L.INP, L.ntb, c, cfmt, true, s);
   if (rc) return rc;
   switch (L.cfg) {
     case 0: return launch_p_t<T, 4, 2, 2, 2>(L, s, kb, batch, n_in, n_out, x, g, cfmt, p, h);

@@ -146,7 +146,15 @@ __device__ inline void bspline_features(float x, float w, int i, const KBasis& b
   const int nk = b.n_knots, m = b.order;
   if (m > KD) return;
   const int j = bspline_interval(x, b.knots_cmp + (size_t)i * nk, nk);
-  if (j < 0) return;
+  if (j < 0) {
+    // outside [t_0, t_last): zeros; a non-finite x turns the zero indicators
+    // into NaN through (x - t) * 0, as the float64 recurrence does
+    if (!__builtin_isfinite(x)) {
+#pragma unroll
+      for (int s = 0; s < KM; ++s) phi[s] = (s < b.K) ? __builtin_nanf("") : 0.f;
+    }
+    return;
+  }
   // L[r] = t_{j-KD+r}, r = 0..2KD+1 (kp[r'] = t_{r'-KD}, so t_{j-KD+r} = kp[j+r])
   const float* kp = b.knots + (size_t)i * (nk + 2 * KD) + j;
   float L[2 * KD + 2];

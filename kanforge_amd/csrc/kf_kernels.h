@@ -24,9 +24,10 @@ constexpr int kThreads = 256;
 // out[j] = sum_k c[o,i,k] fold[k][j]. Tile 32 o x 16 i through LDS.
 template <typename T, bool FMT>
 __global__ __launch_bounds__(kThreads) void permute_coef_kernel(KBasis bs, int OUT, int IN, int OUTP, int INP,
-                                                                const T* __restrict__ c, T* __restrict__ out) {
-  extern __shared__ float tile[];  // [n_t][16][33]
-  const int K = bs.K, n_t = bs.n_t;
+                                                                int n_feat, const T* __restrict__ c,
+                                                                T* __restrict__ out) {
+  extern __shared__ float tile[];  // [n_feat][16][33]
+  const int K = bs.K, n_t = n_feat;  // features past bs.n_t get zero fold columns
   const int o0 = blockIdx.x * 32, i0 = blockIdx.y * 16;
   const int t = threadIdx.x;
   // phase 1: thread (ol = t / 16 .. +16, il = t % 16) covers 2 o rows
@@ -136,36 +137,42 @@ __global__ __launch_bounds__(kThreads) void zmap_kernel(int B, int IN, int BP, i
 // ---------------------------------------------------------------------------
 // F: y[b,o] = sum over input chunks of 32 and kernel features j of
 //            A_j[b][i] * Cfm[j][o][i],  A_j[b][i] = w[b,i] f_j(x[b,i]).
-// One stage = one feature of one chunk (32 reduction elements). A_j is
-// produced in LDS by every thread for the stage after the one the MFMAs
-// consume (double buffer, one barrier per stage):
-//   CHEB : Chebyshev recurrence T_j = 2 z T_{j-1} - T_{j-2} from z = g(x),
-//          one feature per stage, state (2z, T_{j-1}, T_{j-2}) in registers;
+// One stage = FPS features of one chunk (FPS * 32 reduction elements). The
+// A tiles are produced in LDS by every thread for the stage after the one
+// the MFMAs consume (double buffer, one barrier per stage):
+//   CHEB : Chebyshev features from z = g(x) by the three-term recurrence,
+//          two per step in ping-pong registers (a, b) with no copies. A chunk
+//          starts from (a, b) = (T_-2, T_-1) = (w T_2(z), w T_1(z)), so the
+//          first step gives (T_0, T_1) with the same two FMAs as every other.
 //   else : rows of the precomputed features phi_fm[b][j][i].
-// WG tile BM x BN, WAVES_M x WAVES_N waves, 32x32 MFMA tiles.
-template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, bool CHEB, bool HAS_W>
+// Cfm holds n_tp = n_t rounded up to FPS features (zeros past n_t); the MFMAs
+// of a padding feature are skipped.
+template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, int FPS, bool CHEB, bool HAS_W>
 __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void f_kernel(int B, int OUT, int INP, int OUTP, int n_t,
-                                                                 const float* __restrict__ z,
+                                                                 int n_tp, const float* __restrict__ z,
                                                                  const float* __restrict__ wz,
                                                                  const T* __restrict__ cfm,
                                                                  const T* __restrict__ phi_fm, T* __restrict__ y) {
   constexpr int NTH = WAVES_M * WAVES_N * 64;
   constexpr int IC = 32;
-  constexpr int RB = IC * (int)sizeof(T);  // bytes of one stage row
-  constexpr int RS = RB + 16;              // LDS row stride in bytes (+16: conflict-free 16-byte reads)
-  constexpr int FS = RB / 32;              // fragment steps per stage
+  constexpr int RB = IC * (int)sizeof(T);  // bytes of one feature row of a stage
+  constexpr int RS = RB + 16;              // LDS row stride (+16: conflict-free 16-byte reads)
+  constexpr int FSF = RB / 32;             // fragment steps per feature
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N, TM = WM / 32, TN = WN / 32;
   constexpr int TPR = NTH / BM;  // generator threads per A row
   constexpr int EPT = IC / TPR;  // A elements per generator thread
   constexpr int PL = 16 / (int)sizeof(T);
-  constexpr int BCH = BN * (RB / 16);  // 16-byte chunks of one B stage
-  constexpr int BPT = (BCH + NTH - 1) / NTH;
+  constexpr int CPR = RB / 16;                // 16-byte chunks per row
+  constexpr int BCH = FPS * BN * CPR;         // 16-byte chunks of one B stage
+  constexpr int BPT = (BCH + NTH - 1) / NTH;  // per thread
+  constexpr int ABUF = FPS * BM * RS, BBUF = FPS * BN * RS;
   static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile is a multiple of 32");
   static_assert(NTH % BM == 0 && EPT % PL == 0, "generator mapping");
+  static_assert(!CHEB || FPS == 1 || FPS == 2, "Chebyshev stages hold one or two features");
 
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  unsigned char* As = smem;                  // [2][BM][RS]
-  unsigned char* Bs = smem + 2 * BM * RS;    // [2][BN][RS]
+  unsigned char* As = smem;             // [2][FPS][BM][RS]
+  unsigned char* Bs = smem + 2 * ABUF;  // [2][FPS][BN][RS]
 
   const int n_m = (B + BM - 1) / BM, n_n = OUTP / BN;
   int tm_, tn_;
@@ -187,133 +194,154 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void f_kernel(int B, int OUT
   const int gr = tid / TPR, gc = tid % TPR;
   const float* zrow = z + (size_t)(b0 + gr) * INP + gc * EPT;
   const float* wrow = HAS_W ? wz + (size_t)(b0 + gr) * INP + gc * EPT : nullptr;
-  float z2[EPT], tp[EPT], tc[EPT], zn[EPT], wn_[HAS_W ? EPT : 1];
+  unsigned char* a_dst = As + (size_t)gr * RS + gc * EPT * (int)sizeof(T);
+  float ga[EPT], gb[EPT], z2[EPT], zn[EPT], wn_[HAS_W ? EPT : 1];
 
   const int n_chunks = INP / IC;
-  const int S = n_chunks * n_t;
+  const int P = n_tp / FPS;  // stages per chunk
 
-  auto load_chunk = [&](int ch) {
-    if (CHEB) {
+  // per-thread B tile chunks: row r (in the stage's FPS*BN rows), 16-byte column q
+  const T* bsrc[BPT];
+  int bdst[BPT];
 #pragma unroll
-      for (int q = 0; q < EPT / 4; ++q) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(zrow + ch * IC + 4 * q);
+  for (int u = 0; u < BPT; ++u) {
+    const int e = tid + u * NTH;
+    const int ec = e < BCH ? e : BCH - 1;
+    const int r = ec / CPR, q = ec % CPR;
+    const int f = r / BN, rr = r % BN;
+    bsrc[u] = cfm + ((size_t)f * OUTP + o0 + rr) * INP + q * PL;  // + (chunk*IC) + (stage feature base)*OUTP*INP
+    bdst[u] = (f * BN + rr) * RS + 16 * q;
+  }
+  const size_t fstride = (size_t)OUTP * INP;  // one feature of Cfm
+  u32x4 bst[BPT];
+  auto load_b = [&](int ch, int p) {
+    const size_t off = (size_t)p * FPS * fstride + (size_t)ch * IC;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) zn[4 * q + u] = v[u];
-        if (HAS_W) {
-          const f32x4 wv = *reinterpret_cast<const f32x4*>(wrow + ch * IC + 4 * q);
+    for (int u = 0; u < BPT; ++u) bst[u] = gload16(bsrc[u] + off, tid + u * NTH < BCH);
+  };
+  auto store_b = [&](int buf) {
 #pragma unroll
-          for (int u = 0; u < 4; ++u) wn_[4 * q + u] = wv[u];
+    for (int u = 0; u < BPT; ++u)
+      if (tid + u * NTH < BCH) lds_write16(Bs + buf * BBUF + bdst[u], bst[u]);
+  };
+  auto load_z = [&](int ch) {
+#pragma unroll
+    for (int q = 0; q < EPT / 4; ++q) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(zrow + ch * IC + 4 * q);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) zn[4 * q + u] = v[u];
+      if (HAS_W) {
+        const f32x4 wv = *reinterpret_cast<const f32x4*>(wrow + ch * IC + 4 * q);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) wn_[4 * q + u] = wv[u];
+      }
+    }
+  };
+  // Chebyshev: (a, b) <- (T_-2, T_-1) of the chunk held in zn
+  auto cheb_init = [&]() {
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const float wv = HAS_W ? wn_[e] : 1.f;
+      const float zz = zn[e];
+      z2[e] = 2.f * zz;
+      ga[e] = wv * fmaf(2.f * zz, zz, -1.f);
+      gb[e] = wv * zz;
+    }
+  };
+  // next FPS features into A buffer `buf`
+  auto cheb_step = [&](int buf) {
+    unsigned char* dst = a_dst + buf * ABUF;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) ga[e] = fmaf(z2[e], gb[e], -ga[e]);
+#pragma unroll
+    for (int q = 0; q < EPT / PL; ++q) lds_write16(dst + 16 * q, pack16<T>(&ga[q * PL]));
+    if (FPS == 2) {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) gb[e] = fmaf(z2[e], ga[e], -gb[e]);
+#pragma unroll
+      for (int q = 0; q < EPT / PL; ++q) lds_write16(dst + BM * RS + 16 * q, pack16<T>(&gb[q * PL]));
+    } else {
+      // one feature per stage: keep (a, b) = (T_{j-1}, T_j) ordered for the next step
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        const float t = ga[e];
+        ga[e] = gb[e];
+        gb[e] = t;
+      }
+    }
+  };
+  auto copy_a = [&](int buf, int ch, int p) {  // precomputed features
+    for (int e = tid; e < FPS * BM * CPR; e += NTH) {
+      const int r = e / CPR, q = e % CPR;
+      const int f = r / BM, rr = r % BM;
+      const T* src = phi_fm + ((size_t)(b0 + rr) * n_tp + p * FPS + f) * INP + ch * IC + q * PL;
+      lds_write16(As + buf * ABUF + (f * BM + rr) * RS + 16 * q, gload16(src, true));
+    }
+  };
+  auto mfma_stage = [&](int buf, bool second) {
+#pragma unroll
+    for (int f = 0; f < FPS; ++f) {
+      if (f == 0 || second) {
+#pragma unroll
+        for (int fs = 0; fs < FSF; ++fs) {
+          u32x4 af[TM], bfr[TN];
+#pragma unroll
+          for (int a = 0; a < TM; ++a)
+            af[a] = lds_read16(As + buf * ABUF + (f * BM + wm * WM + a * 32 + l32) * RS + fs * 32 + h * 16);
+#pragma unroll
+          for (int c = 0; c < TN; ++c)
+            bfr[c] = lds_read16(Bs + buf * BBUF + (f * BN + wn * WN + c * 32 + l32) * RS + fs * 32 + h * 16);
+#pragma unroll
+          for (int a = 0; a < TM; ++a)
+#pragma unroll
+            for (int c = 0; c < TN; ++c) mma32<T>(acc[a][c], af[a], bfr[c]);
         }
       }
     }
   };
-  // feature j of the current chunk into f (advances the recurrence state)
-  auto gen = [&](int j, float* f) {
-    if (j == 0) {
-#pragma unroll
-      for (int e = 0; e < EPT; ++e) {
-        const float wv = HAS_W ? wn_[e] : 1.f;
-        z2[e] = 2.f * zn[e];
-        tp[e] = wv;
-        tc[e] = wv * zn[e];
-        f[e] = tp[e];
-      }
-    } else if (j == 1) {
-#pragma unroll
-      for (int e = 0; e < EPT; ++e) f[e] = tc[e];
-    } else {
-#pragma unroll
-      for (int e = 0; e < EPT; ++e) {
-        const float nt = fmaf(z2[e], tc[e], -tp[e]);
-        tp[e] = tc[e];
-        tc[e] = nt;
-        f[e] = nt;
-      }
-    }
-  };
-  auto store_a = [&](int buf, const float* f) {
-    unsigned char* dst = As + (size_t)(buf * BM + gr) * RS + gc * EPT * (int)sizeof(T);
-#pragma unroll
-    for (int q = 0; q < EPT / PL; ++q) lds_write16(dst + 16 * q, pack16<T>(&f[q * PL]));
-  };
-  auto copy_a = [&](int buf, int ch, int j) {  // precomputed features
-    for (int e = tid; e < BM * (RB / 16); e += NTH) {
-      const int r = e / (RB / 16), q = e % (RB / 16);
-      const T* src = phi_fm + ((size_t)(b0 + r) * n_t + j) * INP + ch * IC + q * PL;
-      lds_write16(As + (size_t)(buf * BM + r) * RS + 16 * q, gload16(src, true));
-    }
-  };
-  u32x4 bst[BPT];
-  auto load_b = [&](int ch, int j) {
-#pragma unroll
-    for (int u = 0; u < BPT; ++u) {
-      const int e = tid + u * NTH;
-      const int ec = e < BCH ? e : BCH - 1;
-      const int r = ec / (RB / 16), q = ec % (RB / 16);
-      const T* src = cfm + ((size_t)j * OUTP + o0 + r) * INP + ch * IC + q * PL;
-      bst[u] = gload16(src, e < BCH);
-    }
-  };
-  auto store_b = [&](int buf) {
-#pragma unroll
-    for (int u = 0; u < BPT; ++u) {
-      const int e = tid + u * NTH;
-      const int r = e / (RB / 16), q = e % (RB / 16);
-      if (e < BCH) lds_write16(Bs + (size_t)(buf * BN + r) * RS + 16 * q, bst[u]);
-    }
-  };
 
-  // prologue: stage 0 into buffer 0
-  {
-    load_chunk(0);
-    load_b(0, 0);
-    if (CHEB) {
-      float f[EPT];
-      gen(0, f);
-      store_a(0, f);
-    } else {
-      copy_a(0, 0, 0);
-    }
-    store_b(0);
+  // prologue: stage (chunk 0, pair 0) into buffer 0
+  if (CHEB) {
+    load_z(0);
+    cheb_init();
   }
+  load_b(0, 0);
+  if (CHEB)
+    cheb_step(0);
+  else
+    copy_a(0, 0, 0);
+  store_b(0);
   __syncthreads();
 
-  for (int s = 0; s < S; ++s) {
-    const int buf = s & 1;
-    const int ch = s / n_t, j = s - ch * n_t;
-    const bool more = s + 1 < S;
-    const int ch1 = (j + 1 == n_t) ? ch + 1 : ch, j1 = (j + 1 == n_t) ? 0 : j + 1;
-    if (more) {
-      load_b(ch1, j1);
-      if (CHEB && j == 0 && ch + 1 < n_chunks) load_chunk(ch + 1);
+  int buf = 0;
+  for (int ch = 0; ch < n_chunks; ++ch) {
+    const bool more_chunks = ch + 1 < n_chunks;
+    if (CHEB && more_chunks) load_z(ch + 1);  // consumed at the end of this chunk
+    for (int p = 0; p + 1 < P; ++p) {
+      load_b(ch, p + 1);
+      mfma_stage(buf, p * FPS + 1 < n_t);
+      if (CHEB)
+        cheb_step(buf ^ 1);
+      else
+        copy_a(buf ^ 1, ch, p + 1);
+      store_b(buf ^ 1);
+      __syncthreads();
+      buf ^= 1;
     }
-    // MFMAs on this stage
-#pragma unroll
-    for (int fs = 0; fs < FS; ++fs) {
-      u32x4 af[TM], bfr[TN];
-#pragma unroll
-      for (int a = 0; a < TM; ++a)
-        af[a] = lds_read16(As + (size_t)(buf * BM + wm * WM + a * 32 + l32) * RS + fs * 32 + h * 16);
-#pragma unroll
-      for (int c = 0; c < TN; ++c)
-        bfr[c] = lds_read16(Bs + (size_t)(buf * BN + wn * WN + c * 32 + l32) * RS + fs * 32 + h * 16);
-#pragma unroll
-      for (int a = 0; a < TM; ++a)
-#pragma unroll
-        for (int c = 0; c < TN; ++c) mma32<T>(acc[a][c], af[a], bfr[c]);
-    }
-    // next stage's operands into the other buffer
-    if (more) {
+    // last stage of the chunk: the next one opens chunk ch + 1
+    if (more_chunks) load_b(ch + 1, 0);
+    mfma_stage(buf, (P - 1) * FPS + 1 < n_t);
+    if (more_chunks) {
       if (CHEB) {
-        float f[EPT];
-        gen(j1, f);
-        store_a(buf ^ 1, f);
+        cheb_init();
+        cheb_step(buf ^ 1);
       } else {
-        copy_a(buf ^ 1, ch1, j1);
+        copy_a(buf ^ 1, ch + 1, 0);
       }
       store_b(buf ^ 1);
     }
     __syncthreads();
+    buf ^= 1;
   }
 
   // epilogue
@@ -391,8 +419,6 @@ __global__ __launch_bounds__(WAVES_M* WAVES_J * 64) void p_kernel(KBasis bs, int
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WAVES_J, wj = wave % WAVES_J;
   const int h = lane >> 5, l32 = lane & 31;
-  const int n_t = bs.n_t;
-  const int nrows = n_t * 32;
   const bool g_vec = (OUT % PL) == 0;
 
   f32x16 acc[TM][FW];
@@ -424,7 +450,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_J * 64) void p_kernel(KBasis bs, int
     for (int u = 0; u < BPT; ++u) {
       const int e = tid + u * NTH;
       const int r = e / (RB / 16), q = e % (RB / 16);
-      const bool ok = e < BCH && r < nrows;
+      const bool ok = e < BCH;
       const int j = ok ? r / 32 : 0, il = r % 32;
       bst[u] = gload16(cfmt + ((size_t)j * INP + i0 + il) * OUTP + oc0 + q * PL, ok);
     }
@@ -457,12 +483,10 @@ __global__ __launch_bounds__(WAVES_M* WAVES_J * 64) void p_kernel(KBasis bs, int
         af[a] = lds_read16(As + (size_t)(buf * BM + (wm * TM + a) * 32 + l32) * RS + fs * 32 + h * 16);
 #pragma unroll
       for (int f = 0; f < FW; ++f) {
-        const int j = wj * FW + f;
-        if (j < n_t) {
-          const u32x4 bf = lds_read16(Bs + (size_t)(buf * NMAX + j * 32 + l32) * RS + fs * 32 + h * 16);
+        const int j = wj * FW + f;  // padding features past n_t hold zeros (P) or are ignored (G)
+        const u32x4 bf = lds_read16(Bs + (size_t)(buf * NMAX + j * 32 + l32) * RS + fs * 32 + h * 16);
 #pragma unroll
-          for (int a = 0; a < TM; ++a) mma32<T>(acc[a][f], af[a], bf);
-        }
+        for (int a = 0; a < TM; ++a) mma32<T>(acc[a][f], af[a], bf);
       }
     }
     if (s + 1 < S) store(buf ^ 1);
@@ -598,16 +622,23 @@ __global__ __launch_bounds__(WAVES_M* WAVES_J * 64) void g_kernel(KBasis bs, int
           tp[u] = wv;
           tc[u] = wv * fz[u];
         }
+        // all NTB features (those past n_t are computed but not used); two
+        // per step in ping-pong registers: (tp, tc) = (T_j, T_{j+1})
         lds_write16(dst, pack16<T>(tp));
-        if (n_t > 1) lds_write16(dst + 32 * RS, pack16<T>(tc));
-        for (int j = 2; j < n_t; ++j) {
+        lds_write16(dst + 32 * RS, pack16<T>(tc));
 #pragma unroll
-          for (int u = 0; u < PL; ++u) {
-            const float nt = fmaf(z2[u], tc[u], -tp[u]);
-            tp[u] = tc[u];
-            tc[u] = nt;
-          }
-          lds_write16(dst + (size_t)j * 32 * RS, pack16<T>(tc));
+        for (int j = 2; j + 1 < NTB; j += 2) {
+#pragma unroll
+          for (int u = 0; u < PL; ++u) tp[u] = fmaf(z2[u], tc[u], -tp[u]);
+          lds_write16(dst + (size_t)j * 32 * RS, pack16<T>(tp));
+#pragma unroll
+          for (int u = 0; u < PL; ++u) tc[u] = fmaf(z2[u], tp[u], -tc[u]);
+          lds_write16(dst + (size_t)(j + 1) * 32 * RS, pack16<T>(tc));
+        }
+        if (NTB % 2) {
+#pragma unroll
+          for (int u = 0; u < PL; ++u) tp[u] = fmaf(z2[u], tc[u], -tp[u]);
+          lds_write16(dst + (size_t)(NTB - 1) * 32 * RS, pack16<T>(tp));
         }
       } else {
         // one element at a time: all its features, scattered as single elements
@@ -616,8 +647,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_J * 64) void g_kernel(KBasis bs, int
           float f[NTB];
           kernel_features<NTB>(fz[u], fw[u], gin < IN ? gin : 0, bs, f);
 #pragma unroll
-          for (int j = 0; j < NTB; ++j)
-            if (j < n_t) dst_t[(size_t)j * 32 * RS / sizeof(T) + u] = from_f32<T>(f[j]);
+          for (int j = 0; j < NTB; ++j) dst_t[(size_t)j * 32 * RS / sizeof(T) + u] = from_f32<T>(f[j]);
         }
       }
     }
@@ -638,12 +668,10 @@ __global__ __launch_bounds__(WAVES_M* WAVES_J * 64) void g_kernel(KBasis bs, int
         af[a] = lds_read16(As + (size_t)(buf * BM + (wm * TM + a) * 32 + l32) * RS + fs * 32 + h * 16);
 #pragma unroll
       for (int f = 0; f < FW; ++f) {
-        const int j = wj * FW + f;
-        if (j < n_t) {
-          const u32x4 bf = lds_read16(Bs + (size_t)(buf * NMAX + j * 32 + l32) * RS + fs * 32 + h * 16);
+        const int j = wj * FW + f;  // padding features past n_t hold zeros (P) or are ignored (G)
+        const u32x4 bf = lds_read16(Bs + (size_t)(buf * NMAX + j * 32 + l32) * RS + fs * 32 + h * 16);
 #pragma unroll
-          for (int a = 0; a < TM; ++a) mma32<T>(acc[a][f], af[a], bf);
-        }
+        for (int a = 0; a < TM; ++a) mma32<T>(acc[a][f], af[a], bf);
       }
     }
     if (s + 1 < S) store(buf ^ 1);

@@ -186,3 +186,16 @@ def test_zero_batch_and_errors():
         K._raw("F", plan, 0, torch.zeros(3, 8, device="cuda", dtype=torch.float16), None, c.half(), st, 5)
     with pytest.raises(NotImplementedError):
         K._raw("F", plan, 9, torch.zeros(3, 8, device="cuda"), None, c, st, 5)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16"])
+def test_bspline_nonfinite_and_outside_inputs(dtype):
+    # NaN / inf propagate NaN through the recurrence; finite points outside the
+    # extended grid give zeros (kanforge/bases/spline.py:74-92 arithmetic)
+    basis, plan, st, ob, x, rng = setup("bspline53", 4, 3, seed=7)
+    xs = np.array([[np.nan, np.inf, -np.inf], [-50.0, 50.0, 0.1], [0.2, np.nan, 0.3], [0.0, 0.0, 0.0]])
+    phi = K._features_raw(plan, 0, st, torch.as_tensor(xs, dtype=torch.float32).to("cuda", dtype)).float().cpu().numpy()
+    want = ob(rounded(xs, dtype), 0)
+    np.testing.assert_array_equal(np.isnan(phi), np.isnan(want))
+    finite = ~np.isnan(want)
+    np.testing.assert_allclose(phi[finite], want[finite], atol=2e-2 if dtype == torch.bfloat16 else 1e-6)

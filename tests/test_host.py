@@ -1,0 +1,204 @@
+"""Host-side logic without a GPU: plans and fold matrices, knot tables,
+parameter layout and state_dict names, error behaviour, the C ABI library
+(loads, exports every declared symbol, validates arguments before any
+launch), and the CPU baseline route."""
+
+import ctypes
+import math
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+import kanforge_amd as kf
+from kanforge_amd.bases.spline import ceil_f32, knot_tables
+from kanforge_amd.kernels import plan_for
+from kanforge_amd.torch import GRKAN, KAN, KANLinear
+from kanforge_amd.torch import _lib
+from oracle import kan64 as o
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+rng = np.random.default_rng(0)
+
+
+# --- plans and fold matrices ------------------------------------------------------
+
+
+@pytest.mark.parametrize(
+    "basis,name,kw",
+    [
+        (kf.Chebyshev(8), "chebyshev", {}),
+        (kf.Jacobi(6, 0.5, 0.5), "jacobi", {"alpha": 0.5, "beta": 0.5}),
+        (kf.Legendre(4, input_map="identity"), "legendre", {}),
+        (kf.Gegenbauer(5, 0.75), "gegenbauer", {"lam": 0.75}),
+        (kf.Taylor(3), "taylor", {}),
+    ],
+)
+@pytest.mark.parametrize("m", [0, 1, 2, 3])
+def test_plan_fold_matches_oracle(basis, name, kw, m):
+    plan = plan_for(basis)
+    assert plan.kind == "cheb" and plan.size == basis.size
+    A = o.cheb_coefficients(name, basis.degree, **kw)
+    np.testing.assert_allclose(basis._cheb, A, atol=1e-12)
+    np.testing.assert_allclose(plan.fold(m), o.fold_matrix(A, basis.input_map, m), atol=1e-12)
+    assert plan.n_features(m) == plan.fold(m).shape[1]
+
+
+def test_plans_for_every_kind():
+    assert plan_for(kf.BSpline(8, 3)).kind == "bspline" and plan_for(kf.BSpline(8, 3)).size == 11
+    assert plan_for(kf.Rational(5, 4)).kind == "rational"
+    assert plan_for(kf.Gram(4)).kind == "cheb"
+    with pytest.raises(ValueError):
+        kf.Chebyshev(4, input_map="fractional")
+
+
+def test_gram_coefficients_orthonormal():
+    b = kf.Gram(4)
+    grid = np.linspace(-1, 1, b.points)
+    v = b.host_values(np.arctanh(np.clip(grid, -0.999999, 0.999999)))  # tanh map undone
+    gram = v.T @ v / b.points
+    np.testing.assert_allclose(gram, np.eye(5), atol=1e-4)
+
+
+# --- knot tables --------------------------------------------------------------------
+
+
+def test_ceil32_comparisons_are_exact():
+    t = np.sort(rng.uniform(-2, 2, 50)) + rng.uniform(-1e-9, 1e-9, 50)
+    c = ceil_f32(t)
+    assert (c.astype(np.float64) >= t).all()
+    assert (np.nextafter(c, np.float32(-np.inf)).astype(np.float64) < t).all()  # smallest such float32
+    x = np.concatenate([t.astype(np.float32), np.nextafter(t.astype(np.float32), np.float32(np.inf)), rng.uniform(-2, 2, 500).astype(np.float32)])
+    for tk, ck in zip(t, c):
+        np.testing.assert_array_equal(x.astype(np.float64) >= tk, x >= ck)
+
+
+def test_knot_tables_layout():
+    grid = np.stack([np.linspace(-1, 1, 9), np.linspace(-0.5, 2, 9)])
+    pad, cmp_ = knot_tables(grid, 3)
+    t = o.extend_grid(grid, 3)
+    assert cmp_.shape == (2, 15) and pad.shape == (2, 21)
+    np.testing.assert_allclose(pad[:, 3:-3], t.astype(np.float32))
+    assert (np.diff(pad, axis=1) > 0).all()  # padding knots keep the table strictly increasing
+
+
+# --- layer layout and errors -----------------------------------------------------------
+
+
+def test_kanlinear_parameter_layout_matches_reference():
+    layer = KANLinear(5, 3, kf.BSpline(5, 3), edge_scale=True)
+    names = dict(layer.named_parameters())
+    assert set(names) == {"coef", "base_weight", "bias", "edge_scale"}
+    assert layer.coef.shape == (3, 5, 8) and layer.base_weight.shape == (3, 5) and layer.bias.shape == (3,)
+    sd = layer.state_dict()
+    assert set(sd) == {"coef", "base_weight", "bias", "edge_scale", "edge_mask", "sym_code", "sym_params", "basis_grid"}
+    assert sd["basis_grid"].shape == (5, 6) and sd["sym_code"].dtype == torch.int32
+    cheb = KANLinear(3, 2, "chebyshev", base_activation=None, bias=False)
+    assert set(dict(cheb.named_parameters())) == {"coef"}
+
+
+def test_grkan_layout_and_init():
+    torch.manual_seed(0)
+    layer = GRKAN(64, 64, groups=8)
+    assert layer.base_weight is None
+    assert layer.basis_numerator.shape == (8, 6) and layer.basis_denominator.shape == (8, 4)
+    # coef_init "variance": std = 1 / sqrt(in * E[phi^2]) for x ~ N(0, 1)
+    x, w = np.polynomial.hermite_e.hermegauss(96)
+    m2 = float((w / math.sqrt(2 * math.pi)) @ layer.basis.host_values(x)[:, 0] ** 2)
+    assert abs(layer.coef.std().item() - 1 / math.sqrt(64 * m2)) < 0.01
+    z = np.linspace(-3, 3, 301)
+    gelu = 0.5 * z * (1 + np.vectorize(math.erf)(z / math.sqrt(2)))
+    assert np.abs(layer.basis.host_values(z)[:, 0] - gelu).max() < 2e-2  # rationals start as GELU
+
+
+def test_errors_and_backend_selection():
+    with pytest.raises(ValueError):
+        KANLinear(3, 2, backend="fast")
+    with pytest.raises(ValueError, match="must divide"):
+        KANLinear(5, 2, "rational", groups=2)
+    with pytest.raises(ValueError):
+        KANLinear(3, 2, edge_dropout=1.0)
+    with pytest.raises(RuntimeError, match="ROCm|device"):
+        KANLinear(3, 2, "chebyshev")(torch.zeros(1, 3))  # CPU tensors: no silent fallback
+    with pytest.raises(RuntimeError, match="ops"):
+        KANLinear(3, 2, "chebyshev", backend="ops")(torch.zeros(1, 3))
+    with pytest.raises(ValueError):
+        KAN([3])
+    with pytest.raises(ValueError, match="unknown basis"):
+        kf.make_basis("nope")
+    assert kf.make_basis(kf.Chebyshev(4).config()) == kf.Chebyshev(4)
+
+
+# --- the C ABI ------------------------------------------------------------------------
+
+
+def declared_symbols():
+    header = open(os.path.join(ROOT, "include", "kfhip.h")).read()
+    header = re.sub(r"/\*.*?\*/", "", header, flags=re.S)
+    return sorted(set(re.findall(r"\b(kf_[A-Za-z_0-9]+)\s*\(", header)))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    syms = declared_symbols()
+    assert "kf_F" in syms and "kf_G" in syms and "kf_P" in syms
+    for name in syms:
+        assert hasattr(lib, name), name
+    assert set(syms) == set(_lib.EXPORTS)
+    assert _lib.load().kf_version().decode().startswith("kfhip")
+
+
+def test_abi_struct_matches_header():
+    header = open(os.path.join(ROOT, "include", "kfhip.h")).read()
+    body = header[header.index("typedef struct kf_basis") : header.index("} kf_basis;")]
+    fields = re.findall(r"\b(?:int32_t|const float \*)\s*([a-z_]+);", body)
+    assert fields == [f for f, _ in _lib.KfBasis._fields_]
+    for name in ("KF_F32", "KF_BF16", "KF_KIND_CHEB", "KF_KIND_BSPLINE", "KF_KIND_RATIONAL", "KF_MAX_K", "KF_MAX_NT"):
+        value = int(re.search(rf"#define {name} (-?\d+)", header).group(1))
+        assert getattr(_lib, name) == value, name
+
+
+def test_abi_rejects_bad_arguments_without_launching():
+    lib = _lib.load()
+    b = _lib.KfBasis()
+    rc = lib.kf_F(None, 0, 4, 4, 4, None, None, None, None, None, 0, None)
+    assert rc == -1 and b"NULL" in lib.kf_last_error()
+    b.kind, b.size, b.order, b.n_t = _lib.KF_KIND_CHEB, 9, 0, 9
+    rc = lib.kf_F(ctypes.byref(b), 0, 4, 4, 4, None, None, None, None, None, 0, None)
+    assert rc == -1 and b"fold" in lib.kf_last_error()
+    fold = np.eye(9, dtype=np.float32)
+    b.fold = fold.ctypes.data_as(ctypes.c_void_p)
+    rc = lib.kf_F(ctypes.byref(b), 7, 4, 4, 4, None, None, None, None, None, 0, None)
+    assert rc == -1 and b"dtype" in lib.kf_last_error()
+    rc = lib.kf_F(ctypes.byref(b), 1, 4, 4, 4, None, None, None, None, None, 0, None)
+    assert rc == -1 and b"NULL" in lib.kf_last_error()
+    b.order = 12
+    assert lib.kf_G(ctypes.byref(b), 1, 4, 4, 4, None, None, None, None, None, 0, None) == -4
+    b.order = 0
+    assert lib.kf_workspace_bytes(0, ctypes.byref(b), 1, 8192, 768, 3072) > 0
+    # a workspace that is too small is rejected before any launch
+    rc = lib.kf_F(ctypes.byref(b), 1, 4, 4, 4, ctypes.c_void_p(256), None, ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256), 1, None)
+    assert rc == -2 and b"workspace" in lib.kf_last_error()
+    b.kind, b.size, b.n_t, b.spline_k, b.n_knots = _lib.KF_KIND_BSPLINE, 8, 8, 3, 99
+    rc = lib.kf_features(ctypes.byref(b), 0, 4, 4, None, None, None)
+    assert rc == -1 and b"n_knots" in lib.kf_last_error()
+
+
+# --- CPU baseline route ------------------------------------------------------------
+
+
+def test_cpu_baseline_route_matches_oracle():
+    from oracle.torch_cpu import kan_step
+
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(16, 12, generator=g, dtype=torch.float64)
+    coef = torch.randn(7, 12, 9, generator=g, dtype=torch.float64) * 0.1
+    gy = torch.randn(16, 7, generator=g, dtype=torch.float64)
+    y, gx, gc = kan_step(x, coef, gy, 8)
+    ob = o.Basis64("poly", A=np.eye(9), input_map="tanh")
+    xn, cn, gn = x.numpy(), coef.numpy(), gy.numpy()
+    np.testing.assert_allclose(y.detach().numpy(), o.prim_F(xn, cn, None, ob, 0), atol=1e-12)
+    np.testing.assert_allclose(gx.numpy(), o.prim_P(xn, gn, cn, ob, 1), atol=1e-12)
+    np.testing.assert_allclose(gc.numpy(), o.prim_G(xn, gn, None, ob, 0), atol=1e-12)
