@@ -408,6 +408,21 @@ int launch_g_cfg(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, i
   }
 }
 
+template <typename T, int TM, int FW, int RB>
+int launch_g_ws(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out,
+                const float* zt, const float* wt, const void* gt, void* dc) {
+  constexpr int BM = 2 * TM * 32, NMAX = 2 * FW * 32, RS = RB + 16;
+  const size_t lds_ops = (size_t)2 * (BM + NMAX) * RS, lds_red = (size_t)kb.n_t * (BM / 2) * 33 * 4;
+  const size_t lds = lds_ops > lds_red ? lds_ops : lds_red;
+  auto kern = g_ws_kernel<T, TM, FW, RB>;
+  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+    return fail(KF_ELAUNCH, "G: cannot reserve %zu bytes of LDS", lds);
+  const int n_m = (int)(L.OUTP / BM), n_n = (int)((n_in + 31) / 32);
+  hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(512), lds, s, kb, (int)batch, (int)n_in, (int)n_out, (int)L.BP,
+                     (int)L.OUTP, zt, wt, (const T*)gt, (T*)dc);
+  return check_launch("G");
+}
+
 template <typename T>
 int run_G(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
           const void* g, const void* w, void* dc, void* ws, hipStream_t s) {
@@ -428,7 +443,15 @@ int run_G(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
                        kb.input_map, (const T*)x, (const T*)w, zt, wt);
     rc = check_launch("zmapT");
     if (rc) return rc;
-    return launch_g_cfg<T, true>(L, s, kb, batch, n_in, n_out, x, w, zt, wt, gt, dc);
+    switch (L.cfg) {
+      case 0: return launch_g_ws<T, 2, 2, 128>(L, s, kb, batch, n_in, n_out, zt, wt, gt, dc);
+      case 1: return launch_g_ws<T, 2, 3, 128>(L, s, kb, batch, n_in, n_out, zt, wt, gt, dc);
+      case 2: return launch_g_ws<T, 2, 4, 128>(L, s, kb, batch, n_in, n_out, zt, wt, gt, dc);
+      case 3: return launch_g_ws<T, 2, 5, 128>(L, s, kb, batch, n_in, n_out, zt, wt, gt, dc);
+      case 4: return launch_g_ws<T, 2, 6, 128>(L, s, kb, batch, n_in, n_out, zt, wt, gt, dc);
+      case 5: return launch_g_ws<T, 1, 8, 64>(L, s, kb, batch, n_in, n_out, zt, wt, gt, dc);
+      default: return launch_g_ws<T, 1, 12, 64>(L, s, kb, batch, n_in, n_out, zt, wt, gt, dc);
+    }
   }
   return launch_g_cfg<T, false>(L, s, kb, batch, n_in, n_out, x, w, nullptr, nullptr, gt, dc);
 }

@@ -711,6 +711,203 @@ __global__ __launch_bounds__(WAVES_M* WAVES_J * 64) void g_kernel(KBasis bs, int
 }
 
 // ---------------------------------------------------------------------------
+// G, warp-specialised: 4 consumer waves (2 along M x 2 feature groups) only
+// read LDS fragments and issue MFMAs; 4 producer waves load the gT tile and
+// generate the feature tile of the next stage into the other LDS buffer,
+// with their global loads issued one further stage ahead. One barrier per
+// stage for all 8 waves. Chebyshev plans only (features from z^T).
+template <typename T, int TM, int FW, int RB>
+__global__ __launch_bounds__(512) void g_ws_kernel(KBasis bs, int B, int IN, int OUT, int BP, int OUTP,
+                                                   const float* __restrict__ zt, const float* __restrict__ wt,
+                                                   const T* __restrict__ gt, T* __restrict__ dc) {
+  constexpr int WAVES_M = 2, WAVES_J = 2;
+  constexpr int BM = WAVES_M * TM * 32;
+  constexpr int RS = RB + 16, FS = RB / 32;
+  constexpr int EPS = RB / (int)sizeof(T);  // batch rows per stage
+  constexpr int PL = 16 / (int)sizeof(T);   // rows per generator write
+  constexpr int NTB = WAVES_J * FW;
+  constexpr int NMAX = NTB * 32;
+  constexpr int PTH = 256;                  // producer threads
+  constexpr int ACH = BM * (RB / 16), APT = (ACH + PTH - 1) / PTH;
+  constexpr int GTASK = 32 * (EPS / PL);    // generator tasks per stage
+  static_assert(GTASK <= PTH, "one generator task per producer thread");
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  unsigned char* As = smem;                // [2][BM][RS]
+  unsigned char* Bs = smem + 2 * BM * RS;  // [2][NMAX][RS]
+
+  const int n_m = OUTP / BM, n_n = (IN + 31) / 32;
+  int tm_, tn_;
+  xcd_tile(blockIdx.x, n_m, n_n, tm_, tn_);
+  const int o0 = tm_ * BM, i0 = tn_ * 32;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool consumer = wave < 4;
+  const int n_t = bs.n_t, K = bs.K;
+  const int S = BP / EPS;
+
+  // epilogue helpers: raw feature sums go to LDS in halves of the M tile,
+  // then all threads apply the fold dc[o][i][k] = sum_j fold[k][j] GT[o][i][j]
+  // and write k-fastest (coalesced).
+  float* red = reinterpret_cast<float*>(smem);  // [n_t][BM/2][33]
+  constexpr int HM = BM / 2;
+  auto store_phase = [&](int half) {
+    for (int e = tid; e < HM * 32 * K; e += 512) {
+      const int k = e % K, il = (e / K) % 32, row = e / (K * 32);
+      const int o = o0 + half * HM + row, i = i0 + il;
+      if (o < OUT && i < IN) {
+        float sum = 0.f;
+        for (int j = 0; j < n_t; ++j) sum = fmaf(bs.fold[k * KF_MAX_NT + j], red[(j * HM + row) * 33 + il], sum);
+        dc[((size_t)o * IN + i) * K + k] = from_f32<T>(sum);
+      }
+    }
+  };
+
+  if (consumer) {
+    f32x16 acc[TM][FW];
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+      for (int f = 0; f < FW; ++f)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[a][f][r] = 0.f;
+    const int wm = wave / WAVES_J, wj = wave % WAVES_J;
+    const int h = lane >> 5, l32 = lane & 31;
+    const unsigned char* abase = As + (size_t)((wm * TM) * 32 + l32) * RS + h * 16;
+    const unsigned char* bbase = Bs + (size_t)(wj * FW * 32 + l32) * RS + h * 16;
+    __syncthreads();  // stage 0 ready
+    for (int s = 0; s < S; ++s) {
+      const int buf = s & 1;
+      const unsigned char* ab = abase + buf * BM * RS;
+      const unsigned char* bb = bbase + buf * NMAX * RS;
+      // two fragment sets: step fs+1 is read while the MFMAs of step fs run
+      u32x4 fr[2][TM + FW];
+#pragma unroll
+      for (int a = 0; a < TM; ++a) fr[0][a] = lds_read16(ab + a * 32 * RS);
+#pragma unroll
+      for (int f = 0; f < FW; ++f) fr[0][TM + f] = lds_read16(bb + f * 32 * RS);
+#pragma unroll
+      for (int fs = 0; fs < FS; ++fs) {
+        const int cur = fs & 1;
+        if (fs + 1 < FS) {
+#pragma unroll
+          for (int a = 0; a < TM; ++a) fr[cur ^ 1][a] = lds_read16(ab + a * 32 * RS + (fs + 1) * 32);
+#pragma unroll
+          for (int f = 0; f < FW; ++f) fr[cur ^ 1][TM + f] = lds_read16(bb + f * 32 * RS + (fs + 1) * 32);
+        }
+#pragma unroll
+        for (int f = 0; f < FW; ++f)
+#pragma unroll
+          for (int a = 0; a < TM; ++a) mma32<T>(acc[a][f], fr[cur][a], fr[cur][TM + f]);
+      }
+      __syncthreads();
+    }
+    // the rows of wave (wm, wj) are exactly half wm of the M tile (HM = TM * 32)
+    for (int half = 0; half < 2; ++half) {
+      if (wm == half) {
+#pragma unroll
+        for (int f = 0; f < FW; ++f) {
+          const int j = wj * FW + f;
+          if (j < n_t) {
+            float* dst = red + (size_t)j * HM * 33 + l32;
+#pragma unroll
+            for (int a = 0; a < TM; ++a)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) dst[(a * 32 + acc_row(r, lane)) * 33] = acc[a][f][r];
+          }
+        }
+      }
+      __syncthreads();
+      store_phase(half);
+      __syncthreads();
+    }
+  } else {
+    const int ptid = tid - 256;
+    const int gi = ptid % 32, gq = ptid / 32;
+    const bool gen_on = ptid < GTASK;
+    const int gin = i0 + gi;
+    const bool in_ok = gin < IN;
+    const float* zp = zt + (size_t)(in_ok ? gin : 0) * BP + gq * PL;
+    const float* wp = wt ? wt + (size_t)(in_ok ? gin : 0) * BP + gq * PL : nullptr;
+    const T* gsrc[APT];
+    int adst[APT];
+#pragma unroll
+    for (int u = 0; u < APT; ++u) {
+      const int e = ptid + u * PTH;
+      const int ec = e < ACH ? e : ACH - 1;
+      gsrc[u] = gt + (size_t)(o0 + ec / (RB / 16)) * BP + (ec % (RB / 16)) * PL;
+      adst[u] = (ec / (RB / 16)) * RS + 16 * (ec % (RB / 16));
+    }
+    u32x4 ast[APT];
+    float fz[PL], fw[PL];
+    auto load = [&](int st) {
+      const int bc0 = st * EPS;
+#pragma unroll
+      for (int u = 0; u < APT; ++u) ast[u] = gload16(gsrc[u] + bc0, ptid + u * PTH < ACH);
+      if (gen_on) {
+#pragma unroll
+        for (int q = 0; q < PL / 4; ++q) {
+          const f32x4 v = in_ok ? *reinterpret_cast<const f32x4*>(zp + bc0 + 4 * q) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int u = 0; u < 4; ++u) fz[4 * q + u] = v[u];
+          if (wp) {
+            const f32x4 v2 = in_ok ? *reinterpret_cast<const f32x4*>(wp + bc0 + 4 * q) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) fw[4 * q + u] = v2[u];
+          }
+        }
+      }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+      for (int u = 0; u < APT; ++u)
+        if (ptid + u * PTH < ACH) lds_write16(As + buf * BM * RS + adst[u], ast[u]);
+      if (gen_on) {
+        unsigned char* dst = Bs + (size_t)(buf * NMAX + gi) * RS + gq * 16;
+        float z2[PL], tp[PL], tc[PL];
+#pragma unroll
+        for (int u = 0; u < PL; ++u) {
+          const float wv = wp ? fw[u] : (in_ok ? 1.f : 0.f);
+          z2[u] = 2.f * fz[u];
+          tp[u] = wv;
+          tc[u] = wv * fz[u];
+        }
+        lds_write16(dst, pack16<T>(tp));
+        lds_write16(dst + 32 * RS, pack16<T>(tc));
+#pragma unroll
+        for (int j = 2; j + 1 < NTB; j += 2) {
+#pragma unroll
+          for (int u = 0; u < PL; ++u) tp[u] = fmaf(z2[u], tc[u], -tp[u]);
+          lds_write16(dst + (size_t)j * 32 * RS, pack16<T>(tp));
+#pragma unroll
+          for (int u = 0; u < PL; ++u) tc[u] = fmaf(z2[u], tp[u], -tc[u]);
+          lds_write16(dst + (size_t)(j + 1) * 32 * RS, pack16<T>(tc));
+        }
+        if (NTB % 2) {
+#pragma unroll
+          for (int u = 0; u < PL; ++u) tp[u] = fmaf(z2[u], tc[u], -tp[u]);
+          lds_write16(dst + (size_t)(NTB - 1) * 32 * RS, pack16<T>(tp));
+        }
+      }
+    };
+    load(0);
+    store(0);
+    if (S > 1) load(1);
+    __syncthreads();  // stage 0 ready
+    for (int s = 0; s < S; ++s) {
+      if (s + 1 < S) {
+        store((s + 1) & 1);  // data loaded one stage ago
+        if (s + 2 < S) load(s + 2);
+      }
+      __syncthreads();
+    }
+    for (int half = 0; half < 2; ++half) {
+      __syncthreads();
+      store_phase(half);
+      __syncthreads();
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // edge_derivative: out[b,o,i] = sum_k c[o,i,k] phi_k^(m)(x[b,i]) + W[o,i] silu^(m)(x[b,i])
 // Block: ROWS batch rows x 64 inputs, all outputs. Phase 1 evaluates the
 // features into LDS; phase 2 streams the outputs, i fastest (coalesced).
