@@ -137,17 +137,27 @@ struct WsF {
   int64_t INP, OUTP, BP;
   size_t cfm, z, wz, phi, total;
 };
+// bf16 Chebyshev plans run the register-A F kernel: wave tile (32 RA_TM) x
+// (32 RA_TN), four waves along the batch.
+constexpr int F_REGA = -1;
+constexpr int RA_TM = 2, RA_TN = 6, RA_BM = 128 * RA_TM, RA_BN = 32 * RA_TN;
+bool f_uses_rega(const kf_basis* b, int dtype) { return b->kind == KF_KIND_CHEB && dtype == KF_BF16; }
+// odd feature counts with an unpadded, unrolled variant
+bool f_rega_unpadded(int n_t, int64_t n_in) { return n_t == 9; }
+
 WsF ws_f(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, bool has_w) {
   WsF w;
-  w.cfg = pick_f_cfg(batch, n_out);
-  const FCfg& c = F_CFGS[w.cfg];
+  const bool rega = f_uses_rega(b, dtype);
+  w.cfg = rega ? F_REGA : pick_f_cfg(batch, n_out);
+  const int bm = rega ? RA_BM : F_CFGS[w.cfg].bm, bn = rega ? RA_BN : F_CFGS[w.cfg].bn;
   w.INP = round_up(n_in, CHUNK);
-  w.OUTP = round_up(n_out, c.bn);
-  w.BP = round_up(batch, c.bm);
+  w.OUTP = round_up(n_out, bn);
+  w.BP = round_up(batch, bm);
   const int es = elt_size(dtype);
   const bool cheb = b->kind == KF_KIND_CHEB;
   const int fps = dtype == KF_BF16 ? 2 : 1;
-  w.n_tp = (b->n_t + fps - 1) / fps * fps;
+  w.n_tp = rega && f_rega_unpadded(b->n_t, n_in) ? b->n_t : (b->n_t + fps - 1) / fps * fps;
+  if (rega && w.n_tp < 4) w.n_tp = 4;  // the register-A kernel needs two stages per chunk
   w.cfm = align256((size_t)w.n_tp * w.OUTP * w.INP * es);
   w.z = cheb ? align256((size_t)w.BP * w.INP * sizeof(float)) : 0;
   w.wz = cheb && has_w ? align256((size_t)w.BP * w.INP * sizeof(float)) : 0;
@@ -155,10 +165,11 @@ WsF ws_f(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
   w.total = w.cfm + w.z + w.wz + w.phi;
   return w;
 }
-// P / G configurations. The waves split the features in two groups of
+// P / G configurations. The MFMA waves split the features in two groups of
 // FW = ceil(n_t / 2) (FW in {2,3,4,5,6,8,12}); TM 32-row tiles per wave keep
 // the accumulators at <= 192 registers. P: 4x2 waves (512 threads, 64-byte
-// stages); G: 2x2 waves (256 threads, 128-byte stages, 64 from FW = 8).
+// stages); G: warp-specialised for Chebyshev plans (4 MFMA waves + 4
+// producer waves, 128-byte stages, 64 from FW = 8), else 2x2 waves.
 constexpr int FW_LIST[] = {2, 3, 4, 5, 6, 8, 12};
 int fw_index(int n_t) {
   const int need = (n_t + 1) / 2;
@@ -166,7 +177,6 @@ int fw_index(int n_t) {
     if (FW_LIST[k] >= need) return k;
   return 6;
 }
-int p_tm(int fw) { return fw <= 5 ? 2 : 1; }
 int g_tm(int fw) { return fw <= 6 ? 2 : 1; }
 int g_rb(int fw) { return fw <= 6 ? 128 : 64; }
 
@@ -225,15 +235,14 @@ int zero_fill(void* p, long n, hipStream_t s) {
 // n_feat >= n_t features (zeros past n_t)
 template <typename T>
 int launch_permute(const KBasis& kb, int64_t n_out, int64_t n_in, int64_t OUTP, int64_t INP, int n_feat, const void* c,
-                   void* out, bool fmt, hipStream_t s) {
+                   void* out, int fmt, hipStream_t s) {
   dim3 grid((unsigned)((OUTP + 31) / 32), (unsigned)((INP + 15) / 16));
   size_t lds = (size_t)n_feat * 16 * 33 * sizeof(float);
-  if (fmt)
-    hipLaunchKernelGGL((permute_coef_kernel<T, true>), grid, dim3(kThreads), lds, s, kb, (int)n_out, (int)n_in,
-                       (int)OUTP, (int)INP, n_feat, (const T*)c, (T*)out);
-  else
-    hipLaunchKernelGGL((permute_coef_kernel<T, false>), grid, dim3(kThreads), lds, s, kb, (int)n_out, (int)n_in,
-                       (int)OUTP, (int)INP, n_feat, (const T*)c, (T*)out);
+  auto kern = fmt == kPermFMT ? permute_coef_kernel<T, kPermFMT>
+              : fmt == kPermC16 ? permute_coef_kernel<T, kPermC16>
+                                : permute_coef_kernel<T, kPermFM>;
+  hipLaunchKernelGGL(kern, grid, dim3(kThreads), lds, s, kb, (int)n_out, (int)n_in, (int)OUTP, (int)INP, n_feat,
+                     (const T*)c, (T*)out);
   return check_launch("permute_coef");
 }
 
@@ -295,6 +304,20 @@ int launch_f_t(const WsF& L, int64_t batch, int64_t n_out, int n_t, const float*
   return check_launch("F");
 }
 
+template <bool HAS_W>
+int launch_f_rega(const WsF& L, int64_t batch, int64_t n_out, int n_t, const float* zc, const float* wc, const void* cfm,
+              void* y, hipStream_t s) {
+  const int n_m = (int)(L.BP / RA_BM), n_n = (int)(L.OUTP / RA_BN);
+  // 4 stage buffers of 2 features, z (and w) of two chunks
+  const size_t lds = (size_t)4 * 2 * RA_BN * 32 + (size_t)(HAS_W ? 4 : 2) * RA_BM * 64;
+  auto kern = L.n_tp == 9 ? f_rega_kernel<HAS_W, 9, RA_TM, RA_TN> : f_rega_kernel<HAS_W, 0, RA_TM, RA_TN>;
+  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+    return fail(KF_ELAUNCH, "F: cannot reserve %zu bytes of LDS", lds);
+  hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(256), lds, s, (int)batch, (int)n_out, (int)L.OUTP, (int)L.BP,
+                     (int)(L.INP / 16), L.n_tp, zc, wc, (const bf16*)cfm, (bf16*)y);
+  return check_launch("F");
+}
+
 template <typename T, bool CHEB, bool HAS_W>
 int launch_f_cfg(const WsF& L, int64_t batch, int64_t n_out, int n_t, const float* z, const float* wz, const void* cfm,
                  const void* phi, void* y, hipStream_t s) {
@@ -316,7 +339,20 @@ int run_F(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
   float* z = (float*)(base + L.cfm);
   float* wz = has_w && cheb ? (float*)(base + L.cfm + L.z) : nullptr;
   void* phi = base + L.cfm + L.z + L.wz;
-  int rc = launch_permute<T>(kb, n_out, n_in, L.OUTP, L.INP, L.n_tp, c, cfm, false, s);
+  if (L.cfg == F_REGA) {
+    int rc = launch_permute<T>(kb, n_out, n_in, L.OUTP, L.INP, L.n_tp, c, cfm, kPermC16, s);
+    if (rc) return rc;
+    long n = (long)L.BP * L.INP;
+    long blocks = (n + kThreads - 1) / kThreads;
+    if (blocks > 65535 * 4) blocks = 65535 * 4;
+    hipLaunchKernelGGL(zmapc_kernel<T>, dim3((unsigned)blocks), dim3(kThreads), 0, s, (int)batch, (int)n_in,
+                       (int)L.BP, (int)L.INP, kb.input_map, (const T*)x, (const T*)w, z, wz);
+    rc = check_launch("zmapc");
+    if (rc) return rc;
+    if (has_w) return launch_f_rega<true>(L, batch, n_out, kb.n_t, z, wz, cfm, y, s);
+    return launch_f_rega<false>(L, batch, n_out, kb.n_t, z, nullptr, cfm, y, s);
+  }
+  int rc = launch_permute<T>(kb, n_out, n_in, L.OUTP, L.INP, L.n_tp, c, cfm, kPermFM, s);
   if (rc) return rc;
   if (cheb) {
     long n = (long)L.BP * L.INP;
@@ -366,7 +402,7 @@ int run_P(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
           const void* g, const void* c, void* p, float* h, void* ws, hipStream_t s) {
   WsP L = ws_p(b, dtype, n_in, n_out);
   void* cfmt = ws;
-  int rc = launch_permute<T>(kb, n_out, n_in, L.OUTP, L.INP, L.ntb, c, cfmt, true, s);
+  int rc = launch_permute<T>(kb, n_out, n_in, L.OUTP, L.INP, L.ntb, c, cfmt, kPermFMT, s);
   if (rc) return rc;
   switch (L.cfg) {
     case 0: return launch_p_t<T, 4, 2, 2, 2>(L, s, kb, batch, n_in, n_out, x, g, cfmt, p, h);

@@ -112,4 +112,20 @@ __device__ __forceinline__ void xcd_tile(int g, int n_m, int n_n, int& tm, int& 
   tn = logical % n_n;
 }
 
+// Grouped variant: inside each XCD's contiguous range, tiles run in groups
+// of GM m-tiles x every n-tile, m fastest, so the workgroups resident on one
+// XCD at a time share both operand panels in its L2 (GM m-panels and about
+// 32 / GM n-panels instead of 1 x 32 or 32 x 1).
+__device__ __forceinline__ void xcd_tile_grouped(int g, int n_m, int n_n, int GM, int& tm, int& tn) {
+  const int total = n_m * n_n;
+  int logical = g;
+  if (total % 8 == 0) logical = (g % 8) * (total / 8) + g / 8;
+  const int per_group = GM * n_n;
+  const int first_m = (logical / per_group) * GM;
+  const int gm = n_m - first_m < GM ? n_m - first_m : GM;
+  const int r = logical % per_group;
+  tm = first_m + r % gm;
+  tn = r / gm;
+}
+
 }  // namespace kf

@@ -11,6 +11,8 @@
 // feature-major (feature j, then 32 inputs), which lets the Chebyshev
 // recurrence emit one feature per k-group.
 #pragma once
+
+#include <type_traits>
 #include "kf_gemm.h"
 
 namespace kf {
@@ -19,10 +21,14 @@ constexpr int kThreads = 256;
 
 // ---------------------------------------------------------------------------
 // Coefficients c (n_out, n_in, K) -> folded, feature-major, zero-padded copy:
-//   FM : out[j][o][i]  (n_t, OUTP, INP)   B operand of F
-//   FMT: out[j][i][o]  (n_t, INP, OUTP)   B operand of P
+//   kPermFM : out[j][o][i]             (n_t, OUTP, INP)      B operand of F
+//   kPermFMT: out[j][i][o]             (n_t, INP, OUTP)      B operand of P
+//   kPermC16: out[i/16][j][o][i%16]    (INP/16, n_t, OUTP, 16)
+//             every (16-input chunk, feature) block contiguous: B operand
+//             of the register-A F kernel, whose stages read whole blocks
 // out[j] = sum_k c[o,i,k] fold[k][j]. Tile 32 o x 16 i through LDS.
-template <typename T, bool FMT>
+enum { kPermFM = 0, kPermFMT = 1, kPermC16 = 2 };
+template <typename T, int FMT>
 __global__ __launch_bounds__(kThreads) void permute_coef_kernel(KBasis bs, int OUT, int IN, int OUTP, int INP,
                                                                 int n_feat, const T* __restrict__ c,
                                                                 T* __restrict__ out) {
@@ -47,7 +53,15 @@ __global__ __launch_bounds__(kThreads) void permute_coef_kernel(KBasis bs, int O
     }
   }
   __syncthreads();
-  if (!FMT) {
+  if (FMT == kPermC16) {
+    // out[i/16][j][o][i%16]: 16 inputs of one output row contiguous, then o
+    T* blk = out + (size_t)blockIdx.y * n_t * OUTP * 16;
+    for (int e = t; e < n_t * 32 * 16; e += kThreads) {
+      const int il = e % 16, ol = (e / 16) % 32, j = e / (16 * 32);
+      const int o = o0 + ol;
+      if (o < OUTP) blk[((size_t)j * OUTP + o) * 16 + il] = from_f32<T>(tile[(j * 16 + il) * 33 + ol]);
+    }
+  } else if (FMT == kPermFM) {
     // out[j][o][i]: consecutive threads along i
     for (int e = t; e < n_t * 32 * 16; e += kThreads) {
       const int il = e % 16, ol = (e / 16) % 32, j = e / (16 * 32);
@@ -131,6 +145,24 @@ __global__ __launch_bounds__(kThreads) void zmap_kernel(int B, int IN, int BP, i
     const size_t off = (size_t)b * IN + i;
     z[e] = ok ? cheb_map(to_f32(x[off]), input_map) : 0.f;
     if (wz) wz[e] = ok ? to_f32(w[off]) : 0.f;
+  }
+}
+
+// Chunked variant for the register-A F kernel: zc[c][b][e] = g(x[b][16c+e])
+// (and wc likewise), float32, zero-padded to (INP/16, BP, 16), so the 16
+// inputs of one row in one chunk are 64 contiguous bytes.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void zmapc_kernel(int B, int IN, int BP, int INP, int input_map,
+                                                         const T* __restrict__ x, const T* __restrict__ w,
+                                                         float* __restrict__ zc, float* __restrict__ wc) {
+  const long n = (long)BP * INP;
+  for (long e = blockIdx.x * (long)kThreads + threadIdx.x; e < n; e += (long)gridDim.x * kThreads) {
+    const int il = (int)(e % 16), b = (int)((e / 16) % BP), c = (int)(e / (16L * BP));
+    const int i = c * 16 + il;
+    const bool ok = b < B && i < IN;
+    const size_t off = (size_t)b * IN + i;
+    zc[e] = ok ? cheb_map(to_f32(x[off]), input_map) : 0.f;
+    if (wc) wc[e] = ok ? to_f32(w[off]) : 0.f;
   }
 }
 
@@ -708,6 +740,291 @@ __global__ __launch_bounds__(WAVES_M* WAVES_J * 64) void g_kernel(KBasis bs, int
     }
     __syncthreads();
   }
+}
+
+// ---------------------------------------------------------------------------
+// Direct global -> LDS copies (gfx950 global_load_lds_dwordx4): lane l of the
+// wave writes its 16 bytes to LDS at dst + 16 l, no VGPRs involved. The
+// copies count in vmcnt like loads; the compiler does not order them against
+// LDS reads, so kernels wait for them with vmem_wait before the barrier that
+// publishes the data.
+__device__ __forceinline__ void lds_dma16(const void* src, void* lds_dst) {
+  __builtin_amdgcn_global_load_lds(const_cast<void*>(src), reinterpret_cast<__attribute__((address_space(3))) void*>(
+                                                              reinterpret_cast<uintptr_t>(lds_dst)),
+                                   16, 0, 0);
+}
+template <int N>
+__device__ __forceinline__ void vmem_wait() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// ---------------------------------------------------------------------------
+// F for bf16 Chebyshev plans with the A operand in registers:
+//   y[b,o] = sum_{c, j} sum_{e < 16} w T_j(z)[b][16c+e] * Cfm[c][j][o][e]
+// 4 waves stacked along the batch (they share every coefficient fragment,
+// which halves the L2 -> LDS traffic against a 2 x 2 arrangement), wave tile
+// (32 TM) x (32 TN), float32 accumulators in AGPRs. Every lane builds its own MFMA A fragments (rows b, 8 consecutive
+// inputs of a 16-input chunk) with the Chebyshev recurrence in float32
+// registers, so the features never touch LDS; with TM = 2 that costs 24 VALU
+// instructions per feature against 2 TN MFMAs, interleaved so that the
+// matrix core hides them.
+// Operands reach LDS by direct global -> LDS copies into a ring of NBUF stage
+// buffers (prefetch distance NBUF - 1 stages): the coefficient tile of each
+// stage, and z (and w) of a chunk, attached to the stage whose MFMAs first
+// need it, into a double buffer. In LDS a feature's 32-byte output rows are
+// dense with the two 16-byte halves of row o swapped when bit 3 of o is set,
+// which makes the 16-byte fragment reads conflict-free.
+// A stage is two features (slots); it is software-pipelined around one
+// mid-stage barrier: the first half runs the first slot's MFMAs while the
+// second slot's A fragments are generated and its B fragments read; the
+// barrier publishes stage s + 1; the second half runs the second slot's MFMAs
+// while stage s + 1's first slot is prepared. The copies into a buffer are
+// issued at the start of the stage after its last reads, so the one barrier
+// orders both directions.
+// The reduction runs over the flat feature sequence f = c * n_tp + j (Cfm
+// block f at f * OUTP * 16). The recurrence alternates between the registers
+// (a, b) (first slot: a <- 2 z b - a, second: b <- 2 z a - b); a chunk starts
+// by seeding (T_-2, T_-1) = (w T_2(z), w T_1(z)) into (a, b) at a first slot,
+// (b, a) at a second one, so its first step yields w T_0.
+//   NT == 0: n_tp = n_t rounded up to even (zero coefficients past n_t), so
+//            chunks are whole stages; chunk c + 1 is seeded in the second half
+//            of the last stage of chunk c;
+//   NT odd : n_tp = NT, no padding; a chunk pair is NT stages, chunk c + 1 is
+//            seeded in the first half of its middle stage (q = NT / 2), chunk
+//            c + 2 in the second half of its last one (unrolled).
+// The MFMAs are never under a condition, which keeps the accumulators in
+// AGPRs across the loops.
+template <bool HAS_W, int NT, int TM, int TN>
+__global__ __launch_bounds__(256) void f_rega_kernel(int B, int OUT, int OUTP, int BP, int n_chunks, int n_tp,
+                                                     const float* __restrict__ zc, const float* __restrict__ wc,
+                                                     const bf16* __restrict__ cfm, bf16* __restrict__ y) {
+  constexpr int WM = TM * 32, BM = 4 * WM, BN = TN * 32;
+  constexpr int NBUF = 4;
+  constexpr int FB = BN * 32;      // one feature of a stage (dense 32-byte rows)
+  constexpr int SB = 2 * FB;       // one stage
+  constexpr int BPW = SB / 4096;   // 1 KB copy blocks per wave and stage
+  constexpr int ZB = BM * 64;      // z of one chunk: BM rows x 16 floats
+  constexpr int ZPW = ZB / 4096;   // 1 KB copy blocks per wave for z (and again for w)
+  constexpr int ZPW_ALL = HAS_W ? 2 * ZPW : ZPW;
+  static_assert(BPW * 4096 == SB && ZPW * 4096 == ZB, "copy blocks divide over the waves");
+  static_assert(NBUF == 4, "copy waits below count up to two newer stages");
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];  // [NBUF][SB], z [2][ZB], w [2][ZB]
+  unsigned char* zs = smem + NBUF * SB;
+  unsigned char* ws = zs + 2 * ZB;
+
+  const int n_m = BP / BM, n_n = OUTP / BN;
+  int tm_, tn_;
+  xcd_tile_grouped(blockIdx.x, n_m, n_n, 8, tm_, tn_);
+  const int b0 = tm_ * BM, o0 = tn_ * BN;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave;
+  const int h = lane >> 5, l32 = lane & 31;
+  const int S = n_chunks * n_tp / 2;                 // n_chunks is even
+  const int P = n_tp / 2;                            // stages per chunk (NT == 0), at least 2
+  const size_t stage_elems = (size_t)2 * OUTP * 16;  // stage s starts at cfm + s * stage_elems
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int a = 0; a < TM; ++a)
+#pragma unroll
+    for (int c = 0; c < TN; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[a][c][r] = 0.f;
+
+  // z of chunk x travels with the copy group of stage g(x), published at the mid-stage barrier of
+  // stage g(x) - 1: NT == 0: g = x P (chunk x is seeded in the second half of stage x P - 1);
+  // NT odd: odd x is seeded in the first half of stage g = pair NT + NT / 2, even x in the second
+  // half of the pair's last stage, g = pair NT + NT. Groups are copied in stage order, so a small
+  // state machine tracks the next carrier; zbits keeps the carrier flags of the last two groups.
+  int zg_next = NT == 0 ? P : NT / 2, zx_next = 1, zbits = 0;
+  // coefficient copy block k of this wave: stage block blk = wave * BPW + k, feature
+  // blk / (BN / 32), rows 32 (blk % (BN / 32)) .. +32; lane l fills 16-byte chunk l of the
+  // block = row o = base + l / 2, half (l & 1) ^ bit 3 of o
+  const bf16* bsrc = cfm + (size_t)o0 * 16;
+  int doff[BPW];
+#pragma unroll
+  for (int k = 0; k < BPW; ++k) {
+    const int blk = wave * BPW + k;
+    const int f = blk / (BN / 32), o = (blk % (BN / 32)) * 32 + (lane >> 1);
+    const int hh = (lane & 1) ^ ((o >> 3) & 1);
+    doff[k] = (f * OUTP + o) * 16 + hh * 8;
+  }
+  auto copy_z = [&](int x) {  // rows b0 .. b0 + BM of chunk x: BM * 64 contiguous bytes
+    const size_t off = ((size_t)x * BP + b0) * 16 + wave * ZPW * 256 + lane * 4;
+#pragma unroll
+    for (int k = 0; k < ZPW; ++k) {
+      lds_dma16(zc + off + k * 256, zs + (x & 1) * ZB + (wave * ZPW + k) * 1024);
+      if (HAS_W) lds_dma16(wc + off + k * 256, ws + (x & 1) * ZB + (wave * ZPW + k) * 1024);
+    }
+  };
+  // copy group of stage st into buffer st % NBUF; past the last stage the buffer is free and
+  // the copy repeats the last stage's source, which keeps every stage's block count the same
+  auto copy_stage = [&](int st) {
+    const bf16* src = bsrc + (size_t)(st < S ? st : S - 1) * stage_elems;
+    unsigned char* dst = smem + (st % NBUF) * SB + wave * BPW * 1024;
+#pragma unroll
+    for (int k = 0; k < BPW; ++k) lds_dma16(src + doff[k], dst + k * 1024);
+    int flag = 0;
+    if (st == zg_next) {
+      if (zx_next < n_chunks) {
+        copy_z(zx_next);
+        flag = 1;
+      }
+      zg_next += NT == 0 ? P : (zx_next & 1) ? NT / 2 + 1 : NT / 2;
+      ++zx_next;
+    }
+    zbits = ((zbits << 1) | flag) & 3;
+  };
+  // wait until this wave's copies of the group before the last two issued are in LDS (those two
+  // may remain in flight)
+  auto wait_group = [&]() {
+    const int nz = (zbits & 1) + (zbits >> 1);
+    if (nz == 0)
+      vmem_wait<2 * BPW>();
+    else if (nz == 1)
+      vmem_wait<2 * BPW + ZPW_ALL>();
+    else
+      vmem_wait<2 * BPW + 2 * ZPW_ALL>();
+  };
+  // fragment read offset of this lane inside a feature: row l32 (+ 32 t), half h swizzled
+  const int frag_off = (2 * l32 + (h ^ ((l32 >> 3) & 1))) * 16;
+
+  // A generator: row block a (rows b0 + WM wm + 32 a + l32), inputs 8h..8h+7 of the chunk
+  float ga[TM][8], gb[TM][8], z2[TM][8];
+  const int zrow_off = ((wm * WM + l32) * 16 + h * 8) * 4;
+  // seed chunk x for a first (SECOND false) or second slot from its z (w) in LDS
+  auto seed = [&](auto second_tag, int x) {
+    constexpr bool SECOND = decltype(second_tag)::value;
+#pragma unroll
+    for (int a = 0; a < TM; ++a) {
+      const unsigned char* zr = zs + (x & 1) * ZB + zrow_off + a * 32 * 64;
+      const f32x4 z0 = __builtin_bit_cast(f32x4, lds_read16(zr)), z1 = __builtin_bit_cast(f32x4, lds_read16(zr + 16));
+      f32x4 w0 = {1.f, 1.f, 1.f, 1.f}, w1 = w0;
+      if (HAS_W) {
+        const unsigned char* wr = ws + (x & 1) * ZB + zrow_off + a * 32 * 64;
+        w0 = __builtin_bit_cast(f32x4, lds_read16(wr));
+        w1 = __builtin_bit_cast(f32x4, lds_read16(wr + 16));
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float zz = e < 4 ? z0[e] : z1[e - 4], w_ = e < 4 ? w0[e] : w1[e - 4];
+        const float t2 = w_ * fmaf(2.f * zz, zz, -1.f), t1 = w_ * zz;
+        z2[a][e] = 2.f * zz;
+        ga[a][e] = SECOND ? t1 : t2;
+        gb[a][e] = SECOND ? t2 : t1;
+      }
+    }
+  };
+  // A fragments of the two slots and B fragments of the two features of a stage
+  u32x4 af0[TM], af1[TM], bf0[TN], bf1[TN];
+  auto step_first = [&]() {
+#pragma unroll
+    for (int a = 0; a < TM; ++a) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ga[a][e] = fmaf(z2[a][e], gb[a][e], -ga[a][e]);
+      af0[a] = pack16<bf16>(ga[a]);
+    }
+  };
+  auto step_second = [&]() {
+#pragma unroll
+    for (int a = 0; a < TM; ++a) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) gb[a][e] = fmaf(z2[a][e], ga[a][e], -gb[a][e]);
+      af1[a] = pack16<bf16>(gb[a]);
+    }
+  };
+  auto read_b = [&](int st, int f, u32x4(&bf)[TN]) {
+    const unsigned char* bb = smem + (st % NBUF) * SB + f * FB + frag_off;
+#pragma unroll
+    for (int t = 0; t < TN; ++t) bf[t] = lds_read16(bb + t * 1024);
+  };
+  // the MFMAs of one slot: the first one alone (issued before the half stage's other work, so
+  // the matrix core never waits for it), then the rest, each followed by up to 4 VALU
+  // instructions (the next slot's A fragments), which the matrix core hides
+  auto mma_first = [&](const u32x4(&af)[TM], const u32x4(&bf)[TN]) {
+    mma32<bf16>(acc[0][0], af[0], bf[0]);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto mma_rest = [&](const u32x4(&af)[TM], const u32x4(&bf)[TN]) {
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+      for (int t = 0; t < TN; ++t)
+        if (a + t > 0) mma32<bf16>(acc[a][t], af[a], bf[t]);
+#pragma unroll
+    for (int i = 1; i < TM * TN; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+    }
+  };
+  int s = 0;
+  // stage s; on entry af0 / bf0 hold its first slot. SEED2: chunk x2 starts at its second slot;
+  // SEEDN: chunk xn starts at the first slot of stage s + 1.
+  auto stage = [&](auto seed2_tag, auto seedn_tag, int x2, int xn) {
+    constexpr bool SEED2 = decltype(seed2_tag)::value, SEEDN = decltype(seedn_tag)::value;
+    mma_first(af0, bf0);
+    copy_stage(s + NBUF - 1);
+    read_b(s, 1, bf1);
+    if constexpr (SEED2) seed(std::true_type{}, x2);
+    step_second();
+    mma_rest(af0, bf0);
+    // publish stage s + 1 (this wave's copies done, its reads of stage s returned)
+    wait_group();
+    lds_wait();
+    __builtin_amdgcn_s_barrier();
+    mma_first(af1, bf1);
+    read_b(s + 1, 0, bf0);
+    if constexpr (SEEDN) seed(std::false_type{}, xn);
+    step_first();
+    mma_rest(af1, bf1);
+    ++s;
+  };
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+
+  // prologue: z of chunk 0 and the groups of stages 0 .. NBUF - 2 in flight; z(0) and stage 0
+  // published; the first slot of stage 0 prepared
+  copy_z(0);
+  for (int st = 0; st < NBUF - 1; ++st) copy_stage(st);
+  wait_group();
+  __builtin_amdgcn_s_barrier();
+  read_b(0, 0, bf0);
+  seed(F_{}, 0);
+  step_first();
+
+  if constexpr (NT == 0) {
+    for (int c = 0; c < n_chunks; ++c) {
+      for (int p = 0; p + 1 < P; ++p) stage(F_{}, F_{}, 0, 0);
+      stage(F_{}, T_{}, 0, c + 1);  // chunk c + 1 starts at the next stage's first slot
+    }
+  } else {
+    static_assert(NT % 2 == 1, "unpadded variants are for odd feature counts");
+    for (int c = 0; c < n_chunks; c += 2) {
+#pragma unroll
+      for (int q = 0; q < NT; ++q) {
+        if (q == NT / 2)
+          stage(T_{}, F_{}, c + 1, 0);  // chunk c + 1 starts at this stage's second slot
+        else if (q == NT - 1)
+          stage(F_{}, T_{}, 0, c + 2);  // chunk c + 2 starts at the next stage's first slot
+        else
+          stage(F_{}, F_{}, 0, 0);
+      }
+    }
+  }
+
+#pragma unroll
+  for (int a = 0; a < TM; ++a)
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+      const int o = o0 + t * 32 + l32;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int b = b0 + wm * WM + a * 32 + acc_row(r, lane);
+        if (b < B && o < OUT) y[(size_t)b * OUT + o] = from_f32<bf16>(acc[a][t][r]);
+      }
+    }
 }
 
 // ---------------------------------------------------------------------------
