@@ -50,6 +50,10 @@ extern "C" {
 /* input maps of the Chebyshev family (kanforge/bases/polynomial.py:66-85) */
 #define KF_MAP_IDENTITY 0
 #define KF_MAP_TANH 1
+/* tanh map whose kernel features carry the factor (1 - z^2): every x-derivative of f(tanh x)
+ * of order m >= 1 is (1 - z^2) q(z) with deg q = deg f + m - 2, so R_m divided by (1 - z^2)
+ * needs two features fewer than R_m itself (same values; not a reference map) */
+#define KF_MAP_TANH_SQ 2
 
 #define KF_MAX_K 16   /* basis functions per edge */
 #define KF_MAX_NT 24  /* kernel features per edge (K + derivative order for tanh maps) */

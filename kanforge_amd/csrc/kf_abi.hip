@@ -44,7 +44,7 @@ int validate_basis(const kf_basis* b) {
   switch (b->kind) {
     case KF_KIND_CHEB:
       if (!b->fold) return fail(KF_EINVAL, "cheb basis needs the fold matrix");
-      if (b->input_map != KF_MAP_TANH && b->input_map != KF_MAP_IDENTITY)
+      if (b->input_map != KF_MAP_TANH && b->input_map != KF_MAP_IDENTITY && b->input_map != KF_MAP_TANH_SQ)
         return fail(KF_EINVAL, "unknown input map %d", b->input_map);
       break;
     case KF_KIND_BSPLINE:
@@ -141,6 +141,7 @@ struct WsF {
 // (32 RA_TN), four waves along the batch.
 constexpr int F_REGA = -1;
 constexpr int RA_TM = 2, RA_TN = 6, RA_BM = 128 * RA_TM, RA_BN = 32 * RA_TN;
+constexpr int RA_NBUF = 4;  // coefficient stage buffers (prefetch distance RA_NBUF - 1 stages)
 bool f_uses_rega(const kf_basis* b, int dtype) { return b->kind == KF_KIND_CHEB && dtype == KF_BF16; }
 // odd feature counts with an unpadded, unrolled variant
 bool f_rega_unpadded(int n_t, int64_t n_in) { return n_t == 9; }
@@ -157,7 +158,9 @@ WsF ws_f(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
   const bool cheb = b->kind == KF_KIND_CHEB;
   const int fps = dtype == KF_BF16 ? 2 : 1;
   w.n_tp = rega && f_rega_unpadded(b->n_t, n_in) ? b->n_t : (b->n_t + fps - 1) / fps * fps;
-  if (rega && w.n_tp < 4) w.n_tp = 4;  // the register-A kernel needs two stages per chunk
+  // the register-A kernel needs chunks of at least RA_NBUF / 2 (and 2) stages
+  const int min_tp = RA_NBUF < 4 ? 4 : RA_NBUF;
+  if (rega && w.n_tp < min_tp) w.n_tp = min_tp;
   w.cfm = align256((size_t)w.n_tp * w.OUTP * w.INP * es);
   w.z = cheb ? align256((size_t)w.BP * w.INP * sizeof(float)) : 0;
   w.wz = cheb && has_w ? align256((size_t)w.BP * w.INP * sizeof(float)) : 0;
@@ -183,16 +186,23 @@ int g_rb(int fw) { return fw <= 6 ? 128 : 64; }
 struct WsP {
   int cfg, ntb;
   int64_t INP, OUTP;
-  size_t cfmt, total;
+  size_t cfmt, gpad, total;
 };
-WsP ws_p(const kf_basis* b, int dtype, int64_t n_in, int64_t n_out) {
+// P with FW <= 4 runs the copy kernel (p_dma_kernel; 4 x FW accumulator tiles in AGPRs); it needs
+// g with whole 128-byte stages of columns and 16-byte aligned rows, else a zero-padded copy of g
+// in the workspace.
+bool p_uses_dma(int cfg) { return FW_LIST[cfg] <= 4; }
+int64_t p_stage_cols(int dtype) { return 128 / elt_size(dtype); }
+bool p_needs_gpad(int64_t n_out, int dtype) { return n_out % p_stage_cols(dtype) != 0; }
+WsP ws_p(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out) {
   WsP w;
   w.cfg = fw_index(b->n_t);
   w.ntb = 2 * FW_LIST[w.cfg];
   w.INP = round_up(n_in, 32);
-  w.OUTP = round_up(n_out, 32);
+  w.OUTP = round_up(n_out, p_uses_dma(w.cfg) ? p_stage_cols(dtype) : 32);
   w.cfmt = align256((size_t)w.ntb * w.INP * w.OUTP * elt_size(dtype));
-  w.total = w.cfmt;
+  w.gpad = p_uses_dma(w.cfg) && p_needs_gpad(n_out, dtype) ? align256((size_t)batch * w.OUTP * elt_size(dtype)) : 0;
+  w.total = w.cfmt + w.gpad;
   return w;
 }
 struct WsG {
@@ -260,7 +270,8 @@ void launch_features_t(const KBasis& kb, int64_t batch, int64_t n_in, int64_t br
 template <typename T, bool FOLDED>
 int launch_features(const KBasis& kb, int64_t batch, int64_t n_in, int64_t brows, int64_t icols, const void* x,
                     void* out, long sb, long sj, long si, bool b_fastest, hipStream_t s) {
-  const int nb = nt_bucket(FOLDED ? (kb.kind == KF_KIND_CHEB ? kb.n_t : kb.K) : kb.n_t);
+  // folded Chebyshev features need max(n_t, K) slots (n_t < K for the (1 - z^2) reduced fold)
+  const int nb = nt_bucket(FOLDED ? (kb.kind == KF_KIND_CHEB ? (kb.n_t > kb.K ? kb.n_t : kb.K) : kb.K) : kb.n_t);
   switch (nb) {
     case 4: launch_features_t<T, 4, FOLDED>(kb, batch, n_in, brows, icols, x, out, sb, sj, si, b_fastest, s); break;
     case 8: launch_features_t<T, 8, FOLDED>(kb, batch, n_in, brows, icols, x, out, sb, sj, si, b_fastest, s); break;
@@ -308,9 +319,9 @@ template <bool HAS_W>
 int launch_f_rega(const WsF& L, int64_t batch, int64_t n_out, int n_t, const float* zc, const float* wc, const void* cfm,
               void* y, hipStream_t s) {
   const int n_m = (int)(L.BP / RA_BM), n_n = (int)(L.OUTP / RA_BN);
-  // 4 stage buffers of 2 features, z (and w) of two chunks
-  const size_t lds = (size_t)4 * 2 * RA_BN * 32 + (size_t)(HAS_W ? 4 : 2) * RA_BM * 64;
-  auto kern = L.n_tp == 9 ? f_rega_kernel<HAS_W, 9, RA_TM, RA_TN> : f_rega_kernel<HAS_W, 0, RA_TM, RA_TN>;
+  // RA_NBUF stage buffers of 2 features, z (and w) of two chunks
+  const size_t lds = (size_t)RA_NBUF * 2 * RA_BN * 32 + (size_t)(HAS_W ? 4 : 2) * RA_BM * 64;
+  auto kern = L.n_tp == 9 ? f_rega_kernel<HAS_W, 9, RA_TM, RA_TN, RA_NBUF> : f_rega_kernel<HAS_W, 0, RA_TM, RA_TN, RA_NBUF>;
   if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return fail(KF_ELAUNCH, "F: cannot reserve %zu bytes of LDS", lds);
   hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(256), lds, s, (int)batch, (int)n_out, (int)L.OUTP, (int)L.BP,
@@ -333,11 +344,13 @@ int run_F(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
           const void* w, const void* c, void* y, void* ws, hipStream_t s) {
   const bool has_w = w != nullptr;
   const bool cheb = kb.kind == KF_KIND_CHEB;
-  WsF L = ws_f(b, dtype, batch, n_in, n_out, has_w);
+  // Chebyshev features carry a weight when w is given or the map has the (1 - z^2) factor
+  const bool weighted = has_w || (cheb && kb.input_map == KF_MAP_TANH_SQ);
+  WsF L = ws_f(b, dtype, batch, n_in, n_out, weighted);
   char* base = (char*)ws;
   void* cfm = base;
   float* z = (float*)(base + L.cfm);
-  float* wz = has_w && cheb ? (float*)(base + L.cfm + L.z) : nullptr;
+  float* wz = weighted && cheb ? (float*)(base + L.cfm + L.z) : nullptr;
   void* phi = base + L.cfm + L.z + L.wz;
   if (L.cfg == F_REGA) {
     int rc = launch_permute<T>(kb, n_out, n_in, L.OUTP, L.INP, L.n_tp, c, cfm, kPermC16, s);
@@ -349,7 +362,7 @@ int run_F(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
                        (int)L.BP, (int)L.INP, kb.input_map, (const T*)x, (const T*)w, z, wz);
     rc = check_launch("zmapc");
     if (rc) return rc;
-    if (has_w) return launch_f_rega<true>(L, batch, n_out, kb.n_t, z, wz, cfm, y, s);
+    if (weighted) return launch_f_rega<true>(L, batch, n_out, kb.n_t, z, wz, cfm, y, s);
     return launch_f_rega<false>(L, batch, n_out, kb.n_t, z, nullptr, cfm, y, s);
   }
   int rc = launch_permute<T>(kb, n_out, n_in, L.OUTP, L.INP, L.n_tp, c, cfm, kPermFM, s);
@@ -362,7 +375,7 @@ int run_F(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
                        (int)L.INP, kb.input_map, (const T*)x, (const T*)w, z, wz);
     rc = check_launch("zmap");
     if (rc) return rc;
-    if (has_w) return launch_f_cfg<T, true, true>(L, batch, n_out, kb.n_t, z, wz, cfm, nullptr, y, s);
+    if (weighted) return launch_f_cfg<T, true, true>(L, batch, n_out, kb.n_t, z, wz, cfm, nullptr, y, s);
     return launch_f_cfg<T, true, false>(L, batch, n_out, kb.n_t, z, nullptr, cfm, nullptr, y, s);
   }
   // precomputed features phi_fm[b][j][i] (BP, n_t, INP)
@@ -382,13 +395,13 @@ int run_F(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
   return launch_f_cfg<T, false, false>(L, batch, n_out, kb.n_t, nullptr, nullptr, cfm, phi, y, s);
 }
 
-template <typename T, int WMW, int WJW, int TM, int FW>
-int launch_p_t(const WsP& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out,
-               const void* x, const void* g, const void* cfmt, void* p, float* h) {
+template <typename T, int WMW, int WJW, int TM, int FW, int KIND>
+int launch_p_kind(const WsP& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out,
+                  const void* x, const void* g, const void* cfmt, void* p, float* h) {
   constexpr int BM = WMW * TM * 32, NMAX = WJW * FW * 32, RS = 64 + 16;
   const size_t lds_ops = (size_t)2 * (BM + NMAX) * RS, lds_red = (size_t)WJW * BM * 33 * 4;
   const size_t lds = lds_ops > lds_red ? lds_ops : lds_red;
-  auto kern = p_kernel<T, WMW, WJW, TM, FW>;
+  auto kern = p_kernel<T, WMW, WJW, TM, FW, KIND>;
   if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return fail(KF_ELAUNCH, "P: cannot reserve %zu bytes of LDS", lds);
   const int n_m = (int)((batch + BM - 1) / BM), n_n = (int)(L.INP / 32);
@@ -397,17 +410,77 @@ int launch_p_t(const WsP& L, hipStream_t s, const KBasis& kb, int64_t batch, int
   return check_launch("P");
 }
 
+template <typename T, int WMW, int WJW, int TM, int FW>
+int launch_p_t(const WsP& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out,
+               const void* x, const void* g, const void* cfmt, void* p, float* h) {
+  switch (kb.kind) {
+    case KF_KIND_CHEB:
+      return launch_p_kind<T, WMW, WJW, TM, FW, KF_KIND_CHEB>(L, s, kb, batch, n_in, n_out, x, g, cfmt, p, h);
+    case KF_KIND_BSPLINE:
+      return launch_p_kind<T, WMW, WJW, TM, FW, KF_KIND_BSPLINE>(L, s, kb, batch, n_in, n_out, x, g, cfmt, p, h);
+    default:
+      return launch_p_kind<T, WMW, WJW, TM, FW, KF_KIND_RATIONAL>(L, s, kb, batch, n_in, n_out, x, g, cfmt, p, h);
+  }
+}
+
+template <typename T, int FW, int KIND>
+int launch_p_dma_kind(const WsP& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, const void* x,
+                      const void* g, int gstride, const void* cfmt, void* p, float* h) {
+  constexpr int TM = 4, BM = 2 * TM * 32;
+  const size_t lds_ops = (size_t)2 * (BM + 2 * FW * 32) * 128, lds_epi = (size_t)3 * BM * 33 * 4;
+  const size_t lds = lds_ops > lds_epi ? lds_ops : lds_epi;
+  auto kern = p_dma_kernel<T, TM, FW, KIND>;
+  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+    return fail(KF_ELAUNCH, "P: cannot reserve %zu bytes of LDS", lds);
+  const int n_m = (int)((batch + BM - 1) / BM), n_n = (int)(L.INP / 32);
+  hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(256), lds, s, kb, (int)batch, (int)n_in, (int)L.INP, (int)L.OUTP,
+                     (const T*)x, (const T*)g, gstride, (const T*)cfmt, (T*)p, h);
+  return check_launch("P");
+}
+
+template <typename T, int FW>
+int launch_p_dma(const WsP& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, const void* x,
+                 const void* g, int gstride, const void* cfmt, void* p, float* h) {
+  switch (kb.kind) {
+    case KF_KIND_CHEB:
+      return launch_p_dma_kind<T, FW, KF_KIND_CHEB>(L, s, kb, batch, n_in, x, g, gstride, cfmt, p, h);
+    case KF_KIND_BSPLINE:
+      return launch_p_dma_kind<T, FW, KF_KIND_BSPLINE>(L, s, kb, batch, n_in, x, g, gstride, cfmt, p, h);
+    default:
+      return launch_p_dma_kind<T, FW, KF_KIND_RATIONAL>(L, s, kb, batch, n_in, x, g, gstride, cfmt, p, h);
+  }
+}
+
 template <typename T>
 int run_P(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
           const void* g, const void* c, void* p, float* h, void* ws, hipStream_t s) {
-  WsP L = ws_p(b, dtype, n_in, n_out);
+  WsP L = ws_p(b, dtype, batch, n_in, n_out);
   void* cfmt = ws;
   int rc = launch_permute<T>(kb, n_out, n_in, L.OUTP, L.INP, L.ntb, c, cfmt, kPermFMT, s);
   if (rc) return rc;
+  if (p_uses_dma(L.cfg)) {
+    const void* ga = g;
+    int gstride = (int)n_out;
+    if (p_needs_gpad(n_out, dtype) || (reinterpret_cast<uintptr_t>(g) & 15) != 0) {
+      if (!L.gpad) return fail(KF_EINVAL, "P: g must be 16-byte aligned");
+      void* gp = (char*)ws + L.cfmt;
+      long n = (long)batch * L.OUTP;
+      long blocks = (n + kThreads - 1) / kThreads;
+      if (blocks > 65535 * 4) blocks = 65535 * 4;
+      hipLaunchKernelGGL(pad_cols_kernel<T>, dim3((unsigned)blocks), dim3(kThreads), 0, s, (int)batch, (int)n_out,
+                         (int)L.OUTP, (const T*)g, (T*)gp);
+      rc = check_launch("pad_cols");
+      if (rc) return rc;
+      ga = gp;
+      gstride = (int)L.OUTP;
+    }
+    switch (L.cfg) {
+      case 0: return launch_p_dma<T, 2>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p, h);
+      case 1: return launch_p_dma<T, 3>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p, h);
+      default: return launch_p_dma<T, 4>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p, h);
+    }
+  }
   switch (L.cfg) {
-    case 0: return launch_p_t<T, 4, 2, 2, 2>(L, s, kb, batch, n_in, n_out, x, g, cfmt, p, h);
-    case 1: return launch_p_t<T, 4, 2, 2, 3>(L, s, kb, batch, n_in, n_out, x, g, cfmt, p, h);
-    case 2: return launch_p_t<T, 4, 2, 2, 4>(L, s, kb, batch, n_in, n_out, x, g, cfmt, p, h);
     case 3: return launch_p_t<T, 4, 2, 2, 5>(L, s, kb, batch, n_in, n_out, x, g, cfmt, p, h);
     case 4: return launch_p_t<T, 4, 2, 1, 6>(L, s, kb, batch, n_in, n_out, x, g, cfmt, p, h);
     case 5: return launch_p_t<T, 4, 2, 1, 8>(L, s, kb, batch, n_in, n_out, x, g, cfmt, p, h);
@@ -463,11 +536,12 @@ template <typename T>
 int run_G(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
           const void* g, const void* w, void* dc, void* ws, hipStream_t s) {
   const bool cheb = kb.kind == KF_KIND_CHEB;
-  WsG L = ws_g(b, dtype, batch, n_in, n_out, w != nullptr);
+  const bool weighted = w != nullptr || (cheb && kb.input_map == KF_MAP_TANH_SQ);
+  WsG L = ws_g(b, dtype, batch, n_in, n_out, weighted);
   char* base = (char*)ws;
   void* gt = base;
   float* zt = cheb ? (float*)(base + L.gt) : nullptr;
-  float* wt = cheb && w ? (float*)(base + L.gt + L.zt) : nullptr;
+  float* wt = cheb && weighted ? (float*)(base + L.gt + L.zt) : nullptr;
   dim3 tg((unsigned)((L.OUTP + 63) / 64), (unsigned)((L.BP + 63) / 64));
   hipLaunchKernelGGL(transpose_kernel<T>, tg, dim3(kThreads), 0, s, (int)batch, (int)n_out, (int)L.BP, (int)L.OUTP,
                      (const T*)g, (T*)gt);
@@ -524,7 +598,7 @@ size_t kf_workspace_bytes(int op, const kf_basis* b, int dtype, int64_t batch, i
   if (validate_common(b, dtype, batch, n_in, n_out)) return 0;
   switch (op) {
     case KF_OP_F: return ws_f(b, dtype, batch, n_in, n_out, true).total;
-    case KF_OP_P: return ws_p(b, dtype, n_in, n_out).total;
+    case KF_OP_P: return ws_p(b, dtype, batch, n_in, n_out).total;
     case KF_OP_G: return ws_g(b, dtype, batch, n_in, n_out, true).total;
     default: return 0;
   }
@@ -579,7 +653,7 @@ int kf_P(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
   }
   if (!x || !g || !c || !p) return fail(KF_EINVAL, "kf_P: NULL array");
   if (h && b->kind != KF_KIND_RATIONAL) return fail(KF_EINVAL, "kf_P: h output is for the rational kind");
-  size_t need = ws_p(b, dtype, n_in, n_out).total;
+  size_t need = ws_p(b, dtype, batch, n_in, n_out).total;
   if (!workspace || workspace_bytes < need)
     return fail(KF_EWORKSPACE, "kf_P: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
   KBasis kb = to_kbasis(b);

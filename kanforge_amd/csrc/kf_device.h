@@ -97,7 +97,11 @@ __device__ inline float silu_derivative(float x, int m) {
 // every feature by w.
 
 __device__ __forceinline__ float cheb_map(float x, int input_map) {
-  return input_map == KF_MAP_TANH ? fast_tanh(x) : x;
+  return input_map != KF_MAP_IDENTITY ? fast_tanh(x) : x;
+}
+// Weight of the kernel features of one element: w, times (1 - z^2) for KF_MAP_TANH_SQ.
+__device__ __forceinline__ float cheb_weight(float z, float w, int input_map) {
+  return input_map == KF_MAP_TANH_SQ ? w * fmaf(-z, z, 1.f) : w;
 }
 
 template <int NT>
@@ -261,7 +265,8 @@ template <int KM, int NT>
 __device__ inline void basis_features(float x, float w, int i, const KBasis& b, float* phi) {
   if (b.kind == KF_KIND_CHEB) {
     float T[NT];
-    cheb_features<NT>(cheb_map(x, b.input_map), w, b.n_t, T);
+    const float z = cheb_map(x, b.input_map);
+    cheb_features<NT>(z, cheb_weight(z, w, b.input_map), b.n_t, T);
     cheb_folded<KM, NT>(b, T, phi);
   } else if (b.kind == KF_KIND_BSPLINE) {
     bspline_dispatch<KM>(x, w, i, b, phi);
@@ -277,8 +282,26 @@ __device__ inline void basis_features(float x, float w, int i, const KBasis& b, 
 template <int NT>
 __device__ inline void kernel_features(float x, float w, int i, const KBasis& b, float* f) {
   if (b.kind == KF_KIND_CHEB) {
-    cheb_features<NT>(cheb_map(x, b.input_map), w, b.n_t, f);
+    const float z = cheb_map(x, b.input_map);
+    cheb_features<NT>(z, cheb_weight(z, w, b.input_map), b.n_t, f);
   } else if (b.kind == KF_KIND_BSPLINE) {
+    bspline_dispatch<NT>(x, w, i, b, f);
+  } else {
+#pragma unroll
+    for (int s = 0; s < NT; ++s) f[s] = 0.f;
+    f[0] = w * rational_feature(x, i, b, b.order);
+  }
+}
+
+// kernel_features with the basis kind fixed at compile time: a kernel that
+// evaluates features next to live accumulators only carries the code (and
+// the registers) of its own kind.
+template <int KIND, int NT>
+__device__ __forceinline__ void kind_features(float x, float w, int i, const KBasis& b, float* f) {
+  if constexpr (KIND == KF_KIND_CHEB) {
+    const float z = cheb_map(x, b.input_map);
+    cheb_features<NT>(z, cheb_weight(z, w, b.input_map), b.n_t, f);
+  } else if constexpr (KIND == KF_KIND_BSPLINE) {
     bspline_dispatch<NT>(x, w, i, b, f);
   } else {
 #pragma unroll

@@ -130,8 +130,9 @@ __global__ __launch_bounds__(kThreads) void features_kernel(KBasis bs, int B, in
 }
 
 // ---------------------------------------------------------------------------
-// Input map prepass: z[b][i] = g(x[b][i]) (tanh or identity) and, when w is
-// given, wz[b][i] = w[b][i], both float32, zero-padded to (BP, INP). The
+// Input map prepass: z[b][i] = g(x[b][i]) (tanh or identity) and, when wz is
+// given, the feature weight wz[b][i] = w[b][i] (1 where w is NULL), times
+// (1 - z^2) for KF_MAP_TANH_SQ, both float32, zero-padded to (BP, INP). The
 // contraction kernels read z instead of re-evaluating tanh for every output
 // tile that shares the row.
 template <typename T>
@@ -143,14 +144,16 @@ __global__ __launch_bounds__(kThreads) void zmap_kernel(int B, int IN, int BP, i
     const int i = (int)(e % INP), b = (int)(e / INP);
     const bool ok = b < B && i < IN;
     const size_t off = (size_t)b * IN + i;
-    z[e] = ok ? cheb_map(to_f32(x[off]), input_map) : 0.f;
-    if (wz) wz[e] = ok ? to_f32(w[off]) : 0.f;
+    const float zz = ok ? cheb_map(to_f32(x[off]), input_map) : 0.f;
+    z[e] = zz;
+    if (wz) wz[e] = ok ? cheb_weight(zz, w ? to_f32(w[off]) : 1.f, input_map) : 0.f;
   }
 }
 
 // Chunked variant for the register-A F kernel: zc[c][b][e] = g(x[b][16c+e])
-// (and wc likewise), float32, zero-padded to (INP/16, BP, 16), so the 16
-// inputs of one row in one chunk are 64 contiguous bytes.
+// (and the feature weight wc likewise), float32, zero-padded to
+// (INP/16, BP, 16), so the 16 inputs of one row in one chunk are 64
+// contiguous bytes.
 template <typename T>
 __global__ __launch_bounds__(kThreads) void zmapc_kernel(int B, int IN, int BP, int INP, int input_map,
                                                          const T* __restrict__ x, const T* __restrict__ w,
@@ -161,8 +164,9 @@ __global__ __launch_bounds__(kThreads) void zmapc_kernel(int B, int IN, int BP, 
     const int i = c * 16 + il;
     const bool ok = b < B && i < IN;
     const size_t off = (size_t)b * IN + i;
-    zc[e] = ok ? cheb_map(to_f32(x[off]), input_map) : 0.f;
-    if (wc) wc[e] = ok ? to_f32(w[off]) : 0.f;
+    const float zz = ok ? cheb_map(to_f32(x[off]), input_map) : 0.f;
+    zc[e] = zz;
+    if (wc) wc[e] = ok ? cheb_weight(zz, w ? to_f32(w[off]) : 1.f, input_map) : 0.f;
   }
 }
 
@@ -391,8 +395,9 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void f_kernel(int B, int OUT
 }
 
 // ---------------------------------------------------------------------------
-// z^T[i][b] = g(x[b][i]) (float32, zero-padded to (INP, BP)) and, when w is
-// given, w^T the same way: the G kernel generates features with the batch
+// z^T[i][b] = g(x[b][i]) (float32, zero-padded to (INP, BP)) and, when wt is
+// given, the feature weight (as in zmap_kernel) transposed the same way: the
+// G kernel generates features with the batch
 // (its reduction dimension) contiguous. 64x64 tiles through LDS.
 template <typename T>
 __global__ __launch_bounds__(kThreads) void zmapT_kernel(int B, int IN, int BP, int INP, int input_map,
@@ -404,8 +409,9 @@ __global__ __launch_bounds__(kThreads) void zmapT_kernel(int B, int IN, int BP, 
   for (int r = ty; r < 64; r += 4) {
     const int b = b0 + r, i = i0 + tx;
     const bool ok = b < B && i < IN;
-    tz[r][tx] = ok ? cheb_map(to_f32(x[(size_t)b * IN + i]), input_map) : 0.f;
-    if (wt) tw[r][tx] = ok ? to_f32(w[(size_t)b * IN + i]) : 0.f;
+    const float zz = ok ? cheb_map(to_f32(x[(size_t)b * IN + i]), input_map) : 0.f;
+    tz[r][tx] = zz;
+    if (wt) tw[r][tx] = ok ? cheb_weight(zz, w ? to_f32(w[(size_t)b * IN + i]) : 1.f, input_map) : 0.f;
   }
   __syncthreads();
   for (int r = ty; r < 64; r += 4) {
@@ -426,7 +432,7 @@ __global__ __launch_bounds__(kThreads) void zmapT_kernel(int B, int IN, int BP, 
 
 // P: p[b,i] = sum_j f_j(x[b,i]) * sum_o g[b,o] CfmT[j][i][o]
 // M = batch rows (A = g, natural layout), reduction over outputs o.
-template <typename T, int WAVES_M, int WAVES_J, int TM, int FW>
+template <typename T, int WAVES_M, int WAVES_J, int TM, int FW, int KIND>
 __global__ __launch_bounds__(WAVES_M* WAVES_J * 64) void p_kernel(KBasis bs, int B, int IN, int OUT, int INP, int OUTP,
                                                                  const T* __restrict__ x, const T* __restrict__ g,
                                                                  const T* __restrict__ cfmt, T* __restrict__ p,
@@ -537,7 +543,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_J * 64) void p_kernel(KBasis bs, int
       float sum = 0.f;
       if (b < B && i < IN) {
         float f[NTB];
-        kernel_features<NTB>(to_f32(x[(size_t)b * IN + i]), 1.f, i, bs, f);
+        kind_features<KIND, NTB>(to_f32(x[(size_t)b * IN + i]), 1.f, i, bs, f);
 #pragma unroll
         for (int q = 0; q < FW; ++q) sum = fmaf(acc[a][q][r], f[wj * FW + q], sum);
         if (hout && wj == 0) hout[(size_t)b * IN + i] = acc[a][0][r];
@@ -795,12 +801,11 @@ __device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)"
 //            c + 2 in the second half of its last one (unrolled).
 // The MFMAs are never under a condition, which keeps the accumulators in
 // AGPRs across the loops.
-template <bool HAS_W, int NT, int TM, int TN>
+template <bool HAS_W, int NT, int TM, int TN, int NBUF>
 __global__ __launch_bounds__(256) void f_rega_kernel(int B, int OUT, int OUTP, int BP, int n_chunks, int n_tp,
                                                      const float* __restrict__ zc, const float* __restrict__ wc,
                                                      const bf16* __restrict__ cfm, bf16* __restrict__ y) {
   constexpr int WM = TM * 32, BM = 4 * WM, BN = TN * 32;
-  constexpr int NBUF = 4;
   constexpr int FB = BN * 32;      // one feature of a stage (dense 32-byte rows)
   constexpr int SB = 2 * FB;       // one stage
   constexpr int BPW = SB / 4096;   // 1 KB copy blocks per wave and stage
@@ -808,7 +813,7 @@ __global__ __launch_bounds__(256) void f_rega_kernel(int B, int OUT, int OUTP, i
   constexpr int ZPW = ZB / 4096;   // 1 KB copy blocks per wave for z (and again for w)
   constexpr int ZPW_ALL = HAS_W ? 2 * ZPW : ZPW;
   static_assert(BPW * 4096 == SB && ZPW * 4096 == ZB, "copy blocks divide over the waves");
-  static_assert(NBUF == 4, "copy waits below count up to two newer stages");
+  static_assert(NBUF >= 3 && NBUF <= 6, "copy waits below count up to NBUF - 2 newer groups");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];  // [NBUF][SB], z [2][ZB], w [2][ZB]
   unsigned char* zs = smem + NBUF * SB;
   unsigned char* ws = zs + 2 * ZB;
@@ -837,7 +842,9 @@ __global__ __launch_bounds__(256) void f_rega_kernel(int B, int OUT, int OUTP, i
   // stage g(x) - 1: NT == 0: g = x P (chunk x is seeded in the second half of stage x P - 1);
   // NT odd: odd x is seeded in the first half of stage g = pair NT + NT / 2, even x in the second
   // half of the pair's last stage, g = pair NT + NT. Groups are copied in stage order, so a small
-  // state machine tracks the next carrier; zbits keeps the carrier flags of the last two groups.
+  // state machine tracks the next carrier; zbits keeps the carrier flags of the last NBUF - 2
+  // groups. A chunk's z copy is issued NBUF - 1 stages before its carrier stage, after the seed
+  // of chunk x - 2 (same buffer) as long as chunks span at least NBUF / 2 stages.
   int zg_next = NT == 0 ? P : NT / 2, zx_next = 1, zbits = 0;
   // coefficient copy block k of this wave: stage block blk = wave * BPW + k, feature
   // blk / (BN / 32), rows 32 (blk % (BN / 32)) .. +32; lane l fills 16-byte chunk l of the
@@ -875,18 +882,18 @@ __global__ __launch_bounds__(256) void f_rega_kernel(int B, int OUT, int OUTP, i
       zg_next += NT == 0 ? P : (zx_next & 1) ? NT / 2 + 1 : NT / 2;
       ++zx_next;
     }
-    zbits = ((zbits << 1) | flag) & 3;
+    zbits = ((zbits << 1) | flag) & ((1 << (NBUF - 2)) - 1);
   };
-  // wait until this wave's copies of the group before the last two issued are in LDS (those two
-  // may remain in flight)
+  // wait until this wave's copies of the group before the last NBUF - 2 issued are in LDS
+  // (those may remain in flight; at most two of them carry z)
   auto wait_group = [&]() {
-    const int nz = (zbits & 1) + (zbits >> 1);
+    const int nz = __builtin_popcount(zbits);
     if (nz == 0)
-      vmem_wait<2 * BPW>();
+      vmem_wait<(NBUF - 2) * BPW>();
     else if (nz == 1)
-      vmem_wait<2 * BPW + ZPW_ALL>();
+      vmem_wait<(NBUF - 2) * BPW + ZPW_ALL>();
     else
-      vmem_wait<2 * BPW + 2 * ZPW_ALL>();
+      vmem_wait<(NBUF - 2) * BPW + 2 * ZPW_ALL>();
   };
   // fragment read offset of this lane inside a feature: row l32 (+ 32 t), half h swizzled
   const int frag_off = (2 * l32 + (h ^ ((l32 >> 3) & 1))) * 16;
@@ -1025,6 +1032,190 @@ __global__ __launch_bounds__(256) void f_rega_kernel(int B, int OUT, int OUTP, i
         if (b < B && o < OUT) y[(size_t)b * OUT + o] = from_f32<bf16>(acc[a][t][r]);
       }
     }
+}
+
+// ---------------------------------------------------------------------------
+// P as a plain GEMM plus a feature epilogue, operands by direct copies:
+//   H_j[b, i] = sum_o g[b, o] CfmT[j][i][o],  p[b, i] = sum_j f_j(x[b, i]) H_j[b, i]
+// 4 waves: 2 along the batch (TM 32-row blocks each) x 2 feature groups (FW
+// features of the workgroup's 32 inputs each), float32 accumulators in AGPRs
+// (TM x FW <= 16 tiles of 32 x 32). A stage is 128 bytes of the output
+// dimension o (one whole cache line) of BM rows of g and 2 FW x 32 rows of
+// CfmT, copied global -> LDS into one of two buffers; rows are dense 128
+// bytes with their 16-byte chunks XOR-swizzled by bits 1..3 of the row, which
+// makes the fragment reads conflict-free. A stage is 4 k-steps of 32 bytes;
+// the fragments of the next k-step are read while the MFMAs of the current
+// one run (two register sets). After the reads of the last k-step the waves
+// meet at one barrier, which both publishes the next stage and frees the
+// buffer just read, into which the copies of stage s + 2 then go (about three
+// k-steps ahead of their use). The epilogue forms each lane's feature sums
+// and adds the two feature groups through LDS.
+// Rows of g past the batch are clamped to the last row (their results are
+// dropped); g must have whole stages of columns (the caller pads it
+// otherwise) and CfmT is zero past n_out and n_t.
+template <typename T, int TM, int FW, int KIND>
+__global__ __launch_bounds__(256) void p_dma_kernel(KBasis bs, int B, int IN, int INP, int OUTP,
+                                                    const T* __restrict__ x, const T* __restrict__ g, int gstride,
+                                                    const T* __restrict__ cfmt, T* __restrict__ p,
+                                                    float* __restrict__ hout) {
+  constexpr int WM = TM * 32, BM = 2 * WM, BR = 2 * FW * 32;  // g rows, CfmT rows of a stage
+  constexpr int RB = 128, KS = RB / 32;                        // bytes of o per row and stage, k-steps
+  constexpr int EPS = RB / (int)sizeof(T);                     // outputs o per stage
+  constexpr int EPC = 16 / (int)sizeof(T);                     // per 16-byte chunk
+  constexpr int SA = BM * RB, SS = (BM + BR) * RB;             // bytes of a stage
+  constexpr int NBLK = SS / 1024, BPW = NBLK / 4;
+  constexpr int NTB = 2 * FW;
+  static_assert(BPW * 4 == NBLK && BM % 8 == 0, "copy blocks divide over the waves");
+  static_assert(2 * SS <= 160 * 1024 && 3 * BM * 33 * 4 <= 160 * 1024, "two stages and the epilogue fit in LDS");
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];  // [2][SS], later x and the sums
+
+  const int n_m = (B + BM - 1) / BM, n_n = INP / 32;
+  int tm_, tn_;
+  xcd_tile_grouped(blockIdx.x, n_m, n_n, 8, tm_, tn_);
+  const int b0 = tm_ * BM, i0 = tn_ * 32;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wj = wave & 1;
+  const int h = lane >> 5, l32 = lane & 31;
+  const int S = OUTP / EPS;
+
+  f32x16 acc[TM][FW];
+#pragma unroll
+  for (int a = 0; a < TM; ++a)
+#pragma unroll
+    for (int f = 0; f < FW; ++f)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[a][f][r] = 0.f;
+
+  // copy block k of this wave = stage block q = wave * BPW + k (8 rows of 128 bytes): lane l
+  // fills LDS chunk l % 8 of row l / 8, i.e. global chunk (l % 8) ^ ((row >> 1) & 7)
+  const T* src[BPW];
+#pragma unroll
+  for (int k = 0; k < BPW; ++k) {
+    const int row = (wave * BPW + k) * 8 + (lane >> 3);  // row of the stage (g rows first)
+    const int c = (lane & 7) ^ ((row >> 1) & 7);
+    if (row < BM) {
+      const int b = b0 + row < B ? b0 + row : B - 1;
+      src[k] = g + (size_t)b * gstride + c * EPC;
+    } else {
+      const int rr = row - BM, j = rr / 32, il = rr % 32;
+      src[k] = cfmt + ((size_t)j * INP + i0 + il) * OUTP + c * EPC;
+    }
+  }
+  auto copy_stage = [&](int st) {
+    unsigned char* dst = smem + (st & 1) * SS + wave * BPW * 1024;
+#pragma unroll
+    for (int k = 0; k < BPW; ++k) lds_dma16(src[k] + (size_t)st * EPS, dst + k * 1024);
+  };
+  // fragment reads: row l32 of a 32-row block, 16-byte chunk (2 ks + h) swizzled
+  const int sw = (l32 >> 1) & 7;
+  const int a_off = (wm * WM + l32) * RB, b_off = SA + (wj * FW * 32 + l32) * RB;
+  u32x4 fa[2][TM], fb[2][FW];
+  auto read_frags = [&](int st, int ks, int set) {
+    const unsigned char* base = smem + (st & 1) * SS;
+    const int co = 16 * ((2 * ks + h) ^ sw);
+#pragma unroll
+    for (int a = 0; a < TM; ++a) fa[set][a] = lds_read16(base + a_off + a * 32 * RB + co);
+#pragma unroll
+    for (int f = 0; f < FW; ++f) fb[set][f] = lds_read16(base + b_off + f * 32 * RB + co);
+  };
+  // the MFMAs of one k-step: the first one before the next fragment reads are issued (its
+  // operands are ready), the rest after them
+  auto mma_first = [&](int set) {
+    mma32<T>(acc[0][0], fa[set][0], fb[set][0]);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto mma_rest = [&](int set) {
+#pragma unroll
+    for (int f = 0; f < FW; ++f)
+#pragma unroll
+      for (int a = 0; a < TM; ++a)
+        if (a + f > 0) mma32<T>(acc[a][f], fa[set][a], fb[set][f]);
+    __builtin_amdgcn_sched_group_barrier(0x100, TM + FW, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, TM * FW - 1, 0);
+  };
+
+  copy_stage(0);
+  if (S > 1) {
+    copy_stage(1);
+    vmem_wait<BPW>();  // stage 0's copies are done (stage 1's may be in flight)
+  } else {
+    vmem_wait<0>();
+  }
+  __builtin_amdgcn_s_barrier();
+  read_frags(0, 0, 0);
+  for (int s = 0; s < S; ++s) {
+#pragma unroll
+    for (int ks = 0; ks < KS - 1; ++ks) {
+      mma_first(ks & 1);
+      read_frags(s, ks + 1, (ks + 1) & 1);
+      mma_rest(ks & 1);
+    }
+    // every wave's reads of stage s have returned and its copies of stage s + 1 are done
+    vmem_wait<0>();
+    lds_wait();
+    __builtin_amdgcn_s_barrier();
+    mma_first((KS - 1) & 1);
+    if (s + 2 < S) copy_stage(s + 2);
+    if (s + 1 < S) read_frags(s + 1, 0, 0);
+    mma_rest((KS - 1) & 1);
+  }
+  vmem_wait<0>();
+  __syncthreads();  // every wave is done with the stage buffers: reuse them for x and the group sums
+
+  // x of the tile into LDS, all loads in flight at once (coalesced along the inputs)
+  float* red = reinterpret_cast<float*>(smem);  // [2][BM][33]: the two feature groups' sums
+  float* xs = red + 2 * BM * 33;                // [BM][33]
+  {
+    constexpr int PER = BM * 32 / 256;
+    float xv[PER];
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int e = tid + 256 * u, row = e / 32, ii = i0 + e % 32;
+      const int b = b0 + row;
+      xv[u] = b < B && ii < IN ? to_f32(x[(size_t)b * IN + ii]) : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int e = tid + 256 * u;
+      xs[(e / 32) * 33 + e % 32] = xv[u];
+    }
+  }
+  __syncthreads();
+  const int i = i0 + l32;
+#pragma unroll
+  for (int a = 0; a < TM; ++a)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = wm * WM + a * 32 + acc_row(r, lane);
+      const int b = b0 + row;
+      float sum = 0.f;
+      if (b < B && i < IN) {
+        float f[NTB];
+        kind_features<KIND, NTB>(xs[row * 33 + l32], 1.f, i, bs, f);
+#pragma unroll
+        for (int q = 0; q < FW; ++q) sum = fmaf(acc[a][q][r], f[wj * FW + q], sum);
+        if (hout && wj == 0) hout[(size_t)b * IN + i] = acc[a][0][r];
+      }
+      red[(wj * BM + row) * 33 + l32] = sum;
+    }
+  __syncthreads();
+  for (int e = tid; e < BM * 32; e += 256) {
+    const int row = e / 32, il = e % 32;
+    const int b = b0 + row, ii = i0 + il;
+    if (b < B && ii < IN) p[(size_t)b * IN + ii] = from_f32<T>(red[row * 33 + il] + red[(BM + row) * 33 + il]);
+  }
+}
+
+// Copy g (B, OUT) into a zero-padded (B, OUTP) buffer: the P kernel copies whole stages.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void pad_cols_kernel(int B, int OUT, int OUTP, const T* __restrict__ g,
+                                                            T* __restrict__ gp) {
+  const long n = (long)B * OUTP;
+  for (long e = blockIdx.x * (long)kThreads + threadIdx.x; e < n; e += (long)gridDim.x * kThreads) {
+    const int o = (int)(e % OUTP), b = (int)(e / OUTP);
+    gp[e] = o < OUT ? g[(size_t)b * OUT + o] : from_f32<T>(0.f);
+  }
 }
 
 // ---------------------------------------------------------------------------

@@ -63,6 +63,19 @@ class KernelPlan:
             return None
         return _fold(self.consts, self.fold_key, m)
 
+    def device_fold(self, m: int) -> tuple[np.ndarray, bool]:
+        """The fold the HIP kernels evaluate for order m, and whether their features carry the
+        factor (1 - z^2).
+
+        For a tanh map and m >= 1 every row of R_m is (1 - z^2) times a polynomial of degree
+        deg + m - 2 (d/dx = (1 - z^2) d/dz), so the kernels use R_m with that factor divided out
+        and weight each element's features by (1 - z^2): two Chebyshev features fewer per edge,
+        the same values."""
+        d, input_map = self.consts
+        if input_map != "tanh" or m == 0:
+            return self.fold(m), False
+        return _reduced_fold(self.consts, self.fold_key, m), True
+
 
 @lru_cache(maxsize=None)
 def _fold(consts, fold_key, m):
@@ -82,6 +95,25 @@ def _fold(consts, fold_key, m):
     r = np.stack(cols)
     r.setflags(write=False)
     return r
+
+
+@lru_cache(maxsize=None)
+def _reduced_fold(consts, fold_key, m):
+    d, _ = consts
+    r = _fold(consts, fold_key, m)
+    n_t = max(1, d + m - 1)
+    rows = []
+    for row in r:
+        q, rem = C.chebdiv(row, ONE_MINUS_Z2)
+        scale = max(1.0, float(np.abs(row).max()))
+        if np.abs(rem).max() > 1e-9 * scale:  # exact division for tanh maps and m >= 1
+            raise AssertionError("fold row is not divisible by (1 - z^2)")
+        out = np.zeros(n_t)
+        out[: min(len(q), n_t)] = q[:n_t]
+        rows.append(out)
+    out = np.stack(rows)
+    out.setflags(write=False)
+    return out
 
 
 def plan_for(basis) -> KernelPlan | None:

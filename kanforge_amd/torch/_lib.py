@@ -18,7 +18,7 @@ LIB_PATH = Path(__file__).resolve().parent.parent / "libkfhip.so"
 KF_OK = 0
 KF_F32, KF_BF16 = 0, 1
 KF_KIND_CHEB, KF_KIND_BSPLINE, KF_KIND_RATIONAL = 0, 1, 2
-KF_MAP_IDENTITY, KF_MAP_TANH = 0, 1
+KF_MAP_IDENTITY, KF_MAP_TANH, KF_MAP_TANH_SQ = 0, 1, 2
 KF_OP_F, KF_OP_G, KF_OP_P = 0, 1, 2
 KF_MAX_K, KF_MAX_NT = 16, 24
 

@@ -104,11 +104,15 @@ def _desc(plan: KernelPlan, m: int, st: BasisState | None):
     keep = []
     if plan.kind == "cheb":
         degree, input_map = plan.consts
-        r = np.ascontiguousarray(plan.fold(m), dtype=np.float32)
+        fold, factored = plan.device_fold(m)
+        r = np.ascontiguousarray(fold, dtype=np.float32)
         keep.append(r)
         d.order = m
         d.n_t = r.shape[1]
-        d.input_map = _lib.KF_MAP_TANH if input_map == "tanh" else _lib.KF_MAP_IDENTITY
+        if input_map == "tanh":
+            d.input_map = _lib.KF_MAP_TANH_SQ if factored else _lib.KF_MAP_TANH
+        else:
+            d.input_map = _lib.KF_MAP_IDENTITY
         d.fold = r.ctypes.data_as(ctypes.c_void_p)
     elif plan.kind == "bspline":
         g, k = plan.consts
