@@ -134,8 +134,9 @@ int pick_f_cfg(int64_t batch, int64_t n_out) {
 
 struct WsF {
   int cfg, n_tp;
+  bool skip0;  // register-A kernel without feature 0 (T_0 = 1 folded into a per-output sum)
   int64_t INP, OUTP, BP;
-  size_t cfm, z, wz, phi, total;
+  size_t cfm, z, wz, phi, part0, ysum, total;
 };
 // bf16 Chebyshev plans run the register-A F kernel: wave tile (32 RA_TM) x
 // (32 RA_TN), four waves along the batch.
@@ -157,7 +158,9 @@ WsF ws_f(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
   const int es = elt_size(dtype);
   const bool cheb = b->kind == KF_KIND_CHEB;
   const int fps = dtype == KF_BF16 ? 2 : 1;
-  w.n_tp = rega && f_rega_unpadded(b->n_t, n_in) ? b->n_t : (b->n_t + fps - 1) / fps * fps;
+  w.skip0 = rega && !has_w && b->n_t >= 2;
+  const int n_run = b->n_t - (w.skip0 ? 1 : 0);  // features the contraction runs over
+  w.n_tp = rega && f_rega_unpadded(n_run, n_in) ? n_run : (n_run + fps - 1) / fps * fps;
   // the register-A kernel needs chunks of at least RA_NBUF / 2 (and 2) stages
   const int min_tp = RA_NBUF < 4 ? 4 : RA_NBUF;
   if (rega && w.n_tp < min_tp) w.n_tp = min_tp;
@@ -165,7 +168,9 @@ WsF ws_f(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
   w.z = cheb ? align256((size_t)w.BP * w.INP * sizeof(float)) : 0;
   w.wz = cheb && has_w ? align256((size_t)w.BP * w.INP * sizeof(float)) : 0;
   w.phi = cheb ? 0 : align256((size_t)w.BP * w.n_tp * w.INP * es);
-  w.total = w.cfm + w.z + w.wz + w.phi;
+  w.part0 = w.skip0 ? align256((size_t)(w.INP / 16) * w.OUTP * sizeof(float)) : 0;
+  w.ysum = w.skip0 ? align256((size_t)w.OUTP * sizeof(float)) : 0;
+  w.total = w.cfm + w.z + w.wz + w.phi + w.part0 + w.ysum;
   return w;
 }
 // P / G configurations. The MFMA waves split the features in two groups of
@@ -207,12 +212,14 @@ WsP ws_p(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
 }
 struct WsG {
   int cfg;
+  bool skip0;  // Chebyshev, unweighted: T_0 = 1 taken out of the contraction (column sums of g)
   int64_t OUTP, BP, INP;
-  size_t gt, zt, wt, total;
+  size_t gt, zt, wt, part, colsum, total;
 };
 WsG ws_g(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, bool has_w) {
   WsG w;
-  w.cfg = fw_index(b->n_t);
+  w.skip0 = b->kind == KF_KIND_CHEB && !has_w && b->n_t >= 2;
+  w.cfg = fw_index(b->n_t - (w.skip0 ? 1 : 0));
   const int fw = FW_LIST[w.cfg];
   const int bm = 2 * g_tm(fw) * 32;
   const int eps = g_rb(fw) / elt_size(dtype);
@@ -223,7 +230,9 @@ WsG ws_g(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
   w.gt = align256((size_t)w.OUTP * w.BP * elt_size(dtype));
   w.zt = cheb ? align256((size_t)w.INP * w.BP * sizeof(float)) : 0;
   w.wt = cheb && has_w ? align256((size_t)w.INP * w.BP * sizeof(float)) : 0;
-  w.total = w.gt + w.zt + w.wt;
+  w.part = w.skip0 ? align256((size_t)((w.BP + 63) / 64) * w.OUTP * sizeof(float)) : 0;
+  w.colsum = w.skip0 ? align256((size_t)w.OUTP * sizeof(float)) : 0;
+  w.total = w.gt + w.zt + w.wt + w.part + w.colsum;
   return w;
 }
 
@@ -245,14 +254,14 @@ int zero_fill(void* p, long n, hipStream_t s) {
 // n_feat >= n_t features (zeros past n_t)
 template <typename T>
 int launch_permute(const KBasis& kb, int64_t n_out, int64_t n_in, int64_t OUTP, int64_t INP, int n_feat, const void* c,
-                   void* out, int fmt, hipStream_t s) {
+                   void* out, int fmt, hipStream_t s, int j_first = 0, float* part0 = nullptr) {
   dim3 grid((unsigned)((OUTP + 31) / 32), (unsigned)((INP + 15) / 16));
-  size_t lds = (size_t)n_feat * 16 * 33 * sizeof(float);
+  size_t lds = (size_t)(n_feat + j_first) * 16 * 33 * sizeof(float);
   auto kern = fmt == kPermFMT ? permute_coef_kernel<T, kPermFMT>
               : fmt == kPermC16 ? permute_coef_kernel<T, kPermC16>
                                 : permute_coef_kernel<T, kPermFM>;
   hipLaunchKernelGGL(kern, grid, dim3(kThreads), lds, s, kb, (int)n_out, (int)n_in, (int)OUTP, (int)INP, n_feat,
-                     (const T*)c, (T*)out);
+                     j_first, (const T*)c, (T*)out, part0);
   return check_launch("permute_coef");
 }
 
@@ -315,17 +324,19 @@ int launch_f_t(const WsF& L, int64_t batch, int64_t n_out, int n_t, const float*
   return check_launch("F");
 }
 
-template <bool HAS_W>
-int launch_f_rega(const WsF& L, int64_t batch, int64_t n_out, int n_t, const float* zc, const float* wc, const void* cfm,
-              void* y, hipStream_t s) {
+template <bool HAS_W, bool SKIP0>
+int launch_f_rega(const WsF& L, int64_t batch, int64_t n_out, const float* zc, const float* wc, const void* cfm,
+                  const float* ysum, void* y, hipStream_t s) {
   const int n_m = (int)(L.BP / RA_BM), n_n = (int)(L.OUTP / RA_BN);
   // RA_NBUF stage buffers of 2 features, z (and w) of two chunks
   const size_t lds = (size_t)RA_NBUF * 2 * RA_BN * 32 + (size_t)(HAS_W ? 4 : 2) * RA_BM * 64;
-  auto kern = L.n_tp == 9 ? f_rega_kernel<HAS_W, 9, RA_TM, RA_TN, RA_NBUF> : f_rega_kernel<HAS_W, 0, RA_TM, RA_TN, RA_NBUF>;
+  auto kern = L.n_tp == 9   ? f_rega_kernel<HAS_W, 9, RA_TM, RA_TN, RA_NBUF, SKIP0>
+              : L.n_tp == 8 ? f_rega_kernel<HAS_W, 8, RA_TM, RA_TN, RA_NBUF, SKIP0>
+                            : f_rega_kernel<HAS_W, 0, RA_TM, RA_TN, RA_NBUF, SKIP0>;
   if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return fail(KF_ELAUNCH, "F: cannot reserve %zu bytes of LDS", lds);
   hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(256), lds, s, (int)batch, (int)n_out, (int)L.OUTP, (int)L.BP,
-                     (int)(L.INP / 16), L.n_tp, zc, wc, (const bf16*)cfm, (bf16*)y);
+                     (int)(L.INP / 16), L.n_tp, zc, wc, (const bf16*)cfm, ysum, (bf16*)y);
   return check_launch("F");
 }
 
@@ -353,8 +364,16 @@ int run_F(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
   float* wz = weighted && cheb ? (float*)(base + L.cfm + L.z) : nullptr;
   void* phi = base + L.cfm + L.z + L.wz;
   if (L.cfg == F_REGA) {
-    int rc = launch_permute<T>(kb, n_out, n_in, L.OUTP, L.INP, L.n_tp, c, cfm, kPermC16, s);
+    float* part0 = L.skip0 ? (float*)(base + L.cfm + L.z + L.wz + L.phi) : nullptr;
+    float* ysum = L.skip0 ? (float*)(base + L.cfm + L.z + L.wz + L.phi + L.part0) : nullptr;
+    int rc = launch_permute<T>(kb, n_out, n_in, L.OUTP, L.INP, L.n_tp, c, cfm, kPermC16, s, L.skip0 ? 1 : 0, part0);
     if (rc) return rc;
+    if (L.skip0) {
+      hipLaunchKernelGGL(sum_parts_kernel, dim3((unsigned)((L.OUTP + 31) / 32)), dim3(kThreads), 0, s,
+                         (int)(L.INP / 16), (int)L.OUTP, part0, ysum);
+      rc = check_launch("sum_parts");
+      if (rc) return rc;
+    }
     long n = (long)L.BP * L.INP;
     long blocks = (n + kThreads - 1) / kThreads;
     if (blocks > 65535 * 4) blocks = 65535 * 4;
@@ -362,8 +381,9 @@ int run_F(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
                        (int)L.BP, (int)L.INP, kb.input_map, (const T*)x, (const T*)w, z, wz);
     rc = check_launch("zmapc");
     if (rc) return rc;
-    if (weighted) return launch_f_rega<true>(L, batch, n_out, kb.n_t, z, wz, cfm, y, s);
-    return launch_f_rega<false>(L, batch, n_out, kb.n_t, z, nullptr, cfm, y, s);
+    if (weighted) return launch_f_rega<true, false>(L, batch, n_out, z, wz, cfm, nullptr, y, s);
+    if (L.skip0) return launch_f_rega<false, true>(L, batch, n_out, z, nullptr, cfm, ysum, y, s);
+    return launch_f_rega<false, false>(L, batch, n_out, z, nullptr, cfm, nullptr, y, s);
   }
   int rc = launch_permute<T>(kb, n_out, n_in, L.OUTP, L.INP, L.n_tp, c, cfm, kPermFM, s);
   if (rc) return rc;
@@ -519,16 +539,16 @@ int launch_g_cfg(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, i
 
 template <typename T, int TM, int FW, int RB>
 int launch_g_ws(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out,
-                const float* zt, const float* wt, const void* gt, void* dc) {
+                const float* zt, const float* wt, const void* gt, const float* colsum, void* dc) {
   constexpr int BM = 2 * TM * 32, NMAX = 2 * FW * 32, RS = RB + 16;
   const size_t lds_ops = (size_t)2 * (BM + NMAX) * RS, lds_red = (size_t)kb.n_t * (BM / 2) * 33 * 4;
   const size_t lds = lds_ops > lds_red ? lds_ops : lds_red;
-  auto kern = g_ws_kernel<T, TM, FW, RB>;
+  auto kern = L.skip0 ? g_ws_kernel<T, TM, FW, RB, true> : g_ws_kernel<T, TM, FW, RB, false>;
   if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return fail(KF_ELAUNCH, "G: cannot reserve %zu bytes of LDS", lds);
   const int n_m = (int)(L.OUTP / BM), n_n = (int)((n_in + 31) / 32);
   hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(512), lds, s, kb, (int)batch, (int)n_in, (int)n_out, (int)L.BP,
-                     (int)L.OUTP, zt, wt, (const T*)gt, (T*)dc);
+                     (int)L.OUTP, zt, wt, (const T*)gt, colsum, (T*)dc);
   return check_launch("G");
 }
 
@@ -542,11 +562,19 @@ int run_G(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
   void* gt = base;
   float* zt = cheb ? (float*)(base + L.gt) : nullptr;
   float* wt = cheb && weighted ? (float*)(base + L.gt + L.zt) : nullptr;
+  float* part = L.skip0 ? (float*)(base + L.gt + L.zt + L.wt) : nullptr;
+  float* colsum = L.skip0 ? (float*)(base + L.gt + L.zt + L.wt + L.part) : nullptr;
   dim3 tg((unsigned)((L.OUTP + 63) / 64), (unsigned)((L.BP + 63) / 64));
   hipLaunchKernelGGL(transpose_kernel<T>, tg, dim3(kThreads), 0, s, (int)batch, (int)n_out, (int)L.BP, (int)L.OUTP,
-                     (const T*)g, (T*)gt);
+                     (const T*)g, (T*)gt, part);
   int rc = check_launch("transpose");
   if (rc) return rc;
+  if (L.skip0) {
+    hipLaunchKernelGGL(sum_parts_kernel, dim3((unsigned)((L.OUTP + 31) / 32)), dim3(kThreads), 0, s,
+                       (int)((L.BP + 63) / 64), (int)L.OUTP, part, colsum);
+    rc = check_launch("sum_parts");
+    if (rc) return rc;
+  }
   if (cheb) {
     dim3 zg((unsigned)((L.INP + 63) / 64), (unsigned)((L.BP + 63) / 64));
     hipLaunchKernelGGL(zmapT_kernel<T>, zg, dim3(kThreads), 0, s, (int)batch, (int)n_in, (int)L.BP, (int)L.INP,
@@ -554,13 +582,13 @@ int run_G(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
     rc = check_launch("zmapT");
     if (rc) return rc;
     switch (L.cfg) {
-      case 0: return launch_g_ws<T, 2, 2, 128>(L, s, kb, batch, n_in, n_out, zt, wt, gt, dc);
-      case 1: return launch_g_ws<T, 2, 3, 128>(L, s, kb, batch, n_in, n_out, zt, wt, gt, dc);
-      case 2: return launch_g_ws<T, 2, 4, 128>(L, s, kb, batch, n_in, n_out, zt, wt, gt, dc);
-      case 3: return launch_g_ws<T, 2, 5, 128>(L, s, kb, batch, n_in, n_out, zt, wt, gt, dc);
-      case 4: return launch_g_ws<T, 2, 6, 128>(L, s, kb, batch, n_in, n_out, zt, wt, gt, dc);
-      case 5: return launch_g_ws<T, 1, 8, 64>(L, s, kb, batch, n_in, n_out, zt, wt, gt, dc);
-      default: return launch_g_ws<T, 1, 12, 64>(L, s, kb, batch, n_in, n_out, zt, wt, gt, dc);
+      case 0: return launch_g_ws<T, 2, 2, 128>(L, s, kb, batch, n_in, n_out, zt, wt, gt, colsum, dc);
+      case 1: return launch_g_ws<T, 2, 3, 128>(L, s, kb, batch, n_in, n_out, zt, wt, gt, colsum, dc);
+      case 2: return launch_g_ws<T, 2, 4, 128>(L, s, kb, batch, n_in, n_out, zt, wt, gt, colsum, dc);
+      case 3: return launch_g_ws<T, 2, 5, 128>(L, s, kb, batch, n_in, n_out, zt, wt, gt, colsum, dc);
+      case 4: return launch_g_ws<T, 2, 6, 128>(L, s, kb, batch, n_in, n_out, zt, wt, gt, colsum, dc);
+      case 5: return launch_g_ws<T, 1, 8, 64>(L, s, kb, batch, n_in, n_out, zt, wt, gt, colsum, dc);
+      default: return launch_g_ws<T, 1, 12, 64>(L, s, kb, batch, n_in, n_out, zt, wt, gt, colsum, dc);
     }
   }
   return launch_g_cfg<T, false>(L, s, kb, batch, n_in, n_out, x, w, nullptr, nullptr, gt, dc);
@@ -597,9 +625,15 @@ const char* kf_version(void) { return "kfhip 0.1.0 gfx950"; }
 size_t kf_workspace_bytes(int op, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out) {
   if (validate_common(b, dtype, batch, n_in, n_out)) return 0;
   switch (op) {
-    case KF_OP_F: return ws_f(b, dtype, batch, n_in, n_out, true).total;
+    case KF_OP_F: {  // weighted or not (the unweighted register-A layout differs)
+      const size_t a = ws_f(b, dtype, batch, n_in, n_out, true).total, u = ws_f(b, dtype, batch, n_in, n_out, false).total;
+      return a > u ? a : u;
+    }
     case KF_OP_P: return ws_p(b, dtype, batch, n_in, n_out).total;
-    case KF_OP_G: return ws_g(b, dtype, batch, n_in, n_out, true).total;
+    case KF_OP_G: {  // weighted or not (unweighted Chebyshev plans take T_0 out)
+      const size_t a = ws_g(b, dtype, batch, n_in, n_out, true).total, u = ws_g(b, dtype, batch, n_in, n_out, false).total;
+      return a > u ? a : u;
+    }
     default: return 0;
   }
 }

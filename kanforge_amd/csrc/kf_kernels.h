@@ -30,10 +30,10 @@ constexpr int kThreads = 256;
 enum { kPermFM = 0, kPermFMT = 1, kPermC16 = 2 };
 template <typename T, int FMT>
 __global__ __launch_bounds__(kThreads) void permute_coef_kernel(KBasis bs, int OUT, int IN, int OUTP, int INP,
-                                                                int n_feat, const T* __restrict__ c,
-                                                                T* __restrict__ out) {
-  extern __shared__ float tile[];  // [n_feat][16][33]
-  const int K = bs.K, n_t = n_feat;  // features past bs.n_t get zero fold columns
+                                                                int n_feat, int j_first, const T* __restrict__ c,
+                                                                T* __restrict__ out, float* __restrict__ part0) {
+  extern __shared__ float tile[];  // [n_feat + j_first][16][33]
+  const int K = bs.K, n_all = n_feat + j_first;  // features past bs.n_t get zero fold columns
   const int o0 = blockIdx.x * 32, i0 = blockIdx.y * 16;
   const int t = threadIdx.x;
   // phase 1: thread (ol = t / 16 .. +16, il = t % 16) covers 2 o rows
@@ -44,45 +44,77 @@ __global__ __launch_bounds__(kThreads) void permute_coef_kernel(KBasis bs, int O
 #pragma unroll
     for (int k = 0; k < KF_MAX_K; ++k)
       cv[k] = (k < K && o < OUT && i < IN) ? to_f32(c[((size_t)o * IN + i) * K + k]) : 0.f;
-    for (int j = 0; j < n_t; ++j) {
+    for (int j = 0; j < n_all; ++j) {
       float acc = 0.f;
+      if (j < bs.n_t) {
 #pragma unroll
-      for (int k = 0; k < KF_MAX_K; ++k)
-        if (k < K) acc = fmaf(cv[k], bs.fold[k * KF_MAX_NT + j], acc);
+        for (int k = 0; k < KF_MAX_K; ++k)
+          if (k < K) acc = fmaf(cv[k], bs.fold[k * KF_MAX_NT + j], acc);
+      }
       tile[(j * 16 + il) * 33 + ol] = acc;
     }
   }
   __syncthreads();
+  // feature 0 left out (j_first = 1): its partial sums over the block's 16 inputs per output
+  if (j_first && t < 32 && o0 + t < OUTP) {
+    float sum = 0.f;
+    for (int il = 0; il < 16; ++il) sum += tile[il * 33 + t];
+    part0[(size_t)blockIdx.y * OUTP + o0 + t] = sum;
+  }
+  const float* tf = tile + j_first * 16 * 33;
+  const int n_t = n_feat;
   if (FMT == kPermC16) {
     // out[i/16][j][o][i%16]: 16 inputs of one output row contiguous, then o
     T* blk = out + (size_t)blockIdx.y * n_t * OUTP * 16;
     for (int e = t; e < n_t * 32 * 16; e += kThreads) {
       const int il = e % 16, ol = (e / 16) % 32, j = e / (16 * 32);
       const int o = o0 + ol;
-      if (o < OUTP) blk[((size_t)j * OUTP + o) * 16 + il] = from_f32<T>(tile[(j * 16 + il) * 33 + ol]);
+      if (o < OUTP) blk[((size_t)j * OUTP + o) * 16 + il] = from_f32<T>(tf[(j * 16 + il) * 33 + ol]);
     }
   } else if (FMT == kPermFM) {
     // out[j][o][i]: consecutive threads along i
     for (int e = t; e < n_t * 32 * 16; e += kThreads) {
       const int il = e % 16, ol = (e / 16) % 32, j = e / (16 * 32);
       const int o = o0 + ol, i = i0 + il;
-      if (o < OUTP && i < INP) out[((size_t)j * OUTP + o) * INP + i] = from_f32<T>(tile[(j * 16 + il) * 33 + ol]);
+      if (o < OUTP && i < INP) out[((size_t)j * OUTP + o) * INP + i] = from_f32<T>(tf[(j * 16 + il) * 33 + ol]);
     }
   } else {
     // out[j][i][o]: consecutive threads along o
     for (int e = t; e < n_t * 32 * 16; e += kThreads) {
       const int ol = e % 32, il = (e / 32) % 16, j = e / (16 * 32);
       const int o = o0 + ol, i = i0 + il;
-      if (o < OUTP && i < INP) out[((size_t)j * INP + i) * OUTP + o] = from_f32<T>(tile[(j * 16 + il) * 33 + ol]);
+      if (o < OUTP && i < INP) out[((size_t)j * INP + i) * OUTP + o] = from_f32<T>(tf[(j * 16 + il) * 33 + ol]);
     }
   }
 }
 
+// sums[o] = sum over p < n_parts of part[p][o]: the per-output constant of a
+// left-out feature 0 (fixed summation order). Block: 32 outputs x 8 groups
+// of parts, reduced through LDS.
+__global__ __launch_bounds__(kThreads) void sum_parts_kernel(int n_parts, int n, const float* __restrict__ part,
+                                                             float* __restrict__ sums) {
+  __shared__ float red[8][33];
+  const int ol = threadIdx.x % 32, pg = threadIdx.x / 32;
+  const int o = blockIdx.x * 32 + ol;
+  float s = 0.f;
+  if (o < n)
+    for (int q = pg; q < n_parts; q += 8) s += part[(size_t)q * n + o];
+  red[pg][ol] = s;
+  __syncthreads();
+  if (pg == 0 && o < n) {
+    float tot = 0.f;
+#pragma unroll
+    for (int g = 0; g < 8; ++g) tot += red[g][ol];
+    sums[o] = tot;
+  }
+}
+
 // ---------------------------------------------------------------------------
-// g (B, OUT) -> gT (OUTP, BP), zero padded. 64x64 tiles through LDS.
+// g (B, OUT) -> gT (OUTP, BP), zero padded. 64x64 tiles through LDS. With
+// part given, also the column sums of each 64-row block: part[blk][o].
 template <typename T>
 __global__ __launch_bounds__(kThreads) void transpose_kernel(int B, int OUT, int BP, int OUTP, const T* __restrict__ g,
-                                                             T* __restrict__ gt) {
+                                                             T* __restrict__ gt, float* __restrict__ part) {
   __shared__ float tile[64][65];
   const int b0 = blockIdx.y * 64, o0 = blockIdx.x * 64;
   const int tx = threadIdx.x % 64, ty = threadIdx.x / 64;
@@ -91,6 +123,11 @@ __global__ __launch_bounds__(kThreads) void transpose_kernel(int B, int OUT, int
     tile[r][tx] = (b < B && o < OUT) ? to_f32(g[(size_t)b * OUT + o]) : 0.f;
   }
   __syncthreads();
+  if (part && ty == 0 && o0 + tx < OUTP) {
+    float sum = 0.f;
+    for (int r = 0; r < 64; ++r) sum += tile[r][tx];
+    part[(size_t)blockIdx.y * OUTP + o0 + tx] = sum;
+  }
   for (int r = ty; r < 64; r += 4) {
     const int o = o0 + r, b = b0 + tx;
     if (o < OUTP && b < BP) gt[(size_t)o * BP + b] = from_f32<T>(tile[tx][r]);
@@ -793,18 +830,23 @@ __device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)"
 // (a, b) (first slot: a <- 2 z b - a, second: b <- 2 z a - b); a chunk starts
 // by seeding (T_-2, T_-1) = (w T_2(z), w T_1(z)) into (a, b) at a first slot,
 // (b, a) at a second one, so its first step yields w T_0.
-//   NT == 0: n_tp = n_t rounded up to even (zero coefficients past n_t), so
-//            chunks are whole stages; chunk c + 1 is seeded in the second half
+//   SKIP0  : unweighted features: T_0 = 1 contributes the per-output
+//            constant ysum[o] = sum_i Cfm_0[o][i], added in the epilogue, and
+//            the chunks run over T_1 .. (seeded with (T_-1, T_0));
+//   NT even: n_tp = the features run, rounded up to even (zero coefficients
+//            past them), so chunks are whole stages (NT = n_tp, unrolled, or
+//            0 for a runtime count); chunk c + 1 is seeded in the second half
 //            of the last stage of chunk c;
 //   NT odd : n_tp = NT, no padding; a chunk pair is NT stages, chunk c + 1 is
 //            seeded in the first half of its middle stage (q = NT / 2), chunk
 //            c + 2 in the second half of its last one (unrolled).
 // The MFMAs are never under a condition, which keeps the accumulators in
 // AGPRs across the loops.
-template <bool HAS_W, int NT, int TM, int TN, int NBUF>
+template <bool HAS_W, int NT, int TM, int TN, int NBUF, bool SKIP0>
 __global__ __launch_bounds__(256) void f_rega_kernel(int B, int OUT, int OUTP, int BP, int n_chunks, int n_tp,
                                                      const float* __restrict__ zc, const float* __restrict__ wc,
-                                                     const bf16* __restrict__ cfm, bf16* __restrict__ y) {
+                                                     const bf16* __restrict__ cfm, const float* __restrict__ ysum,
+                                                     bf16* __restrict__ y) {
   constexpr int WM = TM * 32, BM = 4 * WM, BN = TN * 32;
   constexpr int FB = BN * 32;      // one feature of a stage (dense 32-byte rows)
   constexpr int SB = 2 * FB;       // one stage
@@ -827,7 +869,8 @@ __global__ __launch_bounds__(256) void f_rega_kernel(int B, int OUT, int OUTP, i
   const int wm = wave;
   const int h = lane >> 5, l32 = lane & 31;
   const int S = n_chunks * n_tp / 2;                 // n_chunks is even
-  const int P = n_tp / 2;                            // stages per chunk (NT == 0), at least 2
+  constexpr bool ODD = NT % 2 == 1;
+  const int P = NT > 0 && !ODD ? NT / 2 : n_tp / 2;  // stages per chunk (NT even), at least 2
   const size_t stage_elems = (size_t)2 * OUTP * 16;  // stage s starts at cfm + s * stage_elems
 
   f32x16 acc[TM][TN];
@@ -839,13 +882,13 @@ __global__ __launch_bounds__(256) void f_rega_kernel(int B, int OUT, int OUTP, i
       for (int r = 0; r < 16; ++r) acc[a][c][r] = 0.f;
 
   // z of chunk x travels with the copy group of stage g(x), published at the mid-stage barrier of
-  // stage g(x) - 1: NT == 0: g = x P (chunk x is seeded in the second half of stage x P - 1);
+  // stage g(x) - 1: NT even: g = x P (chunk x is seeded in the second half of stage x P - 1);
   // NT odd: odd x is seeded in the first half of stage g = pair NT + NT / 2, even x in the second
   // half of the pair's last stage, g = pair NT + NT. Groups are copied in stage order, so a small
   // state machine tracks the next carrier; zbits keeps the carrier flags of the last NBUF - 2
   // groups. A chunk's z copy is issued NBUF - 1 stages before its carrier stage, after the seed
   // of chunk x - 2 (same buffer) as long as chunks span at least NBUF / 2 stages.
-  int zg_next = NT == 0 ? P : NT / 2, zx_next = 1, zbits = 0;
+  int zg_next = !ODD ? P : NT / 2, zx_next = 1, zbits = 0;
   // coefficient copy block k of this wave: stage block blk = wave * BPW + k, feature
   // blk / (BN / 32), rows 32 (blk % (BN / 32)) .. +32; lane l fills 16-byte chunk l of the
   // block = row o = base + l / 2, half (l & 1) ^ bit 3 of o
@@ -879,7 +922,7 @@ __global__ __launch_bounds__(256) void f_rega_kernel(int B, int OUT, int OUTP, i
         copy_z(zx_next);
         flag = 1;
       }
-      zg_next += NT == 0 ? P : (zx_next & 1) ? NT / 2 + 1 : NT / 2;
+      zg_next += !ODD ? P : (zx_next & 1) ? NT / 2 + 1 : NT / 2;
       ++zx_next;
     }
     zbits = ((zbits << 1) | flag) & ((1 << (NBUF - 2)) - 1);
@@ -917,7 +960,9 @@ __global__ __launch_bounds__(256) void f_rega_kernel(int B, int OUT, int OUTP, i
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float zz = e < 4 ? z0[e] : z1[e - 4], w_ = e < 4 ? w0[e] : w1[e - 4];
-        const float t2 = w_ * fmaf(2.f * zz, zz, -1.f), t1 = w_ * zz;
+        // the two terms before the chunk's first feature: (T_-2, T_-1) = (T_2, T_1), or
+        // (T_-1, T_0) = (T_1, 1) when the chunks start at T_1
+        const float t2 = SKIP0 ? w_ * zz : w_ * fmaf(2.f * zz, zz, -1.f), t1 = SKIP0 ? w_ : w_ * zz;
         z2[a][e] = 2.f * zz;
         ga[a][e] = SECOND ? t1 : t2;
         gb[a][e] = SECOND ? t2 : t1;
@@ -1006,8 +1051,13 @@ __global__ __launch_bounds__(256) void f_rega_kernel(int B, int OUT, int OUTP, i
       for (int p = 0; p + 1 < P; ++p) stage(F_{}, F_{}, 0, 0);
       stage(F_{}, T_{}, 0, c + 1);  // chunk c + 1 starts at the next stage's first slot
     }
+  } else if constexpr (!ODD) {
+    for (int c = 0; c < n_chunks; ++c) {
+#pragma unroll
+      for (int p = 0; p + 1 < NT / 2; ++p) stage(F_{}, F_{}, 0, 0);
+      stage(F_{}, T_{}, 0, c + 1);
+    }
   } else {
-    static_assert(NT % 2 == 1, "unpadded variants are for odd feature counts");
     for (int c = 0; c < n_chunks; c += 2) {
 #pragma unroll
       for (int q = 0; q < NT; ++q) {
@@ -1026,10 +1076,11 @@ __global__ __launch_bounds__(256) void f_rega_kernel(int B, int OUT, int OUTP, i
 #pragma unroll
     for (int t = 0; t < TN; ++t) {
       const int o = o0 + t * 32 + l32;
+      const float add = SKIP0 && o < OUT ? ysum[o] : 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int b = b0 + wm * WM + a * 32 + acc_row(r, lane);
-        if (b < B && o < OUT) y[(size_t)b * OUT + o] = from_f32<bf16>(acc[a][t][r]);
+        if (b < B && o < OUT) y[(size_t)b * OUT + o] = from_f32<bf16>(acc[a][t][r] + add);
       }
     }
 }
@@ -1224,10 +1275,11 @@ __global__ __launch_bounds__(kThreads) void pad_cols_kernel(int B, int OUT, int 
 // generate the feature tile of the next stage into the other LDS buffer,
 // with their global loads issued one further stage ahead. One barrier per
 // stage for all 8 waves. Chebyshev plans only (features from z^T).
-template <typename T, int TM, int FW, int RB>
+template <typename T, int TM, int FW, int RB, bool SKIP0>
 __global__ __launch_bounds__(512) void g_ws_kernel(KBasis bs, int B, int IN, int OUT, int BP, int OUTP,
                                                    const float* __restrict__ zt, const float* __restrict__ wt,
-                                                   const T* __restrict__ gt, T* __restrict__ dc) {
+                                                   const T* __restrict__ gt, const float* __restrict__ colsum,
+                                                   T* __restrict__ dc) {
   constexpr int WAVES_M = 2, WAVES_J = 2;
   constexpr int BM = WAVES_M * TM * 32;
   constexpr int RS = RB + 16, FS = RB / 32;
@@ -1249,12 +1301,14 @@ __global__ __launch_bounds__(512) void g_ws_kernel(KBasis bs, int B, int IN, int
   const int o0 = tm_ * BM, i0 = tn_ * 32;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool consumer = wave < 4;
-  const int n_t = bs.n_t, K = bs.K;
+  const int n_t = bs.n_t - (SKIP0 ? 1 : 0), K = bs.K;  // features the contraction runs over
   const int S = BP / EPS;
 
   // epilogue helpers: raw feature sums go to LDS in halves of the M tile,
   // then all threads apply the fold dc[o][i][k] = sum_j fold[k][j] GT[o][i][j]
-  // and write k-fastest (coalesced).
+  // and write k-fastest (coalesced). SKIP0: feature 0 is T_0 = 1, so
+  // GT[o][i][0] = colsum[o] = sum_b g[b][o] for every input; the contraction
+  // runs over T_1, T_2, ...
   float* red = reinterpret_cast<float*>(smem);  // [n_t][BM/2][33]
   constexpr int HM = BM / 2;
   auto store_phase = [&](int half) {
@@ -1262,8 +1316,9 @@ __global__ __launch_bounds__(512) void g_ws_kernel(KBasis bs, int B, int IN, int
       const int k = e % K, il = (e / K) % 32, row = e / (K * 32);
       const int o = o0 + half * HM + row, i = i0 + il;
       if (o < OUT && i < IN) {
-        float sum = 0.f;
-        for (int j = 0; j < n_t; ++j) sum = fmaf(bs.fold[k * KF_MAX_NT + j], red[(j * HM + row) * 33 + il], sum);
+        float sum = SKIP0 ? bs.fold[k * KF_MAX_NT] * colsum[o] : 0.f;
+        for (int j = 0; j < n_t; ++j)
+          sum = fmaf(bs.fold[k * KF_MAX_NT + j + (SKIP0 ? 1 : 0)], red[(j * HM + row) * 33 + il], sum);
         dc[((size_t)o * IN + i) * K + k] = from_f32<T>(sum);
       }
     }
@@ -1375,8 +1430,8 @@ __global__ __launch_bounds__(512) void g_ws_kernel(KBasis bs, int B, int IN, int
         for (int u = 0; u < PL; ++u) {
           const float wv = wp ? fw[u] : (in_ok ? 1.f : 0.f);
           z2[u] = 2.f * fz[u];
-          tp[u] = wv;
-          tc[u] = wv * fz[u];
+          tp[u] = SKIP0 ? wv * fz[u] : wv;                       // first feature: T_1 or T_0
+          tc[u] = SKIP0 ? wv * fmaf(z2[u], fz[u], -1.f) : wv * fz[u];  // then T_2 or T_1
         }
         lds_write16(dst, pack16<T>(tp));
         lds_write16(dst + 32 * RS, pack16<T>(tc));

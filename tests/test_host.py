@@ -46,6 +46,22 @@ def test_plan_fold_matches_oracle(basis, name, kw, m):
     assert plan.n_features(m) == plan.fold(m).shape[1]
 
 
+@pytest.mark.parametrize("basis", [kf.Chebyshev(8), kf.Jacobi(6, 0.5, 0.5), kf.Chebyshev(0), kf.Gegenbauer(5, 0.75)])
+@pytest.mark.parametrize("m", [0, 1, 2, 3, 5])
+def test_device_fold_equals_reference_fold(basis, m):
+    """What the kernels evaluate: for tanh maps and m >= 1, R_m with (1 - z^2) divided out and the
+    features weighted by (1 - z^2) (two features fewer); it must reproduce R_m's polynomials."""
+    plan = plan_for(basis)
+    r, (rd, factored) = plan.fold(m), plan.device_fold(m)
+    assert factored == (m >= 1)
+    if factored:
+        assert rd.shape == (basis.size, max(1, basis.degree + m - 1))
+    z = np.linspace(-0.999, 0.999, 41)
+    want = np.polynomial.chebyshev.chebval(z, r.T)
+    got = np.polynomial.chebyshev.chebval(z, rd.T) * ((1 - z * z) if factored else 1.0)
+    np.testing.assert_allclose(got, want, atol=1e-9 * max(1.0, np.abs(want).max()))
+
+
 def test_plans_for_every_kind():
     assert plan_for(kf.BSpline(8, 3)).kind == "bspline" and plan_for(kf.BSpline(8, 3)).size == 11
     assert plan_for(kf.Rational(5, 4)).kind == "rational"
