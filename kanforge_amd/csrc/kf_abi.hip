@@ -213,6 +213,7 @@ WsP ws_p(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
 struct WsG {
   int cfg;
   bool skip0;  // Chebyshev, unweighted: T_0 = 1 taken out of the contraction (column sums of g)
+  bool g96;    // bf16 Chebyshev with at most 8 features run: g96_kernel (96 x 96 x 8 tiles)
   int64_t OUTP, BP, INP;
   size_t gt, zt, wt, part, colsum, total;
 };
@@ -220,12 +221,13 @@ WsG ws_g(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
   WsG w;
   w.skip0 = b->kind == KF_KIND_CHEB && !has_w && b->n_t >= 2;
   w.cfg = fw_index(b->n_t - (w.skip0 ? 1 : 0));
+  w.g96 = b->kind == KF_KIND_CHEB && dtype == KF_BF16 && b->n_t - (w.skip0 ? 1 : 0) <= 8;
   const int fw = FW_LIST[w.cfg];
-  const int bm = 2 * g_tm(fw) * 32;
-  const int eps = g_rb(fw) / elt_size(dtype);
+  const int bm = w.g96 ? 96 : 2 * g_tm(fw) * 32;
+  const int eps = w.g96 ? 32 : g_rb(fw) / elt_size(dtype);
   w.OUTP = round_up(n_out, bm);
   w.BP = round_up(batch, eps);
-  w.INP = round_up(n_in, 32);
+  w.INP = round_up(n_in, w.g96 ? 96 : 32);
   const bool cheb = b->kind == KF_KIND_CHEB;
   w.gt = align256((size_t)w.OUTP * w.BP * elt_size(dtype));
   w.zt = cheb ? align256((size_t)w.INP * w.BP * sizeof(float)) : 0;
@@ -552,6 +554,19 @@ int launch_g_ws(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, in
   return check_launch("G");
 }
 
+template <bool SKIP0>
+int launch_g96(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out,
+               const float* zt, const float* wt, const void* gt, const float* colsum, void* dc) {
+  const size_t lds = (size_t)2 * (96 * 64 + 8 * 96 * 64);
+  auto kern = g96_kernel<SKIP0>;
+  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+    return fail(KF_ELAUNCH, "G: cannot reserve %zu bytes of LDS", lds);
+  const int n_m = (int)(L.OUTP / 96), n_n = (int)(L.INP / 96);
+  hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(512), lds, s, kb, (int)batch, (int)n_in, (int)n_out, (int)L.BP,
+                     (int)L.OUTP, (int)L.INP, zt, wt, (const bf16*)gt, colsum, (bf16*)dc);
+  return check_launch("G");
+}
+
 template <typename T>
 int run_G(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
           const void* g, const void* w, void* dc, void* ws, hipStream_t s) {
@@ -581,6 +596,10 @@ int run_G(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
                        kb.input_map, (const T*)x, (const T*)w, zt, wt);
     rc = check_launch("zmapT");
     if (rc) return rc;
+    if (L.g96) {
+      if (L.skip0) return launch_g96<true>(L, s, kb, batch, n_in, n_out, zt, wt, gt, colsum, dc);
+      return launch_g96<false>(L, s, kb, batch, n_in, n_out, zt, wt, gt, colsum, dc);
+    }
     switch (L.cfg) {
       case 0: return launch_g_ws<T, 2, 2, 128>(L, s, kb, batch, n_in, n_out, zt, wt, gt, colsum, dc);
       case 1: return launch_g_ws<T, 2, 3, 128>(L, s, kb, batch, n_in, n_out, zt, wt, gt, colsum, dc);
