@@ -213,7 +213,7 @@ WsP ws_p(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
 struct WsG {
   int cfg;
   bool skip0;  // Chebyshev, unweighted: T_0 = 1 taken out of the contraction (column sums of g)
-  bool g96;    // bf16 Chebyshev with at most 8 features run: g96_kernel (96 x 96 x 8 tiles)
+  bool g96;    // bf16 Chebyshev with at most 8 features run: g96_kernel (192 x 48 x 8 tiles)
   int64_t OUTP, BP, INP;
   size_t gt, zt, wt, part, colsum, total;
 };
@@ -223,11 +223,11 @@ WsG ws_g(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
   w.cfg = fw_index(b->n_t - (w.skip0 ? 1 : 0));
   w.g96 = b->kind == KF_KIND_CHEB && dtype == KF_BF16 && b->n_t - (w.skip0 ? 1 : 0) <= 8;
   const int fw = FW_LIST[w.cfg];
-  const int bm = w.g96 ? 96 : 2 * g_tm(fw) * 32;
+  const int bm = w.g96 ? 192 : 2 * g_tm(fw) * 32;
   const int eps = w.g96 ? 32 : g_rb(fw) / elt_size(dtype);
   w.OUTP = round_up(n_out, bm);
   w.BP = round_up(batch, eps);
-  w.INP = round_up(n_in, w.g96 ? 96 : 32);
+  w.INP = round_up(n_in, w.g96 ? 48 : 32);
   const bool cheb = b->kind == KF_KIND_CHEB;
   w.gt = align256((size_t)w.OUTP * w.BP * elt_size(dtype));
   w.zt = cheb ? align256((size_t)w.INP * w.BP * sizeof(float)) : 0;
@@ -557,11 +557,12 @@ int launch_g_ws(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, in
 template <bool SKIP0>
 int launch_g96(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out,
                const float* zt, const float* wt, const void* gt, const float* colsum, void* dc) {
-  const size_t lds = (size_t)2 * (96 * 64 + 8 * 96 * 64);
+  const size_t lds_ops = (size_t)2 * (192 * 64 + 8 * 48 * 64), lds_red = (size_t)8 * 96 * 49 * 4;
+  const size_t lds = lds_ops > lds_red ? lds_ops : lds_red;
   auto kern = g96_kernel<SKIP0>;
   if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return fail(KF_ELAUNCH, "G: cannot reserve %zu bytes of LDS", lds);
-  const int n_m = (int)(L.OUTP / 96), n_n = (int)(L.INP / 96);
+  const int n_m = (int)(L.OUTP / 192), n_n = (int)(L.INP / 48);
   hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(512), lds, s, kb, (int)batch, (int)n_in, (int)n_out, (int)L.BP,
                      (int)L.OUTP, (int)L.INP, zt, wt, (const bf16*)gt, colsum, (bf16*)dc);
   return check_launch("G");

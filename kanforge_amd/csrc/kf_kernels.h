@@ -1271,28 +1271,30 @@ __global__ __launch_bounds__(kThreads) void pad_cols_kernel(int B, int OUT, int 
 
 // ---------------------------------------------------------------------------
 // G in one round of workgroups, for Chebyshev plans with at most 8 features
-// run (bf16): a workgroup owns 96 outputs x 96 inputs x 8 features, so the
+// run (bf16): a workgroup owns 192 outputs x 48 inputs x 8 features, so the
 // 3072 x 768 headline is exactly 256 workgroups.
 //   GT_f[o][i] = sum_b gT[o][b] w[b,i] T_{f + SKIP0}(z[b,i]),
 //   dc[o][i][k] = sum_f fold[k][f + SKIP0] GT_f[o][i] (+ fold[k][0] colsum[o])
-// 8 waves (2 per SIMD); wave w computes feature f = w for the 3 32-output
-// blocks x 3 32-input blocks of the tile (9 accumulator tiles). A stage is 32
-// batch rows: the gT tile (96 rows x 64 bytes) arrives by direct copies
-// (waves 6 and 7), the feature tile (8 x 96 rows x 64 bytes) is generated by
-// waves 0..5 (one input and 8 batch rows per thread, the recurrence over the
-// 8 features) from z^T (and w^T) loaded a stage ahead; both double-buffered,
+// GEMM columns n = f * 48 + i (12 fragments of 32). 8 waves (2 per SIMD):
+// wave (wm, wn) = (wave & 1, wave >> 1) computes output blocks 3 wm .. +2 x
+// column fragments 3 wn .. +2 (9 accumulator tiles). A stage is 32 batch
+// rows: the gT tile (192 rows x 64 bytes) arrives by direct copies (waves
+// 4..7), the feature tile (384 rows x 64 bytes) is generated by waves 0..2,
+// one input and 8 batch rows per thread with the recurrence over the 8
+// features, from z^T (and w^T) loaded a stage ahead; both double-buffered,
 // one barrier per stage. Rows are dense 64 bytes with their 16-byte chunks
 // XOR-swizzled by bits 2..3 of the row (conflict-free fragment reads).
-// Features past n_t - SKIP0 are computed and dropped. Epilogue: per 32-input
-// block, the 8 feature sums go to LDS and every thread applies the fold for
-// (o, i, k), k fastest.
+// Features past n_t - SKIP0 are computed and dropped. Epilogue, per half of
+// the outputs: the 8 feature sums go to LDS and every thread applies the fold
+// for (o, i, k), k fastest.
 template <bool SKIP0>
 __global__ __launch_bounds__(512) void g96_kernel(KBasis bs, int B, int IN, int OUT, int BP, int OUTP, int INP,
                                                   const float* __restrict__ zt, const float* __restrict__ wt,
                                                   const bf16* __restrict__ gt, const float* __restrict__ colsum,
                                                   bf16* __restrict__ dc) {
-  constexpr int TO = 96, TI = 96, NF = 8;
+  constexpr int TO = 192, TI = 48, NF = 8;
   constexpr int SA = TO * 64, SBF = NF * TI * 64, SS = SA + SBF;  // bytes of a stage
+  constexpr int RP = TI + 1;                                         // fold buffer row pitch
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];  // [2][SS], later the fold buffer
 
   const int n_m = OUTP / TO, n_n = INP / TI;
@@ -1301,6 +1303,7 @@ __global__ __launch_bounds__(512) void g96_kernel(KBasis bs, int B, int IN, int 
   const int o0 = tm_ * TO, i0 = tn_ * TI;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
   const int h = lane >> 5, l32 = lane & 31;
   const int S = BP / 32;
   const int n_run = bs.n_t - (SKIP0 ? 1 : 0), K = bs.K;
@@ -1313,28 +1316,28 @@ __global__ __launch_bounds__(512) void g96_kernel(KBasis bs, int B, int IN, int 
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[a][c][r] = 0.f;
 
-  // gT copies (waves 6, 7): block q = 3 (wave - 6) + k of the 6 per stage, 16 rows of 64 bytes;
+  // gT copies (waves 4..7): blocks 3 (wave - 4) .. +2 of the 12 per stage, 16 rows of 64 bytes;
   // lane l fills chunk l % 4 of row l / 4 = global chunk (l % 4) ^ ((row >> 2) & 3)
-  const bool copier = wave >= 6;
+  const bool copier = wave >= 4;
   const bf16* asrc[3];
 #pragma unroll
   for (int k = 0; k < 3; ++k) {
-    const int row = (3 * (copier ? wave - 6 : 0) + k) * 16 + (lane >> 2);
+    const int row = (3 * (copier ? wave - 4 : 0) + k) * 16 + (lane >> 2);
     const int c = (lane & 3) ^ ((row >> 2) & 3);
     asrc[k] = gt + (size_t)(o0 + row) * BP + c * 8;
   }
   auto copy_a = [&](int st) {
-    unsigned char* dst = smem + (st & 1) * SS + (3 * (wave - 6)) * 1024;
+    unsigned char* dst = smem + (st & 1) * SS + (3 * (wave - 4)) * 1024;
 #pragma unroll
     for (int k = 0; k < 3; ++k) lds_dma16(asrc[k] + (size_t)st * 32, dst + k * 1024);
   };
-  // feature generation (threads 0..383): input il = t % 96, batch rows 8 g .. 8 g + 7 of the stage
-  const bool gen = tid < 384;
-  const int gil = tid % 96, gg = tid / 96;
+  // feature generation (threads 0..191): input il = t % 48, batch rows 8 g .. 8 g + 7 of the stage
+  const bool gen = tid < 4 * TI;
+  const int gil = tid % TI, gg = tid / TI;
   const bool in_ok = i0 + gil < IN;
   const float* zp = zt + (size_t)(i0 + gil) * BP + gg * 8;
   const float* wp = wt ? wt + (size_t)(i0 + gil) * BP + gg * 8 : nullptr;
-  float zn[8], wn[8];
+  float zn[8], wn_[8];
   auto load_z = [&](int st) {
     if (gen) {
 #pragma unroll
@@ -1345,7 +1348,7 @@ __global__ __launch_bounds__(512) void g96_kernel(KBasis bs, int B, int IN, int 
         if (wp) {
           const f32x4 ww = *reinterpret_cast<const f32x4*>(wp + (size_t)st * 32 + 4 * q);
 #pragma unroll
-          for (int u = 0; u < 4; ++u) wn[4 * q + u] = ww[u];
+          for (int u = 0; u < 4; ++u) wn_[4 * q + u] = ww[u];
         }
       }
     }
@@ -1356,7 +1359,7 @@ __global__ __launch_bounds__(512) void g96_kernel(KBasis bs, int B, int IN, int 
       float z2[8], tp[8], tc[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const float wv = wp ? wn[u] : (in_ok ? 1.f : 0.f);
+        const float wv = wp ? wn_[u] : (in_ok ? 1.f : 0.f);
         z2[u] = 2.f * zn[u];
         tp[u] = SKIP0 ? wv * zn[u] : wv;                         // first feature: T_1 or T_0
         tc[u] = SKIP0 ? wv * fmaf(z2[u], zn[u], -1.f) : wv * zn[u];  // then T_2 or T_1
@@ -1377,7 +1380,7 @@ __global__ __launch_bounds__(512) void g96_kernel(KBasis bs, int B, int IN, int 
       }
     }
   };
-  // fragments: A row l32 of output block a; B row f * 96 + 32 c + l32 (feature f = wave)
+  // fragments: A row 96 wm + 32 a + l32; B row 32 (3 wn + c) + l32
   const int sw = (l32 >> 2) & 3;
   auto mma_stage = [&](int st) {
     const unsigned char* base = smem + (st & 1) * SS;
@@ -1386,9 +1389,9 @@ __global__ __launch_bounds__(512) void g96_kernel(KBasis bs, int B, int IN, int 
       const int co = 16 * ((2 * ks + h) ^ sw);
       u32x4 fa[3], fb[3];
 #pragma unroll
-      for (int a = 0; a < 3; ++a) fa[a] = lds_read16(base + (a * 32 + l32) * 64 + co);
+      for (int a = 0; a < 3; ++a) fa[a] = lds_read16(base + (wm * 96 + a * 32 + l32) * 64 + co);
 #pragma unroll
-      for (int c = 0; c < 3; ++c) fb[c] = lds_read16(base + SA + (wave * TI + c * 32 + l32) * 64 + co);
+      for (int c = 0; c < 3; ++c) fb[c] = lds_read16(base + SA + ((3 * wn + c) * 32 + l32) * 64 + co);
 #pragma unroll
       for (int a = 0; a < 3; ++a)
 #pragma unroll
@@ -1417,23 +1420,29 @@ __global__ __launch_bounds__(512) void g96_kernel(KBasis bs, int B, int IN, int 
     __builtin_amdgcn_s_barrier();
   }
 
-  // epilogue, one 32-input block at a time: red[f][o][33] feature sums, then the fold
+  // epilogue, one half of the outputs at a time: red[f][o][RP] feature sums, then the fold
   float* red = reinterpret_cast<float*>(smem);
 #pragma unroll
-  for (int c = 0; c < 3; ++c) {
+  for (int half = 0; half < 2; ++half) {
     __syncthreads();
+    if (wm == half) {
 #pragma unroll
-    for (int a = 0; a < 3; ++a)
+      for (int c = 0; c < 3; ++c) {
+        const int col = (3 * wn + c) * 32 + l32, f = col / TI, il = col % TI;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) red[(wave * TO + a * 32 + acc_row(r, lane)) * 33 + l32] = acc[a][c][r];
+        for (int a = 0; a < 3; ++a)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) red[(f * 96 + a * 32 + acc_row(r, lane)) * RP + il] = acc[a][c][r];
+      }
+    }
     __syncthreads();
-    for (int e = tid; e < TO * 32 * K; e += 512) {
-      const int k = e % K, il = (e / K) % 32, ol = e / (K * 32);
-      const int o = o0 + ol, i = i0 + c * 32 + il;
+    for (int e = tid; e < 96 * TI * K; e += 512) {
+      const int k = e % K, il = (e / K) % TI, ol = e / (K * TI);
+      const int o = o0 + half * 96 + ol, i = i0 + il;
       if (o < OUT && i < IN) {
         float sum = SKIP0 ? bs.fold[k * KF_MAX_NT] * colsum[o] : 0.f;
         for (int f = 0; f < n_run; ++f)
-          sum = fmaf(bs.fold[k * KF_MAX_NT + f + (SKIP0 ? 1 : 0)], red[(f * TO + ol) * 33 + il], sum);
+          sum = fmaf(bs.fold[k * KF_MAX_NT + f + (SKIP0 ? 1 : 0)], red[(f * 96 + ol) * RP + il], sum);
         dc[((size_t)o * IN + i) * K + k] = from_f32<bf16>(sum);
       }
     }
