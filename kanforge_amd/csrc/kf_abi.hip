@@ -252,18 +252,33 @@ int zero_fill(void* p, long n, hipStream_t s) {
   return check_launch("fill");
 }
 
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// 16-byte loads of rows of n elements of T: rows start aligned when n is a
+// multiple of the vector width and the array is
+template <typename T>
+bool rows_vec(int64_t n, const void* p) {
+  return n % (int64_t)(16 / sizeof(T)) == 0 && (p == nullptr || aligned16(p));
+}
+
 // permute (and fold) coefficients into a feature-major workspace layout with
 // n_feat >= n_t features (zeros past n_t)
 template <typename T>
 int launch_permute(const KBasis& kb, int64_t n_out, int64_t n_in, int64_t OUTP, int64_t INP, int n_feat, const void* c,
                    void* out, int fmt, hipStream_t s, int j_first = 0, float* part0 = nullptr) {
-  dim3 grid((unsigned)((OUTP + 31) / 32), (unsigned)((INP + 15) / 16));
-  size_t lds = (size_t)(n_feat + j_first) * 16 * 33 * sizeof(float);
+  if (OUTP % 32 || INP % 16 || !aligned16(out)) return fail(KF_EINVAL, "permute: workspace layout not aligned");
+  dim3 grid((unsigned)(OUTP / 32), (unsigned)(INP / 16));
+  const size_t rows = (size_t)32 * (16 * kb.K + 1), tile = (size_t)(n_feat + j_first) * 16 * kPermTS;
+  const size_t lds = (rows > tile ? rows : tile) * sizeof(float);
+  KFoldT ft;
+  for (int j = 0; j < KF_MAX_NT; ++j)
+    for (int k = 0; k < KF_MAX_K; ++k) ft.v[j][k] = k < kb.K && j < kb.n_t ? kb.fold[k * KF_MAX_NT + j] : 0.f;
+  const int vin = n_in % 16 == 0 && rows_vec<T>(n_in * kb.K, c);
   auto kern = fmt == kPermFMT ? permute_coef_kernel<T, kPermFMT>
               : fmt == kPermC16 ? permute_coef_kernel<T, kPermC16>
                                 : permute_coef_kernel<T, kPermFM>;
-  hipLaunchKernelGGL(kern, grid, dim3(kThreads), lds, s, kb, (int)n_out, (int)n_in, (int)OUTP, (int)INP, n_feat,
-                     j_first, (const T*)c, (T*)out, part0);
+  hipLaunchKernelGGL(kern, grid, dim3(kThreads), lds, s, ft, kb.K, kb.n_t, (int)n_out, (int)n_in, (int)OUTP, (int)INP,
+                     n_feat, j_first, vin, (const T*)c, (T*)out, part0);
   return check_launch("permute_coef");
 }
 
@@ -376,11 +391,13 @@ int run_F(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
       rc = check_launch("sum_parts");
       if (rc) return rc;
     }
-    long n = (long)L.BP * L.INP;
+    if (L.INP % 16 || L.BP % 32) return fail(KF_EINVAL, "F: workspace layout not aligned");
+    long n = (L.INP + 63) / 64 * L.BP * (64 / (16 / (long)sizeof(T)));
     long blocks = (n + kThreads - 1) / kThreads;
     if (blocks > 65535 * 4) blocks = 65535 * 4;
+    const int vin = rows_vec<T>(n_in, x) && rows_vec<T>(n_in, w);
     hipLaunchKernelGGL(zmapc_kernel<T>, dim3((unsigned)blocks), dim3(kThreads), 0, s, (int)batch, (int)n_in,
-                       (int)L.BP, (int)L.INP, kb.input_map, (const T*)x, (const T*)w, z, wz);
+                       (int)L.BP, (int)L.INP, kb.input_map, vin, (const T*)x, (const T*)w, z, wz);
     rc = check_launch("zmapc");
     if (rc) return rc;
     if (weighted) return launch_f_rega<true, false>(L, batch, n_out, z, wz, cfm, nullptr, y, s);
@@ -580,9 +597,10 @@ int run_G(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
   float* wt = cheb && weighted ? (float*)(base + L.gt + L.zt) : nullptr;
   float* part = L.skip0 ? (float*)(base + L.gt + L.zt + L.wt) : nullptr;
   float* colsum = L.skip0 ? (float*)(base + L.gt + L.zt + L.wt + L.part) : nullptr;
+  if (L.BP % 32 || !aligned16(gt)) return fail(KF_EINVAL, "G: workspace layout not aligned");
   dim3 tg((unsigned)((L.OUTP + 63) / 64), (unsigned)((L.BP + 63) / 64));
   hipLaunchKernelGGL(transpose_kernel<T>, tg, dim3(kThreads), 0, s, (int)batch, (int)n_out, (int)L.BP, (int)L.OUTP,
-                     (const T*)g, (T*)gt, part);
+                     (int)rows_vec<T>(n_out, g), (const T*)g, (T*)gt, part);
   int rc = check_launch("transpose");
   if (rc) return rc;
   if (L.skip0) {
@@ -593,8 +611,9 @@ int run_G(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
   }
   if (cheb) {
     dim3 zg((unsigned)((L.INP + 63) / 64), (unsigned)((L.BP + 63) / 64));
-    hipLaunchKernelGGL(zmapT_kernel<T>, zg, dim3(kThreads), 0, s, (int)batch, (int)n_in, (int)L.BP, (int)L.INP,
-                       kb.input_map, (const T*)x, (const T*)w, zt, wt);
+    hipLaunchKernelGGL(zmapT_kernel<T>, zg, dim3(kThreads), (size_t)(wt ? 2 : 1) * 64 * 65 * sizeof(float), s, (int)batch, (int)n_in, (int)L.BP, (int)L.INP,
+                       kb.input_map, (int)(rows_vec<T>(n_in, x) && rows_vec<T>(n_in, w)), (const T*)x, (const T*)w,
+                       zt, wt);
     rc = check_launch("zmapT");
     if (rc) return rc;
     if (L.g96) {
@@ -670,6 +689,8 @@ int kf_F(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
   size_t need = ws_f(b, dtype, batch, n_in, n_out, w != nullptr).total;
   if (!workspace || workspace_bytes < need)
     return fail(KF_EWORKSPACE, "kf_F: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  if (reinterpret_cast<uintptr_t>(workspace) & 255)
+    return fail(KF_EWORKSPACE, "kf_F: workspace must be 256-byte aligned");
   KBasis kb = to_kbasis(b);
   if (dtype == KF_BF16) return run_F<bf16>(kb, b, dtype, batch, n_in, n_out, x, w, c, y, workspace, s);
   return run_F<float>(kb, b, dtype, batch, n_in, n_out, x, w, c, y, workspace, s);
@@ -688,6 +709,8 @@ int kf_G(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
   size_t need = ws_g(b, dtype, batch, n_in, n_out, w != nullptr).total;
   if (!workspace || workspace_bytes < need)
     return fail(KF_EWORKSPACE, "kf_G: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  if (reinterpret_cast<uintptr_t>(workspace) & 255)
+    return fail(KF_EWORKSPACE, "kf_G: workspace must be 256-byte aligned");
   KBasis kb = to_kbasis(b);
   if (dtype == KF_BF16) return run_G<bf16>(kb, b, dtype, batch, n_in, n_out, x, g, w, dc, workspace, s);
   return run_G<float>(kb, b, dtype, batch, n_in, n_out, x, g, w, dc, workspace, s);
@@ -710,6 +733,8 @@ int kf_P(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
   size_t need = ws_p(b, dtype, batch, n_in, n_out).total;
   if (!workspace || workspace_bytes < need)
     return fail(KF_EWORKSPACE, "kf_P: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  if (reinterpret_cast<uintptr_t>(workspace) & 255)
+    return fail(KF_EWORKSPACE, "kf_P: workspace must be 256-byte aligned");
   KBasis kb = to_kbasis(b);
   if (dtype == KF_BF16) return run_P<bf16>(kb, b, dtype, batch, n_in, n_out, x, g, c, p, h, workspace, s);
   return run_P<float>(kb, b, dtype, batch, n_in, n_out, x, g, c, p, h, workspace, s);

@@ -61,11 +61,30 @@ __device__ __forceinline__ u32x4 pack16<float>(const float* v) {
   return __builtin_bit_cast(u32x4, r);
 }
 
+// Unpack 16 bytes of T elements into float values.
+template <typename T>
+__device__ __forceinline__ void unpack16(const u32x4& u, float* v);
+template <>
+__device__ __forceinline__ void unpack16<bf16>(const u32x4& u, float* v) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    v[2 * e] = __uint_as_float(u[e] << 16);
+    v[2 * e + 1] = __uint_as_float(u[e] & 0xffff0000u);
+  }
+}
+template <>
+__device__ __forceinline__ void unpack16<float>(const u32x4& u, float* v) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = __uint_as_float(u[e]);
+}
+
 // Load 16 bytes from global memory; `ok` false gives zeros.
 __device__ __forceinline__ u32x4 gload16(const void* p, bool ok) {
   u32x4 z = {0u, 0u, 0u, 0u};
   return ok ? *reinterpret_cast<const u32x4*>(p) : z;
 }
+
+__device__ __forceinline__ void gstore16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
 
 }  // namespace kf
 

@@ -26,64 +26,105 @@ constexpr int kThreads = 256;
 //   kPermC16: out[i/16][j][o][i%16]    (INP/16, n_t, OUTP, 16)
 //             every (16-input chunk, feature) block contiguous: B operand
 //             of the register-A F kernel, whose stages read whole blocks
-// out[j] = sum_k c[o,i,k] fold[k][j]. Tile 32 o x 16 i through LDS.
+// out[j] = sum_k c[o,i,k] fold[k][j]. A block folds 32 outputs x 16 inputs:
+// the 16 K coefficients of one output are contiguous in c and come in with
+// 16-byte loads when vin is set (n_in a multiple of 16, rows 16-byte
+// aligned), the folded tile goes out with 16-byte stores (OUTP a multiple of
+// 32, INP of 16). LDS row stride 36 floats keeps both the fold's writes and
+// the stores' reads free of bank conflicts.
 enum { kPermFM = 0, kPermFMT = 1, kPermC16 = 2 };
+constexpr int kPermTS = 36;
+// The fold matrix transposed (column j of R_m contiguous, zero past K and
+// n_t), passed by value: one scalar load brings a whole column.
+struct KFoldT {
+  float v[KF_MAX_NT][KF_MAX_K];
+};
 template <typename T, int FMT>
-__global__ __launch_bounds__(kThreads) void permute_coef_kernel(KBasis bs, int OUT, int IN, int OUTP, int INP,
-                                                                int n_feat, int j_first, const T* __restrict__ c,
-                                                                T* __restrict__ out, float* __restrict__ part0) {
-  extern __shared__ float tile[];  // [n_feat + j_first][16][33]
-  const int K = bs.K, n_all = n_feat + j_first;  // features past bs.n_t get zero fold columns
-  const int o0 = blockIdx.x * 32, i0 = blockIdx.y * 16;
+__global__ __launch_bounds__(kThreads) void permute_coef_kernel(KFoldT ft, int K, int n_t_fold, int OUT, int IN,
+                                                                int OUTP, int INP, int n_feat, int j_first, int vin,
+                                                                const T* __restrict__ c, T* __restrict__ out,
+                                                                float* __restrict__ part0) {
+  constexpr int VW = 16 / (int)sizeof(T);
+  // crow [32][16K + 1], then (aliased) tile [n_feat + j_first][16][kPermTS]
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
+  float* smem = reinterpret_cast<float*>(smem_raw);
+  const int n_all = n_feat + j_first;  // features past n_t_fold get zero fold columns
+  const int RL = 16 * K, RS = RL + 1;
+  const int ob = blockIdx.x, ib = blockIdx.y;
+  const int o0 = ob * 32, i0 = ib * 16;
   const int t = threadIdx.x;
-  // phase 1: thread (ol = t / 16 .. +16, il = t % 16) covers 2 o rows
+  if (vin) {
+    const int CR = RL / VW;
+    for (int e = t; e < 32 * CR; e += kThreads) {
+      const int ol = e / CR, q = e - ol * CR;
+      const int o = o0 + ol;
+      float v[VW];
+      unpack16<T>(gload16(c + ((size_t)o * IN + i0) * K + q * VW, o < OUT && i0 < IN), v);
+#pragma unroll
+      for (int u = 0; u < VW; ++u) smem[ol * RS + q * VW + u] = v[u];
+    }
+  } else {
+    for (int e = t; e < 32 * RL; e += kThreads) {
+      const int ol = e / RL, r = e - ol * RL;
+      const int o = o0 + ol, i = i0 + r / K;
+      smem[ol * RS + r] = (o < OUT && i < IN) ? to_f32(c[((size_t)o * IN + i0) * K + r]) : 0.f;
+    }
+  }
+  __syncthreads();
+  // thread (ol = t / 16 + 16 rep, il = t % 16): the K coefficients of one edge
+  float cv[2][KF_MAX_K];
+  const int il = t % 16;
+#pragma unroll
   for (int rep = 0; rep < 2; ++rep) {
-    const int ol = t / 16 + rep * 16, il = t % 16;
-    const int o = o0 + ol, i = i0 + il;
-    float cv[KF_MAX_K];
+    const int ol = t / 16 + rep * 16;
 #pragma unroll
-    for (int k = 0; k < KF_MAX_K; ++k)
-      cv[k] = (k < K && o < OUT && i < IN) ? to_f32(c[((size_t)o * IN + i) * K + k]) : 0.f;
-    for (int j = 0; j < n_all; ++j) {
+    for (int k = 0; k < KF_MAX_K; ++k) cv[rep][k] = k < K ? smem[ol * RS + il * K + k] : 0.f;
+  }
+  __syncthreads();
+  float* tile = smem;
+  for (int j = 0; j < n_all; ++j) {
+    const bool live = j < n_t_fold;  // n_t_fold <= KF_MAX_NT
+    const float* fj = ft.v[live ? j : 0];
+#pragma unroll
+    for (int rep = 0; rep < 2; ++rep) {
       float acc = 0.f;
-      if (j < bs.n_t) {
 #pragma unroll
-        for (int k = 0; k < KF_MAX_K; ++k)
-          if (k < K) acc = fmaf(cv[k], bs.fold[k * KF_MAX_NT + j], acc);
-      }
-      tile[(j * 16 + il) * 33 + ol] = acc;
+      for (int k = 0; k < KF_MAX_K; ++k) acc = fmaf(cv[rep][k], fj[k], acc);
+      tile[(j * 16 + il) * kPermTS + t / 16 + rep * 16] = live ? acc : 0.f;
     }
   }
   __syncthreads();
   // feature 0 left out (j_first = 1): its partial sums over the block's 16 inputs per output
   if (j_first && t < 32 && o0 + t < OUTP) {
     float sum = 0.f;
-    for (int il = 0; il < 16; ++il) sum += tile[il * 33 + t];
-    part0[(size_t)blockIdx.y * OUTP + o0 + t] = sum;
+    for (int l = 0; l < 16; ++l) sum += tile[l * kPermTS + t];
+    part0[(size_t)ib * OUTP + o0 + t] = sum;
   }
-  const float* tf = tile + j_first * 16 * 33;
+  const float* tf = tile + j_first * 16 * kPermTS;
   const int n_t = n_feat;
-  if (FMT == kPermC16) {
-    // out[i/16][j][o][i%16]: 16 inputs of one output row contiguous, then o
-    T* blk = out + (size_t)blockIdx.y * n_t * OUTP * 16;
-    for (int e = t; e < n_t * 32 * 16; e += kThreads) {
-      const int il = e % 16, ol = (e / 16) % 32, j = e / (16 * 32);
-      const int o = o0 + ol;
-      if (o < OUTP) blk[((size_t)j * OUTP + o) * 16 + il] = from_f32<T>(tf[(j * 16 + il) * 33 + ol]);
-    }
-  } else if (FMT == kPermFM) {
-    // out[j][o][i]: consecutive threads along i
-    for (int e = t; e < n_t * 32 * 16; e += kThreads) {
-      const int il = e % 16, ol = (e / 16) % 32, j = e / (16 * 32);
-      const int o = o0 + ol, i = i0 + il;
-      if (o < OUTP && i < INP) out[((size_t)j * OUTP + o) * INP + i] = from_f32<T>(tf[(j * 16 + il) * 33 + ol]);
+  if (FMT == kPermFMT) {
+    // out[j][i][o]: rows (j, i) of 32 outputs, 32 / VW lanes each
+    constexpr int LR = 32 / VW;
+    for (int e = t; e < n_t * 16 * LR; e += kThreads) {
+      const int q = e % LR, r = e / LR, j = r / 16, l = r % 16;
+      const int i = i0 + l;
+      float v[VW];
+#pragma unroll
+      for (int u = 0; u < VW; ++u) v[u] = tf[(j * 16 + l) * kPermTS + q * VW + u];
+      if (i < INP && o0 < OUTP) gstore16(out + ((size_t)j * INP + i) * OUTP + o0 + q * VW, pack16<T>(v));
     }
   } else {
-    // out[j][i][o]: consecutive threads along o
-    for (int e = t; e < n_t * 32 * 16; e += kThreads) {
-      const int ol = e % 32, il = (e / 32) % 16, j = e / (16 * 32);
-      const int o = o0 + ol, i = i0 + il;
-      if (o < OUTP && i < INP) out[((size_t)j * INP + i) * OUTP + o] = from_f32<T>(tf[(j * 16 + il) * 33 + ol]);
+    // C16: out[i/16][j][o][i%16]; FM: out[j][o][i]. Rows (j, o) of 16 inputs, 16 / VW lanes each
+    constexpr int LR = 16 / VW;
+    T* base = FMT == kPermC16 ? out + (size_t)ib * n_t * OUTP * 16 : out + i0;
+    const size_t rs = FMT == kPermC16 ? 16 : (size_t)INP;
+    for (int e = t; e < n_t * 32 * LR; e += kThreads) {
+      const int ol = e % 32, q = (e / 32) % LR, j = e / (32 * LR);
+      const int o = o0 + ol;
+      float v[VW];
+#pragma unroll
+      for (int u = 0; u < VW; ++u) v[u] = tf[(j * 16 + q * VW + u) * kPermTS + ol];
+      if (o < OUTP && i0 < INP) gstore16(base + ((size_t)j * OUTP + o) * rs + q * VW, pack16<T>(v));
     }
   }
 }
@@ -96,10 +137,18 @@ __global__ __launch_bounds__(kThreads) void sum_parts_kernel(int n_parts, int n,
   __shared__ float red[8][33];
   const int ol = threadIdx.x % 32, pg = threadIdx.x / 32;
   const int o = blockIdx.x * 32 + ol;
-  float s = 0.f;
-  if (o < n)
-    for (int q = pg; q < n_parts; q += 8) s += part[(size_t)q * n + o];
-  red[pg][ol] = s;
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  if (o < n) {
+    int q = pg;
+    for (; q + 24 < n_parts; q += 32) {
+      s0 += part[(size_t)q * n + o];
+      s1 += part[(size_t)(q + 8) * n + o];
+      s2 += part[(size_t)(q + 16) * n + o];
+      s3 += part[(size_t)(q + 24) * n + o];
+    }
+    for (; q < n_parts; q += 8) s0 += part[(size_t)q * n + o];
+  }
+  red[pg][ol] = (s0 + s1) + (s2 + s3);
   __syncthreads();
   if (pg == 0 && o < n) {
     float tot = 0.f;
@@ -110,27 +159,48 @@ __global__ __launch_bounds__(kThreads) void sum_parts_kernel(int n_parts, int n,
 }
 
 // ---------------------------------------------------------------------------
-// g (B, OUT) -> gT (OUTP, BP), zero padded. 64x64 tiles through LDS. With
-// part given, also the column sums of each 64-row block: part[blk][o].
+// g (B, OUT) -> gT (OUTP, BP), zero padded. 64x64 tiles through LDS with
+// 16-byte loads (when vin: OUT a multiple of the vector width, g aligned) and
+// 16-byte stores (BP a multiple of 32). With part given, also the column sums
+// of each 64-row block, part[blk][o] (per lane over its 16 bytes, then across
+// the lanes of one output row).
 template <typename T>
-__global__ __launch_bounds__(kThreads) void transpose_kernel(int B, int OUT, int BP, int OUTP, const T* __restrict__ g,
-                                                             T* __restrict__ gt, float* __restrict__ part) {
+__global__ __launch_bounds__(kThreads) void transpose_kernel(int B, int OUT, int BP, int OUTP, int vin,
+                                                             const T* __restrict__ g, T* __restrict__ gt,
+                                                             float* __restrict__ part) {
+  constexpr int VW = 16 / (int)sizeof(T), LPR = 64 / VW, RPI = kThreads / LPR;
   __shared__ float tile[64][65];
   const int b0 = blockIdx.y * 64, o0 = blockIdx.x * 64;
-  const int tx = threadIdx.x % 64, ty = threadIdx.x / 64;
-  for (int r = ty; r < 64; r += 4) {
-    const int b = b0 + r, o = o0 + tx;
-    tile[r][tx] = (b < B && o < OUT) ? to_f32(g[(size_t)b * OUT + o]) : 0.f;
+  const int cl = threadIdx.x % LPR, rl = threadIdx.x / LPR;
+#pragma unroll
+  for (int r = rl; r < 64; r += RPI) {
+    const int b = b0 + r, o = o0 + cl * VW;
+    float v[VW];
+    if (vin) {
+      unpack16<T>(gload16(g + (size_t)b * OUT + o, b < B && o < OUT), v);
+    } else {
+#pragma unroll
+      for (int u = 0; u < VW; ++u) v[u] = (b < B && o + u < OUT) ? to_f32(g[(size_t)b * OUT + o + u]) : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < VW; ++u) tile[r][cl * VW + u] = v[u];
   }
   __syncthreads();
-  if (part && ty == 0 && o0 + tx < OUTP) {
-    float sum = 0.f;
-    for (int r = 0; r < 64; ++r) sum += tile[r][tx];
-    part[(size_t)blockIdx.y * OUTP + o0 + tx] = sum;
-  }
-  for (int r = ty; r < 64; r += 4) {
-    const int o = o0 + r, b = b0 + tx;
-    if (o < OUTP && b < BP) gt[(size_t)o * BP + b] = from_f32<T>(tile[tx][r]);
+#pragma unroll
+  for (int r = rl; r < 64; r += RPI) {
+    const int o = o0 + r, b = b0 + cl * VW;
+    float v[VW], sum = 0.f;
+#pragma unroll
+    for (int u = 0; u < VW; ++u) {
+      v[u] = tile[cl * VW + u][r];
+      sum += v[u];
+    }
+    if (part) {
+#pragma unroll
+      for (int m = 1; m < LPR; m <<= 1) sum += __shfl_xor(sum, m);
+      if (cl == 0 && o < OUTP) part[(size_t)blockIdx.y * OUTP + o] = sum;
+    }
+    if (o < OUTP && b < BP) gstore16(gt + (size_t)o * BP + b, pack16<T>(v));
   }
 }
 
@@ -190,20 +260,53 @@ __global__ __launch_bounds__(kThreads) void zmap_kernel(int B, int IN, int BP, i
 // Chunked variant for the register-A F kernel: zc[c][b][e] = g(x[b][16c+e])
 // (and the feature weight wc likewise), float32, zero-padded to
 // (INP/16, BP, 16), so the 16 inputs of one row in one chunk are 64
-// contiguous bytes.
+// contiguous bytes. Lanes run along 64-input row segments (16-byte loads
+// when vin: IN a multiple of the vector width, x and w aligned), then along
+// rows, so each chunk's stores of a wave are contiguous.
 template <typename T>
-__global__ __launch_bounds__(kThreads) void zmapc_kernel(int B, int IN, int BP, int INP, int input_map,
+__global__ __launch_bounds__(kThreads) void zmapc_kernel(int B, int IN, int BP, int INP, int input_map, int vin,
                                                          const T* __restrict__ x, const T* __restrict__ w,
                                                          float* __restrict__ zc, float* __restrict__ wc) {
-  const long n = (long)BP * INP;
+  constexpr int VW = 16 / (int)sizeof(T), LPR = 64 / VW;
+  const long n = (long)((INP + 63) / 64) * BP * LPR;
   for (long e = blockIdx.x * (long)kThreads + threadIdx.x; e < n; e += (long)gridDim.x * kThreads) {
-    const int il = (int)(e % 16), b = (int)((e / 16) % BP), c = (int)(e / (16L * BP));
-    const int i = c * 16 + il;
-    const bool ok = b < B && i < IN;
-    const size_t off = (size_t)b * IN + i;
-    const float zz = ok ? cheb_map(to_f32(x[off]), input_map) : 0.f;
-    zc[e] = zz;
-    if (wc) wc[e] = ok ? cheb_weight(zz, w ? to_f32(w[off]) : 1.f, input_map) : 0.f;
+    const int q = (int)(e % LPR), b = (int)((e / LPR) % BP), seg = (int)(e / ((long)LPR * BP));
+    const int i = seg * 64 + q * VW;
+    if (i >= INP) continue;
+    float xv[VW], wv[VW];
+    if (vin) {
+      const bool ok = b < B && i < IN;
+      unpack16<T>(gload16(x + (size_t)b * IN + i, ok), xv);
+      if (wc && w) unpack16<T>(gload16(w + (size_t)b * IN + i, ok), wv);
+    } else {
+#pragma unroll
+      for (int u = 0; u < VW; ++u) {
+        const bool ok = b < B && i + u < IN;
+        xv[u] = ok ? to_f32(x[(size_t)b * IN + i + u]) : 0.f;
+        if (wc && w) wv[u] = ok ? to_f32(w[(size_t)b * IN + i + u]) : 0.f;
+      }
+    }
+    float zz[VW], ww[VW];
+#pragma unroll
+    for (int u = 0; u < VW; ++u) {
+      const bool ok = b < B && i + u < IN;
+      zz[u] = ok ? cheb_map(xv[u], input_map) : 0.f;
+      ww[u] = ok ? cheb_weight(zz[u], w ? wv[u] : 1.f, input_map) : 0.f;
+    }
+    float* zp = zc + ((size_t)(i / 16) * BP + b) * 16 + i % 16;
+#pragma unroll
+    for (int h = 0; h < VW / 4; ++h) {
+      f32x4 v = {zz[4 * h], zz[4 * h + 1], zz[4 * h + 2], zz[4 * h + 3]};
+      gstore16(zp + 4 * h, __builtin_bit_cast(u32x4, v));
+    }
+    if (wc) {
+      float* wp = wc + ((size_t)(i / 16) * BP + b) * 16 + i % 16;
+#pragma unroll
+      for (int h = 0; h < VW / 4; ++h) {
+        f32x4 v = {ww[4 * h], ww[4 * h + 1], ww[4 * h + 2], ww[4 * h + 3]};
+        gstore16(wp + 4 * h, __builtin_bit_cast(u32x4, v));
+      }
+    }
   }
 }
 
@@ -434,28 +537,55 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void f_kernel(int B, int OUT
 // ---------------------------------------------------------------------------
 // z^T[i][b] = g(x[b][i]) (float32, zero-padded to (INP, BP)) and, when wt is
 // given, the feature weight (as in zmap_kernel) transposed the same way: the
-// G kernel generates features with the batch
-// (its reduction dimension) contiguous. 64x64 tiles through LDS.
+// G kernel generates features with the batch (its reduction dimension)
+// contiguous. 64x64 tiles through LDS; 16-byte loads when vin (IN a multiple
+// of the vector width, x and w aligned), 16-byte stores (BP a multiple of 32).
 template <typename T>
-__global__ __launch_bounds__(kThreads) void zmapT_kernel(int B, int IN, int BP, int INP, int input_map,
+__global__ __launch_bounds__(kThreads) void zmapT_kernel(int B, int IN, int BP, int INP, int input_map, int vin,
                                                          const T* __restrict__ x, const T* __restrict__ w,
                                                          float* __restrict__ zt, float* __restrict__ wt) {
-  __shared__ float tz[64][65], tw[64][65];
+  constexpr int VW = 16 / (int)sizeof(T), LPR = 64 / VW, RPI = kThreads / LPR;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];  // tz [64][65], tw [64][65] when wt
+  float* tz = reinterpret_cast<float*>(smem);
+  float* tw = tz + 64 * 65;
   const int b0 = blockIdx.y * 64, i0 = blockIdx.x * 64;
-  const int tx = threadIdx.x % 64, ty = threadIdx.x / 64;
-  for (int r = ty; r < 64; r += 4) {
-    const int b = b0 + r, i = i0 + tx;
-    const bool ok = b < B && i < IN;
-    const float zz = ok ? cheb_map(to_f32(x[(size_t)b * IN + i]), input_map) : 0.f;
-    tz[r][tx] = zz;
-    if (wt) tw[r][tx] = ok ? cheb_weight(zz, w ? to_f32(w[(size_t)b * IN + i]) : 1.f, input_map) : 0.f;
+  const int cl = threadIdx.x % LPR, rl = threadIdx.x / LPR;
+#pragma unroll
+  for (int r = rl; r < 64; r += RPI) {
+    const int b = b0 + r, i = i0 + cl * VW;
+    float xv[VW], wv[VW];
+    if (vin) {
+      const bool ok = b < B && i < IN;
+      unpack16<T>(gload16(x + (size_t)b * IN + i, ok), xv);
+      if (wt && w) unpack16<T>(gload16(w + (size_t)b * IN + i, ok), wv);
+    } else {
+#pragma unroll
+      for (int u = 0; u < VW; ++u) {
+        const bool ok = b < B && i + u < IN;
+        xv[u] = ok ? to_f32(x[(size_t)b * IN + i + u]) : 0.f;
+        if (wt && w) wv[u] = ok ? to_f32(w[(size_t)b * IN + i + u]) : 0.f;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < VW; ++u) {
+      const bool ok = b < B && i + u < IN;
+      const float zz = ok ? cheb_map(xv[u], input_map) : 0.f;
+      tz[r * 65 + cl * VW + u] = zz;
+      if (wt) tw[r * 65 + cl * VW + u] = ok ? cheb_weight(zz, w ? wv[u] : 1.f, input_map) : 0.f;
+    }
   }
   __syncthreads();
-  for (int r = ty; r < 64; r += 4) {
-    const int i = i0 + r, b = b0 + tx;
+  // rows i of 64 batch values: 16 lanes of 4 floats each
+#pragma unroll
+  for (int r = threadIdx.x / 16; r < 64; r += kThreads / 16) {
+    const int i = i0 + r, bl = (threadIdx.x % 16) * 4, b = b0 + bl;
     if (i < INP && b < BP) {
-      zt[(size_t)i * BP + b] = tz[tx][r];
-      if (wt) wt[(size_t)i * BP + b] = tw[tx][r];
+      f32x4 v = {tz[bl * 65 + r], tz[(bl + 1) * 65 + r], tz[(bl + 2) * 65 + r], tz[(bl + 3) * 65 + r]};
+      gstore16(zt + (size_t)i * BP + b, __builtin_bit_cast(u32x4, v));
+      if (wt) {
+        f32x4 u = {tw[bl * 65 + r], tw[(bl + 1) * 65 + r], tw[(bl + 2) * 65 + r], tw[(bl + 3) * 65 + r]};
+        gstore16(wt + (size_t)i * BP + b, __builtin_bit_cast(u32x4, u));
+      }
     }
   }
 }
