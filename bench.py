@@ -65,6 +65,26 @@ class EntryTimer:
         return {op: (sum(s.elapsed_time(e) for s, e in ev) / len(ev) if ev else 0.0) for op, ev in self.events.items()}
 
 
+TRAFFIC_FILE = os.path.join("profiles", "kanlinear_768x3072_cheb8_bf16_hbm_traffic.md")
+
+
+def measured_traffic(entry):
+    """HBM bytes per launch of one entry point, from the committed counter summary
+    (FETCH_SIZE and WRITE_SIZE passes scaled by a plain copy's readings); None if absent."""
+    try:
+        lines = open(os.path.join(ROOT, TRAFFIC_FILE)).read().splitlines()
+    except OSError:
+        return None
+    for line in lines:
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) == 4 and cells[0] == entry:
+            try:
+                return float(cells[3])
+            except ValueError:
+                return None
+    return None
+
+
 def cpu_baseline():
     from oracle.torch_cpu import cpu_model, time_chebyshev_step
 
@@ -161,7 +181,9 @@ def main():
             "peak": PEAK_BF16 / 1e12,
             "unit": "TFLOP/s",
             "frac": achieved * 1e12 / PEAK_BF16,
-            "traffic": None,
+            "traffic": measured_traffic(f"kf_{dominant}"),
+            "traffic_unit": "bytes per launch",
+            "traffic_source": TRAFFIC_FILE,
         },
     }
     if not args.no_cpu:
