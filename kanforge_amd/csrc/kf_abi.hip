@@ -574,14 +574,20 @@ int launch_g_ws(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, in
 template <bool SKIP0>
 int launch_g96(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out,
                const float* zt, const float* wt, const void* gt, const float* colsum, void* dc) {
-  const size_t lds_ops = (size_t)2 * (192 * 64 + 8 * 48 * 64), lds_red = (size_t)8 * 96 * 49 * 4;
+  const size_t lds_ops = (size_t)2 * (192 * 64 + 8 * 48 * 64), lds_red = (size_t)(8 * 96 * 49 + 96) * 4;
   const size_t lds = lds_ops > lds_red ? lds_ops : lds_red;
   auto kern = g96_kernel<SKIP0>;
   if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return fail(KF_ELAUNCH, "G: cannot reserve %zu bytes of LDS", lds);
   const int n_m = (int)(L.OUTP / 192), n_n = (int)(L.INP / 48);
-  hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(512), lds, s, kb, (int)batch, (int)n_in, (int)n_out, (int)L.BP,
-                     (int)L.OUTP, (int)L.INP, zt, wt, (const bf16*)gt, colsum, (bf16*)dc);
+  const int skip = SKIP0 ? 1 : 0, n_run = kb.n_t - skip;
+  KFoldG fg;
+  for (int k = 0; k < KF_MAX_K; ++k) {
+    fg.v[k][0] = SKIP0 && k < kb.K ? kb.fold[k * KF_MAX_NT] : 0.f;
+    for (int f = 0; f < 8; ++f) fg.v[k][1 + f] = k < kb.K && f < n_run ? kb.fold[k * KF_MAX_NT + f + skip] : 0.f;
+  }
+  hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(512), lds, s, fg, kb.K, n_run, (int)batch, (int)n_in, (int)n_out,
+                     (int)L.BP, (int)L.OUTP, (int)L.INP, zt, wt, (const bf16*)gt, colsum, (bf16*)dc);
   return check_launch("G");
 }
 

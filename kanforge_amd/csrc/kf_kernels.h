@@ -1417,8 +1417,14 @@ __global__ __launch_bounds__(kThreads) void pad_cols_kernel(int B, int OUT, int 
 // Features past n_t - SKIP0 are computed and dropped. Epilogue, per half of
 // the outputs: the 8 feature sums go to LDS and every thread applies the fold
 // for (o, i, k), k fastest.
+// The fold of the G epilogue, passed by value (one scalar load per k):
+// v[k][0] = fold[k][0] (the left-out T_0 times the column sums of g), v[k][1 + f]
+// = the fold of run feature f (zero past the features run and past K).
+struct KFoldG {
+  float v[KF_MAX_K][9];
+};
 template <bool SKIP0>
-__global__ __launch_bounds__(512) void g96_kernel(KBasis bs, int B, int IN, int OUT, int BP, int OUTP, int INP,
+__global__ __launch_bounds__(512) void g96_kernel(KFoldG fg, int K, int n_run, int B, int IN, int OUT, int BP, int OUTP, int INP,
                                                   const float* __restrict__ zt, const float* __restrict__ wt,
                                                   const bf16* __restrict__ gt, const float* __restrict__ colsum,
                                                   bf16* __restrict__ dc) {
@@ -1436,7 +1442,6 @@ __global__ __launch_bounds__(512) void g96_kernel(KBasis bs, int B, int IN, int 
   const int wm = wave & 1, wn = wave >> 1;
   const int h = lane >> 5, l32 = lane & 31;
   const int S = BP / 32;
-  const int n_run = bs.n_t - (SKIP0 ? 1 : 0), K = bs.K;
 
   f32x16 acc[3][3];
 #pragma unroll
@@ -1550,8 +1555,11 @@ __global__ __launch_bounds__(512) void g96_kernel(KBasis bs, int B, int IN, int 
     __builtin_amdgcn_s_barrier();
   }
 
-  // epilogue, one half of the outputs at a time: red[f][o][RP] feature sums, then the fold
+  // epilogue, one half of the outputs at a time: red[f][o][RP] feature sums, then the fold,
+  // one (o, i) edge per thread and step (the feature sums in registers, the fold row k in
+  // scalar registers)
   float* red = reinterpret_cast<float*>(smem);
+  float* csl = red + NF * 96 * RP;  // column sums of g for the half's outputs
 #pragma unroll
   for (int half = 0; half < 2; ++half) {
     __syncthreads();
@@ -1565,15 +1573,24 @@ __global__ __launch_bounds__(512) void g96_kernel(KBasis bs, int B, int IN, int 
           for (int r = 0; r < 16; ++r) red[(f * 96 + a * 32 + acc_row(r, lane)) * RP + il] = acc[a][c][r];
       }
     }
+    if (SKIP0 && tid < 96) csl[tid] = o0 + half * 96 + tid < OUT ? colsum[o0 + half * 96 + tid] : 0.f;
     __syncthreads();
-    for (int e = tid; e < 96 * TI * K; e += 512) {
-      const int k = e % K, il = (e / K) % TI, ol = e / (K * TI);
+    for (int e = tid; e < 96 * TI; e += 512) {
+      const int ol = e / TI, il = e - ol * TI;
       const int o = o0 + half * 96 + ol, i = i0 + il;
       if (o < OUT && i < IN) {
-        float sum = SKIP0 ? bs.fold[k * KF_MAX_NT] * colsum[o] : 0.f;
-        for (int f = 0; f < n_run; ++f)
-          sum = fmaf(bs.fold[k * KF_MAX_NT + f + (SKIP0 ? 1 : 0)], red[(f * 96 + ol) * RP + il], sum);
-        dc[((size_t)o * IN + i) * K + k] = from_f32<bf16>(sum);
+        float v[NF];
+#pragma unroll
+        for (int f = 0; f < NF; ++f) v[f] = f < n_run ? red[(f * 96 + ol) * RP + il] : 0.f;
+        const float cs = SKIP0 ? csl[ol] : 0.f;
+        bf16* out = dc + ((size_t)o * IN + i) * K;
+        for (int k = 0; k < K; ++k) {
+          const float* fk = fg.v[k];
+          float sum = SKIP0 ? fk[0] * cs : 0.f;
+#pragma unroll
+          for (int f = 0; f < NF; ++f) sum = fmaf(fk[1 + f], v[f], sum);
+          out[k] = from_f32<bf16>(sum);
+        }
       }
     }
   }
