@@ -1534,6 +1534,71 @@ __global__ __launch_bounds__(512) void g96_kernel(KFoldG fg, int K, int n_run, i
     }
   };
 
+  // The generator waves' stage: the MFMAs of stage st with the features of the next stage (z
+  // loaded one stage ago) into buffer buf, in 18 fenced (MFMA, VALU work) pairs so that the
+  // VALU work runs in the shadow of the matrix core. The fragment reads come first (the
+  // feature writes may not pass them).
+  auto gen_mma_stage = [&](int st, int buf) {
+    const unsigned char* rbase = smem + (st & 1) * SS;
+    unsigned char* wbase = smem + buf * SS + SA;
+    u32x4 fa[2][3], fb[2][3];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int co = 16 * ((2 * ks + h) ^ sw);
+#pragma unroll
+      for (int a = 0; a < 3; ++a) fa[ks][a] = lds_read16(rbase + (wm * 96 + a * 32 + l32) * 64 + co);
+#pragma unroll
+      for (int c = 0; c < 3; ++c) fb[ks][c] = lds_read16(rbase + SA + ((3 * wn + c) * 32 + l32) * 64 + co);
+    }
+    float z2[8], tp[8], tc[8];
+    auto mm = [&](int q) {
+      const int ks = q / 9, a = (q % 9) / 3, c = q % 3;
+      mma32<bf16>(acc[a][c], fa[ks][a], fb[ks][c]);
+    };
+    auto seed = [&](int u) {
+      const float wv = wp ? wn_[u] : (in_ok ? 1.f : 0.f);
+      z2[u] = 2.f * zn[u];
+      tp[u] = SKIP0 ? wv * zn[u] : wv;                             // first feature: T_1 or T_0
+      tc[u] = SKIP0 ? wv * fmaf(z2[u], zn[u], -1.f) : wv * zn[u];  // then T_2 or T_1
+    };
+    auto step = [&](int f, int half) {
+#pragma unroll
+      for (int u = 4 * half; u < 4 * half + 4; ++u) {
+        if (f & 1)
+          tc[u] = fmaf(z2[u], tp[u], -tc[u]);
+        else
+          tp[u] = fmaf(z2[u], tc[u], -tp[u]);
+      }
+    };
+    auto emit = [&](int f) {
+      const int row = f * TI + gil;
+      lds_write16(wbase + row * 64 + 16 * (gg ^ ((row >> 2) & 3)), pack16<bf16>((f & 1) ? tc : tp));
+    };
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      mm(q);
+      seed(2 * q);
+      seed(2 * q + 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    mm(4);
+    emit(0);
+    __builtin_amdgcn_sched_barrier(0);
+    mm(5);
+    emit(1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int f = 2; f < NF; ++f) {
+      mm(2 * f + 2);
+      step(f, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      mm(2 * f + 3);
+      step(f, 1);
+      emit(f);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
   // prologue: stage 0 in buffer 0, z of stage 1 in registers
   if (copier) copy_a(0);
   load_z(0);
@@ -1543,13 +1608,15 @@ __global__ __launch_bounds__(512) void g96_kernel(KFoldG fg, int K, int n_run, i
   lds_wait();
   __builtin_amdgcn_s_barrier();
   for (int s = 0; s < S; ++s) {
-    // buffer (s + 1) & 1 is free: every wave passed the barrier after its reads of stage s - 1
-    if (s + 1 < S) {
-      if (copier) copy_a(s + 1);
-      gen_features(s + 1);  // z of stage s + 1, loaded one stage ago
-      if (s + 2 < S) load_z(s + 2);
+    // buffer (s + 1) & 1 is free: every wave passed the barrier after its reads of stage s - 1.
+    // The last stage's generator waves fill it with a repeat of stage S - 1, which nothing reads.
+    if (gen) {
+      gen_mma_stage(s, (s + 1) & 1);
+      load_z(s + 2 < S ? s + 2 : S - 1);
+    } else {
+      if (copier && s + 1 < S) copy_a(s + 1);
+      mma_stage(s);
     }
-    mma_stage(s);
     if (copier) vmem_wait<0>();  // the copies of stage s + 1
     lds_wait();                  // feature writes of stage s + 1, fragment reads of stage s
     __builtin_amdgcn_s_barrier();
