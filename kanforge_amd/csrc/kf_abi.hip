@@ -477,6 +477,19 @@ int launch_p_dma_kind(const WsP& L, hipStream_t s, const KBasis& kb, int64_t bat
   return check_launch("P");
 }
 
+int launch_p8(const WsP& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, const void* x, const void* g,
+              int gstride, const void* cfmt, void* p) {
+  const size_t lds_ops = (size_t)3 * 512 * 64, lds_epi = (size_t)8 * 128 * 33 * 4;
+  const size_t lds = lds_ops > lds_epi ? lds_ops : lds_epi;
+  auto kern = p8_kernel<KF_KIND_CHEB>;
+  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+    return fail(KF_ELAUNCH, "P: cannot reserve %zu bytes of LDS", lds);
+  const int n_m = (int)((batch + 255) / 256), n_n = (int)(L.INP / 32);
+  hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(512), lds, s, kb, (int)batch, (int)n_in, (int)L.INP, (int)L.OUTP,
+                     (const bf16*)x, (const bf16*)g, gstride, (const bf16*)cfmt, (bf16*)p);
+  return check_launch("P");
+}
+
 template <typename T, int FW>
 int launch_p_dma(const WsP& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, const void* x,
                  const void* g, int gstride, const void* cfmt, void* p, float* h) {
@@ -513,6 +526,9 @@ int run_P(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
       ga = gp;
       gstride = (int)L.OUTP;
     }
+    // 7 or 8 Chebyshev features in bf16: the two-waves-per-SIMD kernel
+    if (std::is_same<T, bf16>::value && kb.kind == KF_KIND_CHEB && L.ntb == 8 && !h)
+      return launch_p8(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p);
     switch (L.cfg) {
       case 0: return launch_p_dma<T, 2>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p, h);
       case 1: return launch_p_dma<T, 3>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p, h);

@@ -1388,6 +1388,125 @@ __global__ __launch_bounds__(256) void p_dma_kernel(KBasis bs, int B, int IN, in
   }
 }
 
+// P for bf16 plans with 7 or 8 kernel features: the GEMM
+//   H_j[b, i] = sum_o g[b, o] CfmT[j][i][o]   (columns n = j * 32 + i of a 32-input tile)
+// on 8 waves, two per SIMD, so that one wave's waits and barrier arrivals are covered by the
+// other's MFMAs. Workgroup tile 256 rows x (8 features x 32 inputs); wave (wm, wn) = (wave & 1,
+// wave >> 1) owns rows 128 wm .. +127 and features 2 wn, 2 wn + 1 (4 x 2 accumulator tiles). A
+// stage is 64 bytes of o for the 256 rows of g and the 256 rows of CfmT, copied global -> LDS by
+// all waves into a ring of 3 buffers (copies two stages ahead, one barrier per stage); rows are
+// dense 64 bytes with their 16-byte chunks XOR-swizzled by bits 2..3 of the row. Epilogue, one
+// half of the rows at a time: the feature sums H_j go to LDS and every thread forms
+// p[b, i] = sum_j f_j(x[b, i]) H_j[b, i] for (row, input) pairs, the features computed once per
+// pair.
+template <int KIND>
+__global__ __launch_bounds__(512) void p8_kernel(KBasis bs, int B, int IN, int INP, int OUTP,
+                                                 const bf16* __restrict__ x, const bf16* __restrict__ g, int gstride,
+                                                 const bf16* __restrict__ cfmt, bf16* __restrict__ p) {
+  constexpr int BM = 256, NF = 8, BN = NF * 32, SA = BM * 64, SS = (BM + BN) * 64, NBUF = 3, RP = 33;
+  static_assert(NBUF * SS <= 160 * 1024 && NF * 128 * RP * 4 <= 160 * 1024, "stages and the epilogue fit in LDS");
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];  // [NBUF][SS], later the sums
+
+  const int n_m = (B + BM - 1) / BM, n_n = INP / 32;
+  int tm_, tn_;
+  xcd_tile_grouped(blockIdx.x, n_m, n_n, 8, tm_, tn_);
+  const int b0 = tm_ * BM, i0 = tn_ * 32;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+  const int h = lane >> 5, l32 = lane & 31;
+  const int S = OUTP / 32;
+
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[a][t][r] = 0.f;
+
+  // copies: wave w fills blocks 4 w .. 4 w + 3 of the stage's 32 (16 rows of 64 bytes; rows
+  // 0..255 from g, 256..511 from CfmT); lane l fills chunk l % 4 of row l / 4, i.e. global
+  // chunk (l % 4) ^ ((row >> 2) & 3). Rows past the batch repeat row B - 1 (never stored).
+  const bf16* src[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int row = (4 * wave + k) * 16 + (lane >> 2);
+    const int c = (lane & 3) ^ ((row >> 2) & 3);
+    if (row < BM) {
+      const int b = b0 + row < B ? b0 + row : B - 1;
+      src[k] = g + (size_t)b * gstride + c * 8;
+    } else {
+      const int rr = row - BM;
+      src[k] = cfmt + ((size_t)(rr / 32) * INP + i0 + rr % 32) * OUTP + c * 8;
+    }
+  }
+  auto copy_stage = [&](int st) {
+    unsigned char* dst = smem + (st % NBUF) * SS + 4 * wave * 1024;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) lds_dma16(src[k] + (size_t)st * 32, dst + k * 1024);
+  };
+  const int sw = (l32 >> 2) & 3;
+  auto mma_stage = [&](int st) {
+    const unsigned char* base = smem + (st % NBUF) * SS;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int co = 16 * ((2 * ks + h) ^ sw);
+      u32x4 fa[4], fb[2];
+#pragma unroll
+      for (int a = 0; a < 4; ++a) fa[a] = lds_read16(base + (wm * 128 + a * 32 + l32) * 64 + co);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) fb[t] = lds_read16(base + SA + (wn * 64 + t * 32 + l32) * 64 + co);
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) mma32<bf16>(acc[a][t], fa[a], fb[t]);
+    }
+  };
+
+  copy_stage(0);
+  if (S > 1) copy_stage(1);
+  for (int s = 0; s < S; ++s) {
+    // stage s has landed once at most the copies of stage s + 1 are in flight
+    if (s + 1 < S)
+      vmem_wait<4>();
+    else
+      vmem_wait<0>();
+    lds_wait();  // this wave's reads of stage s - 1, whose buffer the copies below refill
+    __builtin_amdgcn_s_barrier();
+    if (s + 2 < S) copy_stage(s + 2);
+    mma_stage(s);
+  }
+  lds_wait();
+
+  float* red = reinterpret_cast<float*>(smem);  // [NF][128][RP]
+#pragma unroll
+  for (int hr = 0; hr < 2; ++hr) {
+    __syncthreads();
+    if (wm == hr) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) red[((2 * wn + t) * 128 + a * 32 + acc_row(r, lane)) * RP + l32] = acc[a][t][r];
+    }
+    __syncthreads();
+    for (int e = tid; e < 128 * 32; e += 512) {
+      const int row = e / 32, il = e % 32;
+      const int b = b0 + hr * 128 + row, i = i0 + il;
+      if (b < B && i < IN) {
+        float f[NF];
+        kind_features<KIND, NF>(to_f32(x[(size_t)b * IN + i]), 1.f, i, bs, f);
+        float sum = 0.f;
+#pragma unroll
+        for (int q = 0; q < NF; ++q) sum = fmaf(red[(q * 128 + row) * RP + il], f[q], sum);
+        p[(size_t)b * IN + i] = from_f32<bf16>(sum);
+      }
+    }
+  }
+}
+
 // Copy g (B, OUT) into a zero-padded (B, OUTP) buffer: the P kernel copies whole stages.
 template <typename T>
 __global__ __launch_bounds__(kThreads) void pad_cols_kernel(int B, int OUT, int OUTP, const T* __restrict__ g,
