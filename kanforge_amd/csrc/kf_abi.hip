@@ -190,6 +190,7 @@ int g_rb(int fw) { return fw <= 6 ? 128 : 64; }
 
 struct WsP {
   int cfg, ntb;
+  bool p8;  // bf16 Chebyshev with 7 or 8 features: p8_kernel (256 x (8 x 48) tiles)
   int64_t INP, OUTP;
   size_t cfmt, gpad, total;
 };
@@ -203,7 +204,8 @@ WsP ws_p(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
   WsP w;
   w.cfg = fw_index(b->n_t);
   w.ntb = 2 * FW_LIST[w.cfg];
-  w.INP = round_up(n_in, 32);
+  w.p8 = b->kind == KF_KIND_CHEB && dtype == KF_BF16 && w.ntb == 8;
+  w.INP = round_up(n_in, w.p8 ? 96 : 32);  // 96: whole tiles of p8_kernel (48) and p_dma_kernel (32)
   w.OUTP = round_up(n_out, p_uses_dma(w.cfg) ? p_stage_cols(dtype) : 32);
   w.cfmt = align256((size_t)w.ntb * w.INP * w.OUTP * elt_size(dtype));
   w.gpad = p_uses_dma(w.cfg) && p_needs_gpad(n_out, dtype) ? align256((size_t)batch * w.OUTP * elt_size(dtype)) : 0;
@@ -477,14 +479,17 @@ int launch_p_dma_kind(const WsP& L, hipStream_t s, const KBasis& kb, int64_t bat
   return check_launch("P");
 }
 
+template <int TN>
 int launch_p8(const WsP& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, const void* x, const void* g,
               int gstride, const void* cfmt, void* p) {
-  const size_t lds_ops = (size_t)3 * 512 * 64, lds_epi = (size_t)8 * 128 * 33 * 4;
+  constexpr int TI = 16 * TN, RPASS = TN == 2 ? 128 : 64;
+  const size_t lds_ops = (size_t)2 * (256 + 8 * TI) * 64, lds_epi = (size_t)8 * RPASS * (TI + 1) * 4;
   const size_t lds = lds_ops > lds_epi ? lds_ops : lds_epi;
-  auto kern = p8_kernel<KF_KIND_CHEB>;
+  auto kern = p8_kernel<KF_KIND_CHEB, TN>;
+  if (L.INP % TI) return fail(KF_EINVAL, "P: workspace layout not aligned");
   if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return fail(KF_ELAUNCH, "P: cannot reserve %zu bytes of LDS", lds);
-  const int n_m = (int)((batch + 255) / 256), n_n = (int)(L.INP / 32);
+  const int n_m = (int)((batch + 255) / 256), n_n = (int)(L.INP / TI);
   hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(512), lds, s, kb, (int)batch, (int)n_in, (int)L.INP, (int)L.OUTP,
                      (const bf16*)x, (const bf16*)g, gstride, (const bf16*)cfmt, (bf16*)p);
   return check_launch("P");
@@ -527,8 +532,7 @@ int run_P(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
       gstride = (int)L.OUTP;
     }
     // 7 or 8 Chebyshev features in bf16: the two-waves-per-SIMD kernel
-    if (std::is_same<T, bf16>::value && kb.kind == KF_KIND_CHEB && L.ntb == 8 && !h)
-      return launch_p8(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p);
+    if (L.p8 && !h) return launch_p8<3>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p);
     switch (L.cfg) {
       case 0: return launch_p_dma<T, 2>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p, h);
       case 1: return launch_p_dma<T, 3>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p, h);

@@ -1389,62 +1389,65 @@ __global__ __launch_bounds__(256) void p_dma_kernel(KBasis bs, int B, int IN, in
 }
 
 // P for bf16 plans with 7 or 8 kernel features: the GEMM
-//   H_j[b, i] = sum_o g[b, o] CfmT[j][i][o]   (columns n = j * 32 + i of a 32-input tile)
+//   H_j[b, i] = sum_o g[b, o] CfmT[j][i][o]   (columns n = j * TI + i of a TI-input tile)
 // on 8 waves, two per SIMD, so that one wave's waits and barrier arrivals are covered by the
-// other's MFMAs. Workgroup tile 256 rows x (8 features x 32 inputs); wave (wm, wn) = (wave & 1,
-// wave >> 1) owns rows 128 wm .. +127 and features 2 wn, 2 wn + 1 (4 x 2 accumulator tiles). A
-// stage is 64 bytes of o for the 256 rows of g and the 256 rows of CfmT, copied global -> LDS by
-// all waves into a ring of 3 buffers (copies two stages ahead, one barrier per stage); rows are
-// dense 64 bytes with their 16-byte chunks XOR-swizzled by bits 2..3 of the row. Epilogue, one
-// half of the rows at a time: the feature sums H_j go to LDS and every thread forms
+// other's MFMAs. Workgroup tile 256 rows x (8 features x TI = 16 TN inputs); wave (wm, wn) =
+// (wave & 1, wave >> 1) owns rows 128 wm .. +127 and column fragments TN wn .. +TN - 1 (4 x TN
+// accumulator tiles). A stage is 64 bytes of o for the 256 rows of g and the 128 TN rows of
+// CfmT, copied global -> LDS by all waves into two buffers (one barrier per stage); rows are
+// dense 64 bytes with their 16-byte chunks XOR-swizzled by bits 2..3 of the row. Epilogue, in
+// passes of RPASS rows: the feature sums H_j go to LDS and every thread forms
 // p[b, i] = sum_j f_j(x[b, i]) H_j[b, i] for (row, input) pairs, the features computed once per
 // pair.
-template <int KIND>
+template <int KIND, int TN>
 __global__ __launch_bounds__(512) void p8_kernel(KBasis bs, int B, int IN, int INP, int OUTP,
                                                  const bf16* __restrict__ x, const bf16* __restrict__ g, int gstride,
                                                  const bf16* __restrict__ cfmt, bf16* __restrict__ p) {
-  constexpr int BM = 256, NF = 8, BN = NF * 32, SA = BM * 64, SS = (BM + BN) * 64, NBUF = 3, RP = 33;
-  static_assert(NBUF * SS <= 160 * 1024 && NF * 128 * RP * 4 <= 160 * 1024, "stages and the epilogue fit in LDS");
+  constexpr int BM = 256, NF = 8, TI = 16 * TN, BN = NF * TI, SA = BM * 64, SS = (BM + BN) * 64, NBUF = 2;
+  constexpr int RP = TI + 1, RPASS = TN == 2 ? 128 : 64, NBLK = (BM + BN) / 16, BPW = NBLK / 8;
+  static_assert(BPW * 8 == NBLK, "copy blocks divide over the waves");
+  static_assert(NBUF * SS <= 160 * 1024 && NF * RPASS * RP * 4 <= 160 * 1024, "stages and the epilogue fit in LDS");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];  // [NBUF][SS], later the sums
 
-  const int n_m = (B + BM - 1) / BM, n_n = INP / 32;
+  const int n_m = (B + BM - 1) / BM, n_n = INP / TI;
   int tm_, tn_;
   xcd_tile_grouped(blockIdx.x, n_m, n_n, 8, tm_, tn_);
-  const int b0 = tm_ * BM, i0 = tn_ * 32;
+  const int b0 = tm_ * BM, i0 = tn_ * TI;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave & 1, wn = wave >> 1;
   const int h = lane >> 5, l32 = lane & 31;
   const int S = OUTP / 32;
 
-  f32x16 acc[4][2];
+  f32x16 acc[4][TN];
 #pragma unroll
   for (int a = 0; a < 4; ++a)
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < TN; ++t)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[a][t][r] = 0.f;
 
-  // copies: wave w fills blocks 4 w .. 4 w + 3 of the stage's 32 (16 rows of 64 bytes; rows
-  // 0..255 from g, 256..511 from CfmT); lane l fills chunk l % 4 of row l / 4, i.e. global
-  // chunk (l % 4) ^ ((row >> 2) & 3). Rows past the batch repeat row B - 1 (never stored).
-  const bf16* src[4];
+  // copies: wave w fills blocks BPW w .. BPW w + BPW - 1 of the stage's NBLK (16 rows of 64
+  // bytes; rows 0..255 from g, the rest from CfmT); lane l fills chunk l % 4 of row l / 4,
+  // i.e. global chunk (l % 4) ^ ((row >> 2) & 3). Rows past the batch repeat row B - 1 (never
+  // stored).
+  const bf16* src[BPW];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int row = (4 * wave + k) * 16 + (lane >> 2);
+  for (int k = 0; k < BPW; ++k) {
+    const int row = (BPW * wave + k) * 16 + (lane >> 2);
     const int c = (lane & 3) ^ ((row >> 2) & 3);
     if (row < BM) {
       const int b = b0 + row < B ? b0 + row : B - 1;
       src[k] = g + (size_t)b * gstride + c * 8;
     } else {
       const int rr = row - BM;
-      src[k] = cfmt + ((size_t)(rr / 32) * INP + i0 + rr % 32) * OUTP + c * 8;
+      src[k] = cfmt + ((size_t)(rr / TI) * INP + i0 + rr % TI) * OUTP + c * 8;
     }
   }
   auto copy_stage = [&](int st) {
-    unsigned char* dst = smem + (st % NBUF) * SS + 4 * wave * 1024;
+    unsigned char* dst = smem + (st % NBUF) * SS + BPW * wave * 1024;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) lds_dma16(src[k] + (size_t)st * 32, dst + k * 1024);
+    for (int k = 0; k < BPW; ++k) lds_dma16(src[k] + (size_t)st * 32, dst + k * 1024);
   };
   const int sw = (l32 >> 2) & 3;
   auto mma_stage = [&](int st) {
@@ -1452,55 +1455,53 @@ __global__ __launch_bounds__(512) void p8_kernel(KBasis bs, int B, int IN, int I
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       const int co = 16 * ((2 * ks + h) ^ sw);
-      u32x4 fa[4], fb[2];
+      u32x4 fa[4], fb[TN];
 #pragma unroll
       for (int a = 0; a < 4; ++a) fa[a] = lds_read16(base + (wm * 128 + a * 32 + l32) * 64 + co);
 #pragma unroll
-      for (int t = 0; t < 2; ++t) fb[t] = lds_read16(base + SA + (wn * 64 + t * 32 + l32) * 64 + co);
+      for (int t = 0; t < TN; ++t) fb[t] = lds_read16(base + SA + ((TN * wn + t) * 32 + l32) * 64 + co);
 #pragma unroll
       for (int a = 0; a < 4; ++a)
 #pragma unroll
-        for (int t = 0; t < 2; ++t) mma32<bf16>(acc[a][t], fa[a], fb[t]);
+        for (int t = 0; t < TN; ++t) mma32<bf16>(acc[a][t], fa[a], fb[t]);
     }
   };
 
   copy_stage(0);
-  if (S > 1) copy_stage(1);
   for (int s = 0; s < S; ++s) {
-    // stage s has landed once at most the copies of stage s + 1 are in flight
-    if (s + 1 < S)
-      vmem_wait<4>();
-    else
-      vmem_wait<0>();
-    lds_wait();  // this wave's reads of stage s - 1, whose buffer the copies below refill
+    vmem_wait<0>();  // this wave's copies of stage s
+    lds_wait();      // this wave's reads of stage s - 1, whose buffer the copies below refill
     __builtin_amdgcn_s_barrier();
-    if (s + 2 < S) copy_stage(s + 2);
+    if (s + 1 < S) copy_stage(s + 1);
     mma_stage(s);
   }
   lds_wait();
 
-  float* red = reinterpret_cast<float*>(smem);  // [NF][128][RP]
+  float* red = reinterpret_cast<float*>(smem);  // [NF][RPASS][RP]
 #pragma unroll
-  for (int hr = 0; hr < 2; ++hr) {
+  for (int ps = 0; ps < BM / RPASS; ++ps) {
     __syncthreads();
-    if (wm == hr) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+    for (int a = 0; a < 4; ++a) {
+      if ((wm * 128 + a * 32) / RPASS != ps) continue;
+      const int rbase = (wm * 128 + a * 32) % RPASS;
 #pragma unroll
-        for (int a = 0; a < 4; ++a)
+      for (int t = 0; t < TN; ++t) {
+        const int col = (TN * wn + t) * 32 + l32, f = col / TI, il = col % TI;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) red[((2 * wn + t) * 128 + a * 32 + acc_row(r, lane)) * RP + l32] = acc[a][t][r];
+        for (int r = 0; r < 16; ++r) red[(f * RPASS + rbase + acc_row(r, lane)) * RP + il] = acc[a][t][r];
+      }
     }
     __syncthreads();
-    for (int e = tid; e < 128 * 32; e += 512) {
-      const int row = e / 32, il = e % 32;
-      const int b = b0 + hr * 128 + row, i = i0 + il;
+    for (int e = tid; e < RPASS * TI; e += 512) {
+      const int row = e / TI, il = e % TI;
+      const int b = b0 + ps * RPASS + row, i = i0 + il;
       if (b < B && i < IN) {
         float f[NF];
         kind_features<KIND, NF>(to_f32(x[(size_t)b * IN + i]), 1.f, i, bs, f);
         float sum = 0.f;
 #pragma unroll
-        for (int q = 0; q < NF; ++q) sum = fmaf(red[(q * 128 + row) * RP + il], f[q], sum);
+        for (int q = 0; q < NF; ++q) sum = fmaf(red[(q * RPASS + row) * RP + il], f[q], sum);
         p[(size_t)b * IN + i] = from_f32<bf16>(sum);
       }
     }
