@@ -276,9 +276,16 @@ int launch_permute(const KBasis& kb, int64_t n_out, int64_t n_in, int64_t OUTP, 
   for (int j = 0; j < KF_MAX_NT; ++j)
     for (int k = 0; k < KF_MAX_K; ++k) ft.v[j][k] = k < kb.K && j < kb.n_t ? kb.fold[k * KF_MAX_NT + j] : 0.f;
   const int vin = n_in % 16 == 0 && rows_vec<T>(n_in * kb.K, c);
-  auto kern = fmt == kPermFMT ? permute_coef_kernel<T, kPermFMT>
-              : fmt == kPermC16 ? permute_coef_kernel<T, kPermC16>
-                                : permute_coef_kernel<T, kPermFM>;
+  auto pick = [&](auto kb_tag) {
+    constexpr int KB = decltype(kb_tag)::value;
+    return fmt == kPermFMT ? permute_coef_kernel<T, kPermFMT, KB>
+           : fmt == kPermC16 ? permute_coef_kernel<T, kPermC16, KB>
+                             : permute_coef_kernel<T, kPermFM, KB>;
+  };
+  auto kern = kb.K <= 4    ? pick(std::integral_constant<int, 4>())
+              : kb.K <= 9  ? pick(std::integral_constant<int, 9>())
+              : kb.K <= 12 ? pick(std::integral_constant<int, 12>())
+                           : pick(std::integral_constant<int, KF_MAX_K>());
   hipLaunchKernelGGL(kern, grid, dim3(kThreads), lds, s, ft, kb.K, kb.n_t, (int)n_out, (int)n_in, (int)OUTP, (int)INP,
                      n_feat, j_first, vin, (const T*)c, (T*)out, part0);
   return check_launch("permute_coef");
@@ -388,7 +395,7 @@ int run_F(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
     int rc = launch_permute<T>(kb, n_out, n_in, L.OUTP, L.INP, L.n_tp, c, cfm, kPermC16, s, L.skip0 ? 1 : 0, part0);
     if (rc) return rc;
     if (L.skip0) {
-      hipLaunchKernelGGL(sum_parts_kernel, dim3((unsigned)((L.OUTP + 31) / 32)), dim3(kThreads), 0, s,
+      hipLaunchKernelGGL(sum_parts_kernel, dim3((unsigned)((L.OUTP + 7) / 8)), dim3(kThreads), 0, s,
                          (int)(L.INP / 16), (int)L.OUTP, part0, ysum);
       rc = check_launch("sum_parts");
       if (rc) return rc;
@@ -630,7 +637,7 @@ int run_G(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
   int rc = check_launch("transpose");
   if (rc) return rc;
   if (L.skip0) {
-    hipLaunchKernelGGL(sum_parts_kernel, dim3((unsigned)((L.OUTP + 31) / 32)), dim3(kThreads), 0, s,
+    hipLaunchKernelGGL(sum_parts_kernel, dim3((unsigned)((L.OUTP + 7) / 8)), dim3(kThreads), 0, s,
                        (int)((L.BP + 63) / 64), (int)L.OUTP, part, colsum);
     rc = check_launch("sum_parts");
     if (rc) return rc;

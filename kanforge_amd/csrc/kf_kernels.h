@@ -39,7 +39,7 @@ constexpr int kPermTS = 36;
 struct KFoldT {
   float v[KF_MAX_NT][KF_MAX_K];
 };
-template <typename T, int FMT>
+template <typename T, int FMT, int KB>  // KB >= K: basis functions the fold loop runs over
 __global__ __launch_bounds__(kThreads) void permute_coef_kernel(KFoldT ft, int K, int n_t_fold, int OUT, int IN,
                                                                 int OUTP, int INP, int n_feat, int j_first, int vin,
                                                                 const T* __restrict__ c, T* __restrict__ out,
@@ -72,13 +72,13 @@ __global__ __launch_bounds__(kThreads) void permute_coef_kernel(KFoldT ft, int K
   }
   __syncthreads();
   // thread (ol = t / 16 + 16 rep, il = t % 16): the K coefficients of one edge
-  float cv[2][KF_MAX_K];
+  float cv[2][KB];
   const int il = t % 16;
 #pragma unroll
   for (int rep = 0; rep < 2; ++rep) {
     const int ol = t / 16 + rep * 16;
 #pragma unroll
-    for (int k = 0; k < KF_MAX_K; ++k) cv[rep][k] = k < K ? smem[ol * RS + il * K + k] : 0.f;
+    for (int k = 0; k < KB; ++k) cv[rep][k] = k < K ? smem[ol * RS + il * K + k] : 0.f;
   }
   __syncthreads();
   float* tile = smem;
@@ -89,7 +89,7 @@ __global__ __launch_bounds__(kThreads) void permute_coef_kernel(KFoldT ft, int K
     for (int rep = 0; rep < 2; ++rep) {
       float acc = 0.f;
 #pragma unroll
-      for (int k = 0; k < KF_MAX_K; ++k) acc = fmaf(cv[rep][k], fj[k], acc);
+      for (int k = 0; k < KB; ++k) acc = fmaf(cv[rep][k], fj[k], acc);
       tile[(j * 16 + il) * kPermTS + t / 16 + rep * 16] = live ? acc : 0.f;
     }
   }
@@ -130,30 +130,30 @@ __global__ __launch_bounds__(kThreads) void permute_coef_kernel(KFoldT ft, int K
 }
 
 // sums[o] = sum over p < n_parts of part[p][o]: the per-output constant of a
-// left-out feature 0 (fixed summation order). Block: 32 outputs x 8 groups
-// of parts, reduced through LDS.
+// left-out feature 0 (fixed summation order). Block: 8 outputs x 32 groups of
+// parts (all loads of a thread in flight at once), reduced through LDS.
 __global__ __launch_bounds__(kThreads) void sum_parts_kernel(int n_parts, int n, const float* __restrict__ part,
                                                              float* __restrict__ sums) {
-  __shared__ float red[8][33];
-  const int ol = threadIdx.x % 32, pg = threadIdx.x / 32;
-  const int o = blockIdx.x * 32 + ol;
+  __shared__ float red[32][9];
+  const int ol = threadIdx.x % 8, pg = threadIdx.x / 8;
+  const int o = blockIdx.x * 8 + ol;
   float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
   if (o < n) {
     int q = pg;
-    for (; q + 24 < n_parts; q += 32) {
+    for (; q + 96 < n_parts; q += 128) {
       s0 += part[(size_t)q * n + o];
-      s1 += part[(size_t)(q + 8) * n + o];
-      s2 += part[(size_t)(q + 16) * n + o];
-      s3 += part[(size_t)(q + 24) * n + o];
+      s1 += part[(size_t)(q + 32) * n + o];
+      s2 += part[(size_t)(q + 64) * n + o];
+      s3 += part[(size_t)(q + 96) * n + o];
     }
-    for (; q < n_parts; q += 8) s0 += part[(size_t)q * n + o];
+    for (; q < n_parts; q += 32) s0 += part[(size_t)q * n + o];
   }
   red[pg][ol] = (s0 + s1) + (s2 + s3);
   __syncthreads();
   if (pg == 0 && o < n) {
     float tot = 0.f;
 #pragma unroll
-    for (int g = 0; g < 8; ++g) tot += red[g][ol];
+    for (int g = 0; g < 32; ++g) tot += red[g][ol];
     sums[o] = tot;
   }
 }
