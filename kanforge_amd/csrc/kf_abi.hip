@@ -394,19 +394,16 @@ int run_F(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
     float* ysum = L.skip0 ? (float*)(base + L.cfm + L.z + L.wz + L.phi + L.part0) : nullptr;
     int rc = launch_permute<T>(kb, n_out, n_in, L.OUTP, L.INP, L.n_tp, c, cfm, kPermC16, s, L.skip0 ? 1 : 0, part0);
     if (rc) return rc;
-    if (L.skip0) {
-      hipLaunchKernelGGL(sum_parts_kernel, dim3((unsigned)((L.OUTP + 7) / 8)), dim3(kThreads), 0, s,
-                         (int)(L.INP / 16), (int)L.OUTP, part0, ysum);
-      rc = check_launch("sum_parts");
-      if (rc) return rc;
-    }
     if (L.INP % 16 || L.BP % 32) return fail(KF_EINVAL, "F: workspace layout not aligned");
     long n = (L.INP + 63) / 64 * L.BP * (64 / (16 / (long)sizeof(T)));
     long blocks = (n + kThreads - 1) / kThreads;
     if (blocks > 65535 * 4) blocks = 65535 * 4;
+    // the same launch totals the feature-0 partial sums in blocks of its own
+    const long sblocks = L.skip0 ? (L.OUTP + 7) / 8 : 0;
     const int vin = rows_vec<T>(n_in, x) && rows_vec<T>(n_in, w);
-    hipLaunchKernelGGL(zmapc_kernel<T>, dim3((unsigned)blocks), dim3(kThreads), 0, s, (int)batch, (int)n_in,
-                       (int)L.BP, (int)L.INP, kb.input_map, vin, (const T*)x, (const T*)w, z, wz);
+    hipLaunchKernelGGL(zmapc_kernel<T>, dim3((unsigned)(blocks + sblocks)), dim3(kThreads), 0, s, (int)batch,
+                       (int)n_in, (int)L.BP, (int)L.INP, kb.input_map, vin, (const T*)x, (const T*)w, z, wz,
+                       (int)blocks, (int)(L.INP / 16), (int)L.OUTP, part0, ysum);
     rc = check_launch("zmapc");
     if (rc) return rc;
     if (weighted) return launch_f_rega<true, false>(L, batch, n_out, z, wz, cfm, nullptr, y, s);
@@ -636,17 +633,14 @@ int run_G(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
                      (int)rows_vec<T>(n_out, g), (const T*)g, (T*)gt, part);
   int rc = check_launch("transpose");
   if (rc) return rc;
-  if (L.skip0) {
-    hipLaunchKernelGGL(sum_parts_kernel, dim3((unsigned)((L.OUTP + 7) / 8)), dim3(kThreads), 0, s,
-                       (int)((L.BP + 63) / 64), (int)L.OUTP, part, colsum);
-    rc = check_launch("sum_parts");
-    if (rc) return rc;
-  }
   if (cheb) {
-    dim3 zg((unsigned)((L.INP + 63) / 64), (unsigned)((L.BP + 63) / 64));
-    hipLaunchKernelGGL(zmapT_kernel<T>, zg, dim3(kThreads), (size_t)(wt ? 2 : 1) * 64 * 65 * sizeof(float), s, (int)batch, (int)n_in, (int)L.BP, (int)L.INP,
-                       kb.input_map, (int)(rows_vec<T>(n_in, x) && rows_vec<T>(n_in, w)), (const T*)x, (const T*)w,
-                       zt, wt);
+    // block rows past the batch tiles total the column sums of g (skip0 implies cheb)
+    const unsigned gx = (unsigned)((L.INP + 63) / 64), sblocks = L.skip0 ? (unsigned)((L.OUTP + 7) / 8) : 0u;
+    dim3 zg(gx, (unsigned)((L.BP + 63) / 64) + (sblocks + gx - 1) / gx);
+    hipLaunchKernelGGL(zmapT_kernel<T>, zg, dim3(kThreads), (size_t)(wt ? 2 : 1) * 64 * 65 * sizeof(float), s,
+                       (int)batch, (int)n_in, (int)L.BP, (int)L.INP, kb.input_map,
+                       (int)(rows_vec<T>(n_in, x) && rows_vec<T>(n_in, w)), (const T*)x, (const T*)w, zt, wt,
+                       (int)((L.BP + 63) / 64), (int)L.OUTP, part, colsum);
     rc = check_launch("zmapT");
     if (rc) return rc;
     if (L.g96) {

@@ -129,14 +129,15 @@ __global__ __launch_bounds__(kThreads) void permute_coef_kernel(KFoldT ft, int K
   }
 }
 
-// sums[o] = sum over p < n_parts of part[p][o]: the per-output constant of a
-// left-out feature 0 (fixed summation order). Block: 8 outputs x 32 groups of
-// parts (all loads of a thread in flight at once), reduced through LDS.
-__global__ __launch_bounds__(kThreads) void sum_parts_kernel(int n_parts, int n, const float* __restrict__ part,
-                                                             float* __restrict__ sums) {
+// sums[o] = sum over p < n_parts of part[p][o] for the 8 outputs of block blk:
+// the per-output constant of a left-out feature 0 (fixed summation order); 32
+// groups of parts (all loads of a thread in flight at once), reduced through
+// LDS. Run by extra blocks of the tanh-map prepass launches.
+__device__ __forceinline__ void sum_parts_block(int blk, int n_parts, int n, const float* __restrict__ part,
+                                                float* __restrict__ sums) {
   __shared__ float red[32][9];
   const int ol = threadIdx.x % 8, pg = threadIdx.x / 8;
-  const int o = blockIdx.x * 8 + ol;
+  const int o = blk * 8 + ol;
   float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
   if (o < n) {
     int q = pg;
@@ -263,13 +264,20 @@ __global__ __launch_bounds__(kThreads) void zmap_kernel(int B, int IN, int BP, i
 // contiguous bytes. Lanes run along 64-input row segments (16-byte loads
 // when vin: IN a multiple of the vector width, x and w aligned), then along
 // rows, so each chunk's stores of a wave are contiguous.
+// Blocks from nzb on total partial sums instead (sum_parts_block), when part is given.
 template <typename T>
 __global__ __launch_bounds__(kThreads) void zmapc_kernel(int B, int IN, int BP, int INP, int input_map, int vin,
                                                          const T* __restrict__ x, const T* __restrict__ w,
-                                                         float* __restrict__ zc, float* __restrict__ wc) {
+                                                         float* __restrict__ zc, float* __restrict__ wc, int nzb,
+                                                         int n_parts, int n_sums, const float* __restrict__ part,
+                                                         float* __restrict__ sums) {
+  if ((int)blockIdx.x >= nzb) {
+    sum_parts_block(blockIdx.x - nzb, n_parts, n_sums, part, sums);
+    return;
+  }
   constexpr int VW = 16 / (int)sizeof(T), LPR = 64 / VW;
   const long n = (long)((INP + 63) / 64) * BP * LPR;
-  for (long e = blockIdx.x * (long)kThreads + threadIdx.x; e < n; e += (long)gridDim.x * kThreads) {
+  for (long e = blockIdx.x * (long)kThreads + threadIdx.x; e < n; e += (long)nzb * kThreads) {
     const int q = (int)(e % LPR), b = (int)((e / LPR) % BP), seg = (int)(e / ((long)LPR * BP));
     const int i = seg * 64 + q * VW;
     if (i >= INP) continue;
@@ -540,10 +548,19 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void f_kernel(int B, int OUT
 // G kernel generates features with the batch (its reduction dimension)
 // contiguous. 64x64 tiles through LDS; 16-byte loads when vin (IN a multiple
 // of the vector width, x and w aligned), 16-byte stores (BP a multiple of 32).
+// Block rows past BP / 64 total partial sums instead (sum_parts_block), when part is given.
 template <typename T>
 __global__ __launch_bounds__(kThreads) void zmapT_kernel(int B, int IN, int BP, int INP, int input_map, int vin,
                                                          const T* __restrict__ x, const T* __restrict__ w,
-                                                         float* __restrict__ zt, float* __restrict__ wt) {
+                                                         float* __restrict__ zt, float* __restrict__ wt, int n_parts,
+                                                         int n_sums, const float* __restrict__ part,
+                                                         float* __restrict__ sums) {
+  const int nby = (BP + 63) / 64;
+  if ((int)blockIdx.y >= nby) {
+    const int blk = (blockIdx.y - nby) * gridDim.x + blockIdx.x;
+    if (blk * 8 < n_sums) sum_parts_block(blk, n_parts, n_sums, part, sums);
+    return;
+  }
   constexpr int VW = 16 / (int)sizeof(T), LPR = 64 / VW, RPI = kThreads / LPR;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];  // tz [64][65], tw [64][65] when wt
   float* tz = reinterpret_cast<float*>(smem);
