@@ -355,14 +355,18 @@ int launch_f_rega(const WsF& L, int64_t batch, int64_t n_out, const float* zc, c
                   const float* ysum, void* y, hipStream_t s) {
   const int n_m = (int)(L.BP / RA_BM), n_n = (int)(L.OUTP / RA_BN);
   // RA_NBUF stage buffers of 2 features, z (and w) of two chunks
-  const size_t lds = (size_t)RA_NBUF * 2 * RA_BN * 32 + (size_t)(HAS_W ? 4 : 2) * RA_BM * 64;
+  // (reused by the epilogue's bf16 staging of the output tile, RA_BM rows of RA_BN * 2 + 16 bytes)
+  const size_t lds_ops = (size_t)RA_NBUF * 2 * RA_BN * 32 + (size_t)(HAS_W ? 4 : 2) * RA_BM * 64;
+  const size_t lds_epi = (size_t)RA_BM * (RA_BN * 2 + 16);
+  const size_t lds = lds_ops > lds_epi ? lds_ops : lds_epi;
+  const int vout = n_out % 8 == 0 && aligned16(y);
   auto kern = L.n_tp == 9   ? f_rega_kernel<HAS_W, 9, RA_TM, RA_TN, RA_NBUF, SKIP0>
               : L.n_tp == 8 ? f_rega_kernel<HAS_W, 8, RA_TM, RA_TN, RA_NBUF, SKIP0>
                             : f_rega_kernel<HAS_W, 0, RA_TM, RA_TN, RA_NBUF, SKIP0>;
   if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return fail(KF_ELAUNCH, "F: cannot reserve %zu bytes of LDS", lds);
   hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(256), lds, s, (int)batch, (int)n_out, (int)L.OUTP, (int)L.BP,
-                     (int)(L.INP / 16), L.n_tp, zc, wc, (const bf16*)cfm, ysum, (bf16*)y);
+                     (int)(L.INP / 16), L.n_tp, zc, wc, (const bf16*)cfm, ysum, (bf16*)y, vout);
   return check_launch("F");
 }
 
@@ -598,7 +602,9 @@ int launch_g_ws(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, in
 template <bool SKIP0>
 int launch_g96(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out,
                const float* zt, const float* wt, const void* gt, const float* colsum, void* dc) {
-  const size_t lds_ops = (size_t)2 * (192 * 64 + 8 * 48 * 64), lds_red = (size_t)(8 * 96 * 49 + 96) * 4;
+  const size_t lds_ops = (size_t)2 * (192 * 64 + 8 * 48 * 64);
+  const size_t lds_red = (size_t)(8 * 32 * 49 + 32) * 4 + (size_t)32 * 48 * kb.K * 2;  // sums, output rows
+  const int vout = (n_in * kb.K * 2) % 16 == 0 && aligned16(dc);
   const size_t lds = lds_ops > lds_red ? lds_ops : lds_red;
   auto kern = g96_kernel<SKIP0>;
   if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
@@ -611,7 +617,7 @@ int launch_g96(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, int
     for (int f = 0; f < 8; ++f) fg.v[k][1 + f] = k < kb.K && f < n_run ? kb.fold[k * KF_MAX_NT + f + skip] : 0.f;
   }
   hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(512), lds, s, fg, kb.K, n_run, (int)batch, (int)n_in, (int)n_out,
-                     (int)L.BP, (int)L.OUTP, (int)L.INP, zt, wt, (const bf16*)gt, colsum, (bf16*)dc);
+                     (int)L.BP, (int)L.OUTP, (int)L.INP, zt, wt, (const bf16*)gt, colsum, (bf16*)dc, vout);
   return check_launch("G");
 }
 

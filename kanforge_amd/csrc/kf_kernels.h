@@ -993,7 +993,7 @@ template <bool HAS_W, int NT, int TM, int TN, int NBUF, bool SKIP0>
 __global__ __launch_bounds__(256) void f_rega_kernel(int B, int OUT, int OUTP, int BP, int n_chunks, int n_tp,
                                                      const float* __restrict__ zc, const float* __restrict__ wc,
                                                      const bf16* __restrict__ cfm, const float* __restrict__ ysum,
-                                                     bf16* __restrict__ y) {
+                                                     bf16* __restrict__ y, int vout) {
   constexpr int WM = TM * 32, BM = 4 * WM, BN = TN * 32;
   constexpr int FB = BN * 32;      // one feature of a stage (dense 32-byte rows)
   constexpr int SB = 2 * FB;       // one stage
@@ -1218,18 +1218,40 @@ __global__ __launch_bounds__(256) void f_rega_kernel(int B, int OUT, int OUTP, i
     }
   }
 
+  // epilogue: each wave's 32 TM x 32 TN tile goes to LDS as bf16 rows (stride EST bytes) over
+  // the stage buffers, once every copy has landed and every wave is done with them, then out
+  // with 16-byte stores when the rows are whole and aligned (vout), else element by element
+  constexpr int EST = BN * 2 + 16;
+  vmem_wait<0>();
+  __syncthreads();
+  unsigned char* est = smem + wave * WM * EST;
 #pragma unroll
-  for (int a = 0; a < TM; ++a)
+  for (int t = 0; t < TN; ++t) {
+    const int o = o0 + t * 32 + l32;
+    const float add = SKIP0 && o < OUT ? ysum[o] : 0.f;
 #pragma unroll
-    for (int t = 0; t < TN; ++t) {
-      const int o = o0 + t * 32 + l32;
-      const float add = SKIP0 && o < OUT ? ysum[o] : 0.f;
+    for (int a = 0; a < TM; ++a)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int b = b0 + wm * WM + a * 32 + acc_row(r, lane);
-        if (b < B && o < OUT) y[(size_t)b * OUT + o] = from_f32<bf16>(acc[a][t][r] + add);
-      }
+      for (int r = 0; r < 16; ++r)
+        *reinterpret_cast<bf16*>(est + (a * 32 + acc_row(r, lane)) * EST + (t * 32 + l32) * 2) =
+            from_f32<bf16>(acc[a][t][r] + add);
+  }
+  if (vout) {
+    constexpr int CPR = BN / 8;  // 16-byte chunks per row
+#pragma unroll 4
+    for (int e = lane; e < WM * CPR; e += 64) {
+      const int row = e / CPR, ch = e % CPR;
+      const int b = b0 + wm * WM + row, o = o0 + ch * 8;
+      const u32x4 v = lds_read16(est + row * EST + ch * 16);
+      if (b < B && o < OUT) gstore16(y + (size_t)b * OUT + o, v);
     }
+  } else {
+    for (int e = lane; e < WM * BN; e += 64) {
+      const int row = e / BN, col = e % BN;
+      const int b = b0 + wm * WM + row, o = o0 + col;
+      if (b < B && o < OUT) y[(size_t)b * OUT + o] = *reinterpret_cast<const bf16*>(est + row * EST + col * 2);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1564,7 +1586,7 @@ template <bool SKIP0>
 __global__ __launch_bounds__(512) void g96_kernel(KFoldG fg, int K, int n_run, int B, int IN, int OUT, int BP, int OUTP, int INP,
                                                   const float* __restrict__ zt, const float* __restrict__ wt,
                                                   const bf16* __restrict__ gt, const float* __restrict__ colsum,
-                                                  bf16* __restrict__ dc) {
+                                                  bf16* __restrict__ dc, int vout) {
   constexpr int TO = 192, TI = 48, NF = 8;
   constexpr int SA = TO * 64, SBF = NF * TI * 64, SS = SA + SBF;  // bytes of a stage
   constexpr int RP = TI + 1;                                         // fold buffer row pitch
@@ -1759,42 +1781,59 @@ __global__ __launch_bounds__(512) void g96_kernel(KFoldG fg, int K, int n_run, i
     __builtin_amdgcn_s_barrier();
   }
 
-  // epilogue, one half of the outputs at a time: red[f][o][RP] feature sums, then the fold,
-  // one (o, i) edge per thread and step (the feature sums in registers, the fold row k in
-  // scalar registers)
-  float* red = reinterpret_cast<float*>(smem);
-  float* csl = red + NF * 96 * RP;  // column sums of g for the half's outputs
+  // epilogue, 32 outputs at a time (passes over the halves wm and their row blocks a):
+  // red[f][o][RP] feature sums, then the fold, one (o, i) edge per thread and step (the feature
+  // sums in registers, the fold row k in scalar registers) into bf16 rows of the tile's
+  // outputs in LDS, then out with 16-byte stores when the rows are whole and aligned (vout)
+  constexpr int RPA = 32;
+  float* red = reinterpret_cast<float*>(smem);                         // [NF][RPA][RP]
+  float* csl = red + NF * RPA * RP;                                    // column sums of g
+  unsigned char* stg = reinterpret_cast<unsigned char*>(csl + RPA);    // [RPA][TI K] bf16
+  const int rowb = TI * K * 2;                                         // a multiple of 16
+  const bool vtile = vout && i0 + TI <= IN;
 #pragma unroll
-  for (int half = 0; half < 2; ++half) {
+  for (int pass = 0; pass < 6; ++pass) {
+    const int half = pass / 3, ap = pass % 3, ob = o0 + half * 96 + ap * 32;
     __syncthreads();
     if (wm == half) {
 #pragma unroll
       for (int c = 0; c < 3; ++c) {
         const int col = (3 * wn + c) * 32 + l32, f = col / TI, il = col % TI;
 #pragma unroll
-        for (int a = 0; a < 3; ++a)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) red[(f * 96 + a * 32 + acc_row(r, lane)) * RP + il] = acc[a][c][r];
+        for (int r = 0; r < 16; ++r) red[(f * RPA + acc_row(r, lane)) * RP + il] = acc[ap][c][r];
       }
     }
-    if (SKIP0 && tid < 96) csl[tid] = o0 + half * 96 + tid < OUT ? colsum[o0 + half * 96 + tid] : 0.f;
+    if (SKIP0 && tid < RPA) csl[tid] = ob + tid < OUT ? colsum[ob + tid] : 0.f;
     __syncthreads();
-    for (int e = tid; e < 96 * TI; e += 512) {
+    for (int e = tid; e < RPA * TI; e += 512) {
       const int ol = e / TI, il = e - ol * TI;
-      const int o = o0 + half * 96 + ol, i = i0 + il;
-      if (o < OUT && i < IN) {
-        float v[NF];
+      float v[NF];
 #pragma unroll
-        for (int f = 0; f < NF; ++f) v[f] = f < n_run ? red[(f * 96 + ol) * RP + il] : 0.f;
-        const float cs = SKIP0 ? csl[ol] : 0.f;
-        bf16* out = dc + ((size_t)o * IN + i) * K;
-        for (int k = 0; k < K; ++k) {
-          const float* fk = fg.v[k];
-          float sum = SKIP0 ? fk[0] * cs : 0.f;
+      for (int f = 0; f < NF; ++f) v[f] = f < n_run ? red[(f * RPA + ol) * RP + il] : 0.f;
+      const float cs = SKIP0 ? csl[ol] : 0.f;
+      bf16* out = reinterpret_cast<bf16*>(stg + ol * rowb) + il * K;
+      for (int k = 0; k < K; ++k) {
+        const float* fk = fg.v[k];
+        float sum = SKIP0 ? fk[0] * cs : 0.f;
 #pragma unroll
-          for (int f = 0; f < NF; ++f) sum = fmaf(fk[1 + f], v[f], sum);
-          out[k] = from_f32<bf16>(sum);
-        }
+        for (int f = 0; f < NF; ++f) sum = fmaf(fk[1 + f], v[f], sum);
+        out[k] = from_f32<bf16>(sum);
+      }
+    }
+    __syncthreads();
+    if (vtile) {
+      const int cpr = rowb / 16;
+      for (int e = tid; e < RPA * cpr; e += 512) {
+        const int ol = e / cpr, ch = e - ol * cpr;
+        if (ob + ol < OUT)
+          gstore16(reinterpret_cast<unsigned char*>(dc + ((size_t)(ob + ol) * IN + i0) * K) + ch * 16,
+                   lds_read16(stg + ol * rowb + ch * 16));
+      }
+    } else {
+      for (int e = tid; e < RPA * TI * K; e += 512) {
+        const int ol = e / (TI * K), r = e - ol * TI * K, i = i0 + r / K;
+        if (ob + ol < OUT && i < IN)
+          dc[((size_t)(ob + ol) * IN + i0) * K + r] = *reinterpret_cast<const bf16*>(stg + ol * rowb + r * 2);
       }
     }
   }
