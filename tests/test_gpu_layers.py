@@ -192,3 +192,19 @@ def test_pinn_laplacian_matches_forward_mode_oracle():
     xr = rounded(x0, torch.float32)
     want = sum(_chained_second_derivative(layers, xr, d) for d in range(2))
     assert o.normwise_err(np64(lap), want) <= 5e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_saved_model_reloads_with_identical_outputs(tmp_path, dtype):
+    """kanforge.save/load round trip (kanforge tests/test_export.py:67-77): the reloaded model
+    gives bit-identical outputs on the HIP path."""
+    from kanforge_amd import convert as cv
+
+    torch.manual_seed(0)
+    model = torch.nn.Sequential(KAN([4, 16, 8], kf.BSpline(5, 3)), GRKAN(8, 8, groups=4)).to(device=DEV, dtype=dtype)
+    path = tmp_path / "m.npz"
+    cv.save(model, path)
+    back = cv.load(path, device=DEV)
+    x = (torch.rand(33, 4, device=DEV) * 2 - 1).to(dtype)
+    with torch.no_grad():
+        torch.testing.assert_close(back(x), model(x), rtol=0, atol=0)
