@@ -1,7 +1,7 @@
 /*
  * kfhip.h — C ABI of the MI355X (gfx950) fused KAN basis kernels.
  *
- * One shared library, libkfhip.so, built from kanforge_amd/csrc/*.hip. The
+ * One shared library, libkfhip.so, built from the HIP sources in kanforge_amd/csrc. The
  * entry points below replace the reference's raw launcher
  *   kanforge/torch/kernels.py:39-55   _raw(op, plan, m, x, a, b, grid, n_out, nf)
  *   kanforge/kernels/triton_kernels.py:225-242   launch(op, ...)
