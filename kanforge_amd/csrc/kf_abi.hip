@@ -487,14 +487,14 @@ int launch_p_dma_kind(const WsP& L, hipStream_t s, const KBasis& kb, int64_t bat
   return check_launch("P");
 }
 
-template <int TN>
+template <int TN, int RB>
 int launch_p8(const WsP& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, const void* x, const void* g,
               int gstride, const void* cfmt, void* p) {
   constexpr int TI = 16 * TN, RPASS = TN == 2 ? 128 : 64;
-  const size_t lds_ops = (size_t)2 * (256 + 8 * TI) * 64, lds_epi = (size_t)8 * RPASS * (TI + 1) * 4;
+  const size_t lds_ops = (size_t)2 * (256 + 8 * TI) * RB, lds_epi = (size_t)8 * RPASS * (TI + 1) * 4;
   const size_t lds = lds_ops > lds_epi ? lds_ops : lds_epi;
-  auto kern = p8_kernel<KF_KIND_CHEB, TN>;
-  if (L.INP % TI) return fail(KF_EINVAL, "P: workspace layout not aligned");
+  auto kern = p8_kernel<KF_KIND_CHEB, TN, RB>;
+  if (L.INP % TI || L.OUTP % (RB / 2)) return fail(KF_EINVAL, "P: workspace layout not aligned");
   if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return fail(KF_ELAUNCH, "P: cannot reserve %zu bytes of LDS", lds);
   const int n_m = (int)((batch + 255) / 256), n_n = (int)(L.INP / TI);
@@ -540,7 +540,7 @@ int run_P(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
       gstride = (int)L.OUTP;
     }
     // 7 or 8 Chebyshev features in bf16: the two-waves-per-SIMD kernel
-    if (L.p8 && !h) return launch_p8<3>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p);
+    if (L.p8 && !h) return launch_p8<3, 128>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p);
     switch (L.cfg) {
       case 0: return launch_p_dma<T, 2>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p, h);
       case 1: return launch_p_dma<T, 3>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p, h);

@@ -1432,18 +1432,21 @@ __global__ __launch_bounds__(256) void p_dma_kernel(KBasis bs, int B, int IN, in
 // on 8 waves, two per SIMD, so that one wave's waits and barrier arrivals are covered by the
 // other's MFMAs. Workgroup tile 256 rows x (8 features x TI = 16 TN inputs); wave (wm, wn) =
 // (wave & 1, wave >> 1) owns rows 128 wm .. +127 and column fragments TN wn .. +TN - 1 (4 x TN
-// accumulator tiles). A stage is 64 bytes of o for the 256 rows of g and the 128 TN rows of
+// accumulator tiles). A stage is RB bytes of o for the 256 rows of g and the 128 TN rows of
 // CfmT, copied global -> LDS by all waves into two buffers (one barrier per stage); rows are
-// dense 64 bytes with their 16-byte chunks XOR-swizzled by bits 2..3 of the row. Epilogue, in
+// dense RB bytes with their 16-byte chunks XOR-swizzled by bits 2..3 (64-byte rows) or 1..3
+// (128-byte rows) of the row. Epilogue, in
 // passes of RPASS rows: the feature sums H_j go to LDS and every thread forms
 // p[b, i] = sum_j f_j(x[b, i]) H_j[b, i] for (row, input) pairs, the features computed once per
 // pair.
-template <int KIND, int TN>
+template <int KIND, int TN, int RB>
 __global__ __launch_bounds__(512) void p8_kernel(KBasis bs, int B, int IN, int INP, int OUTP,
                                                  const bf16* __restrict__ x, const bf16* __restrict__ g, int gstride,
                                                  const bf16* __restrict__ cfmt, bf16* __restrict__ p) {
-  constexpr int BM = 256, NF = 8, TI = 16 * TN, BN = NF * TI, SA = BM * 64, SS = (BM + BN) * 64, NBUF = 2;
-  constexpr int RP = TI + 1, RPASS = TN == 2 ? 128 : 64, NBLK = (BM + BN) / 16, BPW = NBLK / 8;
+  constexpr int BM = 256, NF = 8, TI = 16 * TN, BN = NF * TI, SA = BM * RB, SS = (BM + BN) * RB, NBUF = 2;
+  constexpr int RP = TI + 1, RPASS = TN == 2 ? 128 : 64, NBLK = SS / 1024, BPW = NBLK / 8;
+  constexpr int CPR = RB / 16, RPB = 1024 / RB, KS = RB / 32, EPS = RB / 2;  // chunks per row, rows per block
+  static_assert(RB == 64 || RB == 128, "64- or 128-byte stage rows");
   static_assert(BPW * 8 == NBLK, "copy blocks divide over the waves");
   static_assert(NBUF * SS <= 160 * 1024 && NF * RPASS * RP * 4 <= 160 * 1024, "stages and the epilogue fit in LDS");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];  // [NBUF][SS], later the sums
@@ -1456,7 +1459,9 @@ __global__ __launch_bounds__(512) void p8_kernel(KBasis bs, int B, int IN, int I
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave & 1, wn = wave >> 1;
   const int h = lane >> 5, l32 = lane & 31;
-  const int S = OUTP / 32;
+  const int S = OUTP / EPS;
+  // 16-byte chunk swizzle of a stage row (conflict-free fragment reads)
+  auto swz = [](int row) { return RB == 64 ? (row >> 2) & 3 : (row >> 1) & 7; };
 
   f32x16 acc[4][TN];
 #pragma unroll
@@ -1466,15 +1471,14 @@ __global__ __launch_bounds__(512) void p8_kernel(KBasis bs, int B, int IN, int I
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[a][t][r] = 0.f;
 
-  // copies: wave w fills blocks BPW w .. BPW w + BPW - 1 of the stage's NBLK (16 rows of 64
-  // bytes; rows 0..255 from g, the rest from CfmT); lane l fills chunk l % 4 of row l / 4,
-  // i.e. global chunk (l % 4) ^ ((row >> 2) & 3). Rows past the batch repeat row B - 1 (never
-  // stored).
+  // copies: wave w fills blocks BPW w .. BPW w + BPW - 1 of the stage's NBLK (RPB rows of RB
+  // bytes; rows 0..255 from g, the rest from CfmT); lane l fills chunk l % CPR of row l / CPR,
+  // i.e. global chunk (l % CPR) ^ swz(row). Rows past the batch repeat row B - 1 (never stored).
   const bf16* src[BPW];
 #pragma unroll
   for (int k = 0; k < BPW; ++k) {
-    const int row = (BPW * wave + k) * 16 + (lane >> 2);
-    const int c = (lane & 3) ^ ((row >> 2) & 3);
+    const int row = (BPW * wave + k) * RPB + lane / CPR;
+    const int c = (lane % CPR) ^ swz(row);
     if (row < BM) {
       const int b = b0 + row < B ? b0 + row : B - 1;
       src[k] = g + (size_t)b * gstride + c * 8;
@@ -1486,19 +1490,19 @@ __global__ __launch_bounds__(512) void p8_kernel(KBasis bs, int B, int IN, int I
   auto copy_stage = [&](int st) {
     unsigned char* dst = smem + (st % NBUF) * SS + BPW * wave * 1024;
 #pragma unroll
-    for (int k = 0; k < BPW; ++k) lds_dma16(src[k] + (size_t)st * 32, dst + k * 1024);
+    for (int k = 0; k < BPW; ++k) lds_dma16(src[k] + (size_t)st * EPS, dst + k * 1024);
   };
-  const int sw = (l32 >> 2) & 3;
+  const int sw = swz(l32);
   auto mma_stage = [&](int st) {
     const unsigned char* base = smem + (st % NBUF) * SS;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+    for (int ks = 0; ks < KS; ++ks) {
       const int co = 16 * ((2 * ks + h) ^ sw);
       u32x4 fa[4], fb[TN];
 #pragma unroll
-      for (int a = 0; a < 4; ++a) fa[a] = lds_read16(base + (wm * 128 + a * 32 + l32) * 64 + co);
+      for (int a = 0; a < 4; ++a) fa[a] = lds_read16(base + (wm * 128 + a * 32 + l32) * RB + co);
 #pragma unroll
-      for (int t = 0; t < TN; ++t) fb[t] = lds_read16(base + SA + ((TN * wn + t) * 32 + l32) * 64 + co);
+      for (int t = 0; t < TN; ++t) fb[t] = lds_read16(base + SA + ((TN * wn + t) * 32 + l32) * RB + co);
 #pragma unroll
       for (int a = 0; a < 4; ++a)
 #pragma unroll
