@@ -989,12 +989,12 @@ __device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)"
 //            c + 2 in the second half of its last one (unrolled).
 // The MFMAs are never under a condition, which keeps the accumulators in
 // AGPRs across the loops.
-template <bool HAS_W, int NT, int TM, int TN, int NBUF, bool SKIP0>
-__global__ __launch_bounds__(256) void f_rega_kernel(int B, int OUT, int OUTP, int BP, int n_chunks, int n_tp,
+template <bool HAS_W, int NT, int TM, int TN, int NBUF, bool SKIP0, int WN>
+__global__ __launch_bounds__(256 * WN) void f_rega_kernel(int B, int OUT, int OUTP, int BP, int n_chunks, int n_tp,
                                                      const float* __restrict__ zc, const float* __restrict__ wc,
                                                      const bf16* __restrict__ cfm, const float* __restrict__ ysum,
                                                      bf16* __restrict__ y, int vout) {
-  constexpr int WM = TM * 32, BM = 4 * WM, BN = TN * 32;
+  constexpr int WM = TM * 32, BM = 4 * WM, BN = WN * TN * 32;
   constexpr int FB = BN * 32;      // one feature of a stage (dense 32-byte rows)
   constexpr int SB = 2 * FB;       // one stage
   constexpr int BPW = SB / 4096;   // 1 KB copy blocks per wave and stage
@@ -1013,7 +1013,8 @@ __global__ __launch_bounds__(256) void f_rega_kernel(int B, int OUT, int OUTP, i
   const int b0 = tm_ * BM, o0 = tn_ * BN;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave;
+  const int wm = wave & 3, wn = wave >> 2;  // 4 waves along the batch, WN along the outputs
+  const bool copier = wn == 0;              // the waves of the first column group issue the copies
   const int h = lane >> 5, l32 = lane & 31;
   const int S = n_chunks * n_tp / 2;                 // n_chunks is even
   constexpr bool ODD = NT % 2 == 1;
@@ -1043,26 +1044,29 @@ __global__ __launch_bounds__(256) void f_rega_kernel(int B, int OUT, int OUTP, i
   int doff[BPW];
 #pragma unroll
   for (int k = 0; k < BPW; ++k) {
-    const int blk = wave * BPW + k;
+    const int blk = wm * BPW + k;
     const int f = blk / (BN / 32), o = (blk % (BN / 32)) * 32 + (lane >> 1);
     const int hh = (lane & 1) ^ ((o >> 3) & 1);
     doff[k] = (f * OUTP + o) * 16 + hh * 8;
   }
   auto copy_z = [&](int x) {  // rows b0 .. b0 + BM of chunk x: BM * 64 contiguous bytes
-    const size_t off = ((size_t)x * BP + b0) * 16 + wave * ZPW * 256 + lane * 4;
+    if (!copier) return;
+    const size_t off = ((size_t)x * BP + b0) * 16 + wm * ZPW * 256 + lane * 4;
 #pragma unroll
     for (int k = 0; k < ZPW; ++k) {
-      lds_dma16(zc + off + k * 256, zs + (x & 1) * ZB + (wave * ZPW + k) * 1024);
-      if (HAS_W) lds_dma16(wc + off + k * 256, ws + (x & 1) * ZB + (wave * ZPW + k) * 1024);
+      lds_dma16(zc + off + k * 256, zs + (x & 1) * ZB + (wm * ZPW + k) * 1024);
+      if (HAS_W) lds_dma16(wc + off + k * 256, ws + (x & 1) * ZB + (wm * ZPW + k) * 1024);
     }
   };
   // copy group of stage st into buffer st % NBUF; past the last stage the buffer is free and
   // the copy repeats the last stage's source, which keeps every stage's block count the same
   auto copy_stage = [&](int st) {
     const bf16* src = bsrc + (size_t)(st < S ? st : S - 1) * stage_elems;
-    unsigned char* dst = smem + (st % NBUF) * SB + wave * BPW * 1024;
+    unsigned char* dst = smem + (st % NBUF) * SB + wm * BPW * 1024;
+    if (copier) {
 #pragma unroll
-    for (int k = 0; k < BPW; ++k) lds_dma16(src + doff[k], dst + k * 1024);
+      for (int k = 0; k < BPW; ++k) lds_dma16(src + doff[k], dst + k * 1024);
+    }
     int flag = 0;
     if (st == zg_next) {
       if (zx_next < n_chunks) {
@@ -1086,7 +1090,7 @@ __global__ __launch_bounds__(256) void f_rega_kernel(int B, int OUT, int OUTP, i
       vmem_wait<(NBUF - 2) * BPW + 2 * ZPW_ALL>();
   };
   // fragment read offset of this lane inside a feature: row l32 (+ 32 t), half h swizzled
-  const int frag_off = (2 * l32 + (h ^ ((l32 >> 3) & 1))) * 16;
+  const int frag_off = wn * TN * 1024 + (2 * l32 + (h ^ ((l32 >> 3) & 1))) * 16;
 
   // A generator: row block a (rows b0 + WM wm + 32 a + l32), inputs 8h..8h+7 of the chunk
   float ga[TM][8], gb[TM][8], z2[TM][8];
@@ -1221,13 +1225,15 @@ __global__ __launch_bounds__(256) void f_rega_kernel(int B, int OUT, int OUTP, i
   // epilogue: each wave's 32 TM x 32 TN tile goes to LDS as bf16 rows (stride EST bytes) over
   // the stage buffers, once every copy has landed and every wave is done with them, then out
   // with 16-byte stores when the rows are whole and aligned (vout), else element by element
-  constexpr int EST = BN * 2 + 16;
+  constexpr int WNC = TN * 32;  // output columns of one wave
+  constexpr int EST = WNC * 2 + 16;
   vmem_wait<0>();
   __syncthreads();
   unsigned char* est = smem + wave * WM * EST;
+  const int ow = o0 + wn * WNC;
 #pragma unroll
   for (int t = 0; t < TN; ++t) {
-    const int o = o0 + t * 32 + l32;
+    const int o = ow + t * 32 + l32;
     const float add = SKIP0 && o < OUT ? ysum[o] : 0.f;
 #pragma unroll
     for (int a = 0; a < TM; ++a)
@@ -1237,18 +1243,18 @@ __global__ __launch_bounds__(256) void f_rega_kernel(int B, int OUT, int OUTP, i
             from_f32<bf16>(acc[a][t][r] + add);
   }
   if (vout) {
-    constexpr int CPR = BN / 8;  // 16-byte chunks per row
+    constexpr int CPR = WNC / 8;  // 16-byte chunks per row
 #pragma unroll 4
     for (int e = lane; e < WM * CPR; e += 64) {
       const int row = e / CPR, ch = e % CPR;
-      const int b = b0 + wm * WM + row, o = o0 + ch * 8;
+      const int b = b0 + wm * WM + row, o = ow + ch * 8;
       const u32x4 v = lds_read16(est + row * EST + ch * 16);
       if (b < B && o < OUT) gstore16(y + (size_t)b * OUT + o, v);
     }
   } else {
-    for (int e = lane; e < WM * BN; e += 64) {
-      const int row = e / BN, col = e % BN;
-      const int b = b0 + wm * WM + row, o = o0 + col;
+    for (int e = lane; e < WM * WNC; e += 64) {
+      const int row = e / WNC, col = e % WNC;
+      const int b = b0 + wm * WM + row, o = ow + col;
       if (b < B && o < OUT) y[(size_t)b * OUT + o] = *reinterpret_cast<const bf16*>(est + row * EST + col * 2);
     }
   }
