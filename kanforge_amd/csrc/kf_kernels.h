@@ -1542,16 +1542,29 @@ __global__ __launch_bounds__(512) void p8_kernel(KBasis bs, int B, int IN, int I
       }
     }
     __syncthreads();
-    for (int e = tid; e < RPASS * TI; e += 512) {
-      const int row = e / TI, il = e % TI;
+    // two adjacent inputs per thread: one 4-byte store when both exist, IN is even and p is
+    // 4-byte aligned
+    for (int e = tid; e < RPASS * TI / 2; e += 512) {
+      const int row = e / (TI / 2), il = 2 * (e % (TI / 2));
       const int b = b0 + ps * RPASS + row, i = i0 + il;
-      if (b < B && i < IN) {
-        float f[NF];
-        kind_features<KIND, NF>(to_f32(x[(size_t)b * IN + i]), 1.f, i, bs, f);
-        float sum = 0.f;
+      if (b >= B || i >= IN) continue;
+      float v[2] = {0.f, 0.f};
 #pragma unroll
-        for (int q = 0; q < NF; ++q) sum = fmaf(red[(q * RPASS + row) * RP + il], f[q], sum);
-        p[(size_t)b * IN + i] = from_f32<bf16>(sum);
+      for (int u = 0; u < 2; ++u) {
+        if (i + u < IN) {
+          float f[NF];
+          kind_features<KIND, NF>(to_f32(x[(size_t)b * IN + i + u]), 1.f, i + u, bs, f);
+#pragma unroll
+          for (int q = 0; q < NF; ++q) v[u] = fmaf(red[(q * RPASS + row) * RP + il + u], f[q], v[u]);
+        }
+      }
+      bf16* dst = p + (size_t)b * IN + i;
+      if (IN % 2 == 0 && i + 1 < IN && (reinterpret_cast<uintptr_t>(p) & 3) == 0) {
+        const bf16 pr[2] = {from_f32<bf16>(v[0]), from_f32<bf16>(v[1])};
+        *reinterpret_cast<uint32_t*>(dst) = __builtin_bit_cast(uint32_t, pr);
+      } else {
+        dst[0] = from_f32<bf16>(v[0]);
+        if (i + 1 < IN) dst[1] = from_f32<bf16>(v[1]);
       }
     }
   }
