@@ -18,6 +18,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
+from .. import grid as grid_tools
 from .._layer import basis_param_values, init_stds, resolve_groups
 from ..bases import Basis, Rational, make_basis
 from ..kernels import plan_for
@@ -268,6 +269,100 @@ class KANLinear(nn.Module):
         super()._load_from_state_dict(*args, **kwargs)
         self._refresh_symbolic()
 
+    # --- grid update, refinement, basis conversion (kanforge/_layer.py:99-191) ------------
+
+    def _export_state(self) -> dict:
+        """Float64 NumPy copies of ``coef``, ``edge_scale`` and the basis parameters."""
+        f = self._to_numpy
+        return {
+            "coef": f(self.coef),
+            "edge_scale": None if self.edge_scale is None else f(self.edge_scale),
+            "trainable": {n: f(getattr(self, f"basis_{n}")) for n in self._trainable_names},
+            "buffers": {n: f(getattr(self, f"basis_{n}")) for n in self._buffer_names},
+        }
+
+    def _expanded(self, trainable: dict, buffers: dict) -> dict:
+        """Basis parameters per input (group parameters repeated over their inputs)."""
+        rep = self.in_features // self.groups
+        return {**{k: np.repeat(v, rep, axis=0) for k, v in trainable.items()}, **buffers}
+
+    @torch.no_grad()
+    def _load_state(self, basis: Basis, coef, edge_scale, trainable: dict, buffers: dict) -> None:
+        like = {"dtype": self.coef.dtype, "device": self.coef.device}
+        self.basis = basis
+        self._init_kwargs["basis"] = basis
+        self.coef = nn.Parameter(torch.as_tensor(np.ascontiguousarray(coef), **like))
+        if edge_scale is not None:
+            self.edge_scale = nn.Parameter(torch.as_tensor(np.ascontiguousarray(edge_scale), **like))
+        self._set_basis_state(trainable, buffers)
+
+    def _refit_to(self, new_basis: Basis, new_trainable: dict, new_buffers: dict, x: np.ndarray, ridge: float) -> None:
+        st = self._export_state()
+        scale = st["edge_scale"]
+        coef_eff = st["coef"] if scale is None else st["coef"] * scale[..., None]
+        coef = grid_tools.refit(
+            self.basis,
+            self._expanded(st["trainable"], st["buffers"]),
+            coef_eff,
+            new_basis,
+            self._expanded(new_trainable, new_buffers),
+            x,
+            ridge,
+        )
+        if scale is not None:  # keep the edge scales, fold the refit into coef
+            ok = np.abs(scale) > 1e-12
+            coef = coef / np.where(ok, scale, 1.0)[..., None]
+            scale = np.where(ok, scale, 1.0)
+        self._load_state(new_basis, coef, scale, new_trainable, new_buffers)
+
+    def _samples(self, x, basis: Basis, buffers: dict, n: int) -> np.ndarray:
+        if x is not None:
+            return np.asarray(self._to_numpy(x), dtype=np.float64).reshape(-1, self.in_features)
+        ranges = grid_tools.grid_ranges(basis, buffers)
+        if ranges is None:
+            raise ValueError(f"{type(basis).__name__} has no grid: pass samples x")
+        return grid_tools.sample_inputs(ranges, n)
+
+    def update_grid(self, x, *, margin: float = 0.0, grid_eps: float = 0.02, ridge: float = 0.0) -> None:
+        """Adapt every grid to the inputs ``x`` and refit the edge functions on them (pykan's
+        update_grid_from_samples; approximate, as a spline on a new grid can only approximate
+        the old one)."""
+        if x is None:
+            raise ValueError("update_grid needs input samples x")
+        names = self.basis.grid_names()
+        if not names:
+            raise TypeError(f"{type(self.basis).__name__} has no grid")
+        st = self._export_state()
+        xs = self._samples(x, self.basis, st["buffers"], 0)
+        buffers = dict(st["buffers"])
+        for name in names:
+            buffers[name] = grid_tools.adaptive_grid(xs, buffers[name].shape[-1], margin, grid_eps)
+        self._refit_to(self.basis, st["trainable"], buffers, xs, ridge)
+
+    def refine_grid(self, grid_size: int, x=None, *, ridge: float = 0.0) -> None:
+        """The same basis on a finer (or coarser) grid; each input's grid keeps its shape."""
+        key = _resize_key(self.basis)
+        new_basis = make_basis({**self.basis.config(), key: grid_size})
+        st = self._export_state()
+        trainable, buffers = basis_param_values(new_basis, self.groups, self.in_features)
+        for name in new_basis.grid_names():
+            if name in st["buffers"]:
+                buffers[name] = grid_tools.resample_grid(st["buffers"][name], buffers[name].shape[-1])
+        xs = self._samples(x, self.basis, st["buffers"], 8 * new_basis.size + 64)
+        self._refit_to(new_basis, trainable, buffers, xs, ridge)
+
+    def change_basis(self, basis, x=None, *, ridge: float = 0.0) -> None:
+        """Convert to another basis (e.g. B-spline -> Chebyshev) by least squares; without
+        ``x`` the fit uses points spread over the current grid ranges (or the new basis'
+        ranges), and a new grid inherits each input's range."""
+        new_basis = make_basis(basis)
+        st = self._export_state()
+        old_ranges = grid_tools.grid_ranges(self.basis, st["buffers"])
+        trainable, buffers = basis_param_values(new_basis, self.groups, self.in_features, old_ranges)
+        src, src_buffers = (self.basis, st["buffers"]) if old_ranges is not None else (new_basis, buffers)
+        xs = self._samples(x, src, src_buffers, 8 * max(new_basis.size, self.basis.size) + 64)
+        self._refit_to(new_basis, trainable, buffers, xs, ridge)
+
     def extra_repr(self) -> str:
         groups = "" if self.groups == self.in_features else f", groups={self.groups}"
         return f"in_features={self.in_features}, out_features={self.out_features}, basis={self.basis!r}{groups}"
@@ -319,6 +414,26 @@ class KAN(nn.Sequential):
     def edge_derivative(self, x: torch.Tensor, order: int = 1) -> list[torch.Tensor]:
         """Per-layer edge derivatives at the activations each layer receives."""
         return [layer.edge_derivative(h, order) for layer, h in layer_inputs(self, x)]
+
+    @torch.no_grad()
+    def update_grid(self, x: torch.Tensor, **kwargs) -> None:
+        """Update every layer's grid from the activations it receives (pykan)."""
+        for layer in self:
+            layer.update_grid(x, **kwargs)
+            x = layer(x)
+
+    def refine_grid(self, grid_size: int, **kwargs) -> None:
+        for layer in self:
+            layer.refine_grid(grid_size, **kwargs)
+
+
+def _resize_key(basis: Basis) -> str:
+    """The config entry that sets a basis' number of grid intervals (kanforge/_layer.py:99-104)."""
+    cfg = basis.config()
+    for key in ("grid_size", "count", "num_knots"):
+        if key in cfg:
+            return key
+    raise TypeError(f"{type(basis).__name__} has no grid size to refine")
 
 
 def rebuild_kan(layers: Sequence[KANLinear]) -> KAN:

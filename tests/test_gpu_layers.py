@@ -208,3 +208,19 @@ def test_saved_model_reloads_with_identical_outputs(tmp_path, dtype):
     x = (torch.rand(33, 4, device=DEV) * 2 - 1).to(dtype)
     with torch.no_grad():
         torch.testing.assert_close(back(x), model(x), rtol=0, atol=0)
+
+
+def test_forward_after_grid_update_uses_the_new_grid():
+    """After update_grid / refine_grid the kernel route sees the new grid and coefficients
+    (kanforge tests/test_kernels.py:136-143): the device knot tables are rebuilt."""
+    torch.manual_seed(0)
+    model = KAN([3, 5, 2], kf.BSpline(5, 3)).to(DEV)
+    x = torch.randn(64, 3, device=DEV) * 0.4
+    model(x)  # device tables of the initial grids
+    model.update_grid(x)
+    model[0].refine_grid(8)
+    for layer, h in [(model[0], x), (model[1], model[0](x).detach())]:
+        ob = oracle_of(layer)
+        want = o.kan_linear(np64(h), np64(layer.coef), ob, np64(layer.base_weight), np64(layer.bias))
+        assert o.normwise_err(np64(layer(h)), want) <= TOL[torch.float32]
+    assert model[0].basis.grid_size == 8 and model[0].basis_grid.shape == (3, 9)
