@@ -269,6 +269,29 @@ class KANLinear(nn.Module):
         super()._load_from_state_dict(*args, **kwargs)
         self._refresh_symbolic()
 
+    # --- construction from MLPs (kanforge/torch/layers.py:290-309) ------------------------
+
+    @classmethod
+    def from_linear(cls, linear: nn.Linear, activation: Callable = F.silu, basis="bspline", **kwargs) -> "KANLinear":
+        """``linear(activation(x))`` as a ``KANLinear``: the activation becomes the base branch
+        with the linear's weight and bias, and the spline coefficients start at zero."""
+        layer = cls(
+            linear.in_features,
+            linear.out_features,
+            basis,
+            bias=linear.bias is not None,
+            base_activation=activation,
+            coef_init="zero",
+            device=linear.weight.device,
+            dtype=linear.weight.dtype,
+            **kwargs,
+        )
+        with torch.no_grad():
+            layer.base_weight.copy_(linear.weight)
+            if linear.bias is not None:
+                layer.bias.copy_(linear.bias)
+        return layer
+
     # --- grid update, refinement, basis conversion (kanforge/_layer.py:99-191) ------------
 
     def _export_state(self) -> dict:
@@ -425,6 +448,24 @@ class KAN(nn.Sequential):
     def refine_grid(self, grid_size: int, **kwargs) -> None:
         for layer in self:
             layer.refine_grid(grid_size, **kwargs)
+
+
+def from_mlp(mlp: nn.Sequential, basis="bspline", **kwargs) -> nn.Sequential:
+    """``Linear, act, Linear, act, ..., Linear`` as an equal network (kanforge/torch/layers.py:
+    312-328): the first Linear stays and every (activation, Linear) pair becomes a
+    ``KANLinear`` whose base branch is that activation."""
+    mods = list(mlp)
+    if not mods or not isinstance(mods[0], nn.Linear):
+        raise ValueError("the MLP must start with nn.Linear")
+    out, i = [mods[0]], 1
+    while i < len(mods):
+        if i + 1 < len(mods) and isinstance(mods[i + 1], nn.Linear) and not isinstance(mods[i], nn.Linear):
+            out.append(KANLinear.from_linear(mods[i + 1], mods[i], basis, **kwargs))
+            i += 2
+        else:
+            out.append(mods[i])
+            i += 1
+    return nn.Sequential(*out)
 
 
 def _resize_key(basis: Basis) -> str:

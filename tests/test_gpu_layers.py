@@ -224,3 +224,55 @@ def test_forward_after_grid_update_uses_the_new_grid():
         want = o.kan_linear(np64(h), np64(layer.coef), ob, np64(layer.base_weight), np64(layer.bias))
         assert o.normwise_err(np64(layer(h)), want) <= TOL[torch.float32]
     assert model[0].basis.grid_size == 8 and model[0].basis_grid.shape == (3, 9)
+
+
+@pytest.mark.parametrize("kind", ["kan", "grkan"])
+def test_kanffn_forward_matches_oracle(kind):
+    """KANFFN (kanforge/torch/transformer.py:25-52): two KAN layers back to back."""
+    from kanforge_amd.torch import KANFFN
+
+    torch.manual_seed(0)
+    ffn = KANFFN(16, 48, kind=kind, basis=kf.Chebyshev(6), groups=4).to(DEV)
+    x = torch.randn(40, 16, device=DEV) * 0.7
+    with torch.no_grad():
+        y = ffn(x)
+    def arr(t):
+        return None if t is None else np64(t)
+
+    h = o.kan_linear(np64(x), np64(ffn.fc1.coef), oracle_of(ffn.fc1), arr(ffn.fc1.base_weight), arr(ffn.fc1.bias))
+    want = o.kan_linear(h, np64(ffn.fc2.coef), oracle_of(ffn.fc2), arr(ffn.fc2.base_weight), arr(ffn.fc2.bias))
+    assert o.normwise_err(np64(y), want) <= 2e-5
+
+
+def test_kanify_exact_keeps_outputs_and_katblock_runs():
+    """kanify(mode="exact") (kanforge/torch/transformer.py:127-167) keeps the model's function:
+    the spline parts start at zero."""
+    from kanforge_amd.torch import KATBlock, kanify
+
+    torch.manual_seed(1)
+
+    class Mlp(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.fc1, self.act, self.fc2 = torch.nn.Linear(12, 32), torch.nn.GELU(), torch.nn.Linear(32, 12)
+
+        def forward(self, x):
+            return self.fc2(self.act(self.fc1(x)))
+
+    model = torch.nn.Sequential(Mlp(), torch.nn.LayerNorm(12), Mlp()).to(DEV)
+    x = torch.randn(2, 9, 12, device=DEV)
+    with torch.no_grad():
+        before = model(x)
+        assert kanify(model, "exact", basis=kf.BSpline(5, 3)) == ["0", "2"]
+        after = model(x)
+    torch.testing.assert_close(after, before, rtol=1e-5, atol=1e-6)
+
+    blk = KATBlock(16, 4, mlp_ratio=2.0, groups=4).to(DEV).eval()
+    z = torch.randn(3, 7, 16, device=DEV)
+    with torch.no_grad():
+        out = blk(z)
+        h = blk.norm1(z)
+        ref = z + blk.attn(h, h, h, need_weights=False)[0]
+        ref = ref + blk.ffn(blk.norm2(ref))
+    assert out.shape == z.shape
+    torch.testing.assert_close(out, ref, rtol=0, atol=0)
