@@ -7,7 +7,8 @@ bfloat16 with float32 accumulation, batch 8192; one step = forward + dX + dCoef
 Inputs are seeded synthetic tensors resident in HBM before timing starts:
 x ~ N(0, 1) (seed 0), coef ~ N(0, 1/(768*9)) (seed 1), upstream gradient
 gy ~ N(0, 1) (seed 3). Algorithmic work per step is 3 contractions of
-2*B*in*K*out FLOP = 1.0437 TFLOP.
+2*B*in*K*out FLOP = 1.0437 TFLOP. The line also carries ``with_base``: the
+same step for the layer's defaults (SiLU base branch and bias on, 1.160 TFLOP).
 """
 
 from __future__ import annotations
@@ -37,6 +38,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-base", action="store_true", help="skip the default-layer (base branch on) leg")
     return ap.parse_args()
 
 
@@ -145,6 +147,33 @@ def main():
 
     ms = elapsed / args.steps * 1e3
     per_op = timer.mean_ms()
+
+    with_base = None
+    if not args.no_base:
+        # the default layer (SiLU base branch and bias on): the same step plus the base GEMMs
+        # (2 * B * in * out per contraction, forward, dX and dW: 0.116 TFLOP more)
+        base = KANLinear(IN, OUT, kf.Chebyshev(DEGREE), device=dev, dtype=torch.bfloat16)
+        with torch.no_grad():
+            base.coef.copy_(layer.coef)
+
+        def step_base():
+            y = base(x)
+            return torch.autograd.grad(y, [x, base.coef, base.base_weight, base.bias], gy)
+
+        for _ in range(args.warmup):
+            step_base()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        for _ in range(args.steps):
+            step_base()
+        torch.cuda.synchronize()
+        ms_base = (time.perf_counter() - t1) / args.steps * 1e3
+        with_base = {
+            "layer": "KANLinear(768, 3072, Chebyshev(8)) defaults: SiLU base branch, bias",
+            "ms_per_step": ms_base,
+            "value": B / (ms_base * 1e-3),
+            "tflops": (STEP_FLOP + 3 * 2.0 * B * IN * OUT) / (ms_base * 1e-3) / 1e12,
+        }
     dominant = max(per_op, key=per_op.get)
     achieved = FLOP_PER_CONTRACTION / (per_op[dominant] * 1e-3) / 1e12
     out = {
@@ -174,6 +203,7 @@ def main():
         "tflops": STEP_FLOP / (ms * 1e-3) / 1e12,
         "frac_of_bf16_peak": STEP_FLOP / (ms * 1e-3) / PEAK_BF16,
         "per_entry_ms": per_op,
+        "with_base": with_base,
         "roofline": {
             "bound": "mfma",
             "kernel": f"kf_{dominant}",
