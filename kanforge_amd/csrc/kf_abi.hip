@@ -142,7 +142,7 @@ struct WsF {
 // (32 RA_TN), four waves along the batch times RA_WN along the outputs (wave
 // tile (32 RA_TM) x (32 RA_TN / RA_WN)).
 constexpr int F_REGA = -1;
-constexpr int RA_TM = 2, RA_TN = 6, RA_WN = 1, RA_BM = 128 * RA_TM, RA_BN = 32 * RA_TN;
+constexpr int RA_TM = 1, RA_TN = 6, RA_WN = 1, RA_NWM = 8, RA_BM = 32 * RA_NWM * RA_TM, RA_BN = 32 * RA_TN;
 constexpr int RA_NBUF = 4;  // coefficient stage buffers (prefetch distance RA_NBUF - 1 stages)
 bool f_uses_rega(const kf_basis* b, int dtype) { return b->kind == KF_KIND_CHEB && dtype == KF_BF16; }
 // odd feature counts with an unpadded, unrolled variant
@@ -363,12 +363,12 @@ int launch_f_rega(const WsF& L, int64_t batch, int64_t n_out, const float* zc, c
   const size_t lds = lds_ops > lds_epi ? lds_ops : lds_epi;
   const int vout = n_out % 8 == 0 && aligned16(y);
   constexpr int TNW = RA_TN / RA_WN;
-  auto kern = L.n_tp == 9   ? f_rega_kernel<HAS_W, 9, RA_TM, TNW, RA_NBUF, SKIP0, RA_WN>
-              : L.n_tp == 8 ? f_rega_kernel<HAS_W, 8, RA_TM, TNW, RA_NBUF, SKIP0, RA_WN>
-                            : f_rega_kernel<HAS_W, 0, RA_TM, TNW, RA_NBUF, SKIP0, RA_WN>;
+  auto kern = L.n_tp == 9   ? f_rega_kernel<HAS_W, 9, RA_TM, TNW, RA_NBUF, SKIP0, RA_WN, RA_NWM>
+              : L.n_tp == 8 ? f_rega_kernel<HAS_W, 8, RA_TM, TNW, RA_NBUF, SKIP0, RA_WN, RA_NWM>
+                            : f_rega_kernel<HAS_W, 0, RA_TM, TNW, RA_NBUF, SKIP0, RA_WN, RA_NWM>;
   if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return fail(KF_ELAUNCH, "F: cannot reserve %zu bytes of LDS", lds);
-  hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(256 * RA_WN), lds, s, (int)batch, (int)n_out, (int)L.OUTP, (int)L.BP,
+  hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(64 * RA_NWM * RA_WN), lds, s, (int)batch, (int)n_out, (int)L.OUTP, (int)L.BP,
                      (int)(L.INP / 16), L.n_tp, zc, wc, (const bf16*)cfm, ysum, (bf16*)y, vout);
   return check_launch("F");
 }

@@ -952,9 +952,10 @@ __device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)"
 // ---------------------------------------------------------------------------
 // F for bf16 Chebyshev plans with the A operand in registers:
 //   y[b,o] = sum_{c, j} sum_{e < 16} w T_j(z)[b][16c+e] * Cfm[c][j][o][e]
-// 4 waves stacked along the batch (they share every coefficient fragment,
-// which halves the L2 -> LDS traffic against a 2 x 2 arrangement), wave tile
-// (32 TM) x (32 TN), float32 accumulators in AGPRs. Every lane builds its own MFMA A fragments (rows b, 8 consecutive
+// NWM waves stacked along the batch times WN along the outputs (stacked waves
+// share every coefficient fragment; waves of one column group generate their
+// own rows' features), wave tile (32 TM) x (32 TN), float32 accumulators;
+// waves 0..3 issue the copies. Every lane builds its own MFMA A fragments (rows b, 8 consecutive
 // inputs of a 16-input chunk) with the Chebyshev recurrence in float32
 // registers, so the features never touch LDS; with TM = 2 that costs 24 VALU
 // instructions per feature against 2 TN MFMAs, interleaved so that the
@@ -989,12 +990,12 @@ __device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)"
 //            c + 2 in the second half of its last one (unrolled).
 // The MFMAs are never under a condition, which keeps the accumulators in
 // AGPRs across the loops.
-template <bool HAS_W, int NT, int TM, int TN, int NBUF, bool SKIP0, int WN>
-__global__ __launch_bounds__(256 * WN) void f_rega_kernel(int B, int OUT, int OUTP, int BP, int n_chunks, int n_tp,
+template <bool HAS_W, int NT, int TM, int TN, int NBUF, bool SKIP0, int WN, int NWM>
+__global__ __launch_bounds__(64 * NWM * WN) void f_rega_kernel(int B, int OUT, int OUTP, int BP, int n_chunks, int n_tp,
                                                      const float* __restrict__ zc, const float* __restrict__ wc,
                                                      const bf16* __restrict__ cfm, const float* __restrict__ ysum,
                                                      bf16* __restrict__ y, int vout) {
-  constexpr int WM = TM * 32, BM = 4 * WM, BN = WN * TN * 32;
+  constexpr int WM = TM * 32, BM = NWM * WM, BN = WN * TN * 32;
   constexpr int FB = BN * 32;      // one feature of a stage (dense 32-byte rows)
   constexpr int SB = 2 * FB;       // one stage
   constexpr int BPW = SB / 4096;   // 1 KB copy blocks per wave and stage
@@ -1013,8 +1014,8 @@ __global__ __launch_bounds__(256 * WN) void f_rega_kernel(int B, int OUT, int OU
   const int b0 = tm_ * BM, o0 = tn_ * BN;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave & 3, wn = wave >> 2;  // 4 waves along the batch, WN along the outputs
-  const bool copier = wn == 0;              // the waves of the first column group issue the copies
+  const int wm = wave % NWM, wn = wave / NWM;  // NWM waves along the batch, WN along the outputs
+  const bool copier = wave < 4;                 // waves 0..3 issue the copies (copy index: wave)
   const int h = lane >> 5, l32 = lane & 31;
   const int S = n_chunks * n_tp / 2;                 // n_chunks is even
   constexpr bool ODD = NT % 2 == 1;
@@ -1044,25 +1045,25 @@ __global__ __launch_bounds__(256 * WN) void f_rega_kernel(int B, int OUT, int OU
   int doff[BPW];
 #pragma unroll
   for (int k = 0; k < BPW; ++k) {
-    const int blk = wm * BPW + k;
+    const int blk = wave * BPW + k;
     const int f = blk / (BN / 32), o = (blk % (BN / 32)) * 32 + (lane >> 1);
     const int hh = (lane & 1) ^ ((o >> 3) & 1);
     doff[k] = (f * OUTP + o) * 16 + hh * 8;
   }
   auto copy_z = [&](int x) {  // rows b0 .. b0 + BM of chunk x: BM * 64 contiguous bytes
     if (!copier) return;
-    const size_t off = ((size_t)x * BP + b0) * 16 + wm * ZPW * 256 + lane * 4;
+    const size_t off = ((size_t)x * BP + b0) * 16 + wave * ZPW * 256 + lane * 4;
 #pragma unroll
     for (int k = 0; k < ZPW; ++k) {
-      lds_dma16(zc + off + k * 256, zs + (x & 1) * ZB + (wm * ZPW + k) * 1024);
-      if (HAS_W) lds_dma16(wc + off + k * 256, ws + (x & 1) * ZB + (wm * ZPW + k) * 1024);
+      lds_dma16(zc + off + k * 256, zs + (x & 1) * ZB + (wave * ZPW + k) * 1024);
+      if (HAS_W) lds_dma16(wc + off + k * 256, ws + (x & 1) * ZB + (wave * ZPW + k) * 1024);
     }
   };
   // copy group of stage st into buffer st % NBUF; past the last stage the buffer is free and
   // the copy repeats the last stage's source, which keeps every stage's block count the same
   auto copy_stage = [&](int st) {
     const bf16* src = bsrc + (size_t)(st < S ? st : S - 1) * stage_elems;
-    unsigned char* dst = smem + (st % NBUF) * SB + wm * BPW * 1024;
+    unsigned char* dst = smem + (st % NBUF) * SB + wave * BPW * 1024;
     if (copier) {
 #pragma unroll
       for (int k = 0; k < BPW; ++k) lds_dma16(src + doff[k], dst + k * 1024);
