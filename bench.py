@@ -39,6 +39,12 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-base", action="store_true", help="skip the default-layer (base branch on) leg")
+    ap.add_argument(
+        "--workload",
+        default="cheb768",
+        choices=["cheb768", *WORKLOADS, "all"],
+        help="cheb768 (default) is the headline line; the others time the remaining layer shapes one line each",
+    )
     return ap.parse_args()
 
 
@@ -49,22 +55,25 @@ class EntryTimer:
         self.active = False
         self.events = {"F": [], "G": [], "P": []}
 
-    def wrap(self, raw):
-        def timed(op, *args, **kwargs):
+    def wrap(self, raw, label=None):
+        def timed(*args, **kwargs):
             if not self.active:
-                return raw(op, *args, **kwargs)
+                return raw(*args, **kwargs)
             s = torch.cuda.Event(enable_timing=True)
             e = torch.cuda.Event(enable_timing=True)
             s.record()
-            out = raw(op, *args, **kwargs)
+            out = raw(*args, **kwargs)
             e.record()
-            self.events[op].append((s, e))
+            self.events.setdefault(label or args[0], []).append((s, e))
             return out
 
         return timed
 
     def mean_ms(self):
         return {op: (sum(s.elapsed_time(e) for s, e in ev) / len(ev) if ev else 0.0) for op, ev in self.events.items()}
+
+    def count(self):
+        return {op: len(ev) for op, ev in self.events.items()}
 
 
 TRAFFIC_FILE = os.path.join("profiles", "kanlinear_768x3072_cheb8_bf16_hbm_traffic.md")
@@ -105,6 +114,183 @@ def cpu_baseline():
     }
 
 
+def _timed(step, steps, warmup, timer):
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    timer.active = True
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    timer.active = False
+    return (time.perf_counter() - t0) / steps * 1e3
+
+
+def _randn(shape, seed, scale=1.0):
+    return torch.randn(*shape, generator=torch.Generator().manual_seed(seed)) * scale
+
+
+def wl_bspline_ffn(dev, timer):
+    """kanify'd GPT-2-small FFN: KANLinear 768->3072 then 3072->768, B-spline grid 8 order 3
+    (K=11), layer defaults (SiLU base, bias), bf16, 8 x 2048 tokens, forward + backward."""
+    import kanforge_amd as kf
+    from kanforge_amd.torch.transformer import KANFFN
+
+    tok, dim, hid, k = 8 * 2048, 768, 3072, 11
+    ffn = KANFFN(dim, hid, kind="kan", basis=kf.BSpline(8, 3)).to(dev, torch.bfloat16)
+    with torch.no_grad():
+        ffn.fc1.coef.copy_(_randn(ffn.fc1.coef.shape, 1, 1 / math.sqrt(dim * k)))
+        ffn.fc2.coef.copy_(_randn(ffn.fc2.coef.shape, 1, 1 / math.sqrt(hid * k)))
+    x = _randn((8, 2048, dim), 0).to(dev, torch.bfloat16).requires_grad_()
+    gy = _randn((8, 2048, dim), 3).to(dev, torch.bfloat16)
+    params = [x, *ffn.parameters()]
+
+    def step():
+        return torch.autograd.grad(ffn(x), params, gy)
+
+    per_contraction = 2.0 * tok * dim * k * hid
+    return step, tok, "tokens/s", 6 * per_contraction + 6 * 2.0 * tok * dim * hid, per_contraction, "bf16"
+
+
+def wl_grkan_ffn(dev, timer):
+    """GR-KAN FFN 768->3072->768, 8 groups, rational P degree 5 / Q degree 4, bf16,
+    16 x 1024 tokens, P/Q ~ N(0, 0.1), forward + backward."""
+    from kanforge_amd.torch.transformer import KANFFN
+
+    tok, dim, hid = 16 * 1024, 768, 3072
+    ffn = KANFFN(dim, hid, kind="grkan", groups=8).to(dev, torch.bfloat16)
+    with torch.no_grad():
+        for i, layer in enumerate((ffn.fc1, ffn.fc2)):
+            layer.basis_numerator.copy_(_randn(layer.basis_numerator.shape, 2 + 2 * i, math.sqrt(0.1)))
+            layer.basis_denominator.copy_(_randn(layer.basis_denominator.shape, 3 + 2 * i, math.sqrt(0.1)))
+    x = _randn((16, 1024, dim), 0).to(dev, torch.bfloat16).requires_grad_()
+    gy = _randn((16, 1024, dim), 3).to(dev, torch.bfloat16)
+    params = [x, *ffn.parameters()]
+
+    def step():
+        return torch.autograd.grad(ffn(x), params, gy)
+
+    per_gemm = 2.0 * tok * dim * hid
+    return step, tok, "tokens/s", 6 * per_gemm, per_gemm, "bf16"
+
+
+def _pinn_model(dev):
+    import kanforge_amd as kf
+    from kanforge_amd.torch import KAN
+
+    model = KAN([2, 64, 64, 1], kf.Jacobi(6, 0.5, 0.5, input_map="tanh")).to(dev)
+    with torch.no_grad():
+        for i, layer in enumerate(model):
+            layer.coef.copy_(_randn(layer.coef.shape, 1 + i, 1 / math.sqrt(layer.in_features * 7)))
+    x = (torch.rand(65536, 2, generator=torch.Generator().manual_seed(0)) * 2 - 1).to(dev)
+    return model, x
+
+
+def wl_pinn_edge(dev, timer):
+    """PINN KAN [2, 64, 64, 1] Jacobi(6, 1/2, 1/2) tanh, fp32, 65536 points x ~ U(-1, 1)^2:
+    KAN.edge_derivative(x, 2), every layer's (points, out, in) second derivatives."""
+    model, x = _pinn_model(dev)
+
+    def step():
+        with torch.no_grad():
+            return model.edge_derivative(x, 2)
+
+    n = x.shape[0]
+    out_bytes = 4.0 * n * (64 * 2 + 64 * 64 + 1 * 64)
+    in_bytes = 4.0 * n * (2 + 64 + 64)
+    return step, n, "points/s", None, out_bytes + in_bytes, "f32"
+
+
+def wl_pinn_laplacian(dev, timer):
+    """The same PINN network: the chained Laplacian d2u/dx0^2 + d2u/dx1^2 over the
+    network by reverse-over-reverse autograd through the F/G/P closure."""
+    from kanforge_amd.torch import laplacian
+
+    model, x = _pinn_model(dev)
+
+    def step():
+        return laplacian(model, x)
+
+    n = x.shape[0]
+    layer_pass = 2.0 * n * 7 * (2 * 64 + 64 * 64 + 64)
+    return step, n, "points/s", None, layer_pass, "f32"
+
+
+def wl_kan64(dev, timer):
+    """KANLinear 64->64 B-spline (grid 5, order 3, K=8) on [-1, 1], SiLU base, fp32,
+    batch 4096, x ~ U(-1, 1), coef ~ N(0, 1/(64*8)), forward + backward."""
+    import kanforge_amd as kf
+    from kanforge_amd.torch import KANLinear
+
+    layer = KANLinear(64, 64, kf.BSpline(5, 3)).to(dev)
+    with torch.no_grad():
+        layer.coef.copy_(_randn(layer.coef.shape, 1, 1 / math.sqrt(64 * 8)))
+    x = (torch.rand(4096, 64, generator=torch.Generator().manual_seed(0)) * 2 - 1).to(dev).requires_grad_()
+    gy = _randn((4096, 64), 3).to(dev)
+    params = [x, *layer.parameters()]
+
+    def step():
+        return torch.autograd.grad(layer(x), params, gy)
+
+    per_contraction = 2.0 * 4096 * 64 * 8 * 64
+    return step, 4096, "samples/s", 3 * per_contraction + 3 * 2.0 * 4096 * 64 * 64, per_contraction, "f32"
+
+
+WORKLOADS = {
+    "bspline_ffn": wl_bspline_ffn,
+    "grkan_ffn": wl_grkan_ffn,
+    "pinn_edge": wl_pinn_edge,
+    "pinn_laplacian": wl_pinn_laplacian,
+    "kan64": wl_kan64,
+}
+
+
+def run_workload(name, args, dev):
+    """One JSON line for a non-headline layer shape: whole-step throughput plus HIP-event
+    means of every entry point it calls (F, G, P, edge, features)."""
+    from kanforge_amd.torch import kernels as kmod
+
+    timer = EntryTimer()
+    timer.events = {}
+    orig = kmod._raw, kmod._edge_raw, kmod._features_raw
+    kmod._raw = timer.wrap(orig[0])
+    kmod._edge_raw = timer.wrap(orig[1], "edge")
+    kmod._features_raw = timer.wrap(orig[2], "features")
+    try:
+        step, units, unit, step_flop, per_launch, dtype = WORKLOADS[name](dev, timer)
+        ms = _timed(step, args.steps, args.warmup, timer)
+    finally:
+        kmod._raw, kmod._edge_raw, kmod._features_raw = orig
+    per_op, calls = timer.mean_ms(), timer.count()
+    line = {
+        "metric": f"{name} throughput",
+        "value": units / (ms * 1e-3),
+        "unit": unit,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "dtype": dtype,
+        "data": "synthetic",
+        "config": {"workload": WORKLOADS[name].__doc__.split("\n\n")[0].replace("\n", " ").strip()},
+        "per_entry_ms": per_op,
+        "calls_per_step": {k: v / args.steps for k, v in calls.items()},
+    }
+    if step_flop is not None:
+        line["tflops"] = step_flop / (ms * 1e-3) / 1e12
+        line["frac_of_bf16_peak" if dtype == "bf16" else "frac_of_fp32_peak"] = (
+            step_flop / (ms * 1e-3) / (PEAK_BF16 if dtype == "bf16" else 157.3e12)
+        )
+    if name == "pinn_edge":
+        line["hbm_gbs"] = per_launch / (ms * 1e-3) / 1e9
+        line["frac_of_hbm_peak"] = per_launch / (ms * 1e-3) / 8.0e12
+    elif name == "pinn_laplacian":
+        line["layer_pass_gflop"] = per_launch / 1e9
+    return line
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -114,6 +300,13 @@ def main():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(2)
 
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    if args.workload != "cheb768":
+        for name in WORKLOADS if args.workload == "all" else [args.workload]:
+            print(json.dumps(run_workload(name, args, dev)), flush=True)
+        return
+
     import kanforge_amd as kf
     from kanforge_amd.torch import KANLinear
     from kanforge_amd.torch import kernels as kmod
@@ -121,8 +314,6 @@ def main():
     timer = EntryTimer()
     kmod._raw = timer.wrap(kmod._raw)
 
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
     layer = KANLinear(IN, OUT, kf.Chebyshev(DEGREE), base_activation=None, bias=False, device=dev, dtype=torch.bfloat16)
     gen = torch.Generator().manual_seed(1)
     with torch.no_grad():

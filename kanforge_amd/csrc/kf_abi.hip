@@ -217,9 +217,11 @@ struct WsG {
   int cfg;
   bool skip0;  // Chebyshev, unweighted: T_0 = 1 taken out of the contraction (column sums of g)
   bool g96;    // bf16 Chebyshev with at most 8 features run: g96_kernel (192 x 48 x 8 tiles)
+  int nz;      // other kinds: batch splits of g_kernel (raw sums reduced by g_split_reduce when > 1)
   int64_t OUTP, BP, INP;
-  size_t gt, zt, wt, part, colsum, total;
+  size_t gt, zt, wt, part, colsum, phit, zpart, total;
 };
+constexpr size_t kGSplitBytes = size_t(256) << 20;  // cap of the split partial sums
 WsG ws_g(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, bool has_w) {
   WsG w;
   w.skip0 = b->kind == KF_KIND_CHEB && !has_w && b->n_t >= 2;
@@ -237,7 +239,22 @@ WsG ws_g(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
   w.wt = cheb && has_w ? align256((size_t)w.INP * w.BP * sizeof(float)) : 0;
   w.part = w.skip0 ? align256((size_t)((w.BP + 63) / 64) * w.OUTP * sizeof(float)) : 0;
   w.colsum = w.skip0 ? align256((size_t)w.OUTP * sizeof(float)) : 0;
-  w.total = w.gt + w.zt + w.wt + w.part + w.colsum;
+  w.phit = w.zpart = 0;
+  w.nz = 1;
+  if (!cheb) {
+    w.phit = align256((size_t)b->n_t * w.INP * w.BP * elt_size(dtype));
+    // fewer output tiles than two rounds of the 256 CUs: split the batch
+    const long tiles = (long)(w.OUTP / bm) * (w.INP / 32), stages = w.BP / eps;
+    if (tiles < 512) {
+      const size_t per = (size_t)w.OUTP * w.INP * b->n_t * sizeof(float);
+      long nz = (512 + tiles - 1) / tiles;
+      if (nz > stages) nz = stages;
+      if ((size_t)nz * per > kGSplitBytes) nz = (long)(kGSplitBytes / per);
+      w.nz = nz > 1 ? (int)nz : 1;
+    }
+    w.zpart = w.nz > 1 ? align256((size_t)w.nz * w.OUTP * w.INP * b->n_t * sizeof(float)) : 0;
+  }
+  w.total = w.gt + w.zt + w.wt + w.part + w.colsum + w.phit + w.zpart;
   return w;
 }
 
@@ -316,6 +333,34 @@ int launch_features(const KBasis& kb, int64_t batch, int64_t n_in, int64_t brows
     default: launch_features_t<T, 24, FOLDED>(kb, batch, n_in, brows, icols, x, out, sb, sj, si, b_fastest, s); break;
   }
   return check_launch("features");
+}
+
+template <typename T, int NTB>
+int launch_features_t_nb(const KBasis& kb, int64_t batch, int64_t n_in, int64_t BP, int64_t INP, const void* x,
+                         const void* w, void* phit, hipStream_t s) {
+  constexpr int BT = 128 / (int)sizeof(T);
+  const size_t lds = (size_t)kb.n_t * 32 * 144;
+  auto kern = features_t_kernel<T, NTB>;
+  if (lds > 65536 &&
+      hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+    return fail(KF_ELAUNCH, "features: cannot reserve %zu bytes of LDS", lds);
+  dim3 grid((unsigned)(INP / 32), (unsigned)((BP + BT - 1) / BT));
+  hipLaunchKernelGGL(kern, grid, dim3(kThreads), lds, s, kb, (int)batch, (int)n_in, (int)BP, (int)INP, (const T*)x,
+                     (const T*)w, (T*)phit);
+  return check_launch("features_t");
+}
+
+template <typename T>
+int launch_features_t(const KBasis& kb, int64_t batch, int64_t n_in, int64_t BP, int64_t INP, const void* x,
+                      const void* w, void* phit, hipStream_t s) {
+  if (INP % 32) return fail(KF_EINVAL, "features_t: padded input count not a multiple of 32");
+  switch (nt_bucket(kb.n_t)) {
+    case 4: return launch_features_t_nb<T, 4>(kb, batch, n_in, BP, INP, x, w, phit, s);
+    case 8: return launch_features_t_nb<T, 8>(kb, batch, n_in, BP, INP, x, w, phit, s);
+    case 12: return launch_features_t_nb<T, 12>(kb, batch, n_in, BP, INP, x, w, phit, s);
+    case 16: return launch_features_t_nb<T, 16>(kb, batch, n_in, BP, INP, x, w, phit, s);
+    default: return launch_features_t_nb<T, 24>(kb, batch, n_in, BP, INP, x, w, phit, s);
+  }
 }
 
 }  // namespace
@@ -560,7 +605,7 @@ int run_P(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
 
 template <typename T, int WMW, int WJW, int TM, int FW, int RB, bool CHEB>
 int launch_g_t(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out,
-               const void* x, const void* w, const float* zt, const float* wt, const void* gt, void* dc) {
+               const void* phit, const float* zt, const float* wt, const void* gt, void* dc, float* zpart) {
   constexpr int BM = WMW * TM * 32, NMAX = WJW * FW * 32, RS = RB + 16;
   const size_t lds_ops = (size_t)2 * (BM + NMAX) * RS, lds_red = (size_t)kb.n_t * (BM / 2) * 33 * 4;
   const size_t lds = lds_ops > lds_red ? lds_ops : lds_red;
@@ -568,22 +613,32 @@ int launch_g_t(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, int
   if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return fail(KF_ELAUNCH, "G: cannot reserve %zu bytes of LDS", lds);
   const int n_m = (int)(L.OUTP / BM), n_n = (int)((n_in + 31) / 32);
-  hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(WMW * WJW * 64), lds, s, kb, (int)batch, (int)n_in, (int)n_out,
-                     (int)L.BP, (int)L.OUTP, (const T*)x, (const T*)w, zt, wt, (const T*)gt, (T*)dc);
-  return check_launch("G");
+  hipLaunchKernelGGL(kern, dim3(n_m * n_n, L.nz), dim3(WMW * WJW * 64), lds, s, kb, (int)batch, (int)n_in,
+                     (int)n_out, (int)L.BP, (int)L.OUTP, (int)L.INP, (const T*)phit, zt, wt, (const T*)gt, (T*)dc,
+                     L.nz > 1 ? zpart : nullptr);
+  int rc = check_launch("G");
+  if (rc || L.nz == 1) return rc;
+  long n = (long)n_out * n_in * kb.K;
+  long blocks = (n + kThreads - 1) / kThreads;
+  if (blocks > 65535 * 4) blocks = 65535 * 4;
+  hipLaunchKernelGGL(g_split_reduce<T>, dim3((unsigned)blocks), dim3(kThreads), 0, s, kb, (int)n_out, (int)n_in,
+                     (int)L.OUTP, (int)L.INP, L.nz, (const float*)zpart, (T*)dc);
+  return check_launch("G split reduce");
 }
 
 template <typename T, bool CHEB>
 int launch_g_cfg(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out,
                  const void* x, const void* w, const float* zt, const float* wt, const void* gt, void* dc) {
+  // x: phiT, w: the split partial sums
+  float* zp = (float*)w;
   switch (L.cfg) {
-    case 0: return launch_g_t<T, 2, 2, 2, 2, 128, CHEB>(L, s, kb, batch, n_in, n_out, x, w, zt, wt, gt, dc);
-    case 1: return launch_g_t<T, 2, 2, 2, 3, 128, CHEB>(L, s, kb, batch, n_in, n_out, x, w, zt, wt, gt, dc);
-    case 2: return launch_g_t<T, 2, 2, 2, 4, 128, CHEB>(L, s, kb, batch, n_in, n_out, x, w, zt, wt, gt, dc);
-    case 3: return launch_g_t<T, 2, 2, 2, 5, 128, CHEB>(L, s, kb, batch, n_in, n_out, x, w, zt, wt, gt, dc);
-    case 4: return launch_g_t<T, 2, 2, 2, 6, 128, CHEB>(L, s, kb, batch, n_in, n_out, x, w, zt, wt, gt, dc);
-    case 5: return launch_g_t<T, 2, 2, 1, 8, 64, CHEB>(L, s, kb, batch, n_in, n_out, x, w, zt, wt, gt, dc);
-    default: return launch_g_t<T, 2, 2, 1, 12, 64, CHEB>(L, s, kb, batch, n_in, n_out, x, w, zt, wt, gt, dc);
+    case 0: return launch_g_t<T, 2, 2, 2, 2, 128, CHEB>(L, s, kb, batch, n_in, n_out, x, zt, wt, gt, dc, zp);
+    case 1: return launch_g_t<T, 2, 2, 2, 3, 128, CHEB>(L, s, kb, batch, n_in, n_out, x, zt, wt, gt, dc, zp);
+    case 2: return launch_g_t<T, 2, 2, 2, 4, 128, CHEB>(L, s, kb, batch, n_in, n_out, x, zt, wt, gt, dc, zp);
+    case 3: return launch_g_t<T, 2, 2, 2, 5, 128, CHEB>(L, s, kb, batch, n_in, n_out, x, zt, wt, gt, dc, zp);
+    case 4: return launch_g_t<T, 2, 2, 2, 6, 128, CHEB>(L, s, kb, batch, n_in, n_out, x, zt, wt, gt, dc, zp);
+    case 5: return launch_g_t<T, 2, 2, 1, 8, 64, CHEB>(L, s, kb, batch, n_in, n_out, x, zt, wt, gt, dc, zp);
+    default: return launch_g_t<T, 2, 2, 1, 12, 64, CHEB>(L, s, kb, batch, n_in, n_out, x, zt, wt, gt, dc, zp);
   }
 }
 
@@ -666,7 +721,12 @@ int run_G(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
       default: return launch_g_ws<T, 1, 12, 64>(L, s, kb, batch, n_in, n_out, zt, wt, gt, colsum, dc);
     }
   }
-  return launch_g_cfg<T, false>(L, s, kb, batch, n_in, n_out, x, w, nullptr, nullptr, gt, dc);
+  // other kinds: features (times w) precomputed once into phiT[j][INP][BP]
+  void* phit = base + L.gt + L.zt + L.wt + L.part + L.colsum;
+  float* zpart = L.nz > 1 ? (float*)((char*)phit + L.phit) : nullptr;
+  rc = launch_features_t<T>(kb, batch, n_in, L.BP, L.INP, x, w, phit, s);
+  if (rc) return rc;
+  return launch_g_cfg<T, false>(L, s, kb, batch, n_in, n_out, phit, zpart, nullptr, nullptr, gt, dc);
 }
 
 template <typename T, int KM>

@@ -752,12 +752,19 @@ __global__ __launch_bounds__(WAVES_M* WAVES_J * 64) void p_kernel(KBasis bs, int
 // rows. The B tile (features, batch contiguous) is generated per stage by
 // every thread: input gi, 8 (bf16) or 4 (f32) consecutive rows; Chebyshev
 // features come from z^T by the recurrence, other kinds from x.
+// G for every basis kind. CHEB: features generated per stage from zT (and
+// wT); otherwise the stage's feature rows are copied from phiT[j][INP][BP]
+// (features_t_kernel), exactly like the gT rows. blockIdx.y splits the batch
+// stages: with gridDim.y > 1 each split writes its raw feature sums to
+// part[z][o][i][j] (float32) and g_split_reduce applies the fold; with one
+// split the fold runs in the epilogue and dc is written directly.
 template <typename T, int WAVES_M, int WAVES_J, int TM, int FW, int RB, bool CHEB>
 __global__ __launch_bounds__(WAVES_M* WAVES_J * 64) void g_kernel(KBasis bs, int B, int IN, int OUT, int BP, int OUTP,
-                                                                 const T* __restrict__ x, const T* __restrict__ w,
+                                                                 int INP, const T* __restrict__ phit,
                                                                  const float* __restrict__ zt,
                                                                  const float* __restrict__ wt,
-                                                                 const T* __restrict__ gt, T* __restrict__ dc) {
+                                                                 const T* __restrict__ gt, T* __restrict__ dc,
+                                                                 float* __restrict__ part) {
   constexpr int NTH = WAVES_M * WAVES_J * 64;
   constexpr int BM = WAVES_M * TM * 32;
   constexpr int RS = RB + 16, FS = RB / 32;
@@ -766,6 +773,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_J * 64) void g_kernel(KBasis bs, int
   constexpr int NTB = WAVES_J * FW;
   constexpr int NMAX = NTB * 32;
   constexpr int ACH = BM * (RB / 16), APT = (ACH + NTH - 1) / NTH;
+  constexpr int BCH = NMAX * (RB / 16), BPT = CHEB ? 1 : (BCH + NTH - 1) / NTH;
   constexpr int GTASK = 32 * (EPS / PL);  // generator tasks per stage
   static_assert(GTASK <= NTH, "one generator task per thread");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -790,9 +798,9 @@ __global__ __launch_bounds__(WAVES_M* WAVES_J * 64) void g_kernel(KBasis bs, int
       for (int r = 0; r < 16; ++r) acc[a][f][r] = 0.f;
 
   const int gi = tid % 32, gq = tid / 32;  // generator: input gi, rows gq*PL .. +PL of the stage
-  const bool gen_on = tid < GTASK;
+  const bool gen_on = CHEB && tid < GTASK;
   const int gin = i0 + gi;
-  u32x4 ast[APT];
+  u32x4 ast[APT], bst[BPT];
   float fz[PL], fw[PL];
   auto load = [&](int bc0) {
 #pragma unroll
@@ -817,13 +825,15 @@ __global__ __launch_bounds__(WAVES_M* WAVES_J * 64) void g_kernel(KBasis bs, int
             for (int u = 0; u < 4; ++u) fw[4 * q + u] = v2[u];
           }
         }
-      } else {
+      }
+    }
+    if (!CHEB) {
 #pragma unroll
-        for (int u = 0; u < PL; ++u) {
-          const bool ok = b + u < B && gin < IN;
-          fz[u] = ok ? to_f32(x[(size_t)(b + u) * IN + gin]) : 0.f;
-          fw[u] = ok ? (w ? to_f32(w[(size_t)(b + u) * IN + gin]) : 1.f) : 0.f;
-        }
+      for (int u = 0; u < BPT; ++u) {
+        const int e = tid + u * NTH;
+        const int r = e / (RB / 16), q = e % (RB / 16), j = r / 32;
+        const bool ok = e < BCH && j < bs.n_t;
+        bst[u] = gload16(phit + ((size_t)(ok ? j : 0) * INP + i0 + r % 32) * BP + bc0 + q * PL, ok);
       }
     }
   };
@@ -862,26 +872,28 @@ __global__ __launch_bounds__(WAVES_M* WAVES_J * 64) void g_kernel(KBasis bs, int
           for (int u = 0; u < PL; ++u) tp[u] = fmaf(z2[u], tc[u], -tp[u]);
           lds_write16(dst + (size_t)(NTB - 1) * 32 * RS, pack16<T>(tp));
         }
-      } else {
-        // one element at a time: all its features, scattered as single elements
-        T* dst_t = reinterpret_cast<T*>(dst);
-        for (int u = 0; u < PL; ++u) {
-          float f[NTB];
-          kernel_features<NTB>(fz[u], fw[u], gin < IN ? gin : 0, bs, f);
+      }
+    }
+    if (!CHEB) {
 #pragma unroll
-          for (int j = 0; j < NTB; ++j) dst_t[(size_t)j * 32 * RS / sizeof(T) + u] = from_f32<T>(f[j]);
-        }
+      for (int u = 0; u < BPT; ++u) {
+        const int e = tid + u * NTH;
+        if (e < BCH) lds_write16(Bs + (size_t)(buf * NMAX + e / (RB / 16)) * RS + 16 * (e % (RB / 16)), bst[u]);
       }
     }
   };
 
-  const int S = BP / EPS;
-  load(0);
-  store(0);
+  // this split's stages [s_lo, s_hi)
+  const int S_all = BP / EPS, nz = gridDim.y, z = blockIdx.y;
+  const int s_lo = (int)((long)S_all * z / nz), s_hi = (int)((long)S_all * (z + 1) / nz);
+  if (s_lo < s_hi) {
+    load(s_lo * EPS);
+    store(0);
+  }
   __syncthreads();
-  for (int s = 0; s < S; ++s) {
-    const int buf = s & 1;
-    if (s + 1 < S) load((s + 1) * EPS);
+  for (int s = s_lo; s < s_hi; ++s) {
+    const int buf = (s - s_lo) & 1;
+    if (s + 1 < s_hi) load((s + 1) * EPS);
 #pragma unroll
     for (int fs = 0; fs < FS; ++fs) {
       u32x4 af[TM];
@@ -896,7 +908,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_J * 64) void g_kernel(KBasis bs, int
         for (int a = 0; a < TM; ++a) mma32<T>(acc[a][f], af[a], bf);
       }
     }
-    if (s + 1 < S) store(buf ^ 1);
+    if (s + 1 < s_hi) store(buf ^ 1);
     __syncthreads();
   }
 
@@ -919,16 +931,82 @@ __global__ __launch_bounds__(WAVES_M* WAVES_J * 64) void g_kernel(KBasis bs, int
         }
       }
     __syncthreads();
-    for (int e = tid; e < HM * 32 * K; e += NTH) {
-      const int k = e % K, il = (e / K) % 32, row = e / (K * 32);
-      const int o = o0 + half * HM + row, i = i0 + il;
-      if (o < OUT && i < IN) {
-        float sum = 0.f;
-        for (int j = 0; j < n_t; ++j) sum = fmaf(bs.fold[k * KF_MAX_NT + j], red[(j * HM + row) * 33 + il], sum);
-        dc[((size_t)o * IN + i) * K + k] = from_f32<T>(sum);
+    if (part) {
+      for (int e = tid; e < HM * 32 * n_t; e += NTH) {
+        const int j = e % n_t, il = (e / n_t) % 32, row = e / (n_t * 32);
+        const int o = o0 + half * HM + row, i = i0 + il;
+        if (o < OUT && i < IN) part[(((size_t)z * OUTP + o) * INP + i) * n_t + j] = red[(j * HM + row) * 33 + il];
+      }
+    } else {
+      for (int e = tid; e < HM * 32 * K; e += NTH) {
+        const int k = e % K, il = (e / K) % 32, row = e / (K * 32);
+        const int o = o0 + half * HM + row, i = i0 + il;
+        if (o < OUT && i < IN) {
+          float sum = 0.f;
+          for (int j = 0; j < n_t; ++j) sum = fmaf(bs.fold[k * KF_MAX_NT + j], red[(j * HM + row) * 33 + il], sum);
+          dc[((size_t)o * IN + i) * K + k] = from_f32<T>(sum);
+        }
       }
     }
     __syncthreads();
+  }
+}
+
+// dc[o][i][k] = sum_z sum_j fold[k][j] part[z][o][i][j]: the fold and the sum
+// over the batch splits of g_kernel, in a fixed order (deterministic).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void g_split_reduce(KBasis bs, int OUT, int IN, int OUTP, int INP, int nz,
+                                                           const float* __restrict__ part, T* __restrict__ dc) {
+  const int K = bs.K, n_t = bs.n_t;
+  const long n = (long)OUT * IN * K;
+  const size_t zstride = (size_t)OUTP * INP * n_t;
+  for (long e = blockIdx.x * (long)kThreads + threadIdx.x; e < n; e += (long)gridDim.x * kThreads) {
+    const int k = (int)(e % K);
+    const long oi = e / K;
+    const int i = (int)(oi % IN), o = (int)(oi / IN);
+    const float* p = part + ((size_t)o * INP + i) * n_t;
+    float sum = 0.f;
+    for (int zz = 0; zz < nz; ++zz, p += zstride) {
+      float t = 0.f;
+      for (int j = 0; j < n_t; ++j) t = fmaf(bs.fold[k * KF_MAX_NT + j], p[j], t);
+      sum += t;
+    }
+    dc[e] = from_f32<T>(sum);
+  }
+}
+
+// phiT[j][i][b] = w[b][i] * feature_j(x[b][i]) for j < n_t, zero where
+// b >= B or i >= IN, over the padded (INP, BP) extent: the B operand of G for
+// kinds whose features are not generated in the G kernel. A block covers 32
+// inputs x (128 / sizeof(T)) rows: x is read along the inputs, each element's
+// features go to LDS, and every (j, i) row segment leaves as one 128-byte
+// run along the batch.
+template <typename T, int NTB>
+__global__ __launch_bounds__(kThreads) void features_t_kernel(KBasis bs, int B, int IN, int BP, int INP,
+                                                              const T* __restrict__ x, const T* __restrict__ w,
+                                                              T* __restrict__ phit) {
+  constexpr int BT = 128 / (int)sizeof(T), RSB = 144, PER = 32 * BT / kThreads, VW = 16 / (int)sizeof(T);
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];  // [n_t][32][RSB]
+  const int n_t = bs.n_t;
+  const int i0 = blockIdx.x * 32, b0 = blockIdx.y * BT;
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int e = threadIdx.x + u * kThreads;
+    const int il = e % 32, bl = e / 32, i = i0 + il, b = b0 + bl;
+    const bool ok = b < B && i < IN;
+    const float xv = ok ? to_f32(x[(size_t)b * IN + i]) : 0.f;
+    const float wv = ok ? (w ? to_f32(w[(size_t)b * IN + i]) : 1.f) : 0.f;
+    float f[NTB];
+    kernel_features<NTB>(xv, wv, ok ? i : 0, bs, f);
+#pragma unroll
+    for (int j = 0; j < NTB; ++j)
+      if (j < n_t) reinterpret_cast<T*>(smem + (size_t)(j * 32 + il) * RSB)[bl] = from_f32<T>(ok ? f[j] : 0.f);
+  }
+  __syncthreads();
+  const int total = n_t * 32 * 8;
+  for (int c = threadIdx.x; c < total; c += kThreads) {
+    const int r = c / 8, q = c % 8, j = r / 32, il = r % 32, b = b0 + q * VW;
+    if (b < BP) gstore16(phit + ((size_t)j * INP + i0 + il) * BP + b, lds_read16(smem + (size_t)r * RSB + 16 * q));
   }
 }
 
