@@ -206,7 +206,8 @@ WsP ws_p(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
   w.cfg = fw_index(b->n_t);
   w.ntb = 2 * FW_LIST[w.cfg];
   w.p8 = b->kind == KF_KIND_CHEB && dtype == KF_BF16 && w.ntb == 8;
-  w.INP = round_up(n_in, w.p8 ? 96 : 32);  // 96: whole tiles of p8_kernel (48) and p_dma_kernel (32)
+  // 96: whole tiles of p8_kernel (48) and p_dma_kernel (32); rational: flat tiles of 2 FW x 32 inputs
+  w.INP = round_up(n_in, w.p8 ? 96 : b->kind == KF_KIND_RATIONAL ? 64 * FW_LIST[w.cfg] : 32);
   w.OUTP = round_up(n_out, p_uses_dma(w.cfg) ? p_stage_cols(dtype) : 32);
   w.cfmt = align256((size_t)w.ntb * w.INP * w.OUTP * elt_size(dtype));
   w.gpad = p_uses_dma(w.cfg) && p_needs_gpad(n_out, dtype) ? align256((size_t)batch * w.OUTP * elt_size(dtype)) : 0;
@@ -217,23 +218,39 @@ struct WsG {
   int cfg;
   bool skip0;  // Chebyshev, unweighted: T_0 = 1 taken out of the contraction (column sums of g)
   bool g96;    // bf16 Chebyshev with at most 8 features run: g96_kernel (192 x 48 x 8 tiles)
-  int nz;      // other kinds: batch splits of g_kernel (raw sums reduced by g_split_reduce when > 1)
+  bool pre;    // features precomputed into phiT (other kinds, and Chebyshev plans on small grids)
+  int nz;      // pre: batch splits of g_kernel (raw sums reduced by g_split_reduce when > 1)
   int64_t OUTP, BP, INP;
   size_t gt, zt, wt, part, colsum, phit, zpart, total;
 };
 constexpr size_t kGSplitBytes = size_t(256) << 20;  // cap of the split partial sums
 WsG ws_g(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, bool has_w) {
   WsG w;
-  w.skip0 = b->kind == KF_KIND_CHEB && !has_w && b->n_t >= 2;
+  const bool cheb_kind = b->kind == KF_KIND_CHEB;
+  w.skip0 = cheb_kind && !has_w && b->n_t >= 2;
   w.cfg = fw_index(b->n_t - (w.skip0 ? 1 : 0));
-  w.g96 = b->kind == KF_KIND_CHEB && dtype == KF_BF16 && b->n_t - (w.skip0 ? 1 : 0) <= 8;
+  w.g96 = cheb_kind && dtype == KF_BF16 && b->n_t - (w.skip0 ? 1 : 0) <= 8;
+  w.pre = !cheb_kind;
+  if (cheb_kind) {
+    // the Chebyshev kernels keep one workgroup per output tile over the whole batch;
+    // with fewer than 128 tiles the batch-split precomputed-feature path fills the chip
+    const int fw = FW_LIST[w.cfg];
+    const long bm = w.g96 ? 192 : 2 * g_tm(fw) * 32, bn = w.g96 ? 48 : 32;
+    const long tiles = (round_up(n_out, bm) / bm) * (round_up(n_in, bn) / bn);
+    if (tiles < 128) {
+      w.pre = true;
+      w.skip0 = w.g96 = false;
+      w.cfg = fw_index(b->n_t);
+    }
+  }
   const int fw = FW_LIST[w.cfg];
   const int bm = w.g96 ? 192 : 2 * g_tm(fw) * 32;
   const int eps = w.g96 ? 32 : g_rb(fw) / elt_size(dtype);
   w.OUTP = round_up(n_out, bm);
   w.BP = round_up(batch, eps);
-  w.INP = round_up(n_in, w.g96 ? 48 : 32);
-  const bool cheb = b->kind == KF_KIND_CHEB;
+  const bool flat = b->kind == KF_KIND_RATIONAL;  // g_kernel's flat tiles: 2 FW x 32 inputs
+  w.INP = round_up(n_in, w.g96 ? 48 : flat ? 64 * fw : 32);
+  const bool cheb = cheb_kind && !w.pre;
   w.gt = align256((size_t)w.OUTP * w.BP * elt_size(dtype));
   w.zt = cheb ? align256((size_t)w.INP * w.BP * sizeof(float)) : 0;
   w.wt = cheb && has_w ? align256((size_t)w.INP * w.BP * sizeof(float)) : 0;
@@ -241,10 +258,10 @@ WsG ws_g(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
   w.colsum = w.skip0 ? align256((size_t)w.OUTP * sizeof(float)) : 0;
   w.phit = w.zpart = 0;
   w.nz = 1;
-  if (!cheb) {
+  if (w.pre) {
     w.phit = align256((size_t)b->n_t * w.INP * w.BP * elt_size(dtype));
     // fewer output tiles than two rounds of the 256 CUs: split the batch
-    const long tiles = (long)(w.OUTP / bm) * (w.INP / 32), stages = w.BP / eps;
+    const long tiles = (long)(w.OUTP / bm) * (w.INP / (flat ? 64 * fw : 32)), stages = w.BP / eps;
     if (tiles < 512) {
       const size_t per = (size_t)w.OUTP * w.INP * b->n_t * sizeof(float);
       long nz = (512 + tiles - 1) / tiles;
@@ -529,7 +546,9 @@ int launch_p_dma_kind(const WsP& L, hipStream_t s, const KBasis& kb, int64_t bat
   auto kern = p_dma_kernel<T, TM, FW, KIND>;
   if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return fail(KF_ELAUNCH, "P: cannot reserve %zu bytes of LDS", lds);
-  const int n_m = (int)((batch + BM - 1) / BM), n_n = (int)(L.INP / 32);
+  constexpr int TI = KIND == KF_KIND_RATIONAL ? 64 * FW : 32;  // inputs per tile (flat for rational)
+  if (L.INP % TI) return fail(KF_EINVAL, "P: workspace layout not aligned");
+  const int n_m = (int)((batch + BM - 1) / BM), n_n = (int)(L.INP / TI);
   hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(256), lds, s, kb, (int)batch, (int)n_in, (int)L.INP, (int)L.OUTP,
                      (const T*)x, (const T*)g, gstride, (const T*)cfmt, (T*)p, h);
   return check_launch("P");
@@ -603,16 +622,19 @@ int run_P(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
   }
 }
 
-template <typename T, int WMW, int WJW, int TM, int FW, int RB, bool CHEB>
+template <typename T, int WMW, int WJW, int TM, int FW, int RB, bool CHEB, bool FLAT = false>
 int launch_g_t(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out,
                const void* phit, const float* zt, const float* wt, const void* gt, void* dc, float* zpart) {
   constexpr int BM = WMW * TM * 32, NMAX = WJW * FW * 32, RS = RB + 16;
-  const size_t lds_ops = (size_t)2 * (BM + NMAX) * RS, lds_red = (size_t)kb.n_t * (BM / 2) * 33 * 4;
+  const size_t lds_ops = (size_t)2 * (BM + NMAX) * RS;
+  const size_t lds_red = (size_t)(FLAT ? NMAX / 32 : kb.n_t) * (BM / 2) * 33 * 4;
   const size_t lds = lds_ops > lds_red ? lds_ops : lds_red;
-  auto kern = g_kernel<T, WMW, WJW, TM, FW, RB, CHEB>;
+  auto kern = g_kernel<T, WMW, WJW, TM, FW, RB, CHEB, FLAT>;
   if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return fail(KF_ELAUNCH, "G: cannot reserve %zu bytes of LDS", lds);
-  const int n_m = (int)(L.OUTP / BM), n_n = (int)((n_in + 31) / 32);
+  constexpr int TI = FLAT ? NMAX : 32;
+  if (FLAT && L.INP % TI) return fail(KF_EINVAL, "G: workspace layout not aligned");
+  const int n_m = (int)(L.OUTP / BM), n_n = (int)((n_in + TI - 1) / TI);
   hipLaunchKernelGGL(kern, dim3(n_m * n_n, L.nz), dim3(WMW * WJW * 64), lds, s, kb, (int)batch, (int)n_in,
                      (int)n_out, (int)L.BP, (int)L.OUTP, (int)L.INP, (const T*)phit, zt, wt, (const T*)gt, (T*)dc,
                      L.nz > 1 ? zpart : nullptr);
@@ -631,6 +653,10 @@ int launch_g_cfg(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, i
                  const void* x, const void* w, const float* zt, const float* wt, const void* gt, void* dc) {
   // x: phiT, w: the split partial sums
   float* zp = (float*)w;
+  if (!CHEB && kb.kind == KF_KIND_RATIONAL) {
+    if (L.cfg != 0) return fail(KF_EINVAL, "G: rational plans have one feature");
+    return launch_g_t<T, 2, 2, 2, 2, 128, false, true>(L, s, kb, batch, n_in, n_out, x, zt, wt, gt, dc, zp);
+  }
   switch (L.cfg) {
     case 0: return launch_g_t<T, 2, 2, 2, 2, 128, CHEB>(L, s, kb, batch, n_in, n_out, x, zt, wt, gt, dc, zp);
     case 1: return launch_g_t<T, 2, 2, 2, 3, 128, CHEB>(L, s, kb, batch, n_in, n_out, x, zt, wt, gt, dc, zp);
@@ -682,9 +708,10 @@ int launch_g96(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, int
 template <typename T>
 int run_G(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
           const void* g, const void* w, void* dc, void* ws, hipStream_t s) {
-  const bool cheb = kb.kind == KF_KIND_CHEB;
-  const bool weighted = w != nullptr || (cheb && kb.input_map == KF_MAP_TANH_SQ);
+  const bool cheb_kind = kb.kind == KF_KIND_CHEB;
+  const bool weighted = w != nullptr || (cheb_kind && kb.input_map == KF_MAP_TANH_SQ);
   WsG L = ws_g(b, dtype, batch, n_in, n_out, weighted);
+  const bool cheb = cheb_kind && !L.pre;
   char* base = (char*)ws;
   void* gt = base;
   float* zt = cheb ? (float*)(base + L.gt) : nullptr;
@@ -732,8 +759,11 @@ int run_G(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
 template <typename T, int KM>
 void launch_edge_t(const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* c,
                    const void* bw, void* out, hipStream_t s) {
-  dim3 grid((unsigned)((n_in + 63) / 64), (unsigned)((batch + 7) / 8));
-  hipLaunchKernelGGL((edge_kernel<T, KM>), grid, dim3(kThreads), 0, s, kb, (int)batch, (int)n_in, (int)n_out,
+  constexpr int ROWS = KM <= 8 ? 32 : 16;  // edge_kernel's block: ROWS rows x IW inputs
+  int iw = 32;
+  while (iw / 2 >= n_in && iw > 1) iw /= 2;  // narrow layers: the power of two >= n_in
+  dim3 grid((unsigned)((n_in + iw - 1) / iw), (unsigned)((batch + ROWS - 1) / ROWS));
+  hipLaunchKernelGGL((edge_kernel<T, KM>), grid, dim3(kThreads), 0, s, kb, (int)batch, (int)n_in, (int)n_out, iw,
                      (const T*)x, (const T*)c, (const T*)bw, (T*)out);
 }
 

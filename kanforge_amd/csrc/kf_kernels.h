@@ -758,7 +758,9 @@ __global__ __launch_bounds__(WAVES_M* WAVES_J * 64) void p_kernel(KBasis bs, int
 // stages: with gridDim.y > 1 each split writes its raw feature sums to
 // part[z][o][i][j] (float32) and g_split_reduce applies the fold; with one
 // split the fold runs in the epilogue and dc is written directly.
-template <typename T, int WAVES_M, int WAVES_J, int TM, int FW, int RB, bool CHEB>
+// FLAT (single-feature kinds, n_t = 1): the tile's NTB feature slots hold
+// NTB x 32 consecutive inputs of feature 0 instead of NTB features of 32.
+template <typename T, int WAVES_M, int WAVES_J, int TM, int FW, int RB, bool CHEB, bool FLAT = false>
 __global__ __launch_bounds__(WAVES_M* WAVES_J * 64) void g_kernel(KBasis bs, int B, int IN, int OUT, int BP, int OUTP,
                                                                  int INP, const T* __restrict__ phit,
                                                                  const float* __restrict__ zt,
@@ -780,10 +782,12 @@ __global__ __launch_bounds__(WAVES_M* WAVES_J * 64) void g_kernel(KBasis bs, int
   unsigned char* As = smem;                // [2][BM][RS]
   unsigned char* Bs = smem + 2 * BM * RS;  // [2][NMAX][RS]
 
-  const int n_m = OUTP / BM, n_n = (IN + 31) / 32;
+  static_assert(!(FLAT && CHEB), "flat tiles are for precomputed single-feature kinds");
+  constexpr int TI = FLAT ? NMAX : 32;  // inputs per tile
+  const int n_m = OUTP / BM, n_n = (IN + TI - 1) / TI;
   int tm_, tn_;
   xcd_tile(blockIdx.x, n_m, n_n, tm_, tn_);
-  const int o0 = tm_ * BM, i0 = tn_ * 32;
+  const int o0 = tm_ * BM, i0 = tn_ * TI;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WAVES_J, wj = wave % WAVES_J;
   const int h = lane >> 5, l32 = lane & 31;
@@ -832,8 +836,9 @@ __global__ __launch_bounds__(WAVES_M* WAVES_J * 64) void g_kernel(KBasis bs, int
       for (int u = 0; u < BPT; ++u) {
         const int e = tid + u * NTH;
         const int r = e / (RB / 16), q = e % (RB / 16), j = r / 32;
-        const bool ok = e < BCH && j < bs.n_t;
-        bst[u] = gload16(phit + ((size_t)(ok ? j : 0) * INP + i0 + r % 32) * BP + bc0 + q * PL, ok);
+        const bool ok = e < BCH && (FLAT || j < bs.n_t);
+        const size_t row = FLAT ? (size_t)i0 + r : (size_t)(ok ? j : 0) * INP + i0 + r % 32;
+        bst[u] = gload16(phit + (ok ? row : 0) * BP + bc0 + q * PL, ok);
       }
     }
   };
@@ -926,12 +931,25 @@ __global__ __launch_bounds__(WAVES_M* WAVES_J * 64) void g_kernel(KBasis bs, int
 #pragma unroll
           for (int f = 0; f < FW; ++f) {
             const int j = wj * FW + f;
-            if (j < n_t) red[(j * HM + row % HM) * 33 + l32] = acc[a][f][r];
+            if (FLAT || j < n_t) red[(j * HM + row % HM) * 33 + l32] = acc[a][f][r];
           }
         }
       }
     __syncthreads();
-    if (part) {
+    if (FLAT) {
+      // input i0 + il is slot il / 32, lane il % 32; K = n_t = 1 and the fold is 1
+      for (int e = tid; e < HM * TI; e += NTH) {
+        const int il = e % TI, row = e / TI;
+        const int o = o0 + half * HM + row, i = i0 + il;
+        if (o < OUT && i < IN) {
+          const float v = red[((il / 32) * HM + row) * 33 + il % 32];
+          if (part)
+            part[((size_t)z * OUTP + o) * INP + i] = v;
+          else
+            dc[(size_t)o * IN + i] = from_f32<T>(v);
+        }
+      }
+    } else if (part) {
       for (int e = tid; e < HM * 32 * n_t; e += NTH) {
         const int j = e % n_t, il = (e / n_t) % 32, row = e / (n_t * 32);
         const int o = o0 + half * HM + row, i = i0 + il;
@@ -1374,10 +1392,13 @@ __global__ __launch_bounds__(256) void p_dma_kernel(KBasis bs, int B, int IN, in
   static_assert(2 * SS <= 160 * 1024 && 3 * BM * 33 * 4 <= 160 * 1024, "two stages and the epilogue fit in LDS");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];  // [2][SS], later x and the sums
 
-  const int n_m = (B + BM - 1) / BM, n_n = INP / 32;
+  // single-feature kinds (rational): the NTB slots hold NTB x 32 consecutive inputs
+  constexpr bool FLAT = KIND == KF_KIND_RATIONAL;
+  constexpr int TI = FLAT ? NTB * 32 : 32;  // inputs per tile
+  const int n_m = (B + BM - 1) / BM, n_n = INP / TI;
   int tm_, tn_;
   xcd_tile_grouped(blockIdx.x, n_m, n_n, 8, tm_, tn_);
-  const int b0 = tm_ * BM, i0 = tn_ * 32;
+  const int b0 = tm_ * BM, i0 = tn_ * TI;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wj = wave & 1;
@@ -1404,7 +1425,7 @@ __global__ __launch_bounds__(256) void p_dma_kernel(KBasis bs, int B, int IN, in
       src[k] = g + (size_t)b * gstride + c * EPC;
     } else {
       const int rr = row - BM, j = rr / 32, il = rr % 32;
-      src[k] = cfmt + ((size_t)j * INP + i0 + il) * OUTP + c * EPC;
+      src[k] = cfmt + (FLAT ? (size_t)i0 + rr : (size_t)j * INP + i0 + il) * OUTP + c * EPC;
     }
   }
   auto copy_stage = [&](int st) {
@@ -1466,6 +1487,26 @@ __global__ __launch_bounds__(256) void p_dma_kernel(KBasis bs, int B, int IN, in
     mma_rest((KS - 1) & 1);
   }
   vmem_wait<0>();
+  if constexpr (FLAT) {
+    // every (row, input) has one accumulator: p = f_0(x) H, written from registers
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int b = b0 + wm * WM + a * 32 + acc_row(r, lane);
+#pragma unroll
+        for (int q = 0; q < FW; ++q) {
+          const int i = i0 + (wj * FW + q) * 32 + l32;
+          if (b < B && i < IN) {
+            float f[NTB];
+            kind_features<KIND, NTB>(to_f32(x[(size_t)b * IN + i]), 1.f, i, bs, f);
+            p[(size_t)b * IN + i] = from_f32<T>(f[0] * acc[a][q][r]);
+            if (hout) hout[(size_t)b * IN + i] = acc[a][q][r];
+          }
+        }
+      }
+    return;
+  }
   __syncthreads();  // every wave is done with the stage buffers: reuse them for x and the group sums
 
   // x of the tile into LDS, all loads in flight at once (coalesced along the inputs)
@@ -2144,20 +2185,26 @@ __global__ __launch_bounds__(512) void g_ws_kernel(KBasis bs, int B, int IN, int
 
 // ---------------------------------------------------------------------------
 // edge_derivative: out[b,o,i] = sum_k c[o,i,k] phi_k^(m)(x[b,i]) + W[o,i] silu^(m)(x[b,i])
-// Block: ROWS batch rows x 64 inputs, all outputs. Phase 1 evaluates the
-// features into LDS; phase 2 streams the outputs, i fastest (coalesced).
+// Block: ROWS batch rows x IW inputs (IW = 32, or the power of two >= IN for
+// narrower layers), all outputs. Phase 1 evaluates the features into LDS.
+// Phase 2: a half-wave covers IW inputs x 32/IW consecutive outputs, i.e. 32
+// consecutive output elements of a row (128-byte runs in float32); each
+// thread holds the coefficients of OG such outputs in registers and streams
+// rows for them, so one coefficient read serves many stores. With fewer
+// output groups than the block's 8 half-wave groups, the rows are split
+// among them instead.
 template <typename T, int KM>
-__global__ __launch_bounds__(kThreads) void edge_kernel(KBasis bs, int B, int IN, int OUT, const T* __restrict__ x,
-                                                        const T* __restrict__ c, const T* __restrict__ bw,
-                                                        T* __restrict__ out) {
-  constexpr int ROWS = 8, IT = 64, OG = 4;
-  constexpr int FS = KM + 1;  // features + silu slot
-  __shared__ float feat[ROWS][IT][FS + 1];
-  const int b0 = blockIdx.y * ROWS, i0 = blockIdx.x * IT;
+__global__ __launch_bounds__(kThreads) void edge_kernel(KBasis bs, int B, int IN, int OUT, int IW,
+                                                        const T* __restrict__ x, const T* __restrict__ c,
+                                                        const T* __restrict__ bw, T* __restrict__ out) {
+  constexpr int ROWS = KM <= 8 ? 32 : 16, IT = 32, OG = 8, NG = kThreads / 32;
+  constexpr int FS = (KM + 1) | 1;  // features + silu slot, odd stride (no LDS bank conflicts)
+  __shared__ float feat[ROWS][IT][FS];
+  const int b0 = blockIdx.y * ROWS, i0 = blockIdx.x * IW;
   const int tid = threadIdx.x;
   const int K = bs.K, m = bs.order;
-  for (int e = tid; e < ROWS * IT; e += kThreads) {
-    const int r = e / IT, il = e % IT;
+  for (int e = tid; e < ROWS * IW; e += kThreads) {
+    const int r = e / IW, il = e % IW;
     const int b = b0 + r, i = i0 + il;
     const bool ok = b < B && i < IN;
     const float xv = ok ? to_f32(x[(size_t)b * IN + i]) : 0.f;
@@ -2168,33 +2215,36 @@ __global__ __launch_bounds__(kThreads) void edge_kernel(KBasis bs, int B, int IN
     feat[r][il][KM] = (ok && bw) ? silu_derivative(xv, m) : 0.f;
   }
   __syncthreads();
-  const int il = tid % IT, og0 = tid / IT;  // 4 groups of outputs in parallel
+  const int lane32 = tid % 32, grp = tid / 32;
+  const int il = lane32 % IW, osub = lane32 / IW, OS = 32 / IW;
   const int i = i0 + il;
   if (i >= IN) return;
-  const int n_groups = (OUT + OG - 1) / OG;
-  for (int og = og0; og < n_groups; og += kThreads / IT) {
+  const int rows = B - b0 < ROWS ? B - b0 : ROWS;
+  const int n_groups = (OUT + OG * OS - 1) / (OG * OS);
+  const int RC = n_groups >= NG ? 1 : NG / n_groups;  // row interleave per output group
+  for (int item = grp; item < n_groups * RC; item += NG) {
+    const int og = item / RC, rc = item % RC;
     float cv[OG][KM], wv[OG];
 #pragma unroll
     for (int u = 0; u < OG; ++u) {
-      const int o = og * OG + u;
+      const int o = (og * OG + u) * OS + osub;
 #pragma unroll
       for (int k = 0; k < KM; ++k) cv[u][k] = (o < OUT && k < K) ? to_f32(c[((size_t)o * IN + i) * K + k]) : 0.f;
       wv[u] = (o < OUT && bw) ? to_f32(bw[(size_t)o * IN + i]) : 0.f;
     }
-    for (int r = 0; r < ROWS; ++r) {
+    for (int r = rc; r < rows; r += RC) {
       const int b = b0 + r;
-      if (b >= B) break;
       float fv[KM + 1];
 #pragma unroll
       for (int k = 0; k <= KM; ++k) fv[k] = feat[r][il][k];
 #pragma unroll
       for (int u = 0; u < OG; ++u) {
-        const int o = og * OG + u;
+        const int o = (og * OG + u) * OS + osub;
         if (o < OUT) {
-          float s = wv[u] * fv[KM];
+          float sv = wv[u] * fv[KM];
 #pragma unroll
-          for (int k = 0; k < KM; ++k) s = fmaf(cv[u][k], fv[k], s);
-          out[((size_t)b * OUT + o) * IN + i] = from_f32<T>(s);
+          for (int k = 0; k < KM; ++k) sv = fmaf(cv[u][k], fv[k], sv);
+          __builtin_nontemporal_store(from_f32<T>(sv), out + ((size_t)b * OUT + o) * IN + i);
         }
       }
     }

@@ -20,7 +20,7 @@ pytestmark = pytest.mark.gpu
 
 TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2}
 DTYPES = [torch.float32, torch.bfloat16]
-SHAPES = [(150, 45, 70), (256, 64, 128)]
+SHAPES = [(150, 45, 70), (256, 64, 128), (300, 265, 40)]  # ragged, aligned, several input tiles
 
 
 def setup(name, B, IN, seed=0):
@@ -61,7 +61,7 @@ PRIM_CASES = [
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16"])
-@pytest.mark.parametrize("shape", SHAPES, ids=["ragged", "aligned"])
+@pytest.mark.parametrize("shape", SHAPES, ids=["ragged", "aligned", "wide"])
 @pytest.mark.parametrize("name,m", PRIM_CASES)
 def test_F_matches_oracle(name, m, shape, dtype):
     B, IN, OUT = shape
@@ -77,7 +77,7 @@ def test_F_matches_oracle(name, m, shape, dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16"])
-@pytest.mark.parametrize("shape", SHAPES, ids=["ragged", "aligned"])
+@pytest.mark.parametrize("shape", SHAPES, ids=["ragged", "aligned", "wide"])
 @pytest.mark.parametrize("name,m", PRIM_CASES)
 def test_G_matches_oracle(name, m, shape, dtype):
     B, IN, OUT = shape
@@ -93,7 +93,7 @@ def test_G_matches_oracle(name, m, shape, dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16"])
-@pytest.mark.parametrize("shape", SHAPES, ids=["ragged", "aligned"])
+@pytest.mark.parametrize("shape", SHAPES, ids=["ragged", "aligned", "wide"])
 @pytest.mark.parametrize("name,m", PRIM_CASES)
 def test_P_matches_oracle(name, m, shape, dtype):
     B, IN, OUT = shape
@@ -148,6 +148,21 @@ def test_edge_derivative_matches_oracle(name, m, base, dtype):
     bw = rng.normal(0, 0.5, (OUT, IN)) if base else None
     d = K._edge_raw(plan, m, st, to_dev(x, dtype), to_dev(c, dtype), None if bw is None else to_dev(bw, dtype))
     want = o.edge_derivative(rounded(x, dtype), rounded(c, dtype), ob, m, None if bw is None else rounded(bw, dtype))
+    assert d.shape == want.shape
+    assert err(d, want) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16"])
+@pytest.mark.parametrize("name,m", [("jacobi6", 2), ("bspline53", 1), ("rational", 1)])
+@pytest.mark.parametrize("shape", [(70, 2, 64), (70, 64, 1), (33, 3, 5), (40, 1, 1)], ids=["2to64", "64to1", "3to5", "1to1"])
+def test_edge_derivative_narrow_layers(shape, name, m, dtype):
+    """Layers narrower than a half-wave in inputs or outputs (the PINN's first and last layers)."""
+    B, IN, OUT = shape
+    basis, plan, st, ob, x, rng = setup(name, B, IN, seed=7)
+    c = rng.normal(0, 0.5, (OUT, IN, basis.size))
+    bw = rng.normal(0, 0.5, (OUT, IN))
+    d = K._edge_raw(plan, m, st, to_dev(x, dtype), to_dev(c, dtype), to_dev(bw, dtype))
+    want = o.edge_derivative(rounded(x, dtype), rounded(c, dtype), ob, m, rounded(bw, dtype))
     assert d.shape == want.shape
     assert err(d, want) <= TOL[dtype]
 
