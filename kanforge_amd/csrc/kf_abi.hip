@@ -198,7 +198,8 @@ struct WsP {
 // P with FW <= 4 runs the copy kernel (p_dma_kernel; 4 x FW accumulator tiles in AGPRs); it needs
 // g with whole 128-byte stages of columns and 16-byte aligned rows, else a zero-padded copy of g
 // in the workspace.
-bool p_uses_dma(int cfg) { return FW_LIST[cfg] <= 4; }
+bool p_uses_dma(int cfg) { return FW_LIST[cfg] <= 6; }
+constexpr int p_dma_tm(int fw) { return fw <= 4 ? 4 : 2; }  // row tiles per wave (LDS: two stages fit)
 int64_t p_stage_cols(int dtype) { return 128 / elt_size(dtype); }
 bool p_needs_gpad(int64_t n_out, int dtype) { return n_out % p_stage_cols(dtype) != 0; }
 WsP ws_p(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out) {
@@ -356,7 +357,8 @@ template <typename T, int NTB>
 int launch_features_t_nb(const KBasis& kb, int64_t batch, int64_t n_in, int64_t BP, int64_t INP, const void* x,
                          const void* w, void* phit, hipStream_t s) {
   constexpr int BT = 128 / (int)sizeof(T);
-  const size_t lds = (size_t)kb.n_t * 32 * 144;
+  const size_t knots = kb.kind == KF_KIND_BSPLINE ? (size_t)32 * (2 * kb.n_knots + 2 * kb.spline_k) * 4 : 0;
+  const size_t lds = (size_t)kb.n_t * 32 * 144 + knots;
   auto kern = features_t_kernel<T, NTB>;
   if (lds > 65536 &&
       hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
@@ -540,8 +542,9 @@ int launch_p_t(const WsP& L, hipStream_t s, const KBasis& kb, int64_t batch, int
 template <typename T, int FW, int KIND>
 int launch_p_dma_kind(const WsP& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, const void* x,
                       const void* g, int gstride, const void* cfmt, void* p, float* h) {
-  constexpr int TM = 4, BM = 2 * TM * 32;
-  const size_t lds_ops = (size_t)2 * (BM + 2 * FW * 32) * 128, lds_epi = (size_t)3 * BM * 33 * 4;
+  constexpr int TM = p_dma_tm(FW), BM = 2 * TM * 32;
+  const size_t knots = KIND == KF_KIND_BSPLINE ? (size_t)32 * (2 * kb.n_knots + 2 * kb.spline_k) * 4 : 0;
+  const size_t lds_ops = (size_t)2 * (BM + 2 * FW * 32) * 128, lds_epi = (size_t)3 * BM * 33 * 4 + knots;
   const size_t lds = lds_ops > lds_epi ? lds_ops : lds_epi;
   auto kern = p_dma_kernel<T, TM, FW, KIND>;
   if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
@@ -611,7 +614,9 @@ int run_P(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
     switch (L.cfg) {
       case 0: return launch_p_dma<T, 2>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p, h);
       case 1: return launch_p_dma<T, 3>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p, h);
-      default: return launch_p_dma<T, 4>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p, h);
+      case 2: return launch_p_dma<T, 4>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p, h);
+      case 3: return launch_p_dma<T, 5>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p, h);
+      default: return launch_p_dma<T, 6>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p, h);
     }
   }
   switch (L.cfg) {

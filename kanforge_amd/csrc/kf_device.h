@@ -133,9 +133,17 @@ __device__ __forceinline__ void cheb_folded(const KBasis& b, const float* T, flo
 // spline_k padding knots per side: kp[r] = t_{r - spline_k}.
 
 // Interval j with t_j <= x < t_{j+1}, or -1: count of comparison knots <= x, minus one.
+// The knots are read eight at a time with independent loads (one round trip per
+// eight knots instead of one per knot); knots past n_knots are not read.
 __device__ __forceinline__ int bspline_interval(float x, const float* kc, int n_knots) {
   int cnt = 0;
-  for (int r = 0; r < n_knots; ++r) cnt += (x >= kc[r]) ? 1 : 0;
+  for (int r0 = 0; r0 < n_knots; r0 += 8) {
+    float kv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) kv[u] = r0 + u < n_knots ? kc[r0 + u] : __builtin_inff();
+#pragma unroll
+    for (int u = 0; u < 8; ++u) cnt += (r0 + u < n_knots && x >= kv[u]) ? 1 : 0;
+  }
   int j = cnt - 1;
   return (j >= 0 && j <= n_knots - 2) ? j : -1;
 }
@@ -144,12 +152,15 @@ __device__ __forceinline__ int bspline_interval(float x, const float* kc, int n_
 // Local de Boor on the k+1 splines that can be non-zero in interval j, then
 // m derivative steps (m > k gives zeros). KM >= K.
 template <int KM, int KD>
-__device__ inline void bspline_features(float x, float w, int i, const KBasis& b, float* phi) {
+// kc: the input's n_knots comparison knots; kp0: its n_knots + 2 KD padded knots
+// (global memory, or a copy staged in LDS by a kernel that covers few inputs).
+__device__ inline void bspline_features_rows(float x, float w, const float* kc, const float* kp0, const KBasis& b,
+                                             float* phi) {
 #pragma unroll
   for (int s = 0; s < KM; ++s) phi[s] = 0.f;
   const int nk = b.n_knots, m = b.order;
   if (m > KD) return;
-  const int j = bspline_interval(x, b.knots_cmp + (size_t)i * nk, nk);
+  const int j = bspline_interval(x, kc, nk);
   if (j < 0) {
     // outside [t_0, t_last): zeros; a non-finite x turns the zero indicators
     // into NaN through (x - t) * 0, as the float64 recurrence does
@@ -160,7 +171,7 @@ __device__ inline void bspline_features(float x, float w, int i, const KBasis& b
     return;
   }
   // L[r] = t_{j-KD+r}, r = 0..2KD+1 (kp[r'] = t_{r'-KD}, so t_{j-KD+r} = kp[j+r])
-  const float* kp = b.knots + (size_t)i * (nk + 2 * KD) + j;
+  const float* kp = kp0 + j;
   float L[2 * KD + 2];
 #pragma unroll
   for (int r = 0; r < 2 * KD + 2; ++r) L[r] = kp[r];
@@ -181,10 +192,12 @@ __device__ inline void bspline_features(float x, float w, int i, const KBasis& b
       const float ts = L[KD - q + r], ts1 = L[KD - q + r + 1], tsq = L[KD + r], tsq1 = L[KD + r + 1];
       const float left = (r >= 1) ? N[r - 1] : 0.f;   // B_{q-1,s}
       const float right = (r <= q - 1) ? N[r] : 0.f;  // B_{q-1,s+1}
+      // knot spans divide through the fast reciprocal (<= 2 ulp): an IEEE division
+      // costs a dozen instructions and there are two per term
       if (q <= deg)  // Cox-de Boor
-        nn[r] = (x - ts) / (tsq - ts) * left + (tsq1 - x) / (tsq1 - ts1) * right;
+        nn[r] = __fdividef(x - ts, tsq - ts) * left + __fdividef(tsq1 - x, tsq1 - ts1) * right;
       else  // derivative step
-        nn[r] = (float)q * (left / (tsq - ts) - right / (tsq1 - ts1));
+        nn[r] = (float)q * (__fdividef(left, tsq - ts) - __fdividef(right, tsq1 - ts1));
     }
 #pragma unroll
     for (int r = 0; r <= KD; ++r) N[r] = nn[r];
@@ -199,6 +212,12 @@ __device__ inline void bspline_features(float x, float w, int i, const KBasis& b
     for (int rr = 0; rr <= KD; ++rr) v = (rr == r) ? N[rr] : v;
     phi[s] = (s < b.K) ? w * v : 0.f;
   }
+}
+
+template <int KM, int KD>
+__device__ inline void bspline_features(float x, float w, int i, const KBasis& b, float* phi) {
+  const int nk = b.n_knots;
+  bspline_features_rows<KM, KD>(x, w, b.knots_cmp + (size_t)i * nk, b.knots + (size_t)i * (nk + 2 * KD), b, phi);
 }
 
 // ---------------------------------------------------------------------------
@@ -243,6 +262,38 @@ __device__ inline float rational_feature(float x, int i, const KBasis& b, int m)
     out[n] = acc * invD;
   }
   return out[m < 8 ? m : 8];
+}
+
+// Degree dispatch with the knot rows given (degrees 0..5 are compiled).
+template <int KM>
+__device__ inline void bspline_dispatch_rows(float x, float w, const float* kc, const float* kp0, const KBasis& b,
+                                             float* phi) {
+  switch (b.spline_k) {
+    case 0: bspline_features_rows<KM, 0>(x, w, kc, kp0, b, phi); break;
+    case 1: bspline_features_rows<KM, 1>(x, w, kc, kp0, b, phi); break;
+    case 2: bspline_features_rows<KM, 2>(x, w, kc, kp0, b, phi); break;
+    case 3: bspline_features_rows<KM, 3>(x, w, kc, kp0, b, phi); break;
+    case 4: bspline_features_rows<KM, 4>(x, w, kc, kp0, b, phi); break;
+    default: bspline_features_rows<KM, 5>(x, w, kc, kp0, b, phi); break;
+  }
+}
+
+// Copies the knot rows of inputs i0 .. i0 + n - 1 (zeros past IN) into LDS:
+// kc[il * nk + r], kp[il * (nk + 2k) + r]. Every thread of the block calls it;
+// the caller synchronises before reading.
+__device__ inline void stage_knot_rows(const KBasis& b, int i0, int n, int IN, float* kc, float* kp) {
+  const int nk = b.n_knots, np = nk + 2 * b.spline_k;
+  for (int e = threadIdx.x; e < n * nk; e += blockDim.x) {
+    const int il = e / nk, i = i0 + il;
+    kc[e] = i < IN ? b.knots_cmp[(size_t)i * nk + e % nk] : 0.f;
+  }
+  for (int e = threadIdx.x; e < n * np; e += blockDim.x) {
+    const int il = e / np, i = i0 + il;
+    kp[e] = i < IN ? b.knots[(size_t)i * np + e % np] : 0.f;
+  }
+}
+__device__ __forceinline__ int knot_lds_floats(const KBasis& b, int n) {
+  return n * (2 * b.n_knots + 2 * b.spline_k);
 }
 
 // Degree dispatch (degrees 0..5 are compiled).

@@ -1004,9 +1004,16 @@ __global__ __launch_bounds__(kThreads) void features_t_kernel(KBasis bs, int B, 
                                                               const T* __restrict__ x, const T* __restrict__ w,
                                                               T* __restrict__ phit) {
   constexpr int BT = 128 / (int)sizeof(T), RSB = 144, PER = 32 * BT / kThreads, VW = 16 / (int)sizeof(T);
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];  // [n_t][32][RSB]
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];  // [n_t][32][RSB], B-spline knot rows
   const int n_t = bs.n_t;
   const int i0 = blockIdx.x * 32, b0 = blockIdx.y * BT;
+  const bool bspl = bs.kind == KF_KIND_BSPLINE;
+  float* kcs = reinterpret_cast<float*>(smem + (size_t)n_t * 32 * RSB);
+  float* kps = kcs + 32 * bs.n_knots;
+  if (bspl) {
+    stage_knot_rows(bs, i0, 32, IN, kcs, kps);
+    __syncthreads();
+  }
 #pragma unroll
   for (int u = 0; u < PER; ++u) {
     const int e = threadIdx.x + u * kThreads;
@@ -1015,7 +1022,10 @@ __global__ __launch_bounds__(kThreads) void features_t_kernel(KBasis bs, int B, 
     const float xv = ok ? to_f32(x[(size_t)b * IN + i]) : 0.f;
     const float wv = ok ? (w ? to_f32(w[(size_t)b * IN + i]) : 1.f) : 0.f;
     float f[NTB];
-    kernel_features<NTB>(xv, wv, ok ? i : 0, bs, f);
+    if (bspl)
+      bspline_dispatch_rows<NTB>(xv, wv, kcs + il * bs.n_knots, kps + il * (bs.n_knots + 2 * bs.spline_k), bs, f);
+    else
+      kernel_features<NTB>(xv, wv, ok ? i : 0, bs, f);
 #pragma unroll
     for (int j = 0; j < NTB; ++j)
       if (j < n_t) reinterpret_cast<T*>(smem + (size_t)(j * 32 + il) * RSB)[bl] = from_f32<T>(ok ? f[j] : 0.f);
@@ -1512,6 +1522,9 @@ __global__ __launch_bounds__(256) void p_dma_kernel(KBasis bs, int B, int IN, in
   // x of the tile into LDS, all loads in flight at once (coalesced along the inputs)
   float* red = reinterpret_cast<float*>(smem);  // [2][BM][33]: the two feature groups' sums
   float* xs = red + 2 * BM * 33;                // [BM][33]
+  float* kcs = xs + BM * 33;                    // B-spline: the tile's knot rows
+  float* kps = kcs + 32 * bs.n_knots;
+  if constexpr (KIND == KF_KIND_BSPLINE) stage_knot_rows(bs, i0, 32, IN, kcs, kps);
   {
     constexpr int PER = BM * 32 / 256;
     float xv[PER];
@@ -1538,7 +1551,11 @@ __global__ __launch_bounds__(256) void p_dma_kernel(KBasis bs, int B, int IN, in
       float sum = 0.f;
       if (b < B && i < IN) {
         float f[NTB];
-        kind_features<KIND, NTB>(xs[row * 33 + l32], 1.f, i, bs, f);
+        if constexpr (KIND == KF_KIND_BSPLINE)
+          bspline_dispatch_rows<NTB>(xs[row * 33 + l32], 1.f, kcs + l32 * bs.n_knots,
+                                     kps + l32 * (bs.n_knots + 2 * bs.spline_k), bs, f);
+        else
+          kind_features<KIND, NTB>(xs[row * 33 + l32], 1.f, i, bs, f);
 #pragma unroll
         for (int q = 0; q < FW; ++q) sum = fmaf(acc[a][q][r], f[wj * FW + q], sum);
         if (hout && wj == 0) hout[(size_t)b * IN + i] = acc[a][0][r];
