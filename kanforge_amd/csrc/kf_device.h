@@ -246,10 +246,62 @@ __device__ inline float binom(int n, int k) {
 }
 
 // d^m/dx^m of P/(1+|Q|), m <= 8
+// The same recursion with the degrees fixed at compile time: the group's
+// coefficients live in registers, every polynomial and derivative is straight
+// Horner code (derivatives by differentiating the register coefficients in
+// place), and the orders 0..MAXM are unrolled with m selecting the result.
+template <int NP, int NQ, int MAXM>
+__device__ inline float rational_feature_fixed(float x, const float* __restrict__ a, const float* __restrict__ c,
+                                               int m) {
+  float dp[NP], dq[NQ + 1];  // P = sum_p dp[p] x^p; Q = sum_{q >= 1} dq[q] x^q
+#pragma unroll
+  for (int p = 0; p < NP; ++p) dp[p] = a[p];
+  dq[0] = 0.f;
+#pragma unroll
+  for (int q = 1; q <= NQ; ++q) dq[q] = c[q - 1];
+  float Pd[MAXM + 1], Qd[MAXM + 1];
+#pragma unroll
+  for (int n = 0; n <= MAXM; ++n) {
+    float hp = 0.f, hq = 0.f;
+#pragma unroll
+    for (int p = NP - 1; p >= 0; --p) hp = fmaf(hp, x, dp[p]);
+#pragma unroll
+    for (int q = NQ; q >= 0; --q) hq = fmaf(hq, x, dq[q]);
+    Pd[n] = hp;
+    Qd[n] = hq;
+#pragma unroll
+    for (int p = 0; p + 1 < NP; ++p) dp[p] = (float)(p + 1) * dp[p + 1];
+    dp[NP - 1] = 0.f;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) dq[q] = (float)(q + 1) * dq[q + 1];
+    dq[NQ] = 0.f;
+  }
+  const float sgn = (Qd[0] > 0.f) ? 1.f : ((Qd[0] < 0.f) ? -1.f : 0.f);
+  const float invD = 1.f / (1.f + fabsf(Qd[0]));
+  float out[MAXM + 1];
+  out[0] = Pd[0] * invD;
+  float res = out[0];
+#pragma unroll
+  for (int n = 1; n <= MAXM; ++n) {
+    float acc = Pd[n];
+    float bc = 1.f;  // binomial C(n, k), built incrementally
+#pragma unroll
+    for (int k = 1; k <= n; ++k) {
+      bc = bc * (float)(n - k + 1) / (float)k;
+      acc -= bc * sgn * Qd[k] * out[n - k];
+    }
+    out[n] = acc * invD;
+    res = (n == m) ? out[n] : res;
+  }
+  return res;
+}
+
 __device__ inline float rational_feature(float x, int i, const KBasis& b, int m) {
   const int g = i / b.group_size;
   const float* a = b.num + (size_t)g * (b.num_deg + 1);
   const float* c = b.den + (size_t)g * b.den_deg;
+  // the GR-KAN degrees (P 5, Q 4) up to order 4 take the unrolled register path
+  if (b.num_deg == 5 && b.den_deg == 4 && m <= 4) return rational_feature_fixed<6, 4, 4>(x, a, c, m);
   float out[9];
   float Q0 = poly_dj(c, b.den_deg, 1, 0, x);
   float sgn = (Q0 > 0.f) ? 1.f : ((Q0 < 0.f) ? -1.f : 0.f);
