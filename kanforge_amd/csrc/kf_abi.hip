@@ -225,6 +225,7 @@ struct WsG {
   size_t gt, zt, wt, part, colsum, phit, zpart, total;
 };
 constexpr size_t kGSplitBytes = size_t(256) << 20;  // cap of the split partial sums
+constexpr long kGSplitMax = 64;                      // cap of the batch splits
 WsG ws_g(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, bool has_w) {
   WsG w;
   const bool cheb_kind = b->kind == KF_KIND_CHEB;
@@ -266,6 +267,7 @@ WsG ws_g(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
     if (tiles < 512) {
       const size_t per = (size_t)w.OUTP * w.INP * b->n_t * sizeof(float);
       long nz = (512 + tiles - 1) / tiles;
+      if (nz > kGSplitMax) nz = kGSplitMax;
       if (nz > stages) nz = stages;
       if ((size_t)nz * per > kGSplitBytes) nz = (long)(kGSplitBytes / per);
       w.nz = nz > 1 ? (int)nz : 1;
@@ -645,11 +647,18 @@ int launch_g_t(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, int
                      L.nz > 1 ? zpart : nullptr);
   int rc = check_launch("G");
   if (rc || L.nz == 1) return rc;
+  // the splits summed into split 0 (coalesced), then the fold from that one slice
+  const size_t zstride = (size_t)L.OUTP * L.INP * kb.n_t;
+  long blocks = ((long)zstride + kThreads - 1) / kThreads;
+  if (blocks > 65535 * 4) blocks = 65535 * 4;
+  hipLaunchKernelGGL(g_split_sum, dim3((unsigned)blocks), dim3(kThreads), 0, s, (long)zstride, L.nz, zstride, zpart);
+  rc = check_launch("G split sum");
+  if (rc) return rc;
   long n = (long)n_out * n_in * kb.K;
-  long blocks = (n + kThreads - 1) / kThreads;
+  blocks = (n + kThreads - 1) / kThreads;
   if (blocks > 65535 * 4) blocks = 65535 * 4;
   hipLaunchKernelGGL(g_split_reduce<T>, dim3((unsigned)blocks), dim3(kThreads), 0, s, kb, (int)n_out, (int)n_in,
-                     (int)L.OUTP, (int)L.INP, L.nz, (const float*)zpart, (T*)dc);
+                     (int)L.OUTP, (int)L.INP, 1, (const float*)zpart, (T*)dc);
   return check_launch("G split reduce");
 }
 

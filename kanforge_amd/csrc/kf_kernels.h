@@ -970,6 +970,17 @@ __global__ __launch_bounds__(WAVES_M* WAVES_J * 64) void g_kernel(KBasis bs, int
   }
 }
 
+// part[0][t] = sum_z part[z][t] over the flat (o, i, j) index t: the batch
+// splits of g_kernel summed in a fixed order (deterministic), consecutive
+// threads reading consecutive floats of every split.
+__global__ __launch_bounds__(kThreads) void g_split_sum(long n, int nz, size_t zstride, float* __restrict__ part) {
+  for (long t = blockIdx.x * (long)kThreads + threadIdx.x; t < n; t += (long)gridDim.x * kThreads) {
+    float sum = 0.f;
+    for (int z = 0; z < nz; ++z) sum += part[(size_t)z * zstride + t];
+    part[t] = sum;
+  }
+}
+
 // dc[o][i][k] = sum_z sum_j fold[k][j] part[z][o][i][j]: the fold and the sum
 // over the batch splits of g_kernel, in a fixed order (deterministic).
 template <typename T>
@@ -2293,9 +2304,14 @@ __global__ __launch_bounds__(kThreads) void rational_grad_partial(KBasis bs, int
   const int nP = bs.num_deg + 1, nQ = bs.den_deg, np = nP + nQ;
   const float* a = bs.num + (size_t)g * nP;
   const float* c = bs.den + (size_t)g * nQ;
-  float accp[kRatMaxParams];
+  // accumulators and coefficients indexed only by unrolled loop counters, so they stay in registers
+  float accP[kRatMaxParams], accQ[kRatMaxParams], ca[kRatMaxParams], cc[kRatMaxParams];
 #pragma unroll
-  for (int q = 0; q < kRatMaxParams; ++q) accp[q] = 0.f;
+  for (int q = 0; q < kRatMaxParams; ++q) {
+    accP[q] = accQ[q] = 0.f;
+    ca[q] = q < nP ? a[q] : 0.f;
+    cc[q] = q < nQ ? c[q] : 0.f;
+  }
   const int gs = bs.group_size;
   const long n = (long)kRatRows * gs;
   for (long e = threadIdx.x; e < n; e += kThreads) {
@@ -2305,25 +2321,27 @@ __global__ __launch_bounds__(kThreads) void rational_grad_partial(KBasis bs, int
     const size_t off = (size_t)b * IN + i;
     const float xv = to_f32(x[off]);
     const float hv = hbuf[off] * (w ? to_f32(w[off]) : 1.f);
-    const float P = poly_dj(a, nP, 0, 0, xv);
-    const float Q = poly_dj(c, nQ, 1, 0, xv);
+    float P = 0.f, Q = 0.f;  // Horner; Q = sum_{q >= 1} cc[q - 1] x^q
+#pragma unroll
+    for (int q = kRatMaxParams - 1; q >= 0; --q) {
+      P = fmaf(P, xv, ca[q]);
+      Q = fmaf(Q, xv, cc[q]);
+    }
+    Q *= xv;
     const float sgn = (Q > 0.f) ? 1.f : ((Q < 0.f) ? -1.f : 0.f);
     const float invD = 1.f / (1.f + fabsf(Q));
+    const float hd = hv * invD, coef = -hv * P * sgn * invD * invD;
     float xp = 1.f;
-    for (int q = 0; q < nP; ++q) {
-      accp[q] += hv * xp * invD;
-      xp *= xv;
-    }
-    xp = xv;
-    const float coef = -hv * P * sgn * invD * invD;
-    for (int q = 0; q < nQ; ++q) {
-      accp[nP + q] += coef * xp;
+#pragma unroll
+    for (int q = 0; q < kRatMaxParams; ++q) {
+      accP[q] += hd * xp;         // d/da_q: x^q / D
+      accQ[q] += coef * xp * xv;  // d/db_{q+1}: -P sgn(Q) x^(q+1) / D^2
       xp *= xv;
     }
   }
   __shared__ float red[kThreads];
-  for (int q = 0; q < np; ++q) {
-    red[threadIdx.x] = accp[q];
+  auto block_sum = [&](float v, int q) {
+    red[threadIdx.x] = v;
     __syncthreads();
     for (int s = kThreads / 2; s > 0; s >>= 1) {
       if ((int)threadIdx.x < s) red[threadIdx.x] += red[threadIdx.x + s];
@@ -2331,7 +2349,13 @@ __global__ __launch_bounds__(kThreads) void rational_grad_partial(KBasis bs, int
     }
     if (threadIdx.x == 0) part[((size_t)chunk * gridDim.x + g) * np + q] = red[0];
     __syncthreads();
-  }
+  };
+#pragma unroll
+  for (int q = 0; q < kRatMaxParams; ++q)
+    if (q < nP) block_sum(accP[q], q);
+#pragma unroll
+  for (int q = 0; q < kRatMaxParams; ++q)
+    if (q < nQ) block_sum(accQ[q], nP + q);
 }
 
 __global__ void rational_grad_final(int groups, int nP, int nQ, int n_chunks, const float* __restrict__ part,
