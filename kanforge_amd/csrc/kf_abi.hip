@@ -220,12 +220,14 @@ struct WsG {
   bool skip0;  // Chebyshev, unweighted: T_0 = 1 taken out of the contraction (column sums of g)
   bool g96;    // bf16 Chebyshev with at most 8 features run: g96_kernel (192 x 48 x 8 tiles)
   bool pre;    // features precomputed into phiT (other kinds, and Chebyshev plans on small grids)
+  bool gdma;   // B-spline without batch splits: p_dma_kernel as the flat GEMM gT x phiT^T
   int nz;      // pre: batch splits of g_kernel (raw sums reduced by g_split_reduce when > 1)
   int64_t OUTP, BP, INP;
   size_t gt, zt, wt, part, colsum, phit, zpart, total;
 };
 constexpr size_t kGSplitBytes = size_t(256) << 20;  // cap of the split partial sums
 constexpr long kGSplitMax = 64;                      // cap of the batch splits
+constexpr int kGdmaFW = 4, kGdmaRows = 2 * kGdmaFW * 32;  // G on p_dma_kernel: phiT rows per tile
 WsG ws_g(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, bool has_w) {
   WsG w;
   const bool cheb_kind = b->kind == KF_KIND_CHEB;
@@ -260,6 +262,7 @@ WsG ws_g(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
   w.colsum = w.skip0 ? align256((size_t)w.OUTP * sizeof(float)) : 0;
   w.phit = w.zpart = 0;
   w.nz = 1;
+  w.gdma = false;
   if (w.pre) {
     w.phit = align256((size_t)b->n_t * w.INP * w.BP * elt_size(dtype));
     // fewer output tiles than two rounds of the 256 CUs: split the batch
@@ -273,6 +276,12 @@ WsG ws_g(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
       w.nz = nz > 1 ? (int)nz : 1;
     }
     w.zpart = w.nz > 1 ? align256((size_t)w.nz * w.OUTP * w.INP * b->n_t * sizeof(float)) : 0;
+    // identity fold, one split, stages of 128 bytes (n_t <= 12): flat 256-row tiles of phiT
+    w.gdma = b->kind == KF_KIND_BSPLINE && w.nz == 1 && g_rb(fw) == 128;
+    if (w.gdma) {
+      w.INP = round_up(n_in, kGdmaRows);
+      w.phit = align256((size_t)b->n_t * w.INP * w.BP * elt_size(dtype));
+    }
   }
   w.total = w.gt + w.zt + w.wt + w.part + w.colsum + w.phit + w.zpart;
   return w;
@@ -719,6 +728,22 @@ int launch_g96(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, int
   return check_launch("G");
 }
 
+// G over precomputed B-spline features as p_dma_kernel's flat GEMM (identity fold).
+template <typename T>
+int launch_g_dma(const WsG& L, hipStream_t s, const KBasis& kb, int64_t n_in, int64_t n_out, const void* gt,
+                 const void* phit, void* dc) {
+  constexpr int FW = kGdmaFW, TM = p_dma_tm(FW), BM = 2 * TM * 32, EPS = 128 / (int)sizeof(T);
+  const size_t lds = (size_t)2 * (BM + 2 * FW * 32) * 128;
+  auto kern = p_dma_kernel<T, TM, FW, KF_KIND_BSPLINE, 1>;
+  if (L.INP % kGdmaRows || L.BP % EPS || L.BP / EPS < 1) return fail(KF_EINVAL, "G: workspace layout not aligned");
+  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+    return fail(KF_ELAUNCH, "G: cannot reserve %zu bytes of LDS", lds);
+  const int n_m = (int)((n_out + BM - 1) / BM), n_n = (int)(kb.n_t * L.INP / kGdmaRows);
+  hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(256), lds, s, kb, (int)n_out, (int)n_in, (int)L.INP, (int)L.BP,
+                     (const T*)nullptr, (const T*)gt, (int)L.BP, (const T*)phit, (T*)dc, (float*)nullptr);
+  return check_launch("G");
+}
+
 template <typename T>
 int run_G(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
           const void* g, const void* w, void* dc, void* ws, hipStream_t s) {
@@ -767,6 +792,7 @@ int run_G(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
   float* zpart = L.nz > 1 ? (float*)((char*)phit + L.phit) : nullptr;
   rc = launch_features_t<T>(kb, batch, n_in, L.BP, L.INP, x, w, phit, s);
   if (rc) return rc;
+  if (L.gdma) return launch_g_dma<T>(L, s, kb, n_in, n_out, gt, phit, dc);
   return launch_g_cfg<T, false>(L, s, kb, batch, n_in, n_out, phit, zpart, nullptr, nullptr, gt, dc);
 }
 

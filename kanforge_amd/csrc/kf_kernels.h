@@ -1397,7 +1397,11 @@ __global__ __launch_bounds__(64 * NWM * WN) void f_rega_kernel(int B, int OUT, i
 // Rows of g past the batch are clamped to the last row (their results are
 // dropped); g must have whole stages of columns (the caller pads it
 // otherwise) and CfmT is zero past n_out and n_t.
-template <typename T, int TM, int FW, int KIND>
+// EPI 1 (G over precomputed features, identity fold): the same GEMM with
+// M = outputs o (g := gT, gstride := BP, B := OUT), the reduction over the batch
+// (OUTP := BP) and N = the n_t x INP rows of phiT (cfmt := phiT) in flat tiles;
+// the epilogue stores dc[o][i][j] = acc for row n = j INP + i (p := dc).
+template <typename T, int TM, int FW, int KIND, int EPI = 0>
 __global__ __launch_bounds__(256) void p_dma_kernel(KBasis bs, int B, int IN, int INP, int OUTP,
                                                     const T* __restrict__ x, const T* __restrict__ g, int gstride,
                                                     const T* __restrict__ cfmt, T* __restrict__ p,
@@ -1414,9 +1418,9 @@ __global__ __launch_bounds__(256) void p_dma_kernel(KBasis bs, int B, int IN, in
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];  // [2][SS], later x and the sums
 
   // single-feature kinds (rational): the NTB slots hold NTB x 32 consecutive inputs
-  constexpr bool FLAT = KIND == KF_KIND_RATIONAL;
-  constexpr int TI = FLAT ? NTB * 32 : 32;  // inputs per tile
-  const int n_m = (B + BM - 1) / BM, n_n = INP / TI;
+  constexpr bool FLAT = KIND == KF_KIND_RATIONAL || EPI == 1;
+  constexpr int TI = FLAT ? NTB * 32 : 32;  // inputs (EPI 1: phiT rows) per tile
+  const int n_m = (B + BM - 1) / BM, n_n = (EPI == 1 ? bs.n_t * INP : INP) / TI;
   int tm_, tn_;
   xcd_tile_grouped(blockIdx.x, n_m, n_n, 8, tm_, tn_);
   const int b0 = tm_ * BM, i0 = tn_ * TI;
@@ -1508,7 +1512,21 @@ __global__ __launch_bounds__(256) void p_dma_kernel(KBasis bs, int B, int IN, in
     mma_rest((KS - 1) & 1);
   }
   vmem_wait<0>();
-  if constexpr (FLAT) {
+  if constexpr (EPI == 1) {
+    const int K = bs.K, n_t = bs.n_t;
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int o = b0 + wm * WM + a * 32 + acc_row(r, lane);
+#pragma unroll
+        for (int q = 0; q < FW; ++q) {
+          const int n = i0 + (wj * FW + q) * 32 + l32, j = n / INP, i = n - j * INP;
+          if (o < B && i < IN && j < n_t) p[((size_t)o * IN + i) * K + j] = from_f32<T>(acc[a][q][r]);
+        }
+      }
+    return;
+  } else if constexpr (FLAT) {
     // every (row, input) has one accumulator: p = f_0(x) H, written from registers
 #pragma unroll
     for (int a = 0; a < TM; ++a)

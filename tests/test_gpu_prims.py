@@ -153,6 +153,22 @@ def test_edge_derivative_matches_oracle(name, m, base, dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16"])
+@pytest.mark.parametrize("name,m", [("bspline53", 0), ("bspline83", 1)])
+def test_G_many_output_tiles(name, m, dtype):
+    """Grids of at least two rounds of tiles take G's unsplit B-spline route (a flat GEMM
+    over the precomputed features); the small shapes above take the batch-split route."""
+    B, IN, OUT = 80, 2050, 1030
+    basis, plan, st, ob, x, rng = setup(name, B, IN, seed=11)
+    g = rng.normal(0, 1, (B, OUT))
+    w = rng.uniform(0.5, 1.5, (B, IN))
+    for wt in (None, w):
+        dc = K._raw("G", plan, m, to_dev(x, dtype), None if wt is None else to_dev(wt, dtype), to_dev(g, dtype), st, OUT)
+        want = o.prim_G(rounded(x, dtype), rounded(g, dtype), None if wt is None else rounded(wt, dtype), ob, m)
+        assert dc.shape == want.shape
+        assert err(dc, want) <= TOL[dtype], (name, m, wt is None)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16"])
 @pytest.mark.parametrize("name,m", [("jacobi6", 2), ("bspline53", 1), ("rational", 1)])
 @pytest.mark.parametrize("shape", [(70, 2, 64), (70, 64, 1), (33, 3, 5), (40, 1, 1)], ids=["2to64", "64to1", "3to5", "1to1"])
 def test_edge_derivative_narrow_layers(shape, name, m, dtype):
