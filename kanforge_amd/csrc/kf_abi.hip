@@ -459,6 +459,23 @@ int launch_f_cfg(const WsF& L, int64_t batch, int64_t n_out, int n_t, const floa
 }
 
 template <typename T>
+int run_F_dma(const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* c, void* phi,
+              void* y, hipStream_t s) {
+  constexpr int FW = kGdmaFW, TM = p_dma_tm(FW), BM = 2 * TM * 32, TI = 2 * FW * 32;
+  const long ld = (long)n_in * kb.K;  // Phi row length: the reduction
+  int rc = launch_features<T, false>(kb, batch, n_in, batch, n_in, x, phi, ld, 1L, (long)kb.K, false, s);
+  if (rc) return rc;
+  const size_t lds = (size_t)2 * (BM + TI) * 128;
+  auto kern = p_dma_kernel<T, TM, FW, KF_KIND_BSPLINE, 2>;
+  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+    return fail(KF_ELAUNCH, "F: cannot reserve %zu bytes of LDS", lds);
+  const int n_m = (int)((batch + BM - 1) / BM), n_n = (int)((n_out + TI - 1) / TI);
+  hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(256), lds, s, kb, (int)batch, (int)n_out, n_n * TI, (int)ld,
+                     (const T*)nullptr, (const T*)phi, (int)ld, (const T*)c, (T*)y, (float*)nullptr);
+  return check_launch("F");
+}
+
+template <typename T>
 int run_F(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
           const void* w, const void* c, void* y, void* ws, hipStream_t s) {
   const bool has_w = w != nullptr;
@@ -492,6 +509,13 @@ int run_F(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
     if (L.skip0) return launch_f_rega<false, true>(L, batch, n_out, z, nullptr, cfm, ysum, y, s);
     return launch_f_rega<false, false>(L, batch, n_out, z, nullptr, cfm, nullptr, y, s);
   }
+  // B-spline, unweighted, in K a whole number of 128-byte stages: Phi (B, in K) in the
+  // reference's layout, then the flat GEMM Phi c^T on p_dma_kernel (no coefficient permute)
+  constexpr int EPS = 128 / (int)sizeof(T);
+  const long dma_tiles = ((batch + 255) / 256) * ((n_out + 255) / 256);  // at least half a round of the CUs
+  if (kb.kind == KF_KIND_BSPLINE && !has_w && (n_in * kb.K) % EPS == 0 && aligned16(c) && aligned16(phi) &&
+      dma_tiles >= 128)
+    return run_F_dma<T>(kb, batch, n_in, n_out, x, c, phi, y, s);
   int rc = launch_permute<T>(kb, n_out, n_in, L.OUTP, L.INP, L.n_tp, c, cfm, kPermFM, s);
   if (rc) return rc;
   if (cheb) {

@@ -1397,6 +1397,10 @@ __global__ __launch_bounds__(64 * NWM * WN) void f_rega_kernel(int B, int OUT, i
 // Rows of g past the batch are clamped to the last row (their results are
 // dropped); g must have whole stages of columns (the caller pads it
 // otherwise) and CfmT is zero past n_out and n_t.
+// EPI 2 (F over precomputed features, identity fold): y = Phi c^T with
+// g := Phi (B, in K), OUTP := gstride := in K, cfmt := coef (out, in K), IN :=
+// OUT (coefficient rows past OUT clamp to the last one), INP := OUT rounded to
+// whole tiles; the epilogue stores y[b][o] = acc.
 // EPI 1 (G over precomputed features, identity fold): the same GEMM with
 // M = outputs o (g := gT, gstride := BP, B := OUT), the reduction over the batch
 // (OUTP := BP) and N = the n_t x INP rows of phiT (cfmt := phiT) in flat tiles;
@@ -1418,7 +1422,7 @@ __global__ __launch_bounds__(256) void p_dma_kernel(KBasis bs, int B, int IN, in
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];  // [2][SS], later x and the sums
 
   // single-feature kinds (rational): the NTB slots hold NTB x 32 consecutive inputs
-  constexpr bool FLAT = KIND == KF_KIND_RATIONAL || EPI == 1;
+  constexpr bool FLAT = KIND == KF_KIND_RATIONAL || EPI != 0;
   constexpr int TI = FLAT ? NTB * 32 : 32;  // inputs (EPI 1: phiT rows) per tile
   const int n_m = (B + BM - 1) / BM, n_n = (EPI == 1 ? bs.n_t * INP : INP) / TI;
   int tm_, tn_;
@@ -1450,7 +1454,8 @@ __global__ __launch_bounds__(256) void p_dma_kernel(KBasis bs, int B, int IN, in
       src[k] = g + (size_t)b * gstride + c * EPC;
     } else {
       const int rr = row - BM, j = rr / 32, il = rr % 32;
-      src[k] = cfmt + (FLAT ? (size_t)i0 + rr : (size_t)j * INP + i0 + il) * OUTP + c * EPC;
+      const int fr = EPI == 2 && i0 + rr >= IN ? IN - 1 : i0 + rr;  // F: clamp past the last output
+      src[k] = cfmt + (FLAT ? (size_t)fr : (size_t)j * INP + i0 + il) * OUTP + c * EPC;
     }
   }
   auto copy_stage = [&](int st) {
@@ -1512,7 +1517,20 @@ __global__ __launch_bounds__(256) void p_dma_kernel(KBasis bs, int B, int IN, in
     mma_rest((KS - 1) & 1);
   }
   vmem_wait<0>();
-  if constexpr (EPI == 1) {
+  if constexpr (EPI == 2) {
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int b = b0 + wm * WM + a * 32 + acc_row(r, lane);
+#pragma unroll
+        for (int q = 0; q < FW; ++q) {
+          const int o = i0 + (wj * FW + q) * 32 + l32;
+          if (b < B && o < IN) p[(size_t)b * IN + o] = from_f32<T>(acc[a][q][r]);
+        }
+      }
+    return;
+  } else if constexpr (EPI == 1) {
     const int K = bs.K, n_t = bs.n_t;
 #pragma unroll
     for (int a = 0; a < TM; ++a)
