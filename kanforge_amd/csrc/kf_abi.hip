@@ -509,12 +509,12 @@ int run_F(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
     if (L.skip0) return launch_f_rega<false, true>(L, batch, n_out, z, nullptr, cfm, ysum, y, s);
     return launch_f_rega<false, false>(L, batch, n_out, z, nullptr, cfm, nullptr, y, s);
   }
-  // B-spline, unweighted, in K a whole number of 128-byte stages: Phi (B, in K) in the
+  // B-spline or rational, unweighted, in K a whole number of 128-byte stages: Phi (B, in K) in the
   // reference's layout, then the flat GEMM Phi c^T on p_dma_kernel (no coefficient permute)
   constexpr int EPS = 128 / (int)sizeof(T);
   const long dma_tiles = ((batch + 255) / 256) * ((n_out + 255) / 256);  // at least half a round of the CUs
-  if (kb.kind == KF_KIND_BSPLINE && !has_w && (n_in * kb.K) % EPS == 0 && aligned16(c) && aligned16(phi) &&
-      dma_tiles >= 128)
+  const bool identity_fold = kb.kind == KF_KIND_BSPLINE || kb.kind == KF_KIND_RATIONAL;
+  if (identity_fold && !has_w && (n_in * kb.K) % EPS == 0 && aligned16(c) && aligned16(phi) && dma_tiles >= 128)
     return run_F_dma<T>(kb, batch, n_in, n_out, x, c, phi, y, s);
   int rc = launch_permute<T>(kb, n_out, n_in, L.OUTP, L.INP, L.n_tp, c, cfm, kPermFM, s);
   if (rc) return rc;

@@ -153,10 +153,10 @@ def test_edge_derivative_matches_oracle(name, m, base, dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16"])
-@pytest.mark.parametrize("name,m", [("bspline53", 0), ("bspline83", 1), ("bspline41", 0)])
+@pytest.mark.parametrize("name,m", [("bspline53", 0), ("bspline83", 1), ("bspline41", 0), ("rational", 0), ("rational", 1)])
 def test_F_many_tiles(name, m, dtype):
-    """Unweighted B-spline F over at least half a round of 256 x 256 tiles takes the flat
-    GEMM route (features in (B, in K) layout times coef^T); ragged batch and outputs."""
+    """Unweighted B-spline and rational F over at least half a round of 256 x 256 tiles take
+    the flat GEMM route (features in (B, in K) layout times coef^T); ragged batch and outputs."""
     B, IN, OUT = 4000, 64, 2100
     basis, plan, st, ob, x, rng = setup(name, B, IN, seed=12)
     c = rng.normal(0, 1 / math.sqrt(IN * basis.size), (OUT, IN, basis.size))
