@@ -579,7 +579,12 @@ int launch_p_dma_kind(const WsP& L, hipStream_t s, const KBasis& kb, int64_t bat
                       const void* g, int gstride, const void* cfmt, void* p, float* h) {
   constexpr int TM = p_dma_tm(FW), BM = 2 * TM * 32;
   const size_t knots = KIND == KF_KIND_BSPLINE ? (size_t)32 * (2 * kb.n_knots + 2 * kb.spline_k) * 4 : 0;
-  const size_t lds_ops = (size_t)2 * (BM + 2 * FW * 32) * 128, lds_epi = (size_t)3 * BM * 33 * 4 + knots;
+  size_t lds_epi = (size_t)3 * BM * 33 * 4 + knots;
+  if (KIND == KF_KIND_BSPLINE) {  // x, knots, then the features of one pass or the group sums
+    const size_t fb = (size_t)2 * FW * 64 * 33 * 4, red = (size_t)2 * BM * 33 * 4;
+    lds_epi = (size_t)BM * 33 * 4 + knots + (fb > red ? fb : red);
+  }
+  const size_t lds_ops = (size_t)2 * (BM + 2 * FW * 32) * 128;
   const size_t lds = lds_ops > lds_epi ? lds_ops : lds_epi;
   auto kern = p_dma_kernel<T, TM, FW, KIND>;
   if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)

@@ -1566,6 +1566,66 @@ __global__ __launch_bounds__(256) void p_dma_kernel(KBasis bs, int B, int IN, in
   }
   __syncthreads();  // every wave is done with the stage buffers: reuse them for x and the group sums
 
+  if constexpr (KIND == KF_KIND_BSPLINE && !FLAT) {
+    // B-spline: every (row, input) element's features are evaluated once per block (not once
+    // per feature-group wave), in TM passes of 2 x 32 rows: the block fills fb[j][64][33] in
+    // LDS, then each wave contracts its FW features with its accumulators.
+    float* xsb = reinterpret_cast<float*>(smem);  // [BM][33]
+    float* kcb = xsb + BM * 33;                   // the tile's knot rows
+    float* kpb = kcb + 32 * bs.n_knots;
+    float* fb = kpb + 32 * (bs.n_knots + 2 * bs.spline_k);  // [NTB][64][33]; then the group sums [2][BM][33]
+    stage_knot_rows(bs, i0, 32, IN, kcb, kpb);
+    for (int e = tid; e < BM * 32; e += 256) {
+      const int row = e / 32, ii = i0 + e % 32, b = b0 + row;
+      xsb[row * 33 + e % 32] = b < B && ii < IN ? to_f32(x[(size_t)b * IN + ii]) : 0.f;
+    }
+    __syncthreads();
+    const int n_t = bs.n_t, np = bs.n_knots + 2 * bs.spline_k;
+    float sum[TM][16];
+#pragma unroll
+    for (int a = 0; a < TM; ++a) {
+      for (int e = tid; e < 64 * 32; e += 256) {
+        const int rowp = e / 32, il = e % 32;
+        const int row = (rowp / 32) * WM + a * 32 + rowp % 32;
+        const bool ok = b0 + row < B && i0 + il < IN;
+        float f[NTB];
+        bspline_dispatch_rows<NTB>(xsb[row * 33 + il], 1.f, kcb + il * bs.n_knots, kpb + il * np, bs, f);
+#pragma unroll
+        for (int j = 0; j < NTB; ++j)
+          if (j < n_t) fb[(j * 64 + rowp) * 33 + il] = ok ? f[j] : 0.f;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int rowp = wm * 32 + acc_row(r, lane);
+        float v = 0.f;
+#pragma unroll
+        for (int q = 0; q < FW; ++q)
+          if (wj * FW + q < n_t) v = fmaf(acc[a][q][r], fb[((wj * FW + q) * 64 + rowp) * 33 + l32], v);
+        sum[a][r] = v;
+      }
+      __syncthreads();  // the next pass rewrites fb
+    }
+    float* redb = fb;  // [2][BM][33]
+    const int i = i0 + l32;
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = wm * WM + a * 32 + acc_row(r, lane);
+        const int b = b0 + row;
+        if (hout && wj == 0 && b < B && i < IN) hout[(size_t)b * IN + i] = acc[a][0][r];
+        redb[(wj * BM + row) * 33 + l32] = sum[a][r];
+      }
+    __syncthreads();
+    for (int e = tid; e < BM * 32; e += 256) {
+      const int row = e / 32, il = e % 32;
+      const int b = b0 + row, ii = i0 + il;
+      if (b < B && ii < IN) p[(size_t)b * IN + ii] = from_f32<T>(redb[row * 33 + il] + redb[(BM + row) * 33 + il]);
+    }
+    return;
+  }
+
   // x of the tile into LDS, all loads in flight at once (coalesced along the inputs)
   float* red = reinterpret_cast<float*>(smem);  // [2][BM][33]: the two feature groups' sums
   float* xs = red + 2 * BM * 33;                // [BM][33]
