@@ -367,9 +367,9 @@ int launch_features(const KBasis& kb, int64_t batch, int64_t n_in, int64_t brows
 template <typename T, int NTB>
 int launch_features_t_nb(const KBasis& kb, int64_t batch, int64_t n_in, int64_t BP, int64_t INP, const void* x,
                          const void* w, void* phit, hipStream_t s) {
-  constexpr int BT = 128 / (int)sizeof(T);
+  constexpr int BT = 64 / (int)sizeof(T);  // features_t_kernel: 32 inputs x 64-byte runs of rows
   const size_t knots = kb.kind == KF_KIND_BSPLINE ? (size_t)32 * (2 * kb.n_knots + 2 * kb.spline_k) * 4 : 0;
-  const size_t lds = (size_t)kb.n_t * 32 * 144 + knots;
+  const size_t lds = (size_t)kb.n_t * 32 * 80 + knots;
   auto kern = features_t_kernel<T, NTB>;
   if (lds > 65536 &&
       hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)

@@ -1007,14 +1007,16 @@ __global__ __launch_bounds__(kThreads) void g_split_reduce(KBasis bs, int OUT, i
 // phiT[j][i][b] = w[b][i] * feature_j(x[b][i]) for j < n_t, zero where
 // b >= B or i >= IN, over the padded (INP, BP) extent: the B operand of G for
 // kinds whose features are not generated in the G kernel. A block covers 32
-// inputs x (128 / sizeof(T)) rows: x is read along the inputs, each element's
-// features go to LDS, and every (j, i) row segment leaves as one 128-byte
-// run along the batch.
+// inputs x (64 / sizeof(T)) rows: x is read along the inputs, each element's
+// features go to LDS, and every (j, i) row segment leaves as one 64-byte run
+// along the batch (64-byte rather than 128-byte runs halve the LDS per block,
+// which doubles the resident blocks of this latency-bound kernel).
 template <typename T, int NTB>
 __global__ __launch_bounds__(kThreads) void features_t_kernel(KBasis bs, int B, int IN, int BP, int INP,
                                                               const T* __restrict__ x, const T* __restrict__ w,
                                                               T* __restrict__ phit) {
-  constexpr int BT = 128 / (int)sizeof(T), RSB = 144, PER = 32 * BT / kThreads, VW = 16 / (int)sizeof(T);
+  constexpr int RUN = 64, BT = RUN / (int)sizeof(T), RSB = RUN + 16, CPR = RUN / 16;
+  constexpr int PER = 32 * BT / kThreads, VW = 16 / (int)sizeof(T);
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];  // [n_t][32][RSB], B-spline knot rows
   const int n_t = bs.n_t;
   const int i0 = blockIdx.x * 32, b0 = blockIdx.y * BT;
@@ -1042,9 +1044,9 @@ __global__ __launch_bounds__(kThreads) void features_t_kernel(KBasis bs, int B, 
       if (j < n_t) reinterpret_cast<T*>(smem + (size_t)(j * 32 + il) * RSB)[bl] = from_f32<T>(ok ? f[j] : 0.f);
   }
   __syncthreads();
-  const int total = n_t * 32 * 8;
+  const int total = n_t * 32 * CPR;
   for (int c = threadIdx.x; c < total; c += kThreads) {
-    const int r = c / 8, q = c % 8, j = r / 32, il = r % 32, b = b0 + q * VW;
+    const int r = c / CPR, q = c % CPR, j = r / 32, il = r % 32, b = b0 + q * VW;
     if (b < BP) gstore16(phit + ((size_t)j * INP + i0 + il) * BP + b, lds_read16(smem + (size_t)r * RSB + 16 * q));
   }
 }
