@@ -463,8 +463,23 @@ int run_F_dma(const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out, cons
               void* y, hipStream_t s) {
   constexpr int FW = kGdmaFW, TM = p_dma_tm(FW), BM = 2 * TM * 32, TI = 2 * FW * 32;
   const long ld = (long)n_in * kb.K;  // Phi row length: the reduction
-  int rc = launch_features<T, false>(kb, batch, n_in, batch, n_in, x, phi, ld, 1L, (long)kb.K, false, s);
-  if (rc) return rc;
+  if (kb.n_t != kb.K || (ld * (long)sizeof(T)) % 16) return fail(KF_EINVAL, "F: Phi rows not aligned");
+  if (kb.K == 1) {  // one feature: the plain (B, in) writes are already coalesced
+    int rc = launch_features<T, false>(kb, batch, n_in, batch, n_in, x, phi, ld, 1L, 1L, false, s);
+    if (rc) return rc;
+  } else {
+    dim3 pg((unsigned)((n_in + kThreads - 1) / kThreads), (unsigned)(batch < 65535 ? batch : 65535));
+    const size_t plds = (size_t)kThreads * kb.K * sizeof(T);
+    switch (nt_bucket(kb.n_t)) {
+      case 4: hipLaunchKernelGGL((phi_rows_kernel<T, 4>), pg, dim3(kThreads), plds, s, kb, (int)batch, (int)n_in, (const T*)x, (T*)phi); break;
+      case 8: hipLaunchKernelGGL((phi_rows_kernel<T, 8>), pg, dim3(kThreads), plds, s, kb, (int)batch, (int)n_in, (const T*)x, (T*)phi); break;
+      case 12: hipLaunchKernelGGL((phi_rows_kernel<T, 12>), pg, dim3(kThreads), plds, s, kb, (int)batch, (int)n_in, (const T*)x, (T*)phi); break;
+      case 16: hipLaunchKernelGGL((phi_rows_kernel<T, 16>), pg, dim3(kThreads), plds, s, kb, (int)batch, (int)n_in, (const T*)x, (T*)phi); break;
+      default: hipLaunchKernelGGL((phi_rows_kernel<T, 24>), pg, dim3(kThreads), plds, s, kb, (int)batch, (int)n_in, (const T*)x, (T*)phi); break;
+    }
+    int rc = check_launch("phi_rows");
+    if (rc) return rc;
+  }
   const size_t lds = (size_t)2 * (BM + TI) * 128;
   auto kern = p_dma_kernel<T, TM, FW, KF_KIND_BSPLINE, 2>;
   if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)

@@ -1004,6 +1004,34 @@ __global__ __launch_bounds__(kThreads) void g_split_reduce(KBasis bs, int OUT, i
   }
 }
 
+// Phi[b][i][k] = feature_k(x[b][i]) (n_t = K features, unweighted) in the
+// reference's (B, in K) layout, for F's flat GEMM. A block covers 256 inputs of
+// one row at a time: the features go to LDS and the row's contiguous segment
+// leaves in 16-byte chunks. Needs (IN K sizeof(T)) % 16 == 0.
+template <typename T, int NTB>
+__global__ __launch_bounds__(kThreads) void phi_rows_kernel(KBasis bs, int B, int IN, const T* __restrict__ x,
+                                                            T* __restrict__ phi) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];  // [kThreads * K] T
+  constexpr int VW = 16 / (int)sizeof(T);
+  T* buf = reinterpret_cast<T*>(smem);
+  const int K = bs.n_t, i0 = blockIdx.x * kThreads, i = i0 + threadIdx.x;
+  const int n = (IN - i0 < kThreads ? IN - i0 : kThreads) * K, nv = n / VW;
+  for (int b = blockIdx.y; b < B; b += gridDim.y) {
+    if (i < IN) {
+      float f[NTB];
+      kernel_features<NTB>(to_f32(x[(size_t)b * IN + i]), 1.f, i, bs, f);
+#pragma unroll
+      for (int j = 0; j < NTB; ++j)
+        if (j < K) buf[threadIdx.x * K + j] = from_f32<T>(f[j]);
+    }
+    __syncthreads();
+    T* dst = phi + ((size_t)b * IN + i0) * K;
+    for (int c = threadIdx.x; c < nv; c += kThreads) gstore16(dst + (size_t)c * VW, lds_read16(smem + 16 * c));
+    for (int e = nv * VW + threadIdx.x; e < n; e += kThreads) dst[e] = buf[e];
+    __syncthreads();  // the next row rewrites buf
+  }
+}
+
 // phiT[j][i][b] = w[b][i] * feature_j(x[b][i]) for j < n_t, zero where
 // b >= B or i >= IN, over the padded (INP, BP) extent: the B operand of G for
 // kinds whose features are not generated in the G kernel. A block covers 32
