@@ -2,7 +2,11 @@
 bfloat16 with float32 accumulation, batch 8192; one step = forward + dX + dCoef
 (the F_0, P_1 and G_0 launches of the HIP path). Prints one JSON line.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-base]
+    python bench.py --workload {bspline_ffn,grkan_ffn,pinn_edge,pinn_laplacian,kan64,all}
+
+The second form times the other layer shapes instead of the headline, one JSON
+line each (whole-step throughput and HIP-event means per entry point).
 
 Inputs are seeded synthetic tensors resident in HBM before timing starts:
 x ~ N(0, 1) (seed 0), coef ~ N(0, 1/(768*9)) (seed 1), upstream gradient
@@ -131,7 +135,7 @@ def _randn(shape, seed, scale=1.0):
     return torch.randn(*shape, generator=torch.Generator().manual_seed(seed)) * scale
 
 
-def wl_bspline_ffn(dev, timer):
+def wl_bspline_ffn(dev):
     """kanify'd GPT-2-small FFN: KANLinear 768->3072 then 3072->768, B-spline grid 8 order 3
     (K=11), layer defaults (SiLU base, bias), bf16, 8 x 2048 tokens, forward + backward."""
     import kanforge_amd as kf
@@ -153,7 +157,7 @@ def wl_bspline_ffn(dev, timer):
     return step, tok, "tokens/s", 6 * per_contraction + 6 * 2.0 * tok * dim * hid, per_contraction, "bf16"
 
 
-def wl_grkan_ffn(dev, timer):
+def wl_grkan_ffn(dev):
     """GR-KAN FFN 768->3072->768, 8 groups, rational P degree 5 / Q degree 4, bf16,
     16 x 1024 tokens, P/Q ~ N(0, 0.1), forward + backward."""
     from kanforge_amd.torch.transformer import KANFFN
@@ -187,7 +191,7 @@ def _pinn_model(dev):
     return model, x
 
 
-def wl_pinn_edge(dev, timer):
+def wl_pinn_edge(dev):
     """PINN KAN [2, 64, 64, 1] Jacobi(6, 1/2, 1/2) tanh, fp32, 65536 points x ~ U(-1, 1)^2:
     KAN.edge_derivative(x, 2), every layer's (points, out, in) second derivatives."""
     model, x = _pinn_model(dev)
@@ -202,7 +206,7 @@ def wl_pinn_edge(dev, timer):
     return step, n, "points/s", None, out_bytes + in_bytes, "f32"
 
 
-def wl_pinn_laplacian(dev, timer):
+def wl_pinn_laplacian(dev):
     """The same PINN network: the chained Laplacian d2u/dx0^2 + d2u/dx1^2 over the
     network by reverse-over-reverse autograd through the F/G/P closure."""
     from kanforge_amd.torch import laplacian
@@ -217,7 +221,7 @@ def wl_pinn_laplacian(dev, timer):
     return step, n, "points/s", None, layer_pass, "f32"
 
 
-def wl_kan64(dev, timer):
+def wl_kan64(dev):
     """KANLinear 64->64 B-spline (grid 5, order 3, K=8) on [-1, 1], SiLU base, fp32,
     batch 4096, x ~ U(-1, 1), coef ~ N(0, 1/(64*8)), forward + backward."""
     import kanforge_amd as kf
@@ -258,7 +262,7 @@ def run_workload(name, args, dev):
     kmod._edge_raw = timer.wrap(orig[1], "edge")
     kmod._features_raw = timer.wrap(orig[2], "features")
     try:
-        step, units, unit, step_flop, per_launch, dtype = WORKLOADS[name](dev, timer)
+        step, units, unit, step_flop, per_launch, dtype = WORKLOADS[name](dev)
         ms = _timed(step, args.steps, args.warmup, timer)
     finally:
         kmod._raw, kmod._edge_raw, kmod._features_raw = orig
