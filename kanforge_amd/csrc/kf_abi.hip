@@ -105,6 +105,12 @@ KBasis to_kbasis(const kf_basis* b) {
   return k;
 }
 
+// Whether a call's features carry a per-element weight: an explicit w, or the (1 - z^2) factor of
+// a reduced tanh fold. The workspace size checks and the workspace layouts of F and G both use it.
+bool features_weighted(const kf_basis* b, const void* w) {
+  return w != nullptr || (b->kind == KF_KIND_CHEB && b->input_map == KF_MAP_TANH_SQ);
+}
+
 int nt_bucket(int n) { return n <= 4 ? 4 : n <= 8 ? 8 : n <= 12 ? 12 : n <= 16 ? 16 : 24; }
 
 // F tile configurations: (BM, BN, waves along M, waves along N), 512 threads.
@@ -495,8 +501,7 @@ int run_F(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
           const void* w, const void* c, void* y, void* ws, hipStream_t s) {
   const bool has_w = w != nullptr;
   const bool cheb = kb.kind == KF_KIND_CHEB;
-  // Chebyshev features carry a weight when w is given or the map has the (1 - z^2) factor
-  const bool weighted = has_w || (cheb && kb.input_map == KF_MAP_TANH_SQ);
+  const bool weighted = features_weighted(b, w);
   WsF L = ws_f(b, dtype, batch, n_in, n_out, weighted);
   char* base = (char*)ws;
   void* cfm = base;
@@ -792,7 +797,7 @@ template <typename T>
 int run_G(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
           const void* g, const void* w, void* dc, void* ws, hipStream_t s) {
   const bool cheb_kind = kb.kind == KF_KIND_CHEB;
-  const bool weighted = w != nullptr || (cheb_kind && kb.input_map == KF_MAP_TANH_SQ);
+  const bool weighted = features_weighted(b, w);
   WsG L = ws_g(b, dtype, batch, n_in, n_out, weighted);
   const bool cheb = cheb_kind && !L.pre;
   char* base = (char*)ws;
@@ -896,7 +901,7 @@ int kf_F(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
   hipStream_t s = (hipStream_t)stream;
   if (n_in == 0) return dtype == KF_BF16 ? zero_fill<bf16>(y, (long)batch * n_out, s) : zero_fill<float>(y, (long)batch * n_out, s);
   if (!x || !c || !y) return fail(KF_EINVAL, "kf_F: NULL array");
-  size_t need = ws_f(b, dtype, batch, n_in, n_out, w != nullptr).total;
+  size_t need = ws_f(b, dtype, batch, n_in, n_out, features_weighted(b, w)).total;
   if (!workspace || workspace_bytes < need)
     return fail(KF_EWORKSPACE, "kf_F: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
   if (reinterpret_cast<uintptr_t>(workspace) & 255)
@@ -916,7 +921,7 @@ int kf_G(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
   const long n = (long)n_out * n_in * b->size;
   if (batch == 0) return dtype == KF_BF16 ? zero_fill<bf16>(dc, n, s) : zero_fill<float>(dc, n, s);
   if (!x || !g || !dc) return fail(KF_EINVAL, "kf_G: NULL array");
-  size_t need = ws_g(b, dtype, batch, n_in, n_out, w != nullptr).total;
+  size_t need = ws_g(b, dtype, batch, n_in, n_out, features_weighted(b, w)).total;
   if (!workspace || workspace_bytes < need)
     return fail(KF_EWORKSPACE, "kf_G: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
   if (reinterpret_cast<uintptr_t>(workspace) & 255)

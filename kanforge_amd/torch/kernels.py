@@ -323,19 +323,38 @@ def _features_raw(plan, m, st, x2: torch.Tensor) -> torch.Tensor:
 
 
 class _Features(torch.autograd.Function):
-    """phi^(m)(x) (B, in, K); d/dx is phi^(m+1)."""
+    """phi^(m)(x) (B, in, K); d/dx is phi^(m+1). Rational plans also return the gradients of
+    their parameters ``num``/``den`` (order 0)."""
 
     @staticmethod
-    def forward(ctx, x2, st, plan, m):
-        ctx.save_for_backward(x2)
+    def forward(ctx, x2, num, den, st, plan, m):
+        ctx.save_for_backward(x2, num, den)
         ctx.st, ctx.plan, ctx.m = st, plan, m
         return _features_raw(plan, m, st, x2.contiguous())
 
     @staticmethod
     def backward(ctx, gphi):
-        (x2,) = ctx.saved_tensors
-        d = _Features.apply(x2, ctx.st, ctx.plan, ctx.m + 1)
-        return (gphi * d).sum(-1), None, None, None
+        x2, num, den = ctx.saved_tensors
+        st, plan, m = ctx.st, ctx.plan, ctx.m
+        need = ctx.needs_input_grad
+        gx = gnum = gden = None
+        if need[0]:
+            d = _Features.apply(x2, num, den, st, plan, m + 1)
+            gx = (gphi * d).sum(-1)
+        if need[1] or need[2]:
+            gnum, gden = _rational_grads_of(plan, st, x2, gphi[..., 0], m, num, den, need[1], need[2])
+        return gx, gnum, gden, None, None, None
+
+
+def _rational_grads_of(plan, st, x2, h, m, num, den, want_num, want_den):
+    """d/d(num, den) of sum_{b,i} h[b,i] phi^(m)(x[b,i]) for a rational plan (order 0 only)."""
+    if plan.kind != "rational":
+        return None, None
+    if m != 0 or torch.is_grad_enabled():
+        raise NotImplementedError("rational parameter gradients of derivative features (order >= 1) or of second "
+                                  "order are not compiled into the HIP kernels")
+    dnum, dden = _rational_param_grad(plan, st, x2, h.float().contiguous(), None)
+    return (dnum.to(num.dtype) if want_num else None), (dden.to(den.dtype) if want_den else None)
 
 
 def basis_derivative(basis, x: torch.Tensor, m: int, params: dict | None) -> torch.Tensor:
@@ -353,7 +372,13 @@ def basis_derivative(basis, x: torch.Tensor, m: int, params: dict | None) -> tor
     x2 = x.reshape(-1, x.shape[-1])
     if x2.dtype not in _DTYPES:
         x2 = x2.float()
-    out = _Features.apply(x2, st, plan, m)
+    num = den = None
+    if plan.kind == "rational" and params is not None and isinstance(params.get("numerator"), torch.Tensor):
+        # the (rows, p+1) / (rows, q) views the state was built from, so gradients reach the caller's tensors
+        num, den = params["numerator"], params["denominator"]
+        if num.dim() == 1:
+            num, den = num[None], den[None]
+    out = _Features.apply(x2, num, den, st, plan, m)
     return out.to(x.dtype).reshape(*lead, x.shape[-1], plan.size)
 
 
@@ -403,27 +428,31 @@ class _Edge(torch.autograd.Function):
     """d[b,o,i] = sum_k c[o,i,k] phi_k^(m)(x[b,i]) + W[o,i] silu^(m)(x[b,i])."""
 
     @staticmethod
-    def forward(ctx, x2, c, base_w, st, plan, m):
-        ctx.save_for_backward(x2, c, base_w)
+    def forward(ctx, x2, c, base_w, num, den, st, plan, m):
+        ctx.save_for_backward(x2, c, base_w, num, den)
         ctx.st, ctx.plan, ctx.m = st, plan, m
         return _edge_raw(plan, m, st, x2.contiguous(), c, base_w)
 
     @staticmethod
     def backward(ctx, gd):
-        x2, c, base_w = ctx.saved_tensors
+        x2, c, base_w, num, den = ctx.saved_tensors
         st, plan, m = ctx.st, ctx.plan, ctx.m
         need = ctx.needs_input_grad
-        gx = gc = gw = None
+        gx = gc = gw = gnum = gden = None
         if need[0]:
             # d/dx of the edge is the edge derivative of order m+1
-            gx = (gd * _Edge.apply(x2, c, base_w, st, plan, m + 1)).sum(1)
+            gx = (gd * _Edge.apply(x2, c, base_w, num, den, st, plan, m + 1)).sum(1)
         if need[1]:
-            phi = _Features.apply(x2, st, plan, m)  # (B, in, K)
+            phi = _Features.apply(x2, None, None, st, plan, m)  # (B, in, K)
             gc = torch.einsum("boi,bik->oik", gd, phi)
         if need[2] and base_w is not None:
             s = silu_derivative_t(x2, m)
             gw = torch.einsum("boi,bi->oi", gd, s)
-        return gx, gc, gw, None, None, None
+        if need[3] or need[4]:
+            # one feature per edge: sum_o gd[b,o,i] c[o,i,0] multiplies phi^(m)(x[b,i])
+            h = torch.einsum("boi,oi->bi", gd.float(), c[..., 0].float())
+            gnum, gden = _rational_grads_of(plan, st, x2, h, m, num, den, need[3], need[4])
+        return gx, gc, gw, gnum, gden, None, None, None
 
 
 def silu_derivative_t(x: torch.Tensor, m: int) -> torch.Tensor:
@@ -444,14 +473,16 @@ def silu_derivative_t(x: torch.Tensor, m: int) -> torch.Tensor:
     return x * hp(polys[m]) + m * hp(polys[m - 1])
 
 
-def edge_derivative(x: torch.Tensor, coef_eff: torch.Tensor, base_w: torch.Tensor | None, st, plan, m: int) -> torch.Tensor:
-    """(..., out, in) edge derivatives through kf_edge_derivative."""
+def edge_derivative(x: torch.Tensor, coef_eff: torch.Tensor, base_w: torch.Tensor | None, st, plan, m: int,
+                    num=None, den=None) -> torch.Tensor:
+    """(..., out, in) edge derivatives through kf_edge_derivative; a rational plan's ``num``/``den``
+    (groups, ...) receive gradients (order 0)."""
     _require_device(x)
     lead = x.shape[:-1]
     x2 = x.reshape(-1, x.shape[-1])
     if x2.dtype != coef_eff.dtype:
         x2 = x2.to(coef_eff.dtype)
-    d = _Edge.apply(x2, coef_eff, base_w, st, plan, m)
+    d = _Edge.apply(x2, coef_eff, base_w, num, den, st, plan, m)
     return d.to(x.dtype).reshape(*lead, coef_eff.shape[0], x.shape[-1])
 
 

@@ -236,7 +236,10 @@ class KANLinear(nn.Module):
             raise NotImplementedError("the HIP edge kernel evaluates the SiLU base branch only")
         if self._sym_codes:
             raise NotImplementedError("symbolic edges are not part of the HIP path")
-        return _kernels.edge_derivative(x, self.effective_coef(), bw, self._basis_state(), self._plan, int(order))
+        num = den = None
+        if self._plan.kind == "rational":
+            num, den = self.basis_numerator, self.basis_denominator
+        return _kernels.edge_derivative(x, self.effective_coef(), bw, self._basis_state(), self._plan, int(order), num, den)
 
     # --- state import / export (kanforge.save format) ------------------------------
 

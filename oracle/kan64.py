@@ -352,7 +352,7 @@ def kan_linear(x, coef, basis, base_weight=None, bias=None, edge_scale=None):
     coef = np.asarray(coef, dtype=np.float64)
     if edge_scale is not None:
         coef = coef * np.asarray(edge_scale, dtype=np.float64)[..., None]
-    y = np.einsum("...ik,oik->...o", basis(x), coef)
+    y = np.einsum("...ik,oik->...o", basis(x), coef, optimize=True)
     if base_weight is not None:
         y = y + silu_derivative(x, 0) @ np.asarray(base_weight, dtype=np.float64).T
     if bias is not None:
@@ -369,7 +369,7 @@ def prim_F(x, c, w, basis, m=0):
     phi = basis(x, m)
     if w is not None:
         phi = phi * np.asarray(w, dtype=np.float64)[..., None]
-    return np.einsum("bik,oik->bo", phi, np.asarray(c, dtype=np.float64))
+    return np.einsum("bik,oik->bo", phi, np.asarray(c, dtype=np.float64), optimize=True)
 
 
 def prim_G(x, g, w, basis, m=0):
@@ -377,13 +377,13 @@ def prim_G(x, g, w, basis, m=0):
     phi = basis(x, m)
     if w is not None:
         phi = phi * np.asarray(w, dtype=np.float64)[..., None]
-    return np.einsum("bik,bo->oik", phi, np.asarray(g, dtype=np.float64))
+    return np.einsum("bik,bo->oik", phi, np.asarray(g, dtype=np.float64), optimize=True)
 
 
 def prim_P(x, g, c, basis, m=0):
     """P_m[b,i] = sum_{o,k} g[b,o] c[o,i,k] phi_k^(m)(x[b,i])."""
     phi = basis(x, m)
-    h = np.einsum("bo,oik->bik", np.asarray(g, dtype=np.float64), np.asarray(c, dtype=np.float64))
+    h = np.einsum("bo,oik->bik", np.asarray(g, dtype=np.float64), np.asarray(c, dtype=np.float64), optimize=True)
     return (h * phi).sum(-1)
 
 
@@ -392,7 +392,7 @@ def edge_derivative(x, coef_eff, basis, m=0, base_weight_eff=None):
 
     Follows ``kanforge/torch/layers.py:206-226`` (SiLU base only).
     """
-    d = np.einsum("bik,oik->boi", basis(x, m), np.asarray(coef_eff, dtype=np.float64))
+    d = np.einsum("bik,oik->boi", basis(x, m), np.asarray(coef_eff, dtype=np.float64), optimize=True)
     if base_weight_eff is not None:
         d = d + silu_derivative(x, m)[:, None, :] * np.asarray(base_weight_eff, dtype=np.float64)[None]
     return d

@@ -202,6 +202,36 @@ def test_abi_rejects_bad_arguments_without_launching():
     assert rc == -1 and b"n_knots" in lib.kf_last_error()
 
 
+def _needed_bytes(lib, fn, b, w):
+    """The workspace size an entry point asks for, read from its error text (1-byte workspace)."""
+    p = ctypes.c_void_p(256)
+    if fn is lib.kf_F:  # (x, w, c, y)
+        rc = fn(ctypes.byref(b), _lib.KF_BF16, 8192, 768, 3072, p, w, p, p, p, 1, None)
+    else:  # kf_G: (x, g, w, dc)
+        rc = fn(ctypes.byref(b), _lib.KF_BF16, 8192, 768, 3072, p, p, w, p, p, 1, None)
+    assert rc == -2
+    return int(re.search(rb"workspace of (\d+) bytes needed", lib.kf_last_error()).group(1))
+
+
+@pytest.mark.parametrize("op", ["kf_F", "kf_G"])
+def test_workspace_check_uses_the_layout_of_reduced_tanh_folds(op):
+    """A reduced tanh fold (input map TANH_SQ) carries the (1 - z^2) weight even when w is NULL:
+    the size check must ask for the weighted layout the kernels then carve."""
+    lib = _lib.load()
+    fn = getattr(lib, op)
+    b = _lib.KfBasis()
+    fold = np.ones((9, 8), dtype=np.float32)
+    b.kind, b.size, b.order, b.n_t = _lib.KF_KIND_CHEB, 9, 1, 8
+    b.fold = fold.ctypes.data_as(ctypes.c_void_p)
+    b.input_map = _lib.KF_MAP_TANH_SQ
+    unweighted_call = _needed_bytes(lib, fn, b, None)
+    weighted_call = _needed_bytes(lib, fn, b, ctypes.c_void_p(256))
+    assert unweighted_call == weighted_call
+    assert unweighted_call <= lib.kf_workspace_bytes(_lib.KF_OP_F if op == "kf_F" else _lib.KF_OP_G, ctypes.byref(b), 1, 8192, 768, 3072)
+    b.input_map = _lib.KF_MAP_TANH  # a plain tanh map without w has the smaller unweighted layout
+    assert _needed_bytes(lib, fn, b, None) < weighted_call
+
+
 # --- CPU baseline route ------------------------------------------------------------
 
 
