@@ -118,6 +118,19 @@ int kf_F(const kf_basis *basis, int dtype, int64_t batch, int64_t n_in, int64_t 
          const void *w, const void *c, void *y, void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * kf_F without a workspace argument and without any allocation: the same kernels and result as
+ * kf_F, with their scratch in a static device array of KF_NOALLOC_SCRATCH_BYTES that the library
+ * holds on every GPU it runs on until the process ends. No counterpart in the reference: it is for
+ * callers that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). Shapes whose F workspace exceeds the scratch are rejected with
+ * KF_EWORKSPACE. Every call on one GPU shares that GPU's scratch: calls that overlap on one GPU
+ * (on different streams, or from different threads) race; calls ordered on one stream do not.
+ */
+#define KF_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int kf_F_noalloc(const kf_basis *basis, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void *x,
+                 const void *w, const void *c, void *y, void *stream);
+
+/*
  * dc[o,i,k] = sum_b w[b,i] g[b,o] phi_k^(m)(x[b,i])              (op "G")
  * g (batch, n_out); dc (n_out, n_in, size). Replaces _raw("G", ...) and the
  * fold gt @ R_m^T (kanforge/torch/kernels.py:95-98).

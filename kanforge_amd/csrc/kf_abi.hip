@@ -3,6 +3,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "kf_kernels.h"
@@ -868,6 +869,34 @@ int run_edge(const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out, const
   return check_launch("edge_derivative");
 }
 
+// Scratch of kf_F_noalloc: a file-scope device array, so that entry point never allocates. Every
+// GPU the library runs on holds its own copy (at its own address) until the process ends. Host
+// code never uses the array's name as an address: the address of the current device's copy comes
+// from hipGetSymbolAddress, looked up once per device with that device current.
+static __device__ __align__(256) unsigned char scratch[KF_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::once_flag g_scratch_once[kMaxDevices];
+void* g_scratch_ptr[kMaxDevices];
+hipError_t g_scratch_err[kMaxDevices];
+
+int scratch_of_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(KF_ELAUNCH, "kf_F_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(KF_EUNSUPPORTED, "kf_F_noalloc: device %d >= %d", dev, kMaxDevices);
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* p = nullptr;
+    g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_ptr[dev] = g_scratch_err[dev] == hipSuccess ? p : nullptr;
+  });
+  if (g_scratch_err[dev] != hipSuccess || !g_scratch_ptr[dev])
+    return fail(KF_ELAUNCH, "kf_F_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                hipGetErrorString(g_scratch_err[dev]));
+  *out = g_scratch_ptr[dev];
+  return KF_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -909,6 +938,27 @@ int kf_F(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
   KBasis kb = to_kbasis(b);
   if (dtype == KF_BF16) return run_F<bf16>(kb, b, dtype, batch, n_in, n_out, x, w, c, y, workspace, s);
   return run_F<float>(kb, b, dtype, batch, n_in, n_out, x, w, c, y, workspace, s);
+}
+
+int kf_F_noalloc(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
+                 const void* w, const void* c, void* y, void* stream) {
+  g_err.clear();
+  int rc = validate_common(b, dtype, batch, n_in, n_out);
+  if (rc) return rc;
+  if (batch == 0 || n_out == 0) return KF_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (n_in == 0) return dtype == KF_BF16 ? zero_fill<bf16>(y, (long)batch * n_out, s) : zero_fill<float>(y, (long)batch * n_out, s);
+  if (!x || !c || !y) return fail(KF_EINVAL, "kf_F_noalloc: NULL array");
+  const size_t need = ws_f(b, dtype, batch, n_in, n_out, features_weighted(b, w)).total;
+  if (need > KF_NOALLOC_SCRATCH_BYTES)
+    return fail(KF_EWORKSPACE, "kf_F_noalloc: these shapes need %zu bytes of scratch, the static scratch holds %zu",
+                need, (size_t)KF_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  rc = scratch_of_current_device(&ws);
+  if (rc) return rc;
+  KBasis kb = to_kbasis(b);
+  if (dtype == KF_BF16) return run_F<bf16>(kb, b, dtype, batch, n_in, n_out, x, w, c, y, ws, s);
+  return run_F<float>(kb, b, dtype, batch, n_in, n_out, x, w, c, y, ws, s);
 }
 
 int kf_G(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* g,

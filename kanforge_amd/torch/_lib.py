@@ -21,10 +21,13 @@ KF_KIND_CHEB, KF_KIND_BSPLINE, KF_KIND_RATIONAL = 0, 1, 2
 KF_MAP_IDENTITY, KF_MAP_TANH, KF_MAP_TANH_SQ = 0, 1, 2
 KF_OP_F, KF_OP_G, KF_OP_P = 0, 1, 2
 KF_MAX_K, KF_MAX_NT = 16, 24
+KF_EWORKSPACE = -2
+KF_NOALLOC_SCRATCH_BYTES = 64 << 20
 
 EXPORTS = (
     "kf_workspace_bytes",
     "kf_F",
+    "kf_F_noalloc",
     "kf_G",
     "kf_P",
     "kf_features",
@@ -80,6 +83,7 @@ def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
         lib.kf_workspace_bytes.argtypes = [c_int, P, c_int, c_int64, c_int64, c_int64]
         lib.kf_workspace_bytes.restype = c_size_t
         lib.kf_F.argtypes = [P, c_int, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]
+        lib.kf_F_noalloc.argtypes = [P, c_int, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]
         lib.kf_G.argtypes = [P, c_int, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]
         lib.kf_P.argtypes = [P, c_int, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]
         lib.kf_features.argtypes = [P, c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p]
@@ -88,7 +92,7 @@ def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
         lib.kf_rational_workspace_bytes.argtypes = [P, c_int64, c_int64]
         lib.kf_rational_workspace_bytes.restype = c_size_t
         lib.kf_rational_param_grad.argtypes = [P, c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]
-        for name in ("kf_F", "kf_G", "kf_P", "kf_features", "kf_edge_derivative", "kf_bspline_interval", "kf_rational_param_grad"):
+        for name in ("kf_F", "kf_F_noalloc", "kf_G", "kf_P", "kf_features", "kf_edge_derivative", "kf_bspline_interval", "kf_rational_param_grad"):
             getattr(lib, name).restype = c_int
         lib.kf_last_error.argtypes = []
         lib.kf_last_error.restype = c_char_p

@@ -248,3 +248,16 @@ def test_cpu_baseline_route_matches_oracle():
     np.testing.assert_allclose(y.detach().numpy(), o.prim_F(xn, cn, None, ob, 0), atol=1e-12)
     np.testing.assert_allclose(gx.numpy(), o.prim_P(xn, gn, cn, ob, 1), atol=1e-12)
     np.testing.assert_allclose(gc.numpy(), o.prim_G(xn, gn, None, ob, 0), atol=1e-12)
+
+
+def test_noalloc_F_rejects_shapes_beyond_its_static_scratch_before_any_launch():
+    lib = _lib.load()
+    b = _lib.KfBasis()
+    fold = np.eye(9, dtype=np.float32)
+    b.kind, b.size, b.order, b.n_t, b.input_map = _lib.KF_KIND_CHEB, 9, 0, 9, _lib.KF_MAP_TANH
+    b.fold = fold.ctypes.data_as(ctypes.c_void_p)
+    p = ctypes.c_void_p(256)
+    rc = lib.kf_F_noalloc(ctypes.byref(b), _lib.KF_BF16, 8192, 768, 4096, p, p, p, p, None)
+    assert rc == _lib.KF_EWORKSPACE and b"static scratch" in lib.kf_last_error()
+    need = lib.kf_workspace_bytes(_lib.KF_OP_F, ctypes.byref(b), _lib.KF_BF16, 8192, 768, 4096)
+    assert need > _lib.KF_NOALLOC_SCRATCH_BYTES
