@@ -4,7 +4,9 @@
 #include <cstdio>
 #include <cstring>
 #include <mutex>
+#include <set>
 #include <string>
+#include <utility>
 
 #include "kf_kernels.h"
 
@@ -28,6 +30,25 @@ int check_launch(const char* what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(KF_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
   return KF_OK;
+}
+
+// The dynamic-LDS ceiling of a kernel above the default 64 KB is raised once per (device, kernel)
+// to the whole 160 KB of a CU; launches then pass their actual size. The table of kernels already
+// raised is the library's only mutable state besides the scratch addresses, and is guarded.
+constexpr int kLdsCeiling = 160 * 1024;
+std::mutex g_lds_mutex;
+std::set<std::pair<int, const void*>> g_lds_raised;
+
+bool reserve_lds(const void* kern, size_t lds) {
+  if (lds <= 65536) return true;
+  if (lds > (size_t)kLdsCeiling) return false;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return false;
+  std::lock_guard<std::mutex> lock(g_lds_mutex);
+  if (g_lds_raised.count({dev, kern})) return true;
+  if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsCeiling) != hipSuccess) return false;
+  g_lds_raised.insert({dev, kern});
+  return true;
 }
 
 inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
@@ -378,8 +399,7 @@ int launch_features_t_nb(const KBasis& kb, int64_t batch, int64_t n_in, int64_t 
   const size_t knots = kb.kind == KF_KIND_BSPLINE ? (size_t)32 * (2 * kb.n_knots + 2 * kb.spline_k) * 4 : 0;
   const size_t lds = (size_t)kb.n_t * 32 * 80 + knots;
   auto kern = features_t_kernel<T, NTB>;
-  if (lds > 65536 &&
-      hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+  if (!reserve_lds((const void*)kern, lds))
     return fail(KF_ELAUNCH, "features: cannot reserve %zu bytes of LDS", lds);
   dim3 grid((unsigned)(INP / 32), (unsigned)((BP + BT - 1) / BT));
   hipLaunchKernelGGL(kern, grid, dim3(kThreads), lds, s, kb, (int)batch, (int)n_in, (int)BP, (int)INP, (const T*)x,
@@ -426,7 +446,7 @@ int launch_f_t(const WsF& L, int64_t batch, int64_t n_out, int n_t, const float*
   const int rs = 32 * (int)sizeof(T) + 16;
   const size_t lds = (size_t)2 * FPS * (BM + BN) * rs;
   auto kern = f_kernel<T, BM, BN, WMW, WNW, FPS, CHEB, HAS_W>;
-  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+  if (!reserve_lds((const void*)kern, lds))
     return fail(KF_ELAUNCH, "F: cannot reserve %zu bytes of LDS", lds);
   hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(WMW * WNW * 64), lds, s, (int)batch, (int)n_out, (int)L.INP,
                      (int)L.OUTP, n_t, L.n_tp, z, wz, (const T*)cfm, (const T*)phi, (T*)y);
@@ -448,7 +468,7 @@ int launch_f_rega(const WsF& L, int64_t batch, int64_t n_out, const float* zc, c
   auto kern = L.n_tp == 9   ? f_rega_kernel<HAS_W, 9, RA_TM, TNW, RA_NBUF, SKIP0, RA_WN, RA_NWM>
               : L.n_tp == 8 ? f_rega_kernel<HAS_W, 8, RA_TM, TNW, RA_NBUF, SKIP0, RA_WN, RA_NWM>
                             : f_rega_kernel<HAS_W, 0, RA_TM, TNW, RA_NBUF, SKIP0, RA_WN, RA_NWM>;
-  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+  if (!reserve_lds((const void*)kern, lds))
     return fail(KF_ELAUNCH, "F: cannot reserve %zu bytes of LDS", lds);
   hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(64 * RA_NWM * RA_WN), lds, s, (int)batch, (int)n_out, (int)L.OUTP, (int)L.BP,
                      (int)(L.INP / 16), L.n_tp, zc, wc, (const bf16*)cfm, ysum, (bf16*)y, vout);
@@ -489,7 +509,7 @@ int run_F_dma(const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out, cons
   }
   const size_t lds = (size_t)2 * (BM + TI) * 128;
   auto kern = p_dma_kernel<T, TM, FW, KF_KIND_BSPLINE, 2>;
-  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+  if (!reserve_lds((const void*)kern, lds))
     return fail(KF_ELAUNCH, "F: cannot reserve %zu bytes of LDS", lds);
   const int n_m = (int)((batch + BM - 1) / BM), n_n = (int)((n_out + TI - 1) / TI);
   hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(256), lds, s, kb, (int)batch, (int)n_out, n_n * TI, (int)ld,
@@ -574,7 +594,7 @@ int launch_p_kind(const WsP& L, hipStream_t s, const KBasis& kb, int64_t batch, 
   const size_t lds_ops = (size_t)2 * (BM + NMAX) * RS, lds_red = (size_t)WJW * BM * 33 * 4;
   const size_t lds = lds_ops > lds_red ? lds_ops : lds_red;
   auto kern = p_kernel<T, WMW, WJW, TM, FW, KIND>;
-  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+  if (!reserve_lds((const void*)kern, lds))
     return fail(KF_ELAUNCH, "P: cannot reserve %zu bytes of LDS", lds);
   const int n_m = (int)((batch + BM - 1) / BM), n_n = (int)(L.INP / 32);
   hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(WMW * WJW * 64), lds, s, kb, (int)batch, (int)n_in, (int)n_out,
@@ -608,7 +628,7 @@ int launch_p_dma_kind(const WsP& L, hipStream_t s, const KBasis& kb, int64_t bat
   const size_t lds_ops = (size_t)2 * (BM + 2 * FW * 32) * 128;
   const size_t lds = lds_ops > lds_epi ? lds_ops : lds_epi;
   auto kern = p_dma_kernel<T, TM, FW, KIND>;
-  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+  if (!reserve_lds((const void*)kern, lds))
     return fail(KF_ELAUNCH, "P: cannot reserve %zu bytes of LDS", lds);
   constexpr int TI = KIND == KF_KIND_RATIONAL ? 64 * FW : 32;  // inputs per tile (flat for rational)
   if (L.INP % TI) return fail(KF_EINVAL, "P: workspace layout not aligned");
@@ -626,7 +646,7 @@ int launch_p8(const WsP& L, hipStream_t s, const KBasis& kb, int64_t batch, int6
   const size_t lds = lds_ops > lds_epi ? lds_ops : lds_epi;
   auto kern = p8_kernel<KF_KIND_CHEB, TN, RB>;
   if (L.INP % TI || L.OUTP % (RB / 2)) return fail(KF_EINVAL, "P: workspace layout not aligned");
-  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+  if (!reserve_lds((const void*)kern, lds))
     return fail(KF_ELAUNCH, "P: cannot reserve %zu bytes of LDS", lds);
   const int n_m = (int)((batch + 255) / 256), n_n = (int)(L.INP / TI);
   hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(512), lds, s, kb, (int)batch, (int)n_in, (int)L.INP, (int)L.OUTP,
@@ -696,7 +716,7 @@ int launch_g_t(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, int
   const size_t lds_red = (size_t)(FLAT ? NMAX / 32 : kb.n_t) * (BM / 2) * 33 * 4;
   const size_t lds = lds_ops > lds_red ? lds_ops : lds_red;
   auto kern = g_kernel<T, WMW, WJW, TM, FW, RB, CHEB, FLAT>;
-  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+  if (!reserve_lds((const void*)kern, lds))
     return fail(KF_ELAUNCH, "G: cannot reserve %zu bytes of LDS", lds);
   constexpr int TI = FLAT ? NMAX : 32;
   if (FLAT && L.INP % TI) return fail(KF_EINVAL, "G: workspace layout not aligned");
@@ -748,7 +768,7 @@ int launch_g_ws(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, in
   const size_t lds_ops = (size_t)2 * (BM + NMAX) * RS, lds_red = (size_t)kb.n_t * (BM / 2) * 33 * 4;
   const size_t lds = lds_ops > lds_red ? lds_ops : lds_red;
   auto kern = L.skip0 ? g_ws_kernel<T, TM, FW, RB, true> : g_ws_kernel<T, TM, FW, RB, false>;
-  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+  if (!reserve_lds((const void*)kern, lds))
     return fail(KF_ELAUNCH, "G: cannot reserve %zu bytes of LDS", lds);
   const int n_m = (int)(L.OUTP / BM), n_n = (int)((n_in + 31) / 32);
   hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(512), lds, s, kb, (int)batch, (int)n_in, (int)n_out, (int)L.BP,
@@ -764,7 +784,7 @@ int launch_g96(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, int
   const int vout = (n_in * kb.K * 2) % 16 == 0 && aligned16(dc);
   const size_t lds = lds_ops > lds_red ? lds_ops : lds_red;
   auto kern = g96_kernel<SKIP0>;
-  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+  if (!reserve_lds((const void*)kern, lds))
     return fail(KF_ELAUNCH, "G: cannot reserve %zu bytes of LDS", lds);
   const int n_m = (int)(L.OUTP / 192), n_n = (int)(L.INP / 48);
   const int skip = SKIP0 ? 1 : 0, n_run = kb.n_t - skip;
@@ -786,7 +806,7 @@ int launch_g_dma(const WsG& L, hipStream_t s, const KBasis& kb, int64_t n_in, in
   const size_t lds = (size_t)2 * (BM + 2 * FW * 32) * 128;
   auto kern = p_dma_kernel<T, TM, FW, KF_KIND_BSPLINE, 1>;
   if (L.INP % kGdmaRows || L.BP % EPS || L.BP / EPS < 1) return fail(KF_EINVAL, "G: workspace layout not aligned");
-  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+  if (!reserve_lds((const void*)kern, lds))
     return fail(KF_ELAUNCH, "G: cannot reserve %zu bytes of LDS", lds);
   const int n_m = (int)((n_out + BM - 1) / BM), n_n = (int)(kb.n_t * L.INP / kGdmaRows);
   hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(256), lds, s, kb, (int)n_out, (int)n_in, (int)L.INP, (int)L.BP,

@@ -18,6 +18,8 @@ Differences from the reference, by design:
 from __future__ import annotations
 
 import ctypes
+from functools import lru_cache
+from typing import Optional
 
 import numpy as np
 import torch
@@ -202,98 +204,238 @@ def _rational_param_grad(plan, st: BasisState, x, h, w):
     return dnum, dden
 
 
-# --- differentiable primitives ------------------------------------------------------
+# --- custom ops ---------------------------------------------------------------------
+#
+# Every launch is a torch custom op in the ``kf`` namespace with its autograd formula registered
+# (the F/G/P closure of kanforge/torch/kernels.py:70-128) and a fake kernel for shape inference,
+# so the layers trace under torch.compile. A plan crosses the op boundary as an exact string key;
+# basis tables (B-spline knots, rational parameters) as optional tensors.
+
+
+_PLAN_KEYS: dict = {}
+
+
+def plan_key(plan: KernelPlan | str) -> str:
+    """Exact text form of a plan (floats in hexadecimal); a key passes through unchanged."""
+    if isinstance(plan, str):
+        return plan
+    key = _PLAN_KEYS.get(plan)
+    if key is None:
+        consts = ",".join(str(v) for v in plan.consts)
+        fold = ",".join(float(v).hex() for v in plan.fold_key)
+        key = _PLAN_KEYS[plan] = f"{plan.kind};{consts};{plan.size};{int(plan.grid)};{fold}"
+    return key
+
+
+@lru_cache(maxsize=None)
+def plan_of(key: str) -> KernelPlan:
+    kind, consts, size, grid, fold = key.split(";")
+    parts = consts.split(",")
+    if kind == "cheb":
+        cst = (int(parts[0]), parts[1])
+    else:
+        cst = (int(parts[0]), int(parts[1]))
+    fk = tuple(float.fromhex(v) for v in fold.split(",")) if fold else ()
+    return KernelPlan(kind, cst, int(size), fk, bool(int(grid)))
+
+
+def _state(knots, knots_cmp, num, den, n_in: int) -> BasisState | None:
+    if knots is not None:
+        return BasisState(knots=knots, knots_cmp=knots_cmp)
+    if num is not None:
+        return rational_state(num, den, n_in // num.shape[0])
+    return None
+
+
+def _tables(st: BasisState | None):
+    """(knots, knots_cmp) of a state, for the op arguments."""
+    if st is None or st.knots is None:
+        return None, None
+    return st.knots, st.knots_cmp
+
+
+Opt = Optional[torch.Tensor]
 
 
 def _mul(w, t):
     return t if w is None else w * t
 
 
-class _F(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, x, c, w, num, den, st, plan, m):
-        ctx.save_for_backward(x, c, w, num, den)
-        ctx.st, ctx.plan, ctx.m = st, plan, m
-        return _raw("F", plan, m, x, w, c, st, c.shape[0])
-
-    @staticmethod
-    def backward(ctx, gy):
-        x, c, w, num, den = ctx.saved_tensors
-        st, plan, m = ctx.st, ctx.plan, ctx.m
-        need = ctx.needs_input_grad
-        gx = gc = gw = gnum = gden = None
-        gy = gy.contiguous()
-        need_theta = plan.kind == "rational" and (need[3] or need[4])
-        if need_theta:
-            if m != 0 or torch.is_grad_enabled():
-                raise NotImplementedError("rational parameter gradients are first order only on the HIP path")
-            h = torch.empty(x.shape, dtype=torch.float32, device=x.device)
-            p1 = _raw("P", plan, m + 1, x, gy, c, st, c.shape[0], h=h)
-            if need[0]:
-                gx = _mul(w, p1)
-            dnum, dden = _rational_param_grad(plan, st, x, h, w)
-            gnum = dnum.to(num.dtype) if need[3] else None
-            gden = dden.to(den.dtype) if need[4] else None
-        elif need[0]:
-            gx = _mul(w, prim_P(x, gy, c, st, plan, m + 1))
-        if need[1]:
-            gc = prim_G(x, gy, w, st, plan, m)
-        if need[2]:
-            gw = prim_P(x, gy, c, st, plan, m)
-        return gx, gc, gw, gnum, gden, None, None, None
+@torch.library.custom_op("kf::F", mutates_args=())
+def op_F(x: torch.Tensor, w: Opt, c: torch.Tensor, knots: Opt, knots_cmp: Opt, num: Opt, den: Opt, plan: str, m: int) -> torch.Tensor:
+    """y[b,o] = sum_{i,k} w[b,i] c[o,i,k] phi_k^(m)(x[b,i])."""
+    return _raw("F", plan_of(plan), m, x, w, c, _state(knots, knots_cmp, num, den, x.shape[1]), c.shape[0])
 
 
-class _G(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, x, g, w, st, plan, m):
-        ctx.save_for_backward(x, g, w)
-        ctx.st, ctx.plan, ctx.m = st, plan, m
-        return _raw("G", plan, m, x, w, g, st, g.shape[1])
-
-    @staticmethod
-    def backward(ctx, gg_out):
-        x, g, w = ctx.saved_tensors
-        st, plan, m = ctx.st, ctx.plan, ctx.m
-        need = ctx.needs_input_grad
-        gg_out = gg_out.contiguous()
-        gx = _mul(w, prim_P(x, g, gg_out, st, plan, m + 1)) if need[0] else None
-        gg = prim_F(x, gg_out, w, st, plan, m) if need[1] else None
-        gw = prim_P(x, g, gg_out, st, plan, m) if need[2] else None
-        return gx, gg, gw, None, None, None
+@torch.library.custom_op("kf::G", mutates_args=())
+def op_G(x: torch.Tensor, g: torch.Tensor, w: Opt, knots: Opt, knots_cmp: Opt, num: Opt, den: Opt, plan: str, m: int) -> torch.Tensor:
+    """dc[o,i,k] = sum_b w[b,i] g[b,o] phi_k^(m)(x[b,i])."""
+    return _raw("G", plan_of(plan), m, x, w, g, _state(knots, knots_cmp, num, den, x.shape[1]), g.shape[1])
 
 
-class _P(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, x, g, c, st, plan, m):
-        ctx.save_for_backward(x, g, c)
-        ctx.st, ctx.plan, ctx.m = st, plan, m
-        return _raw("P", plan, m, x, g, c, st, c.shape[0])
+@torch.library.custom_op("kf::P", mutates_args=())
+def op_P(x: torch.Tensor, g: torch.Tensor, c: torch.Tensor, knots: Opt, knots_cmp: Opt, num: Opt, den: Opt, plan: str, m: int) -> torch.Tensor:
+    """p[b,i] = sum_{o,k} g[b,o] c[o,i,k] phi_k^(m)(x[b,i])."""
+    return _raw("P", plan_of(plan), m, x, g, c, _state(knots, knots_cmp, num, den, x.shape[1]), c.shape[0])
 
-    @staticmethod
-    def backward(ctx, gp):
-        x, g, c = ctx.saved_tensors
-        st, plan, m = ctx.st, ctx.plan, ctx.m
-        need = ctx.needs_input_grad
-        gp = gp.contiguous()
-        gx = gp * prim_P(x, g, c, st, plan, m + 1) if need[0] else None
-        gg = prim_F(x, c, gp, st, plan, m) if need[1] else None
-        gc = prim_G(x, g, gp, st, plan, m) if need[2] else None
-        return gx, gg, gc, None, None, None
+
+@torch.library.custom_op("kf::rational_bwd", mutates_args=())
+def op_rational_bwd(
+    x: torch.Tensor, g: torch.Tensor, c: torch.Tensor, w: Opt, num: torch.Tensor, den: torch.Tensor, plan: str
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(P_1(x, g, c), d/dnum, d/dden) of sum_{b,o} g[b,o] F_0(x, c, w)[b,o] for a rational plan:
+    one P launch that also writes h = sum_o g c, then the parameter-gradient reduction."""
+    pl = plan_of(plan)
+    st = _state(None, None, num, den, x.shape[1])
+    h = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+    p1 = _raw("P", pl, 1, x, g, c, st, c.shape[0], h=h)
+    dnum, dden = _rational_param_grad(pl, st, x, h, w)
+    return p1, dnum.to(num.dtype), dden.to(den.dtype)
+
+
+@torch.library.custom_op("kf::rational_param_grad", mutates_args=())
+def op_rational_param_grad(x: torch.Tensor, h: torch.Tensor, w: Opt, num: torch.Tensor, den: torch.Tensor, plan: str) -> tuple[torch.Tensor, torch.Tensor]:
+    """(d/dnum, d/dden) of sum_{b,i} h[b,i] w[b,i] phi(x[b,i]) for a rational plan."""
+    st = _state(None, None, num, den, x.shape[1])
+    dnum, dden = _rational_param_grad(plan_of(plan), st, x, h.float().contiguous(), w)
+    return dnum.to(num.dtype), dden.to(den.dtype)
+
+
+@op_F.register_fake
+def _(x, w, c, knots, knots_cmp, num, den, plan, m):
+    return x.new_empty(x.shape[0], c.shape[0])
+
+
+@op_G.register_fake
+def _(x, g, w, knots, knots_cmp, num, den, plan, m):
+    return x.new_empty(g.shape[1], x.shape[1], plan_of(plan).size)
+
+
+@op_P.register_fake
+def _(x, g, c, knots, knots_cmp, num, den, plan, m):
+    return x.new_empty(x.shape)
+
+
+@op_rational_bwd.register_fake
+def _(x, g, c, w, num, den, plan):
+    return x.new_empty(x.shape), torch.empty_like(num), torch.empty_like(den)
+
+
+@op_rational_param_grad.register_fake
+def _(x, h, w, num, den, plan):
+    return torch.empty_like(num), torch.empty_like(den)
+
+
+def _save(ctx, tensors, plan, m):
+    ctx.save_for_backward(*tensors)
+    ctx.plan, ctx.m = plan, m
+
+
+def _F_setup(ctx, inputs, output):
+    x, w, c, knots, knots_cmp, num, den, plan, m = inputs
+    _save(ctx, (x, w, c, knots, knots_cmp, num, den), plan, m)
+
+
+def _F_backward(ctx, gy):
+    x, w, c, knots, knots_cmp, num, den = ctx.saved_tensors
+    plan, m = ctx.plan, ctx.m
+    need = ctx.needs_input_grad
+    gx = gw = gc = gnum = gden = None
+    gy = gy.contiguous()
+    tabs = (knots, knots_cmp, num, den)
+    if plan_of(plan).kind == "rational" and (need[5] or need[6]):
+        if m != 0:
+            raise NotImplementedError("rational parameter gradients of derivative features are not compiled into the HIP kernels")
+        p1, gnum, gden = op_rational_bwd(x, gy, c, w, num, den, plan)
+        if need[0]:
+            # under create_graph the x-gradient stays differentiable through kf::P
+            gx = _mul(w, op_P(x, gy, c, *tabs, plan, 1) if torch.is_grad_enabled() else p1)
+    elif need[0]:
+        gx = _mul(w, op_P(x, gy, c, *tabs, plan, m + 1))
+    if need[2]:
+        gc = op_G(x, gy, w, *tabs, plan, m)
+    if need[1]:
+        gw = op_P(x, gy, c, *tabs, plan, m)
+    return gx, gw, gc, None, None, gnum, gden, None, None
+
+
+def _G_setup(ctx, inputs, output):
+    x, g, w, knots, knots_cmp, num, den, plan, m = inputs
+    _save(ctx, (x, g, w, knots, knots_cmp, num, den), plan, m)
+
+
+def _G_backward(ctx, gdc):
+    x, g, w, knots, knots_cmp, num, den = ctx.saved_tensors
+    plan, m = ctx.plan, ctx.m
+    need = ctx.needs_input_grad
+    if need[5] or need[6]:
+        raise NotImplementedError("second-order rational parameter gradients are not compiled into the HIP kernels")
+    gdc = gdc.contiguous()
+    tabs = (knots, knots_cmp, num, den)
+    gx = _mul(w, op_P(x, g, gdc, *tabs, plan, m + 1)) if need[0] else None
+    gg = op_F(x, w, gdc, *tabs, plan, m) if need[1] else None
+    gw = op_P(x, g, gdc, *tabs, plan, m) if need[2] else None
+    return gx, gg, gw, None, None, None, None, None, None
+
+
+def _P_setup(ctx, inputs, output):
+    x, g, c, knots, knots_cmp, num, den, plan, m = inputs
+    _save(ctx, (x, g, c, knots, knots_cmp, num, den), plan, m)
+
+
+def _P_backward(ctx, gp):
+    x, g, c, knots, knots_cmp, num, den = ctx.saved_tensors
+    plan, m = ctx.plan, ctx.m
+    need = ctx.needs_input_grad
+    if need[5] or need[6]:
+        raise NotImplementedError("second-order rational parameter gradients are not compiled into the HIP kernels")
+    gp = gp.contiguous()
+    tabs = (knots, knots_cmp, num, den)
+    gx = gp * op_P(x, g, c, *tabs, plan, m + 1) if need[0] else None
+    gg = op_F(x, gp, c, *tabs, plan, m) if need[1] else None
+    gc = op_G(x, g, gp, *tabs, plan, m) if need[2] else None
+    return gx, gg, gc, None, None, None, None, None, None
+
+
+def _no_second_order(ctx, *grads):
+    raise NotImplementedError("second-order rational parameter gradients are not compiled into the HIP kernels")
+
+
+def _no_ctx(ctx, inputs, output):
+    pass
+
+
+op_F.register_autograd(_F_backward, setup_context=_F_setup)
+op_G.register_autograd(_G_backward, setup_context=_G_setup)
+op_P.register_autograd(_P_backward, setup_context=_P_setup)
+op_rational_bwd.register_autograd(_no_second_order, setup_context=_no_ctx)
+op_rational_param_grad.register_autograd(_no_second_order, setup_context=_no_ctx)
+
+
+def _rat(st: BasisState | None, num, den):
+    """The rational parameter tensors an op receives: the caller's (so gradients reach them) or
+    the state's float32 copies."""
+    if st is None or st.num is None:
+        return None, None
+    return (st.num if num is None else num), (st.den if den is None else den)
 
 
 def prim_F(x, c, w, st, plan, m=0, num=None, den=None):
-    return _F.apply(x, c, w, num, den, st, plan, m)
+    num, den = _rat(st, num, den)
+    return op_F(x, w, c, *_tables(st), num, den, plan_key(plan), m)
 
 
-def prim_G(x, g, w, st, plan, m=0):
-    return _G.apply(x, g, w, st, plan, m)
+def prim_G(x, g, w, st, plan, m=0, num=None, den=None):
+    num, den = _rat(st, num, den)
+    return op_G(x, g, w, *_tables(st), num, den, plan_key(plan), m)
 
 
-def prim_P(x, g, c, st, plan, m=0):
-    return _P.apply(x, g, c, st, plan, m)
+def prim_P(x, g, c, st, plan, m=0, num=None, den=None):
+    num, den = _rat(st, num, den)
+    return op_P(x, g, c, *_tables(st), num, den, plan_key(plan), m)
 
 
-def spline_forward(x: torch.Tensor, coef: torch.Tensor, st: BasisState | None, plan: KernelPlan, num=None, den=None) -> torch.Tensor:
+def spline_forward(x: torch.Tensor, coef: torch.Tensor, st: BasisState | None, plan: KernelPlan | str, num=None, den=None) -> torch.Tensor:
     """sum_{i,k} coef[o,i,k] phi_k(x[..., i]) through the HIP F kernel.
 
     Computes in the coefficients' dtype (float32 or bfloat16) and returns
@@ -322,39 +464,43 @@ def _features_raw(plan, m, st, x2: torch.Tensor) -> torch.Tensor:
     return out
 
 
-class _Features(torch.autograd.Function):
-    """phi^(m)(x) (B, in, K); d/dx is phi^(m+1). Rational plans also return the gradients of
-    their parameters ``num``/``den`` (order 0)."""
-
-    @staticmethod
-    def forward(ctx, x2, num, den, st, plan, m):
-        ctx.save_for_backward(x2, num, den)
-        ctx.st, ctx.plan, ctx.m = st, plan, m
-        return _features_raw(plan, m, st, x2.contiguous())
-
-    @staticmethod
-    def backward(ctx, gphi):
-        x2, num, den = ctx.saved_tensors
-        st, plan, m = ctx.st, ctx.plan, ctx.m
-        need = ctx.needs_input_grad
-        gx = gnum = gden = None
-        if need[0]:
-            d = _Features.apply(x2, num, den, st, plan, m + 1)
-            gx = (gphi * d).sum(-1)
-        if need[1] or need[2]:
-            gnum, gden = _rational_grads_of(plan, st, x2, gphi[..., 0], m, num, den, need[1], need[2])
-        return gx, gnum, gden, None, None, None
+@torch.library.custom_op("kf::features", mutates_args=())
+def op_features(x: torch.Tensor, knots: Opt, knots_cmp: Opt, num: Opt, den: Opt, plan: str, m: int) -> torch.Tensor:
+    """phi_k^(m)(x[b,i]), (B, in, K)."""
+    return _features_raw(plan_of(plan), m, _state(knots, knots_cmp, num, den, x.shape[1]), x.contiguous())
 
 
-def _rational_grads_of(plan, st, x2, h, m, num, den, want_num, want_den):
+@op_features.register_fake
+def _(x, knots, knots_cmp, num, den, plan, m):
+    return x.new_empty(x.shape[0], x.shape[1], plan_of(plan).size)
+
+
+def _features_setup(ctx, inputs, output):
+    x, knots, knots_cmp, num, den, plan, m = inputs
+    _save(ctx, (x, knots, knots_cmp, num, den), plan, m)
+
+
+def _features_backward(ctx, gphi):
+    x, knots, knots_cmp, num, den = ctx.saved_tensors
+    plan, m = ctx.plan, ctx.m
+    need = ctx.needs_input_grad
+    gx = gnum = gden = None
+    if need[0]:
+        gx = (gphi * op_features(x, knots, knots_cmp, num, den, plan, m + 1)).sum(-1)
+    if need[3] or need[4]:
+        gnum, gden = _rational_grads_of(plan, x, gphi[..., 0], m, num, den)
+    return gx, None, None, gnum, gden, None, None
+
+
+op_features.register_autograd(_features_backward, setup_context=_features_setup)
+
+
+def _rational_grads_of(plan, x2, h, m, num, den):
     """d/d(num, den) of sum_{b,i} h[b,i] phi^(m)(x[b,i]) for a rational plan (order 0 only)."""
-    if plan.kind != "rational":
-        return None, None
-    if m != 0 or torch.is_grad_enabled():
-        raise NotImplementedError("rational parameter gradients of derivative features (order >= 1) or of second "
-                                  "order are not compiled into the HIP kernels")
-    dnum, dden = _rational_param_grad(plan, st, x2, h.float().contiguous(), None)
-    return (dnum.to(num.dtype) if want_num else None), (dden.to(den.dtype) if want_den else None)
+    if m != 0:
+        raise NotImplementedError("rational parameter gradients of derivative features (order >= 1) are not "
+                                  "compiled into the HIP kernels")
+    return op_rational_param_grad(x2, h.float().contiguous(), None, num, den, plan)
 
 
 def basis_derivative(basis, x: torch.Tensor, m: int, params: dict | None) -> torch.Tensor:
@@ -373,12 +519,14 @@ def basis_derivative(basis, x: torch.Tensor, m: int, params: dict | None) -> tor
     if x2.dtype not in _DTYPES:
         x2 = x2.float()
     num = den = None
-    if plan.kind == "rational" and params is not None and isinstance(params.get("numerator"), torch.Tensor):
-        # the (rows, p+1) / (rows, q) views the state was built from, so gradients reach the caller's tensors
-        num, den = params["numerator"], params["denominator"]
-        if num.dim() == 1:
-            num, den = num[None], den[None]
-    out = _Features.apply(x2, num, den, st, plan, m)
+    if plan.kind == "rational":
+        num, den = st.num, st.den
+        if params is not None and isinstance(params.get("numerator"), torch.Tensor):
+            # the (rows, p+1) / (rows, q) views the state was built from, so gradients reach the caller's tensors
+            num, den = params["numerator"], params["denominator"]
+            if num.dim() == 1:
+                num, den = num[None], den[None]
+    out = op_features(x2, *_tables(st), num, den, plan_key(plan), m)
     return out.to(x.dtype).reshape(*lead, x.shape[-1], plan.size)
 
 
@@ -424,35 +572,44 @@ def _edge_raw(plan, m, st, x2, c, base_w):
     return out
 
 
-class _Edge(torch.autograd.Function):
-    """d[b,o,i] = sum_k c[o,i,k] phi_k^(m)(x[b,i]) + W[o,i] silu^(m)(x[b,i])."""
+@torch.library.custom_op("kf::edge_derivative", mutates_args=())
+def op_edge(x: torch.Tensor, c: torch.Tensor, base_w: Opt, knots: Opt, knots_cmp: Opt, num: Opt, den: Opt, plan: str, m: int) -> torch.Tensor:
+    """d[b,o,i] = sum_k c[o,i,k] phi_k^(m)(x[b,i]) + base_w[o,i] silu^(m)(x[b,i]), (B, out, in)."""
+    return _edge_raw(plan_of(plan), m, _state(knots, knots_cmp, num, den, x.shape[1]), x.contiguous(), c, base_w)
 
-    @staticmethod
-    def forward(ctx, x2, c, base_w, num, den, st, plan, m):
-        ctx.save_for_backward(x2, c, base_w, num, den)
-        ctx.st, ctx.plan, ctx.m = st, plan, m
-        return _edge_raw(plan, m, st, x2.contiguous(), c, base_w)
 
-    @staticmethod
-    def backward(ctx, gd):
-        x2, c, base_w, num, den = ctx.saved_tensors
-        st, plan, m = ctx.st, ctx.plan, ctx.m
-        need = ctx.needs_input_grad
-        gx = gc = gw = gnum = gden = None
-        if need[0]:
-            # d/dx of the edge is the edge derivative of order m+1
-            gx = (gd * _Edge.apply(x2, c, base_w, num, den, st, plan, m + 1)).sum(1)
-        if need[1]:
-            phi = _Features.apply(x2, None, None, st, plan, m)  # (B, in, K)
-            gc = torch.einsum("boi,bik->oik", gd, phi)
-        if need[2] and base_w is not None:
-            s = silu_derivative_t(x2, m)
-            gw = torch.einsum("boi,bi->oi", gd, s)
-        if need[3] or need[4]:
-            # one feature per edge: sum_o gd[b,o,i] c[o,i,0] multiplies phi^(m)(x[b,i])
-            h = torch.einsum("boi,oi->bi", gd.float(), c[..., 0].float())
-            gnum, gden = _rational_grads_of(plan, st, x2, h, m, num, den, need[3], need[4])
-        return gx, gc, gw, gnum, gden, None, None, None
+@op_edge.register_fake
+def _(x, c, base_w, knots, knots_cmp, num, den, plan, m):
+    return x.new_empty(x.shape[0], c.shape[0], x.shape[1])
+
+
+def _edge_setup(ctx, inputs, output):
+    x, c, base_w, knots, knots_cmp, num, den, plan, m = inputs
+    _save(ctx, (x, c, base_w, knots, knots_cmp, num, den), plan, m)
+
+
+def _edge_backward(ctx, gd):
+    x, c, base_w, knots, knots_cmp, num, den = ctx.saved_tensors
+    plan, m = ctx.plan, ctx.m
+    need = ctx.needs_input_grad
+    gx = gc = gw = gnum = gden = None
+    tabs = (knots, knots_cmp, num, den)
+    if need[0]:
+        # d/dx of the edge is the edge derivative of order m+1
+        gx = (gd * op_edge(x, c, base_w, *tabs, plan, m + 1)).sum(1)
+    if need[1]:
+        phi = op_features(x, knots, knots_cmp, num, den, plan, m)  # (B, in, K)
+        gc = torch.einsum("boi,bik->oik", gd, phi)
+    if need[2] and base_w is not None:
+        gw = torch.einsum("boi,bi->oi", gd, silu_derivative_t(x, m))
+    if need[5] or need[6]:
+        # one feature per edge: sum_o gd[b,o,i] c[o,i,0] multiplies phi^(m)(x[b,i])
+        h = torch.einsum("boi,oi->bi", gd.float(), c[..., 0].float())
+        gnum, gden = _rational_grads_of(plan, x, h, m, num, den)
+    return gx, gc, gw, None, None, gnum, gden, None, None
+
+
+op_edge.register_autograd(_edge_backward, setup_context=_edge_setup)
 
 
 def silu_derivative_t(x: torch.Tensor, m: int) -> torch.Tensor:
@@ -482,11 +639,13 @@ def edge_derivative(x: torch.Tensor, coef_eff: torch.Tensor, base_w: torch.Tenso
     x2 = x.reshape(-1, x.shape[-1])
     if x2.dtype != coef_eff.dtype:
         x2 = x2.to(coef_eff.dtype)
-    d = _Edge.apply(x2, coef_eff, base_w, num, den, st, plan, m)
+    num, den = _rat(st, num, den)
+    d = op_edge(x2, coef_eff, base_w, *_tables(st), num, den, plan_key(plan), m)
     return d.to(x.dtype).reshape(*lead, coef_eff.shape[0], x.shape[-1])
 
 
-def bspline_interval(x: torch.Tensor, knots_cmp: torch.Tensor) -> torch.Tensor:
+@torch.library.custom_op("kf::bspline_interval", mutates_args=())
+def op_bspline_interval(x: torch.Tensor, knots_cmp: torch.Tensor) -> torch.Tensor:
     """int32 interval index of float32 x (B, in) on the comparison knots (in, nk); -1 outside."""
     _require_device(x)
     lib = _lib.load()
@@ -497,3 +656,13 @@ def bspline_interval(x: torch.Tensor, knots_cmp: torch.Tensor) -> torch.Tensor:
         rc = lib.kf_bspline_interval(x.shape[0], x.shape[1], _ptr(x), _ptr(kc), kc.shape[1], _ptr(out), _stream(x.device))
     _lib.check(rc, "kf_bspline_interval")
     return out
+
+
+@op_bspline_interval.register_fake
+def _(x, knots_cmp):
+    return torch.empty(x.shape, dtype=torch.int32, device=x.device)
+
+
+def bspline_interval(x: torch.Tensor, knots_cmp: torch.Tensor) -> torch.Tensor:
+    """int32 interval index of float32 x (B, in) on the comparison knots (in, nk); -1 outside."""
+    return op_bspline_interval(x, knots_cmp)

@@ -28,6 +28,10 @@ from . import kernels as _kernels
 BACKENDS = ("auto", "ops", "kernel")
 
 
+def _compiling() -> bool:
+    return torch.compiler.is_compiling()
+
+
 class KANLinear(nn.Module):
     """One KAN layer: y_o = sum_i s_oi * phi_oi(x_i) + sum_i w_oi * act(x_i) + b_o.
 
@@ -124,6 +128,7 @@ class KANLinear(nn.Module):
             self.register_buffer(f"basis_{name}", torch.as_tensor(np.ascontiguousarray(value), **like))
         self._trainable_names, self._buffer_names = list(trainable), list(buffers)
         self._plan = plan_for(self.basis)
+        self._plan_key = None if self._plan is None else _kernels.plan_key(self._plan)
         self._state_cache = None
 
     def reset_parameters(self) -> None:
@@ -165,7 +170,8 @@ class KANLinear(nn.Module):
         return self._mask_cache[1]
 
     def effective_coef(self) -> torch.Tensor:
-        if self.edge_scale is None and self._mask_is_ones():
+        # under torch.compile the mask is applied without looking at its values
+        if self.edge_scale is None and not _compiling() and self._mask_is_ones():
             return self.coef
         scale = self.edge_mask if self.edge_scale is None else self.edge_scale * self.edge_mask
         return self.coef * scale[..., None]
@@ -173,7 +179,9 @@ class KANLinear(nn.Module):
     def effective_base_weight(self) -> torch.Tensor | None:
         if self.base_weight is None:
             return None
-        return self.base_weight if self._mask_is_ones() else self.base_weight * self.edge_mask
+        if not _compiling() and self._mask_is_ones():
+            return self.base_weight
+        return self.base_weight * self.edge_mask
 
     # --- computation ------------------------------------------------------------
 
@@ -183,6 +191,12 @@ class KANLinear(nn.Module):
         if plan.kind == "cheb":
             return None
         if plan.kind == "bspline":
+            if _compiling():
+                # traced graphs use the tables of the last eager call (built again there when the
+                # grid changed); a layer that never ran eagerly builds them now, outside the graph
+                if self._state_cache is None:
+                    self._state_cache = (None, _kernels.bspline_state(self.basis_grid, self.basis.order))
+                return self._state_cache[1]
             grid = self.basis_grid
             key = (grid.data_ptr(), grid._version, grid.device, grid.dtype)
             if self._state_cache is None or self._state_cache[0] != key:
@@ -197,12 +211,13 @@ class KANLinear(nn.Module):
             keep = torch.rand_like(edges) >= self.edge_dropout
             y = (edges * keep).sum(-1) / (1 - self.edge_dropout)
             return y if self.bias is None else y + self.bias
-        self.uses_kernel(x.device)  # raises when the HIP path cannot run
+        if not _compiling():
+            self.uses_kernel(x.device)  # raises when the HIP path cannot run
         st = self._basis_state()
         if self._plan.kind == "rational":
-            y = _kernels.spline_forward(x, self.effective_coef(), st, self._plan, self.basis_numerator, self.basis_denominator)
+            y = _kernels.spline_forward(x, self.effective_coef(), st, self._plan_key, self.basis_numerator, self.basis_denominator)
         else:
-            y = _kernels.spline_forward(x, self.effective_coef(), st, self._plan)
+            y = _kernels.spline_forward(x, self.effective_coef(), st, self._plan_key)
         if self.base_weight is not None:
             y = y + F.linear(self.base_activation(x), self.effective_base_weight())
         if self._sym_codes:

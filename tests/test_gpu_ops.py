@@ -1,0 +1,102 @@
+"""The torch custom-op boundary on the GPU: torch.library.opcheck of every kf:: op (schema,
+autograd registration, fake kernels, AOT dispatch), and torch.compile(fullgraph=True) of
+KANLinear forward + backward giving the eager results."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import kanforge_amd as kf
+from kanforge_amd.kernels import plan_for
+from kanforge_amd.torch import GRKAN, KANLinear
+from kanforge_amd.torch import kernels as K
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _operands(basis, B=37, IN=12, OUT=9, seed=0, grad=True):
+    g = torch.Generator().manual_seed(seed)
+    plan = plan_for(basis)
+    x = (torch.rand(B, IN, generator=g) * 1.6 - 0.8).to(DEV).requires_grad_(grad)
+    c = (torch.randn(OUT, IN, basis.size, generator=g) / math.sqrt(IN * basis.size)).to(DEV).requires_grad_(grad)
+    gy = torch.randn(B, OUT, generator=g).to(DEV).requires_grad_(grad)
+    w = (torch.rand(B, IN, generator=g) + 0.5).to(DEV).requires_grad_(grad)
+    kn = kc = num = den = None
+    if plan.kind == "bspline":
+        grid = torch.linspace(-1, 1, basis.grid_size + 1, dtype=torch.float64).expand(IN, -1).contiguous().to(DEV)
+        st = K.bspline_state(grid, basis.order)
+        kn, kc = st.knots, st.knots_cmp
+    if plan.kind == "rational":
+        groups = 4
+        num = (torch.tensor(basis.param_specs()["numerator"].value, dtype=torch.float32)[None].repeat(groups, 1)
+               + 0.05 * torch.randn(groups, basis.num_degree + 1, generator=g)).to(DEV).requires_grad_(grad)
+        den = (torch.tensor(basis.param_specs()["denominator"].value, dtype=torch.float32)[None].repeat(groups, 1)
+               + 0.05 * torch.randn(groups, basis.den_degree, generator=g)).to(DEV).requires_grad_(grad)
+    return K.plan_key(plan), x, c, gy, w, (kn, kc, num, den)
+
+
+BASES = {"cheb8": kf.Chebyshev(8), "jacobi6": kf.Jacobi(6, 0.5, 0.5), "bspline53": kf.BSpline(5, 3), "rational": kf.Rational(5, 4)}
+
+
+@pytest.mark.parametrize("name", list(BASES))
+def test_opcheck_F_G_P(name):
+    key, x, c, gy, w, tabs = _operands(BASES[name])
+    rational = tabs[2] is not None
+    # rational parameters receive gradients through F at order 0; P and G take them as constants
+    fixed = tabs if not rational else (tabs[0], tabs[1], tabs[2].detach(), tabs[3].detach())
+    for m in (0, 1):
+        torch.library.opcheck(torch.ops.kf.F.default, (x, w, c, *(fixed if m else tabs), key, m))
+        torch.library.opcheck(torch.ops.kf.P.default, (x, gy, c, *fixed, key, m))
+        torch.library.opcheck(torch.ops.kf.G.default, (x, gy, w, *fixed, key, m))
+
+
+@pytest.mark.parametrize("name", list(BASES))
+def test_opcheck_edge_and_features(name):
+    key, x, c, gy, w, tabs = _operands(BASES[name])
+    bw = (0.1 * torch.randn(c.shape[:2], generator=torch.Generator().manual_seed(5))).to(DEV).requires_grad_()
+    torch.library.opcheck(torch.ops.kf.edge_derivative.default, (x, c, bw, *tabs, key, 0))
+    torch.library.opcheck(torch.ops.kf.features.default, (x, *tabs, key, 0))
+    if tabs[2] is None:
+        torch.library.opcheck(torch.ops.kf.edge_derivative.default, (x, c, bw, *tabs, key, 2))
+
+
+def test_opcheck_rational_ops_and_interval():
+    key, x, c, gy, w, tabs = _operands(BASES["rational"], grad=False)
+    torch.library.opcheck(torch.ops.kf.rational_bwd.default, (x, gy, c, None, tabs[2], tabs[3], key))
+    h = torch.randn(x.shape, device=DEV)
+    torch.library.opcheck(torch.ops.kf.rational_param_grad.default, (x, h, w, tabs[2], tabs[3], key))
+    bkey, bx, _, _, _, btabs = _operands(BASES["bspline53"], grad=False)
+    torch.library.opcheck(torch.ops.kf.bspline_interval.default, (bx, btabs[1]))
+
+
+def _grads(layer, x, gy):
+    params = [p for p in layer.parameters()]
+    y = layer(x)
+    return [y] + list(torch.autograd.grad(y, [x] + params, gy))
+
+
+@pytest.mark.parametrize(
+    "make,dtype",
+    [
+        (lambda: KANLinear(96, 80, kf.Chebyshev(8), base_activation=None, bias=False), torch.bfloat16),
+        (lambda: KANLinear(64, 48, kf.BSpline(5, 3)), torch.float32),
+        (lambda: GRKAN(64, 48, groups=8), torch.float32),
+    ],
+    ids=["cheb8-bf16", "bspline53-f32-base", "grkan-f32"],
+)
+def test_compiled_layer_forward_backward_matches_eager(make, dtype):
+    torch.manual_seed(0)
+    layer = make().to(DEV, dtype)
+    x = (torch.rand(256, layer.in_features, device=DEV) * 1.6 - 0.8).to(dtype).requires_grad_()
+    gy = torch.randn(256, layer.out_features, device=DEV).to(dtype)
+    want = _grads(layer, x, gy)
+    torch._dynamo.reset()
+    compiled = torch.compile(layer, fullgraph=True)
+    y = compiled(x)
+    got = [y] + list(torch.autograd.grad(y, [x] + list(layer.parameters()), gy))
+    assert len(got) == len(want)
+    for a, b in zip(got, want):
+        torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-6)

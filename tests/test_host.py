@@ -261,3 +261,34 @@ def test_noalloc_F_rejects_shapes_beyond_its_static_scratch_before_any_launch():
     assert rc == _lib.KF_EWORKSPACE and b"static scratch" in lib.kf_last_error()
     need = lib.kf_workspace_bytes(_lib.KF_OP_F, ctypes.byref(b), _lib.KF_BF16, 8192, 768, 4096)
     assert need > _lib.KF_NOALLOC_SCRATCH_BYTES
+
+
+# --- the custom-op boundary (no GPU: plan keys and fake kernels) ---------------------------
+
+
+@pytest.mark.parametrize("basis", [kf.Chebyshev(8), kf.Jacobi(6, 0.5, 0.5), kf.Legendre(4, input_map="identity"), kf.BSpline(8, 3), kf.Rational(5, 4)])
+def test_plan_key_round_trip_is_exact(basis):
+    from kanforge_amd.torch import kernels as K
+
+    plan = plan_for(basis)
+    key = K.plan_key(plan)
+    assert K.plan_of(key) == plan and K.plan_key(key) is key
+
+
+def test_custom_op_fake_kernels_give_shapes_on_meta_tensors():
+    from kanforge_amd.torch import kernels as K
+
+    key = K.plan_key(plan_for(kf.BSpline(8, 3)))
+    x = torch.empty(33, 7, device="meta")
+    c = torch.empty(5, 7, 11, device="meta")
+    g = torch.empty(33, 5, device="meta")
+    kn, kc = torch.empty(7, 21, device="meta"), torch.empty(7, 15, device="meta")
+    assert torch.ops.kf.F(x, None, c, kn, kc, None, None, key, 0).shape == (33, 5)
+    assert torch.ops.kf.G(x, g, None, kn, kc, None, None, key, 0).shape == (5, 7, 11)
+    assert torch.ops.kf.P(x, g, c, kn, kc, None, None, key, 1).shape == (33, 7)
+    assert torch.ops.kf.features(x, kn, kc, None, None, key, 2).shape == (33, 7, 11)
+    assert torch.ops.kf.edge_derivative(x, c, None, kn, kc, None, None, key, 1).shape == (33, 5, 7)
+    rkey = K.plan_key(plan_for(kf.Rational(5, 4)))
+    num, den = torch.empty(7, 6, device="meta"), torch.empty(7, 4, device="meta")
+    p, dn, dd = torch.ops.kf.rational_bwd(x, g, torch.empty(5, 7, 1, device="meta"), None, num, den, rkey)
+    assert p.shape == (33, 7) and dn.shape == (7, 6) and dd.shape == (7, 4)
