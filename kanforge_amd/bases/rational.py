@@ -23,41 +23,67 @@ TARGETS = {
 }
 
 
+def _design(x, num_degree, den_degree):
+    """Monomial columns of P (x^0..x^p) and of Q (x^1..x^q)."""
+    return x[:, None] ** np.arange(num_degree + 1), x[:, None] ** np.arange(1, den_degree + 1)
+
+
+def _sk_start(vp, vq, y, sweeps=25):
+    """Sanathanan-Koerner iteration for P/(1+|Q|) ~ y.
+
+    With the sign pattern s = sign(Q) and the denominator D = 1 + |Q| of the previous sweep held
+    fixed, (P - y (1 + s Q)) / D is linear in the coefficients: each sweep is one weighted linear
+    least-squares solve, and its solution gives the next s and D."""
+    n_p = vp.shape[1]
+    s = np.ones_like(y)
+    d = np.ones_like(y)
+    theta = np.zeros(n_p + vq.shape[1])
+    for _ in range(sweeps):
+        rows = np.hstack([vp, -(y * s)[:, None] * vq]) / d[:, None]
+        theta = np.linalg.lstsq(rows, y / d, rcond=None)[0]
+        q = vq @ theta[n_p:]
+        s = np.where(q < 0, -1.0, 1.0)
+        d = 1.0 + np.abs(q)
+    return theta
+
+
+def _gauss_newton(vp, vq, y, theta, iters=60):
+    """Gauss-Newton on the true residual P/(1+|Q|) - y, each step shortened by halving until the
+    sum of squares decreases (stops when no shortened step does)."""
+    n_p = vp.shape[1]
+
+    def residual(th):
+        q = vq @ th[n_p:]
+        return (vp @ th[:n_p]) / (1.0 + np.abs(q)) - y, q
+
+    r, q = residual(theta)
+    for _ in range(iters):
+        d = 1.0 + np.abs(q)
+        p = vp @ theta[:n_p]
+        jac = np.hstack([vp / d[:, None], (-p * np.sign(q) / d**2)[:, None] * vq])
+        step = np.linalg.lstsq(jac, -r, rcond=None)[0]
+        t = 1.0
+        while t > 1e-6:
+            r_new, q_new = residual(theta + t * step)
+            if r_new @ r_new < r @ r:
+                theta, r, q = theta + t * step, r_new, q_new
+                break
+            t *= 0.5
+        else:
+            break
+    return theta
+
+
 @lru_cache(maxsize=None)
 def fit_rational(target: str, num_degree: int, den_degree: int, lim: float = 3.0):
-    """(a, b) of P/(1+|Q|) fitted to ``target`` on [-lim, lim].
-
-    Start: the linear least-squares solution of P - f Q = f. Then damped
-    Gauss-Newton (Levenberg-Marquardt) on the true residual P/(1+|Q|) - f.
-    """
-    f = TARGETS[target]
+    """(a, b) of P/(1+|Q|) fitted to ``target`` on [-lim, lim] in the least-squares sense:
+    a Sanathanan-Koerner start (reweighted linear solves) polished by Gauss-Newton."""
     x = np.linspace(-lim, lim, 2001)
-    y = f(x)
-    vp = x[:, None] ** np.arange(num_degree + 1)
-    vq = x[:, None] ** np.arange(1, den_degree + 1)
-    theta = np.linalg.lstsq(np.hstack([vp, -y[:, None] * vq]), y, rcond=None)[0]
-    npar = num_degree + 1
-
-    def resid(th):
-        q = vq @ th[npar:]
-        return (vp @ th[:npar]) / (1 + np.abs(q)) - y, q
-
-    r, q = resid(theta)
-    damping = 1e-3
-    for _ in range(300):
-        d = 1 + np.abs(q)
-        jac = np.hstack([vp / d[:, None], (-(vp @ theta[:npar]) * np.sign(q) / d**2)[:, None] * vq])
-        jtj = jac.T @ jac
-        step = np.linalg.solve(jtj + damping * (np.diag(np.diag(jtj)) + 1e-12 * np.eye(len(theta))), -jac.T @ r)
-        r2, q2 = resid(theta + step)
-        if r2 @ r2 < r @ r:
-            theta, r, q = theta + step, r2, q2
-            damping = max(damping / 3, 1e-12)
-        else:
-            damping *= 4
-            if damping > 1e8:
-                break
-    return theta[:npar].copy(), theta[npar:].copy()
+    y = TARGETS[target](x)
+    vp, vq = _design(x, num_degree, den_degree)
+    theta = _gauss_newton(vp, vq, y, _sk_start(vp, vq, y))
+    n_p = num_degree + 1
+    return theta[:n_p].copy(), theta[n_p:].copy()
 
 
 class Rational(Basis):

@@ -33,6 +33,7 @@ ONE_MINUS_Z2 = np.array([0.5, 0.0, -0.5])  # 1 - z^2 in the Chebyshev basis
 AUTO_KINDS = {"cuda": ("cheb", "bspline", "rational")}
 
 MAX_ORDER = 8  # largest derivative order of the kernel features
+MAX_BASIS = 16  # basis functions per edge the kernels hold (KF_MAX_K)
 
 
 @dataclass(frozen=True)

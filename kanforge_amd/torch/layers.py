@@ -19,10 +19,11 @@ import torch.nn.functional as F
 from torch import nn
 
 from .. import grid as grid_tools
+from .. import symbolic as sym
 from .._layer import basis_param_values, init_stds, resolve_groups
 from ..bases import Basis, Rational, make_basis
 from ..kernels import plan_for
-from ..kernels.plan import AUTO_KINDS
+from ..kernels.plan import AUTO_KINDS, MAX_BASIS
 from . import kernels as _kernels
 
 BACKENDS = ("auto", "ops", "kernel")
@@ -128,6 +129,7 @@ class KANLinear(nn.Module):
             self.register_buffer(f"basis_{name}", torch.as_tensor(np.ascontiguousarray(value), **like))
         self._trainable_names, self._buffer_names = list(trainable), list(buffers)
         self._plan = plan_for(self.basis)
+        _check_kernel_limits(self.basis)
         self._plan_key = None if self._plan is None else _kernels.plan_key(self._plan)
         self._state_cache = None
 
@@ -221,7 +223,7 @@ class KANLinear(nn.Module):
         if self.base_weight is not None:
             y = y + F.linear(self.base_activation(x), self.effective_base_weight())
         if self._sym_codes:
-            raise NotImplementedError("symbolic edges are not part of the HIP path")
+            y = y + self._symbolic_sum(x)
         if self.bias is not None:
             y = y + self.bias
         return y
@@ -245,16 +247,84 @@ class KANLinear(nn.Module):
             raise ValueError("order must be >= 0")
         self.uses_kernel(x.device)
         bw = self.effective_base_weight()
-        if bw is not None and order > 0 and self.base_activation is not F.silu:
+        other_base = bw is not None and self.base_activation is not F.silu
+        if other_base and order > 0:
             raise NotImplementedError("analytic derivatives need base_activation=F.silu or None")
-        if bw is not None and order == 0 and self.base_activation is not F.silu:
-            raise NotImplementedError("the HIP edge kernel evaluates the SiLU base branch only")
-        if self._sym_codes:
-            raise NotImplementedError("symbolic edges are not part of the HIP path")
+        if self._sym_codes and order > 0:
+            raise NotImplementedError("analytic derivatives of symbolic edges are not available; use autograd")
         num = den = None
         if self._plan.kind == "rational":
             num, den = self.basis_numerator, self.basis_denominator
-        return _kernels.edge_derivative(x, self.effective_coef(), bw, self._basis_state(), self._plan, int(order), num, den)
+        # the edge kernel evaluates a SiLU base branch itself; another activation is added here
+        d = _kernels.edge_derivative(
+            x, self.effective_coef(), None if other_base else bw, self._basis_state(), self._plan_key, int(order), num, den
+        )
+        if other_base:
+            d = d + self.base_activation(x).unsqueeze(-2) * bw
+        if self._sym_codes:
+            d = d + self._symbolic_dense(x)
+        return d
+
+    # --- masks and symbolic edges (kanforge/_layer.py:209-272) -------------------------------
+
+    def symbolic_edges(self) -> dict:
+        """``{(o, i): (function name, (a, b, c, d))}`` of the edges fixed to a function."""
+        code = self.sym_code.detach().cpu().numpy()
+        params = self.sym_params.detach().double().cpu().numpy()
+        return {(int(o), int(i)): (sym.NAMES[code[o, i]], tuple(float(v) for v in params[o, i])) for o, i in zip(*np.nonzero(code >= 0))}
+
+    @torch.no_grad()
+    def fix_symbolic(self, o: int, i: int, name: str, params=(1.0, 0.0, 1.0, 0.0)) -> None:
+        """Edge (o, i) becomes ``c * f(a * x + b) + d``; its spline and base parts are masked."""
+        code = sym.code_of(name)
+        self.edge_mask[o, i] = 0.0
+        self.sym_code[o, i] = code
+        self.sym_params[o, i] = torch.as_tensor(params, dtype=self.sym_params.dtype)
+        self._refresh_symbolic()
+
+    @torch.no_grad()
+    def unfix_symbolic(self, o: int, i: int) -> None:
+        """Edge (o, i) is the learned edge again (spline and base parts unmasked)."""
+        self.edge_mask[o, i] = 1.0
+        self.sym_code[o, i] = -1
+        self._refresh_symbolic()
+
+    @torch.no_grad()
+    def set_edge_mask(self, mask) -> None:
+        """0 removes an edge (pruning); symbolic edges stay as they are."""
+        self.edge_mask.copy_(torch.as_tensor(np.asarray(mask, dtype=np.float64), dtype=self.edge_mask.dtype))
+
+    def active_edges(self) -> np.ndarray:
+        """Boolean ``(out, in)``: learned (unmasked) or symbolic edges."""
+        return ((self.edge_mask != 0) | (self.sym_code >= 0)).cpu().numpy()
+
+    def _symbolic_edge_list(self):
+        """(out index, in index, code, (a, b, c, d)) of every symbolic edge, cached per buffer version."""
+        code, params = self.sym_code, self.sym_params
+        key = (code.data_ptr(), code._version, params.data_ptr(), params._version)
+        cached = getattr(self, "_sym_cache", None)
+        if cached is None or cached[0] != key:
+            o_idx, i_idx = torch.nonzero(code >= 0, as_tuple=True)
+            cached = (key, (o_idx, i_idx, code[o_idx, i_idx], params[o_idx, i_idx]))
+            self._sym_cache = cached
+        return cached[1]
+
+    def _symbolic_values(self, x: torch.Tensor) -> torch.Tensor:
+        o_idx, i_idx, codes, params = self._symbolic_edge_list()
+        return sym.evaluate(x.index_select(-1, i_idx), codes, params.to(x.dtype), self._sym_codes)
+
+    def _symbolic_sum(self, x: torch.Tensor) -> torch.Tensor:
+        """``(..., out)``: the symbolic edges summed into their outputs."""
+        o_idx = self._symbolic_edge_list()[0]
+        v = self._symbolic_values(x)
+        return torch.zeros(*x.shape[:-1], self.out_features, dtype=v.dtype, device=v.device).index_add(-1, o_idx, v)
+
+    def _symbolic_dense(self, x: torch.Tensor) -> torch.Tensor:
+        """``(..., out, in)``: the symbolic edges' values, zero on the other edges."""
+        o_idx, i_idx = self._symbolic_edge_list()[:2]
+        v = self._symbolic_values(x)
+        flat = torch.zeros(*x.shape[:-1], self.out_features * self.in_features, dtype=v.dtype, device=v.device)
+        return flat.index_add(-1, o_idx * self.in_features + i_idx, v).unflatten(-1, (self.out_features, self.in_features))
 
     # --- state import / export (kanforge.save format) ------------------------------
 
@@ -310,25 +380,27 @@ class KANLinear(nn.Module):
                 layer.bias.copy_(linear.bias)
         return layer
 
-    # --- grid update, refinement, basis conversion (kanforge/_layer.py:99-191) ------------
+    # --- grid update, refinement, basis conversion ----------------------------------------
+    #
+    # One operation underlies all three tools: snapshot the layer in float64, choose the new
+    # basis, its parameters and the sample points, refit every edge function on those points
+    # (grid.refit, per-input least squares) and install the result. The refit follows
+    # kanforge/_layer.py:116-191 so that a grid change gives the reference's grid and
+    # coefficients; parameter shapes can change, so optimizers are re-created afterwards.
 
-    def _export_state(self) -> dict:
-        """Float64 NumPy copies of ``coef``, ``edge_scale`` and the basis parameters."""
+    def _snapshot(self) -> "_HostLayer":
         f = self._to_numpy
-        return {
-            "coef": f(self.coef),
-            "edge_scale": None if self.edge_scale is None else f(self.edge_scale),
-            "trainable": {n: f(getattr(self, f"basis_{n}")) for n in self._trainable_names},
-            "buffers": {n: f(getattr(self, f"basis_{n}")) for n in self._buffer_names},
-        }
-
-    def _expanded(self, trainable: dict, buffers: dict) -> dict:
-        """Basis parameters per input (group parameters repeated over their inputs)."""
-        rep = self.in_features // self.groups
-        return {**{k: np.repeat(v, rep, axis=0) for k, v in trainable.items()}, **buffers}
+        return _HostLayer(
+            self.in_features,
+            self.groups,
+            f(self.coef),
+            None if self.edge_scale is None else f(self.edge_scale),
+            {n: f(getattr(self, f"basis_{n}")) for n in self._trainable_names},
+            {n: f(getattr(self, f"basis_{n}")) for n in self._buffer_names},
+        )
 
     @torch.no_grad()
-    def _load_state(self, basis: Basis, coef, edge_scale, trainable: dict, buffers: dict) -> None:
+    def _install(self, basis: Basis, coef, edge_scale, trainable: dict, buffers: dict) -> None:
         like = {"dtype": self.coef.dtype, "device": self.coef.device}
         self.basis = basis
         self._init_kwargs["basis"] = basis
@@ -337,32 +409,29 @@ class KANLinear(nn.Module):
             self.edge_scale = nn.Parameter(torch.as_tensor(np.ascontiguousarray(edge_scale), **like))
         self._set_basis_state(trainable, buffers)
 
-    def _refit_to(self, new_basis: Basis, new_trainable: dict, new_buffers: dict, x: np.ndarray, ridge: float) -> None:
-        st = self._export_state()
-        scale = st["edge_scale"]
-        coef_eff = st["coef"] if scale is None else st["coef"] * scale[..., None]
-        coef = grid_tools.refit(
-            self.basis,
-            self._expanded(st["trainable"], st["buffers"]),
-            coef_eff,
-            new_basis,
-            self._expanded(new_trainable, new_buffers),
-            x,
-            ridge,
-        )
-        if scale is not None:  # keep the edge scales, fold the refit into coef
-            ok = np.abs(scale) > 1e-12
-            coef = coef / np.where(ok, scale, 1.0)[..., None]
-            scale = np.where(ok, scale, 1.0)
-        self._load_state(new_basis, coef, scale, new_trainable, new_buffers)
-
-    def _samples(self, x, basis: Basis, buffers: dict, n: int) -> np.ndarray:
+    def _fit_points(self, x, ranges_of: tuple, n_default: int) -> np.ndarray:
+        """The refit's sample points: ``x`` itself, or ``n_default`` points spread over the grid
+        ranges of ``ranges_of = (basis, buffers)``."""
         if x is not None:
             return np.asarray(self._to_numpy(x), dtype=np.float64).reshape(-1, self.in_features)
-        ranges = grid_tools.grid_ranges(basis, buffers)
+        ranges = grid_tools.grid_ranges(*ranges_of)
         if ranges is None:
-            raise ValueError(f"{type(basis).__name__} has no grid: pass samples x")
-        return grid_tools.sample_inputs(ranges, n)
+            raise ValueError(f"{type(ranges_of[0]).__name__} has no grid: pass samples x")
+        return grid_tools.sample_inputs(ranges, n_default)
+
+    def _regrid(self, new_basis: Basis, trainable: dict, buffers: dict, points: np.ndarray, ridge: float) -> None:
+        old = self._snapshot()
+        coef = grid_tools.refit(
+            self.basis, old.per_input(), old.effective_coef(), new_basis, old.per_input(trainable, buffers), points, ridge
+        )
+        scale = old.edge_scale
+        if scale is not None:
+            # edge scales are kept; an edge whose scale vanished restarts at scale 1 and the
+            # refit goes into its coefficients
+            live = np.abs(scale) > 1e-12
+            scale = np.where(live, scale, 1.0)
+            coef = coef / scale[..., None]
+        self._install(new_basis, coef, scale, trainable, buffers)
 
     def update_grid(self, x, *, margin: float = 0.0, grid_eps: float = 0.02, ridge: float = 0.0) -> None:
         """Adapt every grid to the inputs ``x`` and refit the edge functions on them (pykan's
@@ -373,40 +442,59 @@ class KANLinear(nn.Module):
         names = self.basis.grid_names()
         if not names:
             raise TypeError(f"{type(self.basis).__name__} has no grid")
-        st = self._export_state()
-        xs = self._samples(x, self.basis, st["buffers"], 0)
-        buffers = dict(st["buffers"])
-        for name in names:
-            buffers[name] = grid_tools.adaptive_grid(xs, buffers[name].shape[-1], margin, grid_eps)
-        self._refit_to(self.basis, st["trainable"], buffers, xs, ridge)
+        old = self._snapshot()
+        points = self._fit_points(x, (self.basis, old.buffers), 0)
+        buffers = {**old.buffers, **{n: grid_tools.adaptive_grid(points, old.buffers[n].shape[-1], margin, grid_eps) for n in names}}
+        self._regrid(self.basis, old.trainable, buffers, points, ridge)
 
     def refine_grid(self, grid_size: int, x=None, *, ridge: float = 0.0) -> None:
-        """The same basis on a finer (or coarser) grid; each input's grid keeps its shape."""
-        key = _resize_key(self.basis)
-        new_basis = make_basis({**self.basis.config(), key: grid_size})
-        st = self._export_state()
+        """The same basis on a finer (or coarser) grid; each input's grid keeps its range and
+        is resampled to the new number of points."""
+        new_basis = make_basis({**self.basis.config(), _resize_key(self.basis): grid_size})
+        _check_kernel_limits(new_basis)
+        old = self._snapshot()
         trainable, buffers = basis_param_values(new_basis, self.groups, self.in_features)
-        for name in new_basis.grid_names():
-            if name in st["buffers"]:
-                buffers[name] = grid_tools.resample_grid(st["buffers"][name], buffers[name].shape[-1])
-        xs = self._samples(x, self.basis, st["buffers"], 8 * new_basis.size + 64)
-        self._refit_to(new_basis, trainable, buffers, xs, ridge)
+        for n in new_basis.grid_names():
+            if n in old.buffers:
+                buffers[n] = grid_tools.resample_grid(old.buffers[n], buffers[n].shape[-1])
+        points = self._fit_points(x, (self.basis, old.buffers), 8 * new_basis.size + 64)
+        self._regrid(new_basis, trainable, buffers, points, ridge)
 
     def change_basis(self, basis, x=None, *, ridge: float = 0.0) -> None:
         """Convert to another basis (e.g. B-spline -> Chebyshev) by least squares; without
         ``x`` the fit uses points spread over the current grid ranges (or the new basis'
         ranges), and a new grid inherits each input's range."""
         new_basis = make_basis(basis)
-        st = self._export_state()
-        old_ranges = grid_tools.grid_ranges(self.basis, st["buffers"])
+        _check_kernel_limits(new_basis)
+        old = self._snapshot()
+        old_ranges = grid_tools.grid_ranges(self.basis, old.buffers)
         trainable, buffers = basis_param_values(new_basis, self.groups, self.in_features, old_ranges)
-        src, src_buffers = (self.basis, st["buffers"]) if old_ranges is not None else (new_basis, buffers)
-        xs = self._samples(x, src, src_buffers, 8 * max(new_basis.size, self.basis.size) + 64)
-        self._refit_to(new_basis, trainable, buffers, xs, ridge)
+        ranges_of = (self.basis, old.buffers) if old_ranges is not None else (new_basis, buffers)
+        points = self._fit_points(x, ranges_of, 8 * max(new_basis.size, self.basis.size) + 64)
+        self._regrid(new_basis, trainable, buffers, points, ridge)
 
     def extra_repr(self) -> str:
         groups = "" if self.groups == self.in_features else f", groups={self.groups}"
         return f"in_features={self.in_features}, out_features={self.out_features}, basis={self.basis!r}{groups}"
+
+
+class _HostLayer:
+    """Float64 NumPy snapshot of what a grid refit reads from a layer."""
+
+    def __init__(self, n_in: int, groups: int, coef, edge_scale, trainable: dict, buffers: dict):
+        self.n_in, self.groups = n_in, groups
+        self.coef, self.edge_scale = coef, edge_scale
+        self.trainable, self.buffers = trainable, buffers
+
+    def effective_coef(self) -> np.ndarray:
+        return self.coef if self.edge_scale is None else self.coef * self.edge_scale[..., None]
+
+    def per_input(self, trainable: dict | None = None, buffers: dict | None = None) -> dict:
+        """Basis parameters per input: group parameters repeated over their inputs."""
+        trainable = self.trainable if trainable is None else trainable
+        buffers = self.buffers if buffers is None else buffers
+        rep = self.n_in // self.groups
+        return {**{k: np.repeat(v, rep, axis=0) for k, v in trainable.items()}, **buffers}
 
 
 class GRKAN(KANLinear):
@@ -484,6 +572,13 @@ def from_mlp(mlp: nn.Sequential, basis="bspline", **kwargs) -> nn.Sequential:
             out.append(mods[i])
             i += 1
     return nn.Sequential(*out)
+
+
+def _check_kernel_limits(basis: Basis) -> None:
+    """The HIP kernels hold at most ``MAX_BASIS`` basis functions per edge (register and LDS tiles
+    are sized for it); larger bases are rejected when a layer is built or re-gridded."""
+    if basis.size > MAX_BASIS:
+        raise ValueError(f"{basis!r} has {basis.size} basis functions per edge; the HIP kernels support at most {MAX_BASIS}")
 
 
 def _resize_key(basis: Basis) -> str:

@@ -399,6 +399,36 @@ def edge_derivative(x, coef_eff, basis, m=0, base_weight_eff=None):
 
 
 # --------------------------------------------------------------------------
+# symbolic edges (``kanforge/_layer.py:256-272``, ``kanforge/interpret/library.py:34-55``)
+
+SYMBOLIC = (
+    ("0", lambda u: 0 * u), ("x", lambda u: u), ("x^2", lambda u: u * u), ("x^3", lambda u: u * u * u),
+    ("x^4", lambda u: (u * u) * (u * u)), ("1/x", lambda u: 1 / u), ("1/x^2", lambda u: 1 / (u * u)),
+    ("sqrt", np.sqrt), ("1/sqrt", lambda u: 1 / np.sqrt(u)), ("exp", np.exp), ("log", np.log), ("sin", np.sin),
+    ("cos", np.cos), ("tanh", np.tanh), ("sigmoid", lambda u: 1 / (1 + np.exp(-u))), ("gaussian", lambda u: np.exp(-u * u)),
+    ("abs", np.abs), ("arctan", np.arctan),
+)
+
+
+def symbolic_edges(x, code, params):
+    """(..., out, in): c f_code(a x_i + b) + d on edges with code >= 0, zero elsewhere.
+
+    ``code`` (out, in) indexes ``SYMBOLIC`` (the reference's function order); ``params`` (out, in, 4).
+    """
+    x = np.asarray(x, dtype=np.float64)
+    code = np.asarray(code)
+    p = np.asarray(params, dtype=np.float64)
+    u = p[..., 0] * x[..., None, :] + p[..., 1]
+    out = np.zeros(u.shape)
+    for k in np.unique(code[code >= 0]):
+        sel = code == k
+        with np.errstate(all="ignore"):
+            v = p[..., 2] * SYMBOLIC[k][1](np.where(sel, u, 1.0)) + p[..., 3]
+        out = np.where(sel, v, out)
+    return out
+
+
+# --------------------------------------------------------------------------
 # rounding helpers: the oracle always sees the dtype-rounded inputs
 
 
@@ -441,4 +471,5 @@ PINNING = {
     "prim_F/prim_G/prim_P": "brute-force Python loops on tiny shapes; y = F_0(x,c,1) equals kan_linear",
     "edge_derivative": "sum over i of order-0 edges plus bias equals kan_linear (tests/test_layers.py:62-63)",
     "kan_linear": "per-edge manual sum (tests/test_bases.py:64-74)",
+    "symbolic_edges": "defining values of every library function (x^2(3) = 9, sin(pi/2) = 1, ...); affine map inside and out",
 }

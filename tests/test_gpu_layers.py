@@ -228,6 +228,63 @@ def test_edge_dropout_training_step_matches_oracle(name):
         assert err <= 1e-5, (key, err)
 
 
+@pytest.mark.parametrize("name", ["bspline53", "chebyshev8"])
+def test_masked_and_symbolic_layer_matches_oracle(name):
+    """Pruned and symbolic edges on the kernel path (kanforge tests/test_interpret.py:116-133):
+    forward, x/coef/base_weight gradients and the order-0 edge derivative against the oracle."""
+    B, IN, OUT = 41, 5, 4
+    layer = make_layer(name, IN, OUT, torch.float32, edge_scale=False)
+    mask = np.ones((OUT, IN))
+    mask[0, 1] = mask[2, 3] = mask[3, 0] = 0
+    layer.set_edge_mask(mask)
+    layer.fix_symbolic(1, 0, "x^2", (1.0, 0.5, 2.0, 0.25))
+    layer.fix_symbolic(3, 4, "sin", (2.0, 0.1, 1.5, -0.2))
+    layer.fix_symbolic(0, 2, "gaussian", (1.5, 0.0, 0.7, 0.0))
+    ob = oracle_of(layer)
+    rng = np.random.default_rng(10)
+    x0, gy0 = rng.uniform(-0.9, 0.9, (B, IN)), rng.normal(0, 1, (B, OUT))
+    x = torch.as_tensor(x0, dtype=torch.float32, device=DEV).requires_grad_()
+    y = layer(x)
+    gx, gc, gw = torch.autograd.grad(y, [x, layer.coef, layer.base_weight], torch.as_tensor(gy0, dtype=torch.float32, device=DEV))
+    xr = rounded(x0, torch.float32)
+    m = np64(layer.edge_mask)
+    code, sp = layer.sym_code.cpu().numpy(), np64(layer.sym_params)
+    c, W = np64(layer.coef) * m[..., None], np64(layer.base_weight) * m
+    e0 = o.edge_derivative(xr, c, ob, 0, W) + o.symbolic_edges(xr, code, sp)
+    # d/dx of a symbolic edge c f(a x + b) + d by central differences of the oracle (float64)
+    h = 1e-6
+    dsym = (o.symbolic_edges(xr + h, code, sp) - o.symbolic_edges(xr - h, code, sp)) / (2 * h)
+    checks = {
+        "y": (y, e0.sum(-1) + np64(layer.bias)),
+        "edges": (layer.edge_derivative(x, 0), e0),
+        "x": (gx, o.prim_P(xr, gy0, c, ob, 1) + (gy0 @ W) * o.silu_derivative(xr, 1) + np.einsum("bo,boi->bi", gy0, dsym)),
+        "coef": (gc, o.prim_G(xr, gy0, None, ob, 0) * m[..., None]),
+        "base_weight": (gw, (gy0.T @ o.silu_derivative(xr, 0)) * m),
+    }
+    for key, (got, want) in checks.items():
+        err = o.normwise_err(np64(got), want)
+        print(f"masked/symbolic {name} {key}: {err:.3e}", flush=True)
+        assert err <= 1e-5, (key, err)
+
+
+def test_edge_derivative_order0_with_another_base_activation():
+    """Order-0 edges of a layer whose base activation is not SiLU (kanforge/torch/layers.py:213-216)."""
+    torch.manual_seed(0)
+    layer = KANLinear(6, 5, kf.BSpline(5, 3), base_activation=torch.nn.functional.gelu).to(DEV)
+    x0 = np.random.default_rng(11).uniform(-0.9, 0.9, (30, 6))
+    x = torch.as_tensor(x0, dtype=torch.float32, device=DEV)
+    d = layer.edge_derivative(x, 0)
+    xr = rounded(x0, torch.float32)
+    from scipy.special import erf
+
+    gelu = 0.5 * xr * (1 + erf(xr / np.sqrt(2)))
+    want = o.edge_derivative(xr, np64(layer.coef), oracle_of(layer), 0) + gelu[:, None, :] * np64(layer.base_weight)
+    assert o.normwise_err(np64(d), want) <= 1e-5
+    np.testing.assert_allclose(np64(d.sum(-1) + layer.bias), np64(layer(x)), atol=2e-6)
+    with pytest.raises(NotImplementedError):
+        layer.edge_derivative(x, 1)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
 def test_grkan_forward_and_all_gradients(dtype):
     B, IN, OUT = 96, 32, 40

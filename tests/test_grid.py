@@ -17,10 +17,9 @@ rng = np.random.default_rng(0)
 
 def edge_functions(layer, x):
     """(N, out, in) edge function values of a layer at host points x (N, in), float64."""
-    st = layer._export_state()
-    c = st["coef"] if st["edge_scale"] is None else st["coef"] * st["edge_scale"][..., None]
-    phi = layer.basis.host_values(x, layer._expanded(st["trainable"], st["buffers"]))
-    return np.einsum("nik,oik->noi", phi, c)
+    snap = layer._snapshot()
+    phi = layer.basis.host_values(x, snap.per_input())
+    return np.einsum("nik,oik->noi", phi, snap.effective_coef())
 
 
 def test_adaptive_grid_definition():

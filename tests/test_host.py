@@ -292,3 +292,37 @@ def test_custom_op_fake_kernels_give_shapes_on_meta_tensors():
     num, den = torch.empty(7, 6, device="meta"), torch.empty(7, 4, device="meta")
     p, dn, dd = torch.ops.kf.rational_bwd(x, g, torch.empty(5, 7, 1, device="meta"), None, num, den, rkey)
     assert p.shape == (33, 7) and dn.shape == (7, 6) and dd.shape == (7, 4)
+
+
+def test_symbolic_table_and_functions_match_the_oracle():
+    from kanforge_amd import symbolic as sym
+
+    assert list(sym.NAMES) == [n for n, _ in o.SYMBOLIC]
+    x = np.linspace(0.3, 2.5, 23)
+    for k, (name, fn) in enumerate(o.SYMBOLIC):
+        got = sym.function(k)(torch.as_tensor(x)).numpy()
+        np.testing.assert_allclose(got, fn(x), rtol=1e-12, atol=1e-14, err_msg=name)
+    layer = KANLinear(3, 2, kf.Chebyshev(3))
+    layer.fix_symbolic(1, 0, "x^2", (1.0, 0.5, 2.0, 0.25))
+    layer.fix_symbolic(0, 2, "sin", (2.0, 0.0, 1.0, 0.0))
+    assert layer.symbolic_edges() == {(0, 2): ("sin", (2.0, 0.0, 1.0, 0.0)), (1, 0): ("x^2", (1.0, 0.5, 2.0, 0.25))}
+    assert layer.edge_mask[1, 0] == 0 and layer.active_edges().all()
+    layer.unfix_symbolic(1, 0)
+    assert layer.symbolic_edges().keys() == {(0, 2)} and layer.edge_mask[1, 0] == 1
+    with pytest.raises(ValueError, match="unknown symbolic"):
+        layer.fix_symbolic(0, 0, "sinc")
+
+
+def test_bases_beyond_the_kernel_limit_are_rejected_up_front():
+    from kanforge_amd.kernels.plan import MAX_BASIS
+
+    assert MAX_BASIS == _lib.KF_MAX_K
+    with pytest.raises(ValueError, match="at most 16"):
+        KANLinear(3, 2, kf.BSpline(20, 3))
+    layer = KANLinear(3, 2, kf.BSpline(5, 3))
+    before = layer.coef.detach().clone()
+    with pytest.raises(ValueError, match="at most 16"):
+        layer.refine_grid(20)
+    assert torch.equal(layer.coef, before) and layer.basis.grid_size == 5  # untouched
+    layer.refine_grid(13)  # 16 basis functions: the largest supported
+    assert layer.coef.shape == (2, 3, 16)

@@ -277,3 +277,21 @@ def test_planted_mistakes_fail():
     # a transposed coefficient operand fails the brute-force loop check
     basis, xx, c, g, w = tiny()
     assert not np.allclose(o.prim_F(xx, c[::-1], w, basis, 0), o.prim_F(xx, c, w, basis, 0))
+
+
+def test_symbolic_edges_follow_the_function_table():
+    """Each code's function at a defining point, the affine maps inside and outside, zeros on the
+    other edges, and the table order of the reference's library (codes are stored in models)."""
+    names = [n for n, _ in o.SYMBOLIC]
+    assert names[:5] == ["0", "x", "x^2", "x^3", "x^4"] and names[11] == "sin" and names[-1] == "arctan"
+    at = {"0": (2.0, 0.0), "x": (2.0, 2.0), "x^2": (3.0, 9.0), "x^3": (2.0, 8.0), "x^4": (2.0, 16.0), "1/x": (4.0, 0.25),
+          "1/x^2": (2.0, 0.25), "sqrt": (4.0, 2.0), "1/sqrt": (4.0, 0.5), "exp": (0.0, 1.0), "log": (np.e, 1.0),
+          "sin": (np.pi / 2, 1.0), "cos": (0.0, 1.0), "tanh": (0.0, 0.0), "sigmoid": (0.0, 0.5), "gaussian": (0.0, 1.0),
+          "abs": (-3.0, 3.0), "arctan": (1.0, np.pi / 4)}
+    for k, name in enumerate(names):
+        u, want = at[name]
+        code = np.array([[k, -1]])
+        params = np.array([[[2.0, u - 2.0 * 0.5, 3.0, -1.0], [1, 0, 1, 0]]])  # a x + b = u at x = 0.5
+        d = o.symbolic_edges(np.array([[0.5, 0.7]]), code, params)
+        assert np.isclose(d[0, 0, 0], 3.0 * want - 1.0), name
+        assert d[0, 0, 1] == 0.0
