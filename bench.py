@@ -118,6 +118,34 @@ def cpu_baseline():
     }
 
 
+def mfma_probe(dev, iters=4000, blocks=512):
+    """Sustained bf16 MFMA rate of this card (kf_probe_mfma): back-to-back 32x32x16 MFMAs on
+    pseudo-random operands, rotating through eight register sets ("changing") or one ("fixed"),
+    two waves per SIMD; with the shader clock the probe's waves ran at."""
+    import ctypes
+
+    from kanforge_amd.torch import _lib
+
+    lib = _lib.load()
+    out = torch.empty(blocks * 256 * 3, dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    res = {}
+    for label, rotate in (("changing", 1), ("fixed", 0)):
+        for _ in range(2):  # warm-up launch, then the timed one
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record(stream)
+            rc = lib.kf_probe_mfma(blocks, iters, rotate, ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(stream.cuda_stream))
+            e.record(stream)
+            _lib.check(rc, "kf_probe_mfma")
+        torch.cuda.synchronize()
+        ms = s.elapsed_time(e)
+        flop = blocks * 4 * iters * 8 * 2.0 * 32 * 32 * 16
+        t = out.view(blocks, 256, 3)[:, 0, 1:].double().cpu()
+        clock = (t[:, 0] / (t[:, 1] / 1e8)).median().item()
+        res[label] = {"tflops": flop / (ms * 1e-3) / 1e12, "frac_of_peak": flop / (ms * 1e-3) / PEAK_BF16, "clock_ghz": clock / 1e9}
+    return res
+
+
 def _timed(step, steps, warmup, timer):
     for _ in range(warmup):
         step()
@@ -411,6 +439,7 @@ def main():
             "traffic_source": TRAFFIC_FILE,
         },
     }
+    out["mfma_probe"] = mfma_probe(dev)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)

@@ -95,6 +95,10 @@ typedef struct kf_basis {
   const float *knots_cmp; /* bspline, device */
   const float *num;       /* rational, device */
   const float *den;       /* rational, device */
+  /* bspline, device, optional: (n_in, 2) float32 (t_0, 1 / h) of each input whose real knots are
+   * evenly spaced by h (t_0 its first real knot); NULL unless every input's knots are. Only speeds
+   * up the kernels: intervals are still decided by knots_cmp, so results keep their semantics. */
+  const float *knots_uniform;
 } kf_basis;
 
 /* operation ids for kf_workspace_bytes */
@@ -184,6 +188,15 @@ size_t kf_rational_workspace_bytes(const kf_basis *basis, int64_t batch, int64_t
 int kf_rational_param_grad(const kf_basis *basis, int dtype, int64_t batch, int64_t n_in, const void *x,
                            const float *h, const void *w, float *dnum, float *dden, void *workspace,
                            size_t workspace_bytes, void *stream);
+
+/*
+ * Diagnostics, no reference counterpart: the card's sustained bf16 MFMA rate. Launches `blocks`
+ * workgroups of 4 waves, each running iters x 8 v_mfma_f32_32x32x16_bf16 on pseudo-random
+ * operands (taken in rotation from eight register sets when `rotate`, else one fixed set).
+ * out: device float[blocks * 256 * 3]; per workgroup, lane 0's entries 1 and 2 are the
+ * shader-clock cycles and the 100 MHz real-time ticks of its first wave's MFMA loop.
+ */
+int kf_probe_mfma(int blocks, int iters, int rotate, float *out, void *stream);
 
 /* Text of the last error on the calling thread ("" if none). */
 const char *kf_last_error(void);

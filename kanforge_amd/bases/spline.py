@@ -43,6 +43,21 @@ def ceil_f32(t: np.ndarray) -> np.ndarray:
     return f
 
 
+def uniform_table(grid, k: int, rtol: float = 1e-7) -> np.ndarray | None:
+    """``(in, 2)`` float32 ``(t_0, 1/h)`` of the extended knots when every input's knots are evenly
+    spaced by its own h (relative tolerance ``rtol``), else None. The kernels use it to locate a
+    point's interval in constant time; the interval itself is still decided by the comparison
+    table, and the values by the knots being even."""
+    t = extend_grid(np.atleast_2d(np.asarray(grid, dtype=np.float64)), k)
+    if t.shape[1] < 2:
+        return None
+    d = np.diff(t, axis=1)
+    h = (t[:, -1] - t[:, 0]) / (t.shape[1] - 1)
+    if not (h > 0).all() or not (np.abs(d - h[:, None]) <= rtol * h[:, None]).all():
+        return None
+    return np.ascontiguousarray(np.stack([t[:, 0], 1.0 / h], 1).astype(np.float32))
+
+
 def knot_tables(grid, k: int) -> tuple[np.ndarray, np.ndarray]:
     """(arithmetic table (in, nk + 2k), comparison table (in, nk)), float32."""
     t = extend_grid(np.atleast_2d(np.asarray(grid, dtype=np.float64)), k)

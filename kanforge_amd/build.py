@@ -10,6 +10,8 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
@@ -23,7 +25,6 @@ HIPCC_FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     # packed fp32 VALU ops stay off: plain scalar float code only
     "-Xclang",
     "-target-feature",
@@ -44,17 +45,32 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every HIP source into libkfhip.so (always recompiles)."""
-    tmp = LIB.with_suffix(f".so.tmp{os.getpid()}")
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", "-o", str(tmp), *map(str, sources())]
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
-        tmp.unlink(missing_ok=True)
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-6000:]}")
-    os.replace(tmp, LIB)
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every HIP source into libkfhip.so (always recompiles): one object per source,
+    compiled in parallel, then linked."""
+    objdir = Path(tempfile.mkdtemp(prefix="kfhip-build-"))
+    tmp = LIB.with_suffix(f".so.tmp{os.getpid()}")
+    try:
+        srcs = sources()
+        objs = [objdir / (src.stem + ".o") for src in srcs]
+        cc = hipcc()
+        jobs = [[cc, *HIPCC_FLAGS, f"-I{INCLUDE}", "-c", "-o", str(obj), str(src)] for src, obj in zip(srcs, objs)]
+        with ThreadPoolExecutor(max_workers=min(len(jobs), os.cpu_count() or 1)) as pool:
+            for fut in [pool.submit(_run, job, verbose) for job in jobs]:
+                fut.result()
+        _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)], verbose)
+        os.replace(tmp, LIB)
+    finally:
+        tmp.unlink(missing_ok=True)
+        shutil.rmtree(objdir, ignore_errors=True)
     return LIB
 
 

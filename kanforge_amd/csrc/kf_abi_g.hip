@@ -1,0 +1,206 @@
+// kf_G (include/kfhip.h): the coefficient-gradient contraction's launch configurations,
+// workspace carving and dispatch.
+#include "kf_abi.h"
+#include "kf_rational.h"
+
+using namespace kfabi;
+
+namespace {
+
+template <typename T, int WMW, int WJW, int TM, int FW, int RB, bool CHEB, bool FLAT = false>
+int launch_g_t(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out,
+               const void* phit, const float* zt, const float* wt, const void* gt, void* dc, float* zpart) {
+  constexpr int BM = WMW * TM * 32, NMAX = WJW * FW * 32, RS = RB + 16;
+  const size_t lds_ops = (size_t)2 * (BM + NMAX) * RS;
+  const size_t lds_red = (size_t)(FLAT ? NMAX / 32 : kb.n_t) * (BM / 2) * 33 * 4;
+  const size_t lds = lds_ops > lds_red ? lds_ops : lds_red;
+  auto kern = g_kernel<T, WMW, WJW, TM, FW, RB, CHEB, FLAT>;
+  if (!reserve_lds((const void*)kern, lds))
+    return fail(KF_ELAUNCH, "G: cannot reserve %zu bytes of LDS", lds);
+  constexpr int TI = FLAT ? NMAX : 32;
+  if (FLAT && L.INP % TI) return fail(KF_EINVAL, "G: workspace layout not aligned");
+  const int n_m = (int)(L.OUTP / BM), n_n = (int)((n_in + TI - 1) / TI);
+  hipLaunchKernelGGL(kern, dim3(n_m * n_n, L.nz), dim3(WMW * WJW * 64), lds, s, kb, (int)batch, (int)n_in,
+                     (int)n_out, (int)L.BP, (int)L.OUTP, (int)L.INP, (const T*)phit, zt, wt, (const T*)gt, (T*)dc,
+                     L.nz > 1 ? zpart : nullptr);
+  int rc = check_launch("G");
+  if (rc || L.nz == 1) return rc;
+  // the splits summed into split 0 (coalesced), then the fold from that one slice
+  const size_t zstride = (size_t)L.OUTP * L.INP * kb.n_t;
+  long blocks = ((long)zstride + kThreads - 1) / kThreads;
+  if (blocks > 65535 * 4) blocks = 65535 * 4;
+  hipLaunchKernelGGL(g_split_sum, dim3((unsigned)blocks), dim3(kThreads), 0, s, (long)zstride, L.nz, zstride, zpart);
+  rc = check_launch("G split sum");
+  if (rc) return rc;
+  long n = (long)n_out * n_in * kb.K;
+  blocks = (n + kThreads - 1) / kThreads;
+  if (blocks > 65535 * 4) blocks = 65535 * 4;
+  hipLaunchKernelGGL(g_split_reduce<T>, dim3((unsigned)blocks), dim3(kThreads), 0, s, kb, (int)n_out, (int)n_in,
+                     (int)L.OUTP, (int)L.INP, 1, (const float*)zpart, (T*)dc);
+  return check_launch("G split reduce");
+}
+
+template <typename T, bool CHEB>
+int launch_g_cfg(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out,
+                 const void* x, const void* w, const float* zt, const float* wt, const void* gt, void* dc) {
+  // x: phiT, w: the split partial sums
+  float* zp = (float*)w;
+  if (!CHEB && kb.kind == KF_KIND_RATIONAL) {
+    if (L.cfg != 0) return fail(KF_EINVAL, "G: rational plans have one feature");
+    return launch_g_t<T, 2, 2, 2, 2, 128, false, true>(L, s, kb, batch, n_in, n_out, x, zt, wt, gt, dc, zp);
+  }
+  switch (L.cfg) {
+    case 0: return launch_g_t<T, 2, 2, 2, 2, 128, CHEB>(L, s, kb, batch, n_in, n_out, x, zt, wt, gt, dc, zp);
+    case 1: return launch_g_t<T, 2, 2, 2, 3, 128, CHEB>(L, s, kb, batch, n_in, n_out, x, zt, wt, gt, dc, zp);
+    case 2: return launch_g_t<T, 2, 2, 2, 4, 128, CHEB>(L, s, kb, batch, n_in, n_out, x, zt, wt, gt, dc, zp);
+    case 3: return launch_g_t<T, 2, 2, 2, 5, 128, CHEB>(L, s, kb, batch, n_in, n_out, x, zt, wt, gt, dc, zp);
+    case 4: return launch_g_t<T, 2, 2, 2, 6, 128, CHEB>(L, s, kb, batch, n_in, n_out, x, zt, wt, gt, dc, zp);
+    case 5: return launch_g_t<T, 2, 2, 1, 8, 64, CHEB>(L, s, kb, batch, n_in, n_out, x, zt, wt, gt, dc, zp);
+    default: return launch_g_t<T, 2, 2, 1, 12, 64, CHEB>(L, s, kb, batch, n_in, n_out, x, zt, wt, gt, dc, zp);
+  }
+}
+
+template <typename T, int TM, int FW, int RB>
+int launch_g_ws(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out,
+                const float* zt, const float* wt, const void* gt, const float* colsum, void* dc) {
+  constexpr int BM = 2 * TM * 32, NMAX = 2 * FW * 32, RS = RB + 16;
+  const size_t lds_ops = (size_t)2 * (BM + NMAX) * RS, lds_red = (size_t)kb.n_t * (BM / 2) * 33 * 4;
+  const size_t lds = lds_ops > lds_red ? lds_ops : lds_red;
+  auto kern = L.skip0 ? g_ws_kernel<T, TM, FW, RB, true> : g_ws_kernel<T, TM, FW, RB, false>;
+  if (!reserve_lds((const void*)kern, lds))
+    return fail(KF_ELAUNCH, "G: cannot reserve %zu bytes of LDS", lds);
+  const int n_m = (int)(L.OUTP / BM), n_n = (int)((n_in + 31) / 32);
+  hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(512), lds, s, kb, (int)batch, (int)n_in, (int)n_out, (int)L.BP,
+                     (int)L.OUTP, zt, wt, (const T*)gt, colsum, (T*)dc);
+  return check_launch("G");
+}
+
+template <bool SKIP0>
+int launch_g96(const WsG& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out,
+               const float* zt, const float* wt, const void* gt, const float* colsum, void* dc) {
+  const size_t lds_ops = (size_t)2 * (192 * 64 + 8 * 48 * 64);
+  const size_t lds_red = (size_t)(8 * 32 * 49 + 32) * 4 + (size_t)32 * 48 * kb.K * 2;  // sums, output rows
+  const int vout = (n_in * kb.K * 2) % 16 == 0 && aligned16(dc);
+  const size_t lds = lds_ops > lds_red ? lds_ops : lds_red;
+  auto kern = g96_kernel<SKIP0>;
+  if (!reserve_lds((const void*)kern, lds))
+    return fail(KF_ELAUNCH, "G: cannot reserve %zu bytes of LDS", lds);
+  const int n_m = (int)(L.OUTP / 192), n_n = (int)(L.INP / 48);
+  const int skip = SKIP0 ? 1 : 0, n_run = kb.n_t - skip;
+  KFoldG fg;
+  for (int k = 0; k < KF_MAX_K; ++k) {
+    fg.v[k][0] = SKIP0 && k < kb.K ? kb.fold[k * KF_MAX_NT] : 0.f;
+    for (int f = 0; f < 8; ++f) fg.v[k][1 + f] = k < kb.K && f < n_run ? kb.fold[k * KF_MAX_NT + f + skip] : 0.f;
+  }
+  hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(512), lds, s, fg, kb.K, n_run, (int)batch, (int)n_in, (int)n_out,
+                     (int)L.BP, (int)L.OUTP, (int)L.INP, zt, wt, (const bf16*)gt, colsum, (bf16*)dc, vout);
+  return check_launch("G");
+}
+
+// G over precomputed B-spline features as p_dma_kernel's flat GEMM (identity fold).
+template <typename T>
+int launch_g_dma(const WsG& L, hipStream_t s, const KBasis& kb, int64_t n_in, int64_t n_out, const void* gt,
+                 const void* phit, void* dc) {
+  constexpr int FW = kGdmaFW, TM = p_dma_tm(FW), BM = 2 * TM * 32, EPS = 128 / (int)sizeof(T);
+  const size_t lds = (size_t)2 * (BM + 2 * FW * 32) * 128;
+  auto kern = p_dma_kernel<T, TM, FW, KF_KIND_BSPLINE, 1>;
+  if (L.INP % kGdmaRows || L.BP % EPS || L.BP / EPS < 1) return fail(KF_EINVAL, "G: workspace layout not aligned");
+  if (!reserve_lds((const void*)kern, lds))
+    return fail(KF_ELAUNCH, "G: cannot reserve %zu bytes of LDS", lds);
+  const int n_m = (int)((n_out + BM - 1) / BM), n_n = (int)(kb.n_t * L.INP / kGdmaRows);
+  hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(256), lds, s, kb, (int)n_out, (int)n_in, (int)L.INP, (int)L.BP,
+                     (const T*)nullptr, (const T*)gt, (int)L.BP, (const T*)phit, (T*)dc, (float*)nullptr);
+  return check_launch("G");
+}
+
+template <typename T>
+int run_G(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
+          const void* g, const void* w, void* dc, void* ws, hipStream_t s) {
+  const bool cheb_kind = kb.kind == KF_KIND_CHEB;
+  const bool weighted = features_weighted(b, w);
+  WsG L = ws_g(b, dtype, batch, n_in, n_out, weighted);
+  const bool cheb = cheb_kind && !L.pre;
+  char* base = (char*)ws;
+  void* gt = base;
+  float* zt = cheb ? (float*)(base + L.gt) : nullptr;
+  float* wt = cheb && weighted ? (float*)(base + L.gt + L.zt) : nullptr;
+  float* part = L.skip0 ? (float*)(base + L.gt + L.zt + L.wt) : nullptr;
+  float* colsum = L.skip0 ? (float*)(base + L.gt + L.zt + L.wt + L.part) : nullptr;
+  if (L.BP % 32 || !aligned16(gt)) return fail(KF_EINVAL, "G: workspace layout not aligned");
+  dim3 tg((unsigned)((L.OUTP + 63) / 64), (unsigned)((L.BP + 63) / 64));
+  hipLaunchKernelGGL(transpose_kernel<T>, tg, dim3(kThreads), 0, s, (int)batch, (int)n_out, (int)L.BP, (int)L.OUTP,
+                     (int)rows_vec<T>(n_out, g), (const T*)g, (T*)gt, part);
+  int rc = check_launch("transpose");
+  if (rc) return rc;
+  if (cheb) {
+    // block rows past the batch tiles total the column sums of g (skip0 implies cheb)
+    const unsigned gx = (unsigned)((L.INP + 63) / 64), sblocks = L.skip0 ? (unsigned)((L.OUTP + 7) / 8) : 0u;
+    dim3 zg(gx, (unsigned)((L.BP + 63) / 64) + (sblocks + gx - 1) / gx);
+    hipLaunchKernelGGL(zmapT_kernel<T>, zg, dim3(kThreads), (size_t)(wt ? 2 : 1) * 64 * 65 * sizeof(float), s,
+                       (int)batch, (int)n_in, (int)L.BP, (int)L.INP, kb.input_map,
+                       (int)(rows_vec<T>(n_in, x) && rows_vec<T>(n_in, w)), (const T*)x, (const T*)w, zt, wt,
+                       (int)((L.BP + 63) / 64), (int)L.OUTP, part, colsum);
+    rc = check_launch("zmapT");
+    if (rc) return rc;
+    if (L.g96) {
+      if (L.skip0) return launch_g96<true>(L, s, kb, batch, n_in, n_out, zt, wt, gt, colsum, dc);
+      return launch_g96<false>(L, s, kb, batch, n_in, n_out, zt, wt, gt, colsum, dc);
+    }
+    switch (L.cfg) {
+      case 0: return launch_g_ws<T, 2, 2, 128>(L, s, kb, batch, n_in, n_out, zt, wt, gt, colsum, dc);
+      case 1: return launch_g_ws<T, 2, 3, 128>(L, s, kb, batch, n_in, n_out, zt, wt, gt, colsum, dc);
+      case 2: return launch_g_ws<T, 2, 4, 128>(L, s, kb, batch, n_in, n_out, zt, wt, gt, colsum, dc);
+      case 3: return launch_g_ws<T, 2, 5, 128>(L, s, kb, batch, n_in, n_out, zt, wt, gt, colsum, dc);
+      case 4: return launch_g_ws<T, 2, 6, 128>(L, s, kb, batch, n_in, n_out, zt, wt, gt, colsum, dc);
+      case 5: return launch_g_ws<T, 1, 8, 64>(L, s, kb, batch, n_in, n_out, zt, wt, gt, colsum, dc);
+      default: return launch_g_ws<T, 1, 12, 64>(L, s, kb, batch, n_in, n_out, zt, wt, gt, colsum, dc);
+    }
+  }
+  // other kinds: features (times w) precomputed once into phiT[j][INP][BP]
+  void* phit = base + L.gt + L.zt + L.wt + L.part + L.colsum;
+  if constexpr (sizeof(T) == 2) {
+    // GR-KAN degrees in bf16: phi^(m)(x) w transposed to (in, BP), then the GEMM g^T phi over the batch
+    if (rational_fast(kb, n_in) && n_in % 64 == 0 && kb.order <= 2 && L.BP % 64 == 0 && aligned16(x) &&
+        (!w || aligned16(w))) {
+      auto mapt = kb.order == 0 ? rational_map_t_kernel<bf16, 0>
+                  : kb.order == 1 ? rational_map_t_kernel<bf16, 1>
+                                  : rational_map_t_kernel<bf16, 2>;
+      hipLaunchKernelGGL(mapt, dim3((unsigned)(n_in / 64), (unsigned)(L.BP / 64)), dim3(256), 0, s, kb, (int)batch,
+                         (int)n_in, (int)L.BP, (const bf16*)x, (const bf16*)w, (bf16*)phit);
+      rc = check_launch("rational features (transposed)");
+      if (rc) return rc;
+      void* gws = (char*)phit + L.phit + L.zpart;
+      return gemm_nt(n_out, n_in, L.BP, gt, L.BP, phit, L.BP, dc, n_in, false, gws, L.gemm, s);
+    }
+  }
+  float* zpart = L.nz > 1 ? (float*)((char*)phit + L.phit) : nullptr;
+  rc = launch_features_t<T>(kb, batch, n_in, L.BP, L.INP, x, w, phit, s);
+  if (rc) return rc;
+  if (L.gdma) return launch_g_dma<T>(L, s, kb, n_in, n_out, gt, phit, dc);
+  return launch_g_cfg<T, false>(L, s, kb, batch, n_in, n_out, phit, zpart, nullptr, nullptr, gt, dc);
+}
+}  // namespace
+
+extern "C" {
+
+int kf_G(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* g,
+         const void* w, void* dc, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err.clear();
+  int rc = validate_common(b, dtype, batch, n_in, n_out);
+  if (rc) return rc;
+  if (n_in == 0 || n_out == 0) return KF_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const long n = (long)n_out * n_in * b->size;
+  if (batch == 0) return dtype == KF_BF16 ? zero_fill<bf16>(dc, n, s) : zero_fill<float>(dc, n, s);
+  if (!x || !g || !dc) return fail(KF_EINVAL, "kf_G: NULL array");
+  size_t need = ws_g(b, dtype, batch, n_in, n_out, features_weighted(b, w)).total;
+  if (!workspace || workspace_bytes < need)
+    return fail(KF_EWORKSPACE, "kf_G: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  if (reinterpret_cast<uintptr_t>(workspace) & 255)
+    return fail(KF_EWORKSPACE, "kf_G: workspace must be 256-byte aligned");
+  KBasis kb = to_kbasis(b);
+  if (dtype == KF_BF16) return run_G<bf16>(kb, b, dtype, batch, n_in, n_out, x, g, w, dc, workspace, s);
+  return run_G<float>(kb, b, dtype, batch, n_in, n_out, x, g, w, dc, workspace, s);
+}
+
+}  // extern "C"

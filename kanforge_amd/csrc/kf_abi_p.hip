@@ -1,0 +1,176 @@
+// kf_P (include/kfhip.h): the input-gradient contraction's launch configurations, workspace
+// carving and dispatch.
+#include "kf_abi.h"
+#include "kf_rational.h"
+
+using namespace kfabi;
+
+namespace {
+
+template <typename T, int WMW, int WJW, int TM, int FW, int KIND>
+int launch_p_kind(const WsP& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out,
+                  const void* x, const void* g, const void* cfmt, void* p, float* h) {
+  constexpr int BM = WMW * TM * 32, NMAX = WJW * FW * 32, RS = 64 + 16;
+  const size_t lds_ops = (size_t)2 * (BM + NMAX) * RS, lds_red = (size_t)WJW * BM * 33 * 4;
+  const size_t lds = lds_ops > lds_red ? lds_ops : lds_red;
+  auto kern = p_kernel<T, WMW, WJW, TM, FW, KIND>;
+  if (!reserve_lds((const void*)kern, lds))
+    return fail(KF_ELAUNCH, "P: cannot reserve %zu bytes of LDS", lds);
+  const int n_m = (int)((batch + BM - 1) / BM), n_n = (int)(L.INP / 32);
+  hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(WMW * WJW * 64), lds, s, kb, (int)batch, (int)n_in, (int)n_out,
+                     (int)L.INP, (int)L.OUTP, (const T*)x, (const T*)g, (const T*)cfmt, (T*)p, h);
+  return check_launch("P");
+}
+
+template <typename T, int WMW, int WJW, int TM, int FW>
+int launch_p_t(const WsP& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out,
+               const void* x, const void* g, const void* cfmt, void* p, float* h) {
+  switch (kb.kind) {
+    case KF_KIND_CHEB:
+      return launch_p_kind<T, WMW, WJW, TM, FW, KF_KIND_CHEB>(L, s, kb, batch, n_in, n_out, x, g, cfmt, p, h);
+    case KF_KIND_BSPLINE:
+      return launch_p_kind<T, WMW, WJW, TM, FW, KF_KIND_BSPLINE>(L, s, kb, batch, n_in, n_out, x, g, cfmt, p, h);
+    default:
+      return launch_p_kind<T, WMW, WJW, TM, FW, KF_KIND_RATIONAL>(L, s, kb, batch, n_in, n_out, x, g, cfmt, p, h);
+  }
+}
+
+template <typename T, int FW, int KIND>
+int launch_p_dma_kind(const WsP& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, const void* x,
+                      const void* g, int gstride, const void* cfmt, void* p, float* h) {
+  constexpr int TM = p_dma_tm(FW), BM = 2 * TM * 32;
+  const size_t knots = KIND == KF_KIND_BSPLINE ? (size_t)32 * (2 * kb.n_knots + 2 * kb.spline_k) * 4 : 0;
+  size_t lds_epi = (size_t)3 * BM * 33 * 4 + knots;
+  if (KIND == KF_KIND_BSPLINE) {  // x, knots, then the features of one pass or the group sums
+    const size_t fb = (size_t)2 * FW * 64 * 33 * 4, red = (size_t)2 * BM * 33 * 4;
+    lds_epi = (size_t)BM * 33 * 4 + knots + (fb > red ? fb : red);
+  }
+  const size_t lds_ops = (size_t)2 * (BM + 2 * FW * 32) * 128;
+  const size_t lds = lds_ops > lds_epi ? lds_ops : lds_epi;
+  auto kern = p_dma_kernel<T, TM, FW, KIND>;
+  if (!reserve_lds((const void*)kern, lds))
+    return fail(KF_ELAUNCH, "P: cannot reserve %zu bytes of LDS", lds);
+  constexpr int TI = KIND == KF_KIND_RATIONAL ? 64 * FW : 32;  // inputs per tile (flat for rational)
+  if (L.INP % TI) return fail(KF_EINVAL, "P: workspace layout not aligned");
+  const int n_m = (int)((batch + BM - 1) / BM), n_n = (int)(L.INP / TI);
+  hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(256), lds, s, kb, (int)batch, (int)n_in, (int)L.INP, (int)L.OUTP,
+                     (const T*)x, (const T*)g, gstride, (const T*)cfmt, (T*)p, h);
+  return check_launch("P");
+}
+
+template <int TN, int RB>
+int launch_p8(const WsP& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, const void* x, const void* g,
+              int gstride, const void* cfmt, void* p) {
+  constexpr int TI = 16 * TN, RPASS = TN == 2 ? 128 : 64;
+  const size_t lds_ops = (size_t)2 * (256 + 8 * TI) * RB, lds_epi = (size_t)8 * RPASS * (TI + 1) * 4;
+  const size_t lds = lds_ops > lds_epi ? lds_ops : lds_epi;
+  auto kern = p8_kernel<KF_KIND_CHEB, TN, RB>;
+  if (L.INP % TI || L.OUTP % (RB / 2)) return fail(KF_EINVAL, "P: workspace layout not aligned");
+  if (!reserve_lds((const void*)kern, lds))
+    return fail(KF_ELAUNCH, "P: cannot reserve %zu bytes of LDS", lds);
+  const int n_m = (int)((batch + 255) / 256), n_n = (int)(L.INP / TI);
+  hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(512), lds, s, kb, (int)batch, (int)n_in, (int)L.INP, (int)L.OUTP,
+                     (const bf16*)x, (const bf16*)g, gstride, (const bf16*)cfmt, (bf16*)p);
+  return check_launch("P");
+}
+
+template <typename T, int FW>
+int launch_p_dma(const WsP& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, const void* x,
+                 const void* g, int gstride, const void* cfmt, void* p, float* h) {
+  switch (kb.kind) {
+    case KF_KIND_CHEB:
+      return launch_p_dma_kind<T, FW, KF_KIND_CHEB>(L, s, kb, batch, n_in, x, g, gstride, cfmt, p, h);
+    case KF_KIND_BSPLINE:
+      return launch_p_dma_kind<T, FW, KF_KIND_BSPLINE>(L, s, kb, batch, n_in, x, g, gstride, cfmt, p, h);
+    default:
+      return launch_p_dma_kind<T, FW, KF_KIND_RATIONAL>(L, s, kb, batch, n_in, x, g, gstride, cfmt, p, h);
+  }
+}
+
+template <typename T>
+int run_P(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
+          const void* g, const void* c, void* p, float* h, void* ws, hipStream_t s) {
+  WsP L = ws_p(b, dtype, batch, n_in, n_out);
+  void* cfmt = ws;
+  int rc = launch_permute<T>(kb, n_out, n_in, L.OUTP, L.INP, L.ntb, c, cfmt, kPermFMT, s);
+  if (rc) return rc;
+  if (p_uses_dma(L.cfg)) {
+    const void* ga = g;
+    int gstride = (int)n_out;
+    if (p_needs_gpad(n_out, dtype) || (reinterpret_cast<uintptr_t>(g) & 15) != 0) {
+      if (!L.gpad) return fail(KF_EINVAL, "P: g must be 16-byte aligned");
+      void* gp = (char*)ws + L.cfmt;
+      long n = (long)batch * L.OUTP;
+      long blocks = (n + kThreads - 1) / kThreads;
+      if (blocks > 65535 * 4) blocks = 65535 * 4;
+      hipLaunchKernelGGL(pad_cols_kernel<T>, dim3((unsigned)blocks), dim3(kThreads), 0, s, (int)batch, (int)n_out,
+                         (int)L.OUTP, (const T*)g, (T*)gp);
+      rc = check_launch("pad_cols");
+      if (rc) return rc;
+      ga = gp;
+      gstride = (int)L.OUTP;
+    }
+    if constexpr (sizeof(T) == 2) {
+      // GR-KAN degrees in bf16: H = g C^T on the GEMM core (float32, into h when given), then
+      // p = H phi^(m)(x)
+      if (rational_fast(kb, n_in) && kb.order <= 2 && aligned16(x) && aligned16(p) && aligned16(ga) && gstride % 8 == 0) {
+        float* hb = h ? h : (float*)((char*)ws + L.cfmt + L.gpad);
+        void* gws = (char*)ws + L.cfmt + L.gpad + L.hbuf;
+        rc = gemm_nt(batch, n_in, L.OUTP, ga, gstride, cfmt, L.OUTP, hb, n_in, true, gws, L.gemm, s);
+        if (rc) return rc;
+        long blocks = ((long)batch * (n_in / 8) + 255) / 256;
+        if (blocks > 65535 * 4) blocks = 65535 * 4;
+        auto map = kb.order == 0   ? rational_map_kernel<bf16, bf16, 0>
+                   : kb.order == 1 ? rational_map_kernel<bf16, bf16, 1>
+                                   : rational_map_kernel<bf16, bf16, 2>;
+        hipLaunchKernelGGL(map, dim3((unsigned)blocks), dim3(256), 0, s, kb, (int)batch, (int)n_in, (const bf16*)x,
+                           (const bf16*)nullptr, (const float*)hb, (bf16*)p);
+        return check_launch("rational dX");
+      }
+    }
+    // 7 or 8 Chebyshev features in bf16: the two-waves-per-SIMD kernel
+    if (L.p8 && !h) return launch_p8<3, 128>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p);
+    switch (L.cfg) {
+      case 0: return launch_p_dma<T, 2>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p, h);
+      case 1: return launch_p_dma<T, 3>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p, h);
+      case 2: return launch_p_dma<T, 4>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p, h);
+      case 3: return launch_p_dma<T, 5>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p, h);
+      default: return launch_p_dma<T, 6>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p, h);
+    }
+  }
+  switch (L.cfg) {
+    case 3: return launch_p_t<T, 4, 2, 2, 5>(L, s, kb, batch, n_in, n_out, x, g, cfmt, p, h);
+    case 4: return launch_p_t<T, 4, 2, 1, 6>(L, s, kb, batch, n_in, n_out, x, g, cfmt, p, h);
+    case 5: return launch_p_t<T, 4, 2, 1, 8>(L, s, kb, batch, n_in, n_out, x, g, cfmt, p, h);
+    default: return launch_p_t<T, 4, 2, 1, 12>(L, s, kb, batch, n_in, n_out, x, g, cfmt, p, h);
+  }
+}
+}  // namespace
+
+extern "C" {
+
+int kf_P(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* g,
+         const void* c, void* p, float* h, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err.clear();
+  int rc = validate_common(b, dtype, batch, n_in, n_out);
+  if (rc) return rc;
+  if (batch == 0 || n_in == 0) return KF_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (n_out == 0) {
+    rc = dtype == KF_BF16 ? zero_fill<bf16>(p, (long)batch * n_in, s) : zero_fill<float>(p, (long)batch * n_in, s);
+    if (rc == KF_OK && h) rc = zero_fill<float>(h, (long)batch * n_in, s);
+    return rc;
+  }
+  if (!x || !g || !c || !p) return fail(KF_EINVAL, "kf_P: NULL array");
+  if (h && b->kind != KF_KIND_RATIONAL) return fail(KF_EINVAL, "kf_P: h output is for the rational kind");
+  size_t need = ws_p(b, dtype, batch, n_in, n_out).total;
+  if (!workspace || workspace_bytes < need)
+    return fail(KF_EWORKSPACE, "kf_P: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  if (reinterpret_cast<uintptr_t>(workspace) & 255)
+    return fail(KF_EWORKSPACE, "kf_P: workspace must be 256-byte aligned");
+  KBasis kb = to_kbasis(b);
+  if (dtype == KF_BF16) return run_P<bf16>(kb, b, dtype, batch, n_in, n_out, x, g, c, p, h, workspace, s);
+  return run_P<float>(kb, b, dtype, batch, n_in, n_out, x, g, c, p, h, workspace, s);
+}
+
+}  // extern "C"

@@ -30,6 +30,7 @@ struct KBasis {
   const float* knots_cmp;
   const float* num;
   const float* den;
+  const float* knots_uniform;        // (t_0, 1 / h) per input when every input's knots are even
   float fold[KF_MAX_K * KF_MAX_NT];  // R_m, K x n_t row-major (cheb)
 };
 
@@ -214,10 +215,80 @@ __device__ inline void bspline_features_rows(float x, float w, const float* kc, 
   }
 }
 
+// The same features for an input whose real knots t_0 .. t_{nk-1} are evenly spaced by h = 1 / ih.
+// Interval: the affine estimate floor((x - t_0) ih), moved until kc[j] <= x < kc[j + 1] holds on
+// the exact comparison knots (the estimate is off by at most one), so j is the one the general
+// search finds. Values: Cox-de Boor in u = (x - t_j) ih, where every knot difference is a whole
+// number of steps, so each term is a multiply by a constant; a derivative step multiplies by ih.
+template <int KM, int KD>
+__device__ inline void bspline_features_uniform(float x, float w, const float* kc, const float* kp0, float t0,
+                                                float ih, const KBasis& b, float* phi) {
+#pragma unroll
+  for (int s = 0; s < KM; ++s) phi[s] = 0.f;
+  const int nk = b.n_knots, m = b.order;
+  if (m > KD) return;
+  if (!__builtin_isfinite(x) || x < kc[0] || x >= kc[nk - 1]) {
+    if (!__builtin_isfinite(x)) {
+#pragma unroll
+      for (int s = 0; s < KM; ++s) phi[s] = (s < b.K) ? __builtin_nanf("") : 0.f;
+    }
+    return;
+  }
+  int j = (int)floorf((x - t0) * ih);
+  j = j < 0 ? 0 : (j > nk - 2 ? nk - 2 : j);
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    if (x < kc[j]) --j;
+    else if (x >= kc[j + 1]) ++j;
+  }
+  if (!(kc[j] <= x && x < kc[j + 1])) j = bspline_interval(x, kc, nk);  // never taken for even knots
+  const float u = (x - kp0[j + KD]) * ih;
+  // N[r] = B_{q, j-q+r}: with s = j-q+r, (x - t_s) / (t_{s+q} - t_s) = (u + q - r) / q and
+  // (t_{s+q+1} - x) / (t_{s+q+1} - t_{s+1}) = (r + 1 - u) / q
+  float N[KD + 1];
+  N[0] = 1.f;
+#pragma unroll
+  for (int r = 1; r <= KD; ++r) N[r] = 0.f;
+  const int deg = KD - m;
+#pragma unroll
+  for (int q = 1; q <= KD; ++q) {
+    float nn[KD + 1];
+    const float iq = 1.f / (float)q;
+#pragma unroll
+    for (int r = 0; r <= KD; ++r) nn[r] = 0.f;
+#pragma unroll
+    for (int r = 0; r <= q; ++r) {
+      const float left = (r >= 1) ? N[r - 1] : 0.f;
+      const float right = (r <= q - 1) ? N[r] : 0.f;
+      if (q <= deg)
+        nn[r] = ((u + (float)(q - r)) * left + ((float)(r + 1) - u) * right) * iq;
+      else
+        nn[r] = (left - right) * ih;
+    }
+#pragma unroll
+    for (int r = 0; r <= KD; ++r) N[r] = nn[r];
+  }
+  const int base = j - KD;
+#pragma unroll
+  for (int s = 0; s < KM; ++s) {
+    const int r = s - base;
+    float v = 0.f;
+#pragma unroll
+    for (int rr = 0; rr <= KD; ++rr) v = (rr == r) ? N[rr] : v;
+    phi[s] = (s < b.K) ? w * v : 0.f;
+  }
+}
+
 template <int KM, int KD>
 __device__ inline void bspline_features(float x, float w, int i, const KBasis& b, float* phi) {
   const int nk = b.n_knots;
-  bspline_features_rows<KM, KD>(x, w, b.knots_cmp + (size_t)i * nk, b.knots + (size_t)i * (nk + 2 * KD), b, phi);
+  const float* kc = b.knots_cmp + (size_t)i * nk;
+  const float* kp = b.knots + (size_t)i * (nk + 2 * KD);
+  if (b.knots_uniform) {
+    bspline_features_uniform<KM, KD>(x, w, kc, kp, b.knots_uniform[2 * i], b.knots_uniform[2 * i + 1], b, phi);
+    return;
+  }
+  bspline_features_rows<KM, KD>(x, w, kc, kp, b, phi);
 }
 
 // ---------------------------------------------------------------------------
@@ -316,10 +387,21 @@ __device__ inline float rational_feature(float x, int i, const KBasis& b, int m)
   return out[m < 8 ? m : 8];
 }
 
-// Degree dispatch with the knot rows given (degrees 0..5 are compiled).
+// Degree dispatch with the knot rows of input i given (degrees 0..5 are compiled).
 template <int KM>
 __device__ inline void bspline_dispatch_rows(float x, float w, const float* kc, const float* kp0, const KBasis& b,
-                                             float* phi) {
+                                             float* phi, int i) {
+  if (b.knots_uniform) {
+    const float t0 = b.knots_uniform[2 * i], ih = b.knots_uniform[2 * i + 1];
+    switch (b.spline_k) {
+      case 0: bspline_features_uniform<KM, 0>(x, w, kc, kp0, t0, ih, b, phi); return;
+      case 1: bspline_features_uniform<KM, 1>(x, w, kc, kp0, t0, ih, b, phi); return;
+      case 2: bspline_features_uniform<KM, 2>(x, w, kc, kp0, t0, ih, b, phi); return;
+      case 3: bspline_features_uniform<KM, 3>(x, w, kc, kp0, t0, ih, b, phi); return;
+      case 4: bspline_features_uniform<KM, 4>(x, w, kc, kp0, t0, ih, b, phi); return;
+      default: bspline_features_uniform<KM, 5>(x, w, kc, kp0, t0, ih, b, phi); return;
+    }
+  }
   switch (b.spline_k) {
     case 0: bspline_features_rows<KM, 0>(x, w, kc, kp0, b, phi); break;
     case 1: bspline_features_rows<KM, 1>(x, w, kc, kp0, b, phi); break;

@@ -973,7 +973,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_J * 64) void g_kernel(KBasis bs, int
 // part[0][t] = sum_z part[z][t] over the flat (o, i, j) index t: the batch
 // splits of g_kernel summed in a fixed order (deterministic), consecutive
 // threads reading consecutive floats of every split.
-__global__ __launch_bounds__(kThreads) void g_split_sum(long n, int nz, size_t zstride, float* __restrict__ part) {
+static __global__ __launch_bounds__(kThreads) void g_split_sum(long n, int nz, size_t zstride, float* __restrict__ part) {
   for (long t = blockIdx.x * (long)kThreads + threadIdx.x; t < n; t += (long)gridDim.x * kThreads) {
     float sum = 0.f;
     for (int z = 0; z < nz; ++z) sum += part[(size_t)z * zstride + t];
@@ -1064,7 +1064,8 @@ __global__ __launch_bounds__(kThreads) void features_t_kernel(KBasis bs, int B, 
     const float wv = ok ? (w ? to_f32(w[(size_t)b * IN + i]) : 1.f) : 0.f;
     float f[NTB];
     if (bspl)
-      bspline_dispatch_rows<NTB>(xv, wv, kcs + il * bs.n_knots, kps + il * (bs.n_knots + 2 * bs.spline_k), bs, f);
+      bspline_dispatch_rows<NTB>(xv, wv, kcs + il * bs.n_knots, kps + il * (bs.n_knots + 2 * bs.spline_k), bs, f,
+                                 ok ? i : 0);
     else
       kernel_features<NTB>(xv, wv, ok ? i : 0, bs, f);
 #pragma unroll
@@ -1619,7 +1620,8 @@ __global__ __launch_bounds__(256) void p_dma_kernel(KBasis bs, int B, int IN, in
         const int row = (rowp / 32) * WM + a * 32 + rowp % 32;
         const bool ok = b0 + row < B && i0 + il < IN;
         float f[NTB];
-        bspline_dispatch_rows<NTB>(xsb[row * 33 + il], 1.f, kcb + il * bs.n_knots, kpb + il * np, bs, f);
+        bspline_dispatch_rows<NTB>(xsb[row * 33 + il], 1.f, kcb + il * bs.n_knots, kpb + il * np, bs, f,
+                                   i0 + il < IN ? i0 + il : 0);
 #pragma unroll
         for (int j = 0; j < NTB; ++j)
           if (j < n_t) fb[(j * 64 + rowp) * 33 + il] = ok ? f[j] : 0.f;
@@ -1690,7 +1692,7 @@ __global__ __launch_bounds__(256) void p_dma_kernel(KBasis bs, int B, int IN, in
         float f[NTB];
         if constexpr (KIND == KF_KIND_BSPLINE)
           bspline_dispatch_rows<NTB>(xs[row * 33 + l32], 1.f, kcs + l32 * bs.n_knots,
-                                     kps + l32 * (bs.n_knots + 2 * bs.spline_k), bs, f);
+                                     kps + l32 * (bs.n_knots + 2 * bs.spline_k), bs, f, i);
         else
           kind_features<KIND, NTB>(xs[row * 33 + l32], 1.f, i, bs, f);
 #pragma unroll
@@ -2406,7 +2408,7 @@ __global__ __launch_bounds__(kThreads) void edge_kernel(KBasis bs, int B, int IN
 }
 
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kThreads) void interval_kernel(long n, int IN, const float* __restrict__ x,
+static __global__ __launch_bounds__(kThreads) void interval_kernel(long n, int IN, const float* __restrict__ x,
                                                             const float* __restrict__ kc, int nk,
                                                             int32_t* __restrict__ idx) {
   for (long e = blockIdx.x * (long)kThreads + threadIdx.x; e < n; e += (long)gridDim.x * kThreads) {
@@ -2484,7 +2486,7 @@ __global__ __launch_bounds__(kThreads) void rational_grad_partial(KBasis bs, int
     if (q < nQ) block_sum(accQ[q], nP + q);
 }
 
-__global__ void rational_grad_final(int groups, int nP, int nQ, int n_chunks, const float* __restrict__ part,
+static __global__ void rational_grad_final(int groups, int nP, int nQ, int n_chunks, const float* __restrict__ part,
                                     float* __restrict__ dnum, float* __restrict__ dden) {
   const int np = nP + nQ;
   for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < groups * np; e += gridDim.x * blockDim.x) {

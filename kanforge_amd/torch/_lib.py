@@ -35,6 +35,7 @@ EXPORTS = (
     "kf_bspline_interval",
     "kf_rational_workspace_bytes",
     "kf_rational_param_grad",
+    "kf_probe_mfma",
     "kf_last_error",
     "kf_version",
 )
@@ -57,6 +58,7 @@ class KfBasis(ctypes.Structure):
         ("knots_cmp", c_void_p),
         ("num", c_void_p),
         ("den", c_void_p),
+        ("knots_uniform", c_void_p),
     ]
 
 
@@ -94,6 +96,8 @@ def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
         lib.kf_rational_param_grad.argtypes = [P, c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]
         for name in ("kf_F", "kf_F_noalloc", "kf_G", "kf_P", "kf_features", "kf_edge_derivative", "kf_bspline_interval", "kf_rational_param_grad"):
             getattr(lib, name).restype = c_int
+        lib.kf_probe_mfma.argtypes = [c_int, c_int, c_int, c_void_p, c_void_p]
+        lib.kf_probe_mfma.restype = c_int
         lib.kf_last_error.argtypes = []
         lib.kf_last_error.restype = c_char_p
         lib.kf_version.argtypes = []

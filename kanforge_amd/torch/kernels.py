@@ -69,27 +69,34 @@ def _stream(device: torch.device):
 class BasisState:
     """Device tables a plan needs besides x and the coefficients.
 
-    bspline: ``knots`` (in, nk + 2k) and ``knots_cmp`` (in, nk) float32;
+    bspline: ``knots`` (in, nk + 2k) and ``knots_cmp`` (in, nk) float32, and ``knots_u`` (in, 2)
+    ``(t_0, 1/h)`` when every input's knots are evenly spaced (else None);
     rational: ``num`` (groups, p+1), ``den`` (groups, q) float32 and the group size.
     """
 
-    __slots__ = ("knots", "knots_cmp", "num", "den", "group_size")
+    __slots__ = ("knots", "knots_cmp", "knots_u", "num", "den", "group_size")
 
-    def __init__(self, knots=None, knots_cmp=None, num=None, den=None, group_size=1):
-        self.knots, self.knots_cmp = knots, knots_cmp
+    def __init__(self, knots=None, knots_cmp=None, num=None, den=None, group_size=1, knots_u=None):
+        self.knots, self.knots_cmp, self.knots_u = knots, knots_cmp, knots_u
         self.num, self.den, self.group_size = num, den, int(group_size)
 
     def with_params(self, num, den) -> "BasisState":
-        return BasisState(self.knots, self.knots_cmp, num, den, self.group_size)
+        return BasisState(self.knots, self.knots_cmp, num, den, self.group_size, self.knots_u)
 
 
 def bspline_state(grid: torch.Tensor, order: int) -> BasisState:
     """Knot tables of a per-input grid buffer (host float64 preparation)."""
-    from ..bases.spline import knot_tables
+    from ..bases.spline import knot_tables, uniform_table
 
-    pad, cmp_ = knot_tables(grid.detach().double().cpu().numpy(), order)
+    g = grid.detach().double().cpu().numpy()
+    pad, cmp_ = knot_tables(g, order)
+    uni = uniform_table(g, order)
     dev = grid.device
-    return BasisState(knots=torch.from_numpy(pad).to(dev), knots_cmp=torch.from_numpy(cmp_).to(dev))
+    return BasisState(
+        knots=torch.from_numpy(pad).to(dev),
+        knots_cmp=torch.from_numpy(cmp_).to(dev),
+        knots_u=None if uni is None else torch.from_numpy(uni).to(dev),
+    )
 
 
 def rational_state(num: torch.Tensor, den: torch.Tensor, group_size: int) -> BasisState:
@@ -124,6 +131,7 @@ def _desc(plan: KernelPlan, m: int, st: BasisState | None):
         d.n_knots = g + 2 * k + 1
         d.knots = st.knots.data_ptr()
         d.knots_cmp = st.knots_cmp.data_ptr()
+        d.knots_uniform = None if st.knots_u is None else st.knots_u.data_ptr()
     else:
         p, q = plan.consts
         d.order = m
@@ -239,19 +247,19 @@ def plan_of(key: str) -> KernelPlan:
     return KernelPlan(kind, cst, int(size), fk, bool(int(grid)))
 
 
-def _state(knots, knots_cmp, num, den, n_in: int) -> BasisState | None:
+def _state(knots, knots_cmp, knots_u, num, den, n_in: int) -> BasisState | None:
     if knots is not None:
-        return BasisState(knots=knots, knots_cmp=knots_cmp)
+        return BasisState(knots=knots, knots_cmp=knots_cmp, knots_u=knots_u)
     if num is not None:
         return rational_state(num, den, n_in // num.shape[0])
     return None
 
 
 def _tables(st: BasisState | None):
-    """(knots, knots_cmp) of a state, for the op arguments."""
+    """(knots, knots_cmp, knots_u) of a state, for the op arguments."""
     if st is None or st.knots is None:
-        return None, None
-    return st.knots, st.knots_cmp
+        return None, None, None
+    return st.knots, st.knots_cmp, st.knots_u
 
 
 Opt = Optional[torch.Tensor]
@@ -262,21 +270,21 @@ def _mul(w, t):
 
 
 @torch.library.custom_op("kf::F", mutates_args=())
-def op_F(x: torch.Tensor, w: Opt, c: torch.Tensor, knots: Opt, knots_cmp: Opt, num: Opt, den: Opt, plan: str, m: int) -> torch.Tensor:
+def op_F(x: torch.Tensor, w: Opt, c: torch.Tensor, knots: Opt, knots_cmp: Opt, knots_u: Opt, num: Opt, den: Opt, plan: str, m: int) -> torch.Tensor:
     """y[b,o] = sum_{i,k} w[b,i] c[o,i,k] phi_k^(m)(x[b,i])."""
-    return _raw("F", plan_of(plan), m, x, w, c, _state(knots, knots_cmp, num, den, x.shape[1]), c.shape[0])
+    return _raw("F", plan_of(plan), m, x, w, c, _state(knots, knots_cmp, knots_u, num, den, x.shape[1]), c.shape[0])
 
 
 @torch.library.custom_op("kf::G", mutates_args=())
-def op_G(x: torch.Tensor, g: torch.Tensor, w: Opt, knots: Opt, knots_cmp: Opt, num: Opt, den: Opt, plan: str, m: int) -> torch.Tensor:
+def op_G(x: torch.Tensor, g: torch.Tensor, w: Opt, knots: Opt, knots_cmp: Opt, knots_u: Opt, num: Opt, den: Opt, plan: str, m: int) -> torch.Tensor:
     """dc[o,i,k] = sum_b w[b,i] g[b,o] phi_k^(m)(x[b,i])."""
-    return _raw("G", plan_of(plan), m, x, w, g, _state(knots, knots_cmp, num, den, x.shape[1]), g.shape[1])
+    return _raw("G", plan_of(plan), m, x, w, g, _state(knots, knots_cmp, knots_u, num, den, x.shape[1]), g.shape[1])
 
 
 @torch.library.custom_op("kf::P", mutates_args=())
-def op_P(x: torch.Tensor, g: torch.Tensor, c: torch.Tensor, knots: Opt, knots_cmp: Opt, num: Opt, den: Opt, plan: str, m: int) -> torch.Tensor:
+def op_P(x: torch.Tensor, g: torch.Tensor, c: torch.Tensor, knots: Opt, knots_cmp: Opt, knots_u: Opt, num: Opt, den: Opt, plan: str, m: int) -> torch.Tensor:
     """p[b,i] = sum_{o,k} g[b,o] c[o,i,k] phi_k^(m)(x[b,i])."""
-    return _raw("P", plan_of(plan), m, x, g, c, _state(knots, knots_cmp, num, den, x.shape[1]), c.shape[0])
+    return _raw("P", plan_of(plan), m, x, g, c, _state(knots, knots_cmp, knots_u, num, den, x.shape[1]), c.shape[0])
 
 
 @torch.library.custom_op("kf::rational_bwd", mutates_args=())
@@ -286,7 +294,7 @@ def op_rational_bwd(
     """(P_1(x, g, c), d/dnum, d/dden) of sum_{b,o} g[b,o] F_0(x, c, w)[b,o] for a rational plan:
     one P launch that also writes h = sum_o g c, then the parameter-gradient reduction."""
     pl = plan_of(plan)
-    st = _state(None, None, num, den, x.shape[1])
+    st = _state(None, None, None, num, den, x.shape[1])
     h = torch.empty(x.shape, dtype=torch.float32, device=x.device)
     p1 = _raw("P", pl, 1, x, g, c, st, c.shape[0], h=h)
     dnum, dden = _rational_param_grad(pl, st, x, h, w)
@@ -296,23 +304,23 @@ def op_rational_bwd(
 @torch.library.custom_op("kf::rational_param_grad", mutates_args=())
 def op_rational_param_grad(x: torch.Tensor, h: torch.Tensor, w: Opt, num: torch.Tensor, den: torch.Tensor, plan: str) -> tuple[torch.Tensor, torch.Tensor]:
     """(d/dnum, d/dden) of sum_{b,i} h[b,i] w[b,i] phi(x[b,i]) for a rational plan."""
-    st = _state(None, None, num, den, x.shape[1])
+    st = _state(None, None, None, num, den, x.shape[1])
     dnum, dden = _rational_param_grad(plan_of(plan), st, x, h.float().contiguous(), w)
     return dnum.to(num.dtype), dden.to(den.dtype)
 
 
 @op_F.register_fake
-def _(x, w, c, knots, knots_cmp, num, den, plan, m):
+def _(x, w, c, knots, knots_cmp, knots_u, num, den, plan, m):
     return x.new_empty(x.shape[0], c.shape[0])
 
 
 @op_G.register_fake
-def _(x, g, w, knots, knots_cmp, num, den, plan, m):
+def _(x, g, w, knots, knots_cmp, knots_u, num, den, plan, m):
     return x.new_empty(g.shape[1], x.shape[1], plan_of(plan).size)
 
 
 @op_P.register_fake
-def _(x, g, c, knots, knots_cmp, num, den, plan, m):
+def _(x, g, c, knots, knots_cmp, knots_u, num, den, plan, m):
     return x.new_empty(x.shape)
 
 
@@ -332,18 +340,18 @@ def _save(ctx, tensors, plan, m):
 
 
 def _F_setup(ctx, inputs, output):
-    x, w, c, knots, knots_cmp, num, den, plan, m = inputs
-    _save(ctx, (x, w, c, knots, knots_cmp, num, den), plan, m)
+    x, w, c, knots, knots_cmp, knots_u, num, den, plan, m = inputs
+    _save(ctx, (x, w, c, knots, knots_cmp, knots_u, num, den), plan, m)
 
 
 def _F_backward(ctx, gy):
-    x, w, c, knots, knots_cmp, num, den = ctx.saved_tensors
+    x, w, c, knots, knots_cmp, knots_u, num, den = ctx.saved_tensors
     plan, m = ctx.plan, ctx.m
     need = ctx.needs_input_grad
     gx = gw = gc = gnum = gden = None
     gy = gy.contiguous()
-    tabs = (knots, knots_cmp, num, den)
-    if plan_of(plan).kind == "rational" and (need[5] or need[6]):
+    tabs = (knots, knots_cmp, knots_u, num, den)
+    if plan_of(plan).kind == "rational" and (need[6] or need[7]):
         if m != 0:
             raise NotImplementedError("rational parameter gradients of derivative features are not compiled into the HIP kernels")
         p1, gnum, gden = op_rational_bwd(x, gy, c, w, num, den, plan)
@@ -356,45 +364,45 @@ def _F_backward(ctx, gy):
         gc = op_G(x, gy, w, *tabs, plan, m)
     if need[1]:
         gw = op_P(x, gy, c, *tabs, plan, m)
-    return gx, gw, gc, None, None, gnum, gden, None, None
+    return gx, gw, gc, None, None, None, gnum, gden, None, None
 
 
 def _G_setup(ctx, inputs, output):
-    x, g, w, knots, knots_cmp, num, den, plan, m = inputs
-    _save(ctx, (x, g, w, knots, knots_cmp, num, den), plan, m)
+    x, g, w, knots, knots_cmp, knots_u, num, den, plan, m = inputs
+    _save(ctx, (x, g, w, knots, knots_cmp, knots_u, num, den), plan, m)
 
 
 def _G_backward(ctx, gdc):
-    x, g, w, knots, knots_cmp, num, den = ctx.saved_tensors
+    x, g, w, knots, knots_cmp, knots_u, num, den = ctx.saved_tensors
     plan, m = ctx.plan, ctx.m
     need = ctx.needs_input_grad
-    if need[5] or need[6]:
+    if need[6] or need[7]:
         raise NotImplementedError("second-order rational parameter gradients are not compiled into the HIP kernels")
     gdc = gdc.contiguous()
-    tabs = (knots, knots_cmp, num, den)
+    tabs = (knots, knots_cmp, knots_u, num, den)
     gx = _mul(w, op_P(x, g, gdc, *tabs, plan, m + 1)) if need[0] else None
     gg = op_F(x, w, gdc, *tabs, plan, m) if need[1] else None
     gw = op_P(x, g, gdc, *tabs, plan, m) if need[2] else None
-    return gx, gg, gw, None, None, None, None, None, None
+    return gx, gg, gw, None, None, None, None, None, None, None
 
 
 def _P_setup(ctx, inputs, output):
-    x, g, c, knots, knots_cmp, num, den, plan, m = inputs
-    _save(ctx, (x, g, c, knots, knots_cmp, num, den), plan, m)
+    x, g, c, knots, knots_cmp, knots_u, num, den, plan, m = inputs
+    _save(ctx, (x, g, c, knots, knots_cmp, knots_u, num, den), plan, m)
 
 
 def _P_backward(ctx, gp):
-    x, g, c, knots, knots_cmp, num, den = ctx.saved_tensors
+    x, g, c, knots, knots_cmp, knots_u, num, den = ctx.saved_tensors
     plan, m = ctx.plan, ctx.m
     need = ctx.needs_input_grad
-    if need[5] or need[6]:
+    if need[6] or need[7]:
         raise NotImplementedError("second-order rational parameter gradients are not compiled into the HIP kernels")
     gp = gp.contiguous()
-    tabs = (knots, knots_cmp, num, den)
+    tabs = (knots, knots_cmp, knots_u, num, den)
     gx = gp * op_P(x, g, c, *tabs, plan, m + 1) if need[0] else None
     gg = op_F(x, gp, c, *tabs, plan, m) if need[1] else None
     gc = op_G(x, g, gp, *tabs, plan, m) if need[2] else None
-    return gx, gg, gc, None, None, None, None, None, None
+    return gx, gg, gc, None, None, None, None, None, None, None
 
 
 def _no_second_order(ctx, *grads):
@@ -465,31 +473,31 @@ def _features_raw(plan, m, st, x2: torch.Tensor) -> torch.Tensor:
 
 
 @torch.library.custom_op("kf::features", mutates_args=())
-def op_features(x: torch.Tensor, knots: Opt, knots_cmp: Opt, num: Opt, den: Opt, plan: str, m: int) -> torch.Tensor:
+def op_features(x: torch.Tensor, knots: Opt, knots_cmp: Opt, knots_u: Opt, num: Opt, den: Opt, plan: str, m: int) -> torch.Tensor:
     """phi_k^(m)(x[b,i]), (B, in, K)."""
-    return _features_raw(plan_of(plan), m, _state(knots, knots_cmp, num, den, x.shape[1]), x.contiguous())
+    return _features_raw(plan_of(plan), m, _state(knots, knots_cmp, knots_u, num, den, x.shape[1]), x.contiguous())
 
 
 @op_features.register_fake
-def _(x, knots, knots_cmp, num, den, plan, m):
+def _(x, knots, knots_cmp, knots_u, num, den, plan, m):
     return x.new_empty(x.shape[0], x.shape[1], plan_of(plan).size)
 
 
 def _features_setup(ctx, inputs, output):
-    x, knots, knots_cmp, num, den, plan, m = inputs
-    _save(ctx, (x, knots, knots_cmp, num, den), plan, m)
+    x, knots, knots_cmp, knots_u, num, den, plan, m = inputs
+    _save(ctx, (x, knots, knots_cmp, knots_u, num, den), plan, m)
 
 
 def _features_backward(ctx, gphi):
-    x, knots, knots_cmp, num, den = ctx.saved_tensors
+    x, knots, knots_cmp, knots_u, num, den = ctx.saved_tensors
     plan, m = ctx.plan, ctx.m
     need = ctx.needs_input_grad
     gx = gnum = gden = None
     if need[0]:
-        gx = (gphi * op_features(x, knots, knots_cmp, num, den, plan, m + 1)).sum(-1)
-    if need[3] or need[4]:
+        gx = (gphi * op_features(x, knots, knots_cmp, knots_u, num, den, plan, m + 1)).sum(-1)
+    if need[4] or need[5]:
         gnum, gden = _rational_grads_of(plan, x, gphi[..., 0], m, num, den)
-    return gx, None, None, gnum, gden, None, None
+    return gx, None, None, None, gnum, gden, None, None
 
 
 op_features.register_autograd(_features_backward, setup_context=_features_setup)
@@ -573,40 +581,40 @@ def _edge_raw(plan, m, st, x2, c, base_w):
 
 
 @torch.library.custom_op("kf::edge_derivative", mutates_args=())
-def op_edge(x: torch.Tensor, c: torch.Tensor, base_w: Opt, knots: Opt, knots_cmp: Opt, num: Opt, den: Opt, plan: str, m: int) -> torch.Tensor:
+def op_edge(x: torch.Tensor, c: torch.Tensor, base_w: Opt, knots: Opt, knots_cmp: Opt, knots_u: Opt, num: Opt, den: Opt, plan: str, m: int) -> torch.Tensor:
     """d[b,o,i] = sum_k c[o,i,k] phi_k^(m)(x[b,i]) + base_w[o,i] silu^(m)(x[b,i]), (B, out, in)."""
-    return _edge_raw(plan_of(plan), m, _state(knots, knots_cmp, num, den, x.shape[1]), x.contiguous(), c, base_w)
+    return _edge_raw(plan_of(plan), m, _state(knots, knots_cmp, knots_u, num, den, x.shape[1]), x.contiguous(), c, base_w)
 
 
 @op_edge.register_fake
-def _(x, c, base_w, knots, knots_cmp, num, den, plan, m):
+def _(x, c, base_w, knots, knots_cmp, knots_u, num, den, plan, m):
     return x.new_empty(x.shape[0], c.shape[0], x.shape[1])
 
 
 def _edge_setup(ctx, inputs, output):
-    x, c, base_w, knots, knots_cmp, num, den, plan, m = inputs
-    _save(ctx, (x, c, base_w, knots, knots_cmp, num, den), plan, m)
+    x, c, base_w, knots, knots_cmp, knots_u, num, den, plan, m = inputs
+    _save(ctx, (x, c, base_w, knots, knots_cmp, knots_u, num, den), plan, m)
 
 
 def _edge_backward(ctx, gd):
-    x, c, base_w, knots, knots_cmp, num, den = ctx.saved_tensors
+    x, c, base_w, knots, knots_cmp, knots_u, num, den = ctx.saved_tensors
     plan, m = ctx.plan, ctx.m
     need = ctx.needs_input_grad
     gx = gc = gw = gnum = gden = None
-    tabs = (knots, knots_cmp, num, den)
+    tabs = (knots, knots_cmp, knots_u, num, den)
     if need[0]:
         # d/dx of the edge is the edge derivative of order m+1
         gx = (gd * op_edge(x, c, base_w, *tabs, plan, m + 1)).sum(1)
     if need[1]:
-        phi = op_features(x, knots, knots_cmp, num, den, plan, m)  # (B, in, K)
+        phi = op_features(x, knots, knots_cmp, knots_u, num, den, plan, m)  # (B, in, K)
         gc = torch.einsum("boi,bik->oik", gd, phi)
     if need[2] and base_w is not None:
         gw = torch.einsum("boi,bi->oi", gd, silu_derivative_t(x, m))
-    if need[5] or need[6]:
+    if need[6] or need[7]:
         # one feature per edge: sum_o gd[b,o,i] c[o,i,0] multiplies phi^(m)(x[b,i])
         h = torch.einsum("boi,oi->bi", gd.float(), c[..., 0].float())
         gnum, gden = _rational_grads_of(plan, x, h, m, num, den)
-    return gx, gc, gw, None, None, gnum, gden, None, None
+    return gx, gc, gw, None, None, None, gnum, gden, None, None
 
 
 op_edge.register_autograd(_edge_backward, setup_context=_edge_setup)

@@ -24,18 +24,18 @@ def _operands(basis, B=37, IN=12, OUT=9, seed=0, grad=True):
     c = (torch.randn(OUT, IN, basis.size, generator=g) / math.sqrt(IN * basis.size)).to(DEV).requires_grad_(grad)
     gy = torch.randn(B, OUT, generator=g).to(DEV).requires_grad_(grad)
     w = (torch.rand(B, IN, generator=g) + 0.5).to(DEV).requires_grad_(grad)
-    kn = kc = num = den = None
+    kn = kc = ku = num = den = None
     if plan.kind == "bspline":
         grid = torch.linspace(-1, 1, basis.grid_size + 1, dtype=torch.float64).expand(IN, -1).contiguous().to(DEV)
         st = K.bspline_state(grid, basis.order)
-        kn, kc = st.knots, st.knots_cmp
+        kn, kc, ku = st.knots, st.knots_cmp, st.knots_u
     if plan.kind == "rational":
         groups = 4
         num = (torch.tensor(basis.param_specs()["numerator"].value, dtype=torch.float32)[None].repeat(groups, 1)
                + 0.05 * torch.randn(groups, basis.num_degree + 1, generator=g)).to(DEV).requires_grad_(grad)
         den = (torch.tensor(basis.param_specs()["denominator"].value, dtype=torch.float32)[None].repeat(groups, 1)
                + 0.05 * torch.randn(groups, basis.den_degree, generator=g)).to(DEV).requires_grad_(grad)
-    return K.plan_key(plan), x, c, gy, w, (kn, kc, num, den)
+    return K.plan_key(plan), x, c, gy, w, (kn, kc, ku, num, den)
 
 
 BASES = {"cheb8": kf.Chebyshev(8), "jacobi6": kf.Jacobi(6, 0.5, 0.5), "bspline53": kf.BSpline(5, 3), "rational": kf.Rational(5, 4)}
@@ -44,9 +44,9 @@ BASES = {"cheb8": kf.Chebyshev(8), "jacobi6": kf.Jacobi(6, 0.5, 0.5), "bspline53
 @pytest.mark.parametrize("name", list(BASES))
 def test_opcheck_F_G_P(name):
     key, x, c, gy, w, tabs = _operands(BASES[name])
-    rational = tabs[2] is not None
+    rational = tabs[3] is not None
     # rational parameters receive gradients through F at order 0; P and G take them as constants
-    fixed = tabs if not rational else (tabs[0], tabs[1], tabs[2].detach(), tabs[3].detach())
+    fixed = tabs if not rational else (tabs[0], tabs[1], tabs[2], tabs[3].detach(), tabs[4].detach())
     for m in (0, 1):
         torch.library.opcheck(torch.ops.kf.F.default, (x, w, c, *(fixed if m else tabs), key, m))
         torch.library.opcheck(torch.ops.kf.P.default, (x, gy, c, *fixed, key, m))
@@ -59,15 +59,15 @@ def test_opcheck_edge_and_features(name):
     bw = (0.1 * torch.randn(c.shape[:2], generator=torch.Generator().manual_seed(5))).to(DEV).requires_grad_()
     torch.library.opcheck(torch.ops.kf.edge_derivative.default, (x, c, bw, *tabs, key, 0))
     torch.library.opcheck(torch.ops.kf.features.default, (x, *tabs, key, 0))
-    if tabs[2] is None:
+    if tabs[3] is None:
         torch.library.opcheck(torch.ops.kf.edge_derivative.default, (x, c, bw, *tabs, key, 2))
 
 
 def test_opcheck_rational_ops_and_interval():
     key, x, c, gy, w, tabs = _operands(BASES["rational"], grad=False)
-    torch.library.opcheck(torch.ops.kf.rational_bwd.default, (x, gy, c, None, tabs[2], tabs[3], key))
+    torch.library.opcheck(torch.ops.kf.rational_bwd.default, (x, gy, c, None, tabs[3], tabs[4], key))
     h = torch.randn(x.shape, device=DEV)
-    torch.library.opcheck(torch.ops.kf.rational_param_grad.default, (x, h, w, tabs[2], tabs[3], key))
+    torch.library.opcheck(torch.ops.kf.rational_param_grad.default, (x, h, w, tabs[3], tabs[4], key))
     bkey, bx, _, _, _, btabs = _operands(BASES["bspline53"], grad=False)
     torch.library.opcheck(torch.ops.kf.bspline_interval.default, (bx, btabs[1]))
 

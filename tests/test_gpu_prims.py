@@ -11,12 +11,14 @@ import numpy as np
 import pytest
 import torch
 
+import kanforge_amd as kf
 from cases import BASES, oracle_basis, random_grid, rounded, to_dev
 from kanforge_amd.kernels import plan_for
 from kanforge_amd.torch import kernels as K
 from oracle import kan64 as o
 
 pytestmark = pytest.mark.gpu
+DEV = "cuda"
 
 TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2}
 DTYPES = [torch.float32, torch.bfloat16]
@@ -244,3 +246,32 @@ def test_bspline_nonfinite_and_outside_inputs(dtype):
     np.testing.assert_array_equal(np.isnan(phi), np.isnan(want))
     finite = ~np.isnan(want)
     np.testing.assert_allclose(phi[finite], want[finite], atol=2e-2 if dtype == torch.bfloat16 else 1e-6)
+
+
+@pytest.mark.parametrize("k,m", [(3, 0), (3, 1), (3, 2), (2, 0), (1, 1), (0, 0)])
+def test_uniform_grid_features_equal_the_general_path(k, m):
+    """The even-knot fast path (constant-time interval estimate checked against the ceil32 table,
+    de Boor in the normalised coordinate) gives the general path's features at, one ulp around and
+    between every knot, and outside the extended grid."""
+    G, IN = 8, 3
+    grid = np.stack([np.linspace(-1, 1, G + 1), np.linspace(-0.3, 2.1, G + 1), np.linspace(-5, -2, G + 1)])
+    basis = kf.BSpline(G, k)
+    plan = plan_for(basis)
+    st = K.bspline_state(torch.as_tensor(grid, device=DEV), k)
+    assert st.knots_u is not None
+    general = K.BasisState(knots=st.knots, knots_cmp=st.knots_cmp)
+    t = o.extend_grid(grid, k).astype(np.float32)  # (IN, nk)
+    pts = []
+    for row in t.T:
+        for v in row:
+            pts += [np.nextafter(v, np.float32(-np.inf)), v, np.nextafter(v, np.float32(np.inf))]
+    mids = (t[:, 1:] + t[:, :-1]) / 2
+    cols = np.array(pts, dtype=np.float32).reshape(-1, IN)
+    x = np.concatenate([cols, mids.T, t[:, :1].T - 1.0, t[:, -1:].T + 1.0]).astype(np.float32)
+    xd = torch.as_tensor(x, device=DEV)
+    fast = K._features_raw(plan, m, st, xd).cpu().double().numpy()
+    slow = K._features_raw(plan, m, general, xd).cpu().double().numpy()
+    scale = max(1.0, np.abs(slow).max())
+    np.testing.assert_allclose(fast, slow, rtol=0, atol=2e-6 * scale)
+    want = o.Basis64("bspline", grid=grid, k=k)(x.astype(np.float64), m)
+    np.testing.assert_allclose(fast, want, rtol=0, atol=1e-5 * max(1.0, np.abs(want).max()))

@@ -282,12 +282,12 @@ def test_custom_op_fake_kernels_give_shapes_on_meta_tensors():
     x = torch.empty(33, 7, device="meta")
     c = torch.empty(5, 7, 11, device="meta")
     g = torch.empty(33, 5, device="meta")
-    kn, kc = torch.empty(7, 21, device="meta"), torch.empty(7, 15, device="meta")
-    assert torch.ops.kf.F(x, None, c, kn, kc, None, None, key, 0).shape == (33, 5)
-    assert torch.ops.kf.G(x, g, None, kn, kc, None, None, key, 0).shape == (5, 7, 11)
-    assert torch.ops.kf.P(x, g, c, kn, kc, None, None, key, 1).shape == (33, 7)
-    assert torch.ops.kf.features(x, kn, kc, None, None, key, 2).shape == (33, 7, 11)
-    assert torch.ops.kf.edge_derivative(x, c, None, kn, kc, None, None, key, 1).shape == (33, 5, 7)
+    kn, kc, ku = torch.empty(7, 21, device="meta"), torch.empty(7, 15, device="meta"), torch.empty(7, 2, device="meta")
+    assert torch.ops.kf.F(x, None, c, kn, kc, ku, None, None, key, 0).shape == (33, 5)
+    assert torch.ops.kf.G(x, g, None, kn, kc, ku, None, None, key, 0).shape == (5, 7, 11)
+    assert torch.ops.kf.P(x, g, c, kn, kc, None, None, None, key, 1).shape == (33, 7)
+    assert torch.ops.kf.features(x, kn, kc, ku, None, None, key, 2).shape == (33, 7, 11)
+    assert torch.ops.kf.edge_derivative(x, c, None, kn, kc, ku, None, None, key, 1).shape == (33, 5, 7)
     rkey = K.plan_key(plan_for(kf.Rational(5, 4)))
     num, den = torch.empty(7, 6, device="meta"), torch.empty(7, 4, device="meta")
     p, dn, dd = torch.ops.kf.rational_bwd(x, g, torch.empty(5, 7, 1, device="meta"), None, num, den, rkey)
@@ -326,3 +326,16 @@ def test_bases_beyond_the_kernel_limit_are_rejected_up_front():
     assert torch.equal(layer.coef, before) and layer.basis.grid_size == 5  # untouched
     layer.refine_grid(13)  # 16 basis functions: the largest supported
     assert layer.coef.shape == (2, 3, 16)
+
+
+def test_uniform_knot_table():
+    from kanforge_amd.bases.spline import uniform_table
+
+    grid = np.stack([np.linspace(-1, 1, 9), np.linspace(-0.5, 2, 9)])
+    tab = uniform_table(grid, 3)
+    t = o.extend_grid(grid, 3)
+    np.testing.assert_allclose(tab[:, 0], t[:, 0].astype(np.float32))
+    np.testing.assert_allclose(tab[:, 1], (1 / (t[:, 1] - t[:, 0])).astype(np.float32), rtol=1e-6)
+    bent = grid.copy()
+    bent[1, 4] += 1e-3  # one uneven input: the whole layer takes the general path
+    assert uniform_table(bent, 3) is None
