@@ -214,7 +214,8 @@ inline int g_rb(int fw) { return fw <= 6 ? 128 : 64; }
 
 struct WsP {
   int cfg, ntb;
-  bool p8;  // bf16 Chebyshev with 7 or 8 features: p8_kernel (256 x (8 x 48) tiles)
+  bool p8;   // bf16 Chebyshev with 7 or 8 features: p8_kernel (256 x (8 x 48) tiles)
+  bool p12;  // bf16 B-splines with 9 to 12 features: p8_kernel with 12 slots (256 x (12 x 32) tiles)
   int64_t INP, OUTP;
   size_t cfmt, gpad, hbuf, gemm, total;
 };
@@ -230,6 +231,7 @@ inline WsP ws_p(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64
   w.cfg = fw_index(b->n_t);
   w.ntb = 2 * FW_LIST[w.cfg];
   w.p8 = b->kind == KF_KIND_CHEB && dtype == KF_BF16 && w.ntb == 8;
+  w.p12 = b->kind == KF_KIND_BSPLINE && dtype == KF_BF16 && w.ntb == 12 && b->spline_k == 3;
   // 96: whole tiles of p8_kernel (48) and p_dma_kernel (32); rational: flat tiles of 2 FW x 32 inputs
   w.INP = round_up(n_in, w.p8 ? 96 : b->kind == KF_KIND_RATIONAL ? 64 * FW_LIST[w.cfg] : 32);
   w.OUTP = round_up(n_out, p_uses_dma(w.cfg) ? p_stage_cols(dtype) : 32);
@@ -312,6 +314,7 @@ inline WsG ws_g(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64
   }
   // bf16 rational plans contract on the GEMM core (split partial sums)
   w.gemm = dtype == KF_BF16 && b->kind == KF_KIND_RATIONAL ? gemm_nt_workspace(n_out, n_in, w.BP) : 0;
+  if (dtype == KF_BF16 && b->kind == KF_KIND_BSPLINE) w.gemm = gemm_nt_workspace(n_out, n_in * b->size, w.BP);
   w.total = w.gt + w.zt + w.wt + w.part + w.colsum + w.phit + w.zpart + w.gemm;
   return w;
 }
@@ -393,33 +396,57 @@ int launch_features(const KBasis& kb, int64_t batch, int64_t n_in, int64_t brows
   return check_launch("features");
 }
 
-template <typename T, int NTB>
+template <typename T, int NTB, int RUN>
 int launch_features_t_nb(const KBasis& kb, int64_t batch, int64_t n_in, int64_t BP, int64_t INP, const void* x,
-                         const void* w, void* phit, hipStream_t s) {
-  constexpr int BT = 64 / (int)sizeof(T);  // features_t_kernel: 32 inputs x 64-byte runs of rows
+                         const void* w, void* phit, int rows_ij, hipStream_t s) {
+  constexpr int BT = RUN / (int)sizeof(T);  // features_t_kernel: 32 inputs x RUN-byte runs of rows
   const size_t knots = kb.kind == KF_KIND_BSPLINE ? (size_t)32 * (2 * kb.n_knots + 2 * kb.spline_k) * 4 : 0;
-  const size_t lds = (size_t)kb.n_t * 32 * 80 + knots;
-  auto kern = features_t_kernel<T, NTB>;
+  const size_t lds = (size_t)kb.n_t * 32 * (RUN + 16) + knots;
+  auto kern = features_t_kernel<T, NTB, RUN>;
   if (!reserve_lds((const void*)kern, lds))
     return fail(KF_ELAUNCH, "features: cannot reserve %zu bytes of LDS", lds);
   dim3 grid((unsigned)(INP / 32), (unsigned)((BP + BT - 1) / BT));
   hipLaunchKernelGGL(kern, grid, dim3(kThreads), lds, s, kb, (int)batch, (int)n_in, (int)BP, (int)INP, (const T*)x,
-                     (const T*)w, (T*)phit);
+                     (const T*)w, (T*)phit, rows_ij);
   return check_launch("features_t");
 }
 
-template <typename T>
-int launch_features_t(const KBasis& kb, int64_t batch, int64_t n_in, int64_t BP, int64_t INP, const void* x,
-                      const void* w, void* phit, hipStream_t s) {
-  if (INP % 32) return fail(KF_EINVAL, "features_t: padded input count not a multiple of 32");
-  switch (nt_bucket(kb.n_t)) {
-    case 4: return launch_features_t_nb<T, 4>(kb, batch, n_in, BP, INP, x, w, phit, s);
-    case 8: return launch_features_t_nb<T, 8>(kb, batch, n_in, BP, INP, x, w, phit, s);
-    case 12: return launch_features_t_nb<T, 12>(kb, batch, n_in, BP, INP, x, w, phit, s);
-    case 16: return launch_features_t_nb<T, 16>(kb, batch, n_in, BP, INP, x, w, phit, s);
-    default: return launch_features_t_nb<T, 24>(kb, batch, n_in, BP, INP, x, w, phit, s);
-  }
+template <typename T, int KD>
+int launch_bspline_t(const KBasis& kb, int64_t batch, int64_t n_in, int64_t BP, int64_t INP, const void* x,
+                     const void* w, void* phit, int rows_ij, hipStream_t s) {
+  constexpr int RUN = 128, BT = RUN / (int)sizeof(T);
+  const size_t lds = (size_t)kb.K * 32 * (RUN + 16) + (size_t)32 * (2 * kb.n_knots + 2 * KD) * 4;
+  auto kern = bspline_t_kernel<T, KD, RUN>;
+  if (!reserve_lds((const void*)kern, lds)) return fail(KF_ELAUNCH, "features: cannot reserve %zu bytes of LDS", lds);
+  dim3 grid((unsigned)(INP / 32), (unsigned)((BP + BT - 1) / BT));
+  hipLaunchKernelGGL(kern, grid, dim3(kThreads), lds, s, kb, (int)batch, (int)n_in, (int)BP, (int)INP, (const T*)x,
+                     (const T*)w, (T*)phit, rows_ij);
+  return check_launch("bspline_t");
 }
 
+// phiT rows: feature-major (j INP + i), or input-major (i n_t + j, rows_ij)
+template <typename T>
+int launch_features_t(const KBasis& kb, int64_t batch, int64_t n_in, int64_t BP, int64_t INP, const void* x,
+                      const void* w, void* phit, hipStream_t s, int rows_ij = 0) {
+  if (INP % 32) return fail(KF_EINVAL, "features_t: padded input count not a multiple of 32");
+  if (kb.kind == KF_KIND_BSPLINE) {  // B-splines: supports only, degree compiled in
+    switch (kb.spline_k) {
+      case 0: return launch_bspline_t<T, 0>(kb, batch, n_in, BP, INP, x, w, phit, rows_ij, s);
+      case 1: return launch_bspline_t<T, 1>(kb, batch, n_in, BP, INP, x, w, phit, rows_ij, s);
+      case 2: return launch_bspline_t<T, 2>(kb, batch, n_in, BP, INP, x, w, phit, rows_ij, s);
+      case 3: return launch_bspline_t<T, 3>(kb, batch, n_in, BP, INP, x, w, phit, rows_ij, s);
+      case 4: return launch_bspline_t<T, 4>(kb, batch, n_in, BP, INP, x, w, phit, rows_ij, s);
+      default: return launch_bspline_t<T, 5>(kb, batch, n_in, BP, INP, x, w, phit, rows_ij, s);
+    }
+  }
+  if (rows_ij) return fail(KF_EINVAL, "features_t: input-major rows are for B-splines");
+  switch (nt_bucket(kb.n_t)) {
+    case 4: return launch_features_t_nb<T, 4, 64>(kb, batch, n_in, BP, INP, x, w, phit, 0, s);
+    case 8: return launch_features_t_nb<T, 8, 64>(kb, batch, n_in, BP, INP, x, w, phit, 0, s);
+    case 12: return launch_features_t_nb<T, 12, 64>(kb, batch, n_in, BP, INP, x, w, phit, 0, s);
+    case 16: return launch_features_t_nb<T, 16, 64>(kb, batch, n_in, BP, INP, x, w, phit, 0, s);
+    default: return launch_features_t_nb<T, 24, 64>(kb, batch, n_in, BP, INP, x, w, phit, 0, s);
+  }
+}
 
 }  // namespace kfabi

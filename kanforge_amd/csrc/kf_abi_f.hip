@@ -75,7 +75,22 @@ int run_F_dma(const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out, cons
   constexpr int FW = kGdmaFW, TM = p_dma_tm(FW), BM = 2 * TM * 32, TI = 2 * FW * 32;
   const long ld = (long)n_in * kb.K;  // Phi row length: the reduction
   if (kb.n_t != kb.K || (ld * (long)sizeof(T)) % 16) return fail(KF_EINVAL, "F: Phi rows not aligned");
-  if (kb.K == 1) {  // one feature: the plain (B, in) writes are already coalesced
+  if (kb.kind == KF_KIND_BSPLINE && ld % 8 == 0 && aligned16(phi)) {
+    // 32 inputs x 64 rows per block, knot rows staged once per block
+    const size_t rpb = ((size_t)32 * kb.K * sizeof(T) + 15) / 16 * 16 + 16;
+    const size_t plds = 64 * rpb + (size_t)32 * (2 * kb.n_knots + 2 * kb.spline_k) * 4;
+    dim3 pg((unsigned)((n_in + 31) / 32), (unsigned)((batch + 63) / 64));
+    auto kern = kb.spline_k == 0   ? phi_block_kernel<T, 0>
+                : kb.spline_k == 1 ? phi_block_kernel<T, 1>
+                : kb.spline_k == 2 ? phi_block_kernel<T, 2>
+                : kb.spline_k == 3 ? phi_block_kernel<T, 3>
+                : kb.spline_k == 4 ? phi_block_kernel<T, 4>
+                                   : phi_block_kernel<T, 5>;
+    if (!reserve_lds((const void*)kern, plds)) return fail(KF_ELAUNCH, "F: cannot reserve %zu bytes of LDS", plds);
+    hipLaunchKernelGGL(kern, pg, dim3(kThreads), plds, s, kb, (int)batch, (int)n_in, (const T*)x, (T*)phi);
+    int rc = check_launch("phi_block");
+    if (rc) return rc;
+  } else if (kb.K == 1) {  // one feature: the plain (B, in) writes are already coalesced
     int rc = launch_features<T, false>(kb, batch, n_in, batch, n_in, x, phi, ld, 1L, 1L, false, s);
     if (rc) return rc;
   } else {

@@ -174,6 +174,16 @@ int run_G(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
     }
   }
   float* zpart = L.nz > 1 ? (float*)((char*)phit + L.phit) : nullptr;
+  if constexpr (sizeof(T) == 2) {
+    // B-splines in bf16: phiT rows input-major (i K + k), so that dc[o][i][k] is the GEMM
+    // g^T phiT^T stored row by row
+    if (kb.kind == KF_KIND_BSPLINE && L.BP % 64 == 0 && (n_in * kb.K) % 8 == 0 && aligned16(dc)) {
+      rc = launch_features_t<T>(kb, batch, n_in, L.BP, L.INP, x, w, phit, s, 1);
+      if (rc) return rc;
+      void* gws = (char*)phit + L.phit + L.zpart;
+      return gemm_nt(n_out, n_in * kb.K, L.BP, gt, L.BP, phit, L.BP, dc, n_in * kb.K, false, gws, L.gemm, s);
+    }
+  }
   rc = launch_features_t<T>(kb, batch, n_in, L.BP, L.INP, x, w, phit, s);
   if (rc) return rc;
   if (L.gdma) return launch_g_dma<T>(L, s, kb, n_in, n_out, gt, phit, dc);

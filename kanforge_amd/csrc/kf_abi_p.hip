@@ -58,13 +58,14 @@ int launch_p_dma_kind(const WsP& L, hipStream_t s, const KBasis& kb, int64_t bat
   return check_launch("P");
 }
 
-template <int TN, int RB>
+template <int KIND, int NF, int TN, int RB>
 int launch_p8(const WsP& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, const void* x, const void* g,
               int gstride, const void* cfmt, void* p) {
-  constexpr int TI = 16 * TN, RPASS = TN == 2 ? 128 : 64;
-  const size_t lds_ops = (size_t)2 * (256 + 8 * TI) * RB, lds_epi = (size_t)8 * RPASS * (TI + 1) * 4;
+  constexpr int TI = 128 * TN / NF, RPASS = TN == 2 ? 128 : 64;
+  const size_t knots = KIND == KF_KIND_BSPLINE ? (size_t)TI * (2 * kb.n_knots + 2 * kb.spline_k) * 4 : 0;
+  const size_t lds_ops = (size_t)2 * (256 + NF * TI) * RB, lds_epi = (size_t)NF * RPASS * (TI + 1) * 4 + knots;
   const size_t lds = lds_ops > lds_epi ? lds_ops : lds_epi;
-  auto kern = p8_kernel<KF_KIND_CHEB, TN, RB>;
+  auto kern = p8_kernel<KIND, NF, TN, RB>;
   if (L.INP % TI || L.OUTP % (RB / 2)) return fail(KF_EINVAL, "P: workspace layout not aligned");
   if (!reserve_lds((const void*)kern, lds))
     return fail(KF_ELAUNCH, "P: cannot reserve %zu bytes of LDS", lds);
@@ -129,7 +130,9 @@ int run_P(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
       }
     }
     // 7 or 8 Chebyshev features in bf16: the two-waves-per-SIMD kernel
-    if (L.p8 && !h) return launch_p8<3, 128>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p);
+    if (L.p8 && !h) return launch_p8<KF_KIND_CHEB, 8, 3, 128>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p);
+    // 9 to 12 B-spline features in bf16: the same kernel with 12 feature slots
+    if (L.p12 && !h) return launch_p8<KF_KIND_BSPLINE, 12, 3, 128>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p);
     switch (L.cfg) {
       case 0: return launch_p_dma<T, 2>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p, h);
       case 1: return launch_p_dma<T, 3>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p, h);

@@ -149,146 +149,132 @@ __device__ __forceinline__ int bspline_interval(float x, const float* kc, int n_
   return (j >= 0 && j <= n_knots - 2) ? j : -1;
 }
 
-// phi[s] = w * d^m/dx^m B_{k,s}(x), s < K = n_knots - 1 - k, for k == KD.
-// Local de Boor on the k+1 splines that can be non-zero in interval j, then
-// m derivative steps (m > k gives zeros). KM >= K.
-template <int KM, int KD>
-// kc: the input's n_knots comparison knots; kp0: its n_knots + 2 KD padded knots
-// (global memory, or a copy staged in LDS by a kernel that covers few inputs).
-__device__ inline void bspline_features_rows(float x, float w, const float* kc, const float* kp0, const KBasis& b,
-                                             float* phi) {
-#pragma unroll
-  for (int s = 0; s < KM; ++s) phi[s] = 0.f;
+// Support of the B-spline features at x for degree KD: the interval j (t_j <= x < t_{j+1}) and
+// the KD + 1 splines that can be non-zero there, N[r] = w d^m/dx^m B_{KD, j-KD+r}(x), first index
+// base = j - KD (indices outside [0, K) belong to no basis function and are dropped by callers).
+// Returns 1 for that case, 0 when every feature is zero (x outside [t_0, t_last), or m > KD),
+// 2 when x is not finite: every feature is NaN, as the float64 recurrence's (x - t) * 0 gives.
+// kc: the input's n_knots comparison knots (each float64 knot rounded up to float32, so x >= kc[r]
+// is exactly x >= t_r); kp0: its n_knots + 2 KD padded knots (global memory, or a copy in LDS);
+// t0, ih: (t_0, 1/h) when the input's knots are evenly spaced by h, ih == 0 otherwise.
+template <int KD>
+__device__ inline int bspline_support(float x, float w, const float* kc, const float* kp0, float t0, float ih,
+                                      const KBasis& b, int& base, float (&N)[KD + 1]) {
   const int nk = b.n_knots, m = b.order;
-  if (m > KD) return;
-  const int j = bspline_interval(x, kc, nk);
-  if (j < 0) {
-    // outside [t_0, t_last): zeros; a non-finite x turns the zero indicators
-    // into NaN through (x - t) * 0, as the float64 recurrence does
-    if (!__builtin_isfinite(x)) {
+  if (!__builtin_isfinite(x)) return 2;
+  if (m > KD || x < kc[0] || x >= kc[nk - 1]) return 0;
+  int j;
+  if (ih != 0.f) {
+    // even knots: the affine estimate, moved until kc[j] <= x < kc[j + 1] (it is off by at most
+    // one; the search below is the fallback that never runs for even knots)
+    j = (int)floorf((x - t0) * ih);
+    j = j < 0 ? 0 : (j > nk - 2 ? nk - 2 : j);
 #pragma unroll
-      for (int s = 0; s < KM; ++s) phi[s] = (s < b.K) ? __builtin_nanf("") : 0.f;
+    for (int it = 0; it < 2; ++it) {
+      if (x < kc[j]) --j;
+      else if (x >= kc[j + 1]) ++j;
     }
-    return;
+    if (!(kc[j] <= x && x < kc[j + 1])) j = bspline_interval(x, kc, nk);
+  } else {
+    j = bspline_interval(x, kc, nk);
   }
-  // L[r] = t_{j-KD+r}, r = 0..2KD+1 (kp[r'] = t_{r'-KD}, so t_{j-KD+r} = kp[j+r])
-  const float* kp = kp0 + j;
-  float L[2 * KD + 2];
+  // Cox-de Boor to degree KD - m, then m derivative steps; N[r] = B_{q, j-q+r} after step q
 #pragma unroll
-  for (int r = 0; r < 2 * KD + 2; ++r) L[r] = kp[r];
-  // N[r] = B_{q, j-q+r}, r = 0..q. With s = j-q+r:
-  //   t_s = L[KD-q+r], t_{s+1} = L[KD-q+r+1], t_{s+q} = L[KD+r], t_{s+q+1} = L[KD+r+1]
-  float N[KD + 1];
-  N[0] = 1.f;
-#pragma unroll
-  for (int r = 1; r <= KD; ++r) N[r] = 0.f;
+  for (int r = 0; r <= KD; ++r) N[r] = r == 0 ? 1.f : 0.f;
   const int deg = KD - m;
+  if (ih != 0.f) {
+    // every knot difference is a whole number of steps: with u = (x - t_j) / h and s = j-q+r,
+    // (x - t_s) / (t_{s+q} - t_s) = (u + q - r) / q, (t_{s+q+1} - x) / (t_{s+q+1} - t_{s+1}) = (r + 1 - u) / q,
+    // and a derivative step is (left - right) / h
+    const float u = (x - kp0[j + KD]) * ih;
 #pragma unroll
-  for (int q = 1; q <= KD; ++q) {
-    float nn[KD + 1];
+    for (int q = 1; q <= KD; ++q) {
+      float nn[KD + 1];
+      const float iq = 1.f / (float)q;
 #pragma unroll
-    for (int r = 0; r <= KD; ++r) nn[r] = 0.f;
+      for (int r = 0; r <= KD; ++r) {
+        const float left = (r >= 1 && r <= q) ? N[r - 1] : 0.f;
+        const float right = (r <= q - 1) ? N[r] : 0.f;
+        if (r > q)
+          nn[r] = 0.f;
+        else if (q <= deg)
+          nn[r] = ((u + (float)(q - r)) * left + ((float)(r + 1) - u) * right) * iq;
+        else
+          nn[r] = (left - right) * ih;
+      }
 #pragma unroll
-    for (int r = 0; r <= q; ++r) {
-      const float ts = L[KD - q + r], ts1 = L[KD - q + r + 1], tsq = L[KD + r], tsq1 = L[KD + r + 1];
-      const float left = (r >= 1) ? N[r - 1] : 0.f;   // B_{q-1,s}
-      const float right = (r <= q - 1) ? N[r] : 0.f;  // B_{q-1,s+1}
-      // knot spans divide through the fast reciprocal (<= 2 ulp): an IEEE division
-      // costs a dozen instructions and there are two per term
-      if (q <= deg)  // Cox-de Boor
-        nn[r] = __fdividef(x - ts, tsq - ts) * left + __fdividef(tsq1 - x, tsq1 - ts1) * right;
-      else  // derivative step
-        nn[r] = (float)q * (__fdividef(left, tsq - ts) - __fdividef(right, tsq1 - ts1));
+      for (int r = 0; r <= KD; ++r) N[r] = nn[r];
     }
+  } else {
+    // L[r] = t_{j-KD+r}, r = 0..2KD+1 (kp[r'] = t_{r'-KD}, so t_{j-KD+r} = kp[j+r])
+    const float* kp = kp0 + j;
+    float L[2 * KD + 2];
 #pragma unroll
-    for (int r = 0; r <= KD; ++r) N[r] = nn[r];
+    for (int r = 0; r < 2 * KD + 2; ++r) L[r] = kp[r];
+#pragma unroll
+    for (int q = 1; q <= KD; ++q) {
+      float nn[KD + 1];
+#pragma unroll
+      for (int r = 0; r <= KD; ++r) {
+        if (r > q) {
+          nn[r] = 0.f;
+          continue;
+        }
+        const float ts = L[KD - q + r], ts1 = L[KD - q + r + 1], tsq = L[KD + r], tsq1 = L[KD + r + 1];
+        const float left = (r >= 1) ? N[r - 1] : 0.f;   // B_{q-1,s}
+        const float right = (r <= q - 1) ? N[r] : 0.f;  // B_{q-1,s+1}
+        // knot spans divide through the fast reciprocal (<= 2 ulp): an IEEE division costs a
+        // dozen instructions and there are two per term
+        if (q <= deg)  // Cox-de Boor
+          nn[r] = __fdividef(x - ts, tsq - ts) * left + __fdividef(tsq1 - x, tsq1 - ts1) * right;
+        else  // derivative step
+          nn[r] = (float)q * (__fdividef(left, tsq - ts) - __fdividef(right, tsq1 - ts1));
+      }
+#pragma unroll
+      for (int r = 0; r <= KD; ++r) N[r] = nn[r];
+    }
   }
-  // N[r] = B^(m)_{KD, j-KD+r}
-  const int base = j - KD;
 #pragma unroll
-  for (int s = 0; s < KM; ++s) {
-    const int r = s - base;
-    float v = 0.f;
-#pragma unroll
-    for (int rr = 0; rr <= KD; ++rr) v = (rr == r) ? N[rr] : v;
-    phi[s] = (s < b.K) ? w * v : 0.f;
+  for (int r = 0; r <= KD; ++r) N[r] *= w;
+  base = j - KD;
+  return 1;
+}
+
+// (t_0, 1/h) of input i, or ih = 0 when the knots are not evenly spaced
+__device__ __forceinline__ void bspline_affine(const KBasis& b, int i, float& t0, float& ih) {
+  if (b.knots_uniform) {
+    t0 = b.knots_uniform[2 * i];
+    ih = b.knots_uniform[2 * i + 1];
+  } else {
+    t0 = 0.f;
+    ih = 0.f;
   }
 }
 
-// The same features for an input whose real knots t_0 .. t_{nk-1} are evenly spaced by h = 1 / ih.
-// Interval: the affine estimate floor((x - t_0) ih), moved until kc[j] <= x < kc[j + 1] holds on
-// the exact comparison knots (the estimate is off by at most one), so j is the one the general
-// search finds. Values: Cox-de Boor in u = (x - t_j) ih, where every knot difference is a whole
-// number of steps, so each term is a multiply by a constant; a derivative step multiplies by ih.
+// phi[s] = w * d^m/dx^m B_{KD,s}(x) for s < KM (zeros past K = n_knots - 1 - KD) from the support.
 template <int KM, int KD>
-__device__ inline void bspline_features_uniform(float x, float w, const float* kc, const float* kp0, float t0,
-                                                float ih, const KBasis& b, float* phi) {
-#pragma unroll
-  for (int s = 0; s < KM; ++s) phi[s] = 0.f;
-  const int nk = b.n_knots, m = b.order;
-  if (m > KD) return;
-  if (!__builtin_isfinite(x) || x < kc[0] || x >= kc[nk - 1]) {
-    if (!__builtin_isfinite(x)) {
-#pragma unroll
-      for (int s = 0; s < KM; ++s) phi[s] = (s < b.K) ? __builtin_nanf("") : 0.f;
-    }
-    return;
-  }
-  int j = (int)floorf((x - t0) * ih);
-  j = j < 0 ? 0 : (j > nk - 2 ? nk - 2 : j);
-#pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    if (x < kc[j]) --j;
-    else if (x >= kc[j + 1]) ++j;
-  }
-  if (!(kc[j] <= x && x < kc[j + 1])) j = bspline_interval(x, kc, nk);  // never taken for even knots
-  const float u = (x - kp0[j + KD]) * ih;
-  // N[r] = B_{q, j-q+r}: with s = j-q+r, (x - t_s) / (t_{s+q} - t_s) = (u + q - r) / q and
-  // (t_{s+q+1} - x) / (t_{s+q+1} - t_{s+1}) = (r + 1 - u) / q
+__device__ inline void bspline_features_rows(float x, float w, const float* kc, const float* kp0, float t0, float ih,
+                                             const KBasis& b, float* phi) {
+  int base = 0;
   float N[KD + 1];
-  N[0] = 1.f;
-#pragma unroll
-  for (int r = 1; r <= KD; ++r) N[r] = 0.f;
-  const int deg = KD - m;
-#pragma unroll
-  for (int q = 1; q <= KD; ++q) {
-    float nn[KD + 1];
-    const float iq = 1.f / (float)q;
-#pragma unroll
-    for (int r = 0; r <= KD; ++r) nn[r] = 0.f;
-#pragma unroll
-    for (int r = 0; r <= q; ++r) {
-      const float left = (r >= 1) ? N[r - 1] : 0.f;
-      const float right = (r <= q - 1) ? N[r] : 0.f;
-      if (q <= deg)
-        nn[r] = ((u + (float)(q - r)) * left + ((float)(r + 1) - u) * right) * iq;
-      else
-        nn[r] = (left - right) * ih;
-    }
-#pragma unroll
-    for (int r = 0; r <= KD; ++r) N[r] = nn[r];
-  }
-  const int base = j - KD;
+  const int st = bspline_support<KD>(x, w, kc, kp0, t0, ih, b, base, N);
 #pragma unroll
   for (int s = 0; s < KM; ++s) {
     const int r = s - base;
     float v = 0.f;
 #pragma unroll
     for (int rr = 0; rr <= KD; ++rr) v = (rr == r) ? N[rr] : v;
-    phi[s] = (s < b.K) ? w * v : 0.f;
+    phi[s] = (s < b.K) ? (st == 1 ? v : (st == 2 ? __builtin_nanf("") : 0.f)) : 0.f;
   }
 }
 
 template <int KM, int KD>
 __device__ inline void bspline_features(float x, float w, int i, const KBasis& b, float* phi) {
   const int nk = b.n_knots;
-  const float* kc = b.knots_cmp + (size_t)i * nk;
-  const float* kp = b.knots + (size_t)i * (nk + 2 * KD);
-  if (b.knots_uniform) {
-    bspline_features_uniform<KM, KD>(x, w, kc, kp, b.knots_uniform[2 * i], b.knots_uniform[2 * i + 1], b, phi);
-    return;
-  }
-  bspline_features_rows<KM, KD>(x, w, kc, kp, b, phi);
+  float t0, ih;
+  bspline_affine(b, i, t0, ih);
+  bspline_features_rows<KM, KD>(x, w, b.knots_cmp + (size_t)i * nk, b.knots + (size_t)i * (nk + 2 * KD), t0, ih, b,
+                                phi);
 }
 
 // ---------------------------------------------------------------------------
@@ -391,24 +377,15 @@ __device__ inline float rational_feature(float x, int i, const KBasis& b, int m)
 template <int KM>
 __device__ inline void bspline_dispatch_rows(float x, float w, const float* kc, const float* kp0, const KBasis& b,
                                              float* phi, int i) {
-  if (b.knots_uniform) {
-    const float t0 = b.knots_uniform[2 * i], ih = b.knots_uniform[2 * i + 1];
-    switch (b.spline_k) {
-      case 0: bspline_features_uniform<KM, 0>(x, w, kc, kp0, t0, ih, b, phi); return;
-      case 1: bspline_features_uniform<KM, 1>(x, w, kc, kp0, t0, ih, b, phi); return;
-      case 2: bspline_features_uniform<KM, 2>(x, w, kc, kp0, t0, ih, b, phi); return;
-      case 3: bspline_features_uniform<KM, 3>(x, w, kc, kp0, t0, ih, b, phi); return;
-      case 4: bspline_features_uniform<KM, 4>(x, w, kc, kp0, t0, ih, b, phi); return;
-      default: bspline_features_uniform<KM, 5>(x, w, kc, kp0, t0, ih, b, phi); return;
-    }
-  }
+  float t0, ih;
+  bspline_affine(b, i, t0, ih);
   switch (b.spline_k) {
-    case 0: bspline_features_rows<KM, 0>(x, w, kc, kp0, b, phi); break;
-    case 1: bspline_features_rows<KM, 1>(x, w, kc, kp0, b, phi); break;
-    case 2: bspline_features_rows<KM, 2>(x, w, kc, kp0, b, phi); break;
-    case 3: bspline_features_rows<KM, 3>(x, w, kc, kp0, b, phi); break;
-    case 4: bspline_features_rows<KM, 4>(x, w, kc, kp0, b, phi); break;
-    default: bspline_features_rows<KM, 5>(x, w, kc, kp0, b, phi); break;
+    case 0: bspline_features_rows<KM, 0>(x, w, kc, kp0, t0, ih, b, phi); break;
+    case 1: bspline_features_rows<KM, 1>(x, w, kc, kp0, t0, ih, b, phi); break;
+    case 2: bspline_features_rows<KM, 2>(x, w, kc, kp0, t0, ih, b, phi); break;
+    case 3: bspline_features_rows<KM, 3>(x, w, kc, kp0, t0, ih, b, phi); break;
+    case 4: bspline_features_rows<KM, 4>(x, w, kc, kp0, t0, ih, b, phi); break;
+    default: bspline_features_rows<KM, 5>(x, w, kc, kp0, t0, ih, b, phi); break;
   }
 }
 
@@ -416,15 +393,13 @@ __device__ inline void bspline_dispatch_rows(float x, float w, const float* kc, 
 // kc[il * nk + r], kp[il * (nk + 2k) + r]. Every thread of the block calls it;
 // the caller synchronises before reading.
 __device__ inline void stage_knot_rows(const KBasis& b, int i0, int n, int IN, float* kc, float* kp) {
+  // the rows of consecutive inputs are one contiguous run in each table
   const int nk = b.n_knots, np = nk + 2 * b.spline_k;
-  for (int e = threadIdx.x; e < n * nk; e += blockDim.x) {
-    const int il = e / nk, i = i0 + il;
-    kc[e] = i < IN ? b.knots_cmp[(size_t)i * nk + e % nk] : 0.f;
-  }
-  for (int e = threadIdx.x; e < n * np; e += blockDim.x) {
-    const int il = e / np, i = i0 + il;
-    kp[e] = i < IN ? b.knots[(size_t)i * np + e % np] : 0.f;
-  }
+  const long kc_end = (long)IN * nk - (long)i0 * nk, kp_end = (long)IN * np - (long)i0 * np;
+  const float* kcg = b.knots_cmp + (size_t)i0 * nk;
+  const float* kpg = b.knots + (size_t)i0 * np;
+  for (int e = threadIdx.x; e < n * nk; e += blockDim.x) kc[e] = e < kc_end ? kcg[e] : 0.f;
+  for (int e = threadIdx.x; e < n * np; e += blockDim.x) kp[e] = e < kp_end ? kpg[e] : 0.f;
 }
 __device__ __forceinline__ int knot_lds_floats(const KBasis& b, int n) {
   return n * (2 * b.n_knots + 2 * b.spline_k);

@@ -1039,11 +1039,11 @@ __global__ __launch_bounds__(kThreads) void phi_rows_kernel(KBasis bs, int B, in
 // features go to LDS, and every (j, i) row segment leaves as one 64-byte run
 // along the batch (64-byte rather than 128-byte runs halve the LDS per block,
 // which doubles the resident blocks of this latency-bound kernel).
-template <typename T, int NTB>
+template <typename T, int NTB, int RUN = 64>
 __global__ __launch_bounds__(kThreads) void features_t_kernel(KBasis bs, int B, int IN, int BP, int INP,
                                                               const T* __restrict__ x, const T* __restrict__ w,
-                                                              T* __restrict__ phit) {
-  constexpr int RUN = 64, BT = RUN / (int)sizeof(T), RSB = RUN + 16, CPR = RUN / 16;
+                                                              T* __restrict__ phit, int rows_ij) {
+  constexpr int BT = RUN / (int)sizeof(T), RSB = RUN + 16, CPR = RUN / 16;
   constexpr int PER = 32 * BT / kThreads, VW = 16 / (int)sizeof(T);
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];  // [n_t][32][RSB], B-spline knot rows
   const int n_t = bs.n_t;
@@ -1076,7 +1076,104 @@ __global__ __launch_bounds__(kThreads) void features_t_kernel(KBasis bs, int B, 
   const int total = n_t * 32 * CPR;
   for (int c = threadIdx.x; c < total; c += kThreads) {
     const int r = c / CPR, q = c % CPR, j = r / 32, il = r % 32, b = b0 + q * VW;
-    if (b < BP) gstore16(phit + ((size_t)j * INP + i0 + il) * BP + b, lds_read16(smem + (size_t)r * RSB + 16 * q));
+    // rows of phiT: feature-major j * INP + i, or input-major i * n_t + j (rows_ij)
+    const size_t row = rows_ij ? (size_t)(i0 + il) * n_t + j : (size_t)j * INP + i0 + il;
+    if (b < BP) gstore16(phit + row * BP + b, lds_read16(smem + (size_t)r * RSB + 16 * q));
+  }
+}
+
+// B-spline features of degree KD in the reference's (B, in K) layout, phi[b][i K + k], for blocks of
+// 32 inputs x 64 rows: the block's knot rows are staged in LDS once, every thread evaluates 8
+// elements' supports (KD + 1 values) into zeroed LDS copies of the 64 row segments, which leave as
+// 16-byte chunks. (IN K) % 8 == 0 and phi 16-byte aligned; K <= 16.
+template <typename T, int KD>
+__global__ __launch_bounds__(kThreads) void phi_block_kernel(KBasis bs, int B, int IN, const T* __restrict__ x,
+                                                             T* __restrict__ phi) {
+  constexpr int ROWS = 64, PER = 32 * ROWS / kThreads, VW = 16 / (int)sizeof(T);
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];  // [ROWS][rpb] segments, knot rows
+  const int K = bs.K, nk = bs.n_knots, i0 = blockIdx.x * 32, b0 = blockIdx.y * ROWS;
+  const int rpb = (32 * K * (int)sizeof(T) + 15) / 16 * 16 + 16;  // row pitch of the segment copies
+  float* kcs = reinterpret_cast<float*>(smem + (size_t)ROWS * rpb);
+  float* kps = kcs + 32 * nk;
+  stage_knot_rows(bs, i0, 32, IN, kcs, kps);
+  for (int c = threadIdx.x; c < ROWS * rpb / 16; c += kThreads) *reinterpret_cast<u32x4*>(smem + 16 * c) = u32x4{0, 0, 0, 0};
+  __syncthreads();
+  const int il = threadIdx.x % 32, i = i0 + il;
+  float t0 = 0.f, ih = 0.f;
+  if (i < IN) bspline_affine(bs, i, t0, ih);
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int bl = threadIdx.x / 32 + u * (kThreads / 32), b = b0 + bl;
+    if (b >= B || i >= IN) continue;
+    const float xv = to_f32(x[(size_t)b * IN + i]);
+    T* seg = reinterpret_cast<T*>(smem + (size_t)bl * rpb) + il * K;
+    float N[KD + 1];
+    int base = 0;
+    const int st = bspline_support<KD>(xv, 1.f, kcs + il * nk, kps + il * (nk + 2 * KD), t0, ih, bs, base, N);
+    if (st == 1) {
+#pragma unroll
+      for (int r = 0; r <= KD; ++r)
+        if (base + r >= 0 && base + r < K) seg[base + r] = from_f32<T>(N[r]);
+    } else if (st == 2) {
+      for (int j = 0; j < K; ++j) seg[j] = from_f32<T>(__builtin_nanf(""));
+    }
+  }
+  __syncthreads();
+  const int n = (IN - i0 < 32 ? IN - i0 : 32) * K;  // elements of one row's segment
+  const int nv = n / VW, tail = n - nv * VW;
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  for (int bl = wave; bl < ROWS; bl += kThreads / 64) {  // one row per wave at a time, lanes along it
+    const int b = b0 + bl;
+    if (b >= B) break;
+    T* dst = phi + ((size_t)b * IN + i0) * K;
+    for (int q = lane; q < nv; q += 64) gstore16(dst + q * VW, lds_read16(smem + (size_t)bl * rpb + 16 * q));
+    if (lane < tail) dst[nv * VW + lane] = reinterpret_cast<const T*>(smem + (size_t)bl * rpb)[nv * VW + lane];
+  }
+}
+
+// B-spline features of degree KD (times w), transposed: phiT rows j INP + i (feature-major) or
+// i K + j (input-major, rows_ij), batch along the row, for blocks of 32 inputs x RUN bytes of
+// rows; knot rows staged in LDS, supports written into zeroed LDS rows, rows out in 16-byte chunks.
+template <typename T, int KD, int RUN>
+__global__ __launch_bounds__(kThreads) void bspline_t_kernel(KBasis bs, int B, int IN, int BP, int INP,
+                                                             const T* __restrict__ x, const T* __restrict__ w,
+                                                             T* __restrict__ phit, int rows_ij) {
+  constexpr int BT = RUN / (int)sizeof(T), RSB = RUN + 16, CPR = RUN / 16;
+  constexpr int PER = 32 * BT / kThreads, VW = 16 / (int)sizeof(T);
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];  // [K][32][RSB], knot rows
+  const int K = bs.K, nk = bs.n_knots;
+  const int i0 = blockIdx.x * 32, b0 = blockIdx.y * BT;
+  float* kcs = reinterpret_cast<float*>(smem + (size_t)K * 32 * RSB);
+  float* kps = kcs + 32 * nk;
+  stage_knot_rows(bs, i0, 32, IN, kcs, kps);
+  for (int c = threadIdx.x; c < K * 32 * RSB / 16; c += kThreads) *reinterpret_cast<u32x4*>(smem + 16 * c) = u32x4{0, 0, 0, 0};
+  __syncthreads();
+  const int il = threadIdx.x % 32, i = i0 + il;
+  float t0 = 0.f, ih = 0.f;
+  if (i < IN) bspline_affine(bs, i, t0, ih);
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int bl = threadIdx.x / 32 + u * (kThreads / 32), b = b0 + bl;
+    if (b >= B || i >= IN) continue;
+    const size_t off = (size_t)b * IN + i;
+    const float xv = to_f32(x[off]), wv = w ? to_f32(w[off]) : 1.f;
+    float N[KD + 1];
+    int base = 0;
+    const int st = bspline_support<KD>(xv, wv, kcs + il * nk, kps + il * (nk + 2 * KD), t0, ih, bs, base, N);
+    if (st == 1) {
+#pragma unroll
+      for (int r = 0; r <= KD; ++r)
+        if (base + r >= 0 && base + r < K) reinterpret_cast<T*>(smem + (size_t)((base + r) * 32 + il) * RSB)[bl] = from_f32<T>(N[r]);
+    } else if (st == 2) {
+      for (int j = 0; j < K; ++j) reinterpret_cast<T*>(smem + (size_t)(j * 32 + il) * RSB)[bl] = from_f32<T>(__builtin_nanf(""));
+    }
+  }
+  __syncthreads();
+  const int total = K * 32 * CPR;
+  for (int c = threadIdx.x; c < total; c += kThreads) {
+    const int r = c / CPR, q = c % CPR, j = r / 32, ir = r % 32, b = b0 + q * VW;
+    const size_t row = rows_ij ? (size_t)(i0 + ir) * K + j : (size_t)j * INP + i0 + ir;
+    if (b < BP) gstore16(phit + row * BP + b, lds_read16(smem + (size_t)r * RSB + 16 * q));
   }
 }
 
@@ -1709,10 +1806,11 @@ __global__ __launch_bounds__(256) void p_dma_kernel(KBasis bs, int B, int IN, in
   }
 }
 
-// P for bf16 plans with 7 or 8 kernel features: the GEMM
+// P for bf16 plans with NF kernel feature slots (8: Chebyshev with 7 or 8 features; 12: B-splines
+// with 9 to 12): the GEMM
 //   H_j[b, i] = sum_o g[b, o] CfmT[j][i][o]   (columns n = j * TI + i of a TI-input tile)
 // on 8 waves, two per SIMD, so that one wave's waits and barrier arrivals are covered by the
-// other's MFMAs. Workgroup tile 256 rows x (8 features x TI = 16 TN inputs); wave (wm, wn) =
+// other's MFMAs. Workgroup tile 256 rows x (NF features x TI = 128 TN / NF inputs); wave (wm, wn) =
 // (wave & 1, wave >> 1) owns rows 128 wm .. +127 and column fragments TN wn .. +TN - 1 (4 x TN
 // accumulator tiles). A stage is RB bytes of o for the 256 rows of g and the 128 TN rows of
 // CfmT, copied global -> LDS by all waves into two buffers (one barrier per stage); rows are
@@ -1721,11 +1819,12 @@ __global__ __launch_bounds__(256) void p_dma_kernel(KBasis bs, int B, int IN, in
 // passes of RPASS rows: the feature sums H_j go to LDS and every thread forms
 // p[b, i] = sum_j f_j(x[b, i]) H_j[b, i] for (row, input) pairs, the features computed once per
 // pair.
-template <int KIND, int TN, int RB>
+template <int KIND, int NF, int TN, int RB, int KD = 3>
 __global__ __launch_bounds__(512) void p8_kernel(KBasis bs, int B, int IN, int INP, int OUTP,
                                                  const bf16* __restrict__ x, const bf16* __restrict__ g, int gstride,
                                                  const bf16* __restrict__ cfmt, bf16* __restrict__ p) {
-  constexpr int BM = 256, NF = 8, TI = 16 * TN, BN = NF * TI, SA = BM * RB, SS = (BM + BN) * RB, NBUF = 2;
+  constexpr int BM = 256, BN = 128 * TN, TI = BN / NF, SA = BM * RB, SS = (BM + BN) * RB, NBUF = 2;
+  static_assert(TI * NF == BN && TI % 2 == 0, "whole inputs per tile");
   constexpr int RP = TI + 1, RPASS = TN == 2 ? 128 : 64, NBLK = SS / 1024, BPW = NBLK / 8;
   constexpr int CPR = RB / 16, RPB = 1024 / RB, KS = RB / 32, EPS = RB / 2;  // chunks per row, rows per block
   static_assert(RB == 64 || RB == 128, "64- or 128-byte stage rows");
@@ -1803,6 +1902,14 @@ __global__ __launch_bounds__(512) void p8_kernel(KBasis bs, int B, int IN, int I
   lds_wait();
 
   float* red = reinterpret_cast<float*>(smem);  // [NF][RPASS][RP]
+  // B-splines: the tile's knot rows, after the sums (the stage buffers are free once every wave
+  // passed this barrier)
+  float* kcs = red + NF * RPASS * RP;
+  float* kps = kcs + TI * bs.n_knots;
+  if constexpr (KIND == KF_KIND_BSPLINE) {
+    __syncthreads();
+    stage_knot_rows(bs, i0, TI, IN, kcs, kps);
+  }
 #pragma unroll
   for (int ps = 0; ps < BM / RPASS; ++ps) {
     __syncthreads();
@@ -1828,10 +1935,28 @@ __global__ __launch_bounds__(512) void p8_kernel(KBasis bs, int B, int IN, int I
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         if (i + u < IN) {
-          float f[NF];
-          kind_features<KIND, NF>(to_f32(x[(size_t)b * IN + i + u]), 1.f, i + u, bs, f);
+          const float xv = to_f32(x[(size_t)b * IN + i + u]);
+          if constexpr (KIND == KF_KIND_BSPLINE) {
+            // B-splines of degree KD: only the support's sums (KD + 1 LDS reads) enter
+            const int nk = bs.n_knots;
+            float t0, ih, N[KD + 1];
+            int base = 0;
+            bspline_affine(bs, i + u, t0, ih);
+            const int ilu = il + u;
+            const int st = bspline_support<KD>(xv, 1.f, kcs + ilu * nk, kps + ilu * (nk + 2 * KD), t0, ih, bs, base, N);
+            if (st == 1) {
 #pragma unroll
-          for (int q = 0; q < NF; ++q) v[u] = fmaf(red[(q * RPASS + row) * RP + il + u], f[q], v[u]);
+              for (int r = 0; r <= KD; ++r)
+                if (base + r >= 0 && base + r < bs.K) v[u] = fmaf(red[((base + r) * RPASS + row) * RP + il + u], N[r], v[u]);
+            } else if (st == 2) {
+              v[u] = __builtin_nanf("");
+            }
+          } else {
+            float f[NF];
+            kind_features<KIND, NF>(xv, 1.f, i + u, bs, f);
+#pragma unroll
+            for (int q = 0; q < NF; ++q) v[u] = fmaf(red[(q * RPASS + row) * RP + il + u], f[q], v[u]);
+          }
         }
       }
       bf16* dst = p + (size_t)b * IN + i;
