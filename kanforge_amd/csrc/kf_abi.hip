@@ -44,6 +44,15 @@ namespace {
 template <typename T, int KM>
 void launch_edge_t(const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* c,
                    const void* bw, void* out, hipStream_t s) {
+  if constexpr (sizeof(T) == 4) {
+    // wide float32 layers: 16-byte stores of 4 consecutive inputs
+    if (n_in >= 32 && n_in % 4 == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0) {
+      dim3 grid((unsigned)((n_in + 31) / 32), (unsigned)((batch + 31) / 32));
+      hipLaunchKernelGGL((edge4_kernel<KM>), grid, dim3(kThreads), 0, s, kb, (int)batch, (int)n_in, (int)n_out,
+                         (const float*)x, (const float*)c, (const float*)bw, (float*)out);
+      return;
+    }
+  }
   constexpr int ROWS = KM <= 8 ? 32 : 16;  // edge_kernel's block: ROWS rows x IW inputs
   int iw = 32;
   while (iw / 2 >= n_in && iw > 1) iw /= 2;  // narrow layers: the power of two >= n_in

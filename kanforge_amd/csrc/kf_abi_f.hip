@@ -119,12 +119,84 @@ int run_F_dma(const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out, cons
   return check_launch("F");
 }
 
+// Narrow layers (at most 8 outputs, or inputs x basis functions <= 64 with at most 4 inputs):
+// row streaming. Chebyshev-family layers with at most 8 outputs and 128 inputs first fold the
+// coefficients into the workspace's feature-major block and run one lane per (row, input).
+bool f_streams(const KBasis& kb, int64_t n_in, int64_t n_out) {
+  return kb.kind != KF_KIND_RATIONAL && (n_out <= 8 || (n_in <= 4 && n_in * kb.K <= 64 && n_in * 16 <= 64));
+}
+
+template <typename T, int KM, int L, int NC, int OM>
+int launch_f_lanes(const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* w,
+                   const void* cf, void* y, int64_t OUTP, int64_t INP, hipStream_t s) {
+  constexpr int R = 64 / L, WPB = kThreads / 64;
+  const int64_t waves = (batch + R - 1) / R;
+  const int64_t blocks = std::min<int64_t>((waves + WPB - 1) / WPB, 2048);
+  hipLaunchKernelGGL((f_lanes_kernel<T, KM, L, NC, OM>), dim3((unsigned)blocks), dim3(kThreads), 0, s, kb, (int)batch,
+                     (int)n_in, (int)n_out, (const T*)x, (const T*)w, (const T*)cf, (T*)y, (int)OUTP, (int)INP);
+  return check_launch("F lanes");
+}
+
+template <typename T, int KM>
+int pick_f_lanes(const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* w,
+                 const void* cf, void* y, int64_t OUTP, int64_t INP, hipStream_t s) {
+  const auto go = [&](auto l_tag, auto nc_tag) {
+    constexpr int L = decltype(l_tag)::value, NC = decltype(nc_tag)::value;
+    if (n_out == 1) return launch_f_lanes<T, KM, L, NC, 1>(kb, batch, n_in, n_out, x, w, cf, y, OUTP, INP, s);
+    return launch_f_lanes<T, KM, L, NC, 8>(kb, batch, n_in, n_out, x, w, cf, y, OUTP, INP, s);
+  };
+  using I16 = std::integral_constant<int, 16>;
+  using I64 = std::integral_constant<int, 64>;
+  using N1 = std::integral_constant<int, 1>;
+  using N2 = std::integral_constant<int, 2>;
+  if (n_in <= 16) return go(I16{}, N1{});
+  if (n_in <= 64) return go(I64{}, N1{});
+  return go(I64{}, N2{});
+}
+
+// whether the lane kernel takes the layer: registers for NC x OM x KM coefficients per lane
+inline bool f_lanes_fit(const KBasis& kb, int64_t n_in, int64_t n_out) {
+  if (kb.kind != KF_KIND_CHEB || n_out > 8 || n_in > 128) return false;
+  const int km = kb.n_t <= 8 ? 8 : 16;
+  const int nc = n_in <= 64 ? 1 : 2, om = n_out == 1 ? 1 : 8;
+  return kb.n_t <= 16 && nc * om * km <= 128;
+}
+
+template <typename T, int KM>
+int launch_f_stream(const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* w,
+                    const void* c, void* y, hipStream_t s) {
+  dim3 grid((unsigned)((batch + kThreads - 1) / kThreads));
+  if (n_out <= 8)
+    hipLaunchKernelGGL((f_stream_kernel<T, KM, true>), grid, dim3(kThreads), 0, s, kb, (int)batch, (int)n_in,
+                       (int)n_out, (const T*)x, (const T*)w, (const T*)c, (T*)y);
+  else
+    hipLaunchKernelGGL((f_stream_kernel<T, KM, false>), grid, dim3(kThreads), 0, s, kb, (int)batch, (int)n_in,
+                       (int)n_out, (const T*)x, (const T*)w, (const T*)c, (T*)y);
+  return check_launch("F stream");
+}
+
 template <typename T>
 int run_F(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
           const void* w, const void* c, void* y, void* ws, hipStream_t s) {
   const bool has_w = w != nullptr;
   const bool cheb = kb.kind == KF_KIND_CHEB;
   const bool weighted = features_weighted(b, w);
+  const WsF LW = ws_f(b, dtype, batch, n_in, n_out, weighted);
+  // the folded copy holds n_t features (the workspace is sized for at least n_tp of them)
+  const bool lanes_ws = (size_t)kb.n_t * LW.OUTP * LW.INP * elt_size(dtype) <= LW.total;
+  if (batch >= 1024 && lanes_ws && f_lanes_fit(kb, n_in, n_out)) {
+    const WsF& L = LW;
+    int rc = launch_permute<T>(kb, n_out, n_in, L.OUTP, L.INP, kb.n_t, c, ws, kPermFM, s);
+    if (rc) return rc;
+    if (kb.n_t <= 8) return pick_f_lanes<T, 8>(kb, batch, n_in, n_out, x, w, ws, y, L.OUTP, L.INP, s);
+    return pick_f_lanes<T, 16>(kb, batch, n_in, n_out, x, w, ws, y, L.OUTP, L.INP, s);
+  }
+  if (batch >= 1024 && f_streams(kb, n_in, n_out)) {
+    if (kb.K <= 4) return launch_f_stream<T, 4>(kb, batch, n_in, n_out, x, w, c, y, s);
+    if (kb.K <= 8) return launch_f_stream<T, 8>(kb, batch, n_in, n_out, x, w, c, y, s);
+    if (kb.K <= 12) return launch_f_stream<T, 12>(kb, batch, n_in, n_out, x, w, c, y, s);
+    return launch_f_stream<T, 16>(kb, batch, n_in, n_out, x, w, c, y, s);
+  }
   WsF L = ws_f(b, dtype, batch, n_in, n_out, weighted);
   char* base = (char*)ws;
   void* cfm = base;

@@ -2532,6 +2532,222 @@ __global__ __launch_bounds__(kThreads) void edge_kernel(KBasis bs, int B, int IN
   }
 }
 
+// F for narrow layers by row streaming, one thread per row b:
+//   y[b, o] = sum_{i, k} w[b, i] c[o, i, k] phi_k^(m)(x[b, i])
+// with phi from basis_features (the fold already applied, so c is read in its own (out, in, K)
+// layout, the same address for every lane: scalar loads). NARROW_OUT (OUT <= 8): the OUT sums
+// stay in registers while the inputs stream by. Otherwise (IN * KM <= 64): the row's features
+// stay in registers while the outputs stream by, through an LDS tile of 256 rows so that the
+// stores are whole rows.
+template <typename T, int KM, bool NARROW_OUT>
+__global__ __launch_bounds__(kThreads) void f_stream_kernel(KBasis bs, int B, int IN, int OUT, const T* __restrict__ x,
+                                                            const T* __restrict__ w, const T* __restrict__ c,
+                                                            T* __restrict__ y) {
+  constexpr int NT = KM + 8 < KF_MAX_NT ? KM + 8 : KF_MAX_NT;
+  const int K = bs.K;
+  const int b = blockIdx.x * kThreads + threadIdx.x;
+  const bool ok = b < B;
+  if constexpr (NARROW_OUT) {
+    // the block's rows arrive in chunks of 32 inputs through LDS (coalesced loads), each thread
+    // then walks its own row there
+    __shared__ float xs[kThreads][33], wsh[kThreads][33];
+    const int b0 = blockIdx.x * kThreads;
+    float acc[8];
+#pragma unroll
+    for (int o = 0; o < 8; ++o) acc[o] = 0.f;
+    for (int i0 = 0; i0 < IN; i0 += 32) {
+      const int ni = IN - i0 < 32 ? IN - i0 : 32;
+      __syncthreads();
+      for (int e = threadIdx.x; e < kThreads * 32; e += kThreads) {
+        const int r = e / 32, il = e % 32, bb = b0 + r;
+        const bool in = bb < B && il < ni;
+        xs[r][il] = in ? to_f32(x[(size_t)bb * IN + i0 + il]) : 0.f;
+        wsh[r][il] = in ? (w ? to_f32(w[(size_t)bb * IN + i0 + il]) : 1.f) : 0.f;
+      }
+      __syncthreads();
+    for (int il = 0; il < ni; ++il) {
+      const int i = i0 + il;
+      float phi[KM];
+      basis_features<KM, NT>(xs[threadIdx.x][il], wsh[threadIdx.x][il], i, bs, phi);
+#pragma unroll
+      for (int o = 0; o < 8; ++o) {
+        if (o >= OUT) break;
+        const T* cr = c + ((size_t)o * IN + i) * K;
+#pragma unroll
+        for (int k = 0; k < KM; ++k)
+          if (k < K) acc[o] = fmaf(to_f32(cr[k]), phi[k], acc[o]);
+      }
+    }
+    }
+    if (ok) {
+#pragma unroll
+      for (int o = 0; o < 8; ++o)
+        if (o < OUT) y[(size_t)b * OUT + o] = from_f32<T>(acc[o]);
+    }
+  } else {
+    // IN * KM <= 64 features of the row in registers
+    float phi[64];
+#pragma unroll
+    for (int q = 0; q < 64; ++q) phi[q] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 64 / KM; ++i) {
+      if (i >= IN) break;
+      const size_t off = (size_t)(ok ? b : 0) * IN + i;
+      float f[KM];
+      basis_features<KM, NT>(to_f32(x[off]), w ? to_f32(w[off]) : 1.f, i, bs, f);
+#pragma unroll
+      for (int k = 0; k < KM; ++k) phi[i * KM + k] = f[k];
+    }
+    __shared__ float tile[kThreads][65];
+    const int b0 = blockIdx.x * kThreads;
+    const int rows = B - b0 < kThreads ? B - b0 : kThreads;
+    for (int o0 = 0; o0 < OUT; o0 += 64) {
+      const int no = OUT - o0 < 64 ? OUT - o0 : 64;
+      for (int ol = 0; ol < no; ++ol) {
+        const T* cr = c + (size_t)(o0 + ol) * IN * K;
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 64 / KM; ++i) {
+          if (i >= IN) break;
+#pragma unroll
+          for (int k = 0; k < KM; ++k)
+            if (k < K) s = fmaf(to_f32(cr[i * K + k]), phi[i * KM + k], s);
+        }
+        tile[threadIdx.x][ol] = s;
+      }
+      __syncthreads();
+      // rows b0 .. b0 + rows, outputs o0 .. o0 + no: no consecutive elements per row
+      for (int e = threadIdx.x; e < rows * no; e += kThreads) {
+        const int r = e / no, ol = e % no;
+        y[(size_t)(b0 + r) * OUT + o0 + ol] = from_f32<T>(tile[r][ol]);
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// F for layers with at most 8 outputs over a Chebyshev-family basis, one lane per (row, input):
+//   y[b, o] = sum_{i, j} Cf[j, o, i] T_j(x[b, i]) (w and the map factor inside T_j)
+// with Cf the folded coefficients in their feature-major copy (OUTP x INP per feature j). A wave
+// covers 64 / L rows, L lanes (a power of two >= 8) per row and NC inputs per lane (IN <= L NC);
+// each lane keeps its inputs' coefficients in registers for the whole grid-stride loop, and a
+// row's sums are reduced over its L lanes by xor shuffles. Loads of x and w are coalesced rows.
+template <typename T, int KM, int L, int NC, int OM>
+__global__ __launch_bounds__(kThreads) void f_lanes_kernel(KBasis bs, int B, int IN, int OUT, const T* __restrict__ x,
+                                                           const T* __restrict__ w, const T* __restrict__ cf,
+                                                           T* __restrict__ y, int OUTP, int INP) {
+  constexpr int R = 64 / L;
+  const int lane = threadIdx.x & 63, il = lane % L, r = lane / L;
+  const int nt = bs.n_t;
+  float creg[NC][OM][KM];
+#pragma unroll
+  for (int q = 0; q < NC; ++q)
+#pragma unroll
+    for (int o = 0; o < OM; ++o)
+#pragma unroll
+      for (int j = 0; j < KM; ++j) {
+        const int i = il + q * L;
+        creg[q][o][j] = (i < IN && o < OUT && j < nt) ? to_f32(cf[((size_t)j * OUTP + o) * INP + i]) : 0.f;
+      }
+  const long nw = (long)gridDim.x * (kThreads / 64);
+  for (long b0 = ((long)blockIdx.x * (kThreads / 64) + threadIdx.x / 64) * R; b0 < B; b0 += nw * R) {
+    const long b = b0 + r;
+    float acc[OM];
+#pragma unroll
+    for (int o = 0; o < OM; ++o) acc[o] = 0.f;
+#pragma unroll
+    for (int q = 0; q < NC; ++q) {
+      const int i = il + q * L;
+      if (b < B && i < IN) {
+        const size_t off = (size_t)b * IN + i;
+        float f[KM];
+#pragma unroll
+        for (int j = 0; j < KM; ++j) f[j] = 0.f;
+        kernel_features<KM>(to_f32(x[off]), w ? to_f32(w[off]) : 1.f, i, bs, f);
+#pragma unroll
+        for (int o = 0; o < OM; ++o)
+#pragma unroll
+          for (int j = 0; j < KM; ++j) acc[o] = fmaf(creg[q][o][j], f[j], acc[o]);
+      }
+    }
+#pragma unroll
+    for (int o = 0; o < OM; ++o)
+#pragma unroll
+      for (int off = L / 2; off > 0; off >>= 1) acc[o] += __shfl_xor(acc[o], off);
+    float v = acc[0];
+#pragma unroll
+    for (int o = 1; o < OM; ++o)
+      if (il == o) v = acc[o];
+    if (b < B && il < OUT) y[(size_t)b * OUT + il] = from_f32<T>(v);
+  }
+}
+
+// edge_derivative for layers at least 32 inputs wide, float32: the same block of ROWS rows x 32
+// inputs with the features in LDS, but each thread owns 4 consecutive inputs of OG4 outputs and
+// writes them as one 16-byte non-temporal store (IN % 4 == 0 and out 16-byte aligned).
+template <int KM>
+__global__ __launch_bounds__(kThreads) void edge4_kernel(KBasis bs, int B, int IN, int OUT, const float* __restrict__ x,
+                                                         const float* __restrict__ c, const float* __restrict__ bw,
+                                                         float* __restrict__ out) {
+  constexpr int ROWS = 32, IT = 32, OG4 = 2, NGRP = kThreads / 8;
+  constexpr int FS = (KM + 1) | 1;
+  __shared__ float feat[ROWS][IT][FS];
+  const int b0 = blockIdx.y * ROWS, i0 = blockIdx.x * IT;
+  const int tid = threadIdx.x;
+  const int K = bs.K, m = bs.order;
+  for (int e = tid; e < ROWS * IT; e += kThreads) {
+    const int r = e / IT, il = e % IT;
+    const int b = b0 + r, i = i0 + il;
+    const bool ok = b < B && i < IN;
+    const float xv = ok ? x[(size_t)b * IN + i] : 0.f;
+    float phi[KM];
+    basis_features<KM, (KM + 8 < KF_MAX_NT ? KM + 8 : KF_MAX_NT)>(xv, 1.f, ok ? i : 0, bs, phi);
+#pragma unroll
+    for (int k = 0; k < KM; ++k) feat[r][il][k] = ok ? phi[k] : 0.f;
+    feat[r][il][KM] = (ok && bw) ? silu_derivative(xv, m) : 0.f;
+  }
+  __syncthreads();
+  const int q = tid % 8, grp = tid / 8, il0 = 4 * q, i = i0 + il0;
+  if (i >= IN) return;  // IN % 4 == 0: the thread's 4 inputs exist together
+  const int rows = B - b0 < ROWS ? B - b0 : ROWS;
+  const int n_og = (OUT + OG4 - 1) / OG4;
+  for (int og = grp; og < n_og; og += NGRP) {
+    float cv[OG4][4][KM], wv[OG4][4];
+#pragma unroll
+    for (int u = 0; u < OG4; ++u) {
+      const int o = og * OG4 + u;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+#pragma unroll
+        for (int k = 0; k < KM; ++k) cv[u][v][k] = (o < OUT && k < K) ? c[((size_t)o * IN + i + v) * K + k] : 0.f;
+        wv[u][v] = (o < OUT && bw) ? bw[(size_t)o * IN + i + v] : 0.f;
+      }
+    }
+    for (int r = 0; r < rows; ++r) {
+      const int b = b0 + r;
+      float fv[4][KM + 1];
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+#pragma unroll
+        for (int k = 0; k <= KM; ++k) fv[v][k] = feat[r][il0 + v][k];
+#pragma unroll
+      for (int u = 0; u < OG4; ++u) {
+        const int o = og * OG4 + u;
+        if (o >= OUT) break;
+        f32x4 sv;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          float a = wv[u][v] * fv[v][KM];
+#pragma unroll
+          for (int k = 0; k < KM; ++k) a = fmaf(cv[u][v][k], fv[v][k], a);
+          sv[v] = a;
+        }
+        __builtin_nontemporal_store(sv, reinterpret_cast<f32x4*>(out + ((size_t)b * OUT + o) * IN + i));
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 static __global__ __launch_bounds__(kThreads) void interval_kernel(long n, int IN, const float* __restrict__ x,
                                                             const float* __restrict__ kc, int nk,

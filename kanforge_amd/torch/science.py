@@ -1,12 +1,24 @@
-"""PINN derivatives of a field u(x) kept in the autograd graph
-(kanforge/torch/science.py:25-46). Through KAN layers every node of these
-graphs is an F, G or P launch of the HIP kernels."""
+"""PINN derivatives of a field u(x) kept in the autograd graph (kanforge/torch/science.py:25-46).
+
+``derivative``, ``gradient`` and ``laplacian`` accept any callable, as in the reference, and
+differentiate it with autograd (through KAN layers every node is an F, G or P launch of the HIP
+kernels). For a chain of KAN layers (``KAN``, or an ``nn.Sequential`` of ``KANLinear`` with SiLU or
+no base branch) ``laplacian`` instead propagates second-order Taylor coefficients forward: per
+layer and input dimension d, with h' = dh/dx_d and h'' = d2h/dx_d2,
+    h_out   = F_0(h, c) + W silu(h) + b
+    h'_out  = F_1(h, c, w=h')                       + W (silu'(h) h')
+    h''_out = F_2(h, c, w=h'^2) + F_1(h, c, w=h'')  + W (silu''(h) h'^2 + silu'(h) h'')
+with the rows of every dimension stacked into one F launch per derivative order. The result is
+the same function of x and of the parameters, and stays differentiable (F's own autograd).
+"""
 
 from __future__ import annotations
 
 from collections.abc import Callable
 
 import torch
+import torch.nn.functional as F
+from torch import nn
 
 
 def derivative(fn: Callable, x: torch.Tensor, order: int = 1, dim: int = 0) -> torch.Tensor:
@@ -27,7 +39,86 @@ def gradient(fn: Callable, x: torch.Tensor) -> torch.Tensor:
 
 
 def laplacian(fn: Callable, x: torch.Tensor) -> torch.Tensor:
-    """(N,) sum of second derivatives of u = fn(x)."""
+    """(N,) sum of second derivatives of u = fn(x); forward-mode for chains of KAN layers."""
+    layers = kan_chain(fn)
+    if layers is not None and x.dim() == 2:
+        return _laplacian_forward(layers, x)
     x = x if x.requires_grad else x.detach().requires_grad_()
     g = gradient(fn, x)
     return sum(torch.autograd.grad(g[:, k].sum(), x, create_graph=True)[0][:, k] for k in range(x.shape[1]))
+
+
+def kan_chain(fn) -> list | None:
+    """The KANLinear layers of ``fn`` when it is exactly a chain of them whose edges the Taylor
+    pass covers (SiLU or no base branch, no symbolic edges, no edge dropout in training), else
+    None."""
+    from .layers import KANLinear
+
+    if isinstance(fn, KANLinear):
+        mods = [fn]
+    elif isinstance(fn, nn.Sequential):
+        mods = list(fn)
+    else:
+        return None
+    for m in mods:
+        if not isinstance(m, KANLinear):
+            return None
+        if m.base_weight is not None and m.base_activation is not F.silu:
+            return None
+        if m._sym_codes or (m.training and m.edge_dropout > 0):
+            return None
+    return mods
+
+
+def _silu_terms(h: torch.Tensor):
+    """(silu(h), silu'(h), silu''(h)) with s = sigmoid(h)."""
+    s = torch.sigmoid(h)
+    d1 = s * (1 + h * (1 - s))
+    d2 = s * (1 - s) * (2 + h * (1 - 2 * s))
+    return h * s, d1, d2
+
+
+def _taylor_layer(layer, h: torch.Tensor, hp: torch.Tensor, hpp: torch.Tensor | None):
+    """A layer's (h, h', h'') from its input's: h (B, in), hp and hpp (D, B, in) (hpp None: zero)."""
+    from . import kernels as K
+
+    D, B, n_in = hp.shape
+    st = layer._basis_state()
+    key = layer._plan_key
+    c = layer.effective_coef()
+    dt = c.dtype
+    hk = h.to(dt)
+    num = den = None
+    if layer._plan.kind == "rational":
+        num, den = layer.basis_numerator, layer.basis_denominator
+    # value
+    y = K.prim_F(hk, c, None, st, key, 0, num, den)
+    # first-order rows (h' of every dimension, then h'' of every dimension) in one launch
+    w1 = hp if hpp is None else torch.cat([hp, hpp], 0)
+    n1 = w1.shape[0]
+    f1 = K.prim_F(hk.repeat(n1, 1), c, w1.reshape(n1 * B, n_in).to(dt), st, key, 1, num, den).reshape(n1, B, -1)
+    f2 = K.prim_F(hk.repeat(D, 1), c, (hp * hp).reshape(D * B, n_in).to(dt), st, key, 2, num, den).reshape(D, B, -1)
+    yp = f1[:D]
+    ypp = f2 if hpp is None else f2 + f1[D:]
+    W = layer.effective_base_weight()
+    if W is not None:
+        s0, s1, s2 = _silu_terms(h)
+        y = y + F.linear(s0, W)
+        yp = yp + F.linear(s1 * hp, W)
+        base2 = s2 * hp * hp if hpp is None else s2 * hp * hp + s1 * hpp
+        ypp = ypp + F.linear(base2, W)
+    if layer.bias is not None:
+        y = y + layer.bias
+    return y.to(h.dtype), yp.to(h.dtype), ypp.to(h.dtype)
+
+
+def _laplacian_forward(layers, x: torch.Tensor) -> torch.Tensor:
+    B, D = x.shape
+    h = x
+    hp = torch.eye(D, dtype=x.dtype, device=x.device)[:, None, :].expand(D, B, D)  # dx/dx_d
+    hpp = None
+    for layer in layers:
+        h, hp, hpp = _taylor_layer(layer, h, hp, hpp)
+    if h.shape[-1] != 1:
+        raise ValueError(f"laplacian needs a scalar field, the network has {h.shape[-1]} outputs")
+    return hpp.sum(0)[:, 0]

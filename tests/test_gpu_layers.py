@@ -438,3 +438,31 @@ def test_kanify_exact_keeps_outputs_and_katblock_runs():
         ref = ref + blk.ffn(blk.norm2(ref))
     assert out.shape == z.shape
     torch.testing.assert_close(out, ref, rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("basis", [kf.Jacobi(6, 0.5, 0.5), kf.BSpline(5, 3)], ids=["jacobi6", "bspline53"])
+def test_forward_mode_laplacian_equals_reverse_mode_and_trains(basis):
+    """laplacian() on a KAN chain propagates Taylor coefficients forward (F with w); on any other
+    callable it differentiates twice with autograd (kanforge/torch/science.py:25-46). Both give
+    the same field and the same gradients of a PINN loss with respect to every parameter."""
+    torch.manual_seed(0)
+    model = KAN([2, 16, 16, 1], basis).to(DEV)
+    with torch.no_grad():
+        for layer in model:
+            layer.bias.normal_(0, 0.1)
+    x = torch.rand(500, 2, device=DEV) * 1.8 - 0.9
+    lap_f = laplacian(model, x)
+    lap_r = laplacian(lambda z: model(z), x)
+    err = o.normwise_err(np64(lap_f), np64(lap_r))
+    print(f"forward vs reverse laplacian {basis!r}: {err:.3e}", flush=True)
+    assert err <= 1e-5
+    params = [p for p in model.parameters()]
+    # (the last layer's bias does not enter second derivatives: no gradient in either mode)
+    g_f = torch.autograd.grad((lap_f**2).mean(), params, allow_unused=True)
+    g_r = torch.autograd.grad((laplacian(lambda z: model(z), x) ** 2).mean(), params, allow_unused=True)
+    for p, a, b in zip(params, g_f, g_r):
+        assert (a is None) == (b is None)
+        if a is not None:
+            e = o.normwise_err(np64(a), np64(b))
+            assert e <= 1e-5, (p.shape, e)
+    assert g_f[-1] is None  # model[-1].bias

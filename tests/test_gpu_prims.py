@@ -275,3 +275,25 @@ def test_uniform_grid_features_equal_the_general_path(k, m):
     np.testing.assert_allclose(fast, slow, rtol=0, atol=2e-6 * scale)
     want = o.Basis64("bspline", grid=grid, k=k)(x.astype(np.float64), m)
     np.testing.assert_allclose(fast, want, rtol=0, atol=1e-5 * max(1.0, np.abs(want).max()))
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16"])
+@pytest.mark.parametrize("shape", [(2048, 2, 64), (1500, 64, 1), (1300, 3, 40), (1100, 17, 5), (1024, 4, 70),
+                                   (1200, 8, 3), (1100, 100, 1), (1030, 96, 8), (1024, 200, 2)],
+                         ids=["2to64", "64to1", "3to40", "17to5", "4to70", "8to3", "100to1", "96to8", "200to2"])
+@pytest.mark.parametrize("name,m", [("jacobi6", 0), ("jacobi6", 1), ("jacobi6", 2), ("chebyshev5", 1), ("bspline53", 0), ("bspline53", 2)])
+def test_F_narrow_layers_stream_and_match_oracle(name, m, shape, dtype):
+    """Layers with at most 8 outputs or at most 4 inputs stream rows: Chebyshev-family layers with
+    at most 8 outputs and 128 inputs one lane per (row, input) with 16 or 64 lanes per row and one
+    or two inputs per lane, the rest one thread per row with the fold in registers; weighted and
+    unweighted, against the oracle."""
+    B, IN, OUT = shape
+    basis, plan, st, ob, x, rng = setup(name, B, IN)
+    Kb = basis.size
+    c = rng.normal(0, 1 / math.sqrt(IN * Kb), (OUT, IN, Kb))
+    for weighted in (False, True):
+        w = rng.uniform(0.5, 1.5, (B, IN)) if weighted else None
+        y = K._raw("F", plan, m, to_dev(x, dtype), None if w is None else to_dev(w, dtype), to_dev(c, dtype), st, OUT)
+        want = o.prim_F(rounded(x, dtype), rounded(c, dtype), None if w is None else rounded(w, dtype), ob, m)
+        e = err(y, want)
+        assert e <= TOL[dtype], (name, m, weighted, e)
