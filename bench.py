@@ -2,11 +2,19 @@
 bfloat16 with float32 accumulation, batch 8192; one step = forward + dX + dCoef
 (the F_0, P_1 and G_0 launches of the HIP path). Prints one JSON line.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-base]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-base] [--no-workloads]
     python bench.py --workload {bspline_ffn,grkan_ffn,pinn_edge,pinn_laplacian,kan64,all}
+    python bench.py --workload NAME --only {F,G,P,edge,...} --steps N
 
-The second form times the other layer shapes instead of the headline, one JSON
-line each (whole-step throughput and HIP-event means per entry point).
+The headline line carries a ``workloads`` object with one entry per other layer
+shape (KANLinear 64->64 B-spline fp32, GR-KAN FFN, PINN edge derivatives, PINN
+Laplacian, B-spline FFN): step time, throughput, the roofline of the entry
+point with the most GPU time (per-call algorithmic FLOP and bytes over HIP-event
+durations; bound by whichever of MFMA and HBM time is larger) and a torch-CPU
+baseline on a stated sample. The second form prints those lines on their own.
+The third form is for counter runs: one step records the calls of one entry
+point, a one-block probe kernel marks the end of that step in the dispatch
+trace, then only those calls are replayed.
 
 Inputs are seeded synthetic tensors resident in HBM before timing starts:
 x ~ N(0, 1) (seed 0), coef ~ N(0, 1/(768*9)) (seed 1), upstream gradient
@@ -49,45 +57,132 @@ def parse():
         choices=["cheb768", *WORKLOADS, "all"],
         help="cheb768 (default) is the headline line; the others time the remaining layer shapes one line each",
     )
+    ap.add_argument("--no-workloads", action="store_true", help="leave the other layer shapes out of the headline line")
+    ap.add_argument("--workload-steps", type=int, default=10, help="timed steps of each other layer shape in the headline line")
+    ap.add_argument("--only", choices=["F", "G", "P", "edge", "features", "rational_param_grad"],
+                    help="counter runs: replay only this entry point's calls of one step of --workload")
     return ap.parse_args()
 
 
+PEAK_FP32 = 157.3e12  # MI355X dense fp32 MFMA, FLOP/s
+PEAK_HBM = 8.0e12  # MI355X HBM3E, bytes/s
+
+
+def _work(label, args):
+    """Algorithmic (FLOP, HBM bytes) of one entry-point call: contractions count 2 B in K out
+    FLOP (dense over the basis, the reference's convention); bytes count every operand read once
+    and every output written once."""
+    if label in ("F", "G", "P"):
+        _, plan, _m, x, a, b, _st, n_out = args[:8]
+        h = args[8] if len(args) > 8 else None
+        batch, n_in = x.shape
+        es, K = x.element_size(), plan.size
+        flops = 2.0 * batch * n_in * K * n_out
+        coef = n_out * n_in * K
+        if label == "F":
+            elems = batch * n_in * (1 + (a is not None)) + coef + batch * n_out
+        elif label == "G":
+            elems = batch * n_in * (1 + (a is not None)) + batch * n_out + coef
+        else:
+            elems = 2 * batch * n_in + batch * n_out + coef
+        return flops, es * elems + (4.0 * batch * n_in if h is not None else 0.0)
+    if label == "edge":
+        plan, _m, _st, x2, c, base_w = args[:6]
+        batch, n_in = x2.shape
+        n_out, es, K = c.shape[0], x2.element_size(), plan.size
+        elems = batch * n_in + n_out * n_in * K + (0 if base_w is None else n_out * n_in) + batch * n_out * n_in
+        return 2.0 * batch * n_in * K * n_out, float(es * elems)
+    if label == "features":
+        plan, _m, _st, x2 = args[:4]
+        batch, n_in = x2.shape
+        return 0.0, float(x2.element_size() * batch * n_in * (1 + plan.size))
+    if label == "rational_param_grad":
+        _plan, _st, x, h, w = args[:5]
+        n = x.numel()
+        return 0.0, float(n * (x.element_size() + 4 + (0 if w is None else w.element_size())))
+    return 0.0, 0.0
+
+
 class EntryTimer:
-    """HIP events around every F/G/P entry point, on the launch stream."""
+    """HIP events around every entry-point call, on the launch stream, with each call's
+    algorithmic work; ``record`` keeps the calls of one entry for replay."""
 
     def __init__(self):
         self.active = False
-        self.events = {"F": [], "G": [], "P": []}
+        self.events = {}
+        self.record = None  # (label, list) while recording one entry's calls
 
     def wrap(self, raw, label=None):
         def timed(*args, **kwargs):
+            lab = label or args[0]
+            if self.record is not None and self.record[0] == lab:
+                self.record[1].append((raw, args, kwargs))
             if not self.active:
                 return raw(*args, **kwargs)
+            stream = torch.cuda.current_stream()
             s = torch.cuda.Event(enable_timing=True)
             e = torch.cuda.Event(enable_timing=True)
-            s.record()
+            s.record(stream)
             out = raw(*args, **kwargs)
-            e.record()
-            self.events.setdefault(label or args[0], []).append((s, e))
+            e.record(stream)
+            self.events.setdefault(lab, []).append((s, e) + _work(lab, args))
             return out
 
         return timed
 
     def mean_ms(self):
-        return {op: (sum(s.elapsed_time(e) for s, e in ev) / len(ev) if ev else 0.0) for op, ev in self.events.items()}
+        return {op: (sum(ev[0].elapsed_time(ev[1]) for ev in evs) / len(evs) if evs else 0.0) for op, evs in self.events.items()}
 
     def count(self):
         return {op: len(ev) for op, ev in self.events.items()}
+
+    def totals(self):
+        """Per entry: (total ms, total FLOP, total bytes, calls) over the timed region."""
+        return {
+            op: (sum(ev[0].elapsed_time(ev[1]) for ev in evs), sum(ev[2] for ev in evs), sum(ev[3] for ev in evs), len(evs))
+            for op, evs in self.events.items()
+        }
+
+
+def roofline_of(totals, dtype, traffic_file=None):
+    """Roofline of the entry point with the most GPU time: bound by whichever of MFMA time
+    (algorithmic FLOP at the dtype's dense peak) and HBM time (algorithmic bytes at 8 TB/s) is
+    larger; achieved = that work over the entry's measured time (sums over its calls)."""
+    op = max(totals, key=lambda k: totals[k][0])
+    ms, flops, nbytes, calls = totals[op]
+    peak_f = PEAK_BF16 if dtype == "bf16" else PEAK_FP32
+    sec = ms * 1e-3
+    if flops / peak_f >= nbytes / PEAK_HBM:
+        achieved, peak, unit, bound = flops / sec / 1e12, peak_f / 1e12, "TFLOP/s", "mfma"
+    else:
+        achieved, peak, unit, bound = nbytes / sec / 1e9, PEAK_HBM / 1e9, "GB/s", "hbm"
+    traffic = measured_traffic(f"kf_{op}", traffic_file) if traffic_file else None
+    return {
+        "bound": bound,
+        "kernel": f"kf_{op}",
+        "achieved": achieved,
+        "peak": peak,
+        "unit": unit,
+        "frac": achieved / peak,
+        "traffic": traffic,
+        "traffic_unit": "bytes per launch",
+        "traffic_source": traffic_file if traffic is not None else None,
+        "launches_per_step": None,
+        "algorithmic_flop_per_launch": flops / calls,
+        "algorithmic_bytes_per_launch": nbytes / calls,
+        "ms_per_launch": ms / calls,
+    }
 
 
 TRAFFIC_FILE = os.path.join("profiles", "kanlinear_768x3072_cheb8_bf16_hbm_traffic.md")
 
 
-def measured_traffic(entry):
-    """HBM bytes per launch of one entry point, from the committed counter summary
-    (FETCH_SIZE and WRITE_SIZE passes scaled by a plain copy's readings); None if absent."""
+def measured_traffic(entry, path=TRAFFIC_FILE):
+    """HBM bytes per launch of one entry point, from a committed counter summary (FETCH_SIZE and
+    WRITE_SIZE passes scaled by a plain copy's readings; the per-entry table's last column);
+    None if absent."""
     try:
-        lines = open(os.path.join(ROOT, TRAFFIC_FILE)).read().splitlines()
+        lines = open(os.path.join(ROOT, path)).read().splitlines()
     except OSError:
         return None
     for line in lines:
@@ -163,6 +258,29 @@ def _randn(shape, seed, scale=1.0):
     return torch.randn(*shape, generator=torch.Generator().manual_seed(seed)) * scale
 
 
+def _cpu_rows(default):
+    return int(os.environ.get("KF_CPU_ROWS_SCALE", "1") or 1) * default
+
+
+def _cpu_train(layers, x, gy, rows, unit, what):
+    """CPU leg: the torch-CPU plain route on the first ``rows`` rows of the same inputs."""
+    from oracle import torch_cpu as tc
+
+    dtype = x.dtype
+    cl = [tc.CpuLayer(layer, dtype) for layer in layers]
+    xs = x.detach()[:rows].cpu()
+    gs = gy.detach()[:rows].cpu()
+    t, threads = tc.time_train_step(cl, xs.reshape(-1, xs.shape[-1]), gs.reshape(-1, gs.shape[-1]))
+    n = xs.reshape(-1, xs.shape[-1]).shape[0]
+    return _cpu_line(n / t, unit, threads, f"{n} rows of the same inputs: {what}, torch-CPU plain route, median of 3 after 1 warm-up")
+
+
+def _cpu_line(value, unit, threads, sample):
+    from oracle.torch_cpu import cpu_isa, cpu_model
+
+    return {"value": value, "unit": unit, "cores": threads, "kind": "port", "sample": sample, "cpu": cpu_model(), "isa": cpu_isa()}
+
+
 def wl_bspline_ffn(dev):
     """kanify'd GPT-2-small FFN: KANLinear 768->3072 then 3072->768, B-spline grid 8 order 3
     (K=11), layer defaults (SiLU base, bias), bf16, 8 x 2048 tokens, forward + backward."""
@@ -181,8 +299,10 @@ def wl_bspline_ffn(dev):
     def step():
         return torch.autograd.grad(ffn(x), params, gy)
 
-    per_contraction = 2.0 * tok * dim * k * hid
-    return step, tok, "tokens/s", 6 * per_contraction + 6 * 2.0 * tok * dim * hid, per_contraction, "bf16"
+    def cpu():
+        return _cpu_train([ffn.fc1, ffn.fc2], x.reshape(-1, dim), gy.reshape(-1, dim), _cpu_rows(1024), "tokens/s", "B-spline FFN fwd+bwd, bf16")
+
+    return step, tok, "tokens/s", "bf16", cpu
 
 
 def wl_grkan_ffn(dev):
@@ -190,7 +310,8 @@ def wl_grkan_ffn(dev):
     16 x 1024 tokens, P/Q ~ N(0, 0.1), forward + backward."""
     from kanforge_amd.torch.transformer import KANFFN
 
-    tok, dim, hid = 16 * 1024, 768, 3072
+    dim, hid = 768, 3072
+    tok = 16 * 1024
     ffn = KANFFN(dim, hid, kind="grkan", groups=8).to(dev, torch.bfloat16)
     with torch.no_grad():
         for i, layer in enumerate((ffn.fc1, ffn.fc2)):
@@ -203,8 +324,10 @@ def wl_grkan_ffn(dev):
     def step():
         return torch.autograd.grad(ffn(x), params, gy)
 
-    per_gemm = 2.0 * tok * dim * hid
-    return step, tok, "tokens/s", 6 * per_gemm, per_gemm, "bf16"
+    def cpu():
+        return _cpu_train([ffn.fc1, ffn.fc2], x.reshape(-1, dim), gy.reshape(-1, dim), _cpu_rows(4096), "tokens/s", "GR-KAN FFN fwd+bwd incl. P/Q grads, bf16")
+
+    return step, tok, "tokens/s", "bf16", cpu
 
 
 def _pinn_model(dev):
@@ -228,15 +351,19 @@ def wl_pinn_edge(dev):
         with torch.no_grad():
             return model.edge_derivative(x, 2)
 
-    n = x.shape[0]
-    out_bytes = 4.0 * n * (64 * 2 + 64 * 64 + 1 * 64)
-    in_bytes = 4.0 * n * (2 + 64 + 64)
-    return step, n, "points/s", None, out_bytes + in_bytes, "f32"
+    def cpu():
+        from oracle import torch_cpu as tc
+
+        rows = _cpu_rows(16384)
+        t, threads = tc.time_edge_step([tc.CpuLayer(m, torch.float32) for m in model], x[:rows].cpu())
+        return _cpu_line(rows / t, "points/s", threads, f"{rows} of the points: every layer's second edge derivatives by autograd over the basis, fp32, torch-CPU plain route, median of 3 after 1 warm-up")
+
+    return step, x.shape[0], "points/s", "f32", cpu
 
 
 def wl_pinn_laplacian(dev):
-    """The same PINN network: the chained Laplacian d2u/dx0^2 + d2u/dx1^2 over the
-    network by reverse-over-reverse autograd through the F/G/P closure."""
+    """The same PINN network: the Laplacian d2u/dx0^2 + d2u/dx1^2 of the network output
+    (kanforge_amd.torch.laplacian: second-order Taylor terms carried forward through F)."""
     from kanforge_amd.torch import laplacian
 
     model, x = _pinn_model(dev)
@@ -244,9 +371,14 @@ def wl_pinn_laplacian(dev):
     def step():
         return laplacian(model, x)
 
-    n = x.shape[0]
-    layer_pass = 2.0 * n * 7 * (2 * 64 + 64 * 64 + 64)
-    return step, n, "points/s", None, layer_pass, "f32"
+    def cpu():
+        from oracle import torch_cpu as tc
+
+        rows = _cpu_rows(65536)
+        t, threads = tc.time_laplacian_step([tc.CpuLayer(m, torch.float32) for m in model], x[:rows].cpu())
+        return _cpu_line(rows / t, "points/s", threads, f"{rows} of the points: Laplacian by reverse-over-reverse autograd, fp32, torch-CPU plain route, median of 3 after 1 warm-up")
+
+    return step, x.shape[0], "points/s", "f32", cpu
 
 
 def wl_kan64(dev):
@@ -265,36 +397,49 @@ def wl_kan64(dev):
     def step():
         return torch.autograd.grad(layer(x), params, gy)
 
-    per_contraction = 2.0 * 4096 * 64 * 8 * 64
-    return step, 4096, "samples/s", 3 * per_contraction + 3 * 2.0 * 4096 * 64 * 64, per_contraction, "f32"
+    def cpu():
+        return _cpu_train([layer], x, gy, 4096, "samples/s", "the whole batch, fwd+bwd, fp32")
+
+    return step, 4096, "samples/s", "f32", cpu
 
 
 WORKLOADS = {
-    "bspline_ffn": wl_bspline_ffn,
+    "kan64": wl_kan64,
     "grkan_ffn": wl_grkan_ffn,
     "pinn_edge": wl_pinn_edge,
     "pinn_laplacian": wl_pinn_laplacian,
-    "kan64": wl_kan64,
+    "bspline_ffn": wl_bspline_ffn,
 }
 
 
-def run_workload(name, args, dev):
-    """One JSON line for a non-headline layer shape: whole-step throughput plus HIP-event
-    means of every entry point it calls (F, G, P, edge, features)."""
+def traffic_file(name):
+    return os.path.join("profiles", f"{name}_hbm_traffic.md")
+
+
+def _hook_entries(timer):
     from kanforge_amd.torch import kernels as kmod
 
+    names = ("_raw", None), ("_edge_raw", "edge"), ("_features_raw", "features"), ("_rational_param_grad", "rational_param_grad")
+    orig = {n: getattr(kmod, n) for n, _ in names}
+    for n, lab in names:
+        setattr(kmod, n, timer.wrap(orig[n], lab))
+    return lambda: [setattr(kmod, n, f) for n, f in orig.items()]
+
+
+def run_workload(name, args, dev, cpu=True):
+    """One layer shape: whole-step throughput, HIP-event means of every entry point it calls,
+    the roofline of the entry with the most GPU time and the CPU leg."""
     timer = EntryTimer()
-    timer.events = {}
-    orig = kmod._raw, kmod._edge_raw, kmod._features_raw
-    kmod._raw = timer.wrap(orig[0])
-    kmod._edge_raw = timer.wrap(orig[1], "edge")
-    kmod._features_raw = timer.wrap(orig[2], "features")
+    unhook = _hook_entries(timer)
     try:
-        step, units, unit, step_flop, per_launch, dtype = WORKLOADS[name](dev)
+        step, units, unit, dtype, cpu_leg = WORKLOADS[name](dev)
         ms = _timed(step, args.steps, args.warmup, timer)
     finally:
-        kmod._raw, kmod._edge_raw, kmod._features_raw = orig
-    per_op, calls = timer.mean_ms(), timer.count()
+        unhook()
+    per_op, calls, totals = timer.mean_ms(), timer.count(), timer.totals()
+    roof = roofline_of(totals, dtype, traffic_file(name))
+    roof["launches_per_step"] = calls[roof["kernel"][3:]] / args.steps
+    flops = sum(v[1] for v in totals.values()) / args.steps
     line = {
         "metric": f"{name} throughput",
         "value": units / (ms * 1e-3),
@@ -309,18 +454,65 @@ def run_workload(name, args, dev):
         "config": {"workload": WORKLOADS[name].__doc__.split("\n\n")[0].replace("\n", " ").strip()},
         "per_entry_ms": per_op,
         "calls_per_step": {k: v / args.steps for k, v in calls.items()},
+        "contraction_tflops": flops / (ms * 1e-3) / 1e12,
+        "roofline": roof,
     }
-    if step_flop is not None:
-        line["tflops"] = step_flop / (ms * 1e-3) / 1e12
-        line["frac_of_bf16_peak" if dtype == "bf16" else "frac_of_fp32_peak"] = (
-            step_flop / (ms * 1e-3) / (PEAK_BF16 if dtype == "bf16" else 157.3e12)
-        )
-    if name == "pinn_edge":
-        line["hbm_gbs"] = per_launch / (ms * 1e-3) / 1e9
-        line["frac_of_hbm_peak"] = per_launch / (ms * 1e-3) / 8.0e12
-    elif name == "pinn_laplacian":
-        line["layer_pass_gflop"] = per_launch / 1e9
+    if cpu:
+        line["cpu_baseline"] = cpu_leg()
     return line
+
+
+def run_only(name, entry, args, dev):
+    """Counter-run mode: one full step records the calls of ``entry``, a one-block probe kernel
+    marks the end of it in the dispatch trace, then only those calls run ``args.steps`` times."""
+    import ctypes
+
+    from kanforge_amd.torch import _lib
+
+    timer = EntryTimer()
+    rec = []
+    timer.record = (entry, rec)
+    unhook = _hook_entries(timer)
+    try:
+        step, *_ = WORKLOADS[name](dev) if name != "cheb768" else (headline_step(dev),)
+        step()
+    finally:
+        unhook()
+    torch.cuda.synchronize()
+    lib = _lib.load()
+    mark = torch.empty(256 * 3, dtype=torch.float32, device=dev)
+    _lib.check(lib.kf_probe_mfma(1, 1, 0, ctypes.c_void_p(mark.data_ptr()), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "marker")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        for fn, a, kw in rec:
+            fn(*a, **kw)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    return {"workload": name, "entry": entry, "calls_per_replay": len(rec), "replays": args.steps, "ms_per_replay": ms}
+
+
+def headline_layer(dev):
+    import kanforge_amd as kf
+    from kanforge_amd.torch import KANLinear
+
+    layer = KANLinear(IN, OUT, kf.Chebyshev(DEGREE), base_activation=None, bias=False, device=dev, dtype=torch.bfloat16)
+    gen = torch.Generator().manual_seed(1)
+    with torch.no_grad():
+        layer.coef.copy_((torch.randn(OUT, IN, K, generator=gen) / math.sqrt(IN * K)).to(torch.bfloat16))
+    x = torch.randn(B, IN, generator=torch.Generator().manual_seed(0)).to(dev, torch.bfloat16).requires_grad_()
+    gy = torch.randn(B, OUT, generator=torch.Generator().manual_seed(3)).to(dev, torch.bfloat16)
+    return layer, x, gy
+
+
+def headline_step(dev):
+    layer, x, gy = headline_layer(dev)
+
+    def step():
+        y = layer(x)
+        return torch.autograd.grad(y, [x, layer.coef], gy)
+
+    return step
 
 
 def main():
@@ -334,24 +526,20 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.only:
+        print(json.dumps(run_only(args.workload, args.only, args, dev)), flush=True)
+        return
     if args.workload != "cheb768":
         for name in WORKLOADS if args.workload == "all" else [args.workload]:
-            print(json.dumps(run_workload(name, args, dev)), flush=True)
+            print(json.dumps(run_workload(name, args, dev, cpu=not args.no_cpu)), flush=True)
         return
 
     import kanforge_amd as kf
     from kanforge_amd.torch import KANLinear
-    from kanforge_amd.torch import kernels as kmod
 
     timer = EntryTimer()
-    kmod._raw = timer.wrap(kmod._raw)
-
-    layer = KANLinear(IN, OUT, kf.Chebyshev(DEGREE), base_activation=None, bias=False, device=dev, dtype=torch.bfloat16)
-    gen = torch.Generator().manual_seed(1)
-    with torch.no_grad():
-        layer.coef.copy_((torch.randn(OUT, IN, K, generator=gen) / math.sqrt(IN * K)).to(torch.bfloat16))
-    x = torch.randn(B, IN, generator=torch.Generator().manual_seed(0)).to(dev, torch.bfloat16).requires_grad_()
-    gy = torch.randn(B, OUT, generator=torch.Generator().manual_seed(3)).to(dev, torch.bfloat16)
+    unhook = _hook_entries(timer)
+    layer, x, gy = headline_layer(dev)
 
     def step():
         y = layer(x)
@@ -367,6 +555,7 @@ def main():
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     timer.active = False
+    unhook()
 
     ms = elapsed / args.steps * 1e3
     per_op = timer.mean_ms()
@@ -396,6 +585,7 @@ def main():
             "ms_per_step": ms_base,
             "value": B / (ms_base * 1e-3),
             "tflops": (STEP_FLOP + 3 * 2.0 * B * IN * OUT) / (ms_base * 1e-3) / 1e12,
+            "ratio_to_pure_step": ms_base / ms,
         }
     dominant = max(per_op, key=per_op.get)
     achieved = FLOP_PER_CONTRACTION / (per_op[dominant] * 1e-3) / 1e12
@@ -442,6 +632,15 @@ def main():
     out["mfma_probe"] = mfma_probe(dev)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
+    if not args.no_workloads:
+        sub = argparse.Namespace(steps=args.workload_steps, warmup=3)
+        out["workloads"] = {}
+        for name in WORKLOADS:
+            line = run_workload(name, sub, dev, cpu=not args.no_cpu)
+            keep = ("value", "unit", "dtype", "ms_per_step", "steps", "config", "per_entry_ms", "calls_per_step",
+                    "contraction_tflops", "roofline", "cpu_baseline")
+            out["workloads"][name] = {k: line[k] for k in keep if k in line}
+            torch.cuda.empty_cache()
     print(json.dumps(out), flush=True)
 
 
