@@ -12,6 +12,7 @@
 #include <utility>
 
 #include "kf_kernels.h"
+#include "kf_sparse.h"
 
 namespace kfabi {
 
@@ -244,6 +245,36 @@ inline WsP ws_p(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64
   w.total = w.cfmt + w.gpad + w.hbuf + w.gemm;
   return w;
 }
+constexpr size_t kSpGBytes = size_t(256) << 20;  // cap of the sparse G partial sums
+// fp32 B-spline layers of degree <= 3 contract over the k + 1 non-zero splines of each (row,
+// input): f_sparse_kernel, p_sparse_kernel, g_sparse_kernel (+ g_sparse_reduce)
+inline bool bspline_sparse(const kf_basis* b, int dtype) {
+  return b->kind == KF_KIND_BSPLINE && dtype == KF_F32 && b->spline_k >= 0 && b->spline_k <= 3 && b->size <= kSpKMax;
+}
+
+// G's row slices for the sparse kernels: about 512 workgroups, slices of whole 64-row groups,
+// float partial sums capped at kSpGBytes
+struct SpG {
+  int nz, RS;
+  size_t part;
+};
+inline SpG sparse_g_plan(int64_t batch, int64_t n_in, int64_t n_out, int K) {
+  const long base = (long)((n_in + 3) / 4) * (long)((n_out + 63) / 64);
+  long nz = (512 + base - 1) / base;
+  const long groups = (long)((batch + 63) / 64);
+  if (nz > groups) nz = groups;
+  const size_t per = (size_t)n_out * n_in * K * sizeof(float);
+  if (nz > 1 && (size_t)nz * per > kSpGBytes) nz = (long)(kSpGBytes / per);
+  if (nz < 1) nz = 1;
+  const long rs = ((batch + nz - 1) / nz + 63) / 64 * 64;
+  SpG p;
+  p.RS = (int)(rs > 0 ? rs : 64);
+  p.nz = (int)((batch + p.RS - 1) / p.RS);
+  if (p.nz < 1) p.nz = 1;
+  p.part = align256((size_t)p.nz * per);
+  return p;
+}
+
 struct WsG {
   int cfg;
   bool skip0;  // Chebyshev, unweighted: T_0 = 1 taken out of the contraction (column sums of g)
@@ -259,6 +290,11 @@ constexpr long kGSplitMax = 64;                      // cap of the batch splits
 constexpr int kGdmaFW = 4, kGdmaRows = 2 * kGdmaFW * 32;  // G on p_dma_kernel: phiT rows per tile
 inline WsG ws_g(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, bool has_w) {
   WsG w;
+  if (bspline_sparse(b, dtype)) {
+    w = WsG{};
+    w.total = sparse_g_plan(batch, n_in, n_out, b->size).part;
+    return w;
+  }
   const bool cheb_kind = b->kind == KF_KIND_CHEB;
   w.skip0 = cheb_kind && !has_w && b->n_t >= 2;
   w.cfg = fw_index(b->n_t - (w.skip0 ? 1 : 0));
@@ -317,6 +353,64 @@ inline WsG ws_g(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64
   if (dtype == KF_BF16 && b->kind == KF_KIND_BSPLINE) w.gemm = gemm_nt_workspace(n_out, n_in * b->size, w.BP);
   w.total = w.gt + w.zt + w.wt + w.part + w.colsum + w.phit + w.zpart + w.gemm;
   return w;
+}
+
+template <typename Fn>
+int with_spline_degree(int kd, Fn&& fn) {
+  switch (kd) {
+    case 0: return fn(std::integral_constant<int, 0>{});
+    case 1: return fn(std::integral_constant<int, 1>{});
+    case 2: return fn(std::integral_constant<int, 2>{});
+    case 3: return fn(std::integral_constant<int, 3>{});
+    default: return fail(KF_EINVAL, "sparse B-spline route: degree %d above 3", kd);
+  }
+}
+
+template <typename T>
+int launch_f_sparse(const KBasis& kb, int kd, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* w,
+                    const void* c, void* y, hipStream_t s) {
+  const dim3 grid((unsigned)((batch + kSpRows - 1) / kSpRows), (unsigned)((n_out + 63) / 64));
+  return with_spline_degree(kd, [&](auto tag) {
+    constexpr int KD = decltype(tag)::value;
+    hipLaunchKernelGGL((f_sparse_kernel<T, KD>), grid, dim3(512), 0, s, kb, (int)batch, (int)n_in, (int)n_out,
+                       (const T*)x, (const T*)w, (const T*)c, (T*)y);
+    return check_launch("F sparse");
+  });
+}
+
+template <typename T>
+int launch_p_sparse(const KBasis& kb, int kd, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* g,
+                    const void* c, void* p, hipStream_t s) {
+  const dim3 grid((unsigned)((batch + kSpRows - 1) / kSpRows), (unsigned)((n_in + 63) / 64));
+  return with_spline_degree(kd, [&](auto tag) {
+    constexpr int KD = decltype(tag)::value;
+    hipLaunchKernelGGL((p_sparse_kernel<T, KD>), grid, dim3(512), 0, s, kb, (int)batch, (int)n_in, (int)n_out,
+                       (const T*)x, (const T*)g, (const T*)c, (T*)p);
+    return check_launch("P sparse");
+  });
+}
+
+template <typename T>
+int launch_g_sparse(const KBasis& kb, int kd, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* g,
+                    const void* w, void* dc, void* ws, hipStream_t s) {
+  const SpG sp = sparse_g_plan(batch, n_in, n_out, kb.K);
+  const dim3 grid((unsigned)((n_in + 3) / 4), (unsigned)((n_out + 63) / 64), (unsigned)sp.nz);
+  int rc = with_spline_degree(kd, [&](auto tag) {
+    constexpr int KD = decltype(tag)::value;
+    if (kb.K <= 8)
+      hipLaunchKernelGGL((g_sparse_kernel<T, KD, 8>), grid, dim3(256), 0, s, kb, (int)batch, (int)n_in, (int)n_out,
+                         sp.RS, (const T*)x, (const T*)g, (const T*)w, (float*)ws);
+    else
+      hipLaunchKernelGGL((g_sparse_kernel<T, KD, kSpKMax>), grid, dim3(256), 0, s, kb, (int)batch, (int)n_in,
+                         (int)n_out, sp.RS, (const T*)x, (const T*)g, (const T*)w, (float*)ws);
+    return check_launch("G sparse");
+  });
+  if (rc) return rc;
+  const long n = (long)n_out * n_in * kb.K;
+  long blocks = (n + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(g_sparse_reduce<T>, dim3((unsigned)blocks), dim3(256), 0, s, sp.nz, n, (const float*)ws, (T*)dc);
+  return check_launch("G sparse reduce");
 }
 
 template <typename T>

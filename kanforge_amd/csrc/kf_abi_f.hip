@@ -181,6 +181,8 @@ int run_F(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
   const bool has_w = w != nullptr;
   const bool cheb = kb.kind == KF_KIND_CHEB;
   const bool weighted = features_weighted(b, w);
+  if constexpr (sizeof(T) == 4)
+    if (bspline_sparse(b, dtype)) return launch_f_sparse<T>(kb, b->spline_k, batch, n_in, n_out, x, w, c, y, s);
   const WsF LW = ws_f(b, dtype, batch, n_in, n_out, weighted);
   // the folded copy holds n_t features (the workspace is sized for at least n_tp of them)
   const bool lanes_ws = (size_t)kb.n_t * LW.OUTP * LW.INP * elt_size(dtype) <= LW.total;

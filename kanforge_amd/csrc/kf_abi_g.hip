@@ -116,6 +116,8 @@ int launch_g_dma(const WsG& L, hipStream_t s, const KBasis& kb, int64_t n_in, in
 template <typename T>
 int run_G(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
           const void* g, const void* w, void* dc, void* ws, hipStream_t s) {
+  if constexpr (sizeof(T) == 4)
+    if (bspline_sparse(b, dtype)) return launch_g_sparse<T>(kb, b->spline_k, batch, n_in, n_out, x, g, w, dc, ws, s);
   const bool cheb_kind = kb.kind == KF_KIND_CHEB;
   const bool weighted = features_weighted(b, w);
   WsG L = ws_g(b, dtype, batch, n_in, n_out, weighted);

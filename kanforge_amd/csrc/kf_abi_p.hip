@@ -91,6 +91,8 @@ int launch_p_dma(const WsP& L, hipStream_t s, const KBasis& kb, int64_t batch, i
 template <typename T>
 int run_P(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
           const void* g, const void* c, void* p, float* h, void* ws, hipStream_t s) {
+  if constexpr (sizeof(T) == 4)
+    if (bspline_sparse(b, dtype)) return launch_p_sparse<T>(kb, b->spline_k, batch, n_in, n_out, x, g, c, p, s);
   WsP L = ws_p(b, dtype, batch, n_in, n_out);
   void* cfmt = ws;
   int rc = launch_permute<T>(kb, n_out, n_in, L.OUTP, L.INP, L.ntb, c, cfmt, kPermFMT, s);

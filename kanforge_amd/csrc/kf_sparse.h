@@ -1,0 +1,288 @@
+// Sparse B-spline contractions: at any x only the k + 1 splines of its interval are non-zero, so
+// F, P and G multiply k + 1 coefficients per (row, input) instead of K (the reference's dense
+// route, kanforge/torch/layers.py:181-186 over kanforge/bases/spline.py:74-92, counts all K).
+//
+//   F: y[b, o]      = sum_i sum_r V[b, i, r] c[o, i, s0[b, i] + r]
+//   P: p[b, i]      = sum_r V[b, i, r] sum_o g[b, o] c[o, i, s0[b, i] + r]
+//   G: dc[o, i, k] += g[b, o] V[b, i, k - s0[b, i]]        (0 <= k - s0 <= KD)
+//
+// (s0, V) is the support window of (b, i): bspline_support's KD + 1 values w d^m/dx^m B_{KD, s}
+// moved to a start s0 in [0, K - KD - 1] so that every index s0 + r is a basis function (values
+// of indices outside [0, K) become zeros). x outside the knots gives V = 0; a non-finite x gives
+// V = NaN, and G then poisons all K features of the row as the dense recurrence does.
+#pragma once
+
+#include "kf_kernels.h"
+
+namespace kf {
+
+constexpr int kSpKMax = 16;  // basis functions per input (the plan limit)
+constexpr int kSpRows = 16;  // F / P: rows per workgroup
+constexpr int kSpIC = 8;     // F: inputs per staged coefficient chunk
+constexpr int kSpOC = 8;     // P: outputs per staged coefficient chunk
+constexpr int kSpLane = 65;  // padded LDS row: 64 lanes + 1 (conflict-free transposing writes)
+
+// Support window of input i at x (see above); returns 2 for a non-finite x, else 1.
+template <int KD>
+__device__ __forceinline__ int bspline_window(float x, float w, int i, const KBasis& b, int& s0, float (&V)[KD + 1]) {
+  const int nk = b.n_knots, K = b.K;
+  float t0, ih;
+  bspline_affine(b, i, t0, ih);
+  float N[KD + 1];
+  int base = 0;
+  const int st = bspline_support<KD>(x, w, b.knots_cmp + (size_t)i * nk, b.knots + (size_t)i * (nk + 2 * KD), t0, ih,
+                                     b, base, N);
+  s0 = 0;
+  if (st != 1) {
+    const float v = st == 2 ? __builtin_nanf("") : 0.f;
+#pragma unroll
+    for (int r = 0; r <= KD; ++r) V[r] = v;
+    return st == 2 ? 2 : 1;
+  }
+  const int hi = K - KD - 1;
+  s0 = base < 0 ? 0 : (base > hi ? hi : base);
+  const int sh = s0 - base;  // V[r] = N[r + sh] (|sh| <= KD)
+#pragma unroll
+  for (int r = 0; r <= KD; ++r) {
+    float v = 0.f;
+#pragma unroll
+    for (int q = 0; q <= KD; ++q) v = (q == r + sh) ? N[q] : v;
+    V[r] = v;
+  }
+  return 1;
+}
+
+// F: workgroup = kSpRows rows x 64 outputs, 8 waves (lane = output, wave = rows wave + 8 q).
+// The windows of the rows' next 64 inputs are computed once into LDS; the coefficients of kSpIC
+// inputs x K x 64 outputs are staged in LDS per chunk, the next chunk's loads in flight (registers)
+// while the current one is contracted.
+template <typename T, int KD>
+__global__ __launch_bounds__(512) void f_sparse_kernel(KBasis bs, int B, int IN, int OUT, const T* __restrict__ x,
+                                                       const T* __restrict__ w, const T* __restrict__ c,
+                                                       T* __restrict__ y) {
+  constexpr int NW = 8, RQ = kSpRows / NW, WCH = 64;
+  constexpr int PF = kSpIC * kSpKMax * 64 / 512;  // staged values per thread, at most
+  __shared__ float cs[kSpIC * kSpKMax][kSpLane];
+  __shared__ int ss[kSpRows][WCH];
+  __shared__ float vs[kSpRows][WCH][KD + 1];
+  const int K = bs.K;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int b0 = blockIdx.x * kSpRows, o0 = blockIdx.y * 64, o = o0 + lane;
+  const int no = OUT - o0 < 64 ? OUT - o0 : 64;
+  float acc[RQ];
+#pragma unroll
+  for (int q = 0; q < RQ; ++q) acc[q] = 0.f;
+  float pre[PF];
+  // staging map without divisions: output row ol = tid / 8 of the chunk, values r = tid % 8 + 8 u
+  // of its contiguous run of ni K coefficients
+  const int sol = threadIdx.x >> 3, sr = threadIdx.x & 7;
+  auto fetch = [&](int i0) {
+    const int per_o = (IN - i0 < kSpIC ? IN - i0 : kSpIC) * K;
+    const T* src = c + ((size_t)(o0 + sol) * IN + i0) * K;
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+      const int r = sr + 8 * u;
+      pre[u] = (sol < no && r < per_o) ? to_f32(src[r]) : 0.f;
+    }
+  };
+  for (int w0 = 0; w0 < IN; w0 += WCH) {
+    const int nw = IN - w0 < WCH ? IN - w0 : WCH;
+    __syncthreads();
+    for (int e = threadIdx.x; e < kSpRows * WCH; e += 512) {
+      const int rr = e / WCH, il = e % WCH, b = b0 + rr, i = w0 + il;
+      int s0 = 0;
+      float V[KD + 1];
+#pragma unroll
+      for (int r = 0; r <= KD; ++r) V[r] = 0.f;
+      if (b < B && il < nw) {
+        const size_t off = (size_t)b * IN + i;
+        bspline_window<KD>(to_f32(x[off]), w ? to_f32(w[off]) : 1.f, i, bs, s0, V);
+      }
+      ss[rr][il] = s0;
+#pragma unroll
+      for (int r = 0; r <= KD; ++r) vs[rr][il][r] = V[r];
+    }
+    fetch(w0);
+    for (int i0 = w0; i0 < w0 + nw; i0 += kSpIC) {
+      const int ni = IN - i0 < kSpIC ? IN - i0 : kSpIC, per_o = ni * K;
+      __syncthreads();
+#pragma unroll
+      for (int u = 0; u < PF; ++u) {
+        const int r = sr + 8 * u;
+        if (sol < no && r < per_o) cs[r][sol] = pre[u];
+      }
+      __syncthreads();
+      if (i0 + kSpIC < w0 + nw) fetch(i0 + kSpIC);
+      const int ib = i0 - w0;
+#pragma unroll
+      for (int il = 0; il < kSpIC; ++il) {
+        if (il >= ni) break;
+#pragma unroll
+        for (int q = 0; q < RQ; ++q) {
+          const int rr = wave + NW * q;
+          const int row = il * K + ss[rr][ib + il];
+#pragma unroll
+          for (int r = 0; r <= KD; ++r) acc[q] = fmaf(vs[rr][ib + il][r], cs[row + r][lane], acc[q]);
+        }
+      }
+    }
+  }
+  if (lane < no) {
+#pragma unroll
+    for (int q = 0; q < RQ; ++q) {
+      const int b = b0 + wave + NW * q;
+      if (b < B) y[(size_t)b * OUT + o] = from_f32<T>(acc[q]);
+    }
+  }
+}
+
+// P: workgroup = kSpRows rows x 64 inputs, 8 waves (lane = input, wave = rows wave + 8 q); each
+// lane keeps its rows' windows in registers; the coefficients of kSpOC outputs x K x 64 inputs and
+// the rows' g values are staged in LDS per chunk (next chunk prefetched into registers);
+// h_r = sum_o g c[o, i, s0 + r], then p = sum_r V_r h_r.
+template <typename T, int KD>
+__global__ __launch_bounds__(512, 4) void p_sparse_kernel(KBasis bs, int B, int IN, int OUT, const T* __restrict__ x,
+                                                       const T* __restrict__ g, const T* __restrict__ c,
+                                                       T* __restrict__ p) {
+  constexpr int NW = 8, RQ = kSpRows / NW;
+  constexpr int PF = kSpKMax;  // one (output, input)'s K coefficients per thread (kSpOC = NW)
+  static_assert(kSpOC == NW, "P stages one output per wave");
+  __shared__ float cs[kSpOC * kSpKMax][kSpLane];
+  __shared__ float gs[kSpRows][kSpOC];
+  const int K = bs.K;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int b0 = blockIdx.x * kSpRows, i0 = blockIdx.y * 64, i = i0 + lane;
+  const int ni = IN - i0 < 64 ? IN - i0 : 64;
+  float pre[PF], gpre = 0.f;
+  // staging map without divisions: thread (ol = wave, il = lane) moves the K coefficients of
+  // (oc0 + ol, i0 + il)
+  auto fetch = [&](int oc0) {
+    const int no = OUT - oc0 < kSpOC ? OUT - oc0 : kSpOC;
+    const T* src = c + ((size_t)(oc0 + wave) * IN + i0 + lane) * K;
+#pragma unroll
+    for (int u = 0; u < PF; ++u) pre[u] = (wave < no && lane < ni && u < K) ? to_f32(src[u]) : 0.f;
+    if (threadIdx.x < kSpRows * kSpOC) {
+      const int rr = threadIdx.x / kSpOC, ol = threadIdx.x % kSpOC, b = b0 + rr;
+      gpre = (b < B && ol < no) ? to_f32(g[(size_t)b * OUT + oc0 + ol]) : 0.f;
+    }
+  };
+  int s0[RQ];
+  float V[RQ][KD + 1], h[RQ][KD + 1];
+#pragma unroll
+  for (int q = 0; q < RQ; ++q) {
+    const int b = b0 + wave + NW * q;
+    s0[q] = 0;
+#pragma unroll
+    for (int r = 0; r <= KD; ++r) V[q][r] = h[q][r] = 0.f;
+    if (b < B && lane < ni) bspline_window<KD>(to_f32(x[(size_t)b * IN + i]), 1.f, i, bs, s0[q], V[q]);
+  }
+  fetch(0);
+  for (int oc0 = 0; oc0 < OUT; oc0 += kSpOC) {
+    const int no = OUT - oc0 < kSpOC ? OUT - oc0 : kSpOC;
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < PF; ++u)
+      if (wave < no && u < K) cs[wave * K + u][lane] = pre[u];
+    if (threadIdx.x < kSpRows * kSpOC) gs[threadIdx.x / kSpOC][threadIdx.x % kSpOC] = gpre;
+    __syncthreads();
+    if (oc0 + kSpOC < OUT) fetch(oc0 + kSpOC);
+    if (lane < ni) {
+#pragma unroll
+      for (int ol = 0; ol < kSpOC; ++ol) {
+        if (ol >= no) break;
+#pragma unroll
+        for (int q = 0; q < RQ; ++q) {
+          const float gv = gs[wave + NW * q][ol];
+          const int row = ol * K + s0[q];
+#pragma unroll
+          for (int r = 0; r <= KD; ++r) h[q][r] = fmaf(gv, cs[row + r][lane], h[q][r]);
+        }
+      }
+    }
+  }
+  if (lane < ni) {
+#pragma unroll
+    for (int q = 0; q < RQ; ++q) {
+      const int b = b0 + wave + NW * q;
+      float acc = 0.f;
+#pragma unroll
+      for (int r = 0; r <= KD; ++r) acc = fmaf(V[q][r], h[q][r], acc);
+      if (b < B) p[(size_t)b * IN + i] = from_f32<T>(acc);
+    }
+  }
+}
+
+// G partial sums over a slice of rows: workgroup = 4 inputs (one per wave) x 64 outputs (lane)
+// x rows [z RS, (z + 1) RS); part[z][o][i][k] (float, K per (o, i)). For 64 rows at a time each
+// lane turns its row's window into the row's KM features (zeros outside the window, all NaN for a
+// non-finite x) in the wave's LDS slot; every row then costs KM broadcast reads and KM FMAs per
+// lane, with the loads of sixteen rows' g in flight at once.
+template <typename T, int KD, int KM>
+__global__ __launch_bounds__(256) void g_sparse_kernel(KBasis bs, int B, int IN, int OUT, int RS,
+                                                       const T* __restrict__ x, const T* __restrict__ g,
+                                                       const T* __restrict__ w, float* __restrict__ part) {
+  __shared__ float phi[4][64][KM];
+  const int K = bs.K;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int i = blockIdx.x * 4 + wave, o = blockIdx.y * 64 + lane;
+  const bool live = i < IN && o < OUT;
+  const int z = blockIdx.z, r0 = z * RS, r1 = min(B, r0 + RS);
+  float acc[KM];
+#pragma unroll
+  for (int k = 0; k < KM; ++k) acc[k] = 0.f;
+  for (int bb = r0; bb < r1; bb += 64) {
+    const int nb = r1 - bb < 64 ? r1 - bb : 64;
+    __syncthreads();
+    {
+      int s0 = 0;
+      float V[KD + 1];
+#pragma unroll
+      for (int r = 0; r <= KD; ++r) V[r] = 0.f;
+      bool nan = false;
+      if (lane < nb && i < IN) {
+        const size_t off = (size_t)(bb + lane) * IN + i;
+        nan = bspline_window<KD>(to_f32(x[off]), w ? to_f32(w[off]) : 1.f, i, bs, s0, V) == 2;
+      }
+#pragma unroll
+      for (int k = 0; k < KM; ++k) {
+        float v = 0.f;
+#pragma unroll
+        for (int r = 0; r <= KD; ++r) v = (k == s0 + r) ? V[r] : v;
+        phi[wave][lane][k] = nan ? V[0] : v;
+      }
+    }
+    __syncthreads();
+    if (live) {
+      for (int j0 = 0; j0 < nb; j0 += 16) {
+        float gb[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) gb[u] = j0 + u < nb ? to_f32(g[(size_t)(bb + j0 + u) * OUT + o]) : 0.f;
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          if (j0 + u >= nb) break;
+#pragma unroll
+          for (int k = 0; k < KM; ++k) acc[k] = fmaf(gb[u], phi[wave][j0 + u][k], acc[k]);
+        }
+      }
+    }
+  }
+  if (live) {
+    float* dst = part + (((size_t)z * OUT + o) * IN + i) * K;
+#pragma unroll
+    for (int k = 0; k < KM; ++k)
+      if (k < K) dst[k] = acc[k];
+  }
+}
+
+// dc[e] = sum_z part[z][e] over nz slices, e < n (float sums in slice order: deterministic).
+template <typename T>
+__global__ __launch_bounds__(256) void g_sparse_reduce(int nz, long n, const float* __restrict__ part,
+                                                       T* __restrict__ dc) {
+  for (long e = blockIdx.x * 256L + threadIdx.x; e < n; e += (long)gridDim.x * 256) {
+    float s = 0.f;
+    for (int q = 0; q < nz; ++q) s += part[(size_t)q * n + e];
+    dc[e] = from_f32<T>(s);
+  }
+}
+
+}  // namespace kf

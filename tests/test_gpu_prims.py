@@ -248,6 +248,32 @@ def test_bspline_nonfinite_and_outside_inputs(dtype):
     np.testing.assert_allclose(phi[finite], want[finite], atol=2e-2 if dtype == torch.bfloat16 else 1e-6)
 
 
+@pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16"])
+def test_bspline_nonfinite_and_outside_inputs_through_F_P_G(dtype):
+    """Rows with a NaN or infinite input give NaN wherever the dense float64 contraction does (F:
+    the row's outputs; P: that input; G: every feature of that input), points outside the grid
+    contribute nothing; the rest matches the oracle (float32 layers run the sparse k + 1 route)."""
+    B, IN, OUT = 70, 5, 9
+    basis, plan, st, ob, x, rng = setup("bspline53", B, IN, seed=11)
+    x[3, 1], x[10, 4], x[20, 0], x[21, 2], x[30, 3] = np.nan, np.inf, -np.inf, -50.0, 50.0
+    c = rng.normal(0, 0.3, (OUT, IN, basis.size))
+    g = rng.normal(0, 1, (B, OUT))
+    w = rng.uniform(0.5, 1.5, (B, IN))
+    xd, cd, gd, wd = (to_dev(a, dtype) for a in (x, c, g, w))
+    xr, cr, gr, wr = (rounded(a, dtype) for a in (x, c, g, w))
+    atol = 2e-2 if dtype == torch.bfloat16 else 1e-5
+    for got, want in (
+        (K._raw("F", plan, 0, xd, wd, cd, st, OUT), o.prim_F(xr, cr, wr, ob, 0)),
+        (K._raw("P", plan, 1, xd, gd, cd, st, OUT), o.prim_P(xr, gr, cr, ob, 1)),
+        (K._raw("G", plan, 0, xd, wd, gd, st, OUT), o.prim_G(xr, gr, wr, ob, 0)),
+    ):
+        got = got.float().cpu().double().numpy()
+        np.testing.assert_array_equal(np.isnan(got), np.isnan(want))
+        fin = ~np.isnan(want)
+        scale = max(1.0, np.abs(want[fin]).max())
+        np.testing.assert_allclose(got[fin], want[fin], rtol=0, atol=atol * scale)
+
+
 @pytest.mark.parametrize("k,m", [(3, 0), (3, 1), (3, 2), (2, 0), (1, 1), (0, 0)])
 def test_uniform_grid_features_equal_the_general_path(k, m):
     """The even-knot fast path (constant-time interval estimate checked against the ceil32 table,
