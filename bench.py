@@ -3,12 +3,13 @@ bfloat16 with float32 accumulation, batch 8192; one step = forward + dX + dCoef
 (the F_0, P_1 and G_0 launches of the HIP path). Prints one JSON line.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-base] [--no-workloads]
-    python bench.py --workload {bspline_ffn,grkan_ffn,pinn_edge,pinn_laplacian,kan64,all}
+    python bench.py --workload {kan64,grkan_ffn,pinn_edge,pinn_laplacian,bspline_ffn,lut_kan64,all}
     python bench.py --workload NAME --only {F,G,P,edge,...} --steps N
 
 The headline line carries a ``workloads`` object with one entry per other layer
 shape (KANLinear 64->64 B-spline fp32, GR-KAN FFN, PINN edge derivatives, PINN
-Laplacian, B-spline FFN): step time, throughput, the roofline of the entry
+Laplacian, B-spline FFN, lookup-table inference of the 64->64 layer): step time,
+throughput, the roofline of the entry
 point with the most GPU time (per-call algorithmic FLOP and bytes over HIP-event
 durations; bound by whichever of MFMA and HBM time is larger) and a torch-CPU
 baseline on a stated sample. The second form prints those lines on their own.
@@ -59,7 +60,7 @@ def parse():
     )
     ap.add_argument("--no-workloads", action="store_true", help="leave the other layer shapes out of the headline line")
     ap.add_argument("--workload-steps", type=int, default=10, help="timed steps of each other layer shape in the headline line")
-    ap.add_argument("--only", choices=["F", "G", "P", "edge", "features", "rational_param_grad"],
+    ap.add_argument("--only", choices=["F", "G", "P", "edge", "features", "rational_param_grad", "lut"],
                     help="counter runs: replay only this entry point's calls of one step of --workload")
     return ap.parse_args()
 
@@ -96,6 +97,11 @@ def _work(label, args):
         plan, _m, _st, x2 = args[:4]
         batch, n_in = x2.shape
         return 0.0, float(x2.element_size() * batch * n_in * (1 + plan.size))
+    if label == "lut":
+        layer, x = args[:2]
+        n_in, _size, n_out = layer.tables.shape
+        rows = x.numel() // n_in
+        return 3.0 * rows * n_in * n_out, float(4 * rows * (n_in + n_out) + layer.tables.nbytes)
     if label == "rational_param_grad":
         _plan, _st, x, h, w = args[:5]
         n = x.numel()
@@ -144,15 +150,19 @@ class EntryTimer:
         }
 
 
+STREAM_ENTRIES = ("edge", "features", "rational_param_grad", "lut")  # no contraction on MFMA
+
+
 def roofline_of(totals, dtype, traffic_file=None):
-    """Roofline of the entry point with the most GPU time: bound by whichever of MFMA time
-    (algorithmic FLOP at the dtype's dense peak) and HBM time (algorithmic bytes at 8 TB/s) is
-    larger; achieved = that work over the entry's measured time (sums over its calls)."""
+    """Roofline of the entry point with the most GPU time: for contractions (F, G, P) bound by
+    whichever of MFMA time (algorithmic FLOP at the dtype's dense peak) and HBM time (algorithmic
+    bytes at 8 TB/s) is larger, for the streaming entries by HBM; achieved = that work over the
+    entry's measured time (sums over its calls)."""
     op = max(totals, key=lambda k: totals[k][0])
     ms, flops, nbytes, calls = totals[op]
     peak_f = PEAK_BF16 if dtype == "bf16" else PEAK_FP32
     sec = ms * 1e-3
-    if flops / peak_f >= nbytes / PEAK_HBM:
+    if op not in STREAM_ENTRIES and flops / peak_f >= nbytes / PEAK_HBM:
         achieved, peak, unit, bound = flops / sec / 1e12, peak_f / 1e12, "TFLOP/s", "mfma"
     else:
         achieved, peak, unit, bound = nbytes / sec / 1e9, PEAK_HBM / 1e9, "GB/s", "hbm"
@@ -403,12 +413,51 @@ def wl_kan64(dev):
     return step, 4096, "samples/s", "f32", cpu
 
 
+def wl_lut_kan64(dev):
+    """Lookup-table inference of the KANLinear 64->64 B-spline (grid 5, order 3) layer with SiLU
+    base: tables of 256 points per edge over the inputs' range, 65536 rows x ~ U(-1, 1); one step
+    evaluates the float32 tables and their int8 quantisation (gather + lerp + sum)."""
+    import kanforge_amd as kf
+    from kanforge_amd.export import quantize, to_lut
+    from kanforge_amd.torch import KANLinear
+
+    layer = KANLinear(64, 64, kf.BSpline(5, 3)).to(dev)
+    with torch.no_grad():
+        layer.coef.copy_(_randn(layer.coef.shape, 1, 1 / math.sqrt(64 * 8)))
+    x = (torch.rand(65536, 64, generator=torch.Generator().manual_seed(0)) * 2 - 1).to(dev)
+    lut = to_lut(layer, x, 256)
+    q = quantize(lut)
+
+    def step():
+        return lut(x), q(x)
+
+    def cpu():
+        from oracle import kan64 as o
+
+        rows = _cpu_rows(8192)
+        xs = x[:rows].double().cpu().numpy()
+        fl, ql = lut.layers[0], q.layers[0]
+
+        def run():
+            o.lut_layer(xs, fl.tables, fl.lo, fl.hi, fl.bias, None, fl.slope_lo, fl.slope_hi)
+            o.lut_layer(xs, ql.tables, ql.lo, ql.hi, ql.bias, ql.scale, ql.slope_lo, ql.slope_hi)
+
+        run()
+        t0 = time.perf_counter()
+        run()
+        t = time.perf_counter() - t0
+        return _cpu_line(rows / t, "rows/s", 1, f"{rows} of the rows, float32 and int8 tables: the NumPy float64 LUT evaluation, one run after 1 warm-up")
+
+    return step, x.shape[0], "rows/s", "f32", cpu
+
+
 WORKLOADS = {
     "kan64": wl_kan64,
     "grkan_ffn": wl_grkan_ffn,
     "pinn_edge": wl_pinn_edge,
     "pinn_laplacian": wl_pinn_laplacian,
     "bspline_ffn": wl_bspline_ffn,
+    "lut_kan64": wl_lut_kan64,
 }
 
 
@@ -419,11 +468,21 @@ def traffic_file(name):
 def _hook_entries(timer):
     from kanforge_amd.torch import kernels as kmod
 
+    from kanforge_amd.export.lut import LUTLayer
+
     names = ("_raw", None), ("_edge_raw", "edge"), ("_features_raw", "features"), ("_rational_param_grad", "rational_param_grad")
     orig = {n: getattr(kmod, n) for n, _ in names}
     for n, lab in names:
         setattr(kmod, n, timer.wrap(orig[n], lab))
-    return lambda: [setattr(kmod, n, f) for n, f in orig.items()]
+    lut_call = LUTLayer.__call__
+    LUTLayer.__call__ = timer.wrap(lut_call, "lut")
+
+    def unhook():
+        for n, f in orig.items():
+            setattr(kmod, n, f)
+        LUTLayer.__call__ = lut_call
+
+    return unhook
 
 
 def run_workload(name, args, dev, cpu=True):

@@ -41,6 +41,8 @@ extern "C" {
 /* element types */
 #define KF_F32 0
 #define KF_BF16 1
+#define KF_I8 2  /* lookup tables only */
+#define KF_I16 3 /* lookup tables only */
 
 /* basis kinds (kanforge/kernels/plan.py:39-45 KernelPlan.kind, plus rational) */
 #define KF_KIND_CHEB 0     /* T_j(g(x)) features, g = tanh or identity; derivatives folded */
@@ -197,6 +199,23 @@ int kf_rational_param_grad(const kf_basis *basis, int dtype, int64_t batch, int6
  * shader-clock cycles and the 100 MHz real-time ticks of its first wave's MFMA loop.
  */
 int kf_probe_mfma(int blocks, int iters, int rotate, float *out, void *stream);
+
+/*
+ * Lookup-table inference of one tabulated KAN layer. Replaces LUTLayer.__call__
+ * (kanforge/export/lut.py:70-89):
+ *   t = (x[b,i] - lo[i]) * inv_step[i]   (inv_step = (size - 1) / (hi - lo))
+ *   j = min(floor(clip(t, 0, size-1)), size-2),  f = clip(t, 0, size-1) - j
+ *   y[b,o] = bias[o] + scale[o] * sum_i (T[i,j,o] + f (T[i,j+1,o] - T[i,j,o]))
+ *            + sum_i (min(t,0) slope_lo[i,o] + max(t-(size-1),0) slope_hi[i,o])
+ * table_dtype: KF_F32 (scale NULL) or KF_I8 / KF_I16 (scale (n_out), from quantize,
+ * kanforge/export/lut.py:175-197); tables (n_in, size, n_out); slope_lo/slope_hi (n_in, n_out)
+ * per index step for linear extrapolation, both NULL to hold the end values ("clamp").
+ * x (batch, n_in) and y (batch, n_out) float32; lo, inv_step (n_in), bias (n_out) float32.
+ * Non-finite t clamps to the ends (x = NaN reads the first entry); size >= 2.
+ */
+int kf_lut_forward(int table_dtype, int64_t batch, int64_t n_in, int64_t size, int64_t n_out, const float *x,
+                   const void *tables, const float *lo, const float *inv_step, const float *bias, const float *scale,
+                   const float *slope_lo, const float *slope_hi, float *y, void *stream);
 
 /* Text of the last error on the calling thread ("" if none). */
 const char *kf_last_error(void);

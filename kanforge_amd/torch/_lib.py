@@ -17,6 +17,7 @@ LIB_PATH = Path(__file__).resolve().parent.parent / "libkfhip.so"
 # status codes / enums of include/kfhip.h
 KF_OK = 0
 KF_F32, KF_BF16 = 0, 1
+KF_I8, KF_I16 = 2, 3  # lookup-table element types
 KF_KIND_CHEB, KF_KIND_BSPLINE, KF_KIND_RATIONAL = 0, 1, 2
 KF_MAP_IDENTITY, KF_MAP_TANH, KF_MAP_TANH_SQ = 0, 1, 2
 KF_OP_F, KF_OP_G, KF_OP_P = 0, 1, 2
@@ -36,6 +37,7 @@ EXPORTS = (
     "kf_rational_workspace_bytes",
     "kf_rational_param_grad",
     "kf_probe_mfma",
+    "kf_lut_forward",
     "kf_last_error",
     "kf_version",
 )
@@ -97,7 +99,9 @@ def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
         for name in ("kf_F", "kf_F_noalloc", "kf_G", "kf_P", "kf_features", "kf_edge_derivative", "kf_bspline_interval", "kf_rational_param_grad"):
             getattr(lib, name).restype = c_int
         lib.kf_probe_mfma.argtypes = [c_int, c_int, c_int, c_void_p, c_void_p]
+        lib.kf_lut_forward.argtypes = [c_int, c_int64, c_int64, c_int64, c_int64] + [c_void_p] * 10
         lib.kf_probe_mfma.restype = c_int
+        lib.kf_lut_forward.restype = c_int
         lib.kf_last_error.argtypes = []
         lib.kf_last_error.restype = c_char_p
         lib.kf_version.argtypes = []

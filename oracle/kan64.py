@@ -473,3 +473,51 @@ PINNING = {
     "kan_linear": "per-edge manual sum (tests/test_bases.py:64-74)",
     "symbolic_edges": "defining values of every library function (x^2(3) = 9, sin(pi/2) = 1, ...); affine map inside and out",
 }
+
+
+# --------------------------------------------------------------------------
+# lookup tables (kanforge/export/lut.py)
+
+
+def lut_layer(x, tables, lo, hi, bias, scale=None, slope_lo=None, slope_hi=None, extrapolate="linear"):
+    """LUTLayer.__call__ (kanforge/export/lut.py:70-89) in float64: x (B, in), tables
+    (in, size, out); y (B, out) = bias + [scale *] sum_i lerp of T[i, j], T[i, j+1] at
+    t = (x - lo) / step (step = (hi - lo) / (size - 1)), plus the end slopes times how far t
+    leaves [0, size - 1] when extrapolating linearly."""
+    x = np.asarray(x, dtype=np.float64)
+    T = np.asarray(tables, dtype=np.float64)
+    size = T.shape[1]
+    step = (np.asarray(hi, np.float64) - np.asarray(lo, np.float64)) / (size - 1)
+    t_raw = (x - lo) / step
+    t = np.clip(t_raw, 0, size - 1)
+    j = np.clip(np.floor(t), 0, size - 2).astype(np.int64)
+    f = t - j
+    i = np.arange(x.shape[-1])
+    t0, t1 = T[i, j], T[i, j + 1]
+    acc = (t0 + f[..., None] * (t1 - t0)).sum(-2)
+    y = acc * scale + bias if scale is not None else acc + bias
+    if extrapolate == "linear" and slope_lo is not None:
+        below = np.minimum(t_raw, 0.0)[..., None]
+        above = np.maximum(t_raw - (size - 1), 0.0)[..., None]
+        y = y + (below * slope_lo + above * slope_hi).sum(-2)
+    return y
+
+
+def lut_end_slopes(tables):
+    """Per index step, over the first and last max(1, (size-1) // 32) steps
+    (kanforge/export/lut.py:131-135): (slope_lo, slope_hi), each (in, out)."""
+    T = np.asarray(tables, dtype=np.float64)
+    k = max(1, (T.shape[1] - 1) // 32)
+    return (T[:, k] - T[:, 0]) / k, (T[:, -1] - T[:, -1 - k]) / k
+
+
+def lut_quantize(tables, bias, bits=8):
+    """(q, scale, bias') with T ~ centre + scale q (kanforge/export/lut.py:175-197): centre the
+    (max + min) / 2 of each edge, scale per output the largest deviation over qmax."""
+    T = np.asarray(tables, dtype=np.float64)
+    qmax = 2 ** (bits - 1) - 1
+    centre = 0.5 * (T.max(1) + T.min(1))
+    dev = np.abs(T - centre[:, None, :]).max((0, 1))
+    scale = np.where(dev > 0, dev / qmax, 1.0)
+    q = np.round((T - centre[:, None, :]) / scale).astype(np.int8 if bits <= 8 else np.int16)
+    return q, scale, np.asarray(bias, np.float64) + centre.sum(0)

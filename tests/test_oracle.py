@@ -295,3 +295,64 @@ def test_symbolic_edges_follow_the_function_table():
         d = o.symbolic_edges(np.array([[0.5, 0.7]]), code, params)
         assert np.isclose(d[0, 0, 0], 3.0 * want - 1.0), name
         assert d[0, 0, 1] == 0.0
+
+
+# --- lookup tables (kanforge/export/lut.py) ---------------------------------------------------
+
+
+def _linear_tables(rng, n_in=3, size=17, n_out=4):
+    lo = rng.uniform(-2, -0.5, n_in)
+    hi = rng.uniform(0.5, 2, n_in)
+    a, b = rng.normal(size=(n_in, n_out)), rng.normal(size=(n_in, n_out))
+    pts = lo[:, None] + (hi - lo)[:, None] * np.linspace(0, 1, size)[None, :]  # (in, size)
+    return lo, hi, a, b, a[:, None, :] + b[:, None, :] * pts[..., None]
+
+
+def test_lut_reproduces_linear_edges_inside_and_outside():
+    """A table of linear edges a + b x is reproduced exactly by the lerp inside the range and,
+    with its own end slopes (b times the step, per index step), by linear extrapolation outside."""
+    rng = np.random.default_rng(0)
+    lo, hi, a, b, T = _linear_tables(rng)
+    bias = rng.normal(size=4)
+    x = rng.uniform(-4, 4, (200, 3))
+    s_lo, s_hi = o.lut_end_slopes(T)
+    step = (hi - lo) / (T.shape[1] - 1)
+    np.testing.assert_allclose(s_lo, b * step[:, None], rtol=1e-12)
+    got = o.lut_layer(x, T, lo, hi, bias, slope_lo=s_lo, slope_hi=s_hi)
+    want = (a[None] + b[None] * x[..., None]).sum(1) + bias
+    np.testing.assert_allclose(got, want, rtol=1e-10, atol=1e-10)
+
+
+def test_lut_hits_table_values_and_clamps():
+    rng = np.random.default_rng(1)
+    n_in, size, n_out = 2, 9, 3
+    T = rng.normal(size=(n_in, size, n_out))
+    lo, hi = np.array([-1.0, 0.5]), np.array([1.0, 2.5])
+    s = np.array([[0, 8], [3, 5], [8, 0]])  # table indices per row and input
+    x = lo + s * (hi - lo) / (size - 1)
+    got = o.lut_layer(x, T, lo, hi, np.zeros(n_out), extrapolate="clamp")
+    want = np.stack([T[0, s[r, 0]] + T[1, s[r, 1]] for r in range(3)])
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+    far = o.lut_layer(np.array([[50.0, -50.0]]), T, lo, hi, np.zeros(n_out), extrapolate="clamp")
+    np.testing.assert_allclose(far[0], T[0, -1] + T[1, 0], rtol=1e-12)
+
+
+def test_lut_quantize_error_bound():
+    """Dequantised entries are within half a step of the float tables, so a row's sum over n_in
+    inputs is within n_in scale / 2 per output."""
+    rng = np.random.default_rng(2)
+    T = rng.normal(size=(5, 33, 4)) * np.array([1.0, 0.1, 3.0, 0.0])
+    bias = rng.normal(size=4)
+    for bits in (8, 12):
+        q, scale, bias_q = o.lut_quantize(T, bias, bits)
+        assert q.dtype == (np.int8 if bits <= 8 else np.int16)
+        assert np.abs(q).max() <= 2 ** (bits - 1) - 1
+        centre = 0.5 * (T.max(1) + T.min(1))
+        deq = centre[:, None, :] + scale * q
+        assert np.all(np.abs(deq - T) <= scale / 2 + 1e-12)
+        np.testing.assert_allclose(bias_q, bias + centre.sum(0))
+        x = rng.uniform(-1, 1, (50, 5))
+        lo, hi = -np.ones(5), np.ones(5)
+        yq = o.lut_layer(x, q, lo, hi, bias_q, scale=scale, extrapolate="clamp")
+        yf = o.lut_layer(x, T, lo, hi, bias, extrapolate="clamp")
+        assert np.all(np.abs(yq - yf) <= 5 * scale / 2 + 1e-9)
