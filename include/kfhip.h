@@ -179,8 +179,9 @@ int kf_bspline_interval(int64_t batch, int64_t n_in, const float *x, const float
                         int32_t *idx, void *stream);
 
 /*
- * Gradients of sum_{b,i} h[b,i] w[b,i] phi(x[b,i]) with respect to the
- * rational parameters: dnum (groups, num_deg+1), dden (groups, den_deg),
+ * Gradients of sum_{b,i} h[b,i] w[b,i] phi^(m)(x[b,i]) with respect to the
+ * rational parameters, m = basis->order (0, or 1..3 for numerator degree 5 and
+ * denominator degree 4): dnum (groups, num_deg+1), dden (groups, den_deg),
  * float32, overwritten. h float32 (batch, n_in) from kf_P; w may be NULL.
  * What autograd computes through Rational._eval (kanforge/bases/rational.py:84-101).
  * Needs kf_workspace_bytes-independent scratch: workspace of

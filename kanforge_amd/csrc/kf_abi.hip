@@ -170,6 +170,26 @@ int kf_rational_param_grad(const kf_basis* b, int dtype, int64_t batch, int64_t 
   KBasis kb = to_kbasis(b);
   const int chunks = (int)((batch + kRatRows - 1) / kRatRows);
   dim3 grid((unsigned)groups, (unsigned)chunks);
+  if (b->order > 0) {  // gradients of the derivative features: GR-KAN degrees, orders 1..3
+    if (b->num_deg != 5 || b->den_deg != 4 || b->order > 3)
+      return fail(KF_EUNSUPPORTED, "kf_rational_param_grad: order %d needs P 5 / Q 4 and order <= 3", b->order);
+    auto go = [&](auto tag) {
+      constexpr int M = decltype(tag)::value;
+      if (dtype == KF_BF16)
+        hipLaunchKernelGGL((rational_grad_order<bf16, M, kRatRows>), grid, dim3(256), 0, s, kb, (int)batch,
+                           (int)n_in, (const bf16*)x, h, (const bf16*)w, (float*)workspace);
+      else
+        hipLaunchKernelGGL((rational_grad_order<float, M, kRatRows>), grid, dim3(256), 0, s, kb, (int)batch,
+                           (int)n_in, (const float*)x, h, (const float*)w, (float*)workspace);
+      return check_launch("rational_grad_order");
+    };
+    rc = b->order == 1 ? go(std::integral_constant<int, 1>{})
+                       : b->order == 2 ? go(std::integral_constant<int, 2>{}) : go(std::integral_constant<int, 3>{});
+    if (rc) return rc;
+    hipLaunchKernelGGL(rational_grad_final, dim3(1), dim3(256), 0, s, groups, nP, nQ, chunks,
+                       (const float*)workspace, dnum, dden);
+    return check_launch("rational_grad_final");
+  }
   const bool fast = rational_fast(kb, n_in) && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
                     (reinterpret_cast<uintptr_t>(h) & 15) == 0 && (!w || (reinterpret_cast<uintptr_t>(w) & 15) == 0);
   if (fast && dtype == KF_BF16)

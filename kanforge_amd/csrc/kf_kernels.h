@@ -2833,6 +2833,7 @@ static __global__ void rational_grad_final(int groups, int nP, int nQ, int n_chu
   for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < groups * np; e += gridDim.x * blockDim.x) {
     const int g = e / np, q = e % np;
     float s = 0.f;
+#pragma unroll 8
     for (int ch = 0; ch < n_chunks; ++ch) s += part[((size_t)ch * groups + g) * np + q];
     if (q < nP)
       dnum[(size_t)g * nP + q] = s;

@@ -193,10 +193,10 @@ def _raw(op: str, plan: KernelPlan, m: int, x, a, b, st: BasisState | None, n_ou
         return p
 
 
-def _rational_param_grad(plan, st: BasisState, x, h, w):
-    """(d num, d den) float32 of sum_{b,i} h w phi(x) for the rational plan."""
+def _rational_param_grad(plan, st: BasisState, x, h, w, m: int = 0):
+    """(d num, d den) float32 of sum_{b,i} h w phi^(m)(x) for the rational plan."""
     lib = _lib.load()
-    desc, keep = _desc(plan, 0, st)
+    desc, keep = _desc(plan, m, st)
     batch, n_in = x.shape
     dev = x.device
     dnum = torch.empty_like(st.num)
@@ -289,23 +289,24 @@ def op_P(x: torch.Tensor, g: torch.Tensor, c: torch.Tensor, knots: Opt, knots_cm
 
 @torch.library.custom_op("kf::rational_bwd", mutates_args=())
 def op_rational_bwd(
-    x: torch.Tensor, g: torch.Tensor, c: torch.Tensor, w: Opt, num: torch.Tensor, den: torch.Tensor, plan: str
+    x: torch.Tensor, g: torch.Tensor, c: torch.Tensor, w: Opt, num: torch.Tensor, den: torch.Tensor, plan: str, m: int
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """(P_1(x, g, c), d/dnum, d/dden) of sum_{b,o} g[b,o] F_0(x, c, w)[b,o] for a rational plan:
-    one P launch that also writes h = sum_o g c, then the parameter-gradient reduction."""
+    """(P_{m+1}(x, g, c), d/dnum, d/dden) of sum_{b,o} g[b,o] F_m(x, c, w)[b,o] for a rational
+    plan: one P launch that also writes h = sum_o g c, then the parameter-gradient reduction of
+    sum h w phi^(m)."""
     pl = plan_of(plan)
     st = _state(None, None, None, num, den, x.shape[1])
     h = torch.empty(x.shape, dtype=torch.float32, device=x.device)
-    p1 = _raw("P", pl, 1, x, g, c, st, c.shape[0], h=h)
-    dnum, dden = _rational_param_grad(pl, st, x, h, w)
+    p1 = _raw("P", pl, m + 1, x, g, c, st, c.shape[0], h=h)
+    dnum, dden = _rational_param_grad(pl, st, x, h, w, m)
     return p1, dnum.to(num.dtype), dden.to(den.dtype)
 
 
 @torch.library.custom_op("kf::rational_param_grad", mutates_args=())
-def op_rational_param_grad(x: torch.Tensor, h: torch.Tensor, w: Opt, num: torch.Tensor, den: torch.Tensor, plan: str) -> tuple[torch.Tensor, torch.Tensor]:
-    """(d/dnum, d/dden) of sum_{b,i} h[b,i] w[b,i] phi(x[b,i]) for a rational plan."""
+def op_rational_param_grad(x: torch.Tensor, h: torch.Tensor, w: Opt, num: torch.Tensor, den: torch.Tensor, plan: str, m: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """(d/dnum, d/dden) of sum_{b,i} h[b,i] w[b,i] phi^(m)(x[b,i]) for a rational plan."""
     st = _state(None, None, None, num, den, x.shape[1])
-    dnum, dden = _rational_param_grad(plan_of(plan), st, x, h.float().contiguous(), w)
+    dnum, dden = _rational_param_grad(plan_of(plan), st, x, h.float().contiguous(), w, m)
     return dnum.to(num.dtype), dden.to(den.dtype)
 
 
@@ -325,12 +326,12 @@ def _(x, g, c, knots, knots_cmp, knots_u, num, den, plan, m):
 
 
 @op_rational_bwd.register_fake
-def _(x, g, c, w, num, den, plan):
+def _(x, g, c, w, num, den, plan, m):
     return x.new_empty(x.shape), torch.empty_like(num), torch.empty_like(den)
 
 
 @op_rational_param_grad.register_fake
-def _(x, h, w, num, den, plan):
+def _(x, h, w, num, den, plan, m):
     return torch.empty_like(num), torch.empty_like(den)
 
 
@@ -352,9 +353,7 @@ def _F_backward(ctx, gy):
     gy = gy.contiguous()
     tabs = (knots, knots_cmp, knots_u, num, den)
     if plan_of(plan).kind == "rational" and (need[6] or need[7]):
-        if m != 0:
-            raise NotImplementedError("rational parameter gradients of derivative features are not compiled into the HIP kernels")
-        p1, gnum, gden = op_rational_bwd(x, gy, c, w, num, den, plan)
+        p1, gnum, gden = op_rational_bwd(x, gy, c, w, num, den, plan, m)
         if need[0]:
             # under create_graph the x-gradient stays differentiable through kf::P
             gx = _mul(w, op_P(x, gy, c, *tabs, plan, 1) if torch.is_grad_enabled() else p1)
@@ -376,14 +375,19 @@ def _G_backward(ctx, gdc):
     x, g, w, knots, knots_cmp, knots_u, num, den = ctx.saved_tensors
     plan, m = ctx.plan, ctx.m
     need = ctx.needs_input_grad
-    if need[6] or need[7]:
-        raise NotImplementedError("second-order rational parameter gradients are not compiled into the HIP kernels")
     gdc = gdc.contiguous()
     tabs = (knots, knots_cmp, knots_u, num, den)
-    gx = _mul(w, op_P(x, g, gdc, *tabs, plan, m + 1)) if need[0] else None
+    gx = gnum = gden = None
+    if need[6] or need[7]:
+        # d<gdc, G_m>/dtheta = sum_{b,i} (sum_o g gdc) w dphi^(m)/dtheta: the h of P(x, g, gdc)
+        p1, gnum, gden = op_rational_bwd(x, g, gdc, w, num, den, plan, m)
+        if need[0]:
+            gx = _mul(w, op_P(x, g, gdc, *tabs, plan, m + 1) if torch.is_grad_enabled() else p1)
+    elif need[0]:
+        gx = _mul(w, op_P(x, g, gdc, *tabs, plan, m + 1))
     gg = op_F(x, w, gdc, *tabs, plan, m) if need[1] else None
     gw = op_P(x, g, gdc, *tabs, plan, m) if need[2] else None
-    return gx, gg, gw, None, None, None, None, None, None, None
+    return gx, gg, gw, None, None, None, gnum, gden, None, None
 
 
 def _P_setup(ctx, inputs, output):
@@ -395,18 +399,24 @@ def _P_backward(ctx, gp):
     x, g, c, knots, knots_cmp, knots_u, num, den = ctx.saved_tensors
     plan, m = ctx.plan, ctx.m
     need = ctx.needs_input_grad
-    if need[6] or need[7]:
-        raise NotImplementedError("second-order rational parameter gradients are not compiled into the HIP kernels")
     gp = gp.contiguous()
     tabs = (knots, knots_cmp, knots_u, num, den)
-    gx = gp * op_P(x, g, c, *tabs, plan, m + 1) if need[0] else None
+    gx = gnum = gden = None
+    if need[6] or need[7]:
+        # d<gp, P_m>/dtheta = sum_{b,i} gp (sum_o g c) dphi^(m)/dtheta: P(x, g, c)'s h, weight gp
+        p1, gnum, gden = op_rational_bwd(x, g, c, gp, num, den, plan, m)
+        if need[0]:
+            gx = gp * (op_P(x, g, c, *tabs, plan, m + 1) if torch.is_grad_enabled() else p1)
+    elif need[0]:
+        gx = gp * op_P(x, g, c, *tabs, plan, m + 1)
     gg = op_F(x, gp, c, *tabs, plan, m) if need[1] else None
     gc = op_G(x, g, gp, *tabs, plan, m) if need[2] else None
-    return gx, gg, gc, None, None, None, None, None, None, None
+    return gx, gg, gc, None, None, None, gnum, gden, None, None
 
 
 def _no_second_order(ctx, *grads):
-    raise NotImplementedError("second-order rational parameter gradients are not compiled into the HIP kernels")
+    raise NotImplementedError("gradients of the rational parameter gradients themselves (third order in the "
+                              "parameters) are not compiled into the HIP kernels")
 
 
 def _no_ctx(ctx, inputs, output):
@@ -504,11 +514,8 @@ op_features.register_autograd(_features_backward, setup_context=_features_setup)
 
 
 def _rational_grads_of(plan, x2, h, m, num, den):
-    """d/d(num, den) of sum_{b,i} h[b,i] phi^(m)(x[b,i]) for a rational plan (order 0 only)."""
-    if m != 0:
-        raise NotImplementedError("rational parameter gradients of derivative features (order >= 1) are not "
-                                  "compiled into the HIP kernels")
-    return op_rational_param_grad(x2, h.float().contiguous(), None, num, den, plan)
+    """d/d(num, den) of sum_{b,i} h[b,i] phi^(m)(x[b,i]) for a rational plan."""
+    return op_rational_param_grad(x2, h.float().contiguous(), None, num, den, plan, m)
 
 
 def basis_derivative(basis, x: torch.Tensor, m: int, params: dict | None) -> torch.Tensor:

@@ -319,6 +319,46 @@ def test_grkan_forward_and_all_gradients(dtype):
         assert err <= TOL[dtype], (key, err)
 
 
+def test_grkan_gradient_penalty_reaches_the_rational_parameters():
+    """Double backward through a GR-KAN layer with trainable P/Q: the gradient of the penalty
+    sum (dL/dx)^2, L = <y, gy>, with respect to numerator and denominator, against central
+    differences of the oracle's float64 penalty."""
+    B, IN, OUT = 40, 16, 8
+    torch.manual_seed(3)
+    layer = GRKAN(IN, OUT, groups=4)
+    with torch.no_grad():
+        layer.basis_numerator.add_(0.1 * torch.randn_like(layer.basis_numerator))
+        layer.basis_denominator.add_(0.1 * torch.randn_like(layer.basis_denominator))
+    layer = layer.to(DEV)
+    rng = np.random.default_rng(5)
+    x0, gy0 = rng.normal(0, 1, (B, IN)), rng.normal(0, 1, (B, OUT))
+    x = torch.as_tensor(x0, dtype=torch.float32, device=DEV).requires_grad_()
+    gy = torch.as_tensor(gy0, dtype=torch.float32, device=DEV)
+    (gx,) = torch.autograd.grad((layer(x) * gy).sum(), x, create_graph=True)
+    (gx * gx).sum().backward()
+    xr, gyr = rounded(x0, torch.float32), rounded(gy0, torch.float32)
+    c = np64(layer.coef)
+    num, den = np64(layer.basis_numerator), np64(layer.basis_denominator)
+
+    def penalty(nm, dn):
+        ob = o.Basis64("rational", num=np.repeat(nm, IN // 4, 0), den=np.repeat(dn, IN // 4, 0))
+        return (o.prim_P(xr, gyr, c, ob, 1) ** 2).sum()
+
+    for name, arr, got in (("numerator", num, layer.basis_numerator.grad), ("denominator", den, layer.basis_denominator.grad)):
+        want = np.zeros_like(arr)
+        for idx in np.ndindex(arr.shape):
+            eps = 1e-6
+            up, dn = arr.copy(), arr.copy()
+            up[idx] += eps
+            dn[idx] -= eps
+            hi = penalty(up, den) if arr is num else penalty(num, up)
+            lo = penalty(dn, den) if arr is num else penalty(num, dn)
+            want[idx] = (hi - lo) / (2 * eps)
+        err = o.normwise_err(np64(got), want)
+        print(f"grkan penalty d{name}: {err:.3e}", flush=True)
+        assert err <= 1e-4, (name, err)
+
+
 def _chained_second_derivative(layers, x, dim):
     """Forward-mode (h, h', h'') through KAN layers in float64."""
     h = x

@@ -65,9 +65,10 @@ def test_opcheck_edge_and_features(name):
 
 def test_opcheck_rational_ops_and_interval():
     key, x, c, gy, w, tabs = _operands(BASES["rational"], grad=False)
-    torch.library.opcheck(torch.ops.kf.rational_bwd.default, (x, gy, c, None, tabs[3], tabs[4], key))
     h = torch.randn(x.shape, device=DEV)
-    torch.library.opcheck(torch.ops.kf.rational_param_grad.default, (x, h, w, tabs[3], tabs[4], key))
+    for m in (0, 1):
+        torch.library.opcheck(torch.ops.kf.rational_bwd.default, (x, gy, c, None, tabs[3], tabs[4], key, m))
+        torch.library.opcheck(torch.ops.kf.rational_param_grad.default, (x, h, w, tabs[3], tabs[4], key, m))
     bkey, bx, _, _, _, btabs = _operands(BASES["bspline53"], grad=False)
     torch.library.opcheck(torch.ops.kf.bspline_interval.default, (bx, btabs[1]))
 

@@ -221,6 +221,39 @@ def test_rational_param_grad_matches_oracle():
     assert o.normwise_err(dden.cpu().double().numpy(), want_d) <= 1e-5
 
 
+@pytest.mark.parametrize("m", [1, 2, 3])
+def test_rational_param_grad_of_derivative_features_matches_finite_differences(m):
+    """d/dtheta of sum_{b,i} h w phi^(m)(x) (the parameter gradients a gradient penalty needs)
+    against central differences of the oracle's float64 phi^(m) in each of the group's ten
+    parameters."""
+    B, IN = 200, 40
+    basis, plan, st, ob, x, rng = setup("rational", B, IN, seed=7 + m)
+    h = rng.normal(0, 1, (B, IN))
+    w = rng.uniform(0.5, 1.5, (B, IN))
+    xd = to_dev(x, torch.float32)
+    dnum, dden = K._rational_param_grad(plan, st, xd, to_dev(h, torch.float32), to_dev(w, torch.float32), m)
+    xr, hr, wr = rounded(x, torch.float32), rounded(h, torch.float32), rounded(w, torch.float32)
+    num, den = st.num.double().cpu().numpy(), st.den.double().cpu().numpy()
+    groups, gs = num.shape[0], IN // num.shape[0]
+
+    def total(nm, dn):
+        phi = o.rational_basis(xr, np.repeat(nm, gs, 0), np.repeat(dn, gs, 0), m)[..., 0]
+        return (hr * wr * phi).reshape(B, groups, gs).sum((0, 2))  # per group
+
+    want_n, want_d = np.zeros_like(num), np.zeros_like(den)
+    for arr, want in ((num, want_n), (den, want_d)):
+        for j in range(arr.shape[1]):
+            eps = 1e-6
+            up, dn_ = arr.copy(), arr.copy()
+            up[:, j] += eps
+            dn_[:, j] -= eps
+            args_up = (up, den) if arr is num else (num, up)
+            args_dn = (dn_, den) if arr is num else (num, dn_)
+            want[:, j] = (total(*args_up) - total(*args_dn)) / (2 * eps)
+    assert o.normwise_err(dnum.cpu().double().numpy(), want_n) <= 1e-4
+    assert o.normwise_err(dden.cpu().double().numpy(), want_d) <= 1e-4
+
+
 def test_zero_batch_and_errors():
     basis, plan, st, ob, x, rng = setup("chebyshev8", 4, 8)
     xd = torch.zeros(0, 8, device="cuda")

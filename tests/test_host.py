@@ -290,7 +290,7 @@ def test_custom_op_fake_kernels_give_shapes_on_meta_tensors():
     assert torch.ops.kf.edge_derivative(x, c, None, kn, kc, ku, None, None, key, 1).shape == (33, 5, 7)
     rkey = K.plan_key(plan_for(kf.Rational(5, 4)))
     num, den = torch.empty(7, 6, device="meta"), torch.empty(7, 4, device="meta")
-    p, dn, dd = torch.ops.kf.rational_bwd(x, g, torch.empty(5, 7, 1, device="meta"), None, num, den, rkey)
+    p, dn, dd = torch.ops.kf.rational_bwd(x, g, torch.empty(5, 7, 1, device="meta"), None, num, den, rkey, 0)
     assert p.shape == (33, 7) and dn.shape == (7, 6) and dd.shape == (7, 4)
 
 
