@@ -193,6 +193,31 @@ int kf_rational_param_grad(const kf_basis *basis, int dtype, int64_t batch, int6
                            size_t workspace_bytes, void *stream);
 
 /*
+ * The rational part of F's backward in one call: p = P_{m+1}(x, g, c) (the input gradient
+ * without w, batch x n_in in dtype) and the gradients of sum_{b,o} g[b,o] F_m(x, c, w)[b,o]
+ * with respect to the rational parameters, m = basis->order (dnum, dden float32,
+ * overwritten). What autograd computes through Rational._eval inside the reference's
+ * _F.backward (kanforge/torch/kernels.py:79-87, kanforge/bases/rational.py:84-101). At m = 0
+ * for numerator degree 5 / denominator degree 4 in bf16 it fuses the input gradient and the
+ * parameter reduction into one pass over h = g c^T. Workspace of
+ * kf_rational_bwd_workspace_bytes(...) bytes, 256-byte aligned.
+ */
+size_t kf_rational_bwd_workspace_bytes(const kf_basis *basis, int dtype, int64_t batch, int64_t n_in, int64_t n_out);
+int kf_rational_bwd(const kf_basis *basis, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void *x,
+                    const void *g, const void *c, const void *w, void *p, float *dnum, float *dden, void *workspace,
+                    size_t workspace_bytes, void *stream);
+
+/*
+ * out[n] = sum_b g[b, n] for g (rows, n), accumulated in float32, out (n) in dtype: the bias
+ * gradient of the layer's bias add (kanforge/torch/layers.py:191, where torch autograd sums).
+ * Deterministic (slabs of rows summed in order). Workspace of
+ * kf_column_sums_workspace_bytes(rows, n) bytes.
+ */
+size_t kf_column_sums_workspace_bytes(int64_t rows, int64_t n);
+int kf_column_sums(int dtype, int64_t rows, int64_t n, const void *g, void *out, void *workspace,
+                   size_t workspace_bytes, void *stream);
+
+/*
  * Diagnostics, no reference counterpart: the card's sustained bf16 MFMA rate. Launches `blocks`
  * workgroups of 4 waves, each running iters x 8 v_mfma_f32_32x32x16_bf16 on pseudo-random
  * operands (taken in rotation from eight register sets when `rotate`, else one fixed set).

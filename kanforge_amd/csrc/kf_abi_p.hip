@@ -90,7 +90,7 @@ int launch_p_dma(const WsP& L, hipStream_t s, const KBasis& kb, int64_t batch, i
 
 template <typename T>
 int run_P(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
-          const void* g, const void* c, void* p, float* h, void* ws, hipStream_t s) {
+          const void* g, const void* c, void* p, float* h, void* ws, hipStream_t s, bool h_only = false) {
   if constexpr (sizeof(T) == 4)
     if (bspline_sparse(b, dtype)) return launch_p_sparse<T>(kb, b->spline_k, batch, n_in, n_out, x, g, c, p, s);
   WsP L = ws_p(b, dtype, batch, n_in, n_out);
@@ -120,7 +120,7 @@ int run_P(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
         float* hb = h ? h : (float*)((char*)ws + L.cfmt + L.gpad);
         void* gws = (char*)ws + L.cfmt + L.gpad + L.hbuf;
         rc = gemm_nt(batch, n_in, L.OUTP, ga, gstride, cfmt, L.OUTP, hb, n_in, true, gws, L.gemm, s);
-        if (rc) return rc;
+        if (rc || h_only) return rc;
         long blocks = ((long)batch * (n_in / 8) + 255) / 256;
         if (blocks > 65535 * 4) blocks = 65535 * 4;
         auto map = kb.order == 0   ? rational_map_kernel<bf16, bf16, 0>
@@ -150,9 +150,68 @@ int run_P(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
     default: return launch_p_t<T, 4, 2, 1, 12>(L, s, kb, batch, n_in, n_out, x, g, cfmt, p, h);
   }
 }
+constexpr int kRatBwdRows = 64;  // rows per chunk of the fused rational backward
+
+// whether the fused order-0 rational backward applies (the bf16 GEMM route of run_P and the
+// eight-input kernels)
+bool rational_bwd_fuses(const KBasis& kb, int dtype, int64_t n_in, const void* x, const void* g, const void* w,
+                        const void* p) {
+  return dtype == KF_BF16 && kb.order == 0 && rational_fast(kb, n_in) && aligned16(x) && aligned16(p) &&
+         (!w || aligned16(w)) && p_uses_dma(fw_index(1));
+}
 }  // namespace
 
 extern "C" {
+
+size_t kf_rational_bwd_workspace_bytes(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out) {
+  if (!b || b->kind != KF_KIND_RATIONAL || b->group_size < 1 || batch < 0 || n_in < 0 || n_out < 0) return 0;
+  // parameter partials: the fused kernel's 64-row chunks or the unfused reduction's, whichever is more
+  const size_t fused = align256((size_t)((batch + kRatBwdRows - 1) / kRatBwdRows) * (n_in / b->group_size) *
+                                (b->num_deg + 1 + b->den_deg) * sizeof(float));
+  const size_t plain = kf_rational_workspace_bytes(b, batch, n_in);
+  return ws_p(b, dtype, batch, n_in, n_out).total + align256((size_t)batch * n_in * sizeof(float)) +
+         (fused > plain ? fused : plain);
+}
+
+int kf_rational_bwd(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
+                    const void* g, const void* c, const void* w, void* p, float* dnum, float* dden, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+  g_err.clear();
+  int rc = validate_common(b, dtype, batch, n_in, n_out);
+  if (rc) return rc;
+  if (b->kind != KF_KIND_RATIONAL) return fail(KF_EINVAL, "kf_rational_bwd needs the rational kind");
+  if (!p || !dnum || !dden) return fail(KF_EINVAL, "kf_rational_bwd: NULL output");
+  const size_t need = kf_rational_bwd_workspace_bytes(b, dtype, batch, n_in, n_out);
+  if (batch > 0 && n_in > 0 && (!workspace || workspace_bytes < need))
+    return fail(KF_EWORKSPACE, "kf_rational_bwd: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  if (reinterpret_cast<uintptr_t>(workspace) & 255) return fail(KF_EWORKSPACE, "kf_rational_bwd: workspace must be 256-byte aligned");
+  // P at order m + 1 with h = g c^T, then the gradients of sum h w phi^(m)
+  kf_basis b1 = *b;
+  b1.order = b->order + 1;
+  const WsP L = ws_p(b, dtype, batch, n_in, n_out);
+  char* base = (char*)workspace;
+  float* hb = (float*)(base + L.total);
+  void* rws = base + L.total + align256((size_t)batch * n_in * sizeof(float));
+  const size_t rbytes = kf_rational_workspace_bytes(b, batch, n_in);
+  KBasis kb = to_kbasis(b);
+  if (batch > 0 && n_in > 0 && n_out > 0 && x && g && c && rational_bwd_fuses(kb, dtype, n_in, x, g, w, p)) {
+    hipStream_t s = (hipStream_t)stream;
+    rc = run_P<bf16>(kb, b, dtype, batch, n_in, n_out, x, g, c, p, hb, workspace, s, true);
+    if (rc) return rc;
+    const int groups = (int)(n_in / b->group_size), chunks = (int)((batch + kRatBwdRows - 1) / kRatBwdRows);
+    hipLaunchKernelGGL((rational_bwd_fast<bf16, kRatBwdRows>), dim3((unsigned)groups, (unsigned)chunks), dim3(256), 0, s,
+                       kb, (int)batch, (int)n_in, (const bf16*)x, (const float*)hb, (const bf16*)w, (bf16*)p,
+                       (float*)rws);
+    rc = check_launch("rational backward");
+    if (rc) return rc;
+    hipLaunchKernelGGL(rational_grad_final, dim3(1), dim3(256), 0, s, groups, b->num_deg + 1, b->den_deg, chunks,
+                       (const float*)rws, dnum, dden);
+    return check_launch("rational_grad_final");
+  }
+  rc = kf_P(&b1, dtype, batch, n_in, n_out, x, g, c, p, hb, workspace, L.total, stream);
+  if (rc) return rc;
+  return kf_rational_param_grad(b, dtype, batch, n_in, x, hb, w, dnum, dden, rws, rbytes, stream);
+}
 
 int kf_P(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* g,
          const void* c, void* p, float* h, void* workspace, size_t workspace_bytes, void* stream) {

@@ -229,6 +229,82 @@ __global__ __launch_bounds__(256) void rational_grad_fast(KBasis bs, int B, int 
         red[0][threadIdx.x] + red[1][threadIdx.x] + red[2][threadIdx.x] + red[3][threadIdx.x];
 }
 
+// Fused rational backward at order 0 (GR-KAN degrees): one pass over x, H and w writes
+// p[b,i] = H[b,i] phi'(x[b,i]) (the input gradient) and, per (group, chunk of RROWS rows), the
+// partial sums of H w dphi/dtheta (as rational_grad_fast). Eight consecutive inputs per thread.
+template <typename T, int RROWS>
+__global__ __launch_bounds__(256) void rational_bwd_fast(KBasis bs, int B, int IN, const T* __restrict__ x,
+                                                         const float* __restrict__ hbuf, const T* __restrict__ w,
+                                                         T* __restrict__ p, float* __restrict__ part) {
+  constexpr int NP = 6, NQ = 4, NPAR = NP + NQ;
+  const int g = blockIdx.x, chunk = blockIdx.y, gs = bs.group_size;
+  float a[NP], c[NQ];
+#pragma unroll
+  for (int q = 0; q < NP; ++q) a[q] = bs.num[g * NP + q];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) c[q] = bs.den[g * NQ + q];
+  float acc[NPAR];
+#pragma unroll
+  for (int q = 0; q < NPAR; ++q) acc[q] = 0.f;
+  const int per_row = gs / 8;
+  const int n = RROWS * per_row;
+  for (int e = threadIdx.x; e < n; e += 256) {
+    const int r = e / per_row, b = chunk * RROWS + r;
+    if (b >= B) break;  // rows grow with e
+    const size_t off = (size_t)b * IN + g * gs + (e % per_row) * 8;
+    float xv[8], hv[8], wv[8], pv[8];
+    load8<T>(x + off, xv);
+    load8<float>(hbuf + off, hv);
+    if (w) load8<T>(w + off, wv);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float xx = xv[k];
+      // P, P' and q, q' (Q = x q) by simultaneous Horner; phi = P / D, D = 1 + |Q|,
+      // phi' = (P' - phi sign(Q) Q') / D with one reciprocal shared by every term
+      float P = a[NP - 1], dP = 0.f;
+#pragma unroll
+      for (int q = NP - 2; q >= 0; --q) {
+        dP = fmaf(dP, xx, P);
+        P = fmaf(P, xx, a[q]);
+      }
+      float qq = c[NQ - 1], dq = 0.f;
+#pragma unroll
+      for (int q = NQ - 2; q >= 0; --q) {
+        dq = fmaf(dq, xx, qq);
+        qq = fmaf(qq, xx, c[q]);
+      }
+      const float Q = xx * qq, dQ = fmaf(xx, dq, qq);
+      const float sgn = (Q > 0.f) ? 1.f : ((Q < 0.f) ? -1.f : 0.f);
+      const float invD = __builtin_amdgcn_rcpf(1.f + fabsf(Q));
+      const float phi = P * invD;
+      pv[k] = hv[k] * ((dP - phi * sgn * dQ) * invD);
+      const float hh = w ? hv[k] * wv[k] : hv[k];
+      const float hd = hh * invD, hq = -hd * phi * sgn;
+      float xp = 1.f;
+#pragma unroll
+      for (int q = 0; q < NP; ++q) {
+        if (q < NQ) acc[NP + q] = fmaf(hq, xp * xx, acc[NP + q]);
+        acc[q] = fmaf(hd, xp, acc[q]);
+        xp *= xx;
+      }
+    }
+    store8<T>(p + off, pv);
+  }
+  __shared__ float red[4][NPAR];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int q = 0; q < NPAR; ++q) {
+    float v = acc[q];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    if (lane == 0) red[wave][q] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < NPAR)
+    part[((size_t)chunk * gridDim.x + g) * NPAR + threadIdx.x] =
+        red[0][threadIdx.x] + red[1][threadIdx.x] + red[2][threadIdx.x] + red[3][threadIdx.x];
+}
+
 // Partial sums, per (group, chunk of RROWS rows), of the gradients of
 //   sum_{b,i} h[b,i] w[b,i] phi^(M)(x[b,i])          (M >= 1, GR-KAN degrees P 5 / Q 4)
 // with respect to the group's a_0..a_5 and b_1..b_4: forward-mode derivatives of the quotient

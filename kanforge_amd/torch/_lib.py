@@ -36,6 +36,10 @@ EXPORTS = (
     "kf_bspline_interval",
     "kf_rational_workspace_bytes",
     "kf_rational_param_grad",
+    "kf_rational_bwd_workspace_bytes",
+    "kf_rational_bwd",
+    "kf_column_sums_workspace_bytes",
+    "kf_column_sums",
     "kf_probe_mfma",
     "kf_lut_forward",
     "kf_last_error",
@@ -99,6 +103,14 @@ def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
         for name in ("kf_F", "kf_F_noalloc", "kf_G", "kf_P", "kf_features", "kf_edge_derivative", "kf_bspline_interval", "kf_rational_param_grad"):
             getattr(lib, name).restype = c_int
         lib.kf_probe_mfma.argtypes = [c_int, c_int, c_int, c_void_p, c_void_p]
+        lib.kf_rational_bwd_workspace_bytes.argtypes = [P, c_int, c_int64, c_int64, c_int64]
+        lib.kf_rational_bwd_workspace_bytes.restype = c_size_t
+        lib.kf_rational_bwd.argtypes = [P, c_int, c_int64, c_int64, c_int64] + [c_void_p] * 7 + [c_void_p, c_size_t, c_void_p]
+        lib.kf_rational_bwd.restype = c_int
+        lib.kf_column_sums_workspace_bytes.argtypes = [c_int64, c_int64]
+        lib.kf_column_sums_workspace_bytes.restype = c_size_t
+        lib.kf_column_sums.argtypes = [c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]
+        lib.kf_column_sums.restype = c_int
         lib.kf_lut_forward.argtypes = [c_int, c_int64, c_int64, c_int64, c_int64] + [c_void_p] * 10
         lib.kf_probe_mfma.restype = c_int
         lib.kf_lut_forward.restype = c_int

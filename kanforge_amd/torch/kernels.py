@@ -18,6 +18,7 @@ Differences from the reference, by design:
 from __future__ import annotations
 
 import ctypes
+import weakref
 from functools import lru_cache
 from typing import Optional
 
@@ -99,8 +100,27 @@ def bspline_state(grid: torch.Tensor, order: int) -> BasisState:
     )
 
 
+# float32 copies of rational parameters, reused while the parameter is the same tensor at the
+# same version (one cast per parameter update instead of one per launch)
+_F32_COPIES: dict = {}
+
+
+def _as_f32(t: torch.Tensor) -> torch.Tensor:
+    if t.dtype == torch.float32 and t.is_contiguous():
+        return t.detach()
+    key = (id(t), t.device, t.dtype)
+    hit = _F32_COPIES.get(key)
+    if hit is not None and hit[0]() is t and hit[1] == t._version:
+        return hit[2]
+    out = t.detach().float().contiguous()
+    if len(_F32_COPIES) >= 64:
+        _F32_COPIES.clear()
+    _F32_COPIES[key] = (weakref.ref(t), t._version, out)
+    return out
+
+
 def rational_state(num: torch.Tensor, den: torch.Tensor, group_size: int) -> BasisState:
-    return BasisState(num=num.detach().float().contiguous(), den=den.detach().float().contiguous(), group_size=group_size)
+    return BasisState(num=_as_f32(num), den=_as_f32(den), group_size=group_size)
 
 
 def _desc(plan: KernelPlan, m: int, st: BasisState | None):
@@ -296,9 +316,25 @@ def op_rational_bwd(
     sum h w phi^(m)."""
     pl = plan_of(plan)
     st = _state(None, None, None, num, den, x.shape[1])
-    h = torch.empty(x.shape, dtype=torch.float32, device=x.device)
-    p1 = _raw("P", pl, m + 1, x, g, c, st, c.shape[0], h=h)
-    dnum, dden = _rational_param_grad(pl, st, x, h, w, m)
+    _require_device(x)
+    lib = _lib.load()
+    desc, keep = _desc(pl, m, st)
+    dt = _dtype_code(x.dtype)
+    batch, n_in = x.shape
+    n_out = c.shape[0]
+    x, g, c = x.contiguous(), g.contiguous(), c.contiguous()
+    w = None if w is None else w.contiguous()
+    p1 = torch.empty_like(x)
+    dnum, dden = torch.empty_like(st.num), torch.empty_like(st.den)
+    nbytes = lib.kf_rational_bwd_workspace_bytes(ctypes.byref(desc), dt, batch, n_in, n_out)
+    ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=x.device)
+    with torch.cuda.device(x.device):
+        rc = lib.kf_rational_bwd(
+            ctypes.byref(desc), dt, batch, n_in, n_out, _ptr(x), _ptr(g), _ptr(c), _ptr(w), _ptr(p1), _ptr(dnum),
+            _ptr(dden), _ptr(ws), ws.numel(), _stream(x.device),
+        )
+    _lib.check(rc, "kf_rational_bwd")
+    del keep
     return p1, dnum.to(num.dtype), dden.to(den.dtype)
 
 
@@ -511,6 +547,63 @@ def _features_backward(ctx, gphi):
 
 
 op_features.register_autograd(_features_backward, setup_context=_features_setup)
+
+
+@torch.library.custom_op("kf::column_sums", mutates_args=())
+def op_column_sums(g: torch.Tensor) -> torch.Tensor:
+    """sum over the rows of g (rows, n), float32 accumulation, g's dtype (kf_column_sums)."""
+    _require_device(g)
+    g = g.contiguous()
+    rows, n = g.shape
+    lib = _lib.load()
+    out = torch.empty(n, dtype=g.dtype, device=g.device)
+    nbytes = lib.kf_column_sums_workspace_bytes(rows, n)
+    ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=g.device)
+    with torch.cuda.device(g.device):
+        rc = lib.kf_column_sums(_dtype_code(g.dtype), rows, n, _ptr(g), _ptr(out), _ptr(ws), ws.numel(), _stream(g.device))
+    _lib.check(rc, "kf_column_sums")
+    return out
+
+
+@op_column_sums.register_fake
+def _(g):
+    return g.new_empty(g.shape[1])
+
+
+@torch.library.custom_op("kf::bias_add", mutates_args=())
+def op_bias_add(y: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
+    """y + bias over the last dimension; its bias gradient runs on kf_column_sums."""
+    return y + bias
+
+
+@op_bias_add.register_fake
+def _(y, bias):
+    return torch.empty_like(y)
+
+
+def _bias_setup(ctx, inputs, output):
+    ctx.bias_dtype = inputs[1].dtype
+
+
+def _bias_backward(ctx, gy):
+    gb = None
+    if ctx.needs_input_grad[1]:
+        gb = op_column_sums(gy.reshape(-1, gy.shape[-1])).to(ctx.bias_dtype)
+    return gy, gb
+
+
+op_bias_add.register_autograd(_bias_backward, setup_context=_bias_setup)
+
+
+BIAS_OP_MIN_ELEMENTS = 1 << 20  # below this a plain add costs less (one op dispatch fewer)
+
+
+def bias_add(y: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
+    """The layer's bias add: y + bias; for large outputs the bias gradient runs on
+    kf_column_sums (torch's reduction over the rows is several times slower there)."""
+    if y.numel() < BIAS_OP_MIN_ELEMENTS:
+        return y + bias
+    return op_bias_add(y, bias)
 
 
 def _rational_grads_of(plan, x2, h, m, num, den):

@@ -212,7 +212,7 @@ class KANLinear(nn.Module):
             edges = self.edge_derivative(x, 0)
             keep = torch.rand_like(edges) >= self.edge_dropout
             y = (edges * keep).sum(-1) / (1 - self.edge_dropout)
-            return y if self.bias is None else y + self.bias
+            return y if self.bias is None else _kernels.bias_add(y, self.bias)
         if not _compiling():
             self.uses_kernel(x.device)  # raises when the HIP path cannot run
         st = self._basis_state()
@@ -221,11 +221,14 @@ class KANLinear(nn.Module):
         else:
             y = _kernels.spline_forward(x, self.effective_coef(), st, self._plan_key)
         if self.base_weight is not None:
-            y = y + F.linear(self.base_activation(x), self.effective_base_weight())
+            # accumulated into y by the GEMM itself (C = y + act(x) W^T), no separate add
+            y2 = torch.addmm(y.reshape(-1, self.out_features), self.base_activation(x).reshape(-1, self.in_features),
+                             self.effective_base_weight().t())
+            y = y2.reshape(y.shape)
         if self._sym_codes:
             y = y + self._symbolic_sum(x)
         if self.bias is not None:
-            y = y + self.bias
+            y = _kernels.bias_add(y, self.bias)
         return y
 
     def uses_kernel(self, device: torch.device) -> bool:

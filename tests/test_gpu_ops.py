@@ -101,3 +101,28 @@ def test_compiled_layer_forward_backward_matches_eager(make, dtype):
     assert len(got) == len(want)
     for a, b in zip(got, want):
         torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("shape", [(16384, 768), (1000, 77), (3, 4096), (0, 5), (37, 8)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_column_sums_and_bias_add(shape, dtype):
+    """kf_column_sums against a float64 sum (bias gradients), including ragged and empty shapes
+    and a misaligned view; the bias-add op's gradients and opcheck."""
+    g = torch.randn(shape, generator=torch.Generator().manual_seed(1)).to(DEV, dtype)
+    got = torch.ops.kf.column_sums(g).double().cpu()
+    want = g.double().cpu().sum(0)
+    scale = max(1.0, float(want.abs().max())) if want.numel() else 1.0
+    tol = 2e-2 if dtype == torch.bfloat16 else 1e-5
+    assert float((got - want).abs().max() if want.numel() else 0.0) <= tol * scale
+    if shape[0] > 1 and shape[1] > 1:
+        view = g[:, 1:]  # rows not 16-byte aligned
+        np.testing.assert_allclose(torch.ops.kf.column_sums(view.contiguous()).double().cpu(), view.double().cpu().sum(0),
+                                   atol=tol * scale)
+        y = torch.randn(shape, device=DEV, dtype=dtype, requires_grad=True)
+        b = torch.randn(shape[1], device=DEV, dtype=dtype, requires_grad=True)
+        out = torch.ops.kf.bias_add(y, b)
+        out.backward(g)
+        assert torch.equal(y.grad, g)
+        np.testing.assert_allclose(b.grad.double().cpu(), want, atol=tol * scale)
+        torch.library.opcheck(torch.ops.kf.column_sums.default, (g,))
+        torch.library.opcheck(torch.ops.kf.bias_add.default, (y.detach().requires_grad_(), b.detach().requires_grad_()))
