@@ -485,6 +485,42 @@ def _hook_entries(timer):
     return unhook
 
 
+GRAPH_WORKLOADS = ("kan64",)  # launch-bound steps: also timed as one captured HIP graph
+
+
+def graph_timing(step, steps, warmup):
+    """(ms per replay, check) of the step captured as one HIP graph. Before timing, the graph is
+    replayed three times with eager steps in between and every replay's outputs are compared
+    with the eager outputs (bitwise: the same kernels run); on a mismatch the graph is not used."""
+    torch.cuda.synchronize()
+    ref = [t.detach().clone() for t in step()]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = step()
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        if not all(torch.equal(a, b) for a, b in zip(outs, ref)):
+            return None, "replay differs from the eager step"
+        step()
+        torch.cuda.synchronize()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps * 1e3, "replays equal the eager step"
+
+
 def run_workload(name, args, dev, cpu=True):
     """One layer shape: whole-step throughput, HIP-event means of every entry point it calls,
     the roofline of the entry with the most GPU time and the CPU leg."""
@@ -516,6 +552,10 @@ def run_workload(name, args, dev, cpu=True):
         "contraction_tflops": flops / (ms * 1e-3) / 1e12,
         "roofline": roof,
     }
+    if name in GRAPH_WORKLOADS:
+        gms, check = graph_timing(step, args.steps, args.warmup)
+        line["graph"] = {"ms_per_step": gms, "value": None if gms is None else units / (gms * 1e-3), "check": check,
+                         "note": "the same step captured once as a HIP graph and replayed (launch-bound layer)"}
     if cpu:
         line["cpu_baseline"] = cpu_leg()
     return line
@@ -697,7 +737,7 @@ def main():
         for name in WORKLOADS:
             line = run_workload(name, sub, dev, cpu=not args.no_cpu)
             keep = ("value", "unit", "dtype", "ms_per_step", "steps", "config", "per_entry_ms", "calls_per_step",
-                    "contraction_tflops", "roofline", "cpu_baseline")
+                    "contraction_tflops", "roofline", "graph", "cpu_baseline")
             out["workloads"][name] = {k: line[k] for k in keep if k in line}
             torch.cuda.empty_cache()
     print(json.dumps(out), flush=True)
