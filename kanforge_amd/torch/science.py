@@ -3,13 +3,15 @@
 ``derivative``, ``gradient`` and ``laplacian`` accept any callable, as in the reference, and
 differentiate it with autograd (through KAN layers every node is an F, G or P launch of the HIP
 kernels). For a chain of KAN layers (``KAN``, or an ``nn.Sequential`` of ``KANLinear`` with SiLU or
-no base branch) ``laplacian`` instead propagates second-order Taylor coefficients forward: per
-layer and input dimension d, with h' = dh/dx_d and h'' = d2h/dx_d2,
-    h_out   = F_0(h, c) + W silu(h) + b
-    h'_out  = F_1(h, c, w=h')                       + W (silu'(h) h')
-    h''_out = F_2(h, c, w=h'^2) + F_1(h, c, w=h'')  + W (silu''(h) h'^2 + silu'(h) h'')
-with the rows of every dimension stacked into one F launch per derivative order. The result is
-the same function of x and of the parameters, and stays differentiable (F's own autograd).
+no base branch) ``laplacian`` instead propagates second-order Taylor coefficients forward. Per
+layer, with h'_d = dh/dx_d for every input dimension d and S = sum_d d2h/dx_d2:
+    h_out    = F_0(h, c) + W silu(h) + b
+    h'_out,d = F_1(h, c, w=h'_d)                          + W (silu'(h) h'_d)
+    S_out    = F_2(h, c, w=sum_d h'_d^2) + F_1(h, c, w=S) + W (silu''(h) sum_d h'_d^2 + silu'(h) S)
+F is linear in its weight w, so the second-order terms of all dimensions collapse into one F_2
+and one F_1 row block: each layer runs F on (D + 3) rows per point (the first layer D + 2), the
+rows of the first-order launches stacked into one call. The result is the same function of x
+and of the parameters, and stays differentiable (F's own autograd).
 """
 
 from __future__ import annotations
@@ -78,8 +80,9 @@ def _silu_terms(h: torch.Tensor):
     return h * s, d1, d2
 
 
-def _taylor_layer(layer, h: torch.Tensor, hp: torch.Tensor, hpp: torch.Tensor | None):
-    """A layer's (h, h', h'') from its input's: h (B, in), hp and hpp (D, B, in) (hpp None: zero)."""
+def _taylor_layer(layer, h: torch.Tensor, hp: torch.Tensor, S: torch.Tensor | None):
+    """A layer's (h, h', S) from its input's: h (B, in), hp (D, B, in) the first derivatives
+    along every input dimension, S (B, in) the sum of the second derivatives (None: zero)."""
     from . import kernels as K
 
     D, B, n_in = hp.shape
@@ -93,32 +96,33 @@ def _taylor_layer(layer, h: torch.Tensor, hp: torch.Tensor, hpp: torch.Tensor | 
         num, den = layer.basis_numerator, layer.basis_denominator
     # value
     y = K.prim_F(hk, c, None, st, key, 0, num, den)
-    # first-order rows (h' of every dimension, then h'' of every dimension) in one launch
-    w1 = hp if hpp is None else torch.cat([hp, hpp], 0)
+    # first order: the D directions and S stacked into one launch
+    w1 = hp if S is None else torch.cat([hp, S[None]], 0)
     n1 = w1.shape[0]
     f1 = K.prim_F(hk.repeat(n1, 1), c, w1.reshape(n1 * B, n_in).to(dt), st, key, 1, num, den).reshape(n1, B, -1)
-    f2 = K.prim_F(hk.repeat(D, 1), c, (hp * hp).reshape(D * B, n_in).to(dt), st, key, 2, num, den).reshape(D, B, -1)
+    sq = (hp * hp).sum(0)  # sum_d h'_d^2
+    f2 = K.prim_F(hk, c, sq.to(dt), st, key, 2, num, den)
     yp = f1[:D]
-    ypp = f2 if hpp is None else f2 + f1[D:]
+    S_out = f2 if S is None else f2 + f1[D]
     W = layer.effective_base_weight()
     if W is not None:
         s0, s1, s2 = _silu_terms(h)
         y = y + F.linear(s0, W)
         yp = yp + F.linear(s1 * hp, W)
-        base2 = s2 * hp * hp if hpp is None else s2 * hp * hp + s1 * hpp
-        ypp = ypp + F.linear(base2, W)
+        base2 = s2 * sq if S is None else s2 * sq + s1 * S
+        S_out = S_out + F.linear(base2, W)
     if layer.bias is not None:
         y = y + layer.bias
-    return y.to(h.dtype), yp.to(h.dtype), ypp.to(h.dtype)
+    return y.to(h.dtype), yp.to(h.dtype), S_out.to(h.dtype)
 
 
 def _laplacian_forward(layers, x: torch.Tensor) -> torch.Tensor:
     B, D = x.shape
     h = x
     hp = torch.eye(D, dtype=x.dtype, device=x.device)[:, None, :].expand(D, B, D)  # dx/dx_d
-    hpp = None
+    S = None
     for layer in layers:
-        h, hp, hpp = _taylor_layer(layer, h, hp, hpp)
+        h, hp, S = _taylor_layer(layer, h, hp, S)
     if h.shape[-1] != 1:
         raise ValueError(f"laplacian needs a scalar field, the network has {h.shape[-1]} outputs")
-    return hpp.sum(0)[:, 0]
+    return S[:, 0]
