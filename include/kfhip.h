@@ -218,6 +218,16 @@ int kf_column_sums(int dtype, int64_t rows, int64_t n, const void *g, void *out,
                    size_t workspace_bytes, void *stream);
 
 /*
+ * Second-order Taylor terms of the SiLU base branch, for the forward-mode Laplacian of a KAN
+ * chain (what reverse-over-reverse autograd computes through kanforge/torch/science.py:25-46 and
+ * the base branch of kanforge/torch/layers.py:185-191): for h (batch, n), hp (D, batch, n) and S
+ * (batch, n) or NULL, writes sq = sum_d hp_d^2 (batch, n) and the stacked GEMM operand
+ * A ((D + 2) batch, n) = [silu(h); silu'(h) hp_d for each d; silu''(h) sq + silu'(h) S].
+ */
+int kf_silu_taylor(int dtype, int64_t D, int64_t batch, int64_t n, const void *h, const void *hp, const void *S,
+                   void *A, void *sq, void *stream);
+
+/*
  * Diagnostics, no reference counterpart: the card's sustained bf16 MFMA rate. Launches `blocks`
  * workgroups of 4 waves, each running iters x 8 v_mfma_f32_32x32x16_bf16 on pseudo-random
  * operands (taken in rotation from eight register sets when `rotate`, else one fixed set).

@@ -40,6 +40,7 @@ EXPORTS = (
     "kf_rational_bwd",
     "kf_column_sums_workspace_bytes",
     "kf_column_sums",
+    "kf_silu_taylor",
     "kf_probe_mfma",
     "kf_lut_forward",
     "kf_last_error",
@@ -111,6 +112,8 @@ def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
         lib.kf_column_sums_workspace_bytes.restype = c_size_t
         lib.kf_column_sums.argtypes = [c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]
         lib.kf_column_sums.restype = c_int
+        lib.kf_silu_taylor.argtypes = [c_int, c_int64, c_int64, c_int64] + [c_void_p] * 6
+        lib.kf_silu_taylor.restype = c_int
         lib.kf_lut_forward.argtypes = [c_int, c_int64, c_int64, c_int64, c_int64] + [c_void_p] * 10
         lib.kf_probe_mfma.restype = c_int
         lib.kf_lut_forward.restype = c_int

@@ -595,6 +595,62 @@ def _bias_backward(ctx, gy):
 op_bias_add.register_autograd(_bias_backward, setup_context=_bias_setup)
 
 
+@torch.library.custom_op("kf::silu_taylor", mutates_args=())
+def op_silu_taylor(h: torch.Tensor, hp: torch.Tensor, S: Opt) -> tuple[torch.Tensor, torch.Tensor]:
+    """(A, sq) of the SiLU base branch's second-order Taylor terms (kf_silu_taylor): for h (B, n),
+    hp (D, B, n), S (B, n) or None, sq = sum_d hp_d^2 and the stacked GEMM operand
+    A = [silu(h); silu'(h) hp_d ...; silu''(h) sq + silu'(h) S] ((D + 2) B, n)."""
+    _require_device(h)
+    D, B, n = hp.shape
+    h, hp = h.contiguous(), hp.contiguous()
+    S = None if S is None else S.contiguous()
+    A = torch.empty((D + 2) * B, n, dtype=h.dtype, device=h.device)
+    sq = torch.empty_like(h)
+    with torch.cuda.device(h.device):
+        rc = _lib.load().kf_silu_taylor(_dtype_code(h.dtype), D, B, n, _ptr(h), _ptr(hp), _ptr(S), _ptr(A), _ptr(sq),
+                                        _stream(h.device))
+    _lib.check(rc, "kf_silu_taylor")
+    return A, sq
+
+
+@op_silu_taylor.register_fake
+def _(h, hp, S):
+    D, B, n = hp.shape
+    return h.new_empty((D + 2) * B, n), torch.empty_like(h)
+
+
+def _silu_taylor_setup(ctx, inputs, output):
+    h, hp, S = inputs
+    ctx.save_for_backward(h, hp, S, output[1])
+
+
+def _silu_taylor_backward(ctx, gA, gsq):
+    """Derivatives of A and sq through silu^(m), m <= 3, in closed form (s = sigmoid(h)):
+    d1 = s (1 + h (1 - s)), d2 = s (1 - s) (2 + h (1 - 2 s)),
+    d3 = s (1 - s) (3 (1 - 2 s) + h (1 - 6 s + 6 s^2))."""
+    h, hp, S, sq = ctx.saved_tensors
+    D, B, n = hp.shape
+    f = torch.float32
+    x, hpf = h.to(f), hp.to(f)
+    s = torch.sigmoid(x)
+    d1 = s * (1 + x * (1 - s))
+    d2 = s * (1 - s) * (2 + x * (1 - 2 * s))
+    d3 = s * (1 - s) * (3 * (1 - 2 * s) + x * (1 - 6 * s + 6 * s * s))
+    gA = gA.to(f)
+    g0, g1, g2 = gA[:B], gA[B:(D + 1) * B].reshape(D, B, n), gA[(D + 1) * B:]
+    sqf = sq.to(f)
+    dh = g0 * d1 + (g1 * hpf).sum(0) * d2 + g2 * (d3 * sqf)
+    if S is not None:
+        dh = dh + g2 * d2 * S.to(f)
+    gq = g2 * d2 if gsq is None else g2 * d2 + gsq.to(f)
+    dhp = g1 * d1 + 2 * gq * hpf
+    dS = None if S is None else (g2 * d1).to(S.dtype)
+    return dh.to(h.dtype), dhp.to(hp.dtype), dS
+
+
+op_silu_taylor.register_autograd(_silu_taylor_backward, setup_context=_silu_taylor_setup)
+
+
 BIAS_OP_MIN_ELEMENTS = 1 << 20  # below this a plain add costs less (one op dispatch fewer)
 
 

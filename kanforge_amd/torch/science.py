@@ -72,14 +72,6 @@ def kan_chain(fn) -> list | None:
     return mods
 
 
-def _silu_terms(h: torch.Tensor):
-    """(silu(h), silu'(h), silu''(h)) with s = sigmoid(h)."""
-    s = torch.sigmoid(h)
-    d1 = s * (1 + h * (1 - s))
-    d2 = s * (1 - s) * (2 + h * (1 - 2 * s))
-    return h * s, d1, d2
-
-
 def _taylor_layer(layer, h: torch.Tensor, hp: torch.Tensor, S: torch.Tensor | None):
     """A layer's (h, h', S) from its input's: h (B, in), hp (D, B, in) the first derivatives
     along every input dimension, S (B, in) the sum of the second derivatives (None: zero)."""
@@ -94,23 +86,24 @@ def _taylor_layer(layer, h: torch.Tensor, hp: torch.Tensor, S: torch.Tensor | No
     num = den = None
     if layer._plan.kind == "rational":
         num, den = layer.basis_numerator, layer.basis_denominator
-    # value
+    W = layer.effective_base_weight()
+    if W is not None:
+        # the base branch's operands of all three orders in one pass, and sum_d h'_d^2
+        A, sq = K.op_silu_taylor(h, hp, S)
+    else:
+        sq = (hp * hp).sum(0)
+    # value, first order (the D directions and S stacked into one launch), second order
     y = K.prim_F(hk, c, None, st, key, 0, num, den)
-    # first order: the D directions and S stacked into one launch
     w1 = hp if S is None else torch.cat([hp, S[None]], 0)
     n1 = w1.shape[0]
     f1 = K.prim_F(hk.repeat(n1, 1), c, w1.reshape(n1 * B, n_in).to(dt), st, key, 1, num, den).reshape(n1, B, -1)
-    sq = (hp * hp).sum(0)  # sum_d h'_d^2
     f2 = K.prim_F(hk, c, sq.to(dt), st, key, 2, num, den)
-    yp = f1[:D]
-    S_out = f2 if S is None else f2 + f1[D]
-    W = layer.effective_base_weight()
+    S_spline = f2 if S is None else f2 + f1[D]
+    n_out = y.shape[-1]
+    Z = torch.cat([y, f1[:D].reshape(D * B, n_out), S_spline], 0)
     if W is not None:
-        s0, s1, s2 = _silu_terms(h)
-        y = y + F.linear(s0, W)
-        yp = yp + F.linear(s1 * hp, W)
-        base2 = s2 * sq if S is None else s2 * sq + s1 * S
-        S_out = S_out + F.linear(base2, W)
+        Z = torch.addmm(Z, A.to(dt), W.t())  # the base branch of y, every h'_d and S: one GEMM
+    y, yp, S_out = Z[:B], Z[B:(D + 1) * B].reshape(D, B, n_out), Z[(D + 1) * B:]
     if layer.bias is not None:
         y = y + layer.bias
     return y.to(h.dtype), yp.to(h.dtype), S_out.to(h.dtype)

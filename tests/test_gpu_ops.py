@@ -126,3 +126,42 @@ def test_column_sums_and_bias_add(shape, dtype):
         np.testing.assert_allclose(b.grad.double().cpu(), want, atol=tol * scale)
         torch.library.opcheck(torch.ops.kf.column_sums.default, (g,))
         torch.library.opcheck(torch.ops.kf.bias_add.default, (y.detach().requires_grad_(), b.detach().requires_grad_()))
+
+
+@pytest.mark.parametrize("with_S", [False, True])
+def test_silu_taylor_values_and_gradients(with_S):
+    """kf::silu_taylor against the oracle's SiLU derivatives, and its closed-form backward against
+    autograd through the same terms written with torch ops (float32)."""
+    from oracle import kan64 as o
+
+    D, B, n = 2, 300, 17
+    gen = torch.Generator().manual_seed(4)
+    h = (torch.randn(B, n, generator=gen) * 2).to(DEV).requires_grad_()
+    hp = torch.randn(D, B, n, generator=gen).to(DEV).requires_grad_()
+    S = torch.randn(B, n, generator=gen).to(DEV).requires_grad_() if with_S else None
+    A, sq = torch.ops.kf.silu_taylor(h, hp, S)
+    hn, hpn = h.detach().double().cpu().numpy(), hp.detach().double().cpu().numpy()
+    d0, d1, d2 = (o.silu_derivative(hn, m) for m in (0, 1, 2))
+    sqn = (hpn ** 2).sum(0)
+    Sn = S.detach().double().cpu().numpy() if with_S else 0.0
+    want = np.concatenate([d0, (d1 * hpn).reshape(D * B, n), d2 * sqn + d1 * Sn], 0)
+    assert o.normwise_err(A.detach().double().cpu().numpy(), want) <= 1e-5
+    assert o.normwise_err(sq.detach().double().cpu().numpy(), sqn) <= 1e-6
+    gA = torch.randn(A.shape, generator=gen).to(DEV)
+    gq = torch.randn(sq.shape, generator=gen).to(DEV)
+    inputs = [h, hp] + ([S] if with_S else [])
+    got = torch.autograd.grad((A * gA).sum() + (sq * gq).sum(), inputs)
+
+    def ref(h, hp, S):
+        s = torch.sigmoid(h)
+        r1 = s * (1 + h * (1 - s))
+        r2 = s * (1 - s) * (2 + h * (1 - 2 * s))
+        q = (hp * hp).sum(0)
+        last = r2 * q + (0 if S is None else r1 * S)
+        return torch.cat([h * s, (r1 * hp).reshape(D * B, n), last], 0), q
+
+    Ar, qr = ref(h, hp, S)
+    want_g = torch.autograd.grad((Ar * gA).sum() + (qr * gq).sum(), inputs)
+    for a, b in zip(got, want_g):
+        assert o.normwise_err(a.double().cpu().numpy(), b.double().cpu().numpy()) <= 1e-5
+    torch.library.opcheck(torch.ops.kf.silu_taylor.default, (h, hp, S))
