@@ -486,6 +486,8 @@ def _hook_entries(timer):
 
 
 GRAPH_WORKLOADS = ("kan64",)  # launch-bound steps: also timed as one captured HIP graph
+# B-spline layers: k + 1 of the K basis values are non-zero at any x (degree 3: 4 of K)
+SPARSE_MACS = {"kan64": (4, 8), "bspline_ffn": (4, 11), "lut_kan64": None}
 
 
 def graph_timing(step, steps, warmup):
@@ -552,6 +554,11 @@ def run_workload(name, args, dev, cpu=True):
         "contraction_tflops": flops / (ms * 1e-3) / 1e12,
         "roofline": roof,
     }
+    if SPARSE_MACS.get(name):
+        nz, K = SPARSE_MACS[name]
+        line["sparse_mac_fraction"] = nz / K
+        line["sparse_note"] = (f"{nz} of K = {K} B-spline values are non-zero per (row, input); the roofline counts "
+                               "the dense 2 B in K out FLOP, the reference's convention")
     if name in GRAPH_WORKLOADS:
         gms, check = graph_timing(step, args.steps, args.warmup)
         line["graph"] = {"ms_per_step": gms, "value": None if gms is None else units / (gms * 1e-3), "check": check,
@@ -737,7 +744,7 @@ def main():
         for name in WORKLOADS:
             line = run_workload(name, sub, dev, cpu=not args.no_cpu)
             keep = ("value", "unit", "dtype", "ms_per_step", "steps", "config", "per_entry_ms", "calls_per_step",
-                    "contraction_tflops", "roofline", "graph", "cpu_baseline")
+                    "contraction_tflops", "roofline", "graph", "sparse_mac_fraction", "cpu_baseline")
             out["workloads"][name] = {k: line[k] for k in keep if k in line}
             torch.cuda.empty_cache()
     print(json.dumps(out), flush=True)
