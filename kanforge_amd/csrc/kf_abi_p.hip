@@ -90,7 +90,8 @@ int launch_p_dma(const WsP& L, hipStream_t s, const KBasis& kb, int64_t batch, i
 
 template <typename T>
 int run_P(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
-          const void* g, const void* c, void* p, float* h, void* ws, hipStream_t s, bool h_only = false) {
+          const void* g, const void* c, void* p, float* h, void* ws, hipStream_t s, bool h_only = false,
+          bool h_bf16 = false) {
   if constexpr (sizeof(T) == 4)
     if (bspline_sparse(b, dtype)) return launch_p_sparse<T>(kb, b->spline_k, batch, n_in, n_out, x, g, c, p, s);
   WsP L = ws_p(b, dtype, batch, n_in, n_out);
@@ -119,7 +120,8 @@ int run_P(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
       if (rational_fast(kb, n_in) && kb.order <= 2 && aligned16(x) && aligned16(p) && aligned16(ga) && gstride % 8 == 0) {
         float* hb = h ? h : (float*)((char*)ws + L.cfmt + L.gpad);
         void* gws = (char*)ws + L.cfmt + L.gpad + L.hbuf;
-        rc = gemm_nt(batch, n_in, L.OUTP, ga, gstride, cfmt, L.OUTP, hb, n_in, true, gws, L.gemm, s);
+        // h_only: H alone, in bfloat16 when h_bf16 (the fused backward's operand)
+        rc = gemm_nt(batch, n_in, L.OUTP, ga, gstride, cfmt, L.OUTP, hb, n_in, !(h_only && h_bf16), gws, L.gemm, s);
         if (rc || h_only) return rc;
         long blocks = ((long)batch * (n_in / 8) + 255) / 256;
         if (blocks > 65535 * 4) blocks = 65535 * 4;
@@ -196,11 +198,12 @@ int kf_rational_bwd(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, i
   KBasis kb = to_kbasis(b);
   if (batch > 0 && n_in > 0 && n_out > 0 && x && g && c && rational_bwd_fuses(kb, dtype, n_in, x, g, w, p)) {
     hipStream_t s = (hipStream_t)stream;
-    rc = run_P<bf16>(kb, b, dtype, batch, n_in, n_out, x, g, c, p, hb, workspace, s, true);
+    // H = g c^T in bfloat16 (half the traffic of float32 between the GEMM and the fused pass)
+    rc = run_P<bf16>(kb, b, dtype, batch, n_in, n_out, x, g, c, p, hb, workspace, s, true, true);
     if (rc) return rc;
     const int groups = (int)(n_in / b->group_size), chunks = (int)((batch + kRatBwdRows - 1) / kRatBwdRows);
-    hipLaunchKernelGGL((rational_bwd_fast<bf16, kRatBwdRows>), dim3((unsigned)groups, (unsigned)chunks), dim3(256), 0, s,
-                       kb, (int)batch, (int)n_in, (const bf16*)x, (const float*)hb, (const bf16*)w, (bf16*)p,
+    hipLaunchKernelGGL((rational_bwd_fast<bf16, bf16, kRatBwdRows>), dim3((unsigned)groups, (unsigned)chunks), dim3(256),
+                       0, s, kb, (int)batch, (int)n_in, (const bf16*)x, (const bf16*)hb, (const bf16*)w, (bf16*)p,
                        (float*)rws);
     rc = check_launch("rational backward");
     if (rc) return rc;

@@ -229,12 +229,12 @@ __global__ __launch_bounds__(256) void rational_grad_fast(KBasis bs, int B, int 
         red[0][threadIdx.x] + red[1][threadIdx.x] + red[2][threadIdx.x] + red[3][threadIdx.x];
 }
 
-// Fused rational backward at order 0 (GR-KAN degrees): one pass over x, H and w writes
+// Fused rational backward at order 0 (GR-KAN degrees): one pass over x, H (float32 or bf16) and w writes
 // p[b,i] = H[b,i] phi'(x[b,i]) (the input gradient) and, per (group, chunk of RROWS rows), the
 // partial sums of H w dphi/dtheta (as rational_grad_fast). Eight consecutive inputs per thread.
-template <typename T, int RROWS>
+template <typename T, typename TH, int RROWS>
 __global__ __launch_bounds__(256) void rational_bwd_fast(KBasis bs, int B, int IN, const T* __restrict__ x,
-                                                         const float* __restrict__ hbuf, const T* __restrict__ w,
+                                                         const TH* __restrict__ hbuf, const T* __restrict__ w,
                                                          T* __restrict__ p, float* __restrict__ part) {
   constexpr int NP = 6, NQ = 4, NPAR = NP + NQ;
   const int g = blockIdx.x, chunk = blockIdx.y, gs = bs.group_size;
@@ -254,7 +254,7 @@ __global__ __launch_bounds__(256) void rational_bwd_fast(KBasis bs, int B, int I
     const size_t off = (size_t)b * IN + g * gs + (e % per_row) * 8;
     float xv[8], hv[8], wv[8], pv[8];
     load8<T>(x + off, xv);
-    load8<float>(hbuf + off, hv);
+    load8<TH>(hbuf + off, hv);
     if (w) load8<T>(w + off, wv);
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
