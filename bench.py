@@ -60,7 +60,7 @@ def parse():
     )
     ap.add_argument("--no-workloads", action="store_true", help="leave the other layer shapes out of the headline line")
     ap.add_argument("--workload-steps", type=int, default=10, help="timed steps of each other layer shape in the headline line")
-    ap.add_argument("--only", choices=["F", "G", "P", "edge", "features", "rational_param_grad", "lut"],
+    ap.add_argument("--only", choices=["F", "G", "P", "edge", "features", "rational_param_grad", "rational_bwd", "lut"],
                     help="counter runs: replay only this entry point's calls of one step of --workload")
     return ap.parse_args()
 
@@ -102,6 +102,13 @@ def _work(label, args):
         n_in, _size, n_out = layer.tables.shape
         rows = x.numel() // n_in
         return 3.0 * rows * n_in * n_out, float(4 * rows * (n_in + n_out) + layer.tables.nbytes)
+    if label == "rational_bwd":
+        _plan, _m, _st, x, g, c = args[:6]
+        w = args[6] if len(args) > 6 else None
+        batch, n_in = x.shape
+        n_out, es = c.shape[0], x.element_size()
+        elems = 2 * batch * n_in + batch * n_out + n_out * n_in + (0 if w is None else batch * n_in)
+        return 2.0 * batch * n_in * n_out, float(es * elems)
     if label == "rational_param_grad":
         _plan, _st, x, h, w = args[:5]
         n = x.numel()
@@ -470,7 +477,8 @@ def _hook_entries(timer):
 
     from kanforge_amd.export.lut import LUTLayer
 
-    names = ("_raw", None), ("_edge_raw", "edge"), ("_features_raw", "features"), ("_rational_param_grad", "rational_param_grad")
+    names = (("_raw", None), ("_edge_raw", "edge"), ("_features_raw", "features"),
+             ("_rational_param_grad", "rational_param_grad"), ("_rational_bwd_raw", "rational_bwd"))
     orig = {n: getattr(kmod, n) for n, _ in names}
     for n, lab in names:
         setattr(kmod, n, timer.wrap(orig[n], lab))

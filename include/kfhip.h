@@ -209,7 +209,7 @@ int kf_rational_bwd(const kf_basis *basis, int dtype, int64_t batch, int64_t n_i
 
 /*
  * out[n] = sum_b g[b, n] for g (rows, n), accumulated in float32, out (n) in dtype: the bias
- * gradient of the layer's bias add (kanforge/torch/layers.py:191, where torch autograd sums).
+ * gradient of the layer's bias add (kanforge/torch/layers.py:189-190, where torch autograd sums).
  * Deterministic (slabs of rows summed in order). Workspace of
  * kf_column_sums_workspace_bytes(rows, n) bytes.
  */
@@ -220,7 +220,7 @@ int kf_column_sums(int dtype, int64_t rows, int64_t n, const void *g, void *out,
 /*
  * Second-order Taylor terms of the SiLU base branch, for the forward-mode Laplacian of a KAN
  * chain (what reverse-over-reverse autograd computes through kanforge/torch/science.py:25-46 and
- * the base branch of kanforge/torch/layers.py:185-191): for h (batch, n), hp (D, batch, n) and S
+ * the base branch of kanforge/torch/layers.py:183-184): for h (batch, n), hp (D, batch, n) and S
  * (batch, n) or NULL, writes sq = sum_d hp_d^2 (batch, n) and the stacked GEMM operand
  * A ((D + 2) batch, n) = [silu(h); silu'(h) hp_d for each d; silu''(h) sq + silu'(h) S].
  */

@@ -1,5 +1,5 @@
 // Column sums out[n] = sum_b g[b, n]: the bias gradient of y + bias (what autograd computes for
-// the bias add of kanforge/torch/layers.py:191). Slabs of rows are summed per run of 8 columns
+// the bias add of kanforge/torch/layers.py:189-190). Slabs of rows are summed per run of 8 columns
 // into float32 partials (16-byte row loads, 8 row lanes per workgroup), then the slabs
 // (deterministic: fixed lane and slab order).
 #include <hip/hip_runtime.h>

@@ -1,6 +1,6 @@
 // Second-order Taylor terms of the SiLU base branch for the forward-mode Laplacian of a KAN chain
 // (what reverse-over-reverse autograd computes through kanforge/torch/science.py:25-46 and the
-// base branch of kanforge/torch/layers.py:185-191). For a layer input h (B, n) with first
+// base branch of kanforge/torch/layers.py:183-184). For a layer input h (B, n) with first
 // derivatives hp (D, B, n) along the D input dimensions and second-derivative sum S (B, n):
 //   sq            = sum_d hp_d^2
 //   A[0:B]        = silu(h)

@@ -316,6 +316,12 @@ def op_rational_bwd(
     sum h w phi^(m)."""
     pl = plan_of(plan)
     st = _state(None, None, None, num, den, x.shape[1])
+    p1, dnum, dden = _rational_bwd_raw(pl, m, st, x, g, c, w)
+    return p1, dnum.to(num.dtype), dden.to(den.dtype)
+
+
+def _rational_bwd_raw(pl: KernelPlan, m: int, st: BasisState, x, g, c, w):
+    """kf_rational_bwd: (P_{m+1}(x, g, c), float32 d/dnum, d/dden of sum h w phi^(m))."""
     _require_device(x)
     lib = _lib.load()
     desc, keep = _desc(pl, m, st)
@@ -335,7 +341,7 @@ def op_rational_bwd(
         )
     _lib.check(rc, "kf_rational_bwd")
     del keep
-    return p1, dnum.to(num.dtype), dden.to(den.dtype)
+    return p1, dnum, dden
 
 
 @torch.library.custom_op("kf::rational_param_grad", mutates_args=())
