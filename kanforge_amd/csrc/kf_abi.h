@@ -510,7 +510,7 @@ int launch_bspline_t(const KBasis& kb, int64_t batch, int64_t n_in, int64_t BP, 
                      const void* w, void* phit, int rows_ij, hipStream_t s) {
   constexpr int RUN = 128, BT = RUN / (int)sizeof(T);
   const size_t lds = (size_t)kb.K * 32 * (RUN + 16) + (size_t)32 * (2 * kb.n_knots + 2 * KD) * 4;
-  auto kern = bspline_t_kernel<T, KD, RUN>;
+  auto kern = KD == 3 && kb.knots_uniform && kb.n_knots >= 4 ? bspline_t_kernel<T, KD, RUN, true> : bspline_t_kernel<T, KD, RUN>;
   if (!reserve_lds((const void*)kern, lds)) return fail(KF_ELAUNCH, "features: cannot reserve %zu bytes of LDS", lds);
   dim3 grid((unsigned)(INP / 32), (unsigned)((BP + BT - 1) / BT));
   hipLaunchKernelGGL(kern, grid, dim3(kThreads), lds, s, kb, (int)batch, (int)n_in, (int)BP, (int)INP, (const T*)x,

@@ -80,10 +80,11 @@ int run_F_dma(const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out, cons
     const size_t rpb = ((size_t)32 * kb.K * sizeof(T) + 15) / 16 * 16 + 16;
     const size_t plds = 64 * rpb + (size_t)32 * (2 * kb.n_knots + 2 * kb.spline_k) * 4;
     dim3 pg((unsigned)((n_in + 31) / 32), (unsigned)((batch + 63) / 64));
+    const bool even = kb.knots_uniform && kb.n_knots >= 4;  // cubic even knots: the common case
     auto kern = kb.spline_k == 0   ? phi_block_kernel<T, 0>
                 : kb.spline_k == 1 ? phi_block_kernel<T, 1>
                 : kb.spline_k == 2 ? phi_block_kernel<T, 2>
-                : kb.spline_k == 3 ? phi_block_kernel<T, 3>
+                : kb.spline_k == 3 ? (even ? phi_block_kernel<T, 3, true> : phi_block_kernel<T, 3>)
                 : kb.spline_k == 4 ? phi_block_kernel<T, 4>
                                    : phi_block_kernel<T, 5>;
     if (!reserve_lds((const void*)kern, plds)) return fail(KF_ELAUNCH, "F: cannot reserve %zu bytes of LDS", plds);

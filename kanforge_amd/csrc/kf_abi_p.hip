@@ -62,10 +62,13 @@ template <int KIND, int NF, int TN, int RB>
 int launch_p8(const WsP& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, const void* x, const void* g,
               int gstride, const void* cfmt, void* p) {
   constexpr int TI = 128 * TN / NF, RPASS = TN == 2 ? 128 : 64;
-  const size_t knots = KIND == KF_KIND_BSPLINE ? (size_t)TI * (2 * kb.n_knots + 2 * kb.spline_k) * 4 : 0;
+  // B-splines: the tile's knot rows and (t_0, 1/h) per input after the sums
+  const size_t knots = KIND == KF_KIND_BSPLINE ? (size_t)TI * (2 * kb.n_knots + 2 * kb.spline_k + 2) * 4 : 0;
   const size_t lds_ops = (size_t)2 * (256 + NF * TI) * RB, lds_epi = (size_t)NF * RPASS * (TI + 1) * 4 + knots;
   const size_t lds = lds_ops > lds_epi ? lds_ops : lds_epi;
-  auto kern = p8_kernel<KIND, NF, TN, RB>;
+  // cubic B-splines on even knots (the common case): the support without the general-knot path
+  const bool even = KIND == KF_KIND_BSPLINE && kb.knots_uniform && kb.n_knots >= 4;
+  auto kern = even ? p8_kernel<KIND, NF, TN, RB, 3, true> : p8_kernel<KIND, NF, TN, RB>;
   if (L.INP % TI || L.OUTP % (RB / 2)) return fail(KF_EINVAL, "P: workspace layout not aligned");
   if (!reserve_lds((const void*)kern, lds))
     return fail(KF_ELAUNCH, "P: cannot reserve %zu bytes of LDS", lds);

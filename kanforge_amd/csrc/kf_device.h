@@ -9,6 +9,8 @@
 //   d^m silu                                            kanforge/_calculus.py:90-96
 #pragma once
 
+#include <type_traits>
+
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -157,60 +159,77 @@ __device__ __forceinline__ int bspline_interval(float x, const float* kc, int n_
 // kc: the input's n_knots comparison knots (each float64 knot rounded up to float32, so x >= kc[r]
 // is exactly x >= t_r); kp0: its n_knots + 2 KD padded knots (global memory, or a copy in LDS);
 // t0, ih: (t_0, 1/h) when the input's knots are evenly spaced by h, ih == 0 otherwise.
-template <int KD>
-__device__ inline int bspline_support(float x, float w, const float* kc, const float* kp0, float t0, float ih,
-                                      const KBasis& b, int& base, float (&N)[KD + 1]) {
-  const int nk = b.n_knots, m = b.order;
-  if (!__builtin_isfinite(x)) return 2;
-  if (m > KD || x < kc[0] || x >= kc[nk - 1]) return 0;
-  int j;
-  if (ih != 0.f) {
-    // even knots: the affine estimate, moved until kc[j] <= x < kc[j + 1] (it is off by at most
-    // one; the search below is the fallback that never runs for even knots)
-    j = (int)floorf((x - t0) * ih);
-    j = j < 0 ? 0 : (j > nk - 2 ? nk - 2 : j);
-#pragma unroll
-    for (int it = 0; it < 2; ++it) {
-      if (x < kc[j]) --j;
-      else if (x >= kc[j + 1]) ++j;
-    }
-    if (!(kc[j] <= x && x < kc[j + 1])) j = bspline_interval(x, kc, nk);
+// The derivative order M is a template argument here (bspline_support below dispatches on m), so
+// the recurrence's Cox-de Boor / derivative choice is made at compile time.
+// EVEN: the caller guarantees even knots (ih != 0) and nk >= 4, and only that path is compiled.
+template <int KD, int M, bool EVEN = false>
+__device__ inline int bspline_support_m(float x, float w, const float* kc, const float* kp0, float t0, float ih,
+                                        int nk, int& base, float (&N)[KD + 1]) {
+  constexpr int deg = KD - M;
+  const bool fin = __builtin_isfinite(x);
+  if constexpr (M > KD) {
+    return fin ? 0 : 2;  // every derivative of order > KD is zero
   } else {
-    j = bspline_interval(x, kc, nk);
-  }
-  // Cox-de Boor to degree KD - m, then m derivative steps; N[r] = B_{q, j-q+r} after step q
+    if (EVEN || (ih != 0.f && nk >= 4)) {
+      // even knots, without branches on x: the affine estimate e is off by at most one, so with e
+      // clamped to [1, nk - 3] the four knots around it decide j in one round of independent
+      // reads, j = e - 1 + [x >= kc[e]] + [x >= kc[e + 1]] whenever kc[e - 1] <= x < kc[e + 2]
+      // (the search is the fallback that never runs for even knots). x outside the knots or not
+      // finite runs the same instructions on clamped indices; the status discards the values.
+      // (bitwise & and |: no short-circuit branches around the reads)
+      const float kfirst = kc[0], klast = kc[nk - 1];
+      const bool inr = fin & (x >= kfirst) & (x < klast);
+      const float ef = fminf(fmaxf(floorf((x - t0) * ih), 1.f), (float)(nk - 3));
+      const int e = (int)ef;
+      const float k0 = kc[e - 1], k1 = kc[e], k2 = kc[e + 1], k3 = kc[e + 2];
+      int j = e - 1 + (x >= k1 ? 1 : 0) + (x >= k2 ? 1 : 0);
+      if (inr & ((x < k0) | (x >= k3))) j = bspline_interval(x, kc, nk);
+      // every knot difference is a whole number of steps: with u = (x - t_j) / h and s = j-q+r,
+      // (x - t_s) / (t_{s+q} - t_s) = (u + q - r) / q, (t_{s+q+1} - x) / (t_{s+q+1} - t_{s+1}) = (r + 1 - u) / q,
+      // and a derivative step is (left - right) / h; Cox-de Boor to degree KD - M, then M
+      // derivative steps, N[r] = B_{q, j-q+r} after step q. B_{q-1,j-q} and B_{q-1,j+1} are zero
+      // (and the factors multiplying them finite), so the end terms r = 0 and r = q have one product.
+      const float u = (x - kp0[j + KD]) * ih;
 #pragma unroll
-  for (int r = 0; r <= KD; ++r) N[r] = r == 0 ? 1.f : 0.f;
-  const int deg = KD - m;
-  if (ih != 0.f) {
-    // every knot difference is a whole number of steps: with u = (x - t_j) / h and s = j-q+r,
-    // (x - t_s) / (t_{s+q} - t_s) = (u + q - r) / q, (t_{s+q+1} - x) / (t_{s+q+1} - t_{s+1}) = (r + 1 - u) / q,
-    // and a derivative step is (left - right) / h
-    const float u = (x - kp0[j + KD]) * ih;
+      for (int r = 0; r <= KD; ++r) N[r] = r == 0 ? 1.f : 0.f;
 #pragma unroll
-    for (int q = 1; q <= KD; ++q) {
-      float nn[KD + 1];
-      const float iq = 1.f / (float)q;
+      for (int q = 1; q <= KD; ++q) {
+        float nn[KD + 1];
+        const float iq = 1.f / (float)q;
 #pragma unroll
-      for (int r = 0; r <= KD; ++r) {
-        const float left = (r >= 1 && r <= q) ? N[r - 1] : 0.f;
-        const float right = (r <= q - 1) ? N[r] : 0.f;
-        if (r > q)
-          nn[r] = 0.f;
-        else if (q <= deg)
-          nn[r] = ((u + (float)(q - r)) * left + ((float)(r + 1) - u) * right) * iq;
-        else
-          nn[r] = (left - right) * ih;
+        for (int r = 0; r <= KD; ++r) {
+          if (r > q) nn[r] = 0.f;
+          else if (q <= deg) {
+            if (r == 0) nn[r] = (1.f - u) * N[0] * iq;
+            else if (r == q) nn[r] = u * N[r - 1] * iq;
+            else nn[r] = ((u + (float)(q - r)) * N[r - 1] + ((float)(r + 1) - u) * N[r]) * iq;
+          } else {
+            if (r == 0) nn[r] = -N[0] * ih;
+            else if (r == q) nn[r] = N[r - 1] * ih;
+            else nn[r] = (N[r - 1] - N[r]) * ih;
+          }
+        }
+#pragma unroll
+        for (int r = 0; r <= KD; ++r) N[r] = nn[r];
       }
 #pragma unroll
-      for (int r = 0; r <= KD; ++r) N[r] = nn[r];
+      for (int r = 0; r <= KD; ++r) N[r] *= w;
+      base = j - KD;
+      return inr ? 1 : (fin ? 0 : 2);
     }
-  } else {
-    // L[r] = t_{j-KD+r}, r = 0..2KD+1 (kp[r'] = t_{r'-KD}, so t_{j-KD+r} = kp[j+r])
+    if constexpr (EVEN) return 0;  // not reached
+    if (!fin) return 2;
+    if (x < kc[0] || x >= kc[nk - 1]) return 0;
+    const int j = bspline_interval(x, kc, nk);
+    // general knots: L[r] = t_{j-KD+r}, r = 0..2KD+1 (kp[r'] = t_{r'-KD}, so t_{j-KD+r} = kp[j+r]);
+    // the zero end terms are kept: with repeated knots their 0 / 0 gives NaN, as the dense
+    // recurrence does
     const float* kp = kp0 + j;
     float L[2 * KD + 2];
 #pragma unroll
     for (int r = 0; r < 2 * KD + 2; ++r) L[r] = kp[r];
+#pragma unroll
+    for (int r = 0; r <= KD; ++r) N[r] = r == 0 ? 1.f : 0.f;
 #pragma unroll
     for (int q = 1; q <= KD; ++q) {
       float nn[KD + 1];
@@ -233,11 +252,41 @@ __device__ inline int bspline_support(float x, float w, const float* kc, const f
 #pragma unroll
       for (int r = 0; r <= KD; ++r) N[r] = nn[r];
     }
-  }
 #pragma unroll
-  for (int r = 0; r <= KD; ++r) N[r] *= w;
-  base = j - KD;
-  return 1;
+    for (int r = 0; r <= KD; ++r) N[r] *= w;
+    base = j - KD;
+    return 1;
+  }
+}
+
+// f(std::integral_constant<int, M>) for the derivative order m: M = m for m <= KD, KD + 1 above
+// (every feature zero). Hot kernels take the order out of their element loops with it.
+template <int KD, int M = 0, typename F>
+__device__ __forceinline__ void with_spline_order(int m, F&& f) {
+  if constexpr (M > KD) {
+    f(std::integral_constant<int, KD + 1>{});
+  } else {
+    if (m == M) f(std::integral_constant<int, M>{});
+    else with_spline_order<KD, M + 1>(m, static_cast<F&&>(f));
+  }
+}
+
+template <int KD, int M = 0>
+__device__ __forceinline__ int bspline_support_dispatch(int m, float x, float w, const float* kc, const float* kp0,
+                                                        float t0, float ih, int nk, int& base, float (&N)[KD + 1]) {
+  if constexpr (M > KD) {
+    return __builtin_isfinite(x) ? 0 : 2;  // m > KD: every derivative is zero
+  } else {
+    if (m == M) return bspline_support_m<KD, M>(x, w, kc, kp0, t0, ih, nk, base, N);
+    return bspline_support_dispatch<KD, M + 1>(m, x, w, kc, kp0, t0, ih, nk, base, N);
+  }
+}
+
+// bspline_support_m for the basis' derivative order b.order (a launch-uniform branch)
+template <int KD>
+__device__ __forceinline__ int bspline_support(float x, float w, const float* kc, const float* kp0, float t0, float ih,
+                                               const KBasis& b, int& base, float (&N)[KD + 1]) {
+  return bspline_support_dispatch<KD>(b.order, x, w, kc, kp0, t0, ih, b.n_knots, base, N);
 }
 
 // (t_0, 1/h) of input i, or ih = 0 when the knots are not evenly spaced
@@ -392,14 +441,55 @@ __device__ inline void bspline_dispatch_rows(float x, float w, const float* kc, 
 // Copies the knot rows of inputs i0 .. i0 + n - 1 (zeros past IN) into LDS:
 // kc[il * nk + r], kp[il * (nk + 2k) + r]. Every thread of the block calls it;
 // the caller synchronises before reading.
-__device__ inline void stage_knot_rows(const KBasis& b, int i0, int n, int IN, float* kc, float* kp) {
-  // the rows of consecutive inputs are one contiguous run in each table
+// Knot rows of inputs i0 .. i0 + n - 1 into LDS: kc (n x n_knots comparison knots) and kp
+// (n x (n_knots + 2 k) padded knots); rows past IN are zeros. The rows of consecutive inputs are
+// one contiguous run in each table, and both tables are one index range e < n_kc + n_kp here.
+// knot_rows_load issues the first U x blockDim elements' loads (addresses clamped into the
+// existing rows, so no branches: they are in flight together, and the caller can put more loads
+// behind them); knot_rows_store writes them and stages what remains.
+struct KnotRange {
+  int n_kc, n_kp, kc_last, kp_last;  // last: index of the last existing element (-1: none)
+  const float *kcg, *kpg;
+};
+__device__ __forceinline__ KnotRange knot_range(const KBasis& b, int i0, int n, int IN) {
   const int nk = b.n_knots, np = nk + 2 * b.spline_k;
-  const long kc_end = (long)IN * nk - (long)i0 * nk, kp_end = (long)IN * np - (long)i0 * np;
-  const float* kcg = b.knots_cmp + (size_t)i0 * nk;
-  const float* kpg = b.knots + (size_t)i0 * np;
-  for (int e = threadIdx.x; e < n * nk; e += blockDim.x) kc[e] = e < kc_end ? kcg[e] : 0.f;
-  for (int e = threadIdx.x; e < n * np; e += blockDim.x) kp[e] = e < kp_end ? kpg[e] : 0.f;
+  const int rows = IN - i0 < n ? (IN - i0 < 0 ? 0 : IN - i0) : n;
+  return {n * nk, n * np, rows * nk - 1, rows * np - 1, b.knots_cmp + (size_t)i0 * nk, b.knots + (size_t)i0 * np};
+}
+template <int U>
+__device__ __forceinline__ void knot_rows_load(const KnotRange& r, int e0, float (&v)[U]) {
+  if (r.kc_last < 0) return;  // a tile past the last input (padded widths): zeros only
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int e = e0 + u * blockDim.x, ep = e - r.n_kc;
+    const float* src = e < r.n_kc ? r.kcg + (e < r.kc_last ? e : r.kc_last)
+                                  : r.kpg + (ep < 0 ? 0 : (ep < r.kp_last ? ep : r.kp_last));
+    v[u] = *src;
+  }
+}
+template <int U>
+__device__ __forceinline__ void knot_rows_put(const KnotRange& r, int e0, const float (&v)[U], float* kc, float* kp) {
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int e = e0 + u * blockDim.x, ep = e - r.n_kc;
+    if (e < r.n_kc) kc[e] = e <= r.kc_last ? v[u] : 0.f;
+    else if (ep < r.n_kp) kp[ep] = ep <= r.kp_last ? v[u] : 0.f;
+  }
+}
+template <int U>
+__device__ inline void knot_rows_store(const KnotRange& r, const float (&v)[U], float* kc, float* kp) {
+  knot_rows_put<U>(r, threadIdx.x, v, kc, kp);
+  for (int e0 = threadIdx.x + U * blockDim.x; e0 < r.n_kc + r.n_kp; e0 += U * blockDim.x) {
+    float w[U];
+    knot_rows_load<U>(r, e0, w);
+    knot_rows_put<U>(r, e0, w, kc, kp);
+  }
+}
+__device__ inline void stage_knot_rows(const KBasis& b, int i0, int n, int IN, float* kc, float* kp) {
+  const KnotRange r = knot_range(b, i0, n, IN);
+  float v[4];
+  knot_rows_load<4>(r, threadIdx.x, v);
+  knot_rows_store<4>(r, v, kc, kp);
 }
 __device__ __forceinline__ int knot_lds_floats(const KBasis& b, int n) {
   return n * (2 * b.n_knots + 2 * b.spline_k);

@@ -1085,8 +1085,9 @@ __global__ __launch_bounds__(kThreads) void features_t_kernel(KBasis bs, int B, 
 // B-spline features of degree KD in the reference's (B, in K) layout, phi[b][i K + k], for blocks of
 // 32 inputs x 64 rows: the block's knot rows are staged in LDS once, every thread evaluates 8
 // elements' supports (KD + 1 values) into zeroed LDS copies of the 64 row segments, which leave as
-// 16-byte chunks. (IN K) % 8 == 0 and phi 16-byte aligned; K <= 16.
-template <typename T, int KD>
+// 16-byte chunks. (IN K) % 8 == 0 and phi 16-byte aligned; K <= 16. EVEN: every input's knots are
+// evenly spaced (knots_uniform given) and n_knots >= 4.
+template <typename T, int KD, bool EVEN = false>
 __global__ __launch_bounds__(kThreads) void phi_block_kernel(KBasis bs, int B, int IN, const T* __restrict__ x,
                                                              T* __restrict__ phi) {
   constexpr int ROWS = 64, PER = 32 * ROWS / kThreads, VW = 16 / (int)sizeof(T);
@@ -1095,29 +1096,42 @@ __global__ __launch_bounds__(kThreads) void phi_block_kernel(KBasis bs, int B, i
   const int rpb = (32 * K * (int)sizeof(T) + 15) / 16 * 16 + 16;  // row pitch of the segment copies
   float* kcs = reinterpret_cast<float*>(smem + (size_t)ROWS * rpb);
   float* kps = kcs + 32 * nk;
-  stage_knot_rows(bs, i0, 32, IN, kcs, kps);
-  for (int c = threadIdx.x; c < ROWS * rpb / 16; c += kThreads) *reinterpret_cast<u32x4*>(smem + 16 * c) = u32x4{0, 0, 0, 0};
-  __syncthreads();
   const int il = threadIdx.x % 32, i = i0 + il;
-  float t0 = 0.f, ih = 0.f;
-  if (i < IN) bspline_affine(bs, i, t0, ih);
+  // the knot rows, the thread's x values and its knot spacing are loaded together (addresses
+  // clamped into the arrays: loads without branches, all in flight at once)
+  const KnotRange kr = knot_range(bs, i0, 32, IN);
+  float kv[8];
+  knot_rows_load<8>(kr, threadIdx.x, kv);
+  const int ic = i < IN ? i : IN - 1;
+  float xv[PER];
 #pragma unroll
   for (int u = 0; u < PER; ++u) {
-    const int bl = threadIdx.x / 32 + u * (kThreads / 32), b = b0 + bl;
-    if (b >= B || i >= IN) continue;
-    const float xv = to_f32(x[(size_t)b * IN + i]);
-    T* seg = reinterpret_cast<T*>(smem + (size_t)bl * rpb) + il * K;
-    float N[KD + 1];
-    int base = 0;
-    const int st = bspline_support<KD>(xv, 1.f, kcs + il * nk, kps + il * (nk + 2 * KD), t0, ih, bs, base, N);
-    if (st == 1) {
+    const int b = b0 + threadIdx.x / 32 + u * (kThreads / 32);
+    xv[u] = to_f32(x[(size_t)(b < B ? b : B - 1) * IN + ic]);
+  }
+  float t0, ih;
+  bspline_affine(bs, ic, t0, ih);
+  knot_rows_store<8>(kr, kv, kcs, kps);
+  for (int c = threadIdx.x; c < ROWS * rpb / 16; c += kThreads) *reinterpret_cast<u32x4*>(smem + 16 * c) = u32x4{0, 0, 0, 0};
+  __syncthreads();
+  // the derivative order is taken out of the element loop (one fully unrolled body per order)
+  with_spline_order<KD>(bs.order, [&](auto order) {
+    constexpr int M = decltype(order)::value;
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int bl = threadIdx.x / 32 + u * (kThreads / 32), b = b0 + bl;
+      const bool here = b < B && i < IN;
+      T* seg = reinterpret_cast<T*>(smem + (size_t)bl * rpb) + il * K;
+      float N[KD + 1];
+      int base = 0;
+      const int st = bspline_support_m<KD, M, EVEN>(xv[u], 1.f, kcs + il * nk, kps + il * (nk + 2 * KD), t0, ih, nk, base, N);
 #pragma unroll
       for (int r = 0; r <= KD; ++r)
-        if (base + r >= 0 && base + r < K) seg[base + r] = from_f32<T>(N[r]);
-    } else if (st == 2) {
-      for (int j = 0; j < K; ++j) seg[j] = from_f32<T>(__builtin_nanf(""));
+        if (here && st == 1 && base + r >= 0 && base + r < K) seg[base + r] = from_f32<T>(N[r]);
+      if (here && st == 2)
+        for (int j = 0; j < K; ++j) seg[j] = from_f32<T>(__builtin_nanf(""));
     }
-  }
+  });
   __syncthreads();
   const int n = (IN - i0 < 32 ? IN - i0 : 32) * K;  // elements of one row's segment
   const int nv = n / VW, tail = n - nv * VW;
@@ -1134,7 +1148,8 @@ __global__ __launch_bounds__(kThreads) void phi_block_kernel(KBasis bs, int B, i
 // B-spline features of degree KD (times w), transposed: phiT rows j INP + i (feature-major) or
 // i K + j (input-major, rows_ij), batch along the row, for blocks of 32 inputs x RUN bytes of
 // rows; knot rows staged in LDS, supports written into zeroed LDS rows, rows out in 16-byte chunks.
-template <typename T, int KD, int RUN>
+// EVEN as for phi_block_kernel.
+template <typename T, int KD, int RUN, bool EVEN = false>
 __global__ __launch_bounds__(kThreads) void bspline_t_kernel(KBasis bs, int B, int IN, int BP, int INP,
                                                              const T* __restrict__ x, const T* __restrict__ w,
                                                              T* __restrict__ phit, int rows_ij) {
@@ -1145,29 +1160,49 @@ __global__ __launch_bounds__(kThreads) void bspline_t_kernel(KBasis bs, int B, i
   const int i0 = blockIdx.x * 32, b0 = blockIdx.y * BT;
   float* kcs = reinterpret_cast<float*>(smem + (size_t)K * 32 * RSB);
   float* kps = kcs + 32 * nk;
-  stage_knot_rows(bs, i0, 32, IN, kcs, kps);
-  for (int c = threadIdx.x; c < K * 32 * RSB / 16; c += kThreads) *reinterpret_cast<u32x4*>(smem + 16 * c) = u32x4{0, 0, 0, 0};
-  __syncthreads();
   const int il = threadIdx.x % 32, i = i0 + il;
-  float t0 = 0.f, ih = 0.f;
-  if (i < IN) bspline_affine(bs, i, t0, ih);
+  // the knot rows, the thread's x (and w) values and its knot spacing are loaded together
+  // (addresses clamped into the arrays: loads without branches, all in flight at once)
+  const KnotRange kr = knot_range(bs, i0, 32, IN);
+  float kv[8];
+  knot_rows_load<8>(kr, threadIdx.x, kv);
+  const int ic = i < IN ? i : IN - 1;
+  // without w the w loads read x again (cache hits) and the values are replaced by 1: no branch
+  // around loads, so no load waits inside one
+  const T* wsrc = w ? w : x;
+  float xv[PER], wv[PER];
 #pragma unroll
   for (int u = 0; u < PER; ++u) {
-    const int bl = threadIdx.x / 32 + u * (kThreads / 32), b = b0 + bl;
-    if (b >= B || i >= IN) continue;
-    const size_t off = (size_t)b * IN + i;
-    const float xv = to_f32(x[off]), wv = w ? to_f32(w[off]) : 1.f;
-    float N[KD + 1];
-    int base = 0;
-    const int st = bspline_support<KD>(xv, wv, kcs + il * nk, kps + il * (nk + 2 * KD), t0, ih, bs, base, N);
-    if (st == 1) {
+    const int b = b0 + threadIdx.x / 32 + u * (kThreads / 32);
+    const size_t off = (size_t)(b < B ? b : B - 1) * IN + ic;
+    xv[u] = to_f32(x[off]);
+    wv[u] = to_f32(wsrc[off]);
+  }
+#pragma unroll
+  for (int u = 0; u < PER; ++u) wv[u] = w ? wv[u] : 1.f;
+  float t0, ih;
+  bspline_affine(bs, ic, t0, ih);
+  knot_rows_store<8>(kr, kv, kcs, kps);
+  for (int c = threadIdx.x; c < K * 32 * RSB / 16; c += kThreads) *reinterpret_cast<u32x4*>(smem + 16 * c) = u32x4{0, 0, 0, 0};
+  __syncthreads();
+  // the derivative order is taken out of the element loop (one fully unrolled body per order)
+  with_spline_order<KD>(bs.order, [&](auto order) {
+    constexpr int M = decltype(order)::value;
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int bl = threadIdx.x / 32 + u * (kThreads / 32), b = b0 + bl;
+      const bool here = b < B && i < IN;
+      float N[KD + 1];
+      int base = 0;
+      const int st = bspline_support_m<KD, M, EVEN>(xv[u], wv[u], kcs + il * nk, kps + il * (nk + 2 * KD), t0, ih, nk, base, N);
 #pragma unroll
       for (int r = 0; r <= KD; ++r)
-        if (base + r >= 0 && base + r < K) reinterpret_cast<T*>(smem + (size_t)((base + r) * 32 + il) * RSB)[bl] = from_f32<T>(N[r]);
-    } else if (st == 2) {
-      for (int j = 0; j < K; ++j) reinterpret_cast<T*>(smem + (size_t)(j * 32 + il) * RSB)[bl] = from_f32<T>(__builtin_nanf(""));
+        if (here && st == 1 && base + r >= 0 && base + r < K)
+          reinterpret_cast<T*>(smem + (size_t)((base + r) * 32 + il) * RSB)[bl] = from_f32<T>(N[r]);
+      if (here && st == 2)
+        for (int j = 0; j < K; ++j) reinterpret_cast<T*>(smem + (size_t)(j * 32 + il) * RSB)[bl] = from_f32<T>(__builtin_nanf(""));
     }
-  }
+  });
   __syncthreads();
   const int total = K * 32 * CPR;
   for (int c = threadIdx.x; c < total; c += kThreads) {
@@ -1819,7 +1854,7 @@ __global__ __launch_bounds__(256) void p_dma_kernel(KBasis bs, int B, int IN, in
 // passes of RPASS rows: the feature sums H_j go to LDS and every thread forms
 // p[b, i] = sum_j f_j(x[b, i]) H_j[b, i] for (row, input) pairs, the features computed once per
 // pair.
-template <int KIND, int NF, int TN, int RB, int KD = 3>
+template <int KIND, int NF, int TN, int RB, int KD = 3, bool EVEN = false>
 __global__ __launch_bounds__(512) void p8_kernel(KBasis bs, int B, int IN, int INP, int OUTP,
                                                  const bf16* __restrict__ x, const bf16* __restrict__ g, int gstride,
                                                  const bf16* __restrict__ cfmt, bf16* __restrict__ p) {
@@ -1906,69 +1941,132 @@ __global__ __launch_bounds__(512) void p8_kernel(KBasis bs, int B, int IN, int I
   // passed this barrier)
   float* kcs = red + NF * RPASS * RP;
   float* kps = kcs + TI * bs.n_knots;
+  // Epilogue work item e = (row e / (TI / 2), inputs 2 (e % (TI / 2)) and + 1): thread tid takes
+  // e = tid + 512 k, so with 512 a multiple of TI / 2 its two inputs are the same in every pass,
+  // and each pass's x values (EPT items) are loaded before the pass's sums go to LDS, so that
+  // their latency passes behind the stores and the barrier. The inputs' (t_0, 1/h) sit in LDS
+  // after the knot rows.
+  constexpr int EPT = RPASS * TI / 2 / 512;
+  static_assert(EPT * 512 == RPASS * TI / 2, "whole epilogue rounds");
+  constexpr bool FIXED_INPUTS = KIND == KF_KIND_BSPLINE && 512 % (TI / 2) == 0;
+  const int il_t = 2 * (tid % (TI / 2)), i_t = i0 + il_t;
+  float* kus = kps + TI * (bs.n_knots + 2 * bs.spline_k);  // [TI][2]
   if constexpr (KIND == KF_KIND_BSPLINE) {
     __syncthreads();
     stage_knot_rows(bs, i0, TI, IN, kcs, kps);
-  }
-#pragma unroll
-  for (int ps = 0; ps < BM / RPASS; ++ps) {
-    __syncthreads();
-#pragma unroll
-    for (int a = 0; a < 4; ++a) {
-      if ((wm * 128 + a * 32) / RPASS != ps) continue;
-      const int rbase = (wm * 128 + a * 32) % RPASS;
-#pragma unroll
-      for (int t = 0; t < TN; ++t) {
-        const int col = (TN * wn + t) * 32 + l32, f = col / TI, il = col % TI;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) red[(f * RPASS + rbase + acc_row(r, lane)) * RP + il] = acc[a][t][r];
-      }
+    if (tid < TI) {
+      float t0, ih;
+      bspline_affine(bs, i0 + tid < IN ? i0 + tid : IN - 1, t0, ih);
+      kus[2 * tid] = t0;
+      kus[2 * tid + 1] = ih;
     }
-    __syncthreads();
-    // two adjacent inputs per thread: one 4-byte store when both exist, IN is even and p is
-    // 4-byte aligned
-    for (int e = tid; e < RPASS * TI / 2; e += 512) {
-      const int row = e / (TI / 2), il = 2 * (e % (TI / 2));
-      const int b = b0 + ps * RPASS + row, i = i0 + il;
-      if (b >= B || i >= IN) continue;
-      float v[2] = {0.f, 0.f};
+  }
+  // the passes, once per derivative order for B-splines (the order is taken out of the element
+  // loops: one unrolled body per order)
+  auto epilogue = [&](auto order) {
+    constexpr int M = decltype(order)::value;
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        if (i + u < IN) {
-          const float xv = to_f32(x[(size_t)b * IN + i + u]);
-          if constexpr (KIND == KF_KIND_BSPLINE) {
-            // B-splines of degree KD: only the support's sums (KD + 1 LDS reads) enter
-            const int nk = bs.n_knots;
-            float t0, ih, N[KD + 1];
-            int base = 0;
-            bspline_affine(bs, i + u, t0, ih);
-            const int ilu = il + u;
-            const int st = bspline_support<KD>(xv, 1.f, kcs + ilu * nk, kps + ilu * (nk + 2 * KD), t0, ih, bs, base, N);
-            if (st == 1) {
+    for (int ps = 0; ps < BM / RPASS; ++ps) {
+      uint32_t xq[EPT];  // bf16 pairs x[b, i_t], x[b, i_t + 1] of this pass's items
+      if constexpr (FIXED_INPUTS) {
+        const unsigned short* xs = reinterpret_cast<const unsigned short*>(x);
 #pragma unroll
-              for (int r = 0; r <= KD; ++r)
-                if (base + r >= 0 && base + r < bs.K) v[u] = fmaf(red[((base + r) * RPASS + row) * RP + il + u], N[r], v[u]);
-            } else if (st == 2) {
-              v[u] = __builtin_nanf("");
-            }
-          } else {
-            float f[NF];
-            kind_features<KIND, NF>(xv, 1.f, i + u, bs, f);
-#pragma unroll
-            for (int q = 0; q < NF; ++q) v[u] = fmaf(red[(q * RPASS + row) * RP + il + u], f[q], v[u]);
-          }
+        for (int k = 0; k < EPT; ++k) {  // addresses clamped into x: loads without branches
+          const int b = b0 + ps * RPASS + (tid + 512 * k) / (TI / 2);
+          const size_t o = (size_t)(b < B ? b : B - 1) * IN;
+          const uint32_t lo = xs[o + (i_t < IN ? i_t : IN - 1)], hi = xs[o + (i_t + 1 < IN ? i_t + 1 : IN - 1)];
+          xq[k] = lo | hi << 16;
         }
       }
-      bf16* dst = p + (size_t)b * IN + i;
-      if (IN % 2 == 0 && i + 1 < IN && (reinterpret_cast<uintptr_t>(p) & 3) == 0) {
-        const bf16 pr[2] = {from_f32<bf16>(v[0]), from_f32<bf16>(v[1])};
-        *reinterpret_cast<uint32_t*>(dst) = __builtin_bit_cast(uint32_t, pr);
+      __syncthreads();
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        if ((wm * 128 + a * 32) / RPASS != ps) continue;
+        const int rbase = (wm * 128 + a * 32) % RPASS;
+#pragma unroll
+        for (int t = 0; t < TN; ++t) {
+          const int col = (TN * wn + t) * 32 + l32, f = col / TI, il = col % TI;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) red[(f * RPASS + rbase + acc_row(r, lane)) * RP + il] = acc[a][t][r];
+        }
+      }
+      __syncthreads();
+      // two adjacent inputs per thread: one 4-byte store when both exist, IN is even and p is
+      // 4-byte aligned
+      auto store_pair = [&](int b, int i, const float (&v)[2]) {
+        bf16* dst = p + (size_t)b * IN + i;
+        if (IN % 2 == 0 && i + 1 < IN && (reinterpret_cast<uintptr_t>(p) & 3) == 0) {
+          const bf16 pr[2] = {from_f32<bf16>(v[0]), from_f32<bf16>(v[1])};
+          *reinterpret_cast<uint32_t*>(dst) = __builtin_bit_cast(uint32_t, pr);
+        } else {
+          dst[0] = from_f32<bf16>(v[0]);
+          if (i + 1 < IN) dst[1] = from_f32<bf16>(v[1]);
+        }
+      };
+      if constexpr (FIXED_INPUTS) {
+        // B-splines of degree KD: only the support's sums (KD + 1 LDS reads) enter
+        const int nk = bs.n_knots;
+#pragma unroll
+        for (int k = 0; k < EPT; ++k) {
+          const int row = (tid + 512 * k) / (TI / 2);
+          const int b = b0 + ps * RPASS + row;
+          float v[2] = {0.f, 0.f};
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const float xv = __builtin_bit_cast(float, (xq[k] >> (16 * u)) << 16);
+            const int ilu = il_t + u;
+            float N[KD + 1];
+            int base = 0;
+            const int st = bspline_support_m<KD, M, EVEN>(xv, 1.f, kcs + ilu * nk, kps + ilu * (nk + 2 * KD),
+                                                          kus[2 * ilu], kus[2 * ilu + 1], nk, base, N);
+#pragma unroll
+            for (int r = 0; r <= KD; ++r)
+              if (st == 1 && base + r >= 0 && base + r < bs.K)
+                v[u] = fmaf(red[((base + r) * RPASS + row) * RP + ilu], N[r], v[u]);
+            if (st == 2) v[u] = __builtin_nanf("");
+          }
+          if (b < B && i_t < IN) store_pair(b, i_t, v);
+        }
       } else {
-        dst[0] = from_f32<bf16>(v[0]);
-        if (i + 1 < IN) dst[1] = from_f32<bf16>(v[1]);
+        for (int e = tid; e < RPASS * TI / 2; e += 512) {
+          const int row = e / (TI / 2), il = 2 * (e % (TI / 2));
+          const int b = b0 + ps * RPASS + row, i = i0 + il;
+          if (b >= B || i >= IN) continue;
+          float v[2] = {0.f, 0.f};
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            if (i + u >= IN) continue;
+            const float xv = to_f32(x[(size_t)b * IN + i + u]);
+            if constexpr (KIND == KF_KIND_BSPLINE) {
+              const int nk = bs.n_knots;
+              float t0, ih, N[KD + 1];
+              int base = 0;
+              bspline_affine(bs, i + u, t0, ih);
+              const int ilu = il + u;
+              const int st = bspline_support<KD>(xv, 1.f, kcs + ilu * nk, kps + ilu * (nk + 2 * KD), t0, ih, bs, base, N);
+              if (st == 1) {
+#pragma unroll
+                for (int r = 0; r <= KD; ++r)
+                  if (base + r >= 0 && base + r < bs.K) v[u] = fmaf(red[((base + r) * RPASS + row) * RP + ilu], N[r], v[u]);
+              } else if (st == 2) {
+                v[u] = __builtin_nanf("");
+              }
+            } else {
+              float f[NF];
+              kind_features<KIND, NF>(xv, 1.f, i + u, bs, f);
+#pragma unroll
+              for (int q = 0; q < NF; ++q) v[u] = fmaf(red[(q * RPASS + row) * RP + il + u], f[q], v[u]);
+            }
+          }
+          store_pair(b, i, v);
+        }
       }
     }
-  }
+  };
+  if constexpr (FIXED_INPUTS)
+    with_spline_order<KD>(bs.order, epilogue);
+  else
+    epilogue(std::integral_constant<int, 0>{});
 }
 
 // Copy g (B, OUT) into a zero-padded (B, OUTP) buffer: the P kernel copies whole stages.
