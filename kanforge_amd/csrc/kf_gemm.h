@@ -84,6 +84,16 @@ __device__ __forceinline__ u32x4 gload16(const void* p, bool ok) {
   return ok ? *reinterpret_cast<const u32x4*>(p) : z;
 }
 
+// gload16 without a branch: the load always runs, from p when ok and from the valid 16-byte aligned
+// address safe otherwise, and the value is replaced by zeros when !ok. A predicated load compiles
+// to a branch whose body waits for the load, which serialises a thread's loads; these stay in
+// flight together.
+__device__ __forceinline__ u32x4 gload16s(const void* p, bool ok, const void* safe) {
+  const u32x4 v = *reinterpret_cast<const u32x4*>(ok ? p : safe);
+  const u32x4 z = {0u, 0u, 0u, 0u};
+  return ok ? v : z;
+}
+
 __device__ __forceinline__ void gstore16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
 
 }  // namespace kf

@@ -153,28 +153,54 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(int M, int N, int S, int s
 }
 
 // C[m][n] = sum over the splits z (in order) of part[z][m][n] (float32, row pitch N), converted to
-// the output dtype; four consecutive columns per thread.
+// the output dtype; four consecutive columns per thread. With N % 4 == 0 (the partials are 256-byte
+// aligned) every split is one 16-byte load and the loop over z has no branches, so its loads are
+// in flight together; other widths read the four columns with clamped addresses and mask them.
+// VST: C rows take one 8-byte (bf16) or 16-byte (float32) store per thread.
 template <bool OUT_F32>
 __global__ __launch_bounds__(256) void gemm_split_reduce(int M, int N, int nz, const float* __restrict__ part,
-                                                         void* __restrict__ C, long ldc) {
-  const long n4 = (N + 3) / 4, total = (long)M * n4;
+                                                         void* __restrict__ C, long ldc, int vst) {
+  const int n4 = (N + 3) / 4;
+  const long total = (long)M * n4;
   const size_t zs = (size_t)M * N;
   for (long e = blockIdx.x * 256L + threadIdx.x; e < total; e += (long)gridDim.x * 256) {
-    const int m = (int)(e / n4), n = (int)(e % n4) * 4;
+    const int m = (int)(e / n4), n = (int)(e - (long)m * n4) * 4;
+    const float* p = part + (size_t)m * N + n;
     float s[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int z = 0; z < nz; ++z) {
-      const float* p = part + z * zs + (size_t)m * N + n;
+    if (N % 4 == 0) {
+#pragma unroll 4
+      for (int z = 0; z < nz; ++z) {
+        const float4 v = *reinterpret_cast<const float4*>(p + z * zs);
+        s[0] += v.x;
+        s[1] += v.y;
+        s[2] += v.z;
+        s[3] += v.w;
+      }
+    } else {
+      int off[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (n + q < N) s[q] += p[q];
+      for (int q = 0; q < 4; ++q) off[q] = n + q < N ? q : N - 1 - n;
+#pragma unroll 2
+      for (int z = 0; z < nz; ++z)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) s[q] += p[z * zs + off[q]];
     }
+    if (vst && n + 4 <= N) {
+      if (OUT_F32) {
+        *reinterpret_cast<float4*>(reinterpret_cast<float*>(C) + (size_t)m * ldc + n) = float4{s[0], s[1], s[2], s[3]};
+      } else {
+        const bf16 o[4] = {from_f32<bf16>(s[0]), from_f32<bf16>(s[1]), from_f32<bf16>(s[2]), from_f32<bf16>(s[3])};
+        *reinterpret_cast<uint2*>(reinterpret_cast<bf16*>(C) + (size_t)m * ldc + n) = __builtin_bit_cast(uint2, o);
+      }
+    } else {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      if (n + q >= N) break;
-      if (OUT_F32)
-        reinterpret_cast<float*>(C)[(size_t)m * ldc + n + q] = s[q];
-      else
-        reinterpret_cast<bf16*>(C)[(size_t)m * ldc + n + q] = from_f32<bf16>(s[q]);
+      for (int q = 0; q < 4; ++q) {
+        if (n + q >= N) break;
+        if (OUT_F32)
+          reinterpret_cast<float*>(C)[(size_t)m * ldc + n + q] = s[q];
+        else
+          reinterpret_cast<bf16*>(C)[(size_t)m * ldc + n + q] = from_f32<bf16>(s[q]);
+      }
     }
   }
 }
@@ -255,10 +281,12 @@ int gemm_nt(long M, long N, long K, const void* A, long lda, const void* B, long
   if (rc) return rc;
   long blocks = ((long)M * ((N + 3) / 4) + 255) / 256;
   if (blocks > 65535 * 4) blocks = 65535 * 4;
+  // whole 4-column stores: rows start 8- (bf16) or 16-byte (float32) aligned
+  const int vst = ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(C) & (out_f32 ? 15 : 7)) == 0;
   if (out_f32)
-    hipLaunchKernelGGL(gemm_split_reduce<true>, dim3((unsigned)blocks), dim3(256), 0, s, (int)M, (int)N, c.nz, (const float*)ws, C, ldc);
+    hipLaunchKernelGGL(gemm_split_reduce<true>, dim3((unsigned)blocks), dim3(256), 0, s, (int)M, (int)N, c.nz, (const float*)ws, C, ldc, vst);
   else
-    hipLaunchKernelGGL(gemm_split_reduce<false>, dim3((unsigned)blocks), dim3(256), 0, s, (int)M, (int)N, c.nz, (const float*)ws, C, ldc);
+    hipLaunchKernelGGL(gemm_split_reduce<false>, dim3((unsigned)blocks), dim3(256), 0, s, (int)M, (int)N, c.nz, (const float*)ws, C, ldc, vst);
   return check_launch("gemm split reduce");
 }
 

@@ -54,14 +54,25 @@ __global__ __launch_bounds__(kThreads) void permute_coef_kernel(KFoldT ft, int K
   const int o0 = ob * 32, i0 = ib * 16;
   const int t = threadIdx.x;
   if (vin) {
+    // the block's rows in rounds of 4 x 256 chunks, each round's loads issued before any store
+    // (K <= 16: one round; branch-free loads stay in flight together)
     const int CR = RL / VW;
-    for (int e = t; e < 32 * CR; e += kThreads) {
-      const int ol = e / CR, q = e - ol * CR;
-      const int o = o0 + ol;
-      float v[VW];
-      unpack16<T>(gload16(c + ((size_t)o * IN + i0) * K + q * VW, o < OUT && i0 < IN), v);
+    for (int e0 = t; e0 < 32 * CR; e0 += 4 * kThreads) {
+      u32x4 raw[4];
 #pragma unroll
-      for (int u = 0; u < VW; ++u) smem[ol * RS + q * VW + u] = v[u];
+      for (int k = 0; k < 4; ++k) {
+        const int e = e0 + k * kThreads, ol = e / CR, q = e - ol * CR, o = o0 + ol;
+        raw[k] = gload16s(c + ((size_t)o * IN + i0) * K + q * VW, e < 32 * CR && o < OUT && i0 < IN, c);
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int e = e0 + k * kThreads, ol = e / CR, q = e - ol * CR;
+        if (e >= 32 * CR) break;
+        float v[VW];
+        unpack16<T>(raw[k], v);
+#pragma unroll
+        for (int u = 0; u < VW; ++u) smem[ol * RS + q * VW + u] = v[u];
+      }
     }
   } else {
     for (int e = t; e < 32 * RL; e += kThreads) {
@@ -173,12 +184,21 @@ __global__ __launch_bounds__(kThreads) void transpose_kernel(int B, int OUT, int
   __shared__ float tile[64][65];
   const int b0 = blockIdx.y * 64, o0 = blockIdx.x * 64;
   const int cl = threadIdx.x % LPR, rl = threadIdx.x / LPR;
+  constexpr int NR = 64 / RPI;  // rows per thread
+  u32x4 raw[NR];                // vin: every row's load issued before the first LDS store
+  if (vin) {
 #pragma unroll
-  for (int r = rl; r < 64; r += RPI) {
-    const int b = b0 + r, o = o0 + cl * VW;
+    for (int k = 0; k < NR; ++k) {
+      const int b = b0 + rl + k * RPI, o = o0 + cl * VW;
+      raw[k] = gload16s(g + (size_t)b * OUT + o, b < B && o < OUT, g);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < NR; ++k) {
+    const int r = rl + k * RPI, b = b0 + r, o = o0 + cl * VW;
     float v[VW];
     if (vin) {
-      unpack16<T>(gload16(g + (size_t)b * OUT + o, b < B && o < OUT), v);
+      unpack16<T>(raw[k], v);
     } else {
 #pragma unroll
       for (int u = 0; u < VW; ++u) v[u] = (b < B && o + u < OUT) ? to_f32(g[(size_t)b * OUT + o + u]) : 0.f;
@@ -283,9 +303,10 @@ __global__ __launch_bounds__(kThreads) void zmapc_kernel(int B, int IN, int BP, 
     if (i >= INP) continue;
     float xv[VW], wv[VW];
     if (vin) {
+      // without w the w load reads x again (a cache hit) and is not used: no branch around loads
       const bool ok = b < B && i < IN;
-      unpack16<T>(gload16(x + (size_t)b * IN + i, ok), xv);
-      if (wc && w) unpack16<T>(gload16(w + (size_t)b * IN + i, ok), wv);
+      unpack16<T>(gload16s(x + (size_t)b * IN + i, ok, x), xv);
+      unpack16<T>(gload16s((w ? w : x) + (size_t)b * IN + i, ok, x), wv);
     } else {
 #pragma unroll
       for (int u = 0; u < VW; ++u) {
@@ -567,14 +588,25 @@ __global__ __launch_bounds__(kThreads) void zmapT_kernel(int B, int IN, int BP, 
   float* tw = tz + 64 * 65;
   const int b0 = blockIdx.y * 64, i0 = blockIdx.x * 64;
   const int cl = threadIdx.x % LPR, rl = threadIdx.x / LPR;
+  constexpr int NR = 64 / RPI;  // rows per thread
+  u32x4 xraw[NR], wraw[NR];     // vin: every row's loads issued before the first LDS store
+  if (vin) {
+    // without w the w loads read x again (cache hits) and are not used: no branch around loads
 #pragma unroll
-  for (int r = rl; r < 64; r += RPI) {
-    const int b = b0 + r, i = i0 + cl * VW;
+    for (int k = 0; k < NR; ++k) {
+      const int b = b0 + rl + k * RPI, i = i0 + cl * VW;
+      const bool ok = b < B && i < IN;
+      xraw[k] = gload16s(x + (size_t)b * IN + i, ok, x);
+      wraw[k] = gload16s((w ? w : x) + (size_t)b * IN + i, ok, x);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < NR; ++k) {
+    const int r = rl + k * RPI, b = b0 + r, i = i0 + cl * VW;
     float xv[VW], wv[VW];
     if (vin) {
-      const bool ok = b < B && i < IN;
-      unpack16<T>(gload16(x + (size_t)b * IN + i, ok), xv);
-      if (wt && w) unpack16<T>(gload16(w + (size_t)b * IN + i, ok), wv);
+      unpack16<T>(xraw[k], xv);
+      unpack16<T>(wraw[k], wv);
     } else {
 #pragma unroll
       for (int u = 0; u < VW; ++u) {
