@@ -21,7 +21,7 @@ namespace {
 template <int TN, int RB, int NBUF, bool OUT_F32>
 __global__ __launch_bounds__(512) void gemm_nt_kernel(int M, int N, int S, int s_per_split, const bf16* __restrict__ A,
                                                       long lda, const bf16* __restrict__ B, long ldb, void* __restrict__ C,
-                                                      long ldc, long split_stride, int vout) {
+                                                      long ldc, long split_stride, int vout, int tile0, int compact) {
   constexpr int BM = 256, BN = 128 * TN, SA = BM * RB, SS = (BM + BN) * RB, NBLK = SS / 1024, BPW = NBLK / 8;
   constexpr int CPR = RB / 16, RPB = 1024 / RB, KS = RB / 32, EPS = RB / 2;
   constexpr int RPASS = 64, RP = BN + 4;
@@ -32,7 +32,7 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(int M, int N, int S, int s
 
   const int n_m = (M + BM - 1) / BM, n_n = (N + BN - 1) / BN;
   int tm_, tn_;
-  xcd_tile_grouped(blockIdx.x, n_m, n_n, 8, tm_, tn_);
+  xcd_tile_grouped(tile0 + blockIdx.x, n_m, n_n, 8, tm_, tn_);
   const int m0 = tm_ * BM, n0 = tn_ * BN;
   const int z = blockIdx.y;
   const int s_begin = z * s_per_split, s_end = s_begin + s_per_split < S ? s_begin + s_per_split : S;
@@ -109,7 +109,9 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(int M, int N, int S, int s
   // epilogue: passes of RPASS rows, accumulators -> LDS -> global
   float* red = reinterpret_cast<float*>(smem);  // [RPASS][RP]
   constexpr int CH = OUT_F32 ? 4 : 8;            // elements per 16-byte chunk
-  char* cbase = reinterpret_cast<char*>(C) + (size_t)z * split_stride * (OUT_F32 ? 4 : 2);
+  // compact: this workgroup's whole BM x BN float32 tile at (z gridDim.x + blockIdx.x) BM BN
+  char* cbase = compact ? reinterpret_cast<char*>(C) + ((size_t)z * gridDim.x + blockIdx.x) * BM * BN * 4
+                        : reinterpret_cast<char*>(C) + (size_t)z * split_stride * (OUT_F32 ? 4 : 2);
 #pragma unroll
   for (int ps = 0; ps < BM / RPASS; ++ps) {
     __syncthreads();
@@ -128,8 +130,13 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(int M, int N, int S, int s
     for (int e = tid; e < RPASS * (BN / CH); e += 512) {
       const int row = e / (BN / CH), ch = e % (BN / CH);
       const int m = m0 + ps * RPASS + row, n = n0 + ch * CH;
-      if (m >= M || n >= N) continue;
       const float* v = red + row * RP + ch * CH;
+      if (OUT_F32 && compact) {
+        gstore16(reinterpret_cast<float*>(cbase) + (size_t)(ps * RPASS + row) * BN + ch * CH,
+                 __builtin_bit_cast(u32x4, f32x4{v[0], v[1], v[2], v[3]}));
+        continue;
+      }
+      if (m >= M || n >= N) continue;
       if (OUT_F32) {
         float* dst = reinterpret_cast<float*>(cbase) + (size_t)m * ldc + n;
         if (vout && n + CH <= N) {
@@ -205,13 +212,62 @@ __global__ __launch_bounds__(256) void gemm_split_reduce(int M, int N, int nz, c
   }
 }
 
+// The tail tiles of a tail split: tile t of the launch that started at logical tile tile0 holds
+// nz compact float32 partials part[z][t][256][BN]; C gets their sum in split order (deterministic)
+// at the tile's place, rows and columns past M and N dropped. blockIdx.y = t.
+template <bool OUT_F32>
+__global__ __launch_bounds__(256) void gemm_tail_reduce(int M, int N, int n_m, int n_n, int tile0, int n_tail, int nz,
+                                                        int BN, const float* __restrict__ part, void* __restrict__ C,
+                                                        long ldc, int vst) {
+  int tm, tn;
+  xcd_tile_grouped(tile0 + blockIdx.y, n_m, n_n, 8, tm, tn);
+  const int m0 = tm * 256, n0 = tn * BN, c4 = BN / 4;
+  const size_t tsz = (size_t)256 * BN;
+  for (int e = blockIdx.x * 256 + threadIdx.x; e < 256 * c4; e += gridDim.x * 256) {
+    const int r = e / c4, c = (e - r * c4) * 4, m = m0 + r, n = n0 + c;
+    if (m >= M || n >= N) continue;
+    const float* p = part + (size_t)blockIdx.y * tsz + (size_t)r * BN + c;
+    float s[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+    for (int z = 0; z < nz; ++z) {
+      const float4 v = *reinterpret_cast<const float4*>(p + (size_t)z * n_tail * tsz);
+      s[0] += v.x;
+      s[1] += v.y;
+      s[2] += v.z;
+      s[3] += v.w;
+    }
+    if (vst && n + 4 <= N) {
+      if (OUT_F32) {
+        *reinterpret_cast<float4*>(reinterpret_cast<float*>(C) + (size_t)m * ldc + n) = float4{s[0], s[1], s[2], s[3]};
+      } else {
+        const bf16 o[4] = {from_f32<bf16>(s[0]), from_f32<bf16>(s[1]), from_f32<bf16>(s[2]), from_f32<bf16>(s[3])};
+        *reinterpret_cast<uint2*>(reinterpret_cast<bf16*>(C) + (size_t)m * ldc + n) = __builtin_bit_cast(uint2, o);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (n + q >= N) break;
+        if (OUT_F32)
+          reinterpret_cast<float*>(C)[(size_t)m * ldc + n + q] = s[q];
+        else
+          reinterpret_cast<bf16*>(C)[(size_t)m * ldc + n + q] = from_f32<bf16>(s[q]);
+      }
+    }
+  }
+}
+
 struct GemmCfg {
   int tn, nz;
+  int tail_nz = 0;  // > 0: tail split (whole rounds of tiles over the full reduction, the rest split)
+  long full = 0, rem = 0;  // tail split: tiles of the whole rounds, tail tiles
 };
 
 // Tile width and reduction split with the least modelled time: whole rounds of 256 workgroups,
 // each stage of a 256 x 128 TN tile at ~4.7 TFLOP/s per CU (the core's measured rate), plus the
-// float32 partial sums of a split written and read back at ~5 TB/s.
+// float32 partial sums of a split written and read back at ~5 TB/s. The tail split runs the
+// tiles of whole rounds over the full reduction and splits only the remaining tiles, so a tile
+// count just past a multiple of 256 does not cost another whole round (plus ~5 us for its two
+// extra launches).
 GemmCfg pick_gemm(long M, long N, long S) {
   GemmCfg best{3, 1};
   double best_t = 1e300;
@@ -228,22 +284,62 @@ GemmCfg pick_gemm(long M, long N, long S) {
         best = {tn, nz};
       }
     }
+    const long full = tiles / 256 * 256, rem = tiles - full;
+    if (full == 0 || rem == 0) continue;
+    for (int tz : {2, 4, 8, 16, 32}) {
+      if (tz > S || rem * tz > 256) break;
+      const double t = (double)(full / 256) * S * t_stage + (double)((S + tz - 1) / tz) * t_stage +
+                       (double)tz * rem * 256 * 128 * tn * 8.0 / 5e12 + 5e-6;
+      if (t < best_t * 0.98) {
+        best_t = t;
+        best = {tn, 1, tz, full, rem};
+      }
+    }
   }
   return best;
 }
 
 template <int TN, int RB, int NBUF, bool OUT_F32>
 int launch_gemm(int M, int N, int S, int nz, const bf16* A, long lda, const bf16* B, long ldb, void* C, long ldc,
-                long split_stride, int vout, hipStream_t s) {
+                long split_stride, int vout, hipStream_t s, long tile0 = 0, long n_tiles = -1, int compact = 0) {
   constexpr int SS = (256 + 128 * TN) * RB, EPI = 64 * (128 * TN + 4) * 4;
   constexpr size_t lds = (size_t)NBUF * SS > (size_t)EPI ? (size_t)NBUF * SS : (size_t)EPI;
   auto kern = gemm_nt_kernel<TN, RB, NBUF, OUT_F32>;
   if (!reserve_lds((const void*)kern, lds)) return fail(KF_ELAUNCH, "gemm: cannot reserve %zu bytes of LDS", lds);
   const int n_m = (M + 255) / 256, n_n = (N + 128 * TN - 1) / (128 * TN);
+  if (n_tiles < 0) n_tiles = (long)n_m * n_n;
   const int s_per = (S + nz - 1) / nz;
-  hipLaunchKernelGGL(kern, dim3((unsigned)(n_m * n_n), (unsigned)nz), dim3(512), lds, s, M, N, S, s_per, A, lda, B, ldb,
-                     C, ldc, split_stride, vout);
+  hipLaunchKernelGGL(kern, dim3((unsigned)n_tiles, (unsigned)nz), dim3(512), lds, s, M, N, S, s_per, A, lda, B, ldb,
+                     C, ldc, split_stride, vout, (int)tile0, compact);
   return check_launch("gemm_nt");
+}
+
+// Tail split: the whole rounds into C, the tail tiles' compact partials into ws, their sum into C.
+template <int TN>
+int launch_gemm_tail(const GemmCfg& c, int M, int N, int S, const bf16* A, long lda, const bf16* B, long ldb, void* C,
+                     long ldc, bool out_f32, void* ws, hipStream_t s) {
+  const int CH = out_f32 ? 4 : 8;
+  const int vout = ldc % CH == 0 && aligned16(C);
+  int rc = out_f32 ? launch_gemm<TN, 128, 2, true>(M, N, S, 1, A, lda, B, ldb, C, ldc, 0, vout, s, 0, c.full)
+                   : launch_gemm<TN, 128, 2, false>(M, N, S, 1, A, lda, B, ldb, C, ldc, 0, vout, s, 0, c.full);
+  if (rc) return rc;
+  rc = launch_gemm<TN, 128, 2, true>(M, N, S, c.tail_nz, A, lda, B, ldb, ws, 0, 0, 1, s, c.full, c.rem, 1);
+  if (rc) return rc;
+  const int n_m = (M + 255) / 256, n_n = (N + 128 * TN - 1) / (128 * TN), BN = 128 * TN;
+  const int vst = ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(C) & (out_f32 ? 15 : 7)) == 0;
+  const dim3 grid(16, (unsigned)c.rem);
+  if (out_f32)
+    hipLaunchKernelGGL(gemm_tail_reduce<true>, grid, dim3(256), 0, s, M, N, n_m, n_n, (int)c.full, (int)c.rem,
+                       c.tail_nz, BN, (const float*)ws, C, ldc, vst);
+  else
+    hipLaunchKernelGGL(gemm_tail_reduce<false>, grid, dim3(256), 0, s, M, N, n_m, n_n, (int)c.full, (int)c.rem,
+                       c.tail_nz, BN, (const float*)ws, C, ldc, vst);
+  return check_launch("gemm tail reduce");
+}
+
+size_t split_bytes(const GemmCfg& c, long M, long N) {
+  if (c.tail_nz) return (size_t)c.tail_nz * c.rem * 256 * 128 * c.tn * sizeof(float);
+  return c.nz > 1 ? (size_t)c.nz * M * N * sizeof(float) : 0;
 }
 
 }  // namespace
@@ -252,8 +348,8 @@ namespace kfabi {
 
 size_t gemm_nt_workspace(long M, long N, long K) {
   if (K % 64 != 0) return 0;
-  const GemmCfg c = pick_gemm(M, N, K / 64);
-  return c.nz > 1 ? align256((size_t)c.nz * M * N * sizeof(float)) : 0;
+  const size_t b = split_bytes(pick_gemm(M, N, K / 64), M, N);
+  return b ? align256(b) : 0;
 }
 
 int gemm_nt(long M, long N, long K, const void* A, long lda, const void* B, long ldb, void* C, long ldc, bool out_f32,
@@ -265,6 +361,12 @@ int gemm_nt(long M, long N, long K, const void* A, long lda, const void* B, long
   const int S = (int)(K / 64);
   const GemmCfg c = pick_gemm(M, N, S);
   const int CH = out_f32 ? 4 : 8;
+  if (c.tail_nz) {
+    const size_t need = split_bytes(c, M, N);
+    if (!ws || ws_bytes < need || !aligned16(ws)) return fail(KF_EWORKSPACE, "gemm: split workspace of %zu bytes needed", need);
+    return c.tn == 3 ? launch_gemm_tail<3>(c, (int)M, (int)N, S, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, out_f32, ws, s)
+                     : launch_gemm_tail<2>(c, (int)M, (int)N, S, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, out_f32, ws, s);
+  }
   if (c.nz == 1) {
     const int vout = ldc % CH == 0 && aligned16(C);
     if (out_f32)

@@ -1974,15 +1974,29 @@ __global__ __launch_bounds__(512) void p8_kernel(KBasis bs, int B, int IN, int I
   float* kcs = red + NF * RPASS * RP;
   float* kps = kcs + TI * bs.n_knots;
   // Epilogue work item e = (row e / (TI / 2), inputs 2 (e % (TI / 2)) and + 1): thread tid takes
-  // e = tid + 512 k, so with 512 a multiple of TI / 2 its two inputs are the same in every pass,
-  // and each pass's x values (EPT items) are loaded before the pass's sums go to LDS, so that
-  // their latency passes behind the stores and the barrier. The inputs' (t_0, 1/h) sit in LDS
-  // after the knot rows.
+  // e = tid + 512 k, so with 512 a multiple of TI / 2 its two inputs are the same in every pass.
+  // The inputs' (t_0, 1/h) sit in LDS after the knot rows.
   constexpr int EPT = RPASS * TI / 2 / 512;
   static_assert(EPT * 512 == RPASS * TI / 2, "whole epilogue rounds");
   constexpr bool FIXED_INPUTS = KIND == KF_KIND_BSPLINE && 512 % (TI / 2) == 0;
   const int il_t = 2 * (tid % (TI / 2)), i_t = i0 + il_t;
   float* kus = kps + TI * (bs.n_knots + 2 * bs.spline_k);  // [TI][2]
+  // every pass's x values (EPT items per pass), loaded before the passes (addresses clamped into
+  // x: loads without branches, in flight together behind the knot staging and the first pass's
+  // stores)
+  uint32_t xall[FIXED_INPUTS ? BM / RPASS : 1][EPT];
+  if constexpr (FIXED_INPUTS) {
+    const unsigned short* xs = reinterpret_cast<const unsigned short*>(x);
+#pragma unroll
+    for (int ps = 0; ps < BM / RPASS; ++ps)
+#pragma unroll
+      for (int k = 0; k < EPT; ++k) {
+        const int b = b0 + ps * RPASS + (tid + 512 * k) / (TI / 2);
+        const size_t o = (size_t)(b < B ? b : B - 1) * IN;
+        const uint32_t lo = xs[o + (i_t < IN ? i_t : IN - 1)], hi = xs[o + (i_t + 1 < IN ? i_t + 1 : IN - 1)];
+        xall[ps][k] = lo | hi << 16;
+      }
+  }
   if constexpr (KIND == KF_KIND_BSPLINE) {
     __syncthreads();
     stage_knot_rows(bs, i0, TI, IN, kcs, kps);
@@ -1999,17 +2013,7 @@ __global__ __launch_bounds__(512) void p8_kernel(KBasis bs, int B, int IN, int I
     constexpr int M = decltype(order)::value;
 #pragma unroll
     for (int ps = 0; ps < BM / RPASS; ++ps) {
-      uint32_t xq[EPT];  // bf16 pairs x[b, i_t], x[b, i_t + 1] of this pass's items
-      if constexpr (FIXED_INPUTS) {
-        const unsigned short* xs = reinterpret_cast<const unsigned short*>(x);
-#pragma unroll
-        for (int k = 0; k < EPT; ++k) {  // addresses clamped into x: loads without branches
-          const int b = b0 + ps * RPASS + (tid + 512 * k) / (TI / 2);
-          const size_t o = (size_t)(b < B ? b : B - 1) * IN;
-          const uint32_t lo = xs[o + (i_t < IN ? i_t : IN - 1)], hi = xs[o + (i_t + 1 < IN ? i_t + 1 : IN - 1)];
-          xq[k] = lo | hi << 16;
-        }
-      }
+      uint32_t* xq = xall[FIXED_INPUTS ? ps : 0];  // this pass's bf16 pairs x[b, i_t], x[b, i_t + 1]
       __syncthreads();
 #pragma unroll
       for (int a = 0; a < 4; ++a) {

@@ -64,6 +64,24 @@ def _stream(device: torch.device):
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
+class _NoContext:
+    def __enter__(self):
+        return None
+
+    def __exit__(self, *exc):
+        return False
+
+
+_NO_CONTEXT = _NoContext()
+
+
+def _on(device: torch.device):
+    """torch.cuda.device(device), or nothing when it is already the current device."""
+    if device.index is None or device.index == torch.cuda.current_device():
+        return _NO_CONTEXT
+    return torch.cuda.device(device)
+
+
 # --- basis state ---------------------------------------------------------------
 
 
@@ -123,8 +141,25 @@ def rational_state(num: torch.Tensor, den: torch.Tensor, group_size: int) -> Bas
     return BasisState(num=_as_f32(num), den=_as_f32(den), group_size=group_size)
 
 
+_DESC_CACHE: dict = {}
+
+
 def _desc(plan: KernelPlan, m: int, st: BasisState | None):
-    """(kf_basis struct, keep-alive objects) for derivative order m."""
+    """(kf_basis struct, keep-alive objects) for derivative order m, cached: the struct holds only
+    the plan's constants (the fold of order m) and the state tables' device addresses, so equal
+    keys give equal structs."""
+    key = (plan, m) if st is None else (
+        plan, m, st.group_size,
+        *(0 if t is None else t.data_ptr() for t in (st.knots, st.knots_cmp, st.knots_u, st.num, st.den)))
+    hit = _DESC_CACHE.get(key)
+    if hit is None:
+        if len(_DESC_CACHE) > 4096:
+            _DESC_CACHE.clear()
+        hit = _DESC_CACHE[key] = _make_desc(plan, m, st)
+    return hit
+
+
+def _make_desc(plan: KernelPlan, m: int, st: BasisState | None):
     if m > MAX_ORDER:
         raise NotImplementedError(f"derivative order {m} > {MAX_ORDER} is not compiled into the HIP kernels")
     d = _lib.KfBasis()
@@ -184,7 +219,7 @@ def _raw(op: str, plan: KernelPlan, m: int, x, a, b, st: BasisState | None, n_ou
     dev = x.device
     stream = _stream(dev)
     x = x.contiguous()
-    with torch.cuda.device(dev):
+    with _on(dev):
         if op == "F":
             w, c = a, b
             w = None if w is None else w.contiguous()
@@ -223,7 +258,7 @@ def _rational_param_grad(plan, st: BasisState, x, h, w, m: int = 0):
     dden = torch.empty_like(st.den)
     nbytes = lib.kf_rational_workspace_bytes(ctypes.byref(desc), batch, n_in)
     ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
-    with torch.cuda.device(dev):
+    with _on(dev):
         rc = lib.kf_rational_param_grad(
             ctypes.byref(desc), _dtype_code(x.dtype), batch, n_in, _ptr(x.contiguous()), _ptr(h), _ptr(None if w is None else w.contiguous()),
             _ptr(dnum), _ptr(dden), _ptr(ws), ws.numel(), _stream(dev),
@@ -289,26 +324,73 @@ def _mul(w, t):
     return t if w is None else w * t
 
 
-@torch.library.custom_op("kf::F", mutates_args=())
-def op_F(x: torch.Tensor, w: Opt, c: torch.Tensor, knots: Opt, knots_cmp: Opt, knots_u: Opt, num: Opt, den: Opt, plan: str, m: int) -> torch.Tensor:
+def _plain(t) -> bool:
+    """An eager call on a plain device tensor: nothing traces, compiles, fakes or transforms it
+    (meta and CPU tensors go to the op: its fake kernel, or its device check)."""
+    return (
+        type(t) is torch.Tensor
+        and t.is_cuda
+        and not torch.compiler.is_compiling()
+        and torch._C._len_torch_dispatch_stack() == 0
+        and not torch._C._is_torch_function_mode_enabled()
+        and not torch._C._are_functorch_transforms_active()
+    )
+
+
+class _Entry:
+    """How this module calls a kf op. Eager calls on plain tensors run its twin, a
+    torch.autograd.Function with the op's implementation and the op's autograd formula (the
+    custom-op dispatcher costs more host time per call than a small layer's kernels take);
+    traced, compiled and fake-tensor calls run the registered op, so torch.compile and opcheck
+    see the ops."""
+
+    def __init__(self, op, impl, setup, backward):
+        self.op = op
+
+        # forward(ctx, ...) rather than a separate setup_context: with setup_context, every
+        # Function.apply binds its arguments through inspect.signature (tens of microseconds)
+        def forward(ctx, *args):
+            out = impl(*args)
+            setup(ctx, args, out)
+            return out
+
+        self.twin = type(
+            f"{impl.__name__}_twin",
+            (torch.autograd.Function,),
+            {"forward": staticmethod(forward), "backward": staticmethod(backward)},
+        )
+
+    def __call__(self, *args):
+        if _plain(args[0]):
+            return self.twin.apply(*args)
+        return self.op(*args)
+
+
+def _F_impl(x: torch.Tensor, w: Opt, c: torch.Tensor, knots: Opt, knots_cmp: Opt, knots_u: Opt, num: Opt, den: Opt, plan: str, m: int) -> torch.Tensor:
     """y[b,o] = sum_{i,k} w[b,i] c[o,i,k] phi_k^(m)(x[b,i])."""
     return _raw("F", plan_of(plan), m, x, w, c, _state(knots, knots_cmp, knots_u, num, den, x.shape[1]), c.shape[0])
 
 
-@torch.library.custom_op("kf::G", mutates_args=())
-def op_G(x: torch.Tensor, g: torch.Tensor, w: Opt, knots: Opt, knots_cmp: Opt, knots_u: Opt, num: Opt, den: Opt, plan: str, m: int) -> torch.Tensor:
+op_F = torch.library.custom_op("kf::F", mutates_args=())(_F_impl)
+
+
+def _G_impl(x: torch.Tensor, g: torch.Tensor, w: Opt, knots: Opt, knots_cmp: Opt, knots_u: Opt, num: Opt, den: Opt, plan: str, m: int) -> torch.Tensor:
     """dc[o,i,k] = sum_b w[b,i] g[b,o] phi_k^(m)(x[b,i])."""
     return _raw("G", plan_of(plan), m, x, w, g, _state(knots, knots_cmp, knots_u, num, den, x.shape[1]), g.shape[1])
 
 
-@torch.library.custom_op("kf::P", mutates_args=())
-def op_P(x: torch.Tensor, g: torch.Tensor, c: torch.Tensor, knots: Opt, knots_cmp: Opt, knots_u: Opt, num: Opt, den: Opt, plan: str, m: int) -> torch.Tensor:
+op_G = torch.library.custom_op("kf::G", mutates_args=())(_G_impl)
+
+
+def _P_impl(x: torch.Tensor, g: torch.Tensor, c: torch.Tensor, knots: Opt, knots_cmp: Opt, knots_u: Opt, num: Opt, den: Opt, plan: str, m: int) -> torch.Tensor:
     """p[b,i] = sum_{o,k} g[b,o] c[o,i,k] phi_k^(m)(x[b,i])."""
     return _raw("P", plan_of(plan), m, x, g, c, _state(knots, knots_cmp, knots_u, num, den, x.shape[1]), c.shape[0])
 
 
-@torch.library.custom_op("kf::rational_bwd", mutates_args=())
-def op_rational_bwd(
+op_P = torch.library.custom_op("kf::P", mutates_args=())(_P_impl)
+
+
+def _rational_bwd_impl(
     x: torch.Tensor, g: torch.Tensor, c: torch.Tensor, w: Opt, num: torch.Tensor, den: torch.Tensor, plan: str, m: int
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """(P_{m+1}(x, g, c), d/dnum, d/dden) of sum_{b,o} g[b,o] F_m(x, c, w)[b,o] for a rational
@@ -318,6 +400,9 @@ def op_rational_bwd(
     st = _state(None, None, None, num, den, x.shape[1])
     p1, dnum, dden = _rational_bwd_raw(pl, m, st, x, g, c, w)
     return p1, dnum.to(num.dtype), dden.to(den.dtype)
+
+
+op_rational_bwd = torch.library.custom_op("kf::rational_bwd", mutates_args=())(_rational_bwd_impl)
 
 
 def _rational_bwd_raw(pl: KernelPlan, m: int, st: BasisState, x, g, c, w):
@@ -334,7 +419,7 @@ def _rational_bwd_raw(pl: KernelPlan, m: int, st: BasisState, x, g, c, w):
     dnum, dden = torch.empty_like(st.num), torch.empty_like(st.den)
     nbytes = lib.kf_rational_bwd_workspace_bytes(ctypes.byref(desc), dt, batch, n_in, n_out)
     ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=x.device)
-    with torch.cuda.device(x.device):
+    with _on(x.device):
         rc = lib.kf_rational_bwd(
             ctypes.byref(desc), dt, batch, n_in, n_out, _ptr(x), _ptr(g), _ptr(c), _ptr(w), _ptr(p1), _ptr(dnum),
             _ptr(dden), _ptr(ws), ws.numel(), _stream(x.device),
@@ -344,12 +429,14 @@ def _rational_bwd_raw(pl: KernelPlan, m: int, st: BasisState, x, g, c, w):
     return p1, dnum, dden
 
 
-@torch.library.custom_op("kf::rational_param_grad", mutates_args=())
-def op_rational_param_grad(x: torch.Tensor, h: torch.Tensor, w: Opt, num: torch.Tensor, den: torch.Tensor, plan: str, m: int) -> tuple[torch.Tensor, torch.Tensor]:
+def _rational_param_grad_impl(x: torch.Tensor, h: torch.Tensor, w: Opt, num: torch.Tensor, den: torch.Tensor, plan: str, m: int) -> tuple[torch.Tensor, torch.Tensor]:
     """(d/dnum, d/dden) of sum_{b,i} h[b,i] w[b,i] phi^(m)(x[b,i]) for a rational plan."""
     st = _state(None, None, None, num, den, x.shape[1])
     dnum, dden = _rational_param_grad(plan_of(plan), st, x, h.float().contiguous(), w, m)
     return dnum.to(num.dtype), dden.to(den.dtype)
+
+
+op_rational_param_grad = torch.library.custom_op("kf::rational_param_grad", mutates_args=())(_rational_param_grad_impl)
 
 
 @op_F.register_fake
@@ -395,16 +482,16 @@ def _F_backward(ctx, gy):
     gy = gy.contiguous()
     tabs = (knots, knots_cmp, knots_u, num, den)
     if plan_of(plan).kind == "rational" and (need[6] or need[7]):
-        p1, gnum, gden = op_rational_bwd(x, gy, c, w, num, den, plan, m)
+        p1, gnum, gden = _RBWD(x, gy, c, w, num, den, plan, m)
         if need[0]:
             # under create_graph the x-gradient stays differentiable through kf::P
-            gx = _mul(w, op_P(x, gy, c, *tabs, plan, 1) if torch.is_grad_enabled() else p1)
+            gx = _mul(w, _P(x, gy, c, *tabs, plan, 1) if torch.is_grad_enabled() else p1)
     elif need[0]:
-        gx = _mul(w, op_P(x, gy, c, *tabs, plan, m + 1))
+        gx = _mul(w, _P(x, gy, c, *tabs, plan, m + 1))
     if need[2]:
-        gc = op_G(x, gy, w, *tabs, plan, m)
+        gc = _G(x, gy, w, *tabs, plan, m)
     if need[1]:
-        gw = op_P(x, gy, c, *tabs, plan, m)
+        gw = _P(x, gy, c, *tabs, plan, m)
     return gx, gw, gc, None, None, None, gnum, gden, None, None
 
 
@@ -422,13 +509,13 @@ def _G_backward(ctx, gdc):
     gx = gnum = gden = None
     if need[6] or need[7]:
         # d<gdc, G_m>/dtheta = sum_{b,i} (sum_o g gdc) w dphi^(m)/dtheta: the h of P(x, g, gdc)
-        p1, gnum, gden = op_rational_bwd(x, g, gdc, w, num, den, plan, m)
+        p1, gnum, gden = _RBWD(x, g, gdc, w, num, den, plan, m)
         if need[0]:
-            gx = _mul(w, op_P(x, g, gdc, *tabs, plan, m + 1) if torch.is_grad_enabled() else p1)
+            gx = _mul(w, _P(x, g, gdc, *tabs, plan, m + 1) if torch.is_grad_enabled() else p1)
     elif need[0]:
-        gx = _mul(w, op_P(x, g, gdc, *tabs, plan, m + 1))
-    gg = op_F(x, w, gdc, *tabs, plan, m) if need[1] else None
-    gw = op_P(x, g, gdc, *tabs, plan, m) if need[2] else None
+        gx = _mul(w, _P(x, g, gdc, *tabs, plan, m + 1))
+    gg = _F(x, w, gdc, *tabs, plan, m) if need[1] else None
+    gw = _P(x, g, gdc, *tabs, plan, m) if need[2] else None
     return gx, gg, gw, None, None, None, gnum, gden, None, None
 
 
@@ -446,13 +533,13 @@ def _P_backward(ctx, gp):
     gx = gnum = gden = None
     if need[6] or need[7]:
         # d<gp, P_m>/dtheta = sum_{b,i} gp (sum_o g c) dphi^(m)/dtheta: P(x, g, c)'s h, weight gp
-        p1, gnum, gden = op_rational_bwd(x, g, c, gp, num, den, plan, m)
+        p1, gnum, gden = _RBWD(x, g, c, gp, num, den, plan, m)
         if need[0]:
-            gx = gp * (op_P(x, g, c, *tabs, plan, m + 1) if torch.is_grad_enabled() else p1)
+            gx = gp * (_P(x, g, c, *tabs, plan, m + 1) if torch.is_grad_enabled() else p1)
     elif need[0]:
-        gx = gp * op_P(x, g, c, *tabs, plan, m + 1)
-    gg = op_F(x, gp, c, *tabs, plan, m) if need[1] else None
-    gc = op_G(x, g, gp, *tabs, plan, m) if need[2] else None
+        gx = gp * _P(x, g, c, *tabs, plan, m + 1)
+    gg = _F(x, gp, c, *tabs, plan, m) if need[1] else None
+    gc = _G(x, g, gp, *tabs, plan, m) if need[2] else None
     return gx, gg, gc, None, None, None, gnum, gden, None, None
 
 
@@ -482,17 +569,17 @@ def _rat(st: BasisState | None, num, den):
 
 def prim_F(x, c, w, st, plan, m=0, num=None, den=None):
     num, den = _rat(st, num, den)
-    return op_F(x, w, c, *_tables(st), num, den, plan_key(plan), m)
+    return _F(x, w, c, *_tables(st), num, den, plan_key(plan), m)
 
 
 def prim_G(x, g, w, st, plan, m=0, num=None, den=None):
     num, den = _rat(st, num, den)
-    return op_G(x, g, w, *_tables(st), num, den, plan_key(plan), m)
+    return _G(x, g, w, *_tables(st), num, den, plan_key(plan), m)
 
 
 def prim_P(x, g, c, st, plan, m=0, num=None, den=None):
     num, den = _rat(st, num, den)
-    return op_P(x, g, c, *_tables(st), num, den, plan_key(plan), m)
+    return _P(x, g, c, *_tables(st), num, den, plan_key(plan), m)
 
 
 def spline_forward(x: torch.Tensor, coef: torch.Tensor, st: BasisState | None, plan: KernelPlan | str, num=None, den=None) -> torch.Tensor:
@@ -518,16 +605,18 @@ def _features_raw(plan, m, st, x2: torch.Tensor) -> torch.Tensor:
     desc, keep = _desc(plan, m, st)
     batch, n_in = x2.shape
     out = torch.empty(batch, n_in, plan.size, dtype=x2.dtype, device=x2.device)
-    with torch.cuda.device(x2.device):
+    with _on(x2.device):
         rc = lib.kf_features(ctypes.byref(desc), _dtype_code(x2.dtype), batch, n_in, _ptr(x2), _ptr(out), _stream(x2.device))
     _lib.check(rc, "kf_features")
     return out
 
 
-@torch.library.custom_op("kf::features", mutates_args=())
-def op_features(x: torch.Tensor, knots: Opt, knots_cmp: Opt, knots_u: Opt, num: Opt, den: Opt, plan: str, m: int) -> torch.Tensor:
+def _features_impl(x: torch.Tensor, knots: Opt, knots_cmp: Opt, knots_u: Opt, num: Opt, den: Opt, plan: str, m: int) -> torch.Tensor:
     """phi_k^(m)(x[b,i]), (B, in, K)."""
     return _features_raw(plan_of(plan), m, _state(knots, knots_cmp, knots_u, num, den, x.shape[1]), x.contiguous())
+
+
+op_features = torch.library.custom_op("kf::features", mutates_args=())(_features_impl)
 
 
 @op_features.register_fake
@@ -546,7 +635,7 @@ def _features_backward(ctx, gphi):
     need = ctx.needs_input_grad
     gx = gnum = gden = None
     if need[0]:
-        gx = (gphi * op_features(x, knots, knots_cmp, knots_u, num, den, plan, m + 1)).sum(-1)
+        gx = (gphi * _FEAT(x, knots, knots_cmp, knots_u, num, den, plan, m + 1)).sum(-1)
     if need[4] or need[5]:
         gnum, gden = _rational_grads_of(plan, x, gphi[..., 0], m, num, den)
     return gx, None, None, None, gnum, gden, None, None
@@ -555,8 +644,7 @@ def _features_backward(ctx, gphi):
 op_features.register_autograd(_features_backward, setup_context=_features_setup)
 
 
-@torch.library.custom_op("kf::column_sums", mutates_args=())
-def op_column_sums(g: torch.Tensor) -> torch.Tensor:
+def _column_sums_impl(g: torch.Tensor) -> torch.Tensor:
     """sum over the rows of g (rows, n), float32 accumulation, g's dtype (kf_column_sums)."""
     _require_device(g)
     g = g.contiguous()
@@ -565,10 +653,13 @@ def op_column_sums(g: torch.Tensor) -> torch.Tensor:
     out = torch.empty(n, dtype=g.dtype, device=g.device)
     nbytes = lib.kf_column_sums_workspace_bytes(rows, n)
     ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=g.device)
-    with torch.cuda.device(g.device):
+    with _on(g.device):
         rc = lib.kf_column_sums(_dtype_code(g.dtype), rows, n, _ptr(g), _ptr(out), _ptr(ws), ws.numel(), _stream(g.device))
     _lib.check(rc, "kf_column_sums")
     return out
+
+
+op_column_sums = torch.library.custom_op("kf::column_sums", mutates_args=())(_column_sums_impl)
 
 
 @op_column_sums.register_fake
@@ -576,10 +667,23 @@ def _(g):
     return g.new_empty(g.shape[1])
 
 
-@torch.library.custom_op("kf::bias_add", mutates_args=())
-def op_bias_add(y: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
+def _colsum_setup(ctx, inputs, output):
+    ctx.rows = inputs[0].shape[0]
+
+
+def _colsum_backward(ctx, gout):
+    return gout.unsqueeze(0).expand(ctx.rows, -1) if ctx.needs_input_grad[0] else None
+
+
+op_column_sums.register_autograd(_colsum_backward, setup_context=_colsum_setup)
+
+
+def _bias_add_impl(y: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
     """y + bias over the last dimension; its bias gradient runs on kf_column_sums."""
     return y + bias
+
+
+op_bias_add = torch.library.custom_op("kf::bias_add", mutates_args=())(_bias_add_impl)
 
 
 @op_bias_add.register_fake
@@ -594,15 +698,14 @@ def _bias_setup(ctx, inputs, output):
 def _bias_backward(ctx, gy):
     gb = None
     if ctx.needs_input_grad[1]:
-        gb = op_column_sums(gy.reshape(-1, gy.shape[-1])).to(ctx.bias_dtype)
+        gb = _COLSUM(gy.reshape(-1, gy.shape[-1])).to(ctx.bias_dtype)
     return gy, gb
 
 
 op_bias_add.register_autograd(_bias_backward, setup_context=_bias_setup)
 
 
-@torch.library.custom_op("kf::silu_taylor", mutates_args=())
-def op_silu_taylor(h: torch.Tensor, hp: torch.Tensor, S: Opt) -> tuple[torch.Tensor, torch.Tensor]:
+def _silu_taylor_impl(h: torch.Tensor, hp: torch.Tensor, S: Opt) -> tuple[torch.Tensor, torch.Tensor]:
     """(A, sq) of the SiLU base branch's second-order Taylor terms (kf_silu_taylor): for h (B, n),
     hp (D, B, n), S (B, n) or None, sq = sum_d hp_d^2 and the stacked GEMM operand
     A = [silu(h); silu'(h) hp_d ...; silu''(h) sq + silu'(h) S] ((D + 2) B, n)."""
@@ -612,11 +715,14 @@ def op_silu_taylor(h: torch.Tensor, hp: torch.Tensor, S: Opt) -> tuple[torch.Ten
     S = None if S is None else S.contiguous()
     A = torch.empty((D + 2) * B, n, dtype=h.dtype, device=h.device)
     sq = torch.empty_like(h)
-    with torch.cuda.device(h.device):
+    with _on(h.device):
         rc = _lib.load().kf_silu_taylor(_dtype_code(h.dtype), D, B, n, _ptr(h), _ptr(hp), _ptr(S), _ptr(A), _ptr(sq),
                                         _stream(h.device))
     _lib.check(rc, "kf_silu_taylor")
     return A, sq
+
+
+op_silu_taylor = torch.library.custom_op("kf::silu_taylor", mutates_args=())(_silu_taylor_impl)
 
 
 @op_silu_taylor.register_fake
@@ -657,6 +763,11 @@ def _silu_taylor_backward(ctx, gA, gsq):
 op_silu_taylor.register_autograd(_silu_taylor_backward, setup_context=_silu_taylor_setup)
 
 
+def silu_taylor(h: torch.Tensor, hp: torch.Tensor, S: torch.Tensor | None) -> tuple[torch.Tensor, torch.Tensor]:
+    """kf::silu_taylor (see its implementation): the SiLU base branch's Taylor operands."""
+    return _SILU_T(h, hp, S)
+
+
 BIAS_OP_MIN_ELEMENTS = 1 << 20  # below this a plain add costs less (one op dispatch fewer)
 
 
@@ -665,12 +776,12 @@ def bias_add(y: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
     kf_column_sums (torch's reduction over the rows is several times slower there)."""
     if y.numel() < BIAS_OP_MIN_ELEMENTS:
         return y + bias
-    return op_bias_add(y, bias)
+    return _BIAS(y, bias)
 
 
 def _rational_grads_of(plan, x2, h, m, num, den):
     """d/d(num, den) of sum_{b,i} h[b,i] phi^(m)(x[b,i]) for a rational plan."""
-    return op_rational_param_grad(x2, h.float().contiguous(), None, num, den, plan, m)
+    return _RPGRAD(x2, h.float().contiguous(), None, num, den, plan, m)
 
 
 def basis_derivative(basis, x: torch.Tensor, m: int, params: dict | None) -> torch.Tensor:
@@ -696,7 +807,7 @@ def basis_derivative(basis, x: torch.Tensor, m: int, params: dict | None) -> tor
             num, den = params["numerator"], params["denominator"]
             if num.dim() == 1:
                 num, den = num[None], den[None]
-    out = op_features(x2, *_tables(st), num, den, plan_key(plan), m)
+    out = _FEAT(x2, *_tables(st), num, den, plan_key(plan), m)
     return out.to(x.dtype).reshape(*lead, x.shape[-1], plan.size)
 
 
@@ -733,7 +844,7 @@ def _edge_raw(plan, m, st, x2, c, base_w):
     batch, n_in = x2.shape
     n_out = c.shape[0]
     out = torch.empty(batch, n_out, n_in, dtype=x2.dtype, device=x2.device)
-    with torch.cuda.device(x2.device):
+    with _on(x2.device):
         rc = lib.kf_edge_derivative(
             ctypes.byref(desc), _dtype_code(x2.dtype), batch, n_in, n_out, _ptr(x2), _ptr(c.contiguous()),
             _ptr(None if base_w is None else base_w.contiguous()), _ptr(out), _stream(x2.device),
@@ -742,10 +853,12 @@ def _edge_raw(plan, m, st, x2, c, base_w):
     return out
 
 
-@torch.library.custom_op("kf::edge_derivative", mutates_args=())
-def op_edge(x: torch.Tensor, c: torch.Tensor, base_w: Opt, knots: Opt, knots_cmp: Opt, knots_u: Opt, num: Opt, den: Opt, plan: str, m: int) -> torch.Tensor:
+def _edge_impl(x: torch.Tensor, c: torch.Tensor, base_w: Opt, knots: Opt, knots_cmp: Opt, knots_u: Opt, num: Opt, den: Opt, plan: str, m: int) -> torch.Tensor:
     """d[b,o,i] = sum_k c[o,i,k] phi_k^(m)(x[b,i]) + base_w[o,i] silu^(m)(x[b,i]), (B, out, in)."""
     return _edge_raw(plan_of(plan), m, _state(knots, knots_cmp, knots_u, num, den, x.shape[1]), x.contiguous(), c, base_w)
+
+
+op_edge = torch.library.custom_op("kf::edge_derivative", mutates_args=())(_edge_impl)
 
 
 @op_edge.register_fake
@@ -766,9 +879,9 @@ def _edge_backward(ctx, gd):
     tabs = (knots, knots_cmp, knots_u, num, den)
     if need[0]:
         # d/dx of the edge is the edge derivative of order m+1
-        gx = (gd * op_edge(x, c, base_w, *tabs, plan, m + 1)).sum(1)
+        gx = (gd * _EDGE(x, c, base_w, *tabs, plan, m + 1)).sum(1)
     if need[1]:
-        phi = op_features(x, knots, knots_cmp, knots_u, num, den, plan, m)  # (B, in, K)
+        phi = _FEAT(x, knots, knots_cmp, knots_u, num, den, plan, m)  # (B, in, K)
         gc = torch.einsum("boi,bik->oik", gd, phi)
     if need[2] and base_w is not None:
         gw = torch.einsum("boi,bi->oi", gd, silu_derivative_t(x, m))
@@ -810,7 +923,7 @@ def edge_derivative(x: torch.Tensor, coef_eff: torch.Tensor, base_w: torch.Tenso
     if x2.dtype != coef_eff.dtype:
         x2 = x2.to(coef_eff.dtype)
     num, den = _rat(st, num, den)
-    d = op_edge(x2, coef_eff, base_w, *_tables(st), num, den, plan_key(plan), m)
+    d = _EDGE(x2, coef_eff, base_w, *_tables(st), num, den, plan_key(plan), m)
     return d.to(x.dtype).reshape(*lead, coef_eff.shape[0], x.shape[-1])
 
 
@@ -822,7 +935,7 @@ def op_bspline_interval(x: torch.Tensor, knots_cmp: torch.Tensor) -> torch.Tenso
     x = x.contiguous().float()
     kc = knots_cmp.contiguous().float()
     out = torch.empty(x.shape, dtype=torch.int32, device=x.device)
-    with torch.cuda.device(x.device):
+    with _on(x.device):
         rc = lib.kf_bspline_interval(x.shape[0], x.shape[1], _ptr(x), _ptr(kc), kc.shape[1], _ptr(out), _stream(x.device))
     _lib.check(rc, "kf_bspline_interval")
     return out
@@ -836,3 +949,17 @@ def _(x, knots_cmp):
 def bspline_interval(x: torch.Tensor, knots_cmp: torch.Tensor) -> torch.Tensor:
     """int32 interval index of float32 x (B, in) on the comparison knots (in, nk); -1 outside."""
     return op_bspline_interval(x, knots_cmp)
+
+
+# --- eager entries (see _Entry) ---------------------------------------------------
+
+_F = _Entry(op_F, _F_impl, _F_setup, _F_backward)
+_G = _Entry(op_G, _G_impl, _G_setup, _G_backward)
+_P = _Entry(op_P, _P_impl, _P_setup, _P_backward)
+_RBWD = _Entry(op_rational_bwd, _rational_bwd_impl, _no_ctx, _no_second_order)
+_RPGRAD = _Entry(op_rational_param_grad, _rational_param_grad_impl, _no_ctx, _no_second_order)
+_FEAT = _Entry(op_features, _features_impl, _features_setup, _features_backward)
+_COLSUM = _Entry(op_column_sums, _column_sums_impl, _colsum_setup, _colsum_backward)
+_BIAS = _Entry(op_bias_add, _bias_add_impl, _bias_setup, _bias_backward)
+_SILU_T = _Entry(op_silu_taylor, _silu_taylor_impl, _silu_taylor_setup, _silu_taylor_backward)
+_EDGE = _Entry(op_edge, _edge_impl, _edge_setup, _edge_backward)

@@ -89,7 +89,7 @@ def _taylor_layer(layer, h: torch.Tensor, hp: torch.Tensor, S: torch.Tensor | No
     W = layer.effective_base_weight()
     if W is not None:
         # the base branch's operands of all three orders in one pass, and sum_d h'_d^2
-        A, sq = K.op_silu_taylor(h, hp, S)
+        A, sq = K.silu_taylor(h, hp, S)
     else:
         sq = (hp * hp).sum(0)
     # value, first order (the D directions and S stacked into one launch), second order
