@@ -166,13 +166,16 @@ inline bool f_lanes_fit(const KBasis& kb, int64_t n_in, int64_t n_out) {
 template <typename T, int KM>
 int launch_f_stream(const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* w,
                     const void* c, void* y, hipStream_t s) {
-  dim3 grid((unsigned)((batch + kThreads - 1) / kThreads));
-  if (n_out <= 8)
-    hipLaunchKernelGGL((f_stream_kernel<T, KM, true>), grid, dim3(kThreads), 0, s, kb, (int)batch, (int)n_in,
-                       (int)n_out, (const T*)x, (const T*)w, (const T*)c, (T*)y);
-  else
-    hipLaunchKernelGGL((f_stream_kernel<T, KM, false>), grid, dim3(kThreads), 0, s, kb, (int)batch, (int)n_in,
-                       (int)n_out, (const T*)x, (const T*)w, (const T*)c, (T*)y);
+  if (n_out <= 8) {
+    dim3 grid((unsigned)((batch + kThreads - 1) / kThreads));
+    hipLaunchKernelGGL((f_stream_kernel<T, KM>), grid, dim3(kThreads), 0, s, kb, (int)batch, (int)n_in, (int)n_out,
+                       (const T*)x, (const T*)w, (const T*)c, (T*)y);
+  } else {  // at most 4 inputs (f_streams): rows of 128 x chunks of 64 outputs
+    if (n_in > 4) return fail(KF_EINVAL, "F: the wide streaming route takes at most 4 inputs");
+    dim3 grid((unsigned)((batch + 127) / 128), (unsigned)((n_out + 63) / 64));
+    hipLaunchKernelGGL((f_wide_kernel<T, KM>), grid, dim3(kThreads), 0, s, kb, (int)batch, (int)n_in, (int)n_out,
+                       (const T*)x, (const T*)w, (const T*)c, (T*)y);
+  }
   return check_launch("F stream");
 }
 

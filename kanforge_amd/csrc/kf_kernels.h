@@ -2673,7 +2673,7 @@ __global__ __launch_bounds__(kThreads) void edge_kernel(KBasis bs, int B, int IN
 // stay in registers while the inputs stream by. Otherwise (IN * KM <= 64): the row's features
 // stay in registers while the outputs stream by, through an LDS tile of 256 rows so that the
 // stores are whole rows.
-template <typename T, int KM, bool NARROW_OUT>
+template <typename T, int KM>
 __global__ __launch_bounds__(kThreads) void f_stream_kernel(KBasis bs, int B, int IN, int OUT, const T* __restrict__ x,
                                                             const T* __restrict__ w, const T* __restrict__ c,
                                                             T* __restrict__ y) {
@@ -2681,7 +2681,7 @@ __global__ __launch_bounds__(kThreads) void f_stream_kernel(KBasis bs, int B, in
   const int K = bs.K;
   const int b = blockIdx.x * kThreads + threadIdx.x;
   const bool ok = b < B;
-  if constexpr (NARROW_OUT) {
+  {
     // the block's rows arrive in chunks of 32 inputs through LDS (coalesced loads), each thread
     // then walks its own row there
     __shared__ float xs[kThreads][33], wsh[kThreads][33];
@@ -2718,45 +2718,55 @@ __global__ __launch_bounds__(kThreads) void f_stream_kernel(KBasis bs, int B, in
       for (int o = 0; o < 8; ++o)
         if (o < OUT) y[(size_t)b * OUT + o] = from_f32<T>(acc[o]);
     }
-  } else {
-    // IN * KM <= 64 features of the row in registers
-    float phi[64];
+  }
+}
+
+// F for layers of at most 4 inputs (IN KM <= 64 features per row) and more than 8 outputs: the
+// features of RB rows go to LDS once, lane = output (64 per workgroup, grid.y over output chunks)
+// with its IN x KM coefficients in registers, and every row costs a few broadcast LDS reads,
+// IN K FMAs and one coalesced store per lane.
+template <typename T, int KM, int RB = 128>
+__global__ __launch_bounds__(kThreads) void f_wide_kernel(KBasis bs, int B, int IN, int OUT, const T* __restrict__ x,
+                                                          const T* __restrict__ w, const T* __restrict__ c,
+                                                          T* __restrict__ y) {
+  constexpr int NT = KM + 8 < KF_MAX_NT ? KM + 8 : KF_MAX_NT;
+  constexpr int FR = 4 * KM;  // features per row (IN <= 4), a whole number of float4
+  __shared__ __attribute__((aligned(16))) float phs[RB][FR];
+  const int K = bs.K, b0 = blockIdx.x * RB, t = threadIdx.x;
+  for (int e = t; e < RB * 4; e += kThreads) {
+    const int r = e / 4, i = e % 4, b = b0 + r;
+    float f[KM];
 #pragma unroll
-    for (int q = 0; q < 64; ++q) phi[q] = 0.f;
-#pragma unroll
-    for (int i = 0; i < 64 / KM; ++i) {
-      if (i >= IN) break;
-      const size_t off = (size_t)(ok ? b : 0) * IN + i;
-      float f[KM];
+    for (int k = 0; k < KM; ++k) f[k] = 0.f;
+    if (i < IN && b < B) {
+      const size_t off = (size_t)b * IN + i;
       basis_features<KM, NT>(to_f32(x[off]), w ? to_f32(w[off]) : 1.f, i, bs, f);
-#pragma unroll
-      for (int k = 0; k < KM; ++k) phi[i * KM + k] = f[k];
     }
-    __shared__ float tile[kThreads][65];
-    const int b0 = blockIdx.x * kThreads;
-    const int rows = B - b0 < kThreads ? B - b0 : kThreads;
-    for (int o0 = 0; o0 < OUT; o0 += 64) {
-      const int no = OUT - o0 < 64 ? OUT - o0 : 64;
-      for (int ol = 0; ol < no; ++ol) {
-        const T* cr = c + (size_t)(o0 + ol) * IN * K;
-        float s = 0.f;
 #pragma unroll
-        for (int i = 0; i < 64 / KM; ++i) {
-          if (i >= IN) break;
+    for (int k = 0; k < KM; ++k) phs[r][i * KM + k] = f[k];
+  }
+  const int o = blockIdx.y * 64 + t % 64, rg = t / 64;
+  float cv[FR];
 #pragma unroll
-          for (int k = 0; k < KM; ++k)
-            if (k < K) s = fmaf(to_f32(cr[i * K + k]), phi[i * KM + k], s);
-        }
-        tile[threadIdx.x][ol] = s;
-      }
-      __syncthreads();
-      // rows b0 .. b0 + rows, outputs o0 .. o0 + no: no consecutive elements per row
-      for (int e = threadIdx.x; e < rows * no; e += kThreads) {
-        const int r = e / no, ol = e % no;
-        y[(size_t)(b0 + r) * OUT + o0 + ol] = from_f32<T>(tile[r][ol]);
-      }
-      __syncthreads();
+  for (int j = 0; j < FR; ++j) {
+    const int i = j / KM, k = j % KM;
+    cv[j] = (o < OUT && i < IN && k < K) ? to_f32(c[((size_t)o * IN + i) * K + k]) : 0.f;
+  }
+  __syncthreads();
+  if (o >= OUT) return;  // no barrier follows
+  for (int r = rg; r < RB; r += kThreads / 64) {
+    const int b = b0 + r;
+    if (b >= B) break;
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < FR; j += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(&phs[r][j]);
+      s = fmaf(cv[j], v.x, s);
+      s = fmaf(cv[j + 1], v.y, s);
+      s = fmaf(cv[j + 2], v.z, s);
+      s = fmaf(cv[j + 3], v.w, s);
     }
+    y[(size_t)b * OUT + o] = from_f32<T>(s);
   }
 }
 

@@ -72,12 +72,17 @@ def kan_chain(fn) -> list | None:
     return mods
 
 
-def _taylor_layer(layer, h: torch.Tensor, hp: torch.Tensor, S: torch.Tensor | None):
-    """A layer's (h, h', S) from its input's: h (B, in), hp (D, B, in) the first derivatives
-    along every input dimension, S (B, in) the sum of the second derivatives (None: zero)."""
+def _taylor_layer(layer, h: torch.Tensor, hps: torch.Tensor, has_S: bool):
+    """A layer's (h, h', S) from its input's: h (B, in) and hps (n1, B, in), the first derivatives
+    along every input dimension followed, when has_S, by the sum of the second derivatives S
+    (absent: zero). Returns h_out and the same stack (D + 1, B, out) for the next layer: the
+    layer's outputs are computed as one row stack [h; h'_1 .. h'_D; S], whose lower rows are that
+    stack already (no copy)."""
     from . import kernels as K
 
-    D, B, n_in = hp.shape
+    n1, B, n_in = hps.shape
+    D = n1 - 1 if has_S else n1
+    hp, S = hps[:D], (hps[D] if has_S else None)
     st = layer._basis_state()
     key = layer._plan_key
     c = layer.effective_coef()
@@ -94,28 +99,27 @@ def _taylor_layer(layer, h: torch.Tensor, hp: torch.Tensor, S: torch.Tensor | No
         sq = (hp * hp).sum(0)
     # value, first order (the D directions and S stacked into one launch), second order
     y = K.prim_F(hk, c, None, st, key, 0, num, den)
-    w1 = hp if S is None else torch.cat([hp, S[None]], 0)
-    n1 = w1.shape[0]
-    f1 = K.prim_F(hk.repeat(n1, 1), c, w1.reshape(n1 * B, n_in).to(dt), st, key, 1, num, den).reshape(n1, B, -1)
+    f1 = K.prim_F(hk.repeat(n1, 1), c, hps.reshape(n1 * B, n_in).to(dt), st, key, 1, num, den).reshape(n1, B, -1)
     f2 = K.prim_F(hk, c, sq.to(dt), st, key, 2, num, den)
     S_spline = f2 if S is None else f2 + f1[D]
     n_out = y.shape[-1]
     Z = torch.cat([y, f1[:D].reshape(D * B, n_out), S_spline], 0)
     if W is not None:
         Z = torch.addmm(Z, A.to(dt), W.t())  # the base branch of y, every h'_d and S: one GEMM
-    y, yp, S_out = Z[:B], Z[B:(D + 1) * B].reshape(D, B, n_out), Z[(D + 1) * B:]
+    y, hps_out = Z[:B], Z[B:].reshape(D + 1, B, n_out)
     if layer.bias is not None:
         y = y + layer.bias
-    return y.to(h.dtype), yp.to(h.dtype), S_out.to(h.dtype)
+    return y.to(h.dtype), hps_out.to(h.dtype)
 
 
 def _laplacian_forward(layers, x: torch.Tensor) -> torch.Tensor:
     B, D = x.shape
     h = x
-    hp = torch.eye(D, dtype=x.dtype, device=x.device)[:, None, :].expand(D, B, D)  # dx/dx_d
-    S = None
+    hps = torch.eye(D, dtype=x.dtype, device=x.device)[:, None, :].expand(D, B, D)  # dx/dx_d
+    has_S = False
     for layer in layers:
-        h, hp, S = _taylor_layer(layer, h, hp, S)
+        h, hps = _taylor_layer(layer, h, hps, has_S)
+        has_S = True
     if h.shape[-1] != 1:
         raise ValueError(f"laplacian needs a scalar field, the network has {h.shape[-1]} outputs")
-    return S[:, 0]
+    return hps[-1][:, 0]
