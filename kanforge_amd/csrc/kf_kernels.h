@@ -2014,6 +2014,20 @@ __global__ __launch_bounds__(512) void p8_kernel(KBasis bs, int B, int IN, int I
 #pragma unroll
     for (int ps = 0; ps < BM / RPASS; ++ps) {
       uint32_t* xq = xall[FIXED_INPUTS ? ps : 0];  // this pass's bf16 pairs x[b, i_t], x[b, i_t + 1]
+      // other kinds: this pass's x pairs, loaded before the pass's sums go to LDS (addresses
+      // clamped into x, so the loads need no branch and their latency passes behind the stores)
+      constexpr int EPG = (RPASS * TI / 2 + 511) / 512;
+      uint32_t xg[FIXED_INPUTS ? 1 : EPG];
+      if constexpr (!FIXED_INPUTS) {
+        const unsigned short* xs = reinterpret_cast<const unsigned short*>(x);
+#pragma unroll
+        for (int k = 0; k < EPG; ++k) {
+          const int e = tid + 512 * k, row = e / (TI / 2), il = 2 * (e % (TI / 2));
+          const int b = b0 + ps * RPASS + row, i = i0 + il;
+          const size_t o = (size_t)(b < B ? b : B - 1) * IN;
+          xg[k] = (uint32_t)xs[o + (i < IN ? i : IN - 1)] | (uint32_t)xs[o + (i + 1 < IN ? i + 1 : IN - 1)] << 16;
+        }
+      }
       __syncthreads();
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
@@ -2064,7 +2078,10 @@ __global__ __launch_bounds__(512) void p8_kernel(KBasis bs, int B, int IN, int I
           if (b < B && i_t < IN) store_pair(b, i_t, v);
         }
       } else {
-        for (int e = tid; e < RPASS * TI / 2; e += 512) {
+#pragma unroll
+        for (int k = 0; k < EPG; ++k) {
+          const int e = tid + 512 * k;
+          if (e >= RPASS * TI / 2) break;
           const int row = e / (TI / 2), il = 2 * (e % (TI / 2));
           const int b = b0 + ps * RPASS + row, i = i0 + il;
           if (b >= B || i >= IN) continue;
@@ -2072,7 +2089,7 @@ __global__ __launch_bounds__(512) void p8_kernel(KBasis bs, int B, int IN, int I
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
             if (i + u >= IN) continue;
-            const float xv = to_f32(x[(size_t)b * IN + i + u]);
+            const float xv = __builtin_bit_cast(float, (xg[k] >> (16 * u)) << 16);
             if constexpr (KIND == KF_KIND_BSPLINE) {
               const int nk = bs.n_knots;
               float t0, ih, N[KD + 1];
