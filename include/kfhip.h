@@ -103,10 +103,13 @@ typedef struct kf_basis {
   const float *knots_uniform;
 } kf_basis;
 
-/* operation ids for kf_workspace_bytes */
+/* operation ids for kf_workspace_bytes (and kf_base_fused for the *_BASE ids) */
 #define KF_OP_F 0
 #define KF_OP_G 1
 #define KF_OP_P 2
+#define KF_OP_F_BASE 3
+#define KF_OP_P_BASE 4
+#define KF_OP_G_BASE 5
 
 /*
  * Scratch bytes kf_F / kf_G / kf_P need for these shapes (0 is possible).
@@ -152,6 +155,35 @@ int kf_G(const kf_basis *basis, int dtype, int64_t batch, int64_t n_in, int64_t 
  */
 int kf_P(const kf_basis *basis, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void *x,
          const void *g, const void *c, void *p, float *h, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * The KANLinear layer with its SiLU base branch and bias fused into the contractions: what
+ * kanforge/torch/layers.py:185-191 computes as the spline part (_F) plus
+ * F.linear(silu(x), base_weight) plus bias, and what autograd then computes for it.
+ *
+ * kf_base_fused(op, ...) is 1 when the entry point of op (KF_OP_F_BASE, KF_OP_P_BASE,
+ * KF_OP_G_BASE) takes the layer, 0 when the caller composes kf_F / kf_P / kf_G with its own base
+ * branch instead, negative for an invalid descriptor. It takes bf16 Chebyshev plans on their
+ * contraction kernels (F: n_t of 9 or an even count >= 6, not the narrow streaming routes).
+ * Workspace: kf_workspace_bytes(KF_OP_*_BASE, ...).
+ *
+ * kf_F_base: y = F_0(x, c) + silu(x) base_w^T + bias, basis of order 0; base_w (n_out, n_in),
+ *   bias (n_out) or NULL. silu(x) is one more feature per input in the same contraction.
+ * kf_P_base: p = P_m(x, g, c) + silu'(x) * (g base_w), basis of order m >= 1 (the x-gradient's
+ *   descriptor, m = 1); g (batch, n_out).
+ * kf_G_base: dc = G_0(x, g), dbase_w = g^T silu(x) (n_out, n_in), dbias = sum_b g (n_out),
+ *   basis of order 0; each output may be NULL (not wanted).
+ */
+int kf_base_fused(int op, const kf_basis *basis, int dtype, int64_t batch, int64_t n_in, int64_t n_out);
+int kf_F_base(const kf_basis *basis, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void *x,
+              const void *c, const void *base_w, const void *bias, void *y, void *workspace, size_t workspace_bytes,
+              void *stream);
+int kf_P_base(const kf_basis *basis, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void *x,
+              const void *g, const void *c, const void *base_w, void *p, void *workspace, size_t workspace_bytes,
+              void *stream);
+int kf_G_base(const kf_basis *basis, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void *x,
+              const void *g, void *dc, void *dbase_w, void *dbias, void *workspace, size_t workspace_bytes,
+              void *stream);
 
 /*
  * phi[b,i,k] = phi_k^(m)(x[b,i]), out (batch, n_in, size) in dtype.

@@ -169,7 +169,10 @@ inline bool f_uses_rega(const kf_basis* b, int dtype) { return b->kind == KF_KIN
 // odd feature counts with an unpadded, unrolled variant
 inline bool f_rega_unpadded(int n_t, int64_t n_in) { return n_t == 9; }
 
-inline WsF ws_f(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, bool has_w) {
+// base: the fused SiLU base branch (kf_F_base): the register-A kernel's chunks run T_1 ..
+// T_{n_t - 1} and silu(x) (n_tp = n_t, silu(x) in the wz buffer).
+inline WsF ws_f(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, bool has_w,
+                bool base = false) {
   WsF w;
   const bool rega = f_uses_rega(b, dtype);
   w.cfg = rega ? F_REGA : pick_f_cfg(batch, n_out);
@@ -186,9 +189,10 @@ inline WsF ws_f(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64
   // the register-A kernel needs chunks of at least RA_NBUF / 2 (and 2) stages
   const int min_tp = RA_NBUF < 4 ? 4 : RA_NBUF;
   if (rega && w.n_tp < min_tp) w.n_tp = min_tp;
+  if (base) w.n_tp = n_run + 1;
   w.cfm = align256((size_t)w.n_tp * w.OUTP * w.INP * es);
   w.z = cheb ? align256((size_t)w.BP * w.INP * sizeof(float)) : 0;
-  w.wz = cheb && has_w ? align256((size_t)w.BP * w.INP * sizeof(float)) : 0;
+  w.wz = cheb && (has_w || base) ? align256((size_t)w.BP * w.INP * sizeof(float)) : 0;
   w.phi = cheb ? 0 : align256((size_t)w.BP * w.n_tp * w.INP * es);
   w.part0 = w.skip0 ? align256((size_t)(w.INP / 16) * w.OUTP * sizeof(float)) : 0;
   w.ysum = w.skip0 ? align256((size_t)w.OUTP * sizeof(float)) : 0;
@@ -288,7 +292,10 @@ struct WsG {
 constexpr size_t kGSplitBytes = size_t(256) << 20;  // cap of the split partial sums
 constexpr long kGSplitMax = 64;                      // cap of the batch splits
 constexpr int kGdmaFW = 4, kGdmaRows = 2 * kGdmaFW * 32;  // G on p_dma_kernel: phiT rows per tile
-inline WsG ws_g(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, bool has_w) {
+// base: kf_G_base (the batch padded to whole 64-row stages of the GEMM core, which contracts
+// gT with silu(x)^T over it)
+inline WsG ws_g(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, bool has_w,
+                bool base = false) {
   WsG w;
   if (bspline_sparse(b, dtype)) {
     w = WsG{};
@@ -316,7 +323,7 @@ inline WsG ws_g(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64
   const int bm = w.g96 ? 192 : 2 * g_tm(fw) * 32;
   const int eps = w.g96 ? 32 : g_rb(fw) / elt_size(dtype);
   w.OUTP = round_up(n_out, bm);
-  w.BP = round_up(batch, eps);
+  w.BP = round_up(batch, base ? 64 : eps);
   const bool flat = b->kind == KF_KIND_RATIONAL;  // g_kernel's flat tiles: 2 FW x 32 inputs
   w.INP = round_up(n_in, w.g96 ? 48 : flat ? 64 * fw : 32);
   const bool cheb = cheb_kind && !w.pre;
@@ -352,6 +359,53 @@ inline WsG ws_g(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64
   w.gemm = dtype == KF_BF16 && b->kind == KF_KIND_RATIONAL ? gemm_nt_workspace(n_out, n_in, w.BP) : 0;
   if (dtype == KF_BF16 && b->kind == KF_KIND_BSPLINE) w.gemm = gemm_nt_workspace(n_out, n_in * b->size, w.BP);
   w.total = w.gt + w.zt + w.wt + w.part + w.colsum + w.phit + w.zpart + w.gemm;
+  return w;
+}
+
+// The fused SiLU base branch (kf_F_base, kf_P_base, kf_G_base) rides the bf16 Chebyshev kernels:
+// F on the register-A kernel with silu(x) as the last feature of every chunk (T_0 taken out, so
+// n_t features a chunk: 9, or an even count of at least 6); layers narrow enough for F's
+// streaming routes keep those. P on p8_kernel (the order-1 descriptor), G on g96_kernel.
+inline bool f_base_route(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out) {
+  if (!f_uses_rega(b, dtype) || b->order != 0) return false;
+  if (!(b->n_t == 9 || (b->n_t % 2 == 0 && b->n_t >= 6))) return false;
+  const bool narrow = n_out <= 8 || (n_in <= 4 && n_in * b->size <= 64 && n_in * 16 <= 64);
+  return !(batch >= 1024 && narrow);
+}
+inline bool p_base_route(const kf_basis* b1, int dtype, int64_t batch, int64_t n_in, int64_t n_out) {
+  return b1->kind == KF_KIND_CHEB && dtype == KF_BF16 && b1->order >= 1 && ws_p(b1, dtype, batch, n_in, n_out).p8;
+}
+inline bool g_base_route(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out) {
+  if (b->kind != KF_KIND_CHEB || dtype != KF_BF16 || b->order != 0) return false;
+  const WsG w = ws_g(b, dtype, batch, n_in, n_out, false, true);
+  return w.g96 && w.skip0 && !w.pre;
+}
+// workspace of kf_P_base: P's, one more coefficient row (W^T), hb = g W (float32) and the
+// GEMM core's split partial sums
+struct WsPB {
+  WsP p;
+  size_t cfmt, hb, gemm, total;
+};
+inline WsPB ws_p_base(const kf_basis* b1, int dtype, int64_t batch, int64_t n_in, int64_t n_out) {
+  WsPB w;
+  w.p = ws_p(b1, dtype, batch, n_in, n_out);
+  w.cfmt = align256((size_t)(w.p.ntb + 1) * w.p.INP * w.p.OUTP * elt_size(dtype));
+  w.hb = align256((size_t)batch * n_in * sizeof(float));
+  w.gemm = gemm_nt_workspace(batch, n_in, w.p.OUTP);
+  w.total = w.cfmt + w.p.gpad + w.hb + w.gemm;
+  return w;
+}
+// workspace of kf_G_base: G's, silu(x)^T (INP, BP) in bf16 and the GEMM core's partial sums
+struct WsGB {
+  WsG g;
+  size_t st, gemm, total;
+};
+inline WsGB ws_g_base(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out) {
+  WsGB w;
+  w.g = ws_g(b, dtype, batch, n_in, n_out, false, true);
+  w.st = align256((size_t)w.g.INP * w.g.BP * elt_size(dtype));
+  w.gemm = gemm_nt_workspace(n_out, n_in, w.g.BP);
+  w.total = w.g.total + w.st + w.gemm;
   return w;
 }
 
@@ -440,10 +494,10 @@ bool rows_vec(int64_t n, const void* p) {
 // n_feat >= n_t features (zeros past n_t)
 template <typename T>
 int launch_permute(const KBasis& kb, int64_t n_out, int64_t n_in, int64_t OUTP, int64_t INP, int n_feat, const void* c,
-                   void* out, int fmt, hipStream_t s, int j_first = 0, float* part0 = nullptr) {
+                   void* out, int fmt, hipStream_t s, int j_first = 0, float* part0 = nullptr, const void* bw = nullptr) {
   if (OUTP % 32 || INP % 16 || !aligned16(out)) return fail(KF_EINVAL, "permute: workspace layout not aligned");
   dim3 grid((unsigned)(OUTP / 32), (unsigned)(INP / 16));
-  const size_t rows = (size_t)32 * (16 * kb.K + 1), tile = (size_t)(n_feat + j_first) * 16 * kPermTS;
+  const size_t rows = (size_t)32 * (16 * kb.K + 1), tile = (size_t)(n_feat + j_first + (bw ? 1 : 0)) * 16 * kPermTS;
   const size_t lds = (rows > tile ? rows : tile) * sizeof(float);
   KFoldT ft;
   for (int j = 0; j < KF_MAX_NT; ++j)
@@ -460,7 +514,7 @@ int launch_permute(const KBasis& kb, int64_t n_out, int64_t n_in, int64_t OUTP, 
               : kb.K <= 12 ? pick(std::integral_constant<int, 12>())
                            : pick(std::integral_constant<int, KF_MAX_K>());
   hipLaunchKernelGGL(kern, grid, dim3(kThreads), lds, s, ft, kb.K, kb.n_t, (int)n_out, (int)n_in, (int)OUTP, (int)INP,
-                     n_feat, j_first, vin, (const T*)c, (T*)out, part0);
+                     n_feat, j_first, vin, (const T*)c, (const T*)bw, (T*)out, part0);
   return check_launch("permute_coef");
 }
 

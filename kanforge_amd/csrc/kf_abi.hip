@@ -93,7 +93,23 @@ size_t kf_workspace_bytes(int op, const kf_basis* b, int dtype, int64_t batch, i
       const size_t a = ws_g(b, dtype, batch, n_in, n_out, true).total, u = ws_g(b, dtype, batch, n_in, n_out, false).total;
       return a > u ? a : u;
     }
+    case KF_OP_F_BASE: return f_base_route(b, dtype, batch, n_in, n_out) ? ws_f(b, dtype, batch, n_in, n_out, false, true).total : 0;
+    case KF_OP_P_BASE: return p_base_route(b, dtype, batch, n_in, n_out) ? ws_p_base(b, dtype, batch, n_in, n_out).total : 0;
+    case KF_OP_G_BASE: return g_base_route(b, dtype, batch, n_in, n_out) ? ws_g_base(b, dtype, batch, n_in, n_out).total : 0;
     default: return 0;
+  }
+}
+
+int kf_base_fused(int op, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out) {
+  g_err.clear();
+  int rc = validate_common(b, dtype, batch, n_in, n_out);
+  if (rc) return rc;
+  if (batch <= 0 || n_in <= 0 || n_out <= 0) return 0;
+  switch (op) {
+    case KF_OP_F_BASE: return f_base_route(b, dtype, batch, n_in, n_out) ? 1 : 0;
+    case KF_OP_P_BASE: return p_base_route(b, dtype, batch, n_in, n_out) ? 1 : 0;
+    case KF_OP_G_BASE: return g_base_route(b, dtype, batch, n_in, n_out) ? 1 : 0;
+    default: return fail(KF_EINVAL, "kf_base_fused: op %d is not one of KF_OP_F_BASE, KF_OP_P_BASE, KF_OP_G_BASE", op);
   }
 }
 

@@ -37,19 +37,23 @@ int launch_f_t(const WsF& L, int64_t batch, int64_t n_out, int n_t, const float*
   return check_launch("F");
 }
 
-template <bool HAS_W, bool SKIP0>
+template <bool HAS_W, bool SKIP0, bool BASE = false>
 int launch_f_rega(const WsF& L, int64_t batch, int64_t n_out, const float* zc, const float* wc, const void* cfm,
                   const float* ysum, void* y, hipStream_t s) {
   const int n_m = (int)(L.BP / RA_BM), n_n = (int)(L.OUTP / RA_BN);
-  // RA_NBUF stage buffers of 2 features, z (and w) of two chunks
+  // RA_NBUF stage buffers of 2 features, z (and w, or silu(x)) of two chunks
   // (reused by the epilogue's bf16 staging of each wave's output tile: RA_BM rows of
   // RA_BN / RA_WN * 2 + 16 bytes per column group)
-  const size_t lds_ops = (size_t)RA_NBUF * 2 * RA_BN * 32 + (size_t)(HAS_W ? 4 : 2) * RA_BM * 64;
+  const size_t lds_ops = (size_t)RA_NBUF * 2 * RA_BN * 32 + (size_t)(HAS_W || BASE ? 4 : 2) * RA_BM * 64;
   const size_t lds_epi = (size_t)RA_WN * RA_BM * (RA_BN / RA_WN * 2 + 16);
   const size_t lds = lds_ops > lds_epi ? lds_ops : lds_epi;
   const int vout = n_out % 8 == 0 && aligned16(y);
   constexpr int TNW = RA_TN / RA_WN;
-  auto kern = L.n_tp == 9   ? f_rega_kernel<HAS_W, 9, RA_TM, TNW, RA_NBUF, SKIP0, RA_WN, RA_NWM>
+  if (BASE && !(L.n_tp == 9 || (L.n_tp % 2 == 0 && L.n_tp >= 6)))
+    return fail(KF_EINVAL, "F: the base feature needs chunks of 9 or an even count >= 6 features");
+  auto kern = BASE          ? (L.n_tp == 9 ? f_rega_kernel<HAS_W, 9, RA_TM, TNW, RA_NBUF, SKIP0, RA_WN, RA_NWM, BASE>
+                                           : f_rega_kernel<HAS_W, 0, RA_TM, TNW, RA_NBUF, SKIP0, RA_WN, RA_NWM, BASE>)
+              : L.n_tp == 9 ? f_rega_kernel<HAS_W, 9, RA_TM, TNW, RA_NBUF, SKIP0, RA_WN, RA_NWM>
               : L.n_tp == 8 ? f_rega_kernel<HAS_W, 8, RA_TM, TNW, RA_NBUF, SKIP0, RA_WN, RA_NWM>
                             : f_rega_kernel<HAS_W, 0, RA_TM, TNW, RA_NBUF, SKIP0, RA_WN, RA_NWM>;
   if (!reserve_lds((const void*)kern, lds))
@@ -223,7 +227,7 @@ int run_F(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
     const int vin = rows_vec<T>(n_in, x) && rows_vec<T>(n_in, w);
     hipLaunchKernelGGL(zmapc_kernel<T>, dim3((unsigned)(blocks + sblocks)), dim3(kThreads), 0, s, (int)batch,
                        (int)n_in, (int)L.BP, (int)L.INP, kb.input_map, vin, (const T*)x, (const T*)w, z, wz,
-                       (int)blocks, (int)(L.INP / 16), (int)L.OUTP, part0, ysum);
+                       (int)blocks, (int)(L.INP / 16), (int)L.OUTP, part0, ysum, 0, (const T*)nullptr, 0);
     rc = check_launch("zmapc");
     if (rc) return rc;
     if (weighted) return launch_f_rega<true, false>(L, batch, n_out, z, wz, cfm, nullptr, y, s);
@@ -312,6 +316,35 @@ int scratch_of_current_device(void** out) {
   *out = g_scratch_ptr[dev];
   return KF_OK;
 }
+// The layer's forward with its SiLU base branch and bias in the register-A contraction:
+// coefficients folded into C16 blocks with the base weights as every chunk's last block, z and
+// silu(x) in the chunked layout, the T_0 sums plus the bias as the per-output constant.
+int run_F_base(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out,
+               const void* x, const void* c, const void* bw, const void* bias, void* y, void* ws, hipStream_t s) {
+  const WsF L = ws_f(b, dtype, batch, n_in, n_out, false, true);
+  char* base = (char*)ws;
+  void* cfm = base;
+  float* z = (float*)(base + L.cfm);
+  float* sz = (float*)(base + L.cfm + L.z);
+  float* part0 = (float*)(base + L.cfm + L.z + L.wz + L.phi);
+  float* ysum = (float*)(base + L.cfm + L.z + L.wz + L.phi + L.part0);
+  if (L.cfg != F_REGA || !L.skip0 || L.INP % 16 || L.BP % 32)
+    return fail(KF_EINVAL, "kf_F_base: layer not on the register-A route");
+  int rc = launch_permute<bf16>(kb, n_out, n_in, L.OUTP, L.INP, L.n_tp - 1, c, cfm, kPermC16, s, 1, part0, bw);
+  if (rc) return rc;
+  long n = (L.INP + 63) / 64 * L.BP * 8;
+  long blocks = (n + kThreads - 1) / kThreads;
+  if (blocks > 65535 * 4) blocks = 65535 * 4;
+  const long sblocks = (L.OUTP + 7) / 8;
+  const int vin = rows_vec<bf16>(n_in, x);
+  hipLaunchKernelGGL(zmapc_kernel<bf16>, dim3((unsigned)(blocks + sblocks)), dim3(kThreads), 0, s, (int)batch,
+                     (int)n_in, (int)L.BP, (int)L.INP, kb.input_map, vin, (const bf16*)x, (const bf16*)nullptr, z, sz,
+                     (int)blocks, (int)(L.INP / 16), (int)L.OUTP, part0, ysum, 1, (const bf16*)bias, (int)n_out);
+  rc = check_launch("zmapc");
+  if (rc) return rc;
+  return launch_f_rega<false, true, true>(L, batch, n_out, z, sz, cfm, ysum, y, s);
+}
+
 }  // namespace
 
 extern "C" {
@@ -354,6 +387,25 @@ int kf_F_noalloc(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int6
   KBasis kb = to_kbasis(b);
   if (dtype == KF_BF16) return run_F<bf16>(kb, b, dtype, batch, n_in, n_out, x, w, c, y, ws, s);
   return run_F<float>(kb, b, dtype, batch, n_in, n_out, x, w, c, y, ws, s);
+}
+
+int kf_F_base(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* c,
+              const void* base_w, const void* bias, void* y, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err.clear();
+  int rc = validate_common(b, dtype, batch, n_in, n_out);
+  if (rc) return rc;
+  if (batch == 0 || n_out == 0) return KF_OK;
+  if (n_in == 0) return fail(KF_EINVAL, "kf_F_base: no inputs");
+  if (!x || !c || !base_w || !y) return fail(KF_EINVAL, "kf_F_base: NULL array");
+  if (!f_base_route(b, dtype, batch, n_in, n_out))
+    return fail(KF_EUNSUPPORTED, "kf_F_base: this layer does not run the fused base branch (kf_base_fused)");
+  const size_t need = ws_f(b, dtype, batch, n_in, n_out, false, true).total;
+  if (!workspace || workspace_bytes < need)
+    return fail(KF_EWORKSPACE, "kf_F_base: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  if (reinterpret_cast<uintptr_t>(workspace) & 255)
+    return fail(KF_EWORKSPACE, "kf_F_base: workspace must be 256-byte aligned");
+  KBasis kb = to_kbasis(b);
+  return run_F_base(kb, b, dtype, batch, n_in, n_out, x, c, base_w, bias, y, workspace, (hipStream_t)stream);
 }
 
 }  // extern "C"

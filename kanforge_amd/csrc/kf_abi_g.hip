@@ -141,7 +141,7 @@ int run_G(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
     hipLaunchKernelGGL(zmapT_kernel<T>, zg, dim3(kThreads), (size_t)(wt ? 2 : 1) * 64 * 65 * sizeof(float), s,
                        (int)batch, (int)n_in, (int)L.BP, (int)L.INP, kb.input_map,
                        (int)(rows_vec<T>(n_in, x) && rows_vec<T>(n_in, w)), (const T*)x, (const T*)w, zt, wt,
-                       (int)((L.BP + 63) / 64), (int)L.OUTP, part, colsum);
+                       (int)((L.BP + 63) / 64), (int)L.OUTP, part, colsum, (T*)nullptr, (T*)nullptr, 0);
     rc = check_launch("zmapT");
     if (rc) return rc;
     if (L.g96) {
@@ -191,6 +191,43 @@ int run_G(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
   if (L.gdma) return launch_g_dma<T>(L, s, kb, n_in, n_out, gt, phit, dc);
   return launch_g_cfg<T, false>(L, s, kb, batch, n_in, n_out, phit, zpart, nullptr, nullptr, gt, dc);
 }
+// The layer's parameter gradients with its SiLU base branch and bias: the g transpose (with its
+// column sums: the T_0 constant and the bias gradient), z^T and silu(x)^T in one prepass, G on
+// g96_kernel, and the base weights' gradient gT silu(x)^T on the GEMM core. dc, dbw and dbias may
+// each be NULL (not wanted).
+int run_G_base(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out,
+               const void* x, const void* g, void* dc, void* dbw, void* dbias, void* ws, hipStream_t s) {
+  const WsGB LB = ws_g_base(b, dtype, batch, n_in, n_out);
+  const WsG& L = LB.g;
+  char* base = (char*)ws;
+  void* gt = base;
+  float* zt = (float*)(base + L.gt);
+  float* part = (float*)(base + L.gt + L.zt + L.wt);
+  float* colsum = (float*)(base + L.gt + L.zt + L.wt + L.part);
+  bf16* st = dbw ? (bf16*)(base + L.total) : nullptr;
+  void* gws = base + L.total + LB.st;
+  if (!L.g96 || !L.skip0 || L.pre || L.BP % 64 || !aligned16(gt)) return fail(KF_EINVAL, "kf_G_base: layer not on g96");
+  dim3 tg((unsigned)((L.OUTP + 63) / 64), (unsigned)((L.BP + 63) / 64));
+  hipLaunchKernelGGL(transpose_kernel<bf16>, tg, dim3(kThreads), 0, s, (int)batch, (int)n_out, (int)L.BP, (int)L.OUTP,
+                     (int)rows_vec<bf16>(n_out, g), (const bf16*)g, (bf16*)gt, part);
+  int rc = check_launch("transpose");
+  if (rc) return rc;
+  const unsigned gx = (unsigned)((L.INP + 63) / 64), sblocks = (unsigned)((L.OUTP + 7) / 8);
+  dim3 zg(gx, (unsigned)((L.BP + 63) / 64) + (sblocks + gx - 1) / gx);
+  hipLaunchKernelGGL(zmapT_kernel<bf16>, zg, dim3(kThreads), (size_t)(st ? 2 : 1) * 64 * 65 * sizeof(float), s,
+                     (int)batch, (int)n_in, (int)L.BP, (int)L.INP, kb.input_map, (int)rows_vec<bf16>(n_in, x),
+                     (const bf16*)x, (const bf16*)nullptr, zt, (float*)nullptr, (int)((L.BP + 63) / 64), (int)L.OUTP,
+                     part, colsum, st, (bf16*)dbias, (int)n_out);
+  rc = check_launch("zmapT");
+  if (rc) return rc;
+  if (dc) {
+    rc = launch_g96<true>(L, s, kb, batch, n_in, n_out, zt, nullptr, gt, colsum, dc);
+    if (rc) return rc;
+  }
+  if (dbw) return gemm_nt(n_out, n_in, L.BP, gt, L.BP, st, L.BP, dbw, n_in, false, gws, LB.gemm, s);
+  return KF_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -213,6 +250,26 @@ int kf_G(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
   KBasis kb = to_kbasis(b);
   if (dtype == KF_BF16) return run_G<bf16>(kb, b, dtype, batch, n_in, n_out, x, g, w, dc, workspace, s);
   return run_G<float>(kb, b, dtype, batch, n_in, n_out, x, g, w, dc, workspace, s);
+}
+
+int kf_G_base(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* g,
+              void* dc, void* dbase_w, void* dbias, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err.clear();
+  int rc = validate_common(b, dtype, batch, n_in, n_out);
+  if (rc) return rc;
+  if (n_in == 0 || n_out == 0) return KF_OK;
+  if (batch == 0) return fail(KF_EINVAL, "kf_G_base: empty batch");
+  if (!x || !g) return fail(KF_EINVAL, "kf_G_base: NULL array");
+  if (!dc && !dbase_w && !dbias) return KF_OK;
+  if (!g_base_route(b, dtype, batch, n_in, n_out))
+    return fail(KF_EUNSUPPORTED, "kf_G_base: this layer does not run the fused base branch (kf_base_fused)");
+  const size_t need = ws_g_base(b, dtype, batch, n_in, n_out).total;
+  if (!workspace || workspace_bytes < need)
+    return fail(KF_EWORKSPACE, "kf_G_base: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  if (reinterpret_cast<uintptr_t>(workspace) & 255)
+    return fail(KF_EWORKSPACE, "kf_G_base: workspace must be 256-byte aligned");
+  KBasis kb = to_kbasis(b);
+  return run_G_base(kb, b, dtype, batch, n_in, n_out, x, g, dc, dbase_w, dbias, workspace, (hipStream_t)stream);
 }
 
 }  // extern "C"

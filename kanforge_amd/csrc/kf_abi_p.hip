@@ -58,9 +58,9 @@ int launch_p_dma_kind(const WsP& L, hipStream_t s, const KBasis& kb, int64_t bat
   return check_launch("P");
 }
 
-template <int KIND, int NF, int TN, int RB>
+template <int KIND, int NF, int TN, int RB, bool BASE = false>
 int launch_p8(const WsP& L, hipStream_t s, const KBasis& kb, int64_t batch, int64_t n_in, const void* x, const void* g,
-              int gstride, const void* cfmt, void* p) {
+              int gstride, const void* cfmt, void* p, const float* hb = nullptr) {
   constexpr int TI = 128 * TN / NF, RPASS = TN == 2 ? 128 : 64;
   // B-splines: the tile's knot rows and (t_0, 1/h) per input after the sums
   const size_t knots = KIND == KF_KIND_BSPLINE ? (size_t)TI * (2 * kb.n_knots + 2 * kb.spline_k + 2) * 4 : 0;
@@ -68,13 +68,15 @@ int launch_p8(const WsP& L, hipStream_t s, const KBasis& kb, int64_t batch, int6
   const size_t lds = lds_ops > lds_epi ? lds_ops : lds_epi;
   // cubic B-splines on even knots (the common case): the support without the general-knot path
   const bool even = KIND == KF_KIND_BSPLINE && kb.knots_uniform && kb.n_knots >= 4;
-  auto kern = even ? p8_kernel<KIND, NF, TN, RB, 3, true> : p8_kernel<KIND, NF, TN, RB>;
+  auto kern = BASE ? p8_kernel<KIND, NF, TN, RB, 3, false, BASE>
+              : even ? p8_kernel<KIND, NF, TN, RB, 3, true> : p8_kernel<KIND, NF, TN, RB>;
+  if (BASE && (KIND == KF_KIND_BSPLINE || !hb)) return fail(KF_EINVAL, "P: the base term needs hb");
   if (L.INP % TI || L.OUTP % (RB / 2)) return fail(KF_EINVAL, "P: workspace layout not aligned");
   if (!reserve_lds((const void*)kern, lds))
     return fail(KF_ELAUNCH, "P: cannot reserve %zu bytes of LDS", lds);
   const int n_m = (int)((batch + 255) / 256), n_n = (int)(L.INP / TI);
   hipLaunchKernelGGL(kern, dim3(n_m * n_n), dim3(512), lds, s, kb, (int)batch, (int)n_in, (int)L.INP, (int)L.OUTP,
-                     (const bf16*)x, (const bf16*)g, gstride, (const bf16*)cfmt, (bf16*)p);
+                     (const bf16*)x, (const bf16*)g, gstride, (const bf16*)cfmt, (bf16*)p, hb);
   return check_launch("P");
 }
 
@@ -164,6 +166,40 @@ bool rational_bwd_fuses(const KBasis& kb, int dtype, int64_t n_in, const void* x
   return dtype == KF_BF16 && kb.order == 0 && rational_fast(kb, n_in) && aligned16(x) && aligned16(p) &&
          (!w || aligned16(w)) && p_uses_dma(fw_index(1));
 }
+// The layer's input gradient with its SiLU base branch: the coefficients folded feature-major
+// with W^T as one more row, hb = g W on the GEMM core (float32), then p8_kernel, whose epilogue
+// adds silu'(x) hb.
+int run_P_base(const KBasis& kb, const kf_basis* b1, int dtype, int64_t batch, int64_t n_in, int64_t n_out,
+               const void* x, const void* g, const void* c, const void* bw, void* p, void* ws, hipStream_t s) {
+  const WsPB LB = ws_p_base(b1, dtype, batch, n_in, n_out);
+  const WsP& L = LB.p;
+  char* base = (char*)ws;
+  void* cfmt = base;
+  float* hb = (float*)(base + LB.cfmt + L.gpad);
+  void* gws = base + LB.cfmt + L.gpad + LB.hb;
+  int rc = launch_permute<bf16>(kb, n_out, n_in, L.OUTP, L.INP, L.ntb, c, cfmt, kPermFMT, s, 0, nullptr, bw);
+  if (rc) return rc;
+  const void* ga = g;
+  int gstride = (int)n_out;
+  if (p_needs_gpad(n_out, dtype) || (reinterpret_cast<uintptr_t>(g) & 15) != 0) {
+    if (!L.gpad) return fail(KF_EINVAL, "kf_P_base: g must be 16-byte aligned");
+    void* gp = base + LB.cfmt;
+    long n = (long)batch * L.OUTP;
+    long blocks = (n + kThreads - 1) / kThreads;
+    if (blocks > 65535 * 4) blocks = 65535 * 4;
+    hipLaunchKernelGGL(pad_cols_kernel<bf16>, dim3((unsigned)blocks), dim3(kThreads), 0, s, (int)batch, (int)n_out,
+                       (int)L.OUTP, (const bf16*)g, (bf16*)gp);
+    rc = check_launch("pad_cols");
+    if (rc) return rc;
+    ga = gp;
+    gstride = (int)L.OUTP;
+  }
+  const bf16* wt = (const bf16*)cfmt + (size_t)L.ntb * L.INP * L.OUTP;  // W^T (INP, OUTP), zero padded
+  rc = gemm_nt(batch, n_in, L.OUTP, ga, gstride, wt, L.OUTP, hb, n_in, true, gws, LB.gemm, s);
+  if (rc) return rc;
+  return launch_p8<KF_KIND_CHEB, 8, 3, 128, true>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p, hb);
+}
+
 }  // namespace
 
 extern "C" {
@@ -241,6 +277,25 @@ int kf_P(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_ou
   KBasis kb = to_kbasis(b);
   if (dtype == KF_BF16) return run_P<bf16>(kb, b, dtype, batch, n_in, n_out, x, g, c, p, h, workspace, s);
   return run_P<float>(kb, b, dtype, batch, n_in, n_out, x, g, c, p, h, workspace, s);
+}
+
+int kf_P_base(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* g,
+              const void* c, const void* base_w, void* p, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err.clear();
+  int rc = validate_common(b, dtype, batch, n_in, n_out);
+  if (rc) return rc;
+  if (batch == 0 || n_in == 0) return KF_OK;
+  if (n_out == 0) return fail(KF_EINVAL, "kf_P_base: no outputs");
+  if (!x || !g || !c || !base_w || !p) return fail(KF_EINVAL, "kf_P_base: NULL array");
+  if (!p_base_route(b, dtype, batch, n_in, n_out))
+    return fail(KF_EUNSUPPORTED, "kf_P_base: this layer does not run the fused base branch (kf_base_fused)");
+  const size_t need = ws_p_base(b, dtype, batch, n_in, n_out).total;
+  if (!workspace || workspace_bytes < need)
+    return fail(KF_EWORKSPACE, "kf_P_base: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  if (reinterpret_cast<uintptr_t>(workspace) & 255)
+    return fail(KF_EWORKSPACE, "kf_P_base: workspace must be 256-byte aligned");
+  KBasis kb = to_kbasis(b);
+  return run_P_base(kb, b, dtype, batch, n_in, n_out, x, g, c, base_w, p, workspace, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -65,6 +65,12 @@ __device__ __forceinline__ float fast_tanh(float x) {
 }
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
+// silu(x) = x s and silu'(x) = s (1 + x (1 - s)), s = sigmoid(x)
+__device__ __forceinline__ float silu_f(float x) { return x * sigmoidf_(x); }
+__device__ __forceinline__ float dsilu_f(float x) {
+  const float s = sigmoidf_(x);
+  return s * fmaf(x, 1.f - s, 1.f);
+}
 
 // d^m/dx^m silu(x) = x p_m(s) + m p_{m-1}(s), s = sigmoid(x), where
 // p_0 = s and p_{j+1} = p_j'(s) (s - s^2). The polynomial coefficients are

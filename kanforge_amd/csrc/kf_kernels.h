@@ -26,7 +26,10 @@ constexpr int kThreads = 256;
 //   kPermC16: out[i/16][j][o][i%16]    (INP/16, n_t, OUTP, 16)
 //             every (16-input chunk, feature) block contiguous: B operand
 //             of the register-A F kernel, whose stages read whole blocks
-// out[j] = sum_k c[o,i,k] fold[k][j]. A block folds 32 outputs x 16 inputs:
+// out[j] = sum_k c[o,i,k] fold[k][j]. With bw (n_out, n_in) given, one more
+// feature row follows the n_feat folded ones: out[n_feat] = bw[o][i], unfolded
+// (the SiLU base branch's weights as an extra feature column).
+// A block folds 32 outputs x 16 inputs:
 // the 16 K coefficients of one output are contiguous in c and come in with
 // 16-byte loads when vin is set (n_in a multiple of 16, rows 16-byte
 // aligned), the folded tile goes out with 16-byte stores (OUTP a multiple of
@@ -42,10 +45,10 @@ struct KFoldT {
 template <typename T, int FMT, int KB>  // KB >= K: basis functions the fold loop runs over
 __global__ __launch_bounds__(kThreads) void permute_coef_kernel(KFoldT ft, int K, int n_t_fold, int OUT, int IN,
                                                                 int OUTP, int INP, int n_feat, int j_first, int vin,
-                                                                const T* __restrict__ c, T* __restrict__ out,
-                                                                float* __restrict__ part0) {
+                                                                const T* __restrict__ c, const T* __restrict__ bw,
+                                                                T* __restrict__ out, float* __restrict__ part0) {
   constexpr int VW = 16 / (int)sizeof(T);
-  // crow [32][16K + 1], then (aliased) tile [n_feat + j_first][16][kPermTS]
+  // crow [32][16K + 1], then (aliased) tile [n_feat + j_first (+ 1 with bw)][16][kPermTS]
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
   float* smem = reinterpret_cast<float*>(smem_raw);
   const int n_all = n_feat + j_first;  // features past n_t_fold get zero fold columns
@@ -53,6 +56,15 @@ __global__ __launch_bounds__(kThreads) void permute_coef_kernel(KFoldT ft, int K
   const int ob = blockIdx.x, ib = blockIdx.y;
   const int o0 = ob * 32, i0 = ib * 16;
   const int t = threadIdx.x;
+  // the base weights of this thread's two edges (ol = t / 16 + 16 rep, il = t % 16), loaded first
+  float bwv[2] = {0.f, 0.f};
+  if (bw) {
+#pragma unroll
+    for (int rep = 0; rep < 2; ++rep) {
+      const int o = o0 + t / 16 + rep * 16, i = i0 + t % 16;
+      if (o < OUT && i < IN) bwv[rep] = to_f32(bw[(size_t)o * IN + i]);
+    }
+  }
   if (vin) {
     // the block's rows in rounds of 4 x 256 chunks, each round's loads issued before any store
     // (K <= 16: one round; branch-free loads stay in flight together)
@@ -104,6 +116,10 @@ __global__ __launch_bounds__(kThreads) void permute_coef_kernel(KFoldT ft, int K
       tile[(j * 16 + il) * kPermTS + t / 16 + rep * 16] = live ? acc : 0.f;
     }
   }
+  if (bw) {
+#pragma unroll
+    for (int rep = 0; rep < 2; ++rep) tile[(n_all * 16 + il) * kPermTS + t / 16 + rep * 16] = bwv[rep];
+  }
   __syncthreads();
   // feature 0 left out (j_first = 1): its partial sums over the block's 16 inputs per output
   if (j_first && t < 32 && o0 + t < OUTP) {
@@ -112,7 +128,7 @@ __global__ __launch_bounds__(kThreads) void permute_coef_kernel(KFoldT ft, int K
     part0[(size_t)ib * OUTP + o0 + t] = sum;
   }
   const float* tf = tile + j_first * 16 * kPermTS;
-  const int n_t = n_feat;
+  const int n_t = n_feat + (bw ? 1 : 0);
   if (FMT == kPermFMT) {
     // out[j][i][o]: rows (j, i) of 32 outputs, 32 / VW lanes each
     constexpr int LR = 32 / VW;
@@ -143,9 +159,14 @@ __global__ __launch_bounds__(kThreads) void permute_coef_kernel(KFoldT ft, int K
 // sums[o] = sum over p < n_parts of part[p][o] for the 8 outputs of block blk:
 // the per-output constant of a left-out feature 0 (fixed summation order); 32
 // groups of parts (all loads of a thread in flight at once), reduced through
-// LDS. Run by extra blocks of the tanh-map prepass launches.
+// LDS. Run by extra blocks of the tanh-map prepass launches. With add given,
+// sums[o] also gets add[o] (a bias folded into the constant); with copy given,
+// the total also goes to copy[o] in T (the bias gradient); both arrays hold the
+// n_real <= n outputs that exist.
+template <typename T>
 __device__ __forceinline__ void sum_parts_block(int blk, int n_parts, int n, const float* __restrict__ part,
-                                                float* __restrict__ sums) {
+                                                float* __restrict__ sums, const T* __restrict__ add = nullptr,
+                                                T* __restrict__ copy = nullptr, int n_real = 0) {
   __shared__ float red[32][9];
   const int ol = threadIdx.x % 8, pg = threadIdx.x / 8;
   const int o = blk * 8 + ol;
@@ -166,7 +187,8 @@ __device__ __forceinline__ void sum_parts_block(int blk, int n_parts, int n, con
     float tot = 0.f;
 #pragma unroll
     for (int g = 0; g < 32; ++g) tot += red[g][ol];
-    sums[o] = tot;
+    sums[o] = add && o < n_real ? tot + to_f32(add[o]) : tot;
+    if (copy && o < n_real) copy[o] = from_f32<T>(tot);
   }
 }
 
@@ -285,14 +307,17 @@ __global__ __launch_bounds__(kThreads) void zmap_kernel(int B, int IN, int BP, i
 // when vin: IN a multiple of the vector width, x and w aligned), then along
 // rows, so each chunk's stores of a wave are contiguous.
 // Blocks from nzb on total partial sums instead (sum_parts_block), when part is given.
+// With wsilu set, wc gets silu(x) instead of the feature weights (the SiLU base
+// branch as an extra feature), and bias (n_bias outputs, when given) is added to the sums.
 template <typename T>
 __global__ __launch_bounds__(kThreads) void zmapc_kernel(int B, int IN, int BP, int INP, int input_map, int vin,
                                                          const T* __restrict__ x, const T* __restrict__ w,
                                                          float* __restrict__ zc, float* __restrict__ wc, int nzb,
                                                          int n_parts, int n_sums, const float* __restrict__ part,
-                                                         float* __restrict__ sums) {
+                                                         float* __restrict__ sums, int wsilu, const T* __restrict__ bias,
+                                                         int n_bias) {
   if ((int)blockIdx.x >= nzb) {
-    sum_parts_block(blockIdx.x - nzb, n_parts, n_sums, part, sums);
+    sum_parts_block<T>(blockIdx.x - nzb, n_parts, n_sums, part, sums, bias, nullptr, n_bias);
     return;
   }
   constexpr int VW = 16 / (int)sizeof(T), LPR = 64 / VW;
@@ -320,7 +345,7 @@ __global__ __launch_bounds__(kThreads) void zmapc_kernel(int B, int IN, int BP, 
     for (int u = 0; u < VW; ++u) {
       const bool ok = b < B && i + u < IN;
       zz[u] = ok ? cheb_map(xv[u], input_map) : 0.f;
-      ww[u] = ok ? cheb_weight(zz[u], w ? wv[u] : 1.f, input_map) : 0.f;
+      ww[u] = !ok ? 0.f : wsilu ? silu_f(xv[u]) : cheb_weight(zz[u], w ? wv[u] : 1.f, input_map);
     }
     float* zp = zc + ((size_t)(i / 16) * BP + b) * 16 + i % 16;
 #pragma unroll
@@ -570,20 +595,25 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void f_kernel(int B, int OUT
 // contiguous. 64x64 tiles through LDS; 16-byte loads when vin (IN a multiple
 // of the vector width, x and w aligned), 16-byte stores (BP a multiple of 32).
 // Block rows past BP / 64 total partial sums instead (sum_parts_block), when part is given.
+// With st given (unweighted only: it takes wt's LDS tile), also silu(x) transposed into st
+// (INP, BP) in T, zero padded: the B operand of the SiLU base branch's weight gradient; with
+// dsum given, the sums of its n_dsum outputs also go there in T.
 template <typename T>
 __global__ __launch_bounds__(kThreads) void zmapT_kernel(int B, int IN, int BP, int INP, int input_map, int vin,
                                                          const T* __restrict__ x, const T* __restrict__ w,
                                                          float* __restrict__ zt, float* __restrict__ wt, int n_parts,
                                                          int n_sums, const float* __restrict__ part,
-                                                         float* __restrict__ sums) {
+                                                         float* __restrict__ sums, T* __restrict__ st,
+                                                         T* __restrict__ dsum, int n_dsum) {
   const int nby = (BP + 63) / 64;
   if ((int)blockIdx.y >= nby) {
     const int blk = (blockIdx.y - nby) * gridDim.x + blockIdx.x;
-    if (blk * 8 < n_sums) sum_parts_block(blk, n_parts, n_sums, part, sums);
+    if (blk * 8 < n_sums) sum_parts_block<T>(blk, n_parts, n_sums, part, sums, nullptr, dsum, n_dsum);
     return;
   }
   constexpr int VW = 16 / (int)sizeof(T), LPR = 64 / VW, RPI = kThreads / LPR;
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];  // tz [64][65], tw [64][65] when wt
+  // tz [64][65], then tw [64][65] when wt (silu(x) when st)
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   float* tz = reinterpret_cast<float*>(smem);
   float* tw = tz + 64 * 65;
   const int b0 = blockIdx.y * 64, i0 = blockIdx.x * 64;
@@ -621,9 +651,23 @@ __global__ __launch_bounds__(kThreads) void zmapT_kernel(int B, int IN, int BP, 
       const float zz = ok ? cheb_map(xv[u], input_map) : 0.f;
       tz[r * 65 + cl * VW + u] = zz;
       if (wt) tw[r * 65 + cl * VW + u] = ok ? cheb_weight(zz, w ? wv[u] : 1.f, input_map) : 0.f;
+      if (st) tw[r * 65 + cl * VW + u] = ok ? silu_f(xv[u]) : 0.f;
     }
   }
   __syncthreads();
+  if (st) {
+    // rows i of 64 batch values in T: 16-byte stores of 16 / sizeof(T) values
+    constexpr int SV = 16 / (int)sizeof(T), SL = 64 / SV;
+    for (int r = threadIdx.x / SL; r < 64; r += kThreads / SL) {
+      const int i = i0 + r, bl = (threadIdx.x % SL) * SV, b = b0 + bl;
+      if (i < INP && b < BP) {
+        float v[SV];
+#pragma unroll
+        for (int u = 0; u < SV; ++u) v[u] = tw[(bl + u) * 65 + r];
+        gstore16(st + (size_t)i * BP + b, pack16<T>(v));
+      }
+    }
+  }
   // rows i of 64 batch values: 16 lanes of 4 floats each
 #pragma unroll
   for (int r = threadIdx.x / 16; r < 64; r += kThreads / 16) {
@@ -1302,7 +1346,16 @@ __device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)"
 //            c + 2 in the second half of its last one (unrolled).
 // The MFMAs are never under a condition, which keeps the accumulators in
 // AGPRs across the loops.
-template <bool HAS_W, int NT, int TM, int TN, int NBUF, bool SKIP0, int WN, int NWM>
+//   BASE   : (with SKIP0) the last feature of every chunk is silu(x) instead of
+//            a Chebyshev term, its coefficient block the base weights: the
+//            SiLU base branch in the same contraction. silu(x) travels in the
+//            w buffers (copied like w, never multiplied into the features) and
+//            is read when that feature's A fragment is due: NT = 9 (the 8th
+//            slot of a pair's middle stage and the last slot of its last
+//            stage) or an even count of at least 6 (the last slot of a chunk's
+//            last stage), so that chunk x + 2's copy into the same buffer is
+//            issued at least one barrier after that read.
+template <bool HAS_W, int NT, int TM, int TN, int NBUF, bool SKIP0, int WN, int NWM, bool BASE = false>
 __global__ __launch_bounds__(64 * NWM * WN) void f_rega_kernel(int B, int OUT, int OUTP, int BP, int n_chunks, int n_tp,
                                                      const float* __restrict__ zc, const float* __restrict__ wc,
                                                      const bf16* __restrict__ cfm, const float* __restrict__ ysum,
@@ -1313,8 +1366,10 @@ __global__ __launch_bounds__(64 * NWM * WN) void f_rega_kernel(int B, int OUT, i
   constexpr int BPW = SB / 4096;   // 1 KB copy blocks per wave and stage
   constexpr int ZB = BM * 64;      // z of one chunk: BM rows x 16 floats
   constexpr int ZPW = ZB / 4096;   // 1 KB copy blocks per wave for z (and again for w)
-  constexpr int ZPW_ALL = HAS_W ? 2 * ZPW : ZPW;
+  constexpr int ZPW_ALL = HAS_W || BASE ? 2 * ZPW : ZPW;
   static_assert(BPW * 4096 == SB && ZPW * 4096 == ZB, "copy blocks divide over the waves");
+  static_assert(!BASE || (SKIP0 && !HAS_W && (NT == 9 || NT == 0 || (NT % 2 == 0 && NT >= 6))),
+                "the base feature closes unweighted chunks of 9 or of an even count >= 6");
   static_assert(NBUF >= 3 && NBUF <= 6, "copy waits below count up to NBUF - 2 newer groups");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];  // [NBUF][SB], z [2][ZB], w [2][ZB]
   unsigned char* zs = smem + NBUF * SB;
@@ -1368,7 +1423,7 @@ __global__ __launch_bounds__(64 * NWM * WN) void f_rega_kernel(int B, int OUT, i
 #pragma unroll
     for (int k = 0; k < ZPW; ++k) {
       lds_dma16(zc + off + k * 256, zs + (x & 1) * ZB + (wave * ZPW + k) * 1024);
-      if (HAS_W) lds_dma16(wc + off + k * 256, ws + (x & 1) * ZB + (wave * ZPW + k) * 1024);
+      if (HAS_W || BASE) lds_dma16(wc + off + k * 256, ws + (x & 1) * ZB + (wave * ZPW + k) * 1024);
     }
   };
   // copy group of stage st into buffer st % NBUF; past the last stage the buffer is free and
@@ -1451,6 +1506,16 @@ __global__ __launch_bounds__(64 * NWM * WN) void f_rega_kernel(int B, int OUT, i
       af1[a] = pack16<bf16>(gb[a]);
     }
   };
+  // BASE: the A fragments of chunk x's base feature, silu(x) of the lane's rows and inputs
+  auto base_frag = [&](int x, u32x4(&af)[TM]) {
+#pragma unroll
+    for (int a = 0; a < TM; ++a) {
+      const unsigned char* sr = ws + (x & 1) * ZB + zrow_off + a * 32 * 64;
+      const f32x4 s0 = __builtin_bit_cast(f32x4, lds_read16(sr)), s1 = __builtin_bit_cast(f32x4, lds_read16(sr + 16));
+      const float sv[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+      af[a] = pack16<bf16>(sv);
+    }
+  };
   auto read_b = [&](int st, int f, u32x4(&bf)[TN]) {
     const unsigned char* bb = smem + (st % NBUF) * SB + f * FB + frag_off;
 #pragma unroll
@@ -1477,14 +1542,19 @@ __global__ __launch_bounds__(64 * NWM * WN) void f_rega_kernel(int B, int OUT, i
   };
   int s = 0;
   // stage s; on entry af0 / bf0 hold its first slot. SEED2: chunk x2 starts at its second slot;
-  // SEEDN: chunk xn starts at the first slot of stage s + 1.
-  auto stage = [&](auto seed2_tag, auto seedn_tag, int x2, int xn) {
+  // SEEDN: chunk xn starts at the first slot of stage s + 1. BASE2 / BASEN: the second slot of
+  // stage s / the first slot of stage s + 1 is the base feature of chunk xb.
+  auto stage = [&](auto seed2_tag, auto seedn_tag, int x2, int xn, auto base2_tag, auto basen_tag, int xb) {
     constexpr bool SEED2 = decltype(seed2_tag)::value, SEEDN = decltype(seedn_tag)::value;
+    constexpr bool BASE2 = decltype(base2_tag)::value, BASEN = decltype(basen_tag)::value;
     mma_first(af0, bf0);
     copy_stage(s + NBUF - 1);
     read_b(s, 1, bf1);
     if constexpr (SEED2) seed(std::true_type{}, x2);
-    step_second();
+    if constexpr (BASE2)
+      base_frag(xb, af1);
+    else
+      step_second();
     mma_rest(af0, bf0);
     // publish stage s + 1 (this wave's copies done, its reads of stage s returned)
     wait_group();
@@ -1493,12 +1563,16 @@ __global__ __launch_bounds__(64 * NWM * WN) void f_rega_kernel(int B, int OUT, i
     mma_first(af1, bf1);
     read_b(s + 1, 0, bf0);
     if constexpr (SEEDN) seed(std::false_type{}, xn);
-    step_first();
+    if constexpr (BASEN)
+      base_frag(xb, af0);
+    else
+      step_first();
     mma_rest(af1, bf1);
     ++s;
   };
   using T_ = std::true_type;
   using F_ = std::false_type;
+  using B_ = std::integral_constant<bool, BASE>;
 
   // prologue: z of chunk 0 and the groups of stages 0 .. NBUF - 2 in flight; z(0) and stage 0
   // published; the first slot of stage 0 prepared
@@ -1512,25 +1586,27 @@ __global__ __launch_bounds__(64 * NWM * WN) void f_rega_kernel(int B, int OUT, i
 
   if constexpr (NT == 0) {
     for (int c = 0; c < n_chunks; ++c) {
-      for (int p = 0; p + 1 < P; ++p) stage(F_{}, F_{}, 0, 0);
-      stage(F_{}, T_{}, 0, c + 1);  // chunk c + 1 starts at the next stage's first slot
+      for (int p = 0; p + 1 < P; ++p) stage(F_{}, F_{}, 0, 0, F_{}, F_{}, 0);
+      stage(F_{}, T_{}, 0, c + 1, B_{}, F_{}, c);  // chunk c + 1 starts at the next stage's first slot
     }
   } else if constexpr (!ODD) {
     for (int c = 0; c < n_chunks; ++c) {
 #pragma unroll
-      for (int p = 0; p + 1 < NT / 2; ++p) stage(F_{}, F_{}, 0, 0);
-      stage(F_{}, T_{}, 0, c + 1);
+      for (int p = 0; p + 1 < NT / 2; ++p) stage(F_{}, F_{}, 0, 0, F_{}, F_{}, 0);
+      stage(F_{}, T_{}, 0, c + 1, B_{}, F_{}, c);
     }
   } else {
     for (int c = 0; c < n_chunks; c += 2) {
 #pragma unroll
       for (int q = 0; q < NT; ++q) {
         if (q == NT / 2)
-          stage(T_{}, F_{}, c + 1, 0);  // chunk c + 1 starts at this stage's second slot
+          stage(T_{}, F_{}, c + 1, 0, F_{}, F_{}, 0);  // chunk c + 1 starts at this stage's second slot
         else if (q == NT - 1)
-          stage(F_{}, T_{}, 0, c + 2);  // chunk c + 2 starts at the next stage's first slot
+          stage(F_{}, T_{}, 0, c + 2, B_{}, F_{}, c + 1);  // chunk c + 2 starts at the next stage's first slot
+        else if (q == NT / 2 - 1)
+          stage(F_{}, F_{}, 0, 0, F_{}, B_{}, c);  // chunk c ends at the next stage's first slot
         else
-          stage(F_{}, F_{}, 0, 0);
+          stage(F_{}, F_{}, 0, 0, F_{}, F_{}, 0);
       }
     }
   }
@@ -1886,10 +1962,13 @@ __global__ __launch_bounds__(256) void p_dma_kernel(KBasis bs, int B, int IN, in
 // passes of RPASS rows: the feature sums H_j go to LDS and every thread forms
 // p[b, i] = sum_j f_j(x[b, i]) H_j[b, i] for (row, input) pairs, the features computed once per
 // pair.
-template <int KIND, int NF, int TN, int RB, int KD = 3, bool EVEN = false>
+// BASE (kinds other than B-splines): p[b, i] also gets silu'(x[b, i]) hb[b, i], hb (B, IN) float32
+// = g W, the input gradient of the SiLU base branch.
+template <int KIND, int NF, int TN, int RB, int KD = 3, bool EVEN = false, bool BASE = false>
 __global__ __launch_bounds__(512) void p8_kernel(KBasis bs, int B, int IN, int INP, int OUTP,
                                                  const bf16* __restrict__ x, const bf16* __restrict__ g, int gstride,
-                                                 const bf16* __restrict__ cfmt, bf16* __restrict__ p) {
+                                                 const bf16* __restrict__ cfmt, bf16* __restrict__ p,
+                                                 const float* __restrict__ hb) {
   constexpr int BM = 256, BN = 128 * TN, TI = BN / NF, SA = BM * RB, SS = (BM + BN) * RB, NBUF = 2;
   static_assert(TI * NF == BN && TI % 2 == 0, "whole inputs per tile");
   constexpr int RP = TI + 1, RPASS = TN == 2 ? 128 : 64, NBLK = SS / 1024, BPW = NBLK / 8;
@@ -1979,6 +2058,7 @@ __global__ __launch_bounds__(512) void p8_kernel(KBasis bs, int B, int IN, int I
   constexpr int EPT = RPASS * TI / 2 / 512;
   static_assert(EPT * 512 == RPASS * TI / 2, "whole epilogue rounds");
   constexpr bool FIXED_INPUTS = KIND == KF_KIND_BSPLINE && 512 % (TI / 2) == 0;
+  static_assert(!(BASE && KIND == KF_KIND_BSPLINE), "the base term rides the other kinds' epilogue");
   const int il_t = 2 * (tid % (TI / 2)), i_t = i0 + il_t;
   float* kus = kps + TI * (bs.n_knots + 2 * bs.spline_k);  // [TI][2]
   // every pass's x values (EPT items per pass), loaded before the passes (addresses clamped into
@@ -2018,6 +2098,7 @@ __global__ __launch_bounds__(512) void p8_kernel(KBasis bs, int B, int IN, int I
       // clamped into x, so the loads need no branch and their latency passes behind the stores)
       constexpr int EPG = (RPASS * TI / 2 + 511) / 512;
       uint32_t xg[FIXED_INPUTS ? 1 : EPG];
+      float hg[BASE ? EPG : 1][2];
       if constexpr (!FIXED_INPUTS) {
         const unsigned short* xs = reinterpret_cast<const unsigned short*>(x);
 #pragma unroll
@@ -2025,7 +2106,12 @@ __global__ __launch_bounds__(512) void p8_kernel(KBasis bs, int B, int IN, int I
           const int e = tid + 512 * k, row = e / (TI / 2), il = 2 * (e % (TI / 2));
           const int b = b0 + ps * RPASS + row, i = i0 + il;
           const size_t o = (size_t)(b < B ? b : B - 1) * IN;
-          xg[k] = (uint32_t)xs[o + (i < IN ? i : IN - 1)] | (uint32_t)xs[o + (i + 1 < IN ? i + 1 : IN - 1)] << 16;
+          const size_t i_0 = i < IN ? i : IN - 1, i_1 = i + 1 < IN ? i + 1 : IN - 1;
+          xg[k] = (uint32_t)xs[o + i_0] | (uint32_t)xs[o + i_1] << 16;
+          if constexpr (BASE) {
+            hg[k][0] = hb[o + i_0];
+            hg[k][1] = hb[o + i_1];
+          }
         }
       }
       __syncthreads();
@@ -2109,6 +2195,7 @@ __global__ __launch_bounds__(512) void p8_kernel(KBasis bs, int B, int IN, int I
               kind_features<KIND, NF>(xv, 1.f, i + u, bs, f);
 #pragma unroll
               for (int q = 0; q < NF; ++q) v[u] = fmaf(red[(q * RPASS + row) * RP + il + u], f[q], v[u]);
+              if constexpr (BASE) v[u] = fmaf(dsilu_f(xv), hg[k][u], v[u]);
             }
           }
           store_pair(b, i, v);

@@ -216,12 +216,18 @@ class KANLinear(nn.Module):
         if not _compiling():
             self.uses_kernel(x.device)  # raises when the HIP path cannot run
         st = self._basis_state()
+        if self._base_fused(x):
+            # spline part, SiLU base branch and bias in one contraction (and one backward pass)
+            y = _kernels.spline_base_forward(x, self.effective_coef(), self.effective_base_weight(), self.bias,
+                                             self._plan_key)
+            return y + self._symbolic_sum(x) if self._sym_codes else y
         if self._plan.kind == "rational":
             y = _kernels.spline_forward(x, self.effective_coef(), st, self._plan_key, self.basis_numerator, self.basis_denominator)
         else:
             y = _kernels.spline_forward(x, self.effective_coef(), st, self._plan_key)
         if self.base_weight is not None:
-            # accumulated into y by the GEMM itself (C = y + act(x) W^T), no separate add
+            # accumulated into y by the GEMM itself (C = y + act(x) W^T), no separate add (an
+            # in-place addmm_ on F's output costs more: its backward copies through the view)
             y2 = torch.addmm(y.reshape(-1, self.out_features), self.base_activation(x).reshape(-1, self.in_features),
                              self.effective_base_weight().t())
             y = y2.reshape(y.shape)
@@ -230,6 +236,19 @@ class KANLinear(nn.Module):
         if self.bias is not None:
             y = _kernels.bias_add(y, self.bias)
         return y
+
+    def _base_fused(self, x: torch.Tensor) -> bool:
+        """Whether forward runs the spline part, the SiLU base branch and the bias as one fused
+        kernel call (bf16 Chebyshev plans on their contraction kernels, eager)."""
+        if self.base_weight is None or self.base_activation is not F.silu or self._plan.kind != "cheb":
+            return False
+        dt = torch.bfloat16
+        if x.dtype != dt or self.coef.dtype != dt or self.base_weight.dtype != dt:
+            return False
+        if (self.bias is not None and self.bias.dtype != dt) or _compiling() or x.dim() < 1:
+            return False
+        batch = x.numel() // max(self.in_features, 1)
+        return _kernels.base_fused(self._plan_key, dt, batch, self.in_features, self.out_features)[0]
 
     def uses_kernel(self, device: torch.device) -> bool:
         """Whether forward runs the fused kernel on ``device`` (always, or an error)."""

@@ -98,7 +98,7 @@ int main() {
   for (const kf_basis& b : bases)
     for (const Shape& s : shapes)
       for (int dtype : {KF_F32, KF_BF16})
-        for (int op : {KF_OP_F, KF_OP_G, KF_OP_P}) {
+        for (int op : {KF_OP_F, KF_OP_G, KF_OP_P, KF_OP_F_BASE, KF_OP_P_BASE, KF_OP_G_BASE}) {
           const size_t n = kf_workspace_bytes(op, &b, dtype, s.batch, s.n_in, s.n_out);
           check(n < (size_t(1) << 40), "workspace bytes of op " + std::to_string(op) + " kind " +
                                            std::to_string(b.kind) + " shape " + std::to_string(s.batch) + "x" +
@@ -117,6 +117,27 @@ int main() {
                   "rational bwd ws");
           }
   for (const Shape& s : shapes) check(kf_column_sums_workspace_bytes(s.batch, s.n_out) < (size_t(1) << 40), "colsum ws");
+
+  // the fused SiLU base branch: routes and their workspaces (a fused op has a workspace)
+  for (const kf_basis& b : bases)
+    for (const Shape& s : shapes)
+      for (int dtype : {KF_F32, KF_BF16})
+        for (int op : {KF_OP_F_BASE, KF_OP_P_BASE, KF_OP_G_BASE}) {
+          const int r = kf_base_fused(op, &b, dtype, s.batch, s.n_in, s.n_out);
+          const size_t n = kf_workspace_bytes(op, &b, dtype, s.batch, s.n_in, s.n_out);
+          check(r == 0 || (r == 1 && n > 0), "base route " + std::to_string(op) + " reports a workspace");
+          check(r == 0 || (b.kind == KF_KIND_CHEB && dtype == KF_BF16), "base route only for bf16 Chebyshev");
+        }
+  {
+    const kf_basis c0 = cheb(9, 0, 9, KF_MAP_TANH), c1 = cheb(9, 1, 8, KF_MAP_TANH_SQ);
+    check(kf_base_fused(KF_OP_F_BASE, &c0, KF_BF16, 8192, 768, 3072) == 1, "headline F fused");
+    check(kf_base_fused(KF_OP_P_BASE, &c1, KF_BF16, 8192, 768, 3072) == 1, "headline P fused");
+    check(kf_base_fused(KF_OP_G_BASE, &c0, KF_BF16, 8192, 768, 3072) == 1, "headline G fused");
+    const kf_basis c7 = cheb(7, 0, 7, KF_MAP_TANH);  // 7 features a chunk: not fused
+    check(kf_base_fused(KF_OP_F_BASE, &c7, KF_BF16, 8192, 768, 3072) == 0, "7 features not fused");
+    check(kf_base_fused(KF_OP_F_BASE, &c0, KF_BF16, 4096, 64, 4) == 0, "narrow layer not fused");
+    expect_error("kf_base_fused unknown op", kf_base_fused(KF_OP_F, &c0, KF_BF16, 64, 64, 64), KF_EINVAL);
+  }
 
   // descriptor validation (through kf_F: every entry point validates the same way first)
   float* d = g_host;
@@ -239,6 +260,32 @@ int main() {
   expect_error("kf_lut_forward table dtype",
                kf_lut_forward(KF_BF16, 64, 8, 16, 8, d, d, d, d, d, nullptr, nullptr, nullptr, d, nullptr),
                KF_EUNSUPPORTED);
+
+  {
+    const kf_basis c0 = cheb(9, 0, 9, KF_MAP_TANH), c1 = cheb(9, 1, 8, KF_MAP_TANH_SQ);
+    expect_error("kf_F_base NULL base_w",
+                 kf_F_base(&c0, KF_BF16, 8192, 768, 3072, d, d, nullptr, nullptr, d, d, 1 << 30, nullptr), KF_EINVAL);
+    expect_error("kf_F_base float32", kf_F_base(&c0, KF_F32, 8192, 768, 3072, d, d, d, nullptr, d, d, 1 << 30, nullptr),
+                 KF_EUNSUPPORTED);
+    expect_error("kf_F_base order 1", kf_F_base(&c1, KF_BF16, 8192, 768, 3072, d, d, d, nullptr, d, d, 1 << 30, nullptr),
+                 KF_EUNSUPPORTED);
+    expect_error("kf_F_base small workspace",
+                 kf_F_base(&c0, KF_BF16, 8192, 768, 3072, d, d, d, nullptr, d, d, 64, nullptr), KF_EWORKSPACE);
+    expect_error("kf_P_base order 0", kf_P_base(&c0, KF_BF16, 8192, 768, 3072, d, d, d, d, d, d, 1 << 30, nullptr),
+                 KF_EUNSUPPORTED);
+    expect_error("kf_P_base NULL g", kf_P_base(&c1, KF_BF16, 8192, 768, 3072, d, nullptr, d, d, d, d, 1 << 30, nullptr),
+                 KF_EINVAL);
+    expect_error("kf_P_base no workspace", kf_P_base(&c1, KF_BF16, 8192, 768, 3072, d, d, d, d, d, nullptr, 0, nullptr),
+                 KF_EWORKSPACE);
+    expect_error("kf_G_base small workspace",
+                 kf_G_base(&c0, KF_BF16, 8192, 768, 3072, d, d, d, d, d, d, 256, nullptr), KF_EWORKSPACE);
+    expect_error("kf_G_base empty batch", kf_G_base(&c0, KF_BF16, 0, 768, 3072, d, d, d, d, d, d, 256, nullptr),
+                 KF_EINVAL);
+    expect_error("kf_G_base small layer", kf_G_base(&c0, KF_BF16, 64, 48, 192, d, d, d, d, d, d, 1 << 30, nullptr),
+                 KF_EUNSUPPORTED);
+    check(kf_G_base(&c0, KF_BF16, 64, 48, 192, d, d, nullptr, nullptr, nullptr, nullptr, 0, nullptr) == KF_OK,
+          "G_base with nothing wanted");
+  }
 
   // empty calls succeed without touching a device
   check(kf_F(&cb, KF_F32, 0, 4, 4, nullptr, nullptr, nullptr, nullptr, nullptr, 0, nullptr) == KF_OK, "empty F");

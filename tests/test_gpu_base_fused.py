@@ -1,0 +1,178 @@
+"""KANLinear with its SiLU base branch and bias fused into the HIP contractions (kf_F_base,
+kf_P_base, kf_G_base) against the float64 oracle: y and every first-order gradient on layers
+whose three entries all fuse (Chebyshev degrees 8, 7 and 5: chunks of 9 features, and even counts
+on the runtime-count F kernel), ragged shapes (inputs not a multiple of 16, outputs not of 8,
+batch not of 64), the headline shape 768 -> 3072 at batch 8192 against a plain PyTorch float32
+reference, double backward through the fused layer (its backward composes differentiable ops
+there) against the unfused layer, the routes the library reports, and bitwise determinism.
+Tolerance: bfloat16 normwise 2e-2.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import kanforge_amd as kf
+from cases import oracle_basis, rounded
+from kanforge_amd.torch import KANLinear
+from kanforge_amd.torch import kernels as K
+from oracle import kan64 as o
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+BF = torch.bfloat16
+TOL = 2e-2
+
+
+def np64(t):
+    return t.detach().float().cpu().double().numpy()
+
+
+def make_layer(deg, IN, OUT, seed=0, edge_scale=False, bias=True):
+    torch.manual_seed(seed)
+    layer = KANLinear(IN, OUT, kf.Chebyshev(deg), edge_scale=edge_scale, bias=bias)
+    with torch.no_grad():
+        layer.coef.normal_(0, 0.5 / math.sqrt(IN))
+        layer.base_weight.normal_(0, 1 / math.sqrt(IN))
+        if edge_scale:
+            layer.edge_scale.uniform_(0.5, 1.5)
+        if bias:
+            layer.bias.normal_()
+    return layer.to(device=DEV, dtype=BF)
+
+
+def unfused(layer):
+    """The same layer on the unfused route (F, P, G plus torch base-branch ops)."""
+    layer._base_fused = lambda x: False
+    return layer
+
+
+def test_routes_reported_by_the_library():
+    plan = make_layer(8, 48, 8)._plan_key
+    assert K.base_fused(plan, BF, 8192, 768, 3072) == (True, True, True)
+    assert K.base_fused(plan, torch.float32, 8192, 768, 3072) == (False, False, False)
+    assert not K.base_fused(plan, BF, 4096, 64, 4)[0]  # narrow: F's streaming route
+    plan6 = make_layer(6, 48, 8)._plan_key  # 7 features a chunk: not fused
+    assert not K.base_fused(plan6, BF, 8192, 768, 3072)[0]
+
+
+# (batch, in, out, degree): every case has >= 128 G tiles of 192 x 48 (g96_kernel)
+CASES = [
+    (256, 3072, 384, 8),
+    (333, 3000, 400, 8),  # ragged: in % 16, out % 8, batch % 64
+    (200, 3072, 384, 7),  # 8 features a chunk (runtime count)
+    (130, 3072, 384, 5),  # 6 features a chunk; P of order 1 not on p8 (composed)
+]
+
+
+@pytest.mark.parametrize("B,IN,OUT,deg", CASES)
+def test_fused_layer_against_oracle(B, IN, OUT, deg):
+    layer = make_layer(deg, IN, OUT, edge_scale=True)
+    fused = K.base_fused(layer._plan_key, BF, B, IN, OUT)
+    print(f"case B={B} in={IN} out={OUT} deg={deg} fused={fused}", flush=True)
+    assert fused[0] and fused[2]
+    assert fused[1] == (deg != 5)
+    ob = oracle_basis(layer.basis, IN, None)
+    rng = np.random.default_rng(B)
+    x0 = rng.normal(0, 1, (B, IN))
+    gy0 = rng.normal(0, 1, (B, OUT))
+    x = torch.as_tensor(x0, dtype=torch.float32).to(DEV, BF).requires_grad_()
+    gy = torch.as_tensor(gy0, dtype=torch.float32).to(DEV, BF)
+    y = layer(x)
+    y.backward(gy)
+    torch.cuda.synchronize()
+    xr, gyr = rounded(x0, BF), rounded(gy0, BF)
+    c, s, W, b = np64(layer.coef), np64(layer.edge_scale), np64(layer.base_weight), np64(layer.bias)
+    assert o.normwise_err(np64(y), o.kan_linear(xr, c, ob, W, b, s)) <= TOL
+    ceff = c * s[..., None]
+    G0 = o.prim_G(xr, gyr, None, ob, 0)
+    checks = {
+        "x": (x.grad, o.prim_P(xr, gyr, ceff, ob, 1) + (gyr @ W) * o.silu_derivative(xr, 1)),
+        "coef": (layer.coef.grad, G0 * s[..., None]),
+        "edge_scale": (layer.edge_scale.grad, (G0 * c).sum(-1)),
+        "base_weight": (layer.base_weight.grad, gyr.T @ o.silu_derivative(xr, 0)),
+        "bias": (layer.bias.grad, gyr.sum(0)),
+    }
+    for key, (got, want) in checks.items():
+        err = o.normwise_err(np64(got), want)
+        print(f"  {key}: {err:.3e}", flush=True)
+        assert err <= TOL, (key, err)
+
+
+def test_headline_shape_with_base_and_bias():
+    """768 -> 3072 Chebyshev(8), batch 8192: y, dX, dCoef, dW, db against float32 torch."""
+    B, IN, OUT, KB = 8192, 768, 3072, 9
+    torch.manual_seed(0)
+    layer = KANLinear(IN, OUT, kf.Chebyshev(8), device=DEV, dtype=BF)
+    with torch.no_grad():
+        layer.coef.copy_(torch.randn(OUT, IN, KB, device=DEV) / math.sqrt(IN * KB))
+        layer.bias.normal_()
+    assert K.base_fused(layer._plan_key, BF, B, IN, OUT) == (True, True, True)
+    x = torch.randn(B, IN, device=DEV).to(BF).requires_grad_()
+    gy = torch.randn(B, OUT, device=DEV).to(BF)
+    y = layer(x)
+    dx, dc, dw, db = torch.autograd.grad(y, [x, layer.coef, layer.base_weight, layer.bias], gy)
+    torch.cuda.synchronize()
+    a = torch.as_tensor(np.asarray(layer.basis._cheb), dtype=torch.float32, device=DEV)
+    xf, g32 = x.detach().float(), gy.float()
+    z = torch.tanh(xf)
+    t, dt = [torch.ones_like(z), z], [torch.zeros_like(z), torch.ones_like(z)]
+    for j in range(2, KB):
+        t.append(2 * z * t[j - 1] - t[j - 2])
+        dt.append(2 * t[j - 1] + 2 * z * dt[j - 1] - dt[j - 2])
+    phi = (torch.stack(t, -1) @ a).reshape(B, IN * KB)
+    dphi = torch.stack(dt, -1) * (1 - z * z).unsqueeze(-1) @ a
+    c2 = layer.coef.detach().float().reshape(OUT, IN * KB)
+    W = layer.base_weight.detach().float()
+    sx = torch.nn.functional.silu(xf)
+    sig = torch.sigmoid(xf)
+    dsx = sig * (1 + xf * (1 - sig))
+    refs = {
+        "y": (y, phi @ c2.t().contiguous() + sx @ W.t().contiguous() + layer.bias.detach().float()),
+        "dx": (dx, (g32 @ c2).reshape(B, IN, KB).mul_(dphi).sum(-1) + (g32 @ W) * dsx),
+        "dcoef": (dc, (g32.t().contiguous() @ phi).reshape(OUT, IN, KB)),
+        "dbase_w": (dw, g32.t().contiguous() @ sx),
+        "dbias": (db, g32.sum(0)),
+    }
+    for key, (got, want) in refs.items():
+        err = ((got.float() - want).abs().max() / want.abs().max()).item()
+        print(f"headline {key}: {err:.3e}", flush=True)
+        assert torch.isfinite(got).all() and err < TOL, (key, err)
+
+
+def test_double_backward_through_the_fused_layer():
+    """Gradient penalty d/dtheta sum (dy/dx)^2: the fused layer's backward composes kf::P and
+    torch ops under create_graph; the unfused layer gives the same values."""
+    B, IN, OUT = 256, 3072, 384
+    rng = np.random.default_rng(5)
+    x0 = torch.as_tensor(rng.normal(0, 1, (B, IN)), dtype=torch.float32).to(DEV, BF)
+    grads = []
+    for fuse in (True, False):
+        layer = make_layer(8, IN, OUT, seed=3)
+        if not fuse:
+            unfused(layer)
+        x = x0.clone().requires_grad_()
+        y = layer(x)
+        (gx,) = torch.autograd.grad(y.float().sum(), x, create_graph=True)
+        (gx.float() ** 2).sum().backward()
+        grads.append([p.grad.detach().float().clone() for p in (layer.coef, layer.base_weight)] + [gx.detach().float()])
+    torch.cuda.synchronize()
+    for got, want in zip(*grads):
+        err = ((got - want).abs().max() / want.abs().max()).item()
+        assert err < TOL, err
+
+
+def test_fused_calls_are_deterministic():
+    B, IN, OUT = 1024, 768, 3072
+    layer = make_layer(8, IN, OUT, seed=7)
+    x = torch.randn(B, IN, device=DEV).to(BF).requires_grad_()
+    gy = torch.randn(B, OUT, device=DEV).to(BF)
+    outs = []
+    for _ in range(2):
+        y = layer(x)
+        outs.append([y.detach()] + list(torch.autograd.grad(y, [x, layer.coef, layer.base_weight, layer.bias], gy)))
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)

@@ -186,3 +186,105 @@ def test_phi_block_kernel_indexing(n_in, K):
         if nv:
             assert (nv - 1) * VW + VW <= n
             assert (i0 * K + n) <= n_in * K
+
+
+def f_rega_schedule(NT, n_tp, n_chunks, NBUF=4, base=True):
+    """Events of f_rega_kernel (kf_kernels.h) in program order, restated from its loops: the
+    chunk copy issues of copy_stage (with the carrier state machine zg_next / zx_next), the seeds
+    (SEED2 in a stage's first half, SEEDN in its second), the base-feature reads (BASE2 first
+    half, BASEN second half) and the mid-stage barriers. Each event is (stage, half, kind, chunk);
+    half 0 runs before the stage's barrier, half 1 after it; the prologue is stage -1 (its copies
+    before its barrier, the first seed after). A copy event carries the group g it rides with."""
+    ODD = NT % 2 == 1
+    P = NT // 2 if NT > 0 and not ODD else n_tp // 2
+    S = n_chunks * n_tp // 2
+    ev = []
+    st = {"zg": P if not ODD else NT // 2, "zx": 1}
+
+    def copy_stage(stage_issued, g):
+        if g == st["zg"]:
+            if st["zx"] < n_chunks:
+                ev.append((stage_issued, 0, "copy", st["zx"], g))
+            st["zg"] += P if not ODD else (NT // 2 + 1 if st["zx"] & 1 else NT // 2)
+            st["zx"] += 1
+
+    ev.append((-1, 0, "copy", 0, 0))
+    for g in range(NBUF - 1):
+        copy_stage(-1, g)
+    ev.append((-1, 1, "seed", 0, None))
+    s = 0
+
+    def stage(seed2=None, seedn=None, base2=None, basen=None):
+        nonlocal s
+        copy_stage(s, s + NBUF - 1)
+        if seed2 is not None:
+            ev.append((s, 0, "seed", seed2, None))
+        if base2 is not None:
+            ev.append((s, 0, "base", base2, None))
+        if seedn is not None:
+            ev.append((s, 1, "seed", seedn, None))
+        if basen is not None:
+            ev.append((s, 1, "base", basen, None))
+        s += 1
+
+    b = (lambda c: c) if base else (lambda c: None)
+    if not ODD:
+        for c in range(n_chunks):
+            for _ in range(P - 1):
+                stage()
+            stage(seedn=c + 1 if c + 1 < n_chunks else None, base2=b(c))
+    else:
+        for c in range(0, n_chunks, 2):
+            for q in range(NT):
+                if q == NT // 2:
+                    stage(seed2=c + 1)
+                elif q == NT - 1:
+                    stage(seedn=c + 2 if c + 2 < n_chunks else None, base2=b(c + 1))
+                elif q == NT // 2 - 1:
+                    stage(basen=b(c))
+                else:
+                    stage()
+    assert s == S
+    return ev
+
+
+@pytest.mark.parametrize("NT,n_tp", [(9, 9), (0, 6), (0, 8), (0, 10), (8, 8), (0, 4)])
+@pytest.mark.parametrize("n_chunks", [2, 4, 48])
+def test_f_rega_chunk_buffers_published_before_read_and_free_before_refill(NT, n_tp, n_chunks):
+    """Chunk x's z (and silu(x)) lives in LDS buffer x & 1. Every read of it (seed, base feature)
+    must follow the barrier that publishes its copy (barrier g - 1 for a copy issued by
+    copy_stage(g), whose group the wait before that barrier completes), and the copy of chunk
+    x + 2 into the same buffer must be issued after a barrier that follows every read of chunk x.
+    The base variant is exempt at n_tp = 4 (the kernel rejects it there), which this test shows
+    is needed."""
+    base = n_tp != 4
+    ev = f_rega_schedule(NT, n_tp, n_chunks, base=base)
+    issue = {x: (stg, g) for (stg, half, kind, x, g) in ev if kind == "copy"}
+    for x in range(n_chunks):
+        assert x in issue, f"chunk {x} never copied"
+    reads = {}
+    for (stg, half, kind, x, _) in ev:
+        if kind in ("seed", "base"):
+            reads.setdefault(x, []).append((stg, half))
+    for x, rs in reads.items():
+        # the copy riding with group g is complete at barrier g - 1 (chunk 0: the prologue's)
+        pub = -1 if x == 0 else issue[x][1] - 1
+        for (stg, half) in rs:
+            assert (stg, half) > (pub, 0), f"chunk {x} read at {(stg, half)} before barrier {pub}"
+        if x + 2 in issue:
+            last = max(rs)
+            # a barrier between the last read and the refill: a first-half read is followed by
+            # barrier stg; a second-half read needs barrier stg + 1
+            need = last[0] + 1 if last[1] == 0 else last[0] + 2
+            assert issue[x + 2][0] >= need, f"chunk {x + 2} overwrites chunk {x} (read {last}, copy {issue[x + 2]})"
+    n_base = sum(1 for e in ev if e[2] == "base")
+    assert n_base == (n_chunks if base else 0)
+
+
+def test_f_rega_base_at_four_features_would_race():
+    """The reason the base variant needs chunks of at least 6 features (even counts): at 4, chunk
+    x + 2's copy is issued in the stage of chunk x's base read."""
+    ev = f_rega_schedule(0, 4, 4, base=True)
+    issue = {x: stg for (stg, half, kind, x, g) in ev if kind == "copy"}
+    base_reads = {x: stg for (stg, half, kind, x, g) in ev if kind == "base"}
+    assert any(issue.get(x + 2, 1 << 30) <= base_reads[x] for x in base_reads)
