@@ -263,17 +263,18 @@ struct GemmCfg {
 };
 
 // Tile width and reduction split with the least modelled time: whole rounds of 256 workgroups,
-// each stage of a 256 x 128 TN tile at ~4.7 TFLOP/s per CU (the core's measured rate), plus the
-// float32 partial sums of a split written and read back at ~5 TB/s. The tail split runs the
-// tiles of whole rounds over the full reduction and splits only the remaining tiles, so a tile
-// count just past a multiple of 256 does not cost another whole round (plus ~5 us for its two
-// extra launches).
+// each stage of a 256 x 128 TN tile at ~4.7 TFLOP/s per CU (the core's measured rate; 15 % less
+// for TN = 1, whose waves read 5 fragments per 4 MFMAs), plus the float32 partial sums of a split
+// written and read back at ~5 TB/s. The tail split runs the tiles of whole rounds over the full
+// reduction and splits only the remaining tiles, so a tile count just past a multiple of 256
+// does not cost another whole round (plus ~5 us for its two extra launches). Narrow tiles
+// (TN = 1) fill the chip without a split where N is small.
 GemmCfg pick_gemm(long M, long N, long S) {
   GemmCfg best{3, 1};
   double best_t = 1e300;
-  for (int tn : {3, 2}) {
+  for (int tn : {3, 2, 1}) {
     const long tiles = ((M + 255) / 256) * ((N + 128 * tn - 1) / (128 * tn));
-    const double t_stage = 256.0 * 128 * tn * 64 * 2 / 4.7e12;
+    const double t_stage = 256.0 * 128 * tn * 64 * 2 / (tn == 1 ? 4.0e12 : 4.7e12);
     for (int nz : {1, 2, 3, 4, 6, 8, 10, 12, 16, 24, 32}) {
       if (nz > S) break;
       const long wg = tiles * nz, rounds = (wg + 255) / 256, s_per = (S + nz - 1) / nz;
@@ -364,22 +365,26 @@ int gemm_nt(long M, long N, long K, const void* A, long lda, const void* B, long
   if (c.tail_nz) {
     const size_t need = split_bytes(c, M, N);
     if (!ws || ws_bytes < need || !aligned16(ws)) return fail(KF_EWORKSPACE, "gemm: split workspace of %zu bytes needed", need);
-    return c.tn == 3 ? launch_gemm_tail<3>(c, (int)M, (int)N, S, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, out_f32, ws, s)
-                     : launch_gemm_tail<2>(c, (int)M, (int)N, S, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, out_f32, ws, s);
+    return c.tn == 3   ? launch_gemm_tail<3>(c, (int)M, (int)N, S, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, out_f32, ws, s)
+           : c.tn == 2 ? launch_gemm_tail<2>(c, (int)M, (int)N, S, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, out_f32, ws, s)
+                       : launch_gemm_tail<1>(c, (int)M, (int)N, S, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, out_f32, ws, s);
   }
   if (c.nz == 1) {
     const int vout = ldc % CH == 0 && aligned16(C);
     if (out_f32)
-      return c.tn == 3 ? launch_gemm<3, 128, 2, true>((int)M, (int)N, S, 1, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, 0, vout, s)
-                       : launch_gemm<2, 128, 2, true>((int)M, (int)N, S, 1, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, 0, vout, s);
-    return c.tn == 3 ? launch_gemm<3, 128, 2, false>((int)M, (int)N, S, 1, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, 0, vout, s)
-                     : launch_gemm<2, 128, 2, false>((int)M, (int)N, S, 1, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, 0, vout, s);
+      return c.tn == 3   ? launch_gemm<3, 128, 2, true>((int)M, (int)N, S, 1, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, 0, vout, s)
+             : c.tn == 2 ? launch_gemm<2, 128, 2, true>((int)M, (int)N, S, 1, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, 0, vout, s)
+                         : launch_gemm<1, 128, 2, true>((int)M, (int)N, S, 1, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, 0, vout, s);
+    return c.tn == 3   ? launch_gemm<3, 128, 2, false>((int)M, (int)N, S, 1, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, 0, vout, s)
+           : c.tn == 2 ? launch_gemm<2, 128, 2, false>((int)M, (int)N, S, 1, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, 0, vout, s)
+                       : launch_gemm<1, 128, 2, false>((int)M, (int)N, S, 1, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, 0, vout, s);
   }
   const size_t need = (size_t)c.nz * M * N * sizeof(float);
   if (!ws || ws_bytes < need || !aligned16(ws)) return fail(KF_EWORKSPACE, "gemm: split workspace of %zu bytes needed", need);
   const int vout = N % 4 == 0;
-  int rc = c.tn == 3 ? launch_gemm<3, 128, 2, true>((int)M, (int)N, S, c.nz, (const bf16*)A, lda, (const bf16*)B, ldb, ws, N, (long)M * N, vout, s)
-                     : launch_gemm<2, 128, 2, true>((int)M, (int)N, S, c.nz, (const bf16*)A, lda, (const bf16*)B, ldb, ws, N, (long)M * N, vout, s);
+  int rc = c.tn == 3   ? launch_gemm<3, 128, 2, true>((int)M, (int)N, S, c.nz, (const bf16*)A, lda, (const bf16*)B, ldb, ws, N, (long)M * N, vout, s)
+           : c.tn == 2 ? launch_gemm<2, 128, 2, true>((int)M, (int)N, S, c.nz, (const bf16*)A, lda, (const bf16*)B, ldb, ws, N, (long)M * N, vout, s)
+                       : launch_gemm<1, 128, 2, true>((int)M, (int)N, S, c.nz, (const bf16*)A, lda, (const bf16*)B, ldb, ws, N, (long)M * N, vout, s);
   if (rc) return rc;
   long blocks = ((long)M * ((N + 3) / 4) + 255) / 256;
   if (blocks > 65535 * 4) blocks = 65535 * 4;

@@ -21,6 +21,7 @@ GEMM_SHAPES = [
     (16384, 3072, 768), (16384, 768, 3072), (3072, 768, 16384), (768, 3072, 16384),  # GR-KAN
     (3072, 768 * 11, 512), (768, 3072 * 11, 512),  # the 512-token parity tests
     (300, 265 * 11, 1024), (8192, 3072, 768 * 9),
+    (8192, 768, 3072), (3072, 768, 8192),  # the fused SiLU base branch's g W and g^T silu(x)
 ]
 
 
@@ -39,9 +40,9 @@ def xcd_tile_grouped(g, n_m, n_n, GM=8):
 def pick_gemm(M, N, S):
     """kf_gemm_nt.hip pick_gemm: (tn, nz, tail_nz, full, rem)."""
     best, best_t = (3, 1, 0, 0, 0), 1e300
-    for tn in (3, 2):
+    for tn in (3, 2, 1):
         tiles = ((M + 255) // 256) * ((N + 128 * tn - 1) // (128 * tn))
-        t_stage = 256.0 * 128 * tn * 64 * 2 / 4.7e12
+        t_stage = 256.0 * 128 * tn * 64 * 2 / (4.0e12 if tn == 1 else 4.7e12)
         for nz in (1, 2, 3, 4, 6, 8, 10, 12, 16, 24, 32):
             if nz > S:
                 break
