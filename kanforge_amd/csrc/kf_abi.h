@@ -366,6 +366,8 @@ inline WsG ws_g(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64
 // F on the register-A kernel with silu(x) as the last feature of every chunk (T_0 taken out, so
 // n_t features a chunk: 9, or an even count of at least 6); layers narrow enough for F's
 // streaming routes keep those. P on p8_kernel (the order-1 descriptor), G on g96_kernel.
+// bf16 cubic B-splines with at most 11 basis functions: P on p8_kernel's 12 feature slots (W^T
+// in the first spare one), G on the GEMM core (features and silu(x) transposed); no F.
 inline bool f_base_route(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out) {
   if (!f_uses_rega(b, dtype) || b->order != 0) return false;
   if (!(b->n_t == 9 || (b->n_t % 2 == 0 && b->n_t >= 6))) return false;
@@ -373,12 +375,17 @@ inline bool f_base_route(const kf_basis* b, int dtype, int64_t batch, int64_t n_
   return !(batch >= 1024 && narrow);
 }
 inline bool p_base_route(const kf_basis* b1, int dtype, int64_t batch, int64_t n_in, int64_t n_out) {
-  return b1->kind == KF_KIND_CHEB && dtype == KF_BF16 && b1->order >= 1 && ws_p(b1, dtype, batch, n_in, n_out).p8;
+  if (dtype != KF_BF16 || b1->order < 1) return false;
+  const WsP w = ws_p(b1, dtype, batch, n_in, n_out);
+  if (b1->kind == KF_KIND_BSPLINE) return w.p12 && b1->size < 12;
+  return b1->kind == KF_KIND_CHEB && w.p8;
 }
 inline bool g_base_route(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out) {
-  if (b->kind != KF_KIND_CHEB || dtype != KF_BF16 || b->order != 0) return false;
+  if (dtype != KF_BF16 || b->order != 0) return false;
   const WsG w = ws_g(b, dtype, batch, n_in, n_out, false, true);
-  return w.g96 && w.skip0 && !w.pre;
+  // B-splines: features transposed input-major (the GEMM core's route of kf_G)
+  if (b->kind == KF_KIND_BSPLINE) return w.pre && w.BP % 64 == 0 && (n_in * b->size) % 8 == 0;
+  return b->kind == KF_KIND_CHEB && w.g96 && w.skip0 && !w.pre;
 }
 // workspace of kf_P_base: P's, one more coefficient row (W^T), hb = g W (float32) and the
 // GEMM core's split partial sums
@@ -386,26 +393,32 @@ struct WsPB {
   WsP p;
   size_t cfmt, hb, gemm, total;
 };
+// (B-splines: the spare feature slot holds W^T, no hb)
 inline WsPB ws_p_base(const kf_basis* b1, int dtype, int64_t batch, int64_t n_in, int64_t n_out) {
   WsPB w;
   w.p = ws_p(b1, dtype, batch, n_in, n_out);
-  w.cfmt = align256((size_t)(w.p.ntb + 1) * w.p.INP * w.p.OUTP * elt_size(dtype));
-  w.hb = align256((size_t)batch * n_in * sizeof(float));
-  w.gemm = gemm_nt_workspace(batch, n_in, w.p.OUTP);
+  const bool spare = b1->kind == KF_KIND_BSPLINE;
+  w.cfmt = align256((size_t)(w.p.ntb + (spare ? 0 : 1)) * w.p.INP * w.p.OUTP * elt_size(dtype));
+  w.hb = spare ? 0 : align256((size_t)batch * n_in * sizeof(float));
+  w.gemm = spare ? 0 : gemm_nt_workspace(batch, n_in, w.p.OUTP);
   w.total = w.cfmt + w.p.gpad + w.hb + w.gemm;
   return w;
 }
-// workspace of kf_G_base: G's, silu(x)^T (INP, BP) in bf16 and the GEMM core's partial sums
+// workspace of kf_G_base: G's, the column sums of g and their block partials (B-splines; the
+// Chebyshev layout has them), silu(x)^T (INP, BP) in bf16 and the GEMM core's partial sums
 struct WsGB {
   WsG g;
-  size_t st, gemm, total;
+  size_t part, colsum, st, gemm, total;
 };
 inline WsGB ws_g_base(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out) {
   WsGB w;
   w.g = ws_g(b, dtype, batch, n_in, n_out, false, true);
+  const bool own_sums = !w.g.skip0;
+  w.part = own_sums ? align256((size_t)((w.g.BP + 63) / 64) * w.g.OUTP * sizeof(float)) : 0;
+  w.colsum = own_sums ? align256((size_t)w.g.OUTP * sizeof(float)) : 0;
   w.st = align256((size_t)w.g.INP * w.g.BP * elt_size(dtype));
   w.gemm = gemm_nt_workspace(n_out, n_in, w.g.BP);
-  w.total = w.g.total + w.st + w.gemm;
+  w.total = w.g.total + w.part + w.colsum + w.st + w.gemm;
   return w;
 }
 

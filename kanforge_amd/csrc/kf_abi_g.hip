@@ -195,17 +195,57 @@ int run_G(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
 // column sums: the T_0 constant and the bias gradient), z^T and silu(x)^T in one prepass, G on
 // g96_kernel, and the base weights' gradient gT silu(x)^T on the GEMM core. dc, dbw and dbias may
 // each be NULL (not wanted).
+// B-splines: the transposed features (input-major rows) and the dc GEMM of kf_G's GEMM-core
+// route, with the column sums and silu(x)^T from one extra prepass.
+int run_G_base_bspline(const KBasis& kb, const WsGB& LB, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
+                       const void* g, void* dc, void* dbw, void* dbias, void* ws, hipStream_t s) {
+  const WsG& L = LB.g;
+  char* base = (char*)ws;
+  void* gt = base;
+  void* phit = base + L.gt + L.zt + L.wt + L.part + L.colsum;
+  void* gws = (char*)phit + L.phit + L.zpart;
+  float* part = (float*)(base + L.total);
+  float* colsum = (float*)(base + L.total + LB.part);
+  bf16* st = dbw ? (bf16*)(base + L.total + LB.part + LB.colsum) : nullptr;
+  void* gws2 = base + L.total + LB.part + LB.colsum + LB.st;
+  if (!aligned16(gt) || (dc && !aligned16(dc))) return fail(KF_EINVAL, "kf_G_base: arrays not 16-byte aligned");
+  dim3 tg((unsigned)((L.OUTP + 63) / 64), (unsigned)((L.BP + 63) / 64));
+  hipLaunchKernelGGL(transpose_kernel<bf16>, tg, dim3(kThreads), 0, s, (int)batch, (int)n_out, (int)L.BP, (int)L.OUTP,
+                     (int)rows_vec<bf16>(n_out, g), (const bf16*)g, (bf16*)gt, dbias ? part : nullptr);
+  int rc = check_launch("transpose");
+  if (rc) return rc;
+  if (st || dbias) {
+    const unsigned gx = (unsigned)((L.INP + 63) / 64), sblocks = dbias ? (unsigned)((L.OUTP + 7) / 8) : 0u;
+    dim3 zg(gx, (unsigned)((L.BP + 63) / 64) + (sblocks + gx - 1) / gx);
+    hipLaunchKernelGGL(zmapT_kernel<bf16>, zg, dim3(kThreads), (size_t)2 * 64 * 65 * sizeof(float), s, (int)batch,
+                       (int)n_in, (int)L.BP, (int)L.INP, kb.input_map, (int)rows_vec<bf16>(n_in, x), (const bf16*)x,
+                       (const bf16*)nullptr, (float*)nullptr, (float*)nullptr, (int)((L.BP + 63) / 64),
+                       dbias ? (int)L.OUTP : 0, part, colsum, st, (bf16*)dbias, (int)n_out);
+    rc = check_launch("silu transpose");
+    if (rc) return rc;
+  }
+  if (dc) {
+    rc = launch_features_t<bf16>(kb, batch, n_in, L.BP, L.INP, x, nullptr, phit, s, 1);
+    if (rc) return rc;
+    rc = gemm_nt(n_out, n_in * kb.K, L.BP, gt, L.BP, phit, L.BP, dc, n_in * kb.K, false, gws, L.gemm, s);
+    if (rc) return rc;
+  }
+  if (dbw) return gemm_nt(n_out, n_in, L.BP, gt, L.BP, st, L.BP, dbw, n_in, false, gws2, LB.gemm, s);
+  return KF_OK;
+}
+
 int run_G_base(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out,
                const void* x, const void* g, void* dc, void* dbw, void* dbias, void* ws, hipStream_t s) {
   const WsGB LB = ws_g_base(b, dtype, batch, n_in, n_out);
+  if (kb.kind == KF_KIND_BSPLINE) return run_G_base_bspline(kb, LB, batch, n_in, n_out, x, g, dc, dbw, dbias, ws, s);
   const WsG& L = LB.g;
   char* base = (char*)ws;
   void* gt = base;
   float* zt = (float*)(base + L.gt);
   float* part = (float*)(base + L.gt + L.zt + L.wt);
   float* colsum = (float*)(base + L.gt + L.zt + L.wt + L.part);
-  bf16* st = dbw ? (bf16*)(base + L.total) : nullptr;
-  void* gws = base + L.total + LB.st;
+  bf16* st = dbw ? (bf16*)(base + L.total + LB.part + LB.colsum) : nullptr;
+  void* gws = base + L.total + LB.part + LB.colsum + LB.st;
   if (!L.g96 || !L.skip0 || L.pre || L.BP % 64 || !aligned16(gt)) return fail(KF_EINVAL, "kf_G_base: layer not on g96");
   dim3 tg((unsigned)((L.OUTP + 63) / 64), (unsigned)((L.BP + 63) / 64));
   hipLaunchKernelGGL(transpose_kernel<bf16>, tg, dim3(kThreads), 0, s, (int)batch, (int)n_out, (int)L.BP, (int)L.OUTP,

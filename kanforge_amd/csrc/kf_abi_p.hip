@@ -68,9 +68,9 @@ int launch_p8(const WsP& L, hipStream_t s, const KBasis& kb, int64_t batch, int6
   const size_t lds = lds_ops > lds_epi ? lds_ops : lds_epi;
   // cubic B-splines on even knots (the common case): the support without the general-knot path
   const bool even = KIND == KF_KIND_BSPLINE && kb.knots_uniform && kb.n_knots >= 4;
-  auto kern = BASE ? p8_kernel<KIND, NF, TN, RB, 3, false, BASE>
-              : even ? p8_kernel<KIND, NF, TN, RB, 3, true> : p8_kernel<KIND, NF, TN, RB>;
-  if (BASE && (KIND == KF_KIND_BSPLINE || !hb)) return fail(KF_EINVAL, "P: the base term needs hb");
+  auto kern = even ? p8_kernel<KIND, NF, TN, RB, 3, true, BASE> : p8_kernel<KIND, NF, TN, RB, 3, false, BASE>;
+  if (BASE && (KIND == KF_KIND_BSPLINE ? kb.K >= NF : !hb))
+    return fail(KF_EINVAL, "P: the base term needs a spare feature slot (B-splines) or hb");
   if (L.INP % TI || L.OUTP % (RB / 2)) return fail(KF_EINVAL, "P: workspace layout not aligned");
   if (!reserve_lds((const void*)kern, lds))
     return fail(KF_ELAUNCH, "P: cannot reserve %zu bytes of LDS", lds);
@@ -168,7 +168,8 @@ bool rational_bwd_fuses(const KBasis& kb, int dtype, int64_t n_in, const void* x
 }
 // The layer's input gradient with its SiLU base branch: the coefficients folded feature-major
 // with W^T as one more row, hb = g W on the GEMM core (float32), then p8_kernel, whose epilogue
-// adds silu'(x) hb.
+// adds silu'(x) hb; B-splines put W^T in the tile's last feature slot instead, so the same GEMM
+// yields g W next to the feature sums.
 int run_P_base(const KBasis& kb, const kf_basis* b1, int dtype, int64_t batch, int64_t n_in, int64_t n_out,
                const void* x, const void* g, const void* c, const void* bw, void* p, void* ws, hipStream_t s) {
   const WsPB LB = ws_p_base(b1, dtype, batch, n_in, n_out);
@@ -177,7 +178,11 @@ int run_P_base(const KBasis& kb, const kf_basis* b1, int dtype, int64_t batch, i
   void* cfmt = base;
   float* hb = (float*)(base + LB.cfmt + L.gpad);
   void* gws = base + LB.cfmt + L.gpad + LB.hb;
-  int rc = launch_permute<bf16>(kb, n_out, n_in, L.OUTP, L.INP, L.ntb, c, cfmt, kPermFMT, s, 0, nullptr, bw);
+  // B-splines: the folded features and zero rows up to the last slot, W^T in it; Chebyshev: W^T
+  // after the features (the B operand of hb = g W)
+  const bool spare = kb.kind == KF_KIND_BSPLINE;
+  int rc = launch_permute<bf16>(kb, n_out, n_in, L.OUTP, L.INP, spare ? L.ntb - 1 : L.ntb, c, cfmt, kPermFMT, s, 0,
+                                nullptr, bw);
   if (rc) return rc;
   const void* ga = g;
   int gstride = (int)n_out;
@@ -194,6 +199,7 @@ int run_P_base(const KBasis& kb, const kf_basis* b1, int dtype, int64_t batch, i
     ga = gp;
     gstride = (int)L.OUTP;
   }
+  if (spare) return launch_p8<KF_KIND_BSPLINE, 12, 3, 128, true>(L, s, kb, batch, n_in, x, ga, gstride, cfmt, p);
   const bf16* wt = (const bf16*)cfmt + (size_t)L.ntb * L.INP * L.OUTP;  // W^T (INP, OUTP), zero padded
   rc = gemm_nt(batch, n_in, L.OUTP, ga, gstride, wt, L.OUTP, hb, n_in, true, gws, LB.gemm, s);
   if (rc) return rc;

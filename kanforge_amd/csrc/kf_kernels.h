@@ -597,7 +597,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void f_kernel(int B, int OUT
 // Block rows past BP / 64 total partial sums instead (sum_parts_block), when part is given.
 // With st given (unweighted only: it takes wt's LDS tile), also silu(x) transposed into st
 // (INP, BP) in T, zero padded: the B operand of the SiLU base branch's weight gradient; with
-// dsum given, the sums of its n_dsum outputs also go there in T.
+// dsum given, the sums of its n_dsum outputs also go there in T. zt may be NULL (st alone).
 template <typename T>
 __global__ __launch_bounds__(kThreads) void zmapT_kernel(int B, int IN, int BP, int INP, int input_map, int vin,
                                                          const T* __restrict__ x, const T* __restrict__ w,
@@ -674,7 +674,7 @@ __global__ __launch_bounds__(kThreads) void zmapT_kernel(int B, int IN, int BP, 
     const int i = i0 + r, bl = (threadIdx.x % 16) * 4, b = b0 + bl;
     if (i < INP && b < BP) {
       f32x4 v = {tz[bl * 65 + r], tz[(bl + 1) * 65 + r], tz[(bl + 2) * 65 + r], tz[(bl + 3) * 65 + r]};
-      gstore16(zt + (size_t)i * BP + b, __builtin_bit_cast(u32x4, v));
+      if (zt) gstore16(zt + (size_t)i * BP + b, __builtin_bit_cast(u32x4, v));
       if (wt) {
         f32x4 u = {tw[bl * 65 + r], tw[(bl + 1) * 65 + r], tw[(bl + 2) * 65 + r], tw[(bl + 3) * 65 + r]};
         gstore16(wt + (size_t)i * BP + b, __builtin_bit_cast(u32x4, u));
@@ -1962,8 +1962,9 @@ __global__ __launch_bounds__(256) void p_dma_kernel(KBasis bs, int B, int IN, in
 // passes of RPASS rows: the feature sums H_j go to LDS and every thread forms
 // p[b, i] = sum_j f_j(x[b, i]) H_j[b, i] for (row, input) pairs, the features computed once per
 // pair.
-// BASE (kinds other than B-splines): p[b, i] also gets silu'(x[b, i]) hb[b, i], hb (B, IN) float32
-// = g W, the input gradient of the SiLU base branch.
+// BASE: p[b, i] also gets silu'(x[b, i]) (g W)[b, i], the input gradient of the SiLU base branch:
+// B-splines carry W^T as the coefficient rows of the last feature slot, NF - 1 >= K (a slot the
+// tile computes anyway), other kinds read hb (B, IN) float32 = g W.
 template <int KIND, int NF, int TN, int RB, int KD = 3, bool EVEN = false, bool BASE = false>
 __global__ __launch_bounds__(512) void p8_kernel(KBasis bs, int B, int IN, int INP, int OUTP,
                                                  const bf16* __restrict__ x, const bf16* __restrict__ g, int gstride,
@@ -2058,7 +2059,6 @@ __global__ __launch_bounds__(512) void p8_kernel(KBasis bs, int B, int IN, int I
   constexpr int EPT = RPASS * TI / 2 / 512;
   static_assert(EPT * 512 == RPASS * TI / 2, "whole epilogue rounds");
   constexpr bool FIXED_INPUTS = KIND == KF_KIND_BSPLINE && 512 % (TI / 2) == 0;
-  static_assert(!(BASE && KIND == KF_KIND_BSPLINE), "the base term rides the other kinds' epilogue");
   const int il_t = 2 * (tid % (TI / 2)), i_t = i0 + il_t;
   float* kus = kps + TI * (bs.n_knots + 2 * bs.spline_k);  // [TI][2]
   // every pass's x values (EPT items per pass), loaded before the passes (addresses clamped into
@@ -2098,7 +2098,7 @@ __global__ __launch_bounds__(512) void p8_kernel(KBasis bs, int B, int IN, int I
       // clamped into x, so the loads need no branch and their latency passes behind the stores)
       constexpr int EPG = (RPASS * TI / 2 + 511) / 512;
       uint32_t xg[FIXED_INPUTS ? 1 : EPG];
-      float hg[BASE ? EPG : 1][2];
+      float hg[BASE && KIND != KF_KIND_BSPLINE ? EPG : 1][2];
       if constexpr (!FIXED_INPUTS) {
         const unsigned short* xs = reinterpret_cast<const unsigned short*>(x);
 #pragma unroll
@@ -2108,7 +2108,7 @@ __global__ __launch_bounds__(512) void p8_kernel(KBasis bs, int B, int IN, int I
           const size_t o = (size_t)(b < B ? b : B - 1) * IN;
           const size_t i_0 = i < IN ? i : IN - 1, i_1 = i + 1 < IN ? i + 1 : IN - 1;
           xg[k] = (uint32_t)xs[o + i_0] | (uint32_t)xs[o + i_1] << 16;
-          if constexpr (BASE) {
+          if constexpr (BASE && KIND != KF_KIND_BSPLINE) {
             hg[k][0] = hb[o + i_0];
             hg[k][1] = hb[o + i_1];
           }
@@ -2159,6 +2159,7 @@ __global__ __launch_bounds__(512) void p8_kernel(KBasis bs, int B, int IN, int I
             for (int r = 0; r <= KD; ++r)
               if (st == 1 && base + r >= 0 && base + r < bs.K)
                 v[u] = fmaf(red[((base + r) * RPASS + row) * RP + ilu], N[r], v[u]);
+            if constexpr (BASE) v[u] = fmaf(red[((NF - 1) * RPASS + row) * RP + ilu], dsilu_f(xv), v[u]);
             if (st == 2) v[u] = __builtin_nanf("");
           }
           if (b < B && i_t < IN) store_pair(b, i_t, v);
@@ -2187,15 +2188,15 @@ __global__ __launch_bounds__(512) void p8_kernel(KBasis bs, int B, int IN, int I
 #pragma unroll
                 for (int r = 0; r <= KD; ++r)
                   if (base + r >= 0 && base + r < bs.K) v[u] = fmaf(red[((base + r) * RPASS + row) * RP + ilu], N[r], v[u]);
-              } else if (st == 2) {
-                v[u] = __builtin_nanf("");
               }
+              if constexpr (BASE) v[u] = fmaf(red[((NF - 1) * RPASS + row) * RP + ilu], dsilu_f(xv), v[u]);
+              if (st == 2) v[u] = __builtin_nanf("");
             } else {
               float f[NF];
               kind_features<KIND, NF>(xv, 1.f, i + u, bs, f);
 #pragma unroll
               for (int q = 0; q < NF; ++q) v[u] = fmaf(red[(q * RPASS + row) * RP + il + u], f[q], v[u]);
-              if constexpr (BASE) v[u] = fmaf(dsilu_f(xv), hg[k][u], v[u]);
+              if constexpr (BASE && KIND != KF_KIND_BSPLINE) v[u] = fmaf(dsilu_f(xv), hg[k][u], v[u]);
             }
           }
           store_pair(b, i, v);

@@ -954,25 +954,28 @@ def bspline_interval(x: torch.Tensor, knots_cmp: torch.Tensor) -> torch.Tensor:
 # --- the SiLU base branch and bias fused into the contractions ----------------------
 #
 # The reference's layer adds F.linear(silu(x), base_weight) and the bias to the spline part
-# (kanforge/torch/layers.py:185-191); for bf16 Chebyshev plans kf_F_base runs silu(x) as one more
+# (kanforge/torch/layers.py:185-191). For bf16 Chebyshev plans kf_F_base runs silu(x) as one more
 # feature of the F contraction and folds the bias into its per-output constant, kf_P_base adds
 # silu'(x) (g W) in P's epilogue and kf_G_base returns the base weights' and the bias's gradients
-# next to the coefficient gradient.
+# next to the coefficient gradient; bf16 cubic B-splines fuse P (W^T in a spare feature slot) and
+# G, and keep F plus one GEMM for the forward.
 
 _FUSED: dict = {}
 
 
-def base_fused(plan: KernelPlan | str, dtype: torch.dtype, batch: int, n_in: int, n_out: int) -> tuple[bool, bool, bool]:
-    """Whether (kf_F_base, kf_P_base, kf_G_base) take a layer of this plan and these shapes."""
+def base_fused(plan: KernelPlan | str, st: BasisState | None, dtype: torch.dtype, batch: int, n_in: int,
+               n_out: int) -> tuple[bool, bool, bool]:
+    """Whether (kf_F_base, kf_P_base, kf_G_base) take a layer of this plan and these shapes (the
+    routes depend on the plan and the shapes, not on the basis tables)."""
     key = (plan_key(plan), dtype, batch, n_in, n_out)
     hit = _FUSED.get(key)
     if hit is None:
         pl = plan_of(key[0])
         hit = (False, False, False)
-        if pl.kind == "cheb" and dtype == torch.bfloat16 and batch > 0:
+        if pl.kind in ("cheb", "bspline") and dtype == torch.bfloat16 and batch > 0:
             lib = _lib.load()
-            d0, _ = _desc(pl, 0, None)
-            d1, _ = _desc(pl, 1, None)
+            d0, _ = _desc(pl, 0, st)
+            d1, _ = _desc(pl, 1, st)
             q = lambda op, d: lib.kf_base_fused(op, ctypes.byref(d), _lib.KF_BF16, batch, n_in, n_out) == 1
             hit = (q(_lib.KF_OP_F_BASE, d0), q(_lib.KF_OP_P_BASE, d1), q(_lib.KF_OP_G_BASE, d0))
         if len(_FUSED) > 4096:
@@ -986,18 +989,25 @@ def _dsilu(x: torch.Tensor) -> torch.Tensor:
     return s * (1 + x * (1 - s))
 
 
-def _F_base_impl(x: torch.Tensor, c: torch.Tensor, bw: torch.Tensor, bias: Opt, plan: str) -> torch.Tensor:
-    """y = F_0(x, c) + silu(x) bw^T + bias: the layer's forward with its SiLU base branch."""
+def _F_base_impl(x: torch.Tensor, c: torch.Tensor, bw: torch.Tensor, bias: Opt, knots: Opt, knots_cmp: Opt, knots_u: Opt,
+                 plan: str) -> torch.Tensor:
+    """y = F_0(x, c) + silu(x) bw^T + bias: the layer's forward with its SiLU base branch (kf_F_base
+    where it takes the layer, else kf_F and one GEMM)."""
     _require_device(x)
-    lib = _lib.load()
     pl = plan_of(plan)
-    desc, keep = _desc(pl, 0, None)
+    st = _state(knots, knots_cmp, knots_u, None, None, x.shape[1])
     batch, n_in = x.shape
     n_out = c.shape[0]
-    dev = x.device
-    dt = _dtype_code(x.dtype)
     x, c, bw = x.contiguous(), c.contiguous(), bw.contiguous()
     bias = None if bias is None else bias.contiguous()
+    if not base_fused(pl, st, x.dtype, batch, n_in, n_out)[0]:
+        y = _raw("F", pl, 0, x, None, c, st, n_out)
+        y = torch.addmm(y, torch.nn.functional.silu(x), bw.t())
+        return y if bias is None else y.add_(bias)
+    lib = _lib.load()
+    desc, keep = _desc(pl, 0, st)
+    dev = x.device
+    dt = _dtype_code(x.dtype)
     y = torch.empty(batch, n_out, dtype=x.dtype, device=dev)
     ws = _workspace(_lib.KF_OP_F_BASE, desc, dt, batch, n_in, n_out, dev)
     with _on(dev):
@@ -1012,15 +1022,17 @@ op_F_base = torch.library.custom_op("kf::F_base", mutates_args=())(_F_base_impl)
 
 
 @op_F_base.register_fake
-def _(x, c, bw, bias, plan):
+def _(x, c, bw, bias, knots, knots_cmp, knots_u, plan):
     return x.new_empty(x.shape[0], c.shape[0])
 
 
-def _P_base_impl(x: torch.Tensor, g: torch.Tensor, c: torch.Tensor, bw: torch.Tensor, plan: str) -> torch.Tensor:
+def _P_base_impl(x: torch.Tensor, g: torch.Tensor, c: torch.Tensor, bw: torch.Tensor, knots: Opt, knots_cmp: Opt,
+                 knots_u: Opt, plan: str) -> torch.Tensor:
     """P_1(x, g, c) + silu'(x) (g bw): the layer's input gradient with its SiLU base branch."""
     _require_device(x)
     lib = _lib.load()
-    desc, keep = _desc(plan_of(plan), 1, None)
+    st = _state(knots, knots_cmp, knots_u, None, None, x.shape[1])
+    desc, keep = _desc(plan_of(plan), 1, st)
     batch, n_in = x.shape
     n_out = c.shape[0]
     dev = x.device
@@ -1040,17 +1052,19 @@ op_P_base = torch.library.custom_op("kf::P_base", mutates_args=())(_P_base_impl)
 
 
 @op_P_base.register_fake
-def _(x, g, c, bw, plan):
+def _(x, g, c, bw, knots, knots_cmp, knots_u, plan):
     return x.new_empty(x.shape)
 
 
-def _G_base_impl(x: torch.Tensor, g: torch.Tensor, plan: str, want_c: bool, want_w: bool, want_b: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+def _G_base_impl(x: torch.Tensor, g: torch.Tensor, knots: Opt, knots_cmp: Opt, knots_u: Opt, plan: str, want_c: bool,
+                 want_w: bool, want_b: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """(G_0(x, g), g^T silu(x), sum_b g): the layer's parameter gradients with its SiLU base branch
     and bias; an output not wanted comes back empty."""
     _require_device(x)
     lib = _lib.load()
     pl = plan_of(plan)
-    desc, keep = _desc(pl, 0, None)
+    st = _state(knots, knots_cmp, knots_u, None, None, x.shape[1])
+    desc, keep = _desc(pl, 0, st)
     batch, n_in = x.shape
     n_out = g.shape[1]
     dev = x.device
@@ -1072,41 +1086,46 @@ op_G_base = torch.library.custom_op("kf::G_base", mutates_args=())(_G_base_impl)
 
 
 @op_G_base.register_fake
-def _(x, g, plan, want_c, want_w, want_b):
+def _(x, g, knots, knots_cmp, knots_u, plan, want_c, want_w, want_b):
     n_out, n_in, K = g.shape[1], x.shape[1], plan_of(plan).size
     return (x.new_empty((n_out, n_in, K) if want_c else (0,)), x.new_empty((n_out, n_in) if want_w else (0,)),
             x.new_empty((n_out,) if want_b else (0,)))
 
 
 def _F_base_setup(ctx, inputs, output):
-    x, c, bw, bias, plan = inputs
-    ctx.save_for_backward(x, c, bw)
+    x, c, bw, bias, knots, knots_cmp, knots_u, plan = inputs
+    ctx.save_for_backward(x, c, bw, knots, knots_cmp, knots_u)
     ctx.plan = plan
     ctx.bias_dtype = None if bias is None else bias.dtype
 
 
 def _F_base_backward(ctx, gy):
-    x, c, bw = ctx.saved_tensors
+    x, c, bw, knots, knots_cmp, knots_u = ctx.saved_tensors
     plan = ctx.plan
     need = ctx.needs_input_grad
     gy = gy.contiguous()
     gx = gc = gw = gb = None
-    nones = (None, None, None, None, None)
-    fused = (False, False, False) if torch.is_grad_enabled() else base_fused(plan, x.dtype, x.shape[0], x.shape[1], c.shape[0])
+    tabs = (knots, knots_cmp, knots_u)
+    rat = (None, None)
+    if torch.is_grad_enabled():
+        fused = (False, False, False)
+    else:
+        st = _state(knots, knots_cmp, knots_u, None, None, x.shape[1])
+        fused = base_fused(plan, st, x.dtype, x.shape[0], x.shape[1], c.shape[0])
     if need[0]:
         if fused[1]:
-            gx = _P_BASE(x, gy, c, bw, plan)
+            gx = _P_BASE(x, gy, c, bw, *tabs, plan)
         else:  # differentiable composition (also under create_graph)
-            gx = _P(x, gy, c, *nones, plan, 1) + _dsilu(x) * (gy @ bw)
+            gx = _P(x, gy, c, *tabs, *rat, plan, 1) + _dsilu(x) * (gy @ bw)
     if need[1] or need[2] or need[3]:
         if fused[2]:
-            dc, dw, db = _G_BASE(x, gy, plan, need[1], need[2], need[3])
+            dc, dw, db = _G_BASE(x, gy, *tabs, plan, need[1], need[2], need[3])
             gc, gw, gb = (dc if need[1] else None), (dw if need[2] else None), (db if need[3] else None)
         else:
-            gc = _G(x, gy, None, *nones, plan, 0) if need[1] else None
+            gc = _G(x, gy, None, *tabs, *rat, plan, 0) if need[1] else None
             gw = gy.t() @ torch.nn.functional.silu(x) if need[2] else None
             gb = _COLSUM(gy).to(ctx.bias_dtype) if need[3] else None
-    return gx, gc, gw, gb, None
+    return gx, gc, gw, gb, None, None, None, None
 
 
 op_F_base.register_autograd(_F_base_backward, setup_context=_F_base_setup)
@@ -1124,11 +1143,12 @@ class _Direct:
 
 
 def spline_base_forward(x: torch.Tensor, coef: torch.Tensor, base_w: torch.Tensor, bias: torch.Tensor | None,
-                        plan: KernelPlan | str) -> torch.Tensor:
-    """The layer's spline part, SiLU base branch and bias in one contraction (kf_F_base); x (..., in),
-    everything in x's dtype. Callers check base_fused first."""
+                        st: BasisState | None, plan: KernelPlan | str) -> torch.Tensor:
+    """The layer's spline part, SiLU base branch and bias as one op whose forward and backward use
+    the fused entry points where they take the layer; x (..., in), everything in x's dtype.
+    Callers check base_fused first."""
     lead = x.shape[:-1]
-    y = _F_BASE(x.reshape(-1, x.shape[-1]), coef, base_w, bias, plan_key(plan))
+    y = _F_BASE(x.reshape(-1, x.shape[-1]), coef, base_w, bias, *_tables(st), plan_key(plan))
     return y.reshape(*lead, coef.shape[0])
 
 

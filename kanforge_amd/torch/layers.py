@@ -3,9 +3,11 @@
 Same constructor, parameter names, shapes and ``state_dict`` layout as
 kanforge/torch/layers.py (KANLinear :28-116, GRKAN :335-363, KAN :366-398),
 so checkpoints and ``kanforge.save`` files move between the two unchanged.
-The spline branch always takes the fused HIP path (libkfhip.so); the base
-branch F.linear(silu(x), W * mask) and the bias are torch ops on the same
-device.
+The spline branch always takes the fused HIP path (libkfhip.so). The base
+branch F.linear(silu(x), W * mask) and the bias join the contractions for
+bf16 Chebyshev and cubic B-spline layers with a SiLU base (kf_F_base,
+kf_P_base, kf_G_base, where the library takes the shapes); otherwise they
+are torch ops on the same device.
 """
 
 from __future__ import annotations
@@ -218,7 +220,7 @@ class KANLinear(nn.Module):
         st = self._basis_state()
         if self._base_fused(x):
             # spline part, SiLU base branch and bias in one contraction (and one backward pass)
-            y = _kernels.spline_base_forward(x, self.effective_coef(), self.effective_base_weight(), self.bias,
+            y = _kernels.spline_base_forward(x, self.effective_coef(), self.effective_base_weight(), self.bias, st,
                                              self._plan_key)
             return y + self._symbolic_sum(x) if self._sym_codes else y
         if self._plan.kind == "rational":
@@ -238,9 +240,10 @@ class KANLinear(nn.Module):
         return y
 
     def _base_fused(self, x: torch.Tensor) -> bool:
-        """Whether forward runs the spline part, the SiLU base branch and the bias as one fused
-        kernel call (bf16 Chebyshev plans on their contraction kernels, eager)."""
-        if self.base_weight is None or self.base_activation is not F.silu or self._plan.kind != "cheb":
+        """Whether forward runs the spline part, the SiLU base branch and the bias as one op whose
+        kernels fuse the base branch (bf16 Chebyshev and cubic B-spline plans on their contraction
+        kernels, eager)."""
+        if self.base_weight is None or self.base_activation is not F.silu or self._plan.kind not in ("cheb", "bspline"):
             return False
         dt = torch.bfloat16
         if x.dtype != dt or self.coef.dtype != dt or self.base_weight.dtype != dt:
@@ -248,7 +251,7 @@ class KANLinear(nn.Module):
         if (self.bias is not None and self.bias.dtype != dt) or _compiling() or x.dim() < 1:
             return False
         batch = x.numel() // max(self.in_features, 1)
-        return _kernels.base_fused(self._plan_key, dt, batch, self.in_features, self.out_features)[0]
+        return any(_kernels.base_fused(self._plan_key, self._basis_state(), dt, batch, self.in_features, self.out_features))
 
     def uses_kernel(self, device: torch.device) -> bool:
         """Whether forward runs the fused kernel on ``device`` (always, or an error)."""

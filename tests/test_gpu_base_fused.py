@@ -1,7 +1,7 @@
 """KANLinear with its SiLU base branch and bias fused into the HIP contractions (kf_F_base,
 kf_P_base, kf_G_base) against the float64 oracle: y and every first-order gradient on layers
 whose three entries all fuse (Chebyshev degrees 8, 7 and 5: chunks of 9 features, and even counts
-on the runtime-count F kernel), ragged shapes (inputs not a multiple of 16, outputs not of 8,
+on the runtime-count F kernel) and on cubic B-spline layers (P and G fused), ragged shapes (inputs not a multiple of 16, outputs not of 8,
 batch not of 64), the headline shape 768 -> 3072 at batch 8192 against a plain PyTorch float32
 reference, double backward through the fused layer (its backward composes differentiable ops
 there) against the unfused layer, the routes the library reports, and bitwise determinism.
@@ -43,6 +43,16 @@ def make_layer(deg, IN, OUT, seed=0, edge_scale=False, bias=True):
     return layer.to(device=DEV, dtype=BF)
 
 
+def make_spline_layer(IN, OUT, grid=8, seed=0, grid_range=(-3.0, 3.0)):
+    torch.manual_seed(seed)
+    layer = KANLinear(IN, OUT, kf.BSpline(grid, 3, grid_range=grid_range))
+    with torch.no_grad():
+        layer.coef.normal_(0, 0.5 / math.sqrt(IN))
+        layer.base_weight.normal_(0, 1 / math.sqrt(IN))
+        layer.bias.normal_()
+    return layer.to(device=DEV, dtype=BF)
+
+
 def unfused(layer):
     """The same layer on the unfused route (F, P, G plus torch base-branch ops)."""
     layer._base_fused = lambda x: False
@@ -51,11 +61,13 @@ def unfused(layer):
 
 def test_routes_reported_by_the_library():
     plan = make_layer(8, 48, 8)._plan_key
-    assert K.base_fused(plan, BF, 8192, 768, 3072) == (True, True, True)
-    assert K.base_fused(plan, torch.float32, 8192, 768, 3072) == (False, False, False)
-    assert not K.base_fused(plan, BF, 4096, 64, 4)[0]  # narrow: F's streaming route
+    assert K.base_fused(plan, None, BF, 8192, 768, 3072) == (True, True, True)
+    assert K.base_fused(plan, None, torch.float32, 8192, 768, 3072) == (False, False, False)
+    assert not K.base_fused(plan, None, BF, 4096, 64, 4)[0]  # narrow: F's streaming route
     plan6 = make_layer(6, 48, 8)._plan_key  # 7 features a chunk: not fused
-    assert not K.base_fused(plan6, BF, 8192, 768, 3072)[0]
+    assert not K.base_fused(plan6, None, BF, 8192, 768, 3072)[0]
+    sp = make_spline_layer(768, 3072)  # cubic B-splines: P and G fused, F composed
+    assert K.base_fused(sp._plan_key, sp._basis_state(), BF, 16384, 768, 3072) == (False, True, True)
 
 
 # (batch, in, out, degree): every case has >= 128 G tiles of 192 x 48 (g96_kernel)
@@ -70,7 +82,7 @@ CASES = [
 @pytest.mark.parametrize("B,IN,OUT,deg", CASES)
 def test_fused_layer_against_oracle(B, IN, OUT, deg):
     layer = make_layer(deg, IN, OUT, edge_scale=True)
-    fused = K.base_fused(layer._plan_key, BF, B, IN, OUT)
+    fused = K.base_fused(layer._plan_key, None, BF, B, IN, OUT)
     print(f"case B={B} in={IN} out={OUT} deg={deg} fused={fused}", flush=True)
     assert fused[0] and fused[2]
     assert fused[1] == (deg != 5)
@@ -101,6 +113,38 @@ def test_fused_layer_against_oracle(B, IN, OUT, deg):
         assert err <= TOL, (key, err)
 
 
+@pytest.mark.parametrize("B,IN,OUT,grid", [(300, 768, 200, 8), (257, 136, 300, 8)])
+def test_fused_bspline_layer_against_oracle(B, IN, OUT, grid):
+    """Cubic B-splines on 8 intervals (11 basis functions, P's 12-slot tiles): P with W^T in the
+    spare feature slot, G with dW on the GEMM core, F composed; the second shape is ragged."""
+    layer = make_spline_layer(IN, OUT, grid)
+    fused = K.base_fused(layer._plan_key, layer._basis_state(), BF, B, IN, OUT)
+    print(f"B-spline case B={B} in={IN} out={OUT} grid={grid} fused={fused}", flush=True)
+    assert fused == (False, True, True)
+    ob = oracle_basis(layer.basis, IN, {"grid": np64(layer.basis_grid)})
+    rng = np.random.default_rng(B)
+    x0 = rng.normal(0, 1.2, (B, IN))
+    gy0 = rng.normal(0, 1, (B, OUT))
+    x = torch.as_tensor(x0, dtype=torch.float32).to(DEV, BF).requires_grad_()
+    gy = torch.as_tensor(gy0, dtype=torch.float32).to(DEV, BF)
+    y = layer(x)
+    y.backward(gy)
+    torch.cuda.synchronize()
+    xr, gyr = rounded(x0, BF), rounded(gy0, BF)
+    c, W, b = np64(layer.coef), np64(layer.base_weight), np64(layer.bias)
+    checks = {
+        "y": (y, o.kan_linear(xr, c, ob, W, b)),
+        "x": (x.grad, o.prim_P(xr, gyr, c, ob, 1) + (gyr @ W) * o.silu_derivative(xr, 1)),
+        "coef": (layer.coef.grad, o.prim_G(xr, gyr, None, ob, 0)),
+        "base_weight": (layer.base_weight.grad, gyr.T @ o.silu_derivative(xr, 0)),
+        "bias": (layer.bias.grad, gyr.sum(0)),
+    }
+    for key, (got, want) in checks.items():
+        err = o.normwise_err(np64(got), want)
+        print(f"  {key}: {err:.3e}", flush=True)
+        assert err <= TOL, (key, err)
+
+
 def test_headline_shape_with_base_and_bias():
     """768 -> 3072 Chebyshev(8), batch 8192: y, dX, dCoef, dW, db against float32 torch."""
     B, IN, OUT, KB = 8192, 768, 3072, 9
@@ -109,7 +153,7 @@ def test_headline_shape_with_base_and_bias():
     with torch.no_grad():
         layer.coef.copy_(torch.randn(OUT, IN, KB, device=DEV) / math.sqrt(IN * KB))
         layer.bias.normal_()
-    assert K.base_fused(layer._plan_key, BF, B, IN, OUT) == (True, True, True)
+    assert K.base_fused(layer._plan_key, None, BF, B, IN, OUT) == (True, True, True)
     x = torch.randn(B, IN, device=DEV).to(BF).requires_grad_()
     gy = torch.randn(B, OUT, device=DEV).to(BF)
     y = layer(x)
