@@ -45,6 +45,32 @@ STEP_FLOP = 3 * FLOP_PER_CONTRACTION
 PEAK_BF16 = 2.5e15  # MI355X dense bf16 MFMA, FLOP/s
 
 
+def with_base_leg(layer, x, gy, args, dev) -> dict:
+    """The headline layer with its defaults (SiLU base branch and bias on): the same step plus the
+    base branch's three products (2 B in out FLOP each: forward, dX and dW, 0.116 TFLOP more),
+    fused into the contractions where the kernels take the layer."""
+    import kanforge_amd as kf
+    from kanforge_amd.torch import KANLinear
+    from kanforge_amd.torch import kernels as K
+
+    base = KANLinear(IN, OUT, kf.Chebyshev(DEGREE), device=dev, dtype=torch.bfloat16)
+    with torch.no_grad():
+        base.coef.copy_(layer.coef)
+
+    def step_base():
+        y = base(x)
+        return torch.autograd.grad(y, [x, base.coef, base.base_weight, base.bias], gy)
+
+    ms_base = _timed(step_base, args.steps, args.warmup)
+    return {
+        "layer": "KANLinear(768, 3072, Chebyshev(8)) defaults: SiLU base branch, bias",
+        "ms_per_step": ms_base,
+        "value": B / (ms_base * 1e-3),
+        "tflops": (STEP_FLOP + 3 * 2.0 * B * IN * OUT) / (ms_base * 1e-3) / 1e12,
+        "fused_entries": dict(zip(("F", "P", "G"), K.base_fused(base._plan_key, None, torch.bfloat16, B, IN, OUT))),
+    }
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -55,8 +81,9 @@ def parse():
     ap.add_argument(
         "--workload",
         default="cheb768",
-        choices=["cheb768", *WORKLOADS, "all"],
-        help="cheb768 (default) is the headline line; the others time the remaining layer shapes one line each",
+        choices=["cheb768", "cheb768_base", *WORKLOADS, "all"],
+        help="cheb768 (default) is the headline line; cheb768_base times only its default-layer (SiLU base "
+        "branch and bias) leg; the others time the remaining layer shapes one line each",
     )
     ap.add_argument("--no-workloads", action="store_true", help="leave the other layer shapes out of the headline line")
     ap.add_argument("--workload-steps", type=int, default=10, help="timed steps of each other layer shape in the headline line")
@@ -649,17 +676,17 @@ def main():
     if args.only:
         print(json.dumps(run_only(args.workload, args.only, args, dev)), flush=True)
         return
-    if args.workload != "cheb768":
+    if args.workload not in ("cheb768", "cheb768_base"):
         for name in WORKLOADS if args.workload == "all" else [args.workload]:
             print(json.dumps(run_workload(name, args, dev, cpu=not args.no_cpu)), flush=True)
         return
 
-    import kanforge_amd as kf
-    from kanforge_amd.torch import KANLinear
-
     timer = EntryTimer()
-    unhook = _hook_entries(timer)
     layer, x, gy = headline_layer(dev)
+    if args.workload == "cheb768_base":
+        print(json.dumps(with_base_leg(layer, x, gy, args, dev)), flush=True)
+        return
+    unhook = _hook_entries(timer)
 
     def step():
         y = layer(x)
@@ -672,31 +699,8 @@ def main():
 
     with_base = None
     if not args.no_base:
-        # the default layer (SiLU base branch and bias on): the same step plus the base GEMMs
-        # (2 * B * in * out per contraction, forward, dX and dW: 0.116 TFLOP more)
-        base = KANLinear(IN, OUT, kf.Chebyshev(DEGREE), device=dev, dtype=torch.bfloat16)
-        with torch.no_grad():
-            base.coef.copy_(layer.coef)
-
-        def step_base():
-            y = base(x)
-            return torch.autograd.grad(y, [x, base.coef, base.base_weight, base.bias], gy)
-
-        for _ in range(args.warmup):
-            step_base()
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-        for _ in range(args.steps):
-            step_base()
-        torch.cuda.synchronize()
-        ms_base = (time.perf_counter() - t1) / args.steps * 1e3
-        with_base = {
-            "layer": "KANLinear(768, 3072, Chebyshev(8)) defaults: SiLU base branch, bias",
-            "ms_per_step": ms_base,
-            "value": B / (ms_base * 1e-3),
-            "tflops": (STEP_FLOP + 3 * 2.0 * B * IN * OUT) / (ms_base * 1e-3) / 1e12,
-            "ratio_to_pure_step": ms_base / ms,
-        }
+        with_base = with_base_leg(layer, x, gy, args, dev)
+        with_base["ratio_to_pure_step"] = with_base["ms_per_step"] / ms
     dominant = max(per_op, key=per_op.get)
     achieved = FLOP_PER_CONTRACTION / (per_op[dominant] * 1e-3) / 1e12
     out = {
