@@ -87,7 +87,8 @@ def parse():
     )
     ap.add_argument("--no-workloads", action="store_true", help="leave the other layer shapes out of the headline line")
     ap.add_argument("--workload-steps", type=int, default=10, help="timed steps of each other layer shape in the headline line")
-    ap.add_argument("--only", choices=["F", "G", "P", "edge", "features", "rational_param_grad", "rational_bwd", "lut"],
+    ap.add_argument("--only", choices=["F", "G", "P", "F_base", "P_base", "G_base", "edge", "features", "rational_param_grad",
+                                       "rational_bwd", "lut"],
                     help="counter runs: replay only this entry point's calls of one step of --workload")
     return ap.parse_args()
 
@@ -114,6 +115,26 @@ def _work(label, args):
         else:
             elems = 2 * batch * n_in + batch * n_out + coef
         return flops, es * elems + (4.0 * batch * n_in if h is not None else 0.0)
+    if label in ("F_base", "P_base", "G_base"):
+        # the fused SiLU base branch: one more product of 2 B in out FLOP per contraction
+        plan, _st, x, a = args[:4]
+        batch, n_in = x.shape
+        es, K = x.element_size(), plan.size
+        if label == "G_base":
+            want_c, want_w, want_b = args[4:7]
+            n_out = a.shape[1]
+            flops = 2.0 * batch * n_in * n_out * (K * want_c + want_w)
+            elems = batch * n_in + batch * n_out + n_out * n_in * (K * want_c + want_w) + n_out * want_b
+            return flops, float(es * elems)
+        c = a if label == "F_base" else args[4]
+        n_out = c.shape[0]
+        flops = 2.0 * batch * n_in * (K + 1) * n_out
+        coef = n_out * n_in * (K + 1)
+        if label == "F_base":
+            elems = batch * n_in + coef + n_out + batch * n_out
+        else:
+            elems = 2 * batch * n_in + batch * n_out + coef
+        return flops, float(es * elems)
     if label == "edge":
         plan, _m, _st, x2, c, base_w = args[:6]
         batch, n_in = x2.shape
@@ -510,7 +531,8 @@ def _hook_entries(timer):
     from kanforge_amd.export.lut import LUTLayer
 
     names = (("_raw", None), ("_edge_raw", "edge"), ("_features_raw", "features"),
-             ("_rational_param_grad", "rational_param_grad"), ("_rational_bwd_raw", "rational_bwd"))
+             ("_rational_param_grad", "rational_param_grad"), ("_rational_bwd_raw", "rational_bwd"),
+             ("_f_base_raw", "F_base"), ("_p_base_raw", "P_base"), ("_g_base_raw", "G_base"))
     orig = {n: getattr(kmod, n) for n, _ in names}
     for n, lab in names:
         setattr(kmod, n, timer.wrap(orig[n], lab))

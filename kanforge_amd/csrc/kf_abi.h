@@ -366,13 +366,30 @@ inline WsG ws_g(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64
 // F on the register-A kernel with silu(x) as the last feature of every chunk (T_0 taken out, so
 // n_t features a chunk: 9, or an even count of at least 6); layers narrow enough for F's
 // streaming routes keep those. P on p8_kernel (the order-1 descriptor), G on g96_kernel.
-// bf16 cubic B-splines with at most 11 basis functions: P on p8_kernel's 12 feature slots (W^T
-// in the first spare one), G on the GEMM core (features and silu(x) transposed); no F.
+// bf16 B-splines: F on the GEMM core with silu(x) and a ones column after each row's features;
+// cubic with 11 basis functions: P on p8_kernel's 12 feature slots (W^T in the spare one); G on
+// the GEMM core (features and silu(x) transposed).
 inline bool f_base_route(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out) {
-  if (!f_uses_rega(b, dtype) || b->order != 0) return false;
-  if (!(b->n_t == 9 || (b->n_t % 2 == 0 && b->n_t >= 6))) return false;
+  if (dtype != KF_BF16 || b->order != 0) return false;
   const bool narrow = n_out <= 8 || (n_in <= 4 && n_in * b->size <= 64 && n_in * 16 <= 64);
-  return !(batch >= 1024 && narrow);
+  if (batch >= 1024 && narrow) return false;
+  if (b->kind == KF_KIND_BSPLINE) return (n_in * b->size) % 8 == 0;
+  return f_uses_rega(b, dtype) && (b->n_t == 9 || (b->n_t % 2 == 0 && b->n_t >= 6));
+}
+// kf_F_base for B-splines: Phi with the base columns (B, ld), [c | W | bias | 0] (OUT, ld) and
+// the GEMM core's split partial sums; ld = IN K + IN + 1 rounded up to whole 64-element stages
+struct WsFB {
+  int64_t ld;
+  size_t phi, cf, gemm, total;
+};
+inline WsFB ws_f_base_bspline(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out) {
+  WsFB w;
+  w.ld = round_up(n_in * b->size + n_in + 1, 64);
+  w.phi = align256((size_t)batch * w.ld * elt_size(dtype));
+  w.cf = align256((size_t)n_out * w.ld * elt_size(dtype));
+  w.gemm = gemm_nt_workspace(batch, n_out, w.ld);
+  w.total = w.phi + w.cf + w.gemm;
+  return w;
 }
 inline bool p_base_route(const kf_basis* b1, int dtype, int64_t batch, int64_t n_in, int64_t n_out) {
   if (dtype != KF_BF16 || b1->order < 1) return false;

@@ -93,7 +93,10 @@ size_t kf_workspace_bytes(int op, const kf_basis* b, int dtype, int64_t batch, i
       const size_t a = ws_g(b, dtype, batch, n_in, n_out, true).total, u = ws_g(b, dtype, batch, n_in, n_out, false).total;
       return a > u ? a : u;
     }
-    case KF_OP_F_BASE: return f_base_route(b, dtype, batch, n_in, n_out) ? ws_f(b, dtype, batch, n_in, n_out, false, true).total : 0;
+    case KF_OP_F_BASE:
+      if (!f_base_route(b, dtype, batch, n_in, n_out)) return 0;
+      return b->kind == KF_KIND_BSPLINE ? ws_f_base_bspline(b, dtype, batch, n_in, n_out).total
+                                        : ws_f(b, dtype, batch, n_in, n_out, false, true).total;
     case KF_OP_P_BASE: return p_base_route(b, dtype, batch, n_in, n_out) ? ws_p_base(b, dtype, batch, n_in, n_out).total : 0;
     case KF_OP_G_BASE: return g_base_route(b, dtype, batch, n_in, n_out) ? ws_g_base(b, dtype, batch, n_in, n_out).total : 0;
     default: return 0;

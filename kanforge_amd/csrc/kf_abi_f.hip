@@ -73,6 +73,26 @@ int launch_f_cfg(const WsF& L, int64_t batch, int64_t n_out, int n_t, const floa
   }
 }
 
+// B-spline features into rows ld elements apart (plus the base columns, base_cols > 0):
+// 32 inputs x 64 rows per block, knot rows staged once per block
+template <typename T>
+int launch_phi_block(const KBasis& kb, int64_t batch, int64_t n_in, const void* x, void* phi, long ld, int base_cols,
+                     hipStream_t s) {
+  const size_t rpb = ((size_t)32 * kb.K * sizeof(T) + 15) / 16 * 16 + 16;
+  const size_t plds = 64 * rpb + (size_t)32 * (2 * kb.n_knots + 2 * kb.spline_k) * 4;
+  dim3 pg((unsigned)((n_in + 31) / 32), (unsigned)((batch + 63) / 64));
+  const bool even = kb.knots_uniform && kb.n_knots >= 4;  // cubic even knots: the common case
+  auto kern = kb.spline_k == 0   ? phi_block_kernel<T, 0>
+              : kb.spline_k == 1 ? phi_block_kernel<T, 1>
+              : kb.spline_k == 2 ? phi_block_kernel<T, 2>
+              : kb.spline_k == 3 ? (even ? phi_block_kernel<T, 3, true> : phi_block_kernel<T, 3>)
+              : kb.spline_k == 4 ? phi_block_kernel<T, 4>
+                                 : phi_block_kernel<T, 5>;
+  if (!reserve_lds((const void*)kern, plds)) return fail(KF_ELAUNCH, "F: cannot reserve %zu bytes of LDS", plds);
+  hipLaunchKernelGGL(kern, pg, dim3(kThreads), plds, s, kb, (int)batch, (int)n_in, (const T*)x, (T*)phi, ld, base_cols);
+  return check_launch("phi_block");
+}
+
 template <typename T>
 int run_F_dma(const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* c, void* phi,
               void* y, void* gws, size_t gws_bytes, hipStream_t s) {
@@ -80,20 +100,7 @@ int run_F_dma(const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out, cons
   const long ld = (long)n_in * kb.K;  // Phi row length: the reduction
   if (kb.n_t != kb.K || (ld * (long)sizeof(T)) % 16) return fail(KF_EINVAL, "F: Phi rows not aligned");
   if (kb.kind == KF_KIND_BSPLINE && ld % 8 == 0 && aligned16(phi)) {
-    // 32 inputs x 64 rows per block, knot rows staged once per block
-    const size_t rpb = ((size_t)32 * kb.K * sizeof(T) + 15) / 16 * 16 + 16;
-    const size_t plds = 64 * rpb + (size_t)32 * (2 * kb.n_knots + 2 * kb.spline_k) * 4;
-    dim3 pg((unsigned)((n_in + 31) / 32), (unsigned)((batch + 63) / 64));
-    const bool even = kb.knots_uniform && kb.n_knots >= 4;  // cubic even knots: the common case
-    auto kern = kb.spline_k == 0   ? phi_block_kernel<T, 0>
-                : kb.spline_k == 1 ? phi_block_kernel<T, 1>
-                : kb.spline_k == 2 ? phi_block_kernel<T, 2>
-                : kb.spline_k == 3 ? (even ? phi_block_kernel<T, 3, true> : phi_block_kernel<T, 3>)
-                : kb.spline_k == 4 ? phi_block_kernel<T, 4>
-                                   : phi_block_kernel<T, 5>;
-    if (!reserve_lds((const void*)kern, plds)) return fail(KF_ELAUNCH, "F: cannot reserve %zu bytes of LDS", plds);
-    hipLaunchKernelGGL(kern, pg, dim3(kThreads), plds, s, kb, (int)batch, (int)n_in, (const T*)x, (T*)phi);
-    int rc = check_launch("phi_block");
+    int rc = launch_phi_block<T>(kb, batch, n_in, x, phi, ld, 0, s);
     if (rc) return rc;
   } else if (kb.K == 1) {  // one feature: the plain (B, in) writes are already coalesced
     int rc = launch_features<T, false>(kb, batch, n_in, batch, n_in, x, phi, ld, 1L, 1L, false, s);
@@ -345,6 +352,29 @@ int run_F_base(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, in
   return launch_f_rega<false, true, true>(L, batch, n_out, z, sz, cfm, ysum, y, s);
 }
 
+// B-splines: Phi with silu(x), a ones column and zero padding after each row's features, and the
+// coefficients with W, the bias and zeros after each row's: the base branch and the bias are
+// features of the one GEMM-core product.
+int run_F_base_bspline(const KBasis& kb, const kf_basis* b, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
+                       const void* c, const void* bw, const void* bias, void* y, void* ws, hipStream_t s) {
+  const WsFB L = ws_f_base_bspline(b, KF_BF16, batch, n_in, n_out);
+  char* base = (char*)ws;
+  bf16* phi = (bf16*)base;
+  bf16* cf = (bf16*)(base + L.phi);
+  void* gws = base + L.phi + L.cf;
+  if (!aligned16(c) || (n_in * kb.K) % 8) return fail(KF_EINVAL, "kf_F_base: coefficient rows not 16-byte aligned");
+  const long n = (long)n_out * (L.ld / 8);
+  long blocks = (n + kThreads - 1) / kThreads;
+  if (blocks > 65535 * 4) blocks = 65535 * 4;
+  hipLaunchKernelGGL(base_coef_kernel<bf16>, dim3((unsigned)blocks), dim3(kThreads), 0, s, (int)n_out, (int)n_in, kb.K,
+                     (long)L.ld, (const bf16*)c, (const bf16*)bw, (const bf16*)bias, cf);
+  int rc = check_launch("base_coef");
+  if (rc) return rc;
+  rc = launch_phi_block<bf16>(kb, batch, n_in, x, phi, (long)L.ld, (int)(L.ld - n_in * kb.K), s);
+  if (rc) return rc;
+  return gemm_nt(batch, n_out, L.ld, phi, L.ld, cf, L.ld, y, n_out, false, gws, L.gemm, s);
+}
+
 }  // namespace
 
 extern "C" {
@@ -399,12 +429,15 @@ int kf_F_base(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t
   if (!x || !c || !base_w || !y) return fail(KF_EINVAL, "kf_F_base: NULL array");
   if (!f_base_route(b, dtype, batch, n_in, n_out))
     return fail(KF_EUNSUPPORTED, "kf_F_base: this layer does not run the fused base branch (kf_base_fused)");
-  const size_t need = ws_f(b, dtype, batch, n_in, n_out, false, true).total;
+  const bool spline = b->kind == KF_KIND_BSPLINE;
+  const size_t need = spline ? ws_f_base_bspline(b, dtype, batch, n_in, n_out).total
+                             : ws_f(b, dtype, batch, n_in, n_out, false, true).total;
   if (!workspace || workspace_bytes < need)
     return fail(KF_EWORKSPACE, "kf_F_base: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
   if (reinterpret_cast<uintptr_t>(workspace) & 255)
     return fail(KF_EWORKSPACE, "kf_F_base: workspace must be 256-byte aligned");
   KBasis kb = to_kbasis(b);
+  if (spline) return run_F_base_bspline(kb, b, batch, n_in, n_out, x, c, base_w, bias, y, workspace, (hipStream_t)stream);
   return run_F_base(kb, b, dtype, batch, n_in, n_out, x, c, base_w, bias, y, workspace, (hipStream_t)stream);
 }
 

@@ -957,8 +957,9 @@ def bspline_interval(x: torch.Tensor, knots_cmp: torch.Tensor) -> torch.Tensor:
 # (kanforge/torch/layers.py:185-191). For bf16 Chebyshev plans kf_F_base runs silu(x) as one more
 # feature of the F contraction and folds the bias into its per-output constant, kf_P_base adds
 # silu'(x) (g W) in P's epilogue and kf_G_base returns the base weights' and the bias's gradients
-# next to the coefficient gradient; bf16 cubic B-splines fuse P (W^T in a spare feature slot) and
-# G, and keep F plus one GEMM for the forward.
+# next to the coefficient gradient. bf16 B-splines run silu(x) and the bias as extra feature
+# columns of F's GEMM, G as for Chebyshev, and (cubic, 11 basis functions) P with W^T in a spare
+# feature slot of its tile.
 
 _FUSED: dict = {}
 
@@ -989,23 +990,12 @@ def _dsilu(x: torch.Tensor) -> torch.Tensor:
     return s * (1 + x * (1 - s))
 
 
-def _F_base_impl(x: torch.Tensor, c: torch.Tensor, bw: torch.Tensor, bias: Opt, knots: Opt, knots_cmp: Opt, knots_u: Opt,
-                 plan: str) -> torch.Tensor:
-    """y = F_0(x, c) + silu(x) bw^T + bias: the layer's forward with its SiLU base branch (kf_F_base
-    where it takes the layer, else kf_F and one GEMM)."""
-    _require_device(x)
-    pl = plan_of(plan)
-    st = _state(knots, knots_cmp, knots_u, None, None, x.shape[1])
-    batch, n_in = x.shape
-    n_out = c.shape[0]
-    x, c, bw = x.contiguous(), c.contiguous(), bw.contiguous()
-    bias = None if bias is None else bias.contiguous()
-    if not base_fused(pl, st, x.dtype, batch, n_in, n_out)[0]:
-        y = _raw("F", pl, 0, x, None, c, st, n_out)
-        y = torch.addmm(y, torch.nn.functional.silu(x), bw.t())
-        return y if bias is None else y.add_(bias)
+def _f_base_raw(pl: KernelPlan, st: BasisState | None, x, c, bw, bias) -> torch.Tensor:
+    """kf_F_base on contiguous arrays."""
     lib = _lib.load()
     desc, keep = _desc(pl, 0, st)
+    batch, n_in = x.shape
+    n_out = c.shape[0]
     dev = x.device
     dt = _dtype_code(x.dtype)
     y = torch.empty(batch, n_out, dtype=x.dtype, device=dev)
@@ -1018,6 +1008,22 @@ def _F_base_impl(x: torch.Tensor, c: torch.Tensor, bw: torch.Tensor, bias: Opt, 
     return y
 
 
+def _F_base_impl(x: torch.Tensor, c: torch.Tensor, bw: torch.Tensor, bias: Opt, knots: Opt, knots_cmp: Opt, knots_u: Opt,
+                 plan: str) -> torch.Tensor:
+    """y = F_0(x, c) + silu(x) bw^T + bias: the layer's forward with its SiLU base branch (kf_F_base
+    where it takes the layer, else kf_F and one GEMM)."""
+    _require_device(x)
+    pl = plan_of(plan)
+    st = _state(knots, knots_cmp, knots_u, None, None, x.shape[1])
+    x, c, bw = x.contiguous(), c.contiguous(), bw.contiguous()
+    bias = None if bias is None else bias.contiguous()
+    if not base_fused(pl, st, x.dtype, x.shape[0], x.shape[1], c.shape[0])[0]:
+        y = _raw("F", pl, 0, x, None, c, st, c.shape[0])
+        y = torch.addmm(y, torch.nn.functional.silu(x), bw.t())
+        return y if bias is None else y.add_(bias)
+    return _f_base_raw(pl, st, x, c, bw, bias)
+
+
 op_F_base = torch.library.custom_op("kf::F_base", mutates_args=())(_F_base_impl)
 
 
@@ -1026,18 +1032,14 @@ def _(x, c, bw, bias, knots, knots_cmp, knots_u, plan):
     return x.new_empty(x.shape[0], c.shape[0])
 
 
-def _P_base_impl(x: torch.Tensor, g: torch.Tensor, c: torch.Tensor, bw: torch.Tensor, knots: Opt, knots_cmp: Opt,
-                 knots_u: Opt, plan: str) -> torch.Tensor:
-    """P_1(x, g, c) + silu'(x) (g bw): the layer's input gradient with its SiLU base branch."""
-    _require_device(x)
+def _p_base_raw(pl: KernelPlan, st: BasisState | None, x, g, c, bw) -> torch.Tensor:
+    """kf_P_base (order-1 descriptor) on contiguous arrays."""
     lib = _lib.load()
-    st = _state(knots, knots_cmp, knots_u, None, None, x.shape[1])
-    desc, keep = _desc(plan_of(plan), 1, st)
+    desc, keep = _desc(pl, 1, st)
     batch, n_in = x.shape
     n_out = c.shape[0]
     dev = x.device
     dt = _dtype_code(x.dtype)
-    x, g, c, bw = x.contiguous(), g.contiguous(), c.contiguous(), bw.contiguous()
     p = torch.empty(batch, n_in, dtype=x.dtype, device=dev)
     ws = _workspace(_lib.KF_OP_P_BASE, desc, dt, batch, n_in, n_out, dev)
     with _on(dev):
@@ -1048,6 +1050,14 @@ def _P_base_impl(x: torch.Tensor, g: torch.Tensor, c: torch.Tensor, bw: torch.Te
     return p
 
 
+def _P_base_impl(x: torch.Tensor, g: torch.Tensor, c: torch.Tensor, bw: torch.Tensor, knots: Opt, knots_cmp: Opt,
+                 knots_u: Opt, plan: str) -> torch.Tensor:
+    """P_1(x, g, c) + silu'(x) (g bw): the layer's input gradient with its SiLU base branch."""
+    _require_device(x)
+    st = _state(knots, knots_cmp, knots_u, None, None, x.shape[1])
+    return _p_base_raw(plan_of(plan), st, x.contiguous(), g.contiguous(), c.contiguous(), bw.contiguous())
+
+
 op_P_base = torch.library.custom_op("kf::P_base", mutates_args=())(_P_base_impl)
 
 
@@ -1056,20 +1066,14 @@ def _(x, g, c, bw, knots, knots_cmp, knots_u, plan):
     return x.new_empty(x.shape)
 
 
-def _G_base_impl(x: torch.Tensor, g: torch.Tensor, knots: Opt, knots_cmp: Opt, knots_u: Opt, plan: str, want_c: bool,
-                 want_w: bool, want_b: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """(G_0(x, g), g^T silu(x), sum_b g): the layer's parameter gradients with its SiLU base branch
-    and bias; an output not wanted comes back empty."""
-    _require_device(x)
+def _g_base_raw(pl: KernelPlan, st: BasisState | None, x, g, want_c: bool, want_w: bool, want_b: bool):
+    """kf_G_base on contiguous arrays: (dc, dW, db), empty where not wanted."""
     lib = _lib.load()
-    pl = plan_of(plan)
-    st = _state(knots, knots_cmp, knots_u, None, None, x.shape[1])
     desc, keep = _desc(pl, 0, st)
     batch, n_in = x.shape
     n_out = g.shape[1]
     dev = x.device
     dt = _dtype_code(x.dtype)
-    x, g = x.contiguous(), g.contiguous()
     dc = torch.empty((n_out, n_in, pl.size) if want_c else (0,), dtype=x.dtype, device=dev)
     dw = torch.empty((n_out, n_in) if want_w else (0,), dtype=x.dtype, device=dev)
     db = torch.empty((n_out,) if want_b else (0,), dtype=x.dtype, device=dev)
@@ -1080,6 +1084,15 @@ def _G_base_impl(x: torch.Tensor, g: torch.Tensor, knots: Opt, knots_cmp: Opt, k
     _lib.check(rc, "kf_G_base")
     del keep
     return dc, dw, db
+
+
+def _G_base_impl(x: torch.Tensor, g: torch.Tensor, knots: Opt, knots_cmp: Opt, knots_u: Opt, plan: str, want_c: bool,
+                 want_w: bool, want_b: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(G_0(x, g), g^T silu(x), sum_b g): the layer's parameter gradients with its SiLU base branch
+    and bias; an output not wanted comes back empty."""
+    _require_device(x)
+    st = _state(knots, knots_cmp, knots_u, None, None, x.shape[1])
+    return _g_base_raw(plan_of(plan), st, x.contiguous(), g.contiguous(), want_c, want_w, want_b)
 
 
 op_G_base = torch.library.custom_op("kf::G_base", mutates_args=())(_G_base_impl)

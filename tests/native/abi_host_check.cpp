@@ -126,8 +126,8 @@ int main() {
           const int r = kf_base_fused(op, &b, dtype, s.batch, s.n_in, s.n_out);
           const size_t n = kf_workspace_bytes(op, &b, dtype, s.batch, s.n_in, s.n_out);
           check(r == 0 || (r == 1 && n > 0), "base route " + std::to_string(op) + " reports a workspace");
-          check(r == 0 || (dtype == KF_BF16 && (b.kind == KF_KIND_CHEB || (b.kind == KF_KIND_BSPLINE && op != KF_OP_F_BASE))),
-                "base route only for bf16 Chebyshev, and P and G of bf16 B-splines");
+          check(r == 0 || (dtype == KF_BF16 && (b.kind == KF_KIND_CHEB || b.kind == KF_KIND_BSPLINE)),
+                "base route only for bf16 Chebyshev and B-spline layers");
         }
   {
     const kf_basis c0 = cheb(9, 0, 9, KF_MAP_TANH), c1 = cheb(9, 1, 8, KF_MAP_TANH_SQ);
@@ -141,7 +141,8 @@ int main() {
     const kf_basis s0 = bspline(8, 3, 0, true), s1 = bspline(8, 3, 1, true), s5 = bspline(5, 3, 1, true);
     check(kf_base_fused(KF_OP_P_BASE, &s1, KF_BF16, 16384, 768, 3072) == 1, "B-spline(8, 3) P fused");
     check(kf_base_fused(KF_OP_G_BASE, &s0, KF_BF16, 16384, 768, 3072) == 1, "B-spline(8, 3) G fused");
-    check(kf_base_fused(KF_OP_F_BASE, &s0, KF_BF16, 16384, 768, 3072) == 0, "B-spline F composed");
+    check(kf_base_fused(KF_OP_F_BASE, &s0, KF_BF16, 16384, 768, 3072) == 1, "B-spline F fused");
+    check(kf_base_fused(KF_OP_F_BASE, &s0, KF_BF16, 4096, 64, 4) == 0, "narrow B-spline layer not fused");
     check(kf_base_fused(KF_OP_P_BASE, &s5, KF_BF16, 16384, 768, 3072) == 0, "B-spline(5, 3) P: no spare slot tile");
   }
 

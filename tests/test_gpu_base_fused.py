@@ -1,7 +1,7 @@
 """KANLinear with its SiLU base branch and bias fused into the HIP contractions (kf_F_base,
 kf_P_base, kf_G_base) against the float64 oracle: y and every first-order gradient on layers
 whose three entries all fuse (Chebyshev degrees 8, 7 and 5: chunks of 9 features, and even counts
-on the runtime-count F kernel) and on cubic B-spline layers (P and G fused), ragged shapes (inputs not a multiple of 16, outputs not of 8,
+on the runtime-count F kernel) and on cubic B-spline layers, ragged shapes (inputs not a multiple of 16, outputs not of 8,
 batch not of 64), the headline shape 768 -> 3072 at batch 8192 against a plain PyTorch float32
 reference, double backward through the fused layer (its backward composes differentiable ops
 there) against the unfused layer, the routes the library reports, and bitwise determinism.
@@ -66,8 +66,10 @@ def test_routes_reported_by_the_library():
     assert not K.base_fused(plan, None, BF, 4096, 64, 4)[0]  # narrow: F's streaming route
     plan6 = make_layer(6, 48, 8)._plan_key  # 7 features a chunk: not fused
     assert not K.base_fused(plan6, None, BF, 8192, 768, 3072)[0]
-    sp = make_spline_layer(768, 3072)  # cubic B-splines: P and G fused, F composed
-    assert K.base_fused(sp._plan_key, sp._basis_state(), BF, 16384, 768, 3072) == (False, True, True)
+    sp = make_spline_layer(768, 3072)  # cubic B-splines on 8 intervals: all three
+    assert K.base_fused(sp._plan_key, sp._basis_state(), BF, 16384, 768, 3072) == (True, True, True)
+    sp5 = make_spline_layer(768, 3072, grid=5)  # 8 basis functions: no spare slot in P's tile
+    assert K.base_fused(sp5._plan_key, sp5._basis_state(), BF, 16384, 768, 3072) == (True, False, True)
 
 
 # (batch, in, out, degree): every case has >= 128 G tiles of 192 x 48 (g96_kernel)
@@ -113,14 +115,15 @@ def test_fused_layer_against_oracle(B, IN, OUT, deg):
         assert err <= TOL, (key, err)
 
 
-@pytest.mark.parametrize("B,IN,OUT,grid", [(300, 768, 200, 8), (257, 136, 300, 8)])
+@pytest.mark.parametrize("B,IN,OUT,grid", [(300, 768, 200, 8), (257, 136, 300, 8), (200, 96, 130, 5)])
 def test_fused_bspline_layer_against_oracle(B, IN, OUT, grid):
-    """Cubic B-splines on 8 intervals (11 basis functions, P's 12-slot tiles): P with W^T in the
-    spare feature slot, G with dW on the GEMM core, F composed; the second shape is ragged."""
+    """Cubic B-splines: F with silu(x) and a ones column after each row's features, G with dW on
+    the GEMM core, and on 8 intervals (11 basis functions, P's 12-slot tiles) P with W^T in the
+    spare feature slot; the second shape is ragged, the third has 8 basis functions (P composed)."""
     layer = make_spline_layer(IN, OUT, grid)
     fused = K.base_fused(layer._plan_key, layer._basis_state(), BF, B, IN, OUT)
     print(f"B-spline case B={B} in={IN} out={OUT} grid={grid} fused={fused}", flush=True)
-    assert fused == (False, True, True)
+    assert fused == (True, grid == 8, True)
     ob = oracle_basis(layer.basis, IN, {"grid": np64(layer.basis_grid)})
     rng = np.random.default_rng(B)
     x0 = rng.normal(0, 1.2, (B, IN))
