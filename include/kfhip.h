@@ -164,11 +164,13 @@ int kf_P(const kf_basis *basis, int dtype, int64_t batch, int64_t n_in, int64_t 
  * kf_base_fused(op, ...) is 1 when the entry point of op (KF_OP_F_BASE, KF_OP_P_BASE,
  * KF_OP_G_BASE) takes the layer, 0 when the caller composes kf_F / kf_P / kf_G with its own base
  * branch instead, negative for an invalid descriptor. It takes bf16 Chebyshev plans on their
- * contraction kernels (F: n_t of 9 or an even count >= 6, not the narrow streaming routes).
- * Workspace: kf_workspace_bytes(KF_OP_*_BASE, ...).
+ * contraction kernels (F: n_t of 9 or an even count >= 6) and bf16 B-spline plans (P: cubic with
+ * 11 basis functions), not the narrow streaming routes. Workspace: kf_workspace_bytes(KF_OP_*_BASE,
+ * ...).
  *
  * kf_F_base: y = F_0(x, c) + silu(x) base_w^T + bias, basis of order 0; base_w (n_out, n_in),
- *   bias (n_out) or NULL. silu(x) is one more feature per input in the same contraction.
+ *   bias (n_out) or NULL. silu(x) is one more feature per input in the same contraction (B-splines:
+ *   silu(x) and the bias as extra feature columns of the one GEMM).
  * kf_P_base: p = P_m(x, g, c) + silu'(x) * (g base_w), basis of order m >= 1 (the x-gradient's
  *   descriptor, m = 1); g (batch, n_out).
  * kf_G_base: dc = G_0(x, g), dbase_w = g^T silu(x) (n_out, n_in), dbias = sum_b g (n_out),
