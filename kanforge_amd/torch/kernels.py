@@ -1120,11 +1120,13 @@ def _F_base_backward(ctx, gy):
     gx = gc = gw = gb = None
     tabs = (knots, knots_cmp, knots_u)
     rat = (None, None)
-    if torch.is_grad_enabled():
+    dims = (x.shape[0], x.shape[1], c.shape[0])
+    if torch.is_grad_enabled() or not all(type(d) is int for d in dims):
+        # a graph is being built (higher orders), or traced with symbolic shapes: composed ops
         fused = (False, False, False)
     else:
         st = _state(knots, knots_cmp, knots_u, None, None, x.shape[1])
-        fused = base_fused(plan, st, x.dtype, x.shape[0], x.shape[1], c.shape[0])
+        fused = base_fused(plan, st, x.dtype, *dims)
     if need[0]:
         if fused[1]:
             gx = _P_BASE(x, gy, c, bw, *tabs, plan)
