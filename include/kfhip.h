@@ -127,6 +127,17 @@ int kf_F(const kf_basis *basis, int dtype, int64_t batch, int64_t n_in, int64_t 
          const void *w, const void *c, void *y, void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * y[b,o] = F_m(x, w, c)[b,o] + bias[o]: kf_F plus the layer's bias (kanforge/torch/layers.py:
+ * 189-190, `y + self.bias`), bias in dtype (n_out) or NULL (then exactly kf_F). Where F's last
+ * kernel can take the bias (the register-A Chebyshev kernel's per-output constant, the GEMM
+ * core's epilogue: bf16 B-spline and rational routes) it costs no pass of its own; other routes
+ * add it in one more pass over y. Same workspace as kf_F.
+ */
+int kf_F_bias(const kf_basis *basis, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void *x,
+              const void *w, const void *c, const void *bias, void *y, void *workspace, size_t workspace_bytes,
+              void *stream);
+
+/*
  * kf_F without a workspace argument and without any allocation: the same kernels and result as
  * kf_F, with their scratch in a static device array of KF_NOALLOC_SCRATCH_BYTES that the library
  * holds on every GPU it runs on until the process ends. No counterpart in the reference: it is for

@@ -36,12 +36,12 @@ inline int check_launch(const char* what) {
 // false when the request cannot be met.
 bool reserve_lds(const void* kern, size_t lds);
 
-// C = A B^T on the bf16 MFMA GEMM core (kf_gemm_nt.hip): A (M, lda), B (N, ldb) bf16 with k
-// contiguous, K a multiple of 64, rows 16-byte aligned; C (M, ldc) bf16 or float32. A split of
-// the reduction needs gemm_nt_workspace(M, N, K) bytes of workspace.
+// C = A B^T (+ bias[n]) on the bf16 MFMA GEMM core (kf_gemm_nt.hip): A (M, lda), B (N, ldb) bf16
+// with k contiguous, K a multiple of 64, rows 16-byte aligned; C (M, ldc) bf16 or float32; bias
+// bf16 (N) or NULL. A split of the reduction needs gemm_nt_workspace(M, N, K) bytes of workspace.
 size_t gemm_nt_workspace(long M, long N, long K);
 int gemm_nt(long M, long N, long K, const void* A, long lda, const void* B, long ldb, void* C, long ldc, bool out_f32,
-            void* ws, size_t ws_bytes, hipStream_t s);
+            void* ws, size_t ws_bytes, hipStream_t s, const void* bias = nullptr);
 
 inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
@@ -376,15 +376,15 @@ inline bool f_base_route(const kf_basis* b, int dtype, int64_t batch, int64_t n_
   if (b->kind == KF_KIND_BSPLINE) return (n_in * b->size) % 8 == 0;
   return f_uses_rega(b, dtype) && (b->n_t == 9 || (b->n_t % 2 == 0 && b->n_t >= 6));
 }
-// kf_F_base for B-splines: Phi with the base columns (B, ld), [c | W | bias | 0] (OUT, ld) and
-// the GEMM core's split partial sums; ld = IN K + IN + 1 rounded up to whole 64-element stages
+// kf_F_base for B-splines: Phi with the base columns (B, ld), [c | W | 0] (OUT, ld) and the GEMM
+// core's split partial sums; ld = IN K + IN rounded up to whole 64-element stages
 struct WsFB {
   int64_t ld;
   size_t phi, cf, gemm, total;
 };
 inline WsFB ws_f_base_bspline(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out) {
   WsFB w;
-  w.ld = round_up(n_in * b->size + n_in + 1, 64);
+  w.ld = round_up(n_in * b->size + n_in, 64);
   w.phi = align256((size_t)batch * w.ld * elt_size(dtype));
   w.cf = align256((size_t)n_out * w.ld * elt_size(dtype));
   w.gemm = gemm_nt_workspace(batch, n_out, w.ld);

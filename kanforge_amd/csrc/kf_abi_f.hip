@@ -17,6 +17,13 @@ __global__ __launch_bounds__(kThreads) void scale_phi_kernel(int B, int IN, int 
     if (i < IN) phi[e] = from_f32<T>(to_f32(phi[e]) * to_f32(w[(size_t)b * IN + i]));
   }
 }
+// y[b][o] += bias[o] (the bias of routes whose last kernel does not take it).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void bias_rows_kernel(int B, int OUT, const T* __restrict__ bias, T* __restrict__ y) {
+  const long n = (long)B * OUT;
+  for (long e = blockIdx.x * (long)kThreads + threadIdx.x; e < n; e += (long)gridDim.x * kThreads)
+    y[e] = from_f32<T>(to_f32(y[e]) + to_f32(bias[e % OUT]));
+}
 }  // namespace kf
 
 namespace {
@@ -95,7 +102,7 @@ int launch_phi_block(const KBasis& kb, int64_t batch, int64_t n_in, const void* 
 
 template <typename T>
 int run_F_dma(const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* c, void* phi,
-              void* y, void* gws, size_t gws_bytes, hipStream_t s) {
+              void* y, void* gws, size_t gws_bytes, hipStream_t s, const void* bias = nullptr, bool* bias_done = nullptr) {
   constexpr int FW = kGdmaFW, TM = p_dma_tm(FW), BM = 2 * TM * 32, TI = 2 * FW * 32;
   const long ld = (long)n_in * kb.K;  // Phi row length: the reduction
   if (kb.n_t != kb.K || (ld * (long)sizeof(T)) % 16) return fail(KF_EINVAL, "F: Phi rows not aligned");
@@ -119,7 +126,10 @@ int run_F_dma(const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out, cons
     if (rc) return rc;
   }
   if constexpr (sizeof(T) == 2) {
-    if (ld % 64 == 0) return gemm_nt(batch, n_out, ld, phi, ld, c, ld, y, n_out, false, gws, gws_bytes, s);
+    if (ld % 64 == 0) {
+      if (bias_done) *bias_done = bias != nullptr;
+      return gemm_nt(batch, n_out, ld, phi, ld, c, ld, y, n_out, false, gws, gws_bytes, s, bias);
+    }
   }
   const size_t lds = (size_t)2 * (BM + TI) * 128;
   auto kern = p_dma_kernel<T, TM, FW, KF_KIND_BSPLINE, 2>;
@@ -191,8 +201,12 @@ int launch_f_stream(const KBasis& kb, int64_t batch, int64_t n_in, int64_t n_out
 }
 
 template <typename T>
+// bias (dtype, n_out) or NULL: added where the route's last kernel can take it (the register-A
+// kernel's per-output constant, the GEMM core's epilogue), which sets *bias_done; otherwise the
+// caller adds it.
 int run_F(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
-          const void* w, const void* c, void* y, void* ws, hipStream_t s) {
+          const void* w, const void* c, void* y, void* ws, hipStream_t s, const void* bias = nullptr,
+          bool* bias_done = nullptr) {
   const bool has_w = w != nullptr;
   const bool cheb = kb.kind == KF_KIND_CHEB;
   const bool weighted = features_weighted(b, w);
@@ -234,9 +248,11 @@ int run_F(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
     const int vin = rows_vec<T>(n_in, x) && rows_vec<T>(n_in, w);
     hipLaunchKernelGGL(zmapc_kernel<T>, dim3((unsigned)(blocks + sblocks)), dim3(kThreads), 0, s, (int)batch,
                        (int)n_in, (int)L.BP, (int)L.INP, kb.input_map, vin, (const T*)x, (const T*)w, z, wz,
-                       (int)blocks, (int)(L.INP / 16), (int)L.OUTP, part0, ysum, 0, (const T*)nullptr, 0);
+                       (int)blocks, (int)(L.INP / 16), (int)L.OUTP, part0, ysum, 0,
+                       (const T*)(L.skip0 ? bias : nullptr), (int)n_out);
     rc = check_launch("zmapc");
     if (rc) return rc;
+    if (bias_done) *bias_done = L.skip0 && bias;
     if (weighted) return launch_f_rega<true, false>(L, batch, n_out, z, wz, cfm, nullptr, y, s);
     if (L.skip0) return launch_f_rega<false, true>(L, batch, n_out, z, nullptr, cfm, ysum, y, s);
     return launch_f_rega<false, false>(L, batch, n_out, z, nullptr, cfm, nullptr, y, s);
@@ -259,13 +275,14 @@ int run_F(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
                          (const bf16*)w, (const float*)nullptr, (bf16*)phi);
       int rc = check_launch("rational features");
       if (rc) return rc;
-      return gemm_nt(batch, n_out, n_in, phi, n_in, c, n_in, y, n_out, false, gws, L.gemm, s);
+      if (bias_done) *bias_done = bias != nullptr;
+      return gemm_nt(batch, n_out, n_in, phi, n_in, c, n_in, y, n_out, false, gws, L.gemm, s, bias);
     }
   }
   const bool identity_fold = kb.kind == KF_KIND_BSPLINE || kb.kind == KF_KIND_RATIONAL;
   const bool gemm_core = sizeof(T) == 2 && (n_in * kb.K) % 64 == 0;  // any tile count: the core splits
   if (identity_fold && !has_w && (n_in * kb.K) % EPS == 0 && aligned16(c) && aligned16(phi) && (dma_tiles >= 128 || gemm_core))
-    return run_F_dma<T>(kb, batch, n_in, n_out, x, c, phi, y, gws, L.gemm, s);
+    return run_F_dma<T>(kb, batch, n_in, n_out, x, c, phi, y, gws, L.gemm, s, bias, bias_done);
   int rc = launch_permute<T>(kb, n_out, n_in, L.OUTP, L.INP, L.n_tp, c, cfm, kPermFM, s);
   if (rc) return rc;
   if (cheb) {
@@ -352,9 +369,9 @@ int run_F_base(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, in
   return launch_f_rega<false, true, true>(L, batch, n_out, z, sz, cfm, ysum, y, s);
 }
 
-// B-splines: Phi with silu(x), a ones column and zero padding after each row's features, and the
-// coefficients with W, the bias and zeros after each row's: the base branch and the bias are
-// features of the one GEMM-core product.
+// B-splines: Phi with silu(x) and zero padding after each row's features, and the coefficients
+// with W and zeros after each row's: the base branch is features of the one GEMM-core product,
+// whose epilogue adds the bias.
 int run_F_base_bspline(const KBasis& kb, const kf_basis* b, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
                        const void* c, const void* bw, const void* bias, void* y, void* ws, hipStream_t s) {
   const WsFB L = ws_f_base_bspline(b, KF_BF16, batch, n_in, n_out);
@@ -367,12 +384,12 @@ int run_F_base_bspline(const KBasis& kb, const kf_basis* b, int64_t batch, int64
   long blocks = (n + kThreads - 1) / kThreads;
   if (blocks > 65535 * 4) blocks = 65535 * 4;
   hipLaunchKernelGGL(base_coef_kernel<bf16>, dim3((unsigned)blocks), dim3(kThreads), 0, s, (int)n_out, (int)n_in, kb.K,
-                     (long)L.ld, (const bf16*)c, (const bf16*)bw, (const bf16*)bias, cf);
+                     (long)L.ld, (const bf16*)c, (const bf16*)bw, cf);
   int rc = check_launch("base_coef");
   if (rc) return rc;
   rc = launch_phi_block<bf16>(kb, batch, n_in, x, phi, (long)L.ld, (int)(L.ld - n_in * kb.K), s);
   if (rc) return rc;
-  return gemm_nt(batch, n_out, L.ld, phi, L.ld, cf, L.ld, y, n_out, false, gws, L.gemm, s);
+  return gemm_nt(batch, n_out, L.ld, phi, L.ld, cf, L.ld, y, n_out, false, gws, L.gemm, s, bias);
 }
 
 }  // namespace
@@ -439,6 +456,40 @@ int kf_F_base(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t
   KBasis kb = to_kbasis(b);
   if (spline) return run_F_base_bspline(kb, b, batch, n_in, n_out, x, c, base_w, bias, y, workspace, (hipStream_t)stream);
   return run_F_base(kb, b, dtype, batch, n_in, n_out, x, c, base_w, bias, y, workspace, (hipStream_t)stream);
+}
+
+int kf_F_bias(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* w,
+              const void* c, const void* bias, void* y, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err.clear();
+  int rc = validate_common(b, dtype, batch, n_in, n_out);
+  if (rc) return rc;
+  if (batch == 0 || n_out == 0) return KF_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (!y || (n_in > 0 && (!x || !c))) return fail(KF_EINVAL, "kf_F_bias: NULL array");
+  bool done = false;
+  if (n_in == 0) {
+    rc = dtype == KF_BF16 ? zero_fill<bf16>(y, (long)batch * n_out, s) : zero_fill<float>(y, (long)batch * n_out, s);
+  } else {
+    size_t need = ws_f(b, dtype, batch, n_in, n_out, features_weighted(b, w)).total;
+    if (!workspace || workspace_bytes < need)
+      return fail(KF_EWORKSPACE, "kf_F_bias: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+    if (reinterpret_cast<uintptr_t>(workspace) & 255)
+      return fail(KF_EWORKSPACE, "kf_F_bias: workspace must be 256-byte aligned");
+    KBasis kb = to_kbasis(b);
+    rc = dtype == KF_BF16 ? run_F<bf16>(kb, b, dtype, batch, n_in, n_out, x, w, c, y, workspace, s, bias, &done)
+                          : run_F<float>(kb, b, dtype, batch, n_in, n_out, x, w, c, y, workspace, s, bias, &done);
+  }
+  if (rc || !bias || done) return rc;
+  long n = (long)batch * n_out;
+  long blocks = (n + kThreads - 1) / kThreads;
+  if (blocks > 65535 * 4) blocks = 65535 * 4;
+  if (dtype == KF_BF16)
+    hipLaunchKernelGGL(bias_rows_kernel<bf16>, dim3((unsigned)blocks), dim3(kThreads), 0, s, (int)batch, (int)n_out,
+                       (const bf16*)bias, (bf16*)y);
+  else
+    hipLaunchKernelGGL(bias_rows_kernel<float>, dim3((unsigned)blocks), dim3(kThreads), 0, s, (int)batch, (int)n_out,
+                       (const float*)bias, (float*)y);
+  return check_launch("bias rows");
 }
 
 }  // extern "C"

@@ -11,7 +11,9 @@
 // XOR-swizzled by low row bits, so the fragment reads are free of bank conflicts. Rows past M or
 // N repeat the last row (never stored). A split of the reduction (gridDim.y > 1) writes float32
 // partial tiles, summed in split order by gemm_split_reduce (deterministic).
-// Epilogue in passes of 64 rows through LDS, 16-byte stores where rows are aligned.
+// Epilogue in passes of 64 rows through LDS, 16-byte stores where rows are aligned. An optional
+// bias (bf16, one per column n) is added where the final sums are stored (the epilogue without a
+// split, else the reductions).
 #include "kf_abi.h"
 
 using namespace kfabi;
@@ -21,13 +23,15 @@ namespace {
 template <int TN, int RB, int NBUF, bool OUT_F32>
 __global__ __launch_bounds__(512) void gemm_nt_kernel(int M, int N, int S, int s_per_split, const bf16* __restrict__ A,
                                                       long lda, const bf16* __restrict__ B, long ldb, void* __restrict__ C,
-                                                      long ldc, long split_stride, int vout, int tile0, int compact) {
+                                                      long ldc, long split_stride, int vout, int tile0, int compact,
+                                                      const bf16* __restrict__ bias) {
   constexpr int BM = 256, BN = 128 * TN, SA = BM * RB, SS = (BM + BN) * RB, NBLK = SS / 1024, BPW = NBLK / 8;
   constexpr int CPR = RB / 16, RPB = 1024 / RB, KS = RB / 32, EPS = RB / 2;
   constexpr int RPASS = 64, RP = BN + 4;
   static_assert(RB == 64 || RB == 128, "64- or 128-byte stage rows");
   static_assert(BPW * 8 == NBLK, "copy blocks divide over the waves");
-  static_assert(NBUF >= 2 && NBUF * SS <= 160 * 1024 && RPASS * RP * 4 <= 160 * 1024, "stages and epilogue fit in LDS");
+  static_assert(NBUF >= 2 && NBUF * SS <= 160 * 1024 && (RPASS * RP + BN) * 4 <= 160 * 1024,
+                "stages and epilogue fit in LDS");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
   const int n_m = (M + BM - 1) / BM, n_n = (N + BN - 1) / BN;
@@ -107,7 +111,9 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(int M, int N, int S, int s
   lds_wait();
 
   // epilogue: passes of RPASS rows, accumulators -> LDS -> global
-  float* red = reinterpret_cast<float*>(smem);  // [RPASS][RP]
+  float* red = reinterpret_cast<float*>(smem);  // [RPASS][RP], then the tile's bias [BN]
+  float* bsh = red + RPASS * RP;
+  const bool add_bias = bias && gridDim.y == 1 && !compact;  // final sums only
   constexpr int CH = OUT_F32 ? 4 : 8;            // elements per 16-byte chunk
   // compact: this workgroup's whole BM x BN float32 tile at (z gridDim.x + blockIdx.x) BM BN
   char* cbase = compact ? reinterpret_cast<char*>(C) + ((size_t)z * gridDim.x + blockIdx.x) * BM * BN * 4
@@ -126,6 +132,9 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(int M, int N, int S, int s
         for (int r = 0; r < 16; ++r) red[(rbase + acc_row(r, lane)) * RP + col] = acc[a][t][r];
       }
     }
+    // the tile's bias columns, once (after the first barrier: no wave still reads a stage there)
+    if (add_bias && ps == 0)
+      for (int t = tid; t < BN; t += 512) bsh[t] = n0 + t < N ? to_f32(bias[n0 + t]) : 0.f;
     __syncthreads();
     for (int e = tid; e < RPASS * (BN / CH); e += 512) {
       const int row = e / (BN / CH), ch = e % (BN / CH);
@@ -137,22 +146,26 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(int M, int N, int S, int s
         continue;
       }
       if (m >= M || n >= N) continue;
+      float val[CH];
+#pragma unroll
+      for (int q = 0; q < CH; ++q) val[q] = v[q] + (add_bias ? bsh[ch * CH + q] : 0.f);
       if (OUT_F32) {
         float* dst = reinterpret_cast<float*>(cbase) + (size_t)m * ldc + n;
         if (vout && n + CH <= N) {
-          gstore16(dst, __builtin_bit_cast(u32x4, f32x4{v[0], v[1], v[2], v[3]}));
+          gstore16(dst, __builtin_bit_cast(u32x4, f32x4{val[0], val[1], val[2], val[3]}));
         } else {
-          for (int q = 0; q < CH && n + q < N; ++q) dst[q] = v[q];
+#pragma unroll
+          for (int q = 0; q < CH; ++q)
+            if (n + q < N) dst[q] = val[q];
         }
       } else {
         bf16* dst = reinterpret_cast<bf16*>(cbase) + (size_t)m * ldc + n;
         if (vout && n + CH <= N) {
-          float vv[8];
-#pragma unroll
-          for (int q = 0; q < 8; ++q) vv[q] = v[q];
-          gstore16(dst, pack16<bf16>(vv));
+          gstore16(dst, pack16<bf16>(val));
         } else {
-          for (int q = 0; q < CH && n + q < N; ++q) dst[q] = from_f32<bf16>(v[q]);
+#pragma unroll
+          for (int q = 0; q < CH; ++q)
+            if (n + q < N) dst[q] = from_f32<bf16>(val[q]);
         }
       }
     }
@@ -166,7 +179,8 @@ __global__ __launch_bounds__(512) void gemm_nt_kernel(int M, int N, int S, int s
 // VST: C rows take one 8-byte (bf16) or 16-byte (float32) store per thread.
 template <bool OUT_F32>
 __global__ __launch_bounds__(256) void gemm_split_reduce(int M, int N, int nz, const float* __restrict__ part,
-                                                         void* __restrict__ C, long ldc, int vst) {
+                                                         void* __restrict__ C, long ldc, int vst,
+                                                         const bf16* __restrict__ bias) {
   const int n4 = (N + 3) / 4;
   const long total = (long)M * n4;
   const size_t zs = (size_t)M * N;
@@ -191,6 +205,11 @@ __global__ __launch_bounds__(256) void gemm_split_reduce(int M, int N, int nz, c
       for (int z = 0; z < nz; ++z)
 #pragma unroll
         for (int q = 0; q < 4; ++q) s[q] += p[z * zs + off[q]];
+    }
+    if (bias) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (n + q < N) s[q] += to_f32(bias[n + q]);
     }
     if (vst && n + 4 <= N) {
       if (OUT_F32) {
@@ -218,7 +237,7 @@ __global__ __launch_bounds__(256) void gemm_split_reduce(int M, int N, int nz, c
 template <bool OUT_F32>
 __global__ __launch_bounds__(256) void gemm_tail_reduce(int M, int N, int n_m, int n_n, int tile0, int n_tail, int nz,
                                                         int BN, const float* __restrict__ part, void* __restrict__ C,
-                                                        long ldc, int vst) {
+                                                        long ldc, int vst, const bf16* __restrict__ bias) {
   int tm, tn;
   xcd_tile_grouped(tile0 + blockIdx.y, n_m, n_n, 8, tm, tn);
   const int m0 = tm * 256, n0 = tn * BN, c4 = BN / 4;
@@ -235,6 +254,11 @@ __global__ __launch_bounds__(256) void gemm_tail_reduce(int M, int N, int n_m, i
       s[1] += v.y;
       s[2] += v.z;
       s[3] += v.w;
+    }
+    if (bias) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (n + q < N) s[q] += to_f32(bias[n + q]);
     }
     if (vst && n + 4 <= N) {
       if (OUT_F32) {
@@ -302,8 +326,9 @@ GemmCfg pick_gemm(long M, long N, long S) {
 
 template <int TN, int RB, int NBUF, bool OUT_F32>
 int launch_gemm(int M, int N, int S, int nz, const bf16* A, long lda, const bf16* B, long ldb, void* C, long ldc,
-                long split_stride, int vout, hipStream_t s, long tile0 = 0, long n_tiles = -1, int compact = 0) {
-  constexpr int SS = (256 + 128 * TN) * RB, EPI = 64 * (128 * TN + 4) * 4;
+                long split_stride, int vout, hipStream_t s, long tile0 = 0, long n_tiles = -1, int compact = 0,
+                const bf16* bias = nullptr) {
+  constexpr int SS = (256 + 128 * TN) * RB, EPI = 64 * (128 * TN + 4) * 4 + 128 * TN * 4;
   constexpr size_t lds = (size_t)NBUF * SS > (size_t)EPI ? (size_t)NBUF * SS : (size_t)EPI;
   auto kern = gemm_nt_kernel<TN, RB, NBUF, OUT_F32>;
   if (!reserve_lds((const void*)kern, lds)) return fail(KF_ELAUNCH, "gemm: cannot reserve %zu bytes of LDS", lds);
@@ -311,18 +336,18 @@ int launch_gemm(int M, int N, int S, int nz, const bf16* A, long lda, const bf16
   if (n_tiles < 0) n_tiles = (long)n_m * n_n;
   const int s_per = (S + nz - 1) / nz;
   hipLaunchKernelGGL(kern, dim3((unsigned)n_tiles, (unsigned)nz), dim3(512), lds, s, M, N, S, s_per, A, lda, B, ldb,
-                     C, ldc, split_stride, vout, (int)tile0, compact);
+                     C, ldc, split_stride, vout, (int)tile0, compact, bias);
   return check_launch("gemm_nt");
 }
 
 // Tail split: the whole rounds into C, the tail tiles' compact partials into ws, their sum into C.
 template <int TN>
 int launch_gemm_tail(const GemmCfg& c, int M, int N, int S, const bf16* A, long lda, const bf16* B, long ldb, void* C,
-                     long ldc, bool out_f32, void* ws, hipStream_t s) {
+                     long ldc, bool out_f32, void* ws, hipStream_t s, const bf16* bias) {
   const int CH = out_f32 ? 4 : 8;
   const int vout = ldc % CH == 0 && aligned16(C);
-  int rc = out_f32 ? launch_gemm<TN, 128, 2, true>(M, N, S, 1, A, lda, B, ldb, C, ldc, 0, vout, s, 0, c.full)
-                   : launch_gemm<TN, 128, 2, false>(M, N, S, 1, A, lda, B, ldb, C, ldc, 0, vout, s, 0, c.full);
+  int rc = out_f32 ? launch_gemm<TN, 128, 2, true>(M, N, S, 1, A, lda, B, ldb, C, ldc, 0, vout, s, 0, c.full, 0, bias)
+                   : launch_gemm<TN, 128, 2, false>(M, N, S, 1, A, lda, B, ldb, C, ldc, 0, vout, s, 0, c.full, 0, bias);
   if (rc) return rc;
   rc = launch_gemm<TN, 128, 2, true>(M, N, S, c.tail_nz, A, lda, B, ldb, ws, 0, 0, 1, s, c.full, c.rem, 1);
   if (rc) return rc;
@@ -331,10 +356,10 @@ int launch_gemm_tail(const GemmCfg& c, int M, int N, int S, const bf16* A, long 
   const dim3 grid(16, (unsigned)c.rem);
   if (out_f32)
     hipLaunchKernelGGL(gemm_tail_reduce<true>, grid, dim3(256), 0, s, M, N, n_m, n_n, (int)c.full, (int)c.rem,
-                       c.tail_nz, BN, (const float*)ws, C, ldc, vst);
+                       c.tail_nz, BN, (const float*)ws, C, ldc, vst, bias);
   else
     hipLaunchKernelGGL(gemm_tail_reduce<false>, grid, dim3(256), 0, s, M, N, n_m, n_n, (int)c.full, (int)c.rem,
-                       c.tail_nz, BN, (const float*)ws, C, ldc, vst);
+                       c.tail_nz, BN, (const float*)ws, C, ldc, vst, bias);
   return check_launch("gemm tail reduce");
 }
 
@@ -354,7 +379,8 @@ size_t gemm_nt_workspace(long M, long N, long K) {
 }
 
 int gemm_nt(long M, long N, long K, const void* A, long lda, const void* B, long ldb, void* C, long ldc, bool out_f32,
-            void* ws, size_t ws_bytes, hipStream_t s) {
+            void* ws, size_t ws_bytes, hipStream_t s, const void* bias_v) {
+  const bf16* bias = (const bf16*)bias_v;
   if (M <= 0 || N <= 0) return KF_OK;
   if (K % 64 || lda % 8 || ldb % 8 || !aligned16(A) || !aligned16(B) || K > lda || K > ldb)
     return fail(KF_EINVAL, "gemm: operands must be 16-byte aligned with whole 64-element stages");
@@ -365,19 +391,19 @@ int gemm_nt(long M, long N, long K, const void* A, long lda, const void* B, long
   if (c.tail_nz) {
     const size_t need = split_bytes(c, M, N);
     if (!ws || ws_bytes < need || !aligned16(ws)) return fail(KF_EWORKSPACE, "gemm: split workspace of %zu bytes needed", need);
-    return c.tn == 3   ? launch_gemm_tail<3>(c, (int)M, (int)N, S, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, out_f32, ws, s)
-           : c.tn == 2 ? launch_gemm_tail<2>(c, (int)M, (int)N, S, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, out_f32, ws, s)
-                       : launch_gemm_tail<1>(c, (int)M, (int)N, S, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, out_f32, ws, s);
+    return c.tn == 3   ? launch_gemm_tail<3>(c, (int)M, (int)N, S, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, out_f32, ws, s, bias)
+           : c.tn == 2 ? launch_gemm_tail<2>(c, (int)M, (int)N, S, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, out_f32, ws, s, bias)
+                       : launch_gemm_tail<1>(c, (int)M, (int)N, S, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, out_f32, ws, s, bias);
   }
   if (c.nz == 1) {
     const int vout = ldc % CH == 0 && aligned16(C);
     if (out_f32)
-      return c.tn == 3   ? launch_gemm<3, 128, 2, true>((int)M, (int)N, S, 1, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, 0, vout, s)
-             : c.tn == 2 ? launch_gemm<2, 128, 2, true>((int)M, (int)N, S, 1, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, 0, vout, s)
-                         : launch_gemm<1, 128, 2, true>((int)M, (int)N, S, 1, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, 0, vout, s);
-    return c.tn == 3   ? launch_gemm<3, 128, 2, false>((int)M, (int)N, S, 1, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, 0, vout, s)
-           : c.tn == 2 ? launch_gemm<2, 128, 2, false>((int)M, (int)N, S, 1, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, 0, vout, s)
-                       : launch_gemm<1, 128, 2, false>((int)M, (int)N, S, 1, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, 0, vout, s);
+      return c.tn == 3   ? launch_gemm<3, 128, 2, true>((int)M, (int)N, S, 1, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, 0, vout, s, 0, -1, 0, bias)
+             : c.tn == 2 ? launch_gemm<2, 128, 2, true>((int)M, (int)N, S, 1, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, 0, vout, s, 0, -1, 0, bias)
+                         : launch_gemm<1, 128, 2, true>((int)M, (int)N, S, 1, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, 0, vout, s, 0, -1, 0, bias);
+    return c.tn == 3   ? launch_gemm<3, 128, 2, false>((int)M, (int)N, S, 1, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, 0, vout, s, 0, -1, 0, bias)
+           : c.tn == 2 ? launch_gemm<2, 128, 2, false>((int)M, (int)N, S, 1, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, 0, vout, s, 0, -1, 0, bias)
+                       : launch_gemm<1, 128, 2, false>((int)M, (int)N, S, 1, (const bf16*)A, lda, (const bf16*)B, ldb, C, ldc, 0, vout, s, 0, -1, 0, bias);
   }
   const size_t need = (size_t)c.nz * M * N * sizeof(float);
   if (!ws || ws_bytes < need || !aligned16(ws)) return fail(KF_EWORKSPACE, "gemm: split workspace of %zu bytes needed", need);
@@ -391,9 +417,9 @@ int gemm_nt(long M, long N, long K, const void* A, long lda, const void* B, long
   // whole 4-column stores: rows start 8- (bf16) or 16-byte (float32) aligned
   const int vst = ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(C) & (out_f32 ? 15 : 7)) == 0;
   if (out_f32)
-    hipLaunchKernelGGL(gemm_split_reduce<true>, dim3((unsigned)blocks), dim3(256), 0, s, (int)M, (int)N, c.nz, (const float*)ws, C, ldc, vst);
+    hipLaunchKernelGGL(gemm_split_reduce<true>, dim3((unsigned)blocks), dim3(256), 0, s, (int)M, (int)N, c.nz, (const float*)ws, C, ldc, vst, bias);
   else
-    hipLaunchKernelGGL(gemm_split_reduce<false>, dim3((unsigned)blocks), dim3(256), 0, s, (int)M, (int)N, c.nz, (const float*)ws, C, ldc, vst);
+    hipLaunchKernelGGL(gemm_split_reduce<false>, dim3((unsigned)blocks), dim3(256), 0, s, (int)M, (int)N, c.nz, (const float*)ws, C, ldc, vst, bias);
   return check_launch("gemm split reduce");
 }
 

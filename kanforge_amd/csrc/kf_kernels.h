@@ -1164,8 +1164,8 @@ __global__ __launch_bounds__(kThreads) void features_t_kernel(KBasis bs, int B, 
 // 16-byte chunks. (IN K) % 8 == 0, ld % 8 == 0 and phi 16-byte aligned; K <= 16. EVEN: every
 // input's knots are evenly spaced (knots_uniform given) and n_knots >= 4.
 // Rows are ld elements apart. With base_cols > 0 each row continues after its IN K features with
-// silu(x[b, i]) at IN K + i (the SiLU base branch as extra features), a 1 at IN K + IN (the
-// bias's feature) and zeros up to IN K + base_cols (the first column of blocks writes those).
+// silu(x[b, i]) at IN K + i (the SiLU base branch as extra features) and zeros up to
+// IN K + base_cols (the first column of blocks writes those).
 template <typename T, int KD, bool EVEN = false>
 __global__ __launch_bounds__(kThreads) void phi_block_kernel(KBasis bs, int B, int IN, const T* __restrict__ x,
                                                              T* __restrict__ phi, long ld, int base_cols) {
@@ -1230,22 +1230,21 @@ __global__ __launch_bounds__(kThreads) void phi_block_kernel(KBasis bs, int B, i
       if (b < B && i < IN) phi[(size_t)b * ld + c0 + i] = from_f32<T>(silu_f(xv[u]));
     }
     if (blockIdx.x == 0) {
-      const int pad = base_cols - IN;  // the bias's 1, then zeros
+      const int pad = base_cols - IN;  // zeros up to whole stages
       for (int e = threadIdx.x; e < ROWS * pad; e += kThreads) {
         const int bl = e / pad, j = e - bl * pad, b = b0 + bl;
-        if (b < B) phi[(size_t)b * ld + c0 + IN + j] = from_f32<T>(j == 0 ? 1.f : 0.f);
+        if (b < B) phi[(size_t)b * ld + c0 + IN + j] = from_f32<T>(0.f);
       }
     }
   }
 }
 
-// The B operand of a B-spline F with the SiLU base branch and bias as extra features: row o of
-// out (OUT, ld) is c[o] (IN K values), then w[o] (IN), then bias[o] (0 without a bias), then
-// zeros up to ld; 8 elements a thread, 16-byte loads and stores where the row stays inside c.
+// The B operand of a B-spline F with the SiLU base branch as extra features: row o of out
+// (OUT, ld) is c[o] (IN K values), then w[o] (IN), then zeros up to ld; 8 elements a thread,
+// 16-byte loads and stores where the row stays inside c.
 template <typename T>
 __global__ __launch_bounds__(kThreads) void base_coef_kernel(int OUT, int IN, int K, long ld, const T* __restrict__ c,
-                                                             const T* __restrict__ w, const T* __restrict__ bias,
-                                                             T* __restrict__ out) {
+                                                             const T* __restrict__ w, T* __restrict__ out) {
   const long ck = (long)IN * K, per = ld / 8, n = (long)OUT * per;
   for (long e = blockIdx.x * (long)kThreads + threadIdx.x; e < n; e += (long)gridDim.x * kThreads) {
     const int o = (int)(e / per);
@@ -1259,10 +1258,7 @@ __global__ __launch_bounds__(kThreads) void base_coef_kernel(int OUT, int IN, in
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
       const long j = j0 + q;
-      v[q] = j < ck             ? to_f32(c[(size_t)o * ck + j])
-             : j < ck + IN      ? to_f32(w[(size_t)o * IN + (j - ck)])
-             : j == ck + IN && bias ? to_f32(bias[o])
-                                : 0.f;
+      v[q] = j < ck ? to_f32(c[(size_t)o * ck + j]) : j < ck + IN ? to_f32(w[(size_t)o * IN + (j - ck)]) : 0.f;
     }
     gstore16(dst, pack16<T>(v));
   }

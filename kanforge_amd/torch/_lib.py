@@ -46,6 +46,7 @@ EXPORTS = (
     "kf_lut_forward",
     "kf_base_fused",
     "kf_F_base",
+    "kf_F_bias",
     "kf_P_base",
     "kf_G_base",
     "kf_last_error",
@@ -126,7 +127,8 @@ def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
         lib.kf_F_base.argtypes = [P, c_int, c_int64, c_int64, c_int64] + [c_void_p] * 6 + [c_size_t, c_void_p]
         lib.kf_P_base.argtypes = [P, c_int, c_int64, c_int64, c_int64] + [c_void_p] * 6 + [c_size_t, c_void_p]
         lib.kf_G_base.argtypes = [P, c_int, c_int64, c_int64, c_int64] + [c_void_p] * 6 + [c_size_t, c_void_p]
-        for name in ("kf_base_fused", "kf_F_base", "kf_P_base", "kf_G_base"):
+        lib.kf_F_bias.argtypes = [P, c_int, c_int64, c_int64, c_int64] + [c_void_p] * 6 + [c_size_t, c_void_p]
+        for name in ("kf_base_fused", "kf_F_base", "kf_P_base", "kf_G_base", "kf_F_bias"):
             getattr(lib, name).restype = c_int
         lib.kf_last_error.argtypes = []
         lib.kf_last_error.restype = c_char_p

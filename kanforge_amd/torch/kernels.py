@@ -206,8 +206,9 @@ def _workspace(op: int, desc, dt: int, batch: int, n_in: int, n_out: int, device
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
 
-def _raw(op: str, plan: KernelPlan, m: int, x, a, b, st: BasisState | None, n_out: int, h=None):
-    """op F: (x, w, c) -> y (B, out); G: (x, w, g) -> dc (out, in, K); P: (x, g, c) -> p (B, in).
+def _raw(op: str, plan: KernelPlan, m: int, x, a, b, st: BasisState | None, n_out: int, h=None, bias=None):
+    """op F: (x, w, c) -> y (B, out), plus ``bias`` (out) when given (kf_F_bias); G: (x, w, g) ->
+    dc (out, in, K); P: (x, g, c) -> p (B, in).
 
     ``x`` (B, in) and every other array share the dtype of ``x``; ``w`` may be None.
     """
@@ -226,8 +227,13 @@ def _raw(op: str, plan: KernelPlan, m: int, x, a, b, st: BasisState | None, n_ou
             c = c.contiguous()
             y = torch.empty(batch, n_out, dtype=x.dtype, device=dev)
             ws = _workspace(_lib.KF_OP_F, desc, dt, batch, n_in, n_out, dev)
-            rc = lib.kf_F(ctypes.byref(desc), dt, batch, n_in, n_out, _ptr(x), _ptr(w), _ptr(c), _ptr(y), _ptr(ws), ws.numel(), stream)
-            _lib.check(rc, "kf_F")
+            if bias is None:
+                rc = lib.kf_F(ctypes.byref(desc), dt, batch, n_in, n_out, _ptr(x), _ptr(w), _ptr(c), _ptr(y), _ptr(ws), ws.numel(), stream)
+                _lib.check(rc, "kf_F")
+            else:
+                rc = lib.kf_F_bias(ctypes.byref(desc), dt, batch, n_in, n_out, _ptr(x), _ptr(w), _ptr(c),
+                                   _ptr(bias.contiguous()), _ptr(y), _ptr(ws), ws.numel(), stream)
+                _lib.check(rc, "kf_F_bias")
             return y
         if op == "G":
             w, g = a, b
@@ -474,14 +480,11 @@ def _F_setup(ctx, inputs, output):
     _save(ctx, (x, w, c, knots, knots_cmp, knots_u, num, den), plan, m)
 
 
-def _F_backward(ctx, gy):
-    x, w, c, knots, knots_cmp, knots_u, num, den = ctx.saved_tensors
-    plan, m = ctx.plan, ctx.m
-    need = ctx.needs_input_grad
+def _f_grads(x, w, c, tabs, plan, m, need, gy):
+    """(gx, gw, gc, gnum, gden) of sum gy F_m(x, w, c); need = (x, w, c, num, den) flags."""
     gx = gw = gc = gnum = gden = None
-    gy = gy.contiguous()
-    tabs = (knots, knots_cmp, knots_u, num, den)
-    if plan_of(plan).kind == "rational" and (need[6] or need[7]):
+    num, den = tabs[3], tabs[4]
+    if plan_of(plan).kind == "rational" and (need[3] or need[4]):
         p1, gnum, gden = _RBWD(x, gy, c, w, num, den, plan, m)
         if need[0]:
             # under create_graph the x-gradient stays differentiable through kf::P
@@ -492,6 +495,14 @@ def _F_backward(ctx, gy):
         gc = _G(x, gy, w, *tabs, plan, m)
     if need[1]:
         gw = _P(x, gy, c, *tabs, plan, m)
+    return gx, gw, gc, gnum, gden
+
+
+def _F_backward(ctx, gy):
+    x, w, c, knots, knots_cmp, knots_u, num, den = ctx.saved_tensors
+    n = ctx.needs_input_grad
+    gx, gw, gc, gnum, gden = _f_grads(x, w, c, (knots, knots_cmp, knots_u, num, den), ctx.plan, ctx.m,
+                                      (n[0], n[1], n[2], n[6], n[7]), gy.contiguous())
     return gx, gw, gc, None, None, None, gnum, gden, None, None
 
 
@@ -582,18 +593,24 @@ def prim_P(x, g, c, st, plan, m=0, num=None, den=None):
     return _P(x, g, c, *_tables(st), num, den, plan_key(plan), m)
 
 
-def spline_forward(x: torch.Tensor, coef: torch.Tensor, st: BasisState | None, plan: KernelPlan | str, num=None, den=None) -> torch.Tensor:
-    """sum_{i,k} coef[o,i,k] phi_k(x[..., i]) through the HIP F kernel.
+def spline_forward(x: torch.Tensor, coef: torch.Tensor, st: BasisState | None, plan: KernelPlan | str, num=None, den=None,
+                   bias: torch.Tensor | None = None) -> torch.Tensor:
+    """sum_{i,k} coef[o,i,k] phi_k(x[..., i]) (+ bias[o]) through the HIP F kernel.
 
-    Computes in the coefficients' dtype (float32 or bfloat16) and returns
-    ``x.dtype``.
+    Computes in the coefficients' dtype (float32 or bfloat16) and returns ``x.dtype``; a bias in
+    that dtype rides F's last kernel (kf_F_bias), one in another dtype is added afterwards.
     """
     lead = x.shape[:-1]
     x2 = x.reshape(-1, x.shape[-1])
     if x2.dtype != coef.dtype:
         x2 = x2.to(coef.dtype)
+    if bias is not None and bias.dtype == coef.dtype and x.dtype == coef.dtype:
+        nr, dr = _rat(st, num, den)
+        y = _F_BIAS(x2, None, coef, bias, *_tables(st), nr, dr, plan_key(plan), 0)
+        return y.reshape(*lead, coef.shape[0])
     y = prim_F(x2, coef, None, st, plan, 0, num, den)
-    return y.to(x.dtype).reshape(*lead, coef.shape[0])
+    y = y.to(x.dtype).reshape(*lead, coef.shape[0])
+    return y if bias is None else bias_add(y, bias)
 
 
 # --- basis values and edge derivatives ---------------------------------------------
@@ -951,6 +968,43 @@ def bspline_interval(x: torch.Tensor, knots_cmp: torch.Tensor) -> torch.Tensor:
     return op_bspline_interval(x, knots_cmp)
 
 
+# --- F with the layer's bias -----------------------------------------------------------
+
+
+def _F_bias_impl(x: torch.Tensor, w: Opt, c: torch.Tensor, bias: torch.Tensor, knots: Opt, knots_cmp: Opt, knots_u: Opt,
+                 num: Opt, den: Opt, plan: str, m: int) -> torch.Tensor:
+    """y[b,o] = sum_{i,k} w[b,i] c[o,i,k] phi_k^(m)(x[b,i]) + bias[o] (kf_F_bias)."""
+    return _raw("F", plan_of(plan), m, x, w, c, _state(knots, knots_cmp, knots_u, num, den, x.shape[1]), c.shape[0],
+                bias=bias)
+
+
+op_F_bias = torch.library.custom_op("kf::F_bias", mutates_args=())(_F_bias_impl)
+
+
+@op_F_bias.register_fake
+def _(x, w, c, bias, knots, knots_cmp, knots_u, num, den, plan, m):
+    return x.new_empty(x.shape[0], c.shape[0])
+
+
+def _F_bias_setup(ctx, inputs, output):
+    x, w, c, bias, knots, knots_cmp, knots_u, num, den, plan, m = inputs
+    _save(ctx, (x, w, c, knots, knots_cmp, knots_u, num, den), plan, m)
+    ctx.bias_dtype = bias.dtype
+
+
+def _F_bias_backward(ctx, gy):
+    x, w, c, knots, knots_cmp, knots_u, num, den = ctx.saved_tensors
+    n = ctx.needs_input_grad
+    gy = gy.contiguous()
+    gx, gw, gc, gnum, gden = _f_grads(x, w, c, (knots, knots_cmp, knots_u, num, den), ctx.plan, ctx.m,
+                                      (n[0], n[1], n[2], n[7], n[8]), gy)
+    gb = _COLSUM(gy).to(ctx.bias_dtype) if n[3] else None
+    return gx, gw, gc, gb, None, None, None, gnum, gden, None, None
+
+
+op_F_bias.register_autograd(_F_bias_backward, setup_context=_F_bias_setup)
+
+
 # --- the SiLU base branch and bias fused into the contractions ----------------------
 #
 # The reference's layer adds F.linear(silu(x), base_weight) and the bias to the spline part
@@ -1182,3 +1236,4 @@ _EDGE = _Entry(op_edge, _edge_impl, _edge_setup, _edge_backward)
 _F_BASE = _Entry(op_F_base, _F_base_impl, _F_base_setup, _F_base_backward)
 _P_BASE = _Direct(op_P_base, _P_base_impl)
 _G_BASE = _Direct(op_G_base, _G_base_impl)
+_F_BIAS = _Entry(op_F_bias, _F_bias_impl, _F_bias_setup, _F_bias_backward)

@@ -223,10 +223,14 @@ class KANLinear(nn.Module):
             y = _kernels.spline_base_forward(x, self.effective_coef(), self.effective_base_weight(), self.bias, st,
                                              self._plan_key)
             return y + self._symbolic_sum(x) if self._sym_codes else y
+        # without a base branch or symbolic part to add after F, the bias rides F's last kernel
+        fold_bias = self.bias is not None and self.base_weight is None and not self._sym_codes
+        b = self.bias if fold_bias else None
         if self._plan.kind == "rational":
-            y = _kernels.spline_forward(x, self.effective_coef(), st, self._plan_key, self.basis_numerator, self.basis_denominator)
+            y = _kernels.spline_forward(x, self.effective_coef(), st, self._plan_key, self.basis_numerator,
+                                        self.basis_denominator, bias=b)
         else:
-            y = _kernels.spline_forward(x, self.effective_coef(), st, self._plan_key)
+            y = _kernels.spline_forward(x, self.effective_coef(), st, self._plan_key, bias=b)
         if self.base_weight is not None:
             # accumulated into y by the GEMM itself (C = y + act(x) W^T), no separate add (an
             # in-place addmm_ on F's output costs more: its backward copies through the view)
@@ -235,7 +239,7 @@ class KANLinear(nn.Module):
             y = y2.reshape(y.shape)
         if self._sym_codes:
             y = y + self._symbolic_sum(x)
-        if self.bias is not None:
+        if self.bias is not None and not fold_bias:
             y = _kernels.bias_add(y, self.bias)
         return y
 

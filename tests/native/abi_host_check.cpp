@@ -294,6 +294,16 @@ int main() {
           "G_base with nothing wanted");
   }
 
+  {
+    const kf_basis c0 = cheb(9, 0, 9, KF_MAP_TANH);
+    expect_error("kf_F_bias NULL y", kf_F_bias(&c0, KF_BF16, 64, 32, 16, d, nullptr, d, d, nullptr, d, 1 << 20, nullptr),
+                 KF_EINVAL);
+    expect_error("kf_F_bias small workspace",
+                 kf_F_bias(&c0, KF_BF16, 8192, 768, 3072, d, nullptr, d, d, d, d, 64, nullptr), KF_EWORKSPACE);
+    check(kf_F_bias(&c0, KF_F32, 0, 4, 4, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0, nullptr) == KF_OK,
+          "empty F_bias");
+  }
+
   // empty calls succeed without touching a device
   check(kf_F(&cb, KF_F32, 0, 4, 4, nullptr, nullptr, nullptr, nullptr, nullptr, 0, nullptr) == KF_OK, "empty F");
   check(kf_G(&cb, KF_F32, 4, 0, 4, nullptr, nullptr, nullptr, nullptr, nullptr, 0, nullptr) == KF_OK, "empty G");

@@ -1,5 +1,5 @@
 """KANLinear with its SiLU base branch and bias fused into the HIP contractions (kf_F_base,
-kf_P_base, kf_G_base) against the float64 oracle: y and every first-order gradient on layers
+kf_P_base, kf_G_base), and F with the bias alone (kf_F_bias), against the float64 oracle: y and every first-order gradient on layers
 whose three entries all fuse (Chebyshev degrees 8, 7 and 5: chunks of 9 features, and even counts
 on the runtime-count F kernel) and on cubic B-spline layers, ragged shapes (inputs not a multiple of 16, outputs not of 8,
 batch not of 64), the headline shape 768 -> 3072 at batch 8192 against a plain PyTorch float32
@@ -223,3 +223,38 @@ def test_fused_calls_are_deterministic():
     torch.cuda.synchronize()
     for a, b in zip(*outs):
         assert torch.equal(a, b)
+
+
+BIAS_CASES = [
+    ("cheb8", kf.Chebyshev(8), torch.bfloat16, 300, 96, 200),  # register-A kernel: per-output constant
+    ("bspline83", kf.BSpline(8, 3), torch.bfloat16, 257, 64, 130),  # GEMM core epilogue
+    ("rational", kf.Rational(5, 4), torch.bfloat16, 300, 128, 96),  # GEMM core epilogue
+    ("cheb8_f32", kf.Chebyshev(8), torch.float32, 77, 24, 19),  # one more pass
+    ("bspline53_f32", kf.BSpline(5, 3), torch.float32, 4096, 64, 64),  # sparse route, one more pass
+]
+
+
+@pytest.mark.parametrize("name,basis,dtype,B,IN,OUT", BIAS_CASES, ids=[c[0] for c in BIAS_CASES])
+def test_F_bias_is_F_plus_bias(name, basis, dtype, B, IN, OUT):
+    """kf_F_bias against kf_F plus the bias in float32 (bf16: the fused routes add the bias before
+    the one rounding, so within two bf16 roundings of it; float32 routes add it exactly)."""
+    torch.manual_seed(1)
+    layer = KANLinear(IN, OUT, basis, base_activation=None, groups=8 if name == "rational" else None).to(DEV, dtype)
+    with torch.no_grad():
+        layer.bias.normal_()
+    x = torch.randn(B, IN, device=DEV).to(dtype) * 0.8
+    st = layer._basis_state()
+    num = den = None
+    if layer._plan.kind == "rational":
+        num, den = layer.basis_numerator, layer.basis_denominator
+    with torch.no_grad():
+        fused = K.spline_forward(x, layer.coef, st, layer._plan_key, num, den, bias=layer.bias)
+        plain = K.spline_forward(x, layer.coef, st, layer._plan_key, num, den)
+    torch.cuda.synchronize()
+    want = plain.float() + layer.bias.float()
+    if dtype == torch.float32:
+        torch.testing.assert_close(fused, want, rtol=1e-6, atol=1e-6)
+    else:
+        err = ((fused.float() - want).abs().max() / want.abs().max()).item()
+        assert err <= 1e-2, err
+

@@ -103,6 +103,13 @@ def test_opcheck_fused_base_ops(kind):
     torch.library.opcheck(torch.ops.kf.G_base.default, (x, gy, *t3, key, False, True, False))
 
 
+@pytest.mark.parametrize("name", ["cheb8", "bspline53", "rational"])
+def test_opcheck_F_bias(name):
+    key, x, c, gy, w, tabs = _operands(BASES[name])
+    bias = torch.randn(c.shape[0], device=DEV).requires_grad_()
+    torch.library.opcheck(torch.ops.kf.F_bias.default, (x, None, c, bias, *tabs, key, 0))
+
+
 def _grads(layer, x, gy):
     params = [p for p in layer.parameters()]
     y = layer(x)
