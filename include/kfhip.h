@@ -110,6 +110,7 @@ typedef struct kf_basis {
 #define KF_OP_F_BASE 3
 #define KF_OP_P_BASE 4
 #define KF_OP_G_BASE 5
+#define KF_OP_G_BIAS 6 /* kf_G_bias (kf_F_bias needs kf_F's workspace, KF_OP_F) */
 
 /*
  * Scratch bytes kf_F / kf_G / kf_P need for these shapes (0 is possible).
@@ -157,6 +158,16 @@ int kf_F_noalloc(const kf_basis *basis, int dtype, int64_t batch, int64_t n_in, 
  */
 int kf_G(const kf_basis *basis, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void *x,
          const void *g, const void *w, void *dc, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * kf_G plus the bias gradient dbias[o] = sum_b g[b,o] (dtype, n_out; NULL: exactly kf_G), what
+ * autograd computes for `y + self.bias` (kanforge/torch/layers.py:189-190) next to _G. The column
+ * sums come from the block partials of G's own transpose of g where its route has one, else from
+ * kf_column_sums. Workspace: kf_workspace_bytes(KF_OP_G_BIAS, ...).
+ */
+int kf_G_bias(const kf_basis *basis, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void *x,
+              const void *g, const void *w, void *dc, void *dbias, void *workspace, size_t workspace_bytes,
+              void *stream);
 
 /*
  * p[b,i] = sum_{o,k} g[b,o] c[o,i,k] phi_k^(m)(x[b,i])            (op "P")

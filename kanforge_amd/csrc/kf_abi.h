@@ -439,6 +439,23 @@ inline WsGB ws_g_base(const kf_basis* b, int dtype, int64_t batch, int64_t n_in,
   return w;
 }
 
+// workspace of kf_G_bias: G's (the larger of its weighted and unweighted layouts), then the
+// transpose's block partials and the column sums for the bias gradient, then the column-sum
+// kernels' scratch for the routes without a transpose (the sparse ones)
+struct WsGBias {
+  size_t g, part, sums, cws, total;
+};
+inline WsGBias ws_g_bias(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, bool has_w) {
+  WsGBias w;
+  const WsG L = ws_g(b, dtype, batch, n_in, n_out, has_w);
+  w.g = L.total;
+  w.part = align256((size_t)((L.BP + 63) / 64) * L.OUTP * sizeof(float));
+  w.sums = align256((size_t)L.OUTP * sizeof(float));
+  w.cws = align256(kf_column_sums_workspace_bytes(batch, n_out));
+  w.total = w.g + w.part + w.sums + w.cws;
+  return w;
+}
+
 template <typename Fn>
 int with_spline_degree(int kd, Fn&& fn) {
   switch (kd) {

@@ -93,6 +93,10 @@ size_t kf_workspace_bytes(int op, const kf_basis* b, int dtype, int64_t batch, i
       const size_t a = ws_g(b, dtype, batch, n_in, n_out, true).total, u = ws_g(b, dtype, batch, n_in, n_out, false).total;
       return a > u ? a : u;
     }
+    case KF_OP_G_BIAS: {
+      const size_t a = ws_g_bias(b, dtype, batch, n_in, n_out, true).total, u = ws_g_bias(b, dtype, batch, n_in, n_out, false).total;
+      return a > u ? a : u;
+    }
     case KF_OP_F_BASE:
       if (!f_base_route(b, dtype, batch, n_in, n_out)) return 0;
       return b->kind == KF_KIND_BSPLINE ? ws_f_base_bspline(b, dtype, batch, n_in, n_out).total

@@ -114,8 +114,13 @@ int launch_g_dma(const WsG& L, hipStream_t s, const KBasis& kb, int64_t n_in, in
 }
 
 template <typename T>
+// dbias (dtype, n_out) or NULL: the column sums of g, taken from the transpose's block partials
+// (bias_part / bias_sums: (BP / 64, OUTP) and OUTP floats after G's own workspace, unless the
+// Chebyshev layout already has them), which sets *dbias_done; the sparse route leaves it to the
+// caller.
 int run_G(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
-          const void* g, const void* w, void* dc, void* ws, hipStream_t s) {
+          const void* g, const void* w, void* dc, void* ws, hipStream_t s, void* dbias = nullptr,
+          float* bias_part = nullptr, float* bias_sums = nullptr, bool* dbias_done = nullptr) {
   if constexpr (sizeof(T) == 4)
     if (bspline_sparse(b, dtype)) return launch_g_sparse<T>(kb, b->spline_k, batch, n_in, n_out, x, g, w, dc, ws, s);
   const bool cheb_kind = kb.kind == KF_KIND_CHEB;
@@ -128,12 +133,23 @@ int run_G(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
   float* wt = cheb && weighted ? (float*)(base + L.gt + L.zt) : nullptr;
   float* part = L.skip0 ? (float*)(base + L.gt + L.zt + L.wt) : nullptr;
   float* colsum = L.skip0 ? (float*)(base + L.gt + L.zt + L.wt + L.part) : nullptr;
+  // the bias gradient from the same partials: the Chebyshev sums (skip0) copy it out, other
+  // routes total the partials in a launch of their own
+  const bool own_sums = dbias && !L.skip0;
+  if (own_sums) part = bias_part;
   if (L.BP % 32 || !aligned16(gt)) return fail(KF_EINVAL, "G: workspace layout not aligned");
   dim3 tg((unsigned)((L.OUTP + 63) / 64), (unsigned)((L.BP + 63) / 64));
   hipLaunchKernelGGL(transpose_kernel<T>, tg, dim3(kThreads), 0, s, (int)batch, (int)n_out, (int)L.BP, (int)L.OUTP,
                      (int)rows_vec<T>(n_out, g), (const T*)g, (T*)gt, part);
   int rc = check_launch("transpose");
   if (rc) return rc;
+  if (own_sums) {
+    hipLaunchKernelGGL(sum_parts_kernel<T>, dim3((unsigned)((L.OUTP + 7) / 8)), dim3(kThreads), 0, s,
+                       (int)((L.BP + 63) / 64), (int)L.OUTP, (const float*)part, bias_sums, (T*)dbias, (int)n_out);
+    rc = check_launch("bias gradient");
+    if (rc) return rc;
+  }
+  if (dbias_done) *dbias_done = dbias != nullptr && (own_sums || cheb);
   if (cheb) {
     // block rows past the batch tiles total the column sums of g (skip0 implies cheb)
     const unsigned gx = (unsigned)((L.INP + 63) / 64), sblocks = L.skip0 ? (unsigned)((L.OUTP + 7) / 8) : 0u;
@@ -141,7 +157,8 @@ int run_G(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t
     hipLaunchKernelGGL(zmapT_kernel<T>, zg, dim3(kThreads), (size_t)(wt ? 2 : 1) * 64 * 65 * sizeof(float), s,
                        (int)batch, (int)n_in, (int)L.BP, (int)L.INP, kb.input_map,
                        (int)(rows_vec<T>(n_in, x) && rows_vec<T>(n_in, w)), (const T*)x, (const T*)w, zt, wt,
-                       (int)((L.BP + 63) / 64), (int)L.OUTP, part, colsum, (T*)nullptr, (T*)nullptr, 0);
+                       (int)((L.BP + 63) / 64), (int)L.OUTP, part, colsum, (T*)nullptr,
+                       (T*)(L.skip0 ? dbias : nullptr), (int)n_out);
     rc = check_launch("zmapT");
     if (rc) return rc;
     if (L.g96) {
@@ -310,6 +327,38 @@ int kf_G_base(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t
     return fail(KF_EWORKSPACE, "kf_G_base: workspace must be 256-byte aligned");
   KBasis kb = to_kbasis(b);
   return run_G_base(kb, b, dtype, batch, n_in, n_out, x, g, dc, dbase_w, dbias, workspace, (hipStream_t)stream);
+}
+
+int kf_G_bias(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* g,
+              const void* w, void* dc, void* dbias, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err.clear();
+  if (!dbias) return kf_G(b, dtype, batch, n_in, n_out, x, g, w, dc, workspace, workspace_bytes, stream);
+  int rc = validate_common(b, dtype, batch, n_in, n_out);
+  if (rc) return rc;
+  if (n_out == 0) return KF_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (batch == 0 || n_in == 0) {
+    rc = kf_G(b, dtype, batch, n_in, n_out, x, g, w, dc, workspace, workspace_bytes, stream);
+    if (rc) return rc;
+    if (batch == 0) return dtype == KF_BF16 ? zero_fill<bf16>(dbias, n_out, s) : zero_fill<float>(dbias, n_out, s);
+    return kf_column_sums(dtype, batch, n_out, g, dbias, workspace, workspace_bytes, stream);
+  }
+  if (!x || !g || !dc) return fail(KF_EINVAL, "kf_G_bias: NULL array");
+  const bool weighted = features_weighted(b, w);
+  const WsGBias L = ws_g_bias(b, dtype, batch, n_in, n_out, weighted);
+  if (!workspace || workspace_bytes < L.total)
+    return fail(KF_EWORKSPACE, "kf_G_bias: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
+  if (reinterpret_cast<uintptr_t>(workspace) & 255)
+    return fail(KF_EWORKSPACE, "kf_G_bias: workspace must be 256-byte aligned");
+  KBasis kb = to_kbasis(b);
+  char* extra = (char*)workspace + L.g;
+  float* bpart = (float*)extra;
+  float* bsums = (float*)(extra + L.part);
+  bool done = false;
+  rc = dtype == KF_BF16 ? run_G<bf16>(kb, b, dtype, batch, n_in, n_out, x, g, w, dc, workspace, s, dbias, bpart, bsums, &done)
+                        : run_G<float>(kb, b, dtype, batch, n_in, n_out, x, g, w, dc, workspace, s, dbias, bpart, bsums, &done);
+  if (rc || done) return rc;
+  return kf_column_sums(dtype, batch, n_out, g, dbias, extra + L.part + L.sums, L.cws, stream);
 }
 
 }  // extern "C"

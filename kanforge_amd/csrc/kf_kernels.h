@@ -192,6 +192,13 @@ __device__ __forceinline__ void sum_parts_block(int blk, int n_parts, int n, con
   }
 }
 
+// sum_parts_block as a launch of its own: blocks of 8 outputs.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void sum_parts_kernel(int n_parts, int n, const float* __restrict__ part,
+                                                             float* __restrict__ sums, T* __restrict__ copy, int n_real) {
+  sum_parts_block<T>(blockIdx.x, n_parts, n, part, sums, nullptr, copy, n_real);
+}
+
 // ---------------------------------------------------------------------------
 // g (B, OUT) -> gT (OUTP, BP), zero padded. 64x64 tiles through LDS with
 // 16-byte loads (when vin: OUT a multiple of the vector width, g aligned) and

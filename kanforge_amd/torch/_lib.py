@@ -21,7 +21,7 @@ KF_I8, KF_I16 = 2, 3  # lookup-table element types
 KF_KIND_CHEB, KF_KIND_BSPLINE, KF_KIND_RATIONAL = 0, 1, 2
 KF_MAP_IDENTITY, KF_MAP_TANH, KF_MAP_TANH_SQ = 0, 1, 2
 KF_OP_F, KF_OP_G, KF_OP_P = 0, 1, 2
-KF_OP_F_BASE, KF_OP_P_BASE, KF_OP_G_BASE = 3, 4, 5
+KF_OP_F_BASE, KF_OP_P_BASE, KF_OP_G_BASE, KF_OP_G_BIAS = 3, 4, 5, 6
 KF_MAX_K, KF_MAX_NT = 16, 24
 KF_EWORKSPACE = -2
 KF_NOALLOC_SCRATCH_BYTES = 64 << 20
@@ -47,6 +47,7 @@ EXPORTS = (
     "kf_base_fused",
     "kf_F_base",
     "kf_F_bias",
+    "kf_G_bias",
     "kf_P_base",
     "kf_G_base",
     "kf_last_error",
@@ -128,7 +129,8 @@ def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
         lib.kf_P_base.argtypes = [P, c_int, c_int64, c_int64, c_int64] + [c_void_p] * 6 + [c_size_t, c_void_p]
         lib.kf_G_base.argtypes = [P, c_int, c_int64, c_int64, c_int64] + [c_void_p] * 6 + [c_size_t, c_void_p]
         lib.kf_F_bias.argtypes = [P, c_int, c_int64, c_int64, c_int64] + [c_void_p] * 6 + [c_size_t, c_void_p]
-        for name in ("kf_base_fused", "kf_F_base", "kf_P_base", "kf_G_base", "kf_F_bias"):
+        lib.kf_G_bias.argtypes = [P, c_int, c_int64, c_int64, c_int64] + [c_void_p] * 6 + [c_size_t, c_void_p]
+        for name in ("kf_base_fused", "kf_F_base", "kf_P_base", "kf_G_base", "kf_F_bias", "kf_G_bias"):
             getattr(lib, name).restype = c_int
         lib.kf_last_error.argtypes = []
         lib.kf_last_error.restype = c_char_p

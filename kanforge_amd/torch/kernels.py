@@ -206,9 +206,10 @@ def _workspace(op: int, desc, dt: int, batch: int, n_in: int, n_out: int, device
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
 
-def _raw(op: str, plan: KernelPlan, m: int, x, a, b, st: BasisState | None, n_out: int, h=None, bias=None):
+def _raw(op: str, plan: KernelPlan, m: int, x, a, b, st: BasisState | None, n_out: int, h=None, bias=None,
+         bias_grad: bool = False):
     """op F: (x, w, c) -> y (B, out), plus ``bias`` (out) when given (kf_F_bias); G: (x, w, g) ->
-    dc (out, in, K); P: (x, g, c) -> p (B, in).
+    dc (out, in, K), or (dc, sum_b g) with ``bias_grad`` (kf_G_bias); P: (x, g, c) -> p (B, in).
 
     ``x`` (B, in) and every other array share the dtype of ``x``; ``w`` may be None.
     """
@@ -240,6 +241,13 @@ def _raw(op: str, plan: KernelPlan, m: int, x, a, b, st: BasisState | None, n_ou
             w = None if w is None else w.contiguous()
             g = g.contiguous()
             dc = torch.empty(n_out, n_in, plan.size, dtype=x.dtype, device=dev)
+            if bias_grad:
+                db = torch.empty(n_out, dtype=x.dtype, device=dev)
+                ws = _workspace(_lib.KF_OP_G_BIAS, desc, dt, batch, n_in, n_out, dev)
+                rc = lib.kf_G_bias(ctypes.byref(desc), dt, batch, n_in, n_out, _ptr(x), _ptr(g), _ptr(w), _ptr(dc),
+                                   _ptr(db), _ptr(ws), ws.numel(), stream)
+                _lib.check(rc, "kf_G_bias")
+                return dc, db
             ws = _workspace(_lib.KF_OP_G, desc, dt, batch, n_in, n_out, dev)
             rc = lib.kf_G(ctypes.byref(desc), dt, batch, n_in, n_out, _ptr(x), _ptr(g), _ptr(w), _ptr(dc), _ptr(ws), ws.numel(), stream)
             _lib.check(rc, "kf_G")
@@ -996,13 +1004,50 @@ def _F_bias_backward(ctx, gy):
     x, w, c, knots, knots_cmp, knots_u, num, den = ctx.saved_tensors
     n = ctx.needs_input_grad
     gy = gy.contiguous()
-    gx, gw, gc, gnum, gden = _f_grads(x, w, c, (knots, knots_cmp, knots_u, num, den), ctx.plan, ctx.m,
-                                      (n[0], n[1], n[2], n[7], n[8]), gy)
-    gb = _COLSUM(gy).to(ctx.bias_dtype) if n[3] else None
+    tabs = (knots, knots_cmp, knots_u, num, den)
+    both = n[2] and n[3]  # coefficient and bias gradients: one G launch with the column sums
+    gx, gw, gc, gnum, gden = _f_grads(x, w, c, tabs, ctx.plan, ctx.m, (n[0], n[1], n[2] and not both, n[7], n[8]), gy)
+    gb = None
+    if both:
+        gc, gb = _G_BIAS(x, gy, w, *tabs, ctx.plan, ctx.m)
+        gb = gb.to(ctx.bias_dtype)
+    elif n[3]:
+        gb = _COLSUM(gy).to(ctx.bias_dtype)
     return gx, gw, gc, gb, None, None, None, gnum, gden, None, None
 
 
 op_F_bias.register_autograd(_F_bias_backward, setup_context=_F_bias_setup)
+
+
+def _G_bias_impl(x: torch.Tensor, g: torch.Tensor, w: Opt, knots: Opt, knots_cmp: Opt, knots_u: Opt, num: Opt, den: Opt,
+                 plan: str, m: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """(dc, db): G_m(x, g, w) and the column sums of g (kf_G_bias)."""
+    return _raw("G", plan_of(plan), m, x, w, g, _state(knots, knots_cmp, knots_u, num, den, x.shape[1]), g.shape[1],
+                bias_grad=True)
+
+
+op_G_bias = torch.library.custom_op("kf::G_bias", mutates_args=())(_G_bias_impl)
+
+
+@op_G_bias.register_fake
+def _(x, g, w, knots, knots_cmp, knots_u, num, den, plan, m):
+    return x.new_empty(g.shape[1], x.shape[1], plan_of(plan).size), x.new_empty(g.shape[1])
+
+
+def _G_bias_backward(ctx, gdc, gdb):
+    """G's formula for dc; the column sums send gdb to every row of g."""
+    if gdc is None:
+        gdc = torch.zeros(ctx.saved_tensors[1].shape[1], ctx.saved_tensors[0].shape[1], plan_of(ctx.plan).size,
+                          dtype=ctx.saved_tensors[0].dtype, device=ctx.saved_tensors[0].device)
+    res = list(_G_backward(ctx, gdc))
+    if gdb is not None and ctx.needs_input_grad[1]:
+        g = ctx.saved_tensors[1]
+        extra = gdb.to(g.dtype)[None, :].expand(g.shape[0], -1)
+        res[1] = extra if res[1] is None else res[1] + extra
+    return tuple(res)
+
+
+op_G_bias.register_autograd(_G_bias_backward, setup_context=_G_setup)
 
 
 # --- the SiLU base branch and bias fused into the contractions ----------------------
@@ -1237,3 +1282,4 @@ _F_BASE = _Entry(op_F_base, _F_base_impl, _F_base_setup, _F_base_backward)
 _P_BASE = _Direct(op_P_base, _P_base_impl)
 _G_BASE = _Direct(op_G_base, _G_base_impl)
 _F_BIAS = _Entry(op_F_bias, _F_bias_impl, _F_bias_setup, _F_bias_backward)
+_G_BIAS = _Entry(op_G_bias, _G_bias_impl, _G_setup, _G_bias_backward)

@@ -98,7 +98,7 @@ int main() {
   for (const kf_basis& b : bases)
     for (const Shape& s : shapes)
       for (int dtype : {KF_F32, KF_BF16})
-        for (int op : {KF_OP_F, KF_OP_G, KF_OP_P, KF_OP_F_BASE, KF_OP_P_BASE, KF_OP_G_BASE}) {
+        for (int op : {KF_OP_F, KF_OP_G, KF_OP_P, KF_OP_F_BASE, KF_OP_P_BASE, KF_OP_G_BASE, KF_OP_G_BIAS}) {
           const size_t n = kf_workspace_bytes(op, &b, dtype, s.batch, s.n_in, s.n_out);
           check(n < (size_t(1) << 40), "workspace bytes of op " + std::to_string(op) + " kind " +
                                            std::to_string(b.kind) + " shape " + std::to_string(s.batch) + "x" +
@@ -302,6 +302,10 @@ int main() {
                  kf_F_bias(&c0, KF_BF16, 8192, 768, 3072, d, nullptr, d, d, d, d, 64, nullptr), KF_EWORKSPACE);
     check(kf_F_bias(&c0, KF_F32, 0, 4, 4, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0, nullptr) == KF_OK,
           "empty F_bias");
+    expect_error("kf_G_bias NULL dc", kf_G_bias(&c0, KF_BF16, 64, 32, 16, d, d, nullptr, nullptr, d, d, 1 << 20, nullptr),
+                 KF_EINVAL);
+    expect_error("kf_G_bias small workspace",
+                 kf_G_bias(&c0, KF_BF16, 8192, 768, 3072, d, d, nullptr, d, d, d, 256, nullptr), KF_EWORKSPACE);
   }
 
   // empty calls succeed without touching a device

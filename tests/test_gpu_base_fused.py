@@ -1,5 +1,6 @@
 """KANLinear with its SiLU base branch and bias fused into the HIP contractions (kf_F_base,
-kf_P_base, kf_G_base), and F with the bias alone (kf_F_bias), against the float64 oracle: y and every first-order gradient on layers
+kf_P_base, kf_G_base), and F and G with the bias alone (kf_F_bias, kf_G_bias), against the float64
+oracle: y and every first-order gradient on layers
 whose three entries all fuse (Chebyshev degrees 8, 7 and 5: chunks of 9 features, and even counts
 on the runtime-count F kernel) and on cubic B-spline layers, ragged shapes (inputs not a multiple of 16, outputs not of 8,
 batch not of 64), the headline shape 768 -> 3072 at batch 8192 against a plain PyTorch float32
@@ -257,4 +258,37 @@ def test_F_bias_is_F_plus_bias(name, basis, dtype, B, IN, OUT):
     else:
         err = ((fused.float() - want).abs().max() / want.abs().max()).item()
         assert err <= 1e-2, err
+
+
+G_BIAS_CASES = [
+    ("cheb8_g96", kf.Chebyshev(8), torch.bfloat16, 200, 3072, 384),  # column sums of the T_0 term
+    ("cheb8_small", kf.Chebyshev(8), torch.bfloat16, 77, 24, 19),  # precomputed features, own sums
+    ("bspline83", kf.BSpline(8, 3), torch.bfloat16, 257, 64, 130),  # GEMM core route
+    ("rational", kf.Rational(5, 4), torch.bfloat16, 300, 128, 96),  # GEMM core route
+    ("cheb8_f32", kf.Chebyshev(8), torch.float32, 333, 96, 200),
+    ("bspline53_f32", kf.BSpline(5, 3), torch.float32, 4096, 64, 64),  # sparse route: kf_column_sums
+]
+
+
+@pytest.mark.parametrize("name,basis,dtype,B,IN,OUT", G_BIAS_CASES, ids=[c[0] for c in G_BIAS_CASES])
+def test_G_bias_is_G_plus_column_sums(name, basis, dtype, B, IN, OUT):
+    """kf_G_bias: dc bitwise equal to kf_G's (the same kernels), dbias against float64 column sums
+    of g at the dtype's tolerance."""
+    torch.manual_seed(2)
+    layer = KANLinear(IN, OUT, basis, base_activation=None, groups=8 if name == "rational" else None).to(DEV, dtype)
+    x = (torch.randn(B, IN, device=DEV) * 0.8).to(dtype)
+    g = torch.randn(B, OUT, device=DEV).to(dtype)
+    st = layer._basis_state()
+    num = den = None
+    if layer._plan.kind == "rational":
+        num, den = K._rat(st, layer.basis_numerator, layer.basis_denominator)
+    key = layer._plan_key
+    with torch.no_grad():
+        dc, db = K._G_BIAS(x, g, None, *K._tables(st), num, den, key, 0)
+        dc0 = K._G(x, g, None, *K._tables(st), num, den, key, 0)
+    torch.cuda.synchronize()
+    assert torch.equal(dc, dc0)
+    want = g.double().sum(0)
+    err = ((db.double() - want).abs().max() / want.abs().max()).item()
+    assert err <= (1e-5 if dtype == torch.float32 else 1e-2), err
 

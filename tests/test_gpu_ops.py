@@ -104,10 +104,11 @@ def test_opcheck_fused_base_ops(kind):
 
 
 @pytest.mark.parametrize("name", ["cheb8", "bspline53", "rational"])
-def test_opcheck_F_bias(name):
+def test_opcheck_F_bias_and_G_bias(name):
     key, x, c, gy, w, tabs = _operands(BASES[name])
     bias = torch.randn(c.shape[0], device=DEV).requires_grad_()
     torch.library.opcheck(torch.ops.kf.F_bias.default, (x, None, c, bias, *tabs, key, 0))
+    torch.library.opcheck(torch.ops.kf.G_bias.default, (x, gy, None, *tabs, key, 0))
 
 
 def _grads(layer, x, gy):
