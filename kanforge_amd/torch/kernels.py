@@ -32,16 +32,23 @@ _DTYPES = {torch.float32: _lib.KF_F32, torch.bfloat16: _lib.KF_BF16}
 _KINDS = {"cheb": _lib.KF_KIND_CHEB, "bspline": _lib.KF_KIND_BSPLINE, "rational": _lib.KF_KIND_RATIONAL}
 
 
+_AVAILABLE: dict = {}
+
+
 def available(device: torch.device) -> bool:
-    """True on a ROCm (HIP) device with libkfhip.so loadable."""
+    """True on a ROCm (HIP) device with libkfhip.so loadable (decided once per device: neither
+    changes while the process runs)."""
     device = torch.device(device)
-    if device.type != "cuda" or torch.version.hip is None or not torch.cuda.is_available():
-        return False
-    try:
-        _lib.load()
-    except (RuntimeError, OSError):
-        return False
-    return True
+    hit = _AVAILABLE.get(device)
+    if hit is None:
+        hit = device.type == "cuda" and torch.version.hip is not None and torch.cuda.is_available()
+        if hit:
+            try:
+                _lib.load()
+            except (RuntimeError, OSError):
+                hit = False
+        _AVAILABLE[device] = hit
+    return hit
 
 
 def _require_device(t: torch.Tensor) -> None:
@@ -61,7 +68,10 @@ def _ptr(t: torch.Tensor | None):
 
 
 def _stream(device: torch.device):
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    """The device's current stream as a hipStream_t (the raw handle, without building a Stream
+    object)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    return ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(idx))
 
 
 class _NoContext:
@@ -201,9 +211,19 @@ def _make_desc(plan: KernelPlan, m: int, st: BasisState | None):
 # --- raw launches (no autograd) ----------------------------------------------------
 
 
+_WS_BYTES: dict = {}
+
+
 def _workspace(op: int, desc, dt: int, batch: int, n_in: int, n_out: int, device) -> torch.Tensor | None:
-    nbytes = _lib.load().kf_workspace_bytes(op, ctypes.byref(desc), dt, batch, n_in, n_out)
-    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+    """A workspace for one call; its size is queried once per (op, descriptor, dtype, shape) (the
+    cached entry keeps its descriptor, so a reused id never matches a stale size)."""
+    key = (op, id(desc), dt, batch, n_in, n_out)
+    hit = _WS_BYTES.get(key)
+    if hit is None or hit[0] is not desc:
+        if len(_WS_BYTES) > 4096:
+            _WS_BYTES.clear()
+        hit = _WS_BYTES[key] = (desc, int(_lib.load().kf_workspace_bytes(op, ctypes.byref(desc), dt, batch, n_in, n_out)))
+    return torch.empty(max(hit[1], 1), dtype=torch.uint8, device=device)
 
 
 def _raw(op: str, plan: KernelPlan, m: int, x, a, b, st: BasisState | None, n_out: int, h=None, bias=None,
