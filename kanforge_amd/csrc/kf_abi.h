@@ -370,11 +370,20 @@ inline WsG ws_g(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64
 // cubic with 11 basis functions: P on p8_kernel's 12 feature slots (W^T in the spare one); G on
 // the GEMM core (features and silu(x) transposed).
 inline bool f_base_route(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out) {
+  if (bspline_sparse(b, dtype)) return b->order == 0 && b->size < kSpKMax;  // base weight as basis function K
   if (dtype != KF_BF16 || b->order != 0) return false;
   const bool narrow = n_out <= 8 || (n_in <= 4 && n_in * b->size <= 64 && n_in * 16 <= 64);
   if (batch >= 1024 && narrow) return false;
   if (b->kind == KF_KIND_BSPLINE) return (n_in * b->size) % 8 == 0;
   return f_uses_rega(b, dtype) && (b->n_t == 9 || (b->n_t % 2 == 0 && b->n_t >= 6));
+}
+// The base entry points on the sparse route (float32 B-splines): F and P read c' (n_out, n_in,
+// K + 1) = the coefficients with W after each (o, i)'s K; G needs its K + 1-feature partial sums
+// and the column-sum kernels' scratch for the bias gradient.
+inline size_t ws_base_sparse(int op, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out) {
+  if (op == KF_OP_G_BASE)
+    return sparse_g_plan(batch, n_in, n_out, b->size + 1).part + align256(kf_column_sums_workspace_bytes(batch, n_out));
+  return align256((size_t)n_out * n_in * (b->size + 1) * elt_size(dtype));
 }
 // kf_F_base for B-splines: Phi with the base columns (B, ld), [c | W | 0] (OUT, ld) and the GEMM
 // core's split partial sums; ld = IN K + IN rounded up to whole 64-element stages
@@ -392,12 +401,14 @@ inline WsFB ws_f_base_bspline(const kf_basis* b, int dtype, int64_t batch, int64
   return w;
 }
 inline bool p_base_route(const kf_basis* b1, int dtype, int64_t batch, int64_t n_in, int64_t n_out) {
+  if (bspline_sparse(b1, dtype)) return b1->order >= 1 && b1->size < kSpKMax;
   if (dtype != KF_BF16 || b1->order < 1) return false;
   const WsP w = ws_p(b1, dtype, batch, n_in, n_out);
   if (b1->kind == KF_KIND_BSPLINE) return w.p12 && b1->size < 12;
   return b1->kind == KF_KIND_CHEB && w.p8;
 }
 inline bool g_base_route(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out) {
+  if (bspline_sparse(b, dtype)) return b->order == 0 && b->size < kSpKMax;
   if (dtype != KF_BF16 || b->order != 0) return false;
   const WsG w = ws_g(b, dtype, batch, n_in, n_out, false, true);
   // B-splines: features transposed input-major (the GEMM core's route of kf_G)
@@ -469,24 +480,26 @@ int with_spline_degree(int kd, Fn&& fn) {
 
 template <typename T>
 int launch_f_sparse(const KBasis& kb, int kd, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* w,
-                    const void* c, void* y, hipStream_t s) {
+                    const void* c, void* y, hipStream_t s, int kc = 0, const void* bias = nullptr) {
   const dim3 grid((unsigned)((batch + kSpRows - 1) / kSpRows), (unsigned)((n_out + 63) / 64));
+  if (kc == 0) kc = kb.K;
   return with_spline_degree(kd, [&](auto tag) {
     constexpr int KD = decltype(tag)::value;
     hipLaunchKernelGGL((f_sparse_kernel<T, KD>), grid, dim3(512), 0, s, kb, (int)batch, (int)n_in, (int)n_out,
-                       (const T*)x, (const T*)w, (const T*)c, (T*)y);
+                       (const T*)x, (const T*)w, (const T*)c, (T*)y, kc, (const T*)bias);
     return check_launch("F sparse");
   });
 }
 
 template <typename T>
 int launch_p_sparse(const KBasis& kb, int kd, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* g,
-                    const void* c, void* p, hipStream_t s) {
+                    const void* c, void* p, hipStream_t s, int kc = 0) {
   const dim3 grid((unsigned)((batch + kSpRows - 1) / kSpRows), (unsigned)((n_in + 63) / 64));
+  if (kc == 0) kc = kb.K;
   return with_spline_degree(kd, [&](auto tag) {
     constexpr int KD = decltype(tag)::value;
     hipLaunchKernelGGL((p_sparse_kernel<T, KD>), grid, dim3(512), 0, s, kb, (int)batch, (int)n_in, (int)n_out,
-                       (const T*)x, (const T*)g, (const T*)c, (T*)p);
+                       (const T*)x, (const T*)g, (const T*)c, (T*)p, kc);
     return check_launch("P sparse");
   });
 }
@@ -500,10 +513,10 @@ int launch_g_sparse(const KBasis& kb, int kd, int64_t batch, int64_t n_in, int64
     constexpr int KD = decltype(tag)::value;
     if (kb.K <= 8)
       hipLaunchKernelGGL((g_sparse_kernel<T, KD, 8>), grid, dim3(256), 0, s, kb, (int)batch, (int)n_in, (int)n_out,
-                         sp.RS, (const T*)x, (const T*)g, (const T*)w, (float*)ws);
+                         sp.RS, (const T*)x, (const T*)g, (const T*)w, (float*)ws, kb.K);
     else
       hipLaunchKernelGGL((g_sparse_kernel<T, KD, kSpKMax>), grid, dim3(256), 0, s, kb, (int)batch, (int)n_in,
-                         (int)n_out, sp.RS, (const T*)x, (const T*)g, (const T*)w, (float*)ws);
+                         (int)n_out, sp.RS, (const T*)x, (const T*)g, (const T*)w, (float*)ws, kb.K);
     return check_launch("G sparse");
   });
   if (rc) return rc;
@@ -512,6 +525,44 @@ int launch_g_sparse(const KBasis& kb, int kd, int64_t batch, int64_t n_in, int64
   if (blocks > 4096) blocks = 4096;
   hipLaunchKernelGGL(g_sparse_reduce<T>, dim3((unsigned)blocks), dim3(256), 0, s, sp.nz, n, (const float*)ws, (T*)dc);
   return check_launch("G sparse reduce");
+}
+
+// The sparse G with the base branch's feature silu(x) as basis function K: partials of K + 1 sums
+// per (o, i) (plan sparse_g_plan(..., K + 1)), split into dc and dw by the reduction.
+template <typename T>
+int launch_g_sparse_base(const KBasis& kb, int kd, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
+                         const void* g, void* dc, void* dw, void* ws, hipStream_t s) {
+  const SpG sp = sparse_g_plan(batch, n_in, n_out, kb.K + 1);
+  const dim3 grid((unsigned)((n_in + 3) / 4), (unsigned)((n_out + 63) / 64), (unsigned)sp.nz);
+  if (kb.K + 1 > kSpKMax) return fail(KF_EINVAL, "G sparse: base feature needs K < %d", kSpKMax);
+  int rc = with_spline_degree(kd, [&](auto tag) {
+    constexpr int KD = decltype(tag)::value;
+    if (kb.K + 1 <= 8)
+      hipLaunchKernelGGL((g_sparse_kernel<T, KD, 8>), grid, dim3(256), 0, s, kb, (int)batch, (int)n_in, (int)n_out,
+                         sp.RS, (const T*)x, (const T*)g, (const T*)nullptr, (float*)ws, kb.K + 1);
+    else
+      hipLaunchKernelGGL((g_sparse_kernel<T, KD, kSpKMax>), grid, dim3(256), 0, s, kb, (int)batch, (int)n_in,
+                         (int)n_out, sp.RS, (const T*)x, (const T*)g, (const T*)nullptr, (float*)ws, kb.K + 1);
+    return check_launch("G sparse");
+  });
+  if (rc) return rc;
+  const long n = (long)n_out * n_in * (kb.K + 1);
+  long blocks = (n + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(g_sparse_reduce_base<T>, dim3((unsigned)blocks), dim3(256), 0, s, sp.nz, (long)n_out * n_in, kb.K,
+                     (const float*)ws, (T*)dc, (T*)dw);
+  return check_launch("G sparse reduce");
+}
+
+// c' (n_out, n_in, K + 1) = the coefficients with W[o, i] after each (o, i)'s K (sparse base branch)
+template <typename T>
+int launch_coef_with_base(int64_t n_out, int64_t n_in, int K, const void* c, const void* w, void* out, hipStream_t s) {
+  const long n = (long)n_out * n_in * (K + 1);
+  long blocks = (n + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(coef_with_base_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, s, (int)n_out, (int)n_in, K,
+                     (const T*)c, (const T*)w, (T*)out);
+  return check_launch("coefficients with base");
 }
 
 template <typename T>

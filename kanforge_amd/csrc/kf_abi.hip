@@ -99,10 +99,17 @@ size_t kf_workspace_bytes(int op, const kf_basis* b, int dtype, int64_t batch, i
     }
     case KF_OP_F_BASE:
       if (!f_base_route(b, dtype, batch, n_in, n_out)) return 0;
+      if (bspline_sparse(b, dtype)) return ws_base_sparse(op, b, dtype, batch, n_in, n_out);
       return b->kind == KF_KIND_BSPLINE ? ws_f_base_bspline(b, dtype, batch, n_in, n_out).total
                                         : ws_f(b, dtype, batch, n_in, n_out, false, true).total;
-    case KF_OP_P_BASE: return p_base_route(b, dtype, batch, n_in, n_out) ? ws_p_base(b, dtype, batch, n_in, n_out).total : 0;
-    case KF_OP_G_BASE: return g_base_route(b, dtype, batch, n_in, n_out) ? ws_g_base(b, dtype, batch, n_in, n_out).total : 0;
+    case KF_OP_P_BASE:
+      if (!p_base_route(b, dtype, batch, n_in, n_out)) return 0;
+      return bspline_sparse(b, dtype) ? ws_base_sparse(op, b, dtype, batch, n_in, n_out)
+                                      : ws_p_base(b, dtype, batch, n_in, n_out).total;
+    case KF_OP_G_BASE:
+      if (!g_base_route(b, dtype, batch, n_in, n_out)) return 0;
+      return bspline_sparse(b, dtype) ? ws_base_sparse(op, b, dtype, batch, n_in, n_out)
+                                      : ws_g_base(b, dtype, batch, n_in, n_out).total;
     default: return 0;
   }
 }

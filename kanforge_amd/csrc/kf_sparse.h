@@ -56,16 +56,20 @@ __device__ __forceinline__ int bspline_window(float x, float w, int i, const KBa
 // The windows of the rows' next 64 inputs are computed once into LDS; the coefficients of kSpIC
 // inputs x K x 64 outputs are staged in LDS per chunk, the next chunk's loads in flight (registers)
 // while the current one is contracted.
+// Base branch (KC = K + 1): c holds K + 1 values per (o, i), the last the base weight W[o, i],
+// whose feature silu(x) is staged next to the windows; y starts from bias[o] when given.
 template <typename T, int KD>
 __global__ __launch_bounds__(512) void f_sparse_kernel(KBasis bs, int B, int IN, int OUT, const T* __restrict__ x,
                                                        const T* __restrict__ w, const T* __restrict__ c,
-                                                       T* __restrict__ y) {
+                                                       T* __restrict__ y, int KC, const T* __restrict__ bias) {
   constexpr int NW = 8, RQ = kSpRows / NW, WCH = 64;
-  constexpr int PF = kSpIC * kSpKMax * 64 / 512;  // staged values per thread, at most
-  __shared__ float cs[kSpIC * kSpKMax][kSpLane];
+  constexpr int PF = (kSpIC * (kSpKMax + 1) * 64 + 511) / 512;  // staged values per thread, at most
+  __shared__ float cs[kSpIC * (kSpKMax + 1)][kSpLane];
   __shared__ int ss[kSpRows][WCH];
   __shared__ float vs[kSpRows][WCH][KD + 1];
+  __shared__ float svs[kSpRows][WCH];  // silu(x) of the base branch (KC > K)
   const int K = bs.K;
+  const bool base = KC > K;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int b0 = blockIdx.x * kSpRows, o0 = blockIdx.y * 64, o = o0 + lane;
   const int no = OUT - o0 < 64 ? OUT - o0 : 64;
@@ -77,8 +81,8 @@ __global__ __launch_bounds__(512) void f_sparse_kernel(KBasis bs, int B, int IN,
   // of its contiguous run of ni K coefficients
   const int sol = threadIdx.x >> 3, sr = threadIdx.x & 7;
   auto fetch = [&](int i0) {
-    const int per_o = (IN - i0 < kSpIC ? IN - i0 : kSpIC) * K;
-    const T* src = c + ((size_t)(o0 + sol) * IN + i0) * K;
+    const int per_o = (IN - i0 < kSpIC ? IN - i0 : kSpIC) * KC;
+    const T* src = c + ((size_t)(o0 + sol) * IN + i0) * KC;
 #pragma unroll
     for (int u = 0; u < PF; ++u) {
       const int r = sr + 8 * u;
@@ -94,17 +98,21 @@ __global__ __launch_bounds__(512) void f_sparse_kernel(KBasis bs, int B, int IN,
       float V[KD + 1];
 #pragma unroll
       for (int r = 0; r <= KD; ++r) V[r] = 0.f;
+      float sv = 0.f;
       if (b < B && il < nw) {
         const size_t off = (size_t)b * IN + i;
-        bspline_window<KD>(to_f32(x[off]), w ? to_f32(w[off]) : 1.f, i, bs, s0, V);
+        const float xv = to_f32(x[off]);
+        bspline_window<KD>(xv, w ? to_f32(w[off]) : 1.f, i, bs, s0, V);
+        sv = silu_f(xv);
       }
       ss[rr][il] = s0;
+      if (base) svs[rr][il] = sv;
 #pragma unroll
       for (int r = 0; r <= KD; ++r) vs[rr][il][r] = V[r];
     }
     fetch(w0);
     for (int i0 = w0; i0 < w0 + nw; i0 += kSpIC) {
-      const int ni = IN - i0 < kSpIC ? IN - i0 : kSpIC, per_o = ni * K;
+      const int ni = IN - i0 < kSpIC ? IN - i0 : kSpIC, per_o = ni * KC;
       __syncthreads();
 #pragma unroll
       for (int u = 0; u < PF; ++u) {
@@ -120,18 +128,20 @@ __global__ __launch_bounds__(512) void f_sparse_kernel(KBasis bs, int B, int IN,
 #pragma unroll
         for (int q = 0; q < RQ; ++q) {
           const int rr = wave + NW * q;
-          const int row = il * K + ss[rr][ib + il];
+          const int row = il * KC + ss[rr][ib + il];
 #pragma unroll
           for (int r = 0; r <= KD; ++r) acc[q] = fmaf(vs[rr][ib + il][r], cs[row + r][lane], acc[q]);
+          if (base) acc[q] = fmaf(svs[rr][ib + il], cs[il * KC + K][lane], acc[q]);
         }
       }
     }
   }
   if (lane < no) {
+    const float bo = bias ? to_f32(bias[o]) : 0.f;
 #pragma unroll
     for (int q = 0; q < RQ; ++q) {
       const int b = b0 + wave + NW * q;
-      if (b < B) y[(size_t)b * OUT + o] = from_f32<T>(acc[q]);
+      if (b < B) y[(size_t)b * OUT + o] = from_f32<T>(acc[q] + bo);
     }
   }
 }
@@ -140,16 +150,19 @@ __global__ __launch_bounds__(512) void f_sparse_kernel(KBasis bs, int B, int IN,
 // lane keeps its rows' windows in registers; the coefficients of kSpOC outputs x K x 64 inputs and
 // the rows' g values are staged in LDS per chunk (next chunk prefetched into registers);
 // h_r = sum_o g c[o, i, s0 + r], then p = sum_r V_r h_r.
+// Base branch (KC = K + 1): the last of each (o, i)'s K + 1 coefficients is W[o, i]; hb = sum_o g W
+// accumulates next to h and p gets silu'(x) hb.
 template <typename T, int KD>
 __global__ __launch_bounds__(512, 4) void p_sparse_kernel(KBasis bs, int B, int IN, int OUT, const T* __restrict__ x,
                                                        const T* __restrict__ g, const T* __restrict__ c,
-                                                       T* __restrict__ p) {
+                                                       T* __restrict__ p, int KC) {
   constexpr int NW = 8, RQ = kSpRows / NW;
-  constexpr int PF = kSpKMax;  // one (output, input)'s K coefficients per thread (kSpOC = NW)
+  constexpr int PF = kSpKMax + 1;  // one (output, input)'s KC coefficients per thread (kSpOC = NW)
   static_assert(kSpOC == NW, "P stages one output per wave");
-  __shared__ float cs[kSpOC * kSpKMax][kSpLane];
+  __shared__ float cs[kSpOC * (kSpKMax + 1)][kSpLane];
   __shared__ float gs[kSpRows][kSpOC];
   const int K = bs.K;
+  const bool base = KC > K;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int b0 = blockIdx.x * kSpRows, i0 = blockIdx.y * 64, i = i0 + lane;
   const int ni = IN - i0 < 64 ? IN - i0 : 64;
@@ -158,23 +171,27 @@ __global__ __launch_bounds__(512, 4) void p_sparse_kernel(KBasis bs, int B, int 
   // (oc0 + ol, i0 + il)
   auto fetch = [&](int oc0) {
     const int no = OUT - oc0 < kSpOC ? OUT - oc0 : kSpOC;
-    const T* src = c + ((size_t)(oc0 + wave) * IN + i0 + lane) * K;
+    const T* src = c + ((size_t)(oc0 + wave) * IN + i0 + lane) * KC;
 #pragma unroll
-    for (int u = 0; u < PF; ++u) pre[u] = (wave < no && lane < ni && u < K) ? to_f32(src[u]) : 0.f;
+    for (int u = 0; u < PF; ++u) pre[u] = (wave < no && lane < ni && u < KC) ? to_f32(src[u]) : 0.f;
     if (threadIdx.x < kSpRows * kSpOC) {
       const int rr = threadIdx.x / kSpOC, ol = threadIdx.x % kSpOC, b = b0 + rr;
       gpre = (b < B && ol < no) ? to_f32(g[(size_t)b * OUT + oc0 + ol]) : 0.f;
     }
   };
   int s0[RQ];
-  float V[RQ][KD + 1], h[RQ][KD + 1];
+  float V[RQ][KD + 1], h[RQ][KD + 1], hb[RQ], xq[RQ];
 #pragma unroll
   for (int q = 0; q < RQ; ++q) {
     const int b = b0 + wave + NW * q;
     s0[q] = 0;
+    hb[q] = xq[q] = 0.f;
 #pragma unroll
     for (int r = 0; r <= KD; ++r) V[q][r] = h[q][r] = 0.f;
-    if (b < B && lane < ni) bspline_window<KD>(to_f32(x[(size_t)b * IN + i]), 1.f, i, bs, s0[q], V[q]);
+    if (b < B && lane < ni) {
+      xq[q] = to_f32(x[(size_t)b * IN + i]);
+      bspline_window<KD>(xq[q], 1.f, i, bs, s0[q], V[q]);
+    }
   }
   fetch(0);
   for (int oc0 = 0; oc0 < OUT; oc0 += kSpOC) {
@@ -182,7 +199,7 @@ __global__ __launch_bounds__(512, 4) void p_sparse_kernel(KBasis bs, int B, int 
     __syncthreads();
 #pragma unroll
     for (int u = 0; u < PF; ++u)
-      if (wave < no && u < K) cs[wave * K + u][lane] = pre[u];
+      if (wave < no && u < KC) cs[wave * KC + u][lane] = pre[u];
     if (threadIdx.x < kSpRows * kSpOC) gs[threadIdx.x / kSpOC][threadIdx.x % kSpOC] = gpre;
     __syncthreads();
     if (oc0 + kSpOC < OUT) fetch(oc0 + kSpOC);
@@ -193,9 +210,10 @@ __global__ __launch_bounds__(512, 4) void p_sparse_kernel(KBasis bs, int B, int 
 #pragma unroll
         for (int q = 0; q < RQ; ++q) {
           const float gv = gs[wave + NW * q][ol];
-          const int row = ol * K + s0[q];
+          const int row = ol * KC + s0[q];
 #pragma unroll
           for (int r = 0; r <= KD; ++r) h[q][r] = fmaf(gv, cs[row + r][lane], h[q][r]);
+          if (base) hb[q] = fmaf(gv, cs[ol * KC + K][lane], hb[q]);
         }
       }
     }
@@ -207,6 +225,7 @@ __global__ __launch_bounds__(512, 4) void p_sparse_kernel(KBasis bs, int B, int 
       float acc = 0.f;
 #pragma unroll
       for (int r = 0; r <= KD; ++r) acc = fmaf(V[q][r], h[q][r], acc);
+      if (base) acc = fmaf(dsilu_f(xq[q]), hb[q], acc);
       if (b < B) p[(size_t)b * IN + i] = from_f32<T>(acc);
     }
   }
@@ -217,10 +236,12 @@ __global__ __launch_bounds__(512, 4) void p_sparse_kernel(KBasis bs, int B, int 
 // lane turns its row's window into the row's KM features (zeros outside the window, all NaN for a
 // non-finite x) in the wave's LDS slot; every row then costs KM broadcast reads and KM FMAs per
 // lane, with the loads of sixteen rows' g in flight at once.
+// Base branch (KO = K + 1 <= KM): feature K is silu(x), so part holds K + 1 sums per (o, i), the
+// last the base weight's gradient.
 template <typename T, int KD, int KM>
 __global__ __launch_bounds__(256) void g_sparse_kernel(KBasis bs, int B, int IN, int OUT, int RS,
                                                        const T* __restrict__ x, const T* __restrict__ g,
-                                                       const T* __restrict__ w, float* __restrict__ part) {
+                                                       const T* __restrict__ w, float* __restrict__ part, int KO) {
   __shared__ float phi[4][64][KM];
   const int K = bs.K;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -239,16 +260,20 @@ __global__ __launch_bounds__(256) void g_sparse_kernel(KBasis bs, int B, int IN,
 #pragma unroll
       for (int r = 0; r <= KD; ++r) V[r] = 0.f;
       bool nan = false;
+      float sv = 0.f;
       if (lane < nb && i < IN) {
         const size_t off = (size_t)(bb + lane) * IN + i;
-        nan = bspline_window<KD>(to_f32(x[off]), w ? to_f32(w[off]) : 1.f, i, bs, s0, V) == 2;
+        const float xv = to_f32(x[off]);
+        nan = bspline_window<KD>(xv, w ? to_f32(w[off]) : 1.f, i, bs, s0, V) == 2;
+        sv = silu_f(xv);
       }
 #pragma unroll
       for (int k = 0; k < KM; ++k) {
         float v = 0.f;
 #pragma unroll
         for (int r = 0; r <= KD; ++r) v = (k == s0 + r) ? V[r] : v;
-        phi[wave][lane][k] = nan ? V[0] : v;
+        v = nan ? V[0] : v;
+        phi[wave][lane][k] = k < K ? v : (k == K && KO > K ? sv : 0.f);
       }
     }
     __syncthreads();
@@ -267,10 +292,41 @@ __global__ __launch_bounds__(256) void g_sparse_kernel(KBasis bs, int B, int IN,
     }
   }
   if (live) {
-    float* dst = part + (((size_t)z * OUT + o) * IN + i) * K;
+    float* dst = part + (((size_t)z * OUT + o) * IN + i) * KO;
 #pragma unroll
     for (int k = 0; k < KM; ++k)
-      if (k < K) dst[k] = acc[k];
+      if (k < KO) dst[k] = acc[k];
+  }
+}
+
+// The base branch's G partials (K + 1 sums per (o, i), the last dW): dc[o][i][k] and dw[o][i] =
+// sum_z part[z][o][i][.] (slice order: deterministic); dc or dw may be NULL.
+template <typename T>
+__global__ __launch_bounds__(256) void g_sparse_reduce_base(int nz, long n_oi, int K, const float* __restrict__ part,
+                                                            T* __restrict__ dc, T* __restrict__ dw) {
+  const long n = n_oi * (K + 1);
+  for (long e = blockIdx.x * 256L + threadIdx.x; e < n; e += (long)gridDim.x * 256) {
+    float s = 0.f;
+    for (int q = 0; q < nz; ++q) s += part[(size_t)q * n + e];
+    const long oi = e / (K + 1);
+    const int k = (int)(e - oi * (K + 1));
+    if (k < K) {
+      if (dc) dc[oi * K + k] = from_f32<T>(s);
+    } else if (dw) {
+      dw[oi] = from_f32<T>(s);
+    }
+  }
+}
+
+// c' (OUT, IN, K + 1): each (o, i)'s K coefficients, then W[o, i] (the sparse kernels' base branch)
+template <typename T>
+__global__ __launch_bounds__(256) void coef_with_base_kernel(int OUT, int IN, int K, const T* __restrict__ c,
+                                                             const T* __restrict__ w, T* __restrict__ out) {
+  const long n = (long)OUT * IN * (K + 1);
+  for (long e = blockIdx.x * 256L + threadIdx.x; e < n; e += (long)gridDim.x * 256) {
+    const long oi = e / (K + 1);
+    const int k = (int)(e - oi * (K + 1));
+    out[e] = k < K ? c[oi * K + k] : w[oi];
   }
 }
 

@@ -1078,7 +1078,8 @@ op_G_bias.register_autograd(_G_bias_backward, setup_context=_G_setup)
 # silu'(x) (g W) in P's epilogue and kf_G_base returns the base weights' and the bias's gradients
 # next to the coefficient gradient. bf16 B-splines run silu(x) and the bias as extra feature
 # columns of F's GEMM, G as for Chebyshev, and (cubic, 11 basis functions) P with W^T in a spare
-# feature slot of its tile.
+# feature slot of its tile; float32 B-splines (the sparse route) take W as one more basis function
+# whose feature is silu(x) in F, P and G.
 
 _FUSED: dict = {}
 
@@ -1092,11 +1093,12 @@ def base_fused(plan: KernelPlan | str, st: BasisState | None, dtype: torch.dtype
     if hit is None:
         pl = plan_of(key[0])
         hit = (False, False, False)
-        if pl.kind in ("cheb", "bspline") and dtype == torch.bfloat16 and batch > 0:
+        if pl.kind in ("cheb", "bspline") and dtype in _DTYPES and batch > 0:
             lib = _lib.load()
             d0, _ = _desc(pl, 0, st)
             d1, _ = _desc(pl, 1, st)
-            q = lambda op, d: lib.kf_base_fused(op, ctypes.byref(d), _lib.KF_BF16, batch, n_in, n_out) == 1
+            dt = _DTYPES[dtype]
+            q = lambda op, d: lib.kf_base_fused(op, ctypes.byref(d), dt, batch, n_in, n_out) == 1
             hit = (q(_lib.KF_OP_F_BASE, d0), q(_lib.KF_OP_P_BASE, d1), q(_lib.KF_OP_G_BASE, d0))
         if len(_FUSED) > 4096:
             _FUSED.clear()

@@ -245,12 +245,12 @@ class KANLinear(nn.Module):
 
     def _base_fused(self, x: torch.Tensor) -> bool:
         """Whether forward runs the spline part, the SiLU base branch and the bias as one op whose
-        kernels fuse the base branch (bf16 Chebyshev and cubic B-spline plans on their contraction
-        kernels, eager)."""
+        kernels fuse the base branch (bf16 Chebyshev and B-spline plans on their contraction
+        kernels, float32 B-splines on the sparse route; eager)."""
         if self.base_weight is None or self.base_activation is not F.silu or self._plan.kind not in ("cheb", "bspline"):
             return False
-        dt = torch.bfloat16
-        if x.dtype != dt or self.coef.dtype != dt or self.base_weight.dtype != dt:
+        dt = x.dtype
+        if self.coef.dtype != dt or self.base_weight.dtype != dt:
             return False
         if (self.bias is not None and self.bias.dtype != dt) or _compiling() or x.dim() < 1:
             return False

@@ -126,8 +126,9 @@ int main() {
           const int r = kf_base_fused(op, &b, dtype, s.batch, s.n_in, s.n_out);
           const size_t n = kf_workspace_bytes(op, &b, dtype, s.batch, s.n_in, s.n_out);
           check(r == 0 || (r == 1 && n > 0), "base route " + std::to_string(op) + " reports a workspace");
-          check(r == 0 || (dtype == KF_BF16 && (b.kind == KF_KIND_CHEB || b.kind == KF_KIND_BSPLINE)),
-                "base route only for bf16 Chebyshev and B-spline layers");
+          check(r == 0 || (dtype == KF_BF16 && (b.kind == KF_KIND_CHEB || b.kind == KF_KIND_BSPLINE)) ||
+                    (dtype == KF_F32 && b.kind == KF_KIND_BSPLINE),
+                "base route only for bf16 Chebyshev and B-spline layers and float32 B-splines");
         }
   {
     const kf_basis c0 = cheb(9, 0, 9, KF_MAP_TANH), c1 = cheb(9, 1, 8, KF_MAP_TANH_SQ);
@@ -144,6 +145,15 @@ int main() {
     check(kf_base_fused(KF_OP_F_BASE, &s0, KF_BF16, 16384, 768, 3072) == 1, "B-spline F fused");
     check(kf_base_fused(KF_OP_F_BASE, &s0, KF_BF16, 4096, 64, 4) == 0, "narrow B-spline layer not fused");
     check(kf_base_fused(KF_OP_P_BASE, &s5, KF_BF16, 16384, 768, 3072) == 0, "B-spline(5, 3) P: no spare slot tile");
+    // float32 B-splines: the sparse kernels take W as basis function K
+    const kf_basis f0 = bspline(5, 3, 0, false), f1 = bspline(5, 3, 1, false);
+    for (int op : {KF_OP_F_BASE, KF_OP_G_BASE})
+      check(kf_base_fused(op, &f0, KF_F32, 4096, 64, 64) == 1, "64 -> 64 float32 B-spline fused " + std::to_string(op));
+    check(kf_base_fused(KF_OP_P_BASE, &f1, KF_F32, 4096, 64, 64) == 1, "64 -> 64 float32 B-spline P fused");
+    check(kf_base_fused(KF_OP_F_BASE, &c0, KF_F32, 4096, 64, 64) == 0, "float32 Chebyshev not fused");
+    check(kf_workspace_bytes(KF_OP_G_BASE, &f0, KF_F32, 4096, 64, 64) >
+              kf_workspace_bytes(KF_OP_G, &f0, KF_F32, 4096, 64, 64),
+          "sparse G_base partials hold K + 1 features");
   }
 
   // descriptor validation (through kf_F: every entry point validates the same way first)

@@ -292,3 +292,40 @@ def test_G_bias_is_G_plus_column_sums(name, basis, dtype, B, IN, OUT):
     err = ((db.double() - want).abs().max() / want.abs().max()).item()
     assert err <= (1e-5 if dtype == torch.float32 else 1e-2), err
 
+
+@pytest.mark.parametrize("B,IN,OUT,grid,k", [(4096, 64, 64, 5, 3), (333, 70, 45, 8, 3), (200, 40, 33, 5, 1)])
+def test_fused_sparse_float32_layer_against_oracle(B, IN, OUT, grid, k):
+    """float32 B-splines on the sparse route: W as basis function K (feature silu(x)) in F, P and
+    G, the bias in F's stores; the first shape is the 64 -> 64 benchmark layer, the others ragged
+    and of degree 1. Tolerance: float32 normwise 1e-5."""
+    torch.manual_seed(4)
+    layer = KANLinear(IN, OUT, kf.BSpline(grid, k, grid_range=(-2.0, 2.0)))
+    with torch.no_grad():
+        layer.coef.normal_(0, 0.5 / math.sqrt(IN))
+        layer.bias.normal_()
+    layer = layer.to(DEV)
+    fused = K.base_fused(layer._plan_key, layer._basis_state(), torch.float32, B, IN, OUT)
+    print(f"sparse case B={B} in={IN} out={OUT} grid={grid} k={k} fused={fused}", flush=True)
+    assert fused == (True, True, True)
+    ob = oracle_basis(layer.basis, IN, {"grid": np64(layer.basis_grid)})
+    rng = np.random.default_rng(B)
+    x0 = rng.uniform(-2.2, 2.2, (B, IN))
+    gy0 = rng.normal(0, 1, (B, OUT))
+    x = torch.as_tensor(x0, dtype=torch.float32, device=DEV).requires_grad_()
+    gy = torch.as_tensor(gy0, dtype=torch.float32, device=DEV)
+    y = layer(x)
+    y.backward(gy)
+    torch.cuda.synchronize()
+    c, W, b = np64(layer.coef), np64(layer.base_weight), np64(layer.bias)
+    checks = {
+        "y": (y, o.kan_linear(x0, c, ob, W, b)),
+        "x": (x.grad, o.prim_P(x0, gy0, c, ob, 1) + (gy0 @ W) * o.silu_derivative(x0, 1)),
+        "coef": (layer.coef.grad, o.prim_G(x0, gy0, None, ob, 0)),
+        "base_weight": (layer.base_weight.grad, gy0.T @ o.silu_derivative(x0, 0)),
+        "bias": (layer.bias.grad, gy0.sum(0)),
+    }
+    for key, (got, want) in checks.items():
+        err = o.normwise_err(np64(got), want)
+        print(f"  {key}: {err:.3e}", flush=True)
+        assert err <= 1e-5, (key, err)
+

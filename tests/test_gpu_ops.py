@@ -139,11 +139,11 @@ def test_compiled_layer_forward_backward_matches_eager(make, dtype):
     got = [y] + list(torch.autograd.grad(y, [x] + list(layer.parameters()), gy))
     assert len(got) == len(want)
     for a, b in zip(got, want):
-        if getattr(layer, "base_weight", None) is not None and dtype == torch.bfloat16:
+        if getattr(layer, "base_weight", None) is not None:
             # compiled graphs take the composed base branch (kf::F, hipBLASLt, torch ops), eager
-            # the fused entries: two bf16 roundings of the same sums
+            # the fused entries: the same sums in another order (and, in bf16, rounded twice)
             err = ((a.float() - b.float()).abs().max() / b.float().abs().max()).item()
-            assert err <= 2e-2, err
+            assert err <= (2e-2 if dtype == torch.bfloat16 else 1e-5), err
         else:
             torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-6)
 
