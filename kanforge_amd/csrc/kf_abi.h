@@ -3,6 +3,7 @@
 // points use.
 #pragma once
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -377,13 +378,16 @@ inline bool f_base_route(const kf_basis* b, int dtype, int64_t batch, int64_t n_
   if (b->kind == KF_KIND_BSPLINE) return (n_in * b->size) % 8 == 0;
   return f_uses_rega(b, dtype) && (b->n_t == 9 || (b->n_t % 2 == 0 && b->n_t >= 6));
 }
-// The base entry points on the sparse route (float32 B-splines): F and P read c' (n_out, n_in,
-// K + 1) = the coefficients with W after each (o, i)'s K; G needs its K + 1-feature partial sums
-// and the column-sum kernels' scratch for the bias gradient.
+// The base entry points on the sparse route (float32 B-splines): F and P stage W next to the
+// coefficients themselves (no workspace); G needs its K + 1-feature partial sums and, after them,
+// the bias gradient's slice partials (or, for the bias gradient alone, the column-sum kernels'
+// scratch).
 inline size_t ws_base_sparse(int op, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out) {
-  if (op == KF_OP_G_BASE)
-    return sparse_g_plan(batch, n_in, n_out, b->size + 1).part + align256(kf_column_sums_workspace_bytes(batch, n_out));
-  return align256((size_t)n_out * n_in * (b->size + 1) * elt_size(dtype));
+  (void)dtype;
+  if (op != KF_OP_G_BASE) return 0;
+  const SpG sp = sparse_g_plan(batch, n_in, n_out, b->size + 1);
+  const size_t bias = std::max((size_t)sp.nz * n_out * sizeof(float), kf_column_sums_workspace_bytes(batch, n_out));
+  return sp.part + align256(bias);
 }
 // kf_F_base for B-splines: Phi with the base columns (B, ld), [c | W | 0] (OUT, ld) and the GEMM
 // core's split partial sums; ld = IN K + IN rounded up to whole 64-element stages
@@ -480,27 +484,49 @@ int with_spline_degree(int kd, Fn&& fn) {
 
 template <typename T>
 int launch_f_sparse(const KBasis& kb, int kd, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* w,
-                    const void* c, void* y, hipStream_t s, int kc = 0, const void* bias = nullptr) {
+                    const void* c, void* y, hipStream_t s, const void* bw = nullptr, const void* bias = nullptr) {
   const dim3 grid((unsigned)((batch + kSpRows - 1) / kSpRows), (unsigned)((n_out + 63) / 64));
-  if (kc == 0) kc = kb.K;
+  if (bw && kb.K + 1 > kSpKMax) return fail(KF_EINVAL, "F sparse: base weight needs K < %d", kSpKMax);
   return with_spline_degree(kd, [&](auto tag) {
     constexpr int KD = decltype(tag)::value;
     hipLaunchKernelGGL((f_sparse_kernel<T, KD>), grid, dim3(512), 0, s, kb, (int)batch, (int)n_in, (int)n_out,
-                       (const T*)x, (const T*)w, (const T*)c, (T*)y, kc, (const T*)bias);
+                       (const T*)x, (const T*)w, (const T*)c, (T*)y, (const T*)bw, (const T*)bias);
     return check_launch("F sparse");
   });
 }
 
 template <typename T>
 int launch_p_sparse(const KBasis& kb, int kd, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* g,
-                    const void* c, void* p, hipStream_t s, int kc = 0) {
+                    const void* c, void* p, hipStream_t s, const void* bw = nullptr) {
   const dim3 grid((unsigned)((batch + kSpRows - 1) / kSpRows), (unsigned)((n_in + 63) / 64));
-  if (kc == 0) kc = kb.K;
+  if (bw && kb.K + 1 > kSpKMax) return fail(KF_EINVAL, "P sparse: base weight needs K < %d", kSpKMax);
   return with_spline_degree(kd, [&](auto tag) {
     constexpr int KD = decltype(tag)::value;
     hipLaunchKernelGGL((p_sparse_kernel<T, KD>), grid, dim3(512), 0, s, kb, (int)batch, (int)n_in, (int)n_out,
-                       (const T*)x, (const T*)g, (const T*)c, (T*)p, kc);
+                       (const T*)x, (const T*)g, (const T*)c, (T*)p, (const T*)bw);
     return check_launch("P sparse");
+  });
+}
+
+// g_sparse_kernel with the smallest feature tile KM in {8, 12, 16} that holds ko features
+template <typename T>
+int launch_g_sparse_kernel(const KBasis& kb, int kd, dim3 grid, int64_t batch, int64_t n_in, int64_t n_out, int rs,
+                           const void* x, const void* g, const void* w, float* part, int ko, float* bpart,
+                           hipStream_t s) {
+  return with_spline_degree(kd, [&](auto tag) {
+    constexpr int KD = decltype(tag)::value;
+    auto go = [&](auto km) {
+      constexpr int KM = decltype(km)::value;
+      hipLaunchKernelGGL((g_sparse_kernel<T, KD, KM>), grid, dim3(256), 0, s, kb, (int)batch, (int)n_in, (int)n_out,
+                         rs, (const T*)x, (const T*)g, (const T*)w, part, ko, bpart);
+    };
+    if (ko <= 8)
+      go(std::integral_constant<int, 8>{});
+    else if (ko <= 12)
+      go(std::integral_constant<int, 12>{});
+    else
+      go(std::integral_constant<int, kSpKMax>{});
+    return check_launch("G sparse");
   });
 }
 
@@ -509,16 +535,7 @@ int launch_g_sparse(const KBasis& kb, int kd, int64_t batch, int64_t n_in, int64
                     const void* w, void* dc, void* ws, hipStream_t s) {
   const SpG sp = sparse_g_plan(batch, n_in, n_out, kb.K);
   const dim3 grid((unsigned)((n_in + 3) / 4), (unsigned)((n_out + 63) / 64), (unsigned)sp.nz);
-  int rc = with_spline_degree(kd, [&](auto tag) {
-    constexpr int KD = decltype(tag)::value;
-    if (kb.K <= 8)
-      hipLaunchKernelGGL((g_sparse_kernel<T, KD, 8>), grid, dim3(256), 0, s, kb, (int)batch, (int)n_in, (int)n_out,
-                         sp.RS, (const T*)x, (const T*)g, (const T*)w, (float*)ws, kb.K);
-    else
-      hipLaunchKernelGGL((g_sparse_kernel<T, KD, kSpKMax>), grid, dim3(256), 0, s, kb, (int)batch, (int)n_in,
-                         (int)n_out, sp.RS, (const T*)x, (const T*)g, (const T*)w, (float*)ws, kb.K);
-    return check_launch("G sparse");
-  });
+  int rc = launch_g_sparse_kernel<T>(kb, kd, grid, batch, n_in, n_out, sp.RS, x, g, w, (float*)ws, kb.K, nullptr, s);
   if (rc) return rc;
   const long n = (long)n_out * n_in * kb.K;
   long blocks = (n + 255) / 256;
@@ -528,42 +545,26 @@ int launch_g_sparse(const KBasis& kb, int kd, int64_t batch, int64_t n_in, int64
 }
 
 // The sparse G with the base branch's feature silu(x) as basis function K: partials of K + 1 sums
-// per (o, i) (plan sparse_g_plan(..., K + 1)), split into dc and dw by the reduction.
+// per (o, i) (plan sparse_g_plan(..., K + 1)) and, with db, the bias gradient's slice partials
+// after them (nz x n_out floats at ws + part); the reduction splits them into dc, dw and db.
 template <typename T>
 int launch_g_sparse_base(const KBasis& kb, int kd, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
-                         const void* g, void* dc, void* dw, void* ws, hipStream_t s) {
+                         const void* g, void* dc, void* dw, void* db, void* ws, hipStream_t s) {
   const SpG sp = sparse_g_plan(batch, n_in, n_out, kb.K + 1);
   const dim3 grid((unsigned)((n_in + 3) / 4), (unsigned)((n_out + 63) / 64), (unsigned)sp.nz);
   if (kb.K + 1 > kSpKMax) return fail(KF_EINVAL, "G sparse: base feature needs K < %d", kSpKMax);
-  int rc = with_spline_degree(kd, [&](auto tag) {
-    constexpr int KD = decltype(tag)::value;
-    if (kb.K + 1 <= 8)
-      hipLaunchKernelGGL((g_sparse_kernel<T, KD, 8>), grid, dim3(256), 0, s, kb, (int)batch, (int)n_in, (int)n_out,
-                         sp.RS, (const T*)x, (const T*)g, (const T*)nullptr, (float*)ws, kb.K + 1);
-    else
-      hipLaunchKernelGGL((g_sparse_kernel<T, KD, kSpKMax>), grid, dim3(256), 0, s, kb, (int)batch, (int)n_in,
-                         (int)n_out, sp.RS, (const T*)x, (const T*)g, (const T*)nullptr, (float*)ws, kb.K + 1);
-    return check_launch("G sparse");
-  });
+  float* bpart = db ? (float*)((char*)ws + sp.part) : nullptr;
+  int rc = launch_g_sparse_kernel<T>(kb, kd, grid, batch, n_in, n_out, sp.RS, x, g, nullptr, (float*)ws, kb.K + 1,
+                                     bpart, s);
   if (rc) return rc;
-  const long n = (long)n_out * n_in * (kb.K + 1);
+  const long n = (long)n_out * n_in * (kb.K + 1) + (db ? n_out : 0);
   long blocks = (n + 255) / 256;
   if (blocks > 4096) blocks = 4096;
   hipLaunchKernelGGL(g_sparse_reduce_base<T>, dim3((unsigned)blocks), dim3(256), 0, s, sp.nz, (long)n_out * n_in, kb.K,
-                     (const float*)ws, (T*)dc, (T*)dw);
+                     (const float*)ws, (T*)dc, (T*)dw, (int)n_out, (const float*)bpart, (T*)db);
   return check_launch("G sparse reduce");
 }
 
-// c' (n_out, n_in, K + 1) = the coefficients with W[o, i] after each (o, i)'s K (sparse base branch)
-template <typename T>
-int launch_coef_with_base(int64_t n_out, int64_t n_in, int K, const void* c, const void* w, void* out, hipStream_t s) {
-  const long n = (long)n_out * n_in * (K + 1);
-  long blocks = (n + 255) / 256;
-  if (blocks > 4096) blocks = 4096;
-  hipLaunchKernelGGL(coef_with_base_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, s, (int)n_out, (int)n_in, K,
-                     (const T*)c, (const T*)w, (T*)out);
-  return check_launch("coefficients with base");
-}
 
 template <typename T>
 __global__ void fill_zero_kernel(T* p, long n) {

@@ -450,17 +450,14 @@ int kf_F_base(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t
   const size_t need = sparse   ? ws_base_sparse(KF_OP_F_BASE, b, dtype, batch, n_in, n_out)
                       : spline ? ws_f_base_bspline(b, dtype, batch, n_in, n_out).total
                                : ws_f(b, dtype, batch, n_in, n_out, false, true).total;
-  if (!workspace || workspace_bytes < need)
+  if (need && (!workspace || workspace_bytes < need))
     return fail(KF_EWORKSPACE, "kf_F_base: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
-  if (reinterpret_cast<uintptr_t>(workspace) & 255)
+  if (need && (reinterpret_cast<uintptr_t>(workspace) & 255))
     return fail(KF_EWORKSPACE, "kf_F_base: workspace must be 256-byte aligned");
   KBasis kb = to_kbasis(b);
-  if (sparse) {  // float32: W as basis function K of the sparse route, the bias in its stores
-    hipStream_t s = (hipStream_t)stream;
-    rc = launch_coef_with_base<float>(n_out, n_in, kb.K, c, base_w, workspace, s);
-    if (rc) return rc;
-    return launch_f_sparse<float>(kb, b->spline_k, batch, n_in, n_out, x, nullptr, workspace, y, s, kb.K + 1, bias);
-  }
+  if (sparse)  // float32: W as basis function K of the sparse route, the bias in its stores
+    return launch_f_sparse<float>(kb, b->spline_k, batch, n_in, n_out, x, nullptr, c, y, (hipStream_t)stream, base_w,
+                                  bias);
   if (spline) return run_F_base_bspline(kb, b, batch, n_in, n_out, x, c, base_w, bias, y, workspace, (hipStream_t)stream);
   return run_F_base(kb, b, dtype, batch, n_in, n_out, x, c, base_w, bias, y, workspace, (hipStream_t)stream);
 }

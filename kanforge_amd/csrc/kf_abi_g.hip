@@ -328,14 +328,11 @@ int kf_G_base(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t
   if (reinterpret_cast<uintptr_t>(workspace) & 255)
     return fail(KF_EWORKSPACE, "kf_G_base: workspace must be 256-byte aligned");
   KBasis kb = to_kbasis(b);
-  if (sparse) {  // float32: silu(x) as basis function K of the sparse G, the bias from kf_column_sums
-    hipStream_t s = (hipStream_t)stream;
+  if (sparse) {  // float32: silu(x) as basis function K of the sparse G, the bias gradient beside it
+    if (dc || dbase_w)
+      return launch_g_sparse_base<float>(kb, b->spline_k, batch, n_in, n_out, x, g, dc, dbase_w, dbias, workspace,
+                                         (hipStream_t)stream);
     const size_t part = sparse_g_plan(batch, n_in, n_out, kb.K + 1).part;
-    if (dc || dbase_w) {
-      rc = launch_g_sparse_base<float>(kb, b->spline_k, batch, n_in, n_out, x, g, dc, dbase_w, workspace, s);
-      if (rc) return rc;
-    }
-    if (!dbias) return KF_OK;
     return kf_column_sums(dtype, batch, n_out, g, dbias, (char*)workspace + part, need - part, stream);
   }
   return run_G_base(kb, b, dtype, batch, n_in, n_out, x, g, dc, dbase_w, dbias, workspace, (hipStream_t)stream);

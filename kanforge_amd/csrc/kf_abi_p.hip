@@ -298,17 +298,13 @@ int kf_P_base(const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t
   const bool sparse = bspline_sparse(b, dtype);
   const size_t need = sparse ? ws_base_sparse(KF_OP_P_BASE, b, dtype, batch, n_in, n_out)
                              : ws_p_base(b, dtype, batch, n_in, n_out).total;
-  if (!workspace || workspace_bytes < need)
+  if (need && (!workspace || workspace_bytes < need))
     return fail(KF_EWORKSPACE, "kf_P_base: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
-  if (reinterpret_cast<uintptr_t>(workspace) & 255)
+  if (need && (reinterpret_cast<uintptr_t>(workspace) & 255))
     return fail(KF_EWORKSPACE, "kf_P_base: workspace must be 256-byte aligned");
   KBasis kb = to_kbasis(b);
-  if (sparse) {  // float32: W as basis function K of the sparse route
-    hipStream_t s = (hipStream_t)stream;
-    rc = launch_coef_with_base<float>(n_out, n_in, kb.K, c, base_w, workspace, s);
-    if (rc) return rc;
-    return launch_p_sparse<float>(kb, b->spline_k, batch, n_in, n_out, x, g, workspace, p, s, kb.K + 1);
-  }
+  if (sparse)  // float32: W as basis function K of the sparse route
+    return launch_p_sparse<float>(kb, b->spline_k, batch, n_in, n_out, x, g, c, p, (hipStream_t)stream, base_w);
   return run_P_base(kb, b, dtype, batch, n_in, n_out, x, g, c, base_w, p, workspace, (hipStream_t)stream);
 }
 

@@ -56,38 +56,44 @@ __device__ __forceinline__ int bspline_window(float x, float w, int i, const KBa
 // The windows of the rows' next 64 inputs are computed once into LDS; the coefficients of kSpIC
 // inputs x K x 64 outputs are staged in LDS per chunk, the next chunk's loads in flight (registers)
 // while the current one is contracted.
-// Base branch (KC = K + 1): c holds K + 1 values per (o, i), the last the base weight W[o, i],
-// whose feature silu(x) is staged next to the windows; y starts from bias[o] when given.
+// Base branch (bw given): the base weight W[o, i] is staged as each (o, i)'s basis function K
+// (LDS rows KC = K + 1 apart), its feature silu(x) next to the windows; y starts from bias[o]
+// when given.
 template <typename T, int KD>
 __global__ __launch_bounds__(512) void f_sparse_kernel(KBasis bs, int B, int IN, int OUT, const T* __restrict__ x,
                                                        const T* __restrict__ w, const T* __restrict__ c,
-                                                       T* __restrict__ y, int KC, const T* __restrict__ bias) {
+                                                       T* __restrict__ y, const T* __restrict__ bw,
+                                                       const T* __restrict__ bias) {
   constexpr int NW = 8, RQ = kSpRows / NW, WCH = 64;
-  constexpr int PF = (kSpIC * (kSpKMax + 1) * 64 + 511) / 512;  // staged values per thread, at most
+  constexpr int PF = (kSpIC * kSpKMax * 64 + 511) / 512;  // staged coefficients per thread, at most
+  static_assert(kSpIC == 8, "the base weights of a chunk: one per thread of an output's 8");
   __shared__ float cs[kSpIC * (kSpKMax + 1)][kSpLane];
   __shared__ int ss[kSpRows][WCH];
   __shared__ float vs[kSpRows][WCH][KD + 1];
   __shared__ float svs[kSpRows][WCH];  // silu(x) of the base branch (KC > K)
   const int K = bs.K;
-  const bool base = KC > K;
+  const bool base = bw != nullptr;
+  const int KC = base ? K + 1 : K;
+  const float inv_k = 1.f / (float)K;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int b0 = blockIdx.x * kSpRows, o0 = blockIdx.y * 64, o = o0 + lane;
   const int no = OUT - o0 < 64 ? OUT - o0 : 64;
   float acc[RQ];
 #pragma unroll
   for (int q = 0; q < RQ; ++q) acc[q] = 0.f;
-  float pre[PF];
+  float pre[PF], wpre = 0.f;
   // staging map without divisions: output row ol = tid / 8 of the chunk, values r = tid % 8 + 8 u
-  // of its contiguous run of ni K coefficients
+  // of its contiguous run of ni K coefficients (and, with the base branch, W[ol][i0 + tid % 8])
   const int sol = threadIdx.x >> 3, sr = threadIdx.x & 7;
   auto fetch = [&](int i0) {
-    const int per_o = (IN - i0 < kSpIC ? IN - i0 : kSpIC) * KC;
-    const T* src = c + ((size_t)(o0 + sol) * IN + i0) * KC;
+    const int ni = IN - i0 < kSpIC ? IN - i0 : kSpIC, per_o = ni * K;
+    const T* src = c + ((size_t)(o0 + sol) * IN + i0) * K;
 #pragma unroll
     for (int u = 0; u < PF; ++u) {
       const int r = sr + 8 * u;
       pre[u] = (sol < no && r < per_o) ? to_f32(src[r]) : 0.f;
     }
+    if (base) wpre = (sol < no && sr < ni) ? to_f32(bw[(size_t)(o0 + sol) * IN + i0 + sr]) : 0.f;
   };
   for (int w0 = 0; w0 < IN; w0 += WCH) {
     const int nw = IN - w0 < WCH ? IN - w0 : WCH;
@@ -112,13 +118,17 @@ __global__ __launch_bounds__(512) void f_sparse_kernel(KBasis bs, int B, int IN,
     }
     fetch(w0);
     for (int i0 = w0; i0 < w0 + nw; i0 += kSpIC) {
-      const int ni = IN - i0 < kSpIC ? IN - i0 : kSpIC, per_o = ni * KC;
+      const int ni = IN - i0 < kSpIC ? IN - i0 : kSpIC, per_o = ni * K;
       __syncthreads();
 #pragma unroll
       for (int u = 0; u < PF; ++u) {
         const int r = sr + 8 * u;
-        if (sol < no && r < per_o) cs[r][sol] = pre[u];
+        // with the base branch, value r (input r / K, function r % K) goes to row r + r / K;
+        // (r + 1/2) / K is at least 1 / (2 K) from an integer, so the float quotient is exact
+        const int row = base ? r + (int)(((float)r + 0.5f) * inv_k) : r;
+        if (sol < no && r < per_o) cs[row][sol] = pre[u];
       }
+      if (base && sol < no && sr < ni) cs[sr * KC + K][sol] = wpre;
       __syncthreads();
       if (i0 + kSpIC < w0 + nw) fetch(i0 + kSpIC);
       const int ib = i0 - w0;
@@ -150,19 +160,20 @@ __global__ __launch_bounds__(512) void f_sparse_kernel(KBasis bs, int B, int IN,
 // lane keeps its rows' windows in registers; the coefficients of kSpOC outputs x K x 64 inputs and
 // the rows' g values are staged in LDS per chunk (next chunk prefetched into registers);
 // h_r = sum_o g c[o, i, s0 + r], then p = sum_r V_r h_r.
-// Base branch (KC = K + 1): the last of each (o, i)'s K + 1 coefficients is W[o, i]; hb = sum_o g W
-// accumulates next to h and p gets silu'(x) hb.
+// Base branch (bw given): W[o, i] is staged as each (o, i)'s basis function K (LDS rows KC = K + 1
+// apart); hb = sum_o g W accumulates next to h and p gets silu'(x) hb.
 template <typename T, int KD>
 __global__ __launch_bounds__(512, 4) void p_sparse_kernel(KBasis bs, int B, int IN, int OUT, const T* __restrict__ x,
                                                        const T* __restrict__ g, const T* __restrict__ c,
-                                                       T* __restrict__ p, int KC) {
+                                                       T* __restrict__ p, const T* __restrict__ bw) {
   constexpr int NW = 8, RQ = kSpRows / NW;
-  constexpr int PF = kSpKMax + 1;  // one (output, input)'s KC coefficients per thread (kSpOC = NW)
+  constexpr int PF = kSpKMax + 1;  // one (output, input)'s K coefficients and W per thread (kSpOC = NW)
   static_assert(kSpOC == NW, "P stages one output per wave");
   __shared__ float cs[kSpOC * (kSpKMax + 1)][kSpLane];
   __shared__ float gs[kSpRows][kSpOC];
   const int K = bs.K;
-  const bool base = KC > K;
+  const bool base = bw != nullptr;
+  const int KC = base ? K + 1 : K;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int b0 = blockIdx.x * kSpRows, i0 = blockIdx.y * 64, i = i0 + lane;
   const int ni = IN - i0 < 64 ? IN - i0 : 64;
@@ -171,9 +182,11 @@ __global__ __launch_bounds__(512, 4) void p_sparse_kernel(KBasis bs, int B, int 
   // (oc0 + ol, i0 + il)
   auto fetch = [&](int oc0) {
     const int no = OUT - oc0 < kSpOC ? OUT - oc0 : kSpOC;
-    const T* src = c + ((size_t)(oc0 + wave) * IN + i0 + lane) * KC;
+    const size_t oi = (size_t)(oc0 + wave) * IN + i0 + lane;
+    const T* src = c + oi * K;
+    const bool in = wave < no && lane < ni;
 #pragma unroll
-    for (int u = 0; u < PF; ++u) pre[u] = (wave < no && lane < ni && u < KC) ? to_f32(src[u]) : 0.f;
+    for (int u = 0; u < PF; ++u) pre[u] = (in && u < K) ? to_f32(src[u]) : (in && u == K && base ? to_f32(bw[oi]) : 0.f);
     if (threadIdx.x < kSpRows * kSpOC) {
       const int rr = threadIdx.x / kSpOC, ol = threadIdx.x % kSpOC, b = b0 + rr;
       gpre = (b < B && ol < no) ? to_f32(g[(size_t)b * OUT + oc0 + ol]) : 0.f;
@@ -237,18 +250,21 @@ __global__ __launch_bounds__(512, 4) void p_sparse_kernel(KBasis bs, int B, int 
 // non-finite x) in the wave's LDS slot; every row then costs KM broadcast reads and KM FMAs per
 // lane, with the loads of sixteen rows' g in flight at once.
 // Base branch (KO = K + 1 <= KM): feature K is silu(x), so part holds K + 1 sums per (o, i), the
-// last the base weight's gradient.
+// last the base weight's gradient; with bpart, the lanes of input 0 also sum g over the slice's
+// rows into bpart[z][o] (the bias gradient's slice partials).
 template <typename T, int KD, int KM>
 __global__ __launch_bounds__(256) void g_sparse_kernel(KBasis bs, int B, int IN, int OUT, int RS,
                                                        const T* __restrict__ x, const T* __restrict__ g,
-                                                       const T* __restrict__ w, float* __restrict__ part, int KO) {
+                                                       const T* __restrict__ w, float* __restrict__ part, int KO,
+                                                       float* __restrict__ bpart) {
   __shared__ float phi[4][64][KM];
   const int K = bs.K;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int i = blockIdx.x * 4 + wave, o = blockIdx.y * 64 + lane;
   const bool live = i < IN && o < OUT;
   const int z = blockIdx.z, r0 = z * RS, r1 = min(B, r0 + RS);
-  float acc[KM];
+  const bool bsum = bpart != nullptr && i == 0;
+  float acc[KM], bacc = 0.f;
 #pragma unroll
   for (int k = 0; k < KM; ++k) acc[k] = 0.f;
   for (int bb = r0; bb < r1; bb += 64) {
@@ -287,6 +303,7 @@ __global__ __launch_bounds__(256) void g_sparse_kernel(KBasis bs, int B, int IN,
           if (j0 + u >= nb) break;
 #pragma unroll
           for (int k = 0; k < KM; ++k) acc[k] = fmaf(gb[u], phi[wave][j0 + u][k], acc[k]);
+          if (bsum) bacc += gb[u];
         }
       }
     }
@@ -296,16 +313,26 @@ __global__ __launch_bounds__(256) void g_sparse_kernel(KBasis bs, int B, int IN,
 #pragma unroll
     for (int k = 0; k < KM; ++k)
       if (k < KO) dst[k] = acc[k];
+    if (bsum) bpart[(size_t)z * OUT + o] = bacc;
   }
 }
 
 // The base branch's G partials (K + 1 sums per (o, i), the last dW): dc[o][i][k] and dw[o][i] =
-// sum_z part[z][o][i][.] (slice order: deterministic); dc or dw may be NULL.
+// sum_z part[z][o][i][.], and with db, db[o] = sum_z bpart[z][o] (slice order: deterministic);
+// dc or dw may be NULL.
 template <typename T>
 __global__ __launch_bounds__(256) void g_sparse_reduce_base(int nz, long n_oi, int K, const float* __restrict__ part,
-                                                            T* __restrict__ dc, T* __restrict__ dw) {
-  const long n = n_oi * (K + 1);
-  for (long e = blockIdx.x * 256L + threadIdx.x; e < n; e += (long)gridDim.x * 256) {
+                                                            T* __restrict__ dc, T* __restrict__ dw, int n_out,
+                                                            const float* __restrict__ bpart, T* __restrict__ db) {
+  const long n = n_oi * (K + 1), n_all = n + (db ? n_out : 0);
+  for (long e = blockIdx.x * 256L + threadIdx.x; e < n_all; e += (long)gridDim.x * 256) {
+    if (e >= n) {
+      const int o = (int)(e - n);
+      float s = 0.f;
+      for (int q = 0; q < nz; ++q) s += bpart[(size_t)q * n_out + o];
+      db[o] = from_f32<T>(s);
+      continue;
+    }
     float s = 0.f;
     for (int q = 0; q < nz; ++q) s += part[(size_t)q * n + e];
     const long oi = e / (K + 1);
@@ -315,18 +342,6 @@ __global__ __launch_bounds__(256) void g_sparse_reduce_base(int nz, long n_oi, i
     } else if (dw) {
       dw[oi] = from_f32<T>(s);
     }
-  }
-}
-
-// c' (OUT, IN, K + 1): each (o, i)'s K coefficients, then W[o, i] (the sparse kernels' base branch)
-template <typename T>
-__global__ __launch_bounds__(256) void coef_with_base_kernel(int OUT, int IN, int K, const T* __restrict__ c,
-                                                             const T* __restrict__ w, T* __restrict__ out) {
-  const long n = (long)OUT * IN * (K + 1);
-  for (long e = blockIdx.x * 256L + threadIdx.x; e < n; e += (long)gridDim.x * 256) {
-    const long oi = e / (K + 1);
-    const int k = (int)(e - oi * (K + 1));
-    out[e] = k < K ? c[oi * K + k] : w[oi];
   }
 }
 
