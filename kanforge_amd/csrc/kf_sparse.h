@@ -67,6 +67,7 @@ __global__ __launch_bounds__(512) void f_sparse_kernel(KBasis bs, int B, int IN,
   constexpr int NW = 8, RQ = kSpRows / NW, WCH = 64;
   constexpr int PF = (kSpIC * kSpKMax * 64 + 511) / 512;  // staged coefficients per thread, at most
   static_assert(kSpIC == 8, "the base weights of a chunk: one per thread of an output's 8");
+  static_assert(WCH % kSpIC == 0, "windows of whole chunks");
   __shared__ float cs[kSpIC * (kSpKMax + 1)][kSpLane];
   __shared__ int ss[kSpRows][WCH];
   __shared__ float vs[kSpRows][WCH][KD + 1];
@@ -95,6 +96,7 @@ __global__ __launch_bounds__(512) void f_sparse_kernel(KBasis bs, int B, int IN,
     }
     if (base) wpre = (sol < no && sr < ni) ? to_f32(bw[(size_t)(o0 + sol) * IN + i0 + sr]) : 0.f;
   };
+  fetch(0);  // the first chunk's loads in flight while the windows are computed
   for (int w0 = 0; w0 < IN; w0 += WCH) {
     const int nw = IN - w0 < WCH ? IN - w0 : WCH;
     __syncthreads();
@@ -116,7 +118,6 @@ __global__ __launch_bounds__(512) void f_sparse_kernel(KBasis bs, int B, int IN,
 #pragma unroll
       for (int r = 0; r <= KD; ++r) vs[rr][il][r] = V[r];
     }
-    fetch(w0);
     for (int i0 = w0; i0 < w0 + nw; i0 += kSpIC) {
       const int ni = IN - i0 < kSpIC ? IN - i0 : kSpIC, per_o = ni * K;
       __syncthreads();
@@ -130,7 +131,8 @@ __global__ __launch_bounds__(512) void f_sparse_kernel(KBasis bs, int B, int IN,
       }
       if (base && sol < no && sr < ni) cs[sr * KC + K][sol] = wpre;
       __syncthreads();
-      if (i0 + kSpIC < w0 + nw) fetch(i0 + kSpIC);
+      // the next chunk, also across windows (they are whole chunks: WCH = 8 kSpIC)
+      if (i0 + kSpIC < IN) fetch(i0 + kSpIC);
       const int ib = i0 - w0;
 #pragma unroll
       for (int il = 0; il < kSpIC; ++il) {
@@ -169,7 +171,9 @@ __global__ __launch_bounds__(512, 4) void p_sparse_kernel(KBasis bs, int B, int 
   constexpr int NW = 8, RQ = kSpRows / NW;
   constexpr int PF = kSpKMax + 1;  // one (output, input)'s K coefficients and W per thread (kSpOC = NW)
   static_assert(kSpOC == NW, "P stages one output per wave");
-  __shared__ float cs[kSpOC * (kSpKMax + 1)][kSpLane];
+  // rows of 64: a wave writes one row at a time, and reads rows that differ per lane (each
+  // lane's own window), which a 64-float stride keeps on distinct banks
+  __shared__ float cs[kSpOC * (kSpKMax + 1)][64];
   __shared__ float gs[kSpRows][kSpOC];
   const int K = bs.K;
   const bool base = bw != nullptr;
@@ -192,6 +196,7 @@ __global__ __launch_bounds__(512, 4) void p_sparse_kernel(KBasis bs, int B, int 
       gpre = (b < B && ol < no) ? to_f32(g[(size_t)b * OUT + oc0 + ol]) : 0.f;
     }
   };
+  fetch(0);  // the first chunk's loads in flight while the windows are computed
   int s0[RQ];
   float V[RQ][KD + 1], h[RQ][KD + 1], hb[RQ], xq[RQ];
 #pragma unroll
@@ -206,7 +211,6 @@ __global__ __launch_bounds__(512, 4) void p_sparse_kernel(KBasis bs, int B, int 
       bspline_window<KD>(xq[q], 1.f, i, bs, s0[q], V[q]);
     }
   }
-  fetch(0);
   for (int oc0 = 0; oc0 < OUT; oc0 += kSpOC) {
     const int no = OUT - oc0 < kSpOC ? OUT - oc0 : kSpOC;
     __syncthreads();
