@@ -482,6 +482,22 @@ int with_spline_degree(int kd, Fn&& fn) {
   }
 }
 
+// The small-layer P's dense feature count for kc = K (+ 1 with the base branch) features, or 0
+// where the staged sparse P runs (a side above 128, or more than 12 features)
+inline int small_km(int64_t n_in, int64_t n_out, int kc) {
+  if (n_in > 128 || n_out > 128) return 0;
+  return kc <= 8 ? 8 : kc <= 9 ? 9 : kc <= 12 ? 12 : 0;
+}
+template <typename Fn>
+void with_small_km(int km, Fn&& fn) {
+  if (km == 8)
+    fn(std::integral_constant<int, 8>{});
+  else if (km == 9)
+    fn(std::integral_constant<int, 9>{});
+  else
+    fn(std::integral_constant<int, 12>{});
+}
+
 template <typename T>
 int launch_f_sparse(const KBasis& kb, int kd, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* w,
                     const void* c, void* y, hipStream_t s, const void* bw = nullptr, const void* bias = nullptr) {
@@ -500,6 +516,17 @@ int launch_p_sparse(const KBasis& kb, int kd, int64_t batch, int64_t n_in, int64
                     const void* c, void* p, hipStream_t s, const void* bw = nullptr) {
   const dim3 grid((unsigned)((batch + kSpRows - 1) / kSpRows), (unsigned)((n_in + 63) / 64));
   if (bw && kb.K + 1 > kSpKMax) return fail(KF_EINVAL, "P sparse: base weight needs K < %d", kSpKMax);
+  static_assert(kSmRows == kSpRows, "one grid for both P kernels");
+  if (const int km = small_km(n_in, n_out, kb.K + (bw ? 1 : 0)))
+    return with_spline_degree(kd, [&](auto tag) {
+      constexpr int KD = decltype(tag)::value;
+      with_small_km(km, [&](auto kmc) {
+        constexpr int KM = decltype(kmc)::value;
+        hipLaunchKernelGGL((p_small_kernel<T, KD, KM>), grid, dim3(512), 0, s, kb, (int)batch, (int)n_in, (int)n_out,
+                           (const T*)x, (const T*)g, (const T*)c, (T*)p, (const T*)bw);
+      });
+      return check_launch("P small");
+    });
   return with_spline_degree(kd, [&](auto tag) {
     constexpr int KD = decltype(tag)::value;
     hipLaunchKernelGGL((p_sparse_kernel<T, KD>), grid, dim3(512), 0, s, kb, (int)batch, (int)n_in, (int)n_out,

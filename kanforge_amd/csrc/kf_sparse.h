@@ -67,9 +67,9 @@ __global__ __launch_bounds__(512) void f_sparse_kernel(KBasis bs, int B, int IN,
   constexpr int NW = 8, RQ = kSpRows / NW, WCH = 64;
   constexpr int PF = (kSpIC * kSpKMax * 64 + 511) / 512;  // staged coefficients per thread, at most
   static_assert(kSpIC == 8, "the base weights of a chunk: one per thread of an output's 8");
-  static_assert(WCH % kSpIC == 0, "windows of whole chunks");
+  static_assert(WCH % kSpIC == 0 && kSpIC == 8, "windows of whole chunks, read as two int4");
   __shared__ float cs[kSpIC * (kSpKMax + 1)][kSpLane];
-  __shared__ int ss[kSpRows][WCH];
+  __shared__ __align__(16) int ss[kSpRows][WCH];
   __shared__ float vs[kSpRows][WCH][KD + 1];
   __shared__ float svs[kSpRows][WCH];  // silu(x) of the base branch (KC > K)
   const int K = bs.K;
@@ -100,7 +100,12 @@ __global__ __launch_bounds__(512) void f_sparse_kernel(KBasis bs, int B, int IN,
   for (int w0 = 0; w0 < IN; w0 += WCH) {
     const int nw = IN - w0 < WCH ? IN - w0 : WCH;
     __syncthreads();
-    for (int e = threadIdx.x; e < kSpRows * WCH; e += 512) {
+    static_assert(kSpRows * WCH % 512 == 0, "whole passes of the workgroup");
+    // unrolled: the passes' knot-table reads (x, then the knots around it, then the padded
+    // knots) are dependent chains, which the two passes then run side by side
+#pragma unroll
+    for (int t = 0; t < kSpRows * WCH / 512; ++t) {
+      const int e = threadIdx.x + 512 * t;
       const int rr = e / WCH, il = e % WCH, b = b0 + rr, i = w0 + il;
       int s0 = 0;
       float V[KD + 1];
@@ -119,7 +124,6 @@ __global__ __launch_bounds__(512) void f_sparse_kernel(KBasis bs, int B, int IN,
       for (int r = 0; r <= KD; ++r) vs[rr][il][r] = V[r];
     }
     for (int i0 = w0; i0 < w0 + nw; i0 += kSpIC) {
-      const int ni = IN - i0 < kSpIC ? IN - i0 : kSpIC, per_o = ni * K;
       __syncthreads();
 #pragma unroll
       for (int u = 0; u < PF; ++u) {
@@ -127,20 +131,31 @@ __global__ __launch_bounds__(512) void f_sparse_kernel(KBasis bs, int B, int IN,
         // with the base branch, value r (input r / K, function r % K) goes to row r + r / K;
         // (r + 1/2) / K is at least 1 / (2 K) from an integer, so the float quotient is exact
         const int row = base ? r + (int)(((float)r + 0.5f) * inv_k) : r;
-        if (sol < no && r < per_o) cs[row][sol] = pre[u];
+        // the whole chunk's rows, zeros past its ni inputs (fetch leaves them 0), so that the
+        // contraction below runs over all kSpIC inputs without a data-dependent exit
+        if (r < kSpIC * K) cs[row][sol] = pre[u];
       }
-      if (base && sol < no && sr < ni) cs[sr * KC + K][sol] = wpre;
+      if (base) cs[sr * KC + K][sol] = wpre;
       __syncthreads();
       // the next chunk, also across windows (they are whole chunks: WCH = 8 kSpIC)
       if (i0 + kSpIC < IN) fetch(i0 + kSpIC);
       const int ib = i0 - w0;
+      // the chunk's window starts first, then the contraction: inputs past ni have V = 0 and
+      // silu 0 from the window pass (they lie past nw) and zero coefficient rows
+      int s0q[RQ][kSpIC];
+#pragma unroll
+      for (int q = 0; q < RQ; ++q) {
+        const int4* sp = reinterpret_cast<const int4*>(&ss[wave + NW * q][ib]);
+        const int4 a = sp[0], b = sp[1];
+        s0q[q][0] = a.x, s0q[q][1] = a.y, s0q[q][2] = a.z, s0q[q][3] = a.w;
+        s0q[q][4] = b.x, s0q[q][5] = b.y, s0q[q][6] = b.z, s0q[q][7] = b.w;
+      }
 #pragma unroll
       for (int il = 0; il < kSpIC; ++il) {
-        if (il >= ni) break;
 #pragma unroll
         for (int q = 0; q < RQ; ++q) {
           const int rr = wave + NW * q;
-          const int row = il * KC + ss[rr][ib + il];
+          const int row = il * KC + s0q[q][il];
 #pragma unroll
           for (int r = 0; r <= KD; ++r) acc[q] = fmaf(vs[rr][ib + il][r], cs[row + r][lane], acc[q]);
           if (base) acc[q] = fmaf(svs[rr][ib + il], cs[il * KC + K][lane], acc[q]);
@@ -244,6 +259,133 @@ __global__ __launch_bounds__(512, 4) void p_sparse_kernel(KBasis bs, int B, int 
       for (int r = 0; r <= KD; ++r) acc = fmaf(V[q][r], h[q][r], acc);
       if (base) acc = fmaf(dsilu_f(xq[q]), hb[q], acc);
       if (b < B) p[(size_t)b * IN + i] = from_f32<T>(acc);
+    }
+  }
+}
+
+// P for small layers (in and out <= 128, K [+ 1] <= 12): a workgroup = kSmRows rows x 64 inputs
+// (lanes) whose 8 waves split the outputs. Each lane holds the coefficients of its 8 (output,
+// input) pairs of the current 64-wide output group in registers (one load per group, in flight
+// during the window pass; lanes read neighbouring inputs' runs); the rows' derivative windows sit
+// in LDS as dense rows of KM features (zeros outside the window; with the base branch, silu'(x)
+// as function K), and the waves' partial sums are added in wave order at the end. Dense over the
+// features (KM + 1 FMAs per row, input and output instead of k + 2), for one window pass and two
+// barriers per 64 outputs instead of eight staged chunks. (The same shape for F, lanes =
+// outputs, reads rows IN K apart per lane, 64 cache lines per load, and lost to the staged F.)
+constexpr int kSmRows = 16;
+// dense-row stride in floats: whole float4s, and not a multiple of 8, so that the per-lane rows
+// of P's reads (one row per lane, 16 bytes at a time) fall on distinct banks
+template <int KM>
+struct SmPad {
+  static constexpr int q = (KM + 3) / 4 * 4;
+  static constexpr int value = q % 8 == 0 ? q + 4 : q;
+};
+
+// the dense row of one (row, input): V at s0 .. s0 + KD, extra at K when with_extra, else zeros
+template <int KD, int KP>
+__device__ __forceinline__ void sm_dense_row(float* dst, int K, int s0, const float (&V)[KD + 1], bool with_extra,
+                                             float extra) {
+#pragma unroll
+  for (int k4 = 0; k4 < KP / 4; ++k4) {
+    float v4[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int k = 4 * k4 + u;
+      float v = 0.f;
+#pragma unroll
+      for (int r = 0; r <= KD; ++r) v = (k == s0 + r) ? V[r] : v;
+      v4[u] = k < K ? v : (with_extra && k == K ? extra : 0.f);
+    }
+    reinterpret_cast<float4*>(dst)[k4] = make_float4(v4[0], v4[1], v4[2], v4[3]);
+  }
+}
+
+template <typename T, int KD, int KM>
+__global__ __launch_bounds__(512) void p_small_kernel(KBasis bs, int B, int IN, int OUT, const T* __restrict__ x,
+                                                      const T* __restrict__ g, const T* __restrict__ c,
+                                                      T* __restrict__ p, const T* __restrict__ bw) {
+  constexpr int NW = 8, R = kSmRows, KP = SmPad<KM>::value, OCH = 64, OPW = OCH / NW;
+  constexpr int PH = R * 64 * KP, RED = NW * R * 64;
+  __shared__ __align__(16) float lds[PH > RED ? PH : RED];
+  __shared__ __align__(16) float gs[R * OCH];
+  const int K = bs.K;
+  const bool base = bw != nullptr;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int b0 = blockIdx.x * R, i0 = blockIdx.y * 64, i = i0 + lane;
+  float cr[OPW][KM];
+  auto load_coef = [&](int o0) {
+#pragma unroll
+    for (int j = 0; j < OPW; ++j) {
+      const int o = o0 + wave * OPW + j;
+      const bool in = i < IN && o < OUT;
+      const size_t oi = (size_t)o * IN + i;
+#pragma unroll
+      for (int k = 0; k < KM; ++k)
+        cr[j][k] = (in && k < K) ? to_f32(c[oi * K + k]) : ((in && base && k == K) ? to_f32(bw[oi]) : 0.f);
+    }
+  };
+  load_coef(0);  // in flight during the window pass
+#pragma unroll
+  for (int t = 0; t < R * 64 / 512; ++t) {  // unrolled: the passes' dependent knot reads side by side
+    const int e = threadIdx.x + 512 * t;
+    const int rr = e / 64, il = e % 64, b = b0 + rr, ii = i0 + il;
+    int s0 = 0;
+    float V[KD + 1];
+#pragma unroll
+    for (int r = 0; r <= KD; ++r) V[r] = 0.f;
+    float sd = 0.f;
+    if (b < B && ii < IN) {
+      const float xv = to_f32(x[(size_t)b * IN + ii]);
+      bspline_window<KD>(xv, 1.f, ii, bs, s0, V);
+      sd = dsilu_f(xv);
+    }
+    sm_dense_row<KD, KP>(lds + (size_t)e * KP, K, s0, V, base, sd);
+  }
+  float acc[R];
+#pragma unroll
+  for (int q = 0; q < R; ++q) acc[q] = 0.f;
+  for (int o0 = 0; o0 < OUT; o0 += OCH) {
+    if (o0 > 0) load_coef(o0);
+    __syncthreads();  // the windows are written; the previous group's g readers are done
+    for (int e = threadIdx.x; e < R * OCH; e += 512) {
+      const int rr = e / OCH, ol = e % OCH, b = b0 + rr, o = o0 + ol;
+      gs[e] = (b < B && o < OUT) ? to_f32(g[(size_t)b * OUT + o]) : 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < R; ++q) {
+      const float4* ph = reinterpret_cast<const float4*>(lds + (size_t)(q * 64 + lane) * KP);
+      float f[(KM + 3) / 4 * 4];
+#pragma unroll
+      for (int k4 = 0; k4 < (KM + 3) / 4; ++k4) {
+        const float4 v = ph[k4];
+        f[4 * k4] = v.x;
+        f[4 * k4 + 1] = v.y;
+        f[4 * k4 + 2] = v.z;
+        f[4 * k4 + 3] = v.w;
+      }
+      float a = acc[q];
+#pragma unroll
+      for (int j = 0; j < OPW; ++j) {
+        float t = 0.f;
+#pragma unroll
+        for (int k = 0; k < KM; ++k) t = fmaf(f[k], cr[j][k], t);
+        a = fmaf(gs[q * OCH + wave * OPW + j], t, a);
+      }
+      acc[q] = a;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < R; ++q) lds[(wave * R + q) * 64 + lane] = acc[q];
+  __syncthreads();
+  for (int e = threadIdx.x; e < R * 64; e += 512) {
+    const int q = e / 64, l = e % 64, b = b0 + q, ii = i0 + l;
+    if (b < B && ii < IN) {
+      float sum = 0.f;
+#pragma unroll
+      for (int v = 0; v < NW; ++v) sum += lds[(v * R + q) * 64 + l];
+      p[(size_t)b * IN + ii] = from_f32<T>(sum);
     }
   }
 }

@@ -293,11 +293,11 @@ def test_G_bias_is_G_plus_column_sums(name, basis, dtype, B, IN, OUT):
     assert err <= (1e-5 if dtype == torch.float32 else 1e-2), err
 
 
-@pytest.mark.parametrize("B,IN,OUT,grid,k", [(4096, 64, 64, 5, 3), (333, 70, 45, 8, 3), (200, 40, 33, 5, 1)])
+@pytest.mark.parametrize("B,IN,OUT,grid,k", [(4096, 64, 64, 5, 3), (333, 70, 45, 8, 3), (200, 40, 33, 5, 1), (300, 200, 150, 5, 3)])
 def test_fused_sparse_float32_layer_against_oracle(B, IN, OUT, grid, k):
     """float32 B-splines on the sparse route: W as basis function K (feature silu(x)) in F, P and
-    G, the bias in F's stores; the first shape is the 64 -> 64 benchmark layer, the others ragged
-    and of degree 1. Tolerance: float32 normwise 1e-5."""
+    G, the bias in F's stores; the first shape is the 64 -> 64 benchmark layer (the small-layer
+    kernels, like the next two: ragged, degree 1), the last runs the staged kernels (sides above 128). Tolerance: float32 normwise 1e-5."""
     torch.manual_seed(4)
     layer = KANLinear(IN, OUT, kf.BSpline(grid, k, grid_range=(-2.0, 2.0)))
     with torch.no_grad():
