@@ -14,7 +14,8 @@
  *    (no strides); the caller owns every buffer. The library never
  *    allocates, frees or synchronises.
  *  - Work that needs scratch memory takes a caller-provided workspace of at
- *    least kf_workspace_bytes(...) bytes (256-byte aligned).
+ *    least kf_workspace_bytes(...) bytes (256-byte aligned); where that size is
+ *    0 the workspace may be NULL.
  *  - `stream` is a hipStream_t (passed as void*); every launch is ordered on it.
  *  - Return value: 0 on success, a negative KF_E* code otherwise; the text
  *    of the last error of the calling thread is kf_last_error().
@@ -186,9 +187,11 @@ int kf_P(const kf_basis *basis, int dtype, int64_t batch, int64_t n_in, int64_t 
  * kf_base_fused(op, ...) is 1 when the entry point of op (KF_OP_F_BASE, KF_OP_P_BASE,
  * KF_OP_G_BASE) takes the layer, 0 when the caller composes kf_F / kf_P / kf_G with its own base
  * branch instead, negative for an invalid descriptor. It takes bf16 Chebyshev plans on their
- * contraction kernels (F: n_t of 9 or an even count >= 6) and bf16 B-spline plans (P: cubic with
- * 11 basis functions), not the narrow streaming routes. Workspace: kf_workspace_bytes(KF_OP_*_BASE,
- * ...).
+ * contraction kernels (F: n_t of 9 or an even count >= 6), bf16 B-spline plans (P: cubic with
+ * 11 basis functions) and float32 B-spline plans with fewer than 16 basis functions (the sparse
+ * route, base weight as basis function K), not the narrow streaming routes. Workspace:
+ * kf_workspace_bytes(KF_OP_*_BASE, ...) (0, workspace may be NULL, for F and P on the sparse
+ * route).
  *
  * kf_F_base: y = F_0(x, c) + silu(x) base_w^T + bias, basis of order 0; base_w (n_out, n_in),
  *   bias (n_out) or NULL. silu(x) is one more feature per input in the same contraction (B-splines:
