@@ -329,3 +329,38 @@ def test_fused_sparse_float32_layer_against_oracle(B, IN, OUT, grid, k):
         print(f"  {key}: {err:.3e}", flush=True)
         assert err <= 1e-5, (key, err)
 
+
+
+def test_sparse_base_entries_take_a_null_workspace():
+    """On the float32 sparse route kf_F_base and kf_P_base need no workspace
+    (kf_workspace_bytes is 0): called through the C ABI with NULL they give the same bits as with
+    one (the same kernels)."""
+    import ctypes
+
+    from kanforge_amd.torch import _lib
+
+    torch.manual_seed(5)
+    B, IN, OUT = 333, 64, 48
+    layer = KANLinear(IN, OUT, kf.BSpline(5, 3)).to(DEV)
+    pl, st = layer._plan, layer._basis_state()
+    x = (torch.rand(B, IN, device=DEV) * 2 - 1).contiguous()
+    g = torch.randn(B, OUT, device=DEV).contiguous()
+    c, bw, bias = (t.detach().contiguous() for t in (layer.coef, layer.base_weight, layer.bias))
+    lib = _lib.load()
+    d0, _k0 = K._desc(pl, 0, st)
+    d1, _k1 = K._desc(pl, 1, st)
+    for op, d in ((_lib.KF_OP_F_BASE, d0), (_lib.KF_OP_P_BASE, d1)):
+        assert lib.kf_workspace_bytes(op, ctypes.byref(d), _lib.KF_F32, B, IN, OUT) == 0
+    stream = torch.cuda.current_stream().cuda_stream
+    y = torch.empty(B, OUT, device=DEV)
+    p = torch.empty(B, IN, device=DEV)
+    print(f"null workspace case B={B} in={IN} out={OUT}", flush=True)
+    rc = lib.kf_F_base(ctypes.byref(d0), _lib.KF_F32, B, IN, OUT, x.data_ptr(), c.data_ptr(), bw.data_ptr(),
+                       bias.data_ptr(), y.data_ptr(), None, 0, stream)
+    assert rc == 0, lib.kf_last_error()
+    rc = lib.kf_P_base(ctypes.byref(d1), _lib.KF_F32, B, IN, OUT, x.data_ptr(), g.data_ptr(), c.data_ptr(),
+                       bw.data_ptr(), p.data_ptr(), None, 0, stream)
+    assert rc == 0, lib.kf_last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(y, K._f_base_raw(pl, st, x, c, bw, bias))
+    assert torch.equal(p, K._p_base_raw(pl, st, x, g, c, bw))
