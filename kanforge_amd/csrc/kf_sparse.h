@@ -463,6 +463,21 @@ __global__ __launch_bounds__(256) void g_sparse_kernel(KBasis bs, int B, int IN,
   }
 }
 
+// sum_q p[q * stride] for q < nz, added in q order; the loads eight at a time in flight
+__device__ __forceinline__ float slice_sum(const float* __restrict__ p, size_t stride, int nz) {
+  float s = 0.f;
+  int q = 0;
+  for (; q + 8 <= nz; q += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = p[(size_t)(q + u) * stride];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s += v[u];
+  }
+  for (; q < nz; ++q) s += p[(size_t)q * stride];
+  return s;
+}
+
 // The base branch's G partials (K + 1 sums per (o, i), the last dW): dc[o][i][k] and dw[o][i] =
 // sum_z part[z][o][i][.], and with db, db[o] = sum_z bpart[z][o] (slice order: deterministic);
 // dc or dw may be NULL.
@@ -474,13 +489,11 @@ __global__ __launch_bounds__(256) void g_sparse_reduce_base(int nz, long n_oi, i
   for (long e = blockIdx.x * 256L + threadIdx.x; e < n_all; e += (long)gridDim.x * 256) {
     if (e >= n) {
       const int o = (int)(e - n);
-      float s = 0.f;
-      for (int q = 0; q < nz; ++q) s += bpart[(size_t)q * n_out + o];
+      const float s = slice_sum(bpart + o, (size_t)n_out, nz);
       db[o] = from_f32<T>(s);
       continue;
     }
-    float s = 0.f;
-    for (int q = 0; q < nz; ++q) s += part[(size_t)q * n + e];
+    const float s = slice_sum(part + e, (size_t)n, nz);
     const long oi = e / (K + 1);
     const int k = (int)(e - oi * (K + 1));
     if (k < K) {
@@ -496,9 +509,7 @@ template <typename T>
 __global__ __launch_bounds__(256) void g_sparse_reduce(int nz, long n, const float* __restrict__ part,
                                                        T* __restrict__ dc) {
   for (long e = blockIdx.x * 256L + threadIdx.x; e < n; e += (long)gridDim.x * 256) {
-    float s = 0.f;
-    for (int q = 0; q < nz; ++q) s += part[(size_t)q * n + e];
-    dc[e] = from_f32<T>(s);
+    dc[e] = from_f32<T>(slice_sum(part + e, (size_t)n, nz));
   }
 }
 
