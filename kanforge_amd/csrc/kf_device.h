@@ -137,6 +137,21 @@ __device__ __forceinline__ void cheb_folded(const KBasis& b, const float* T, flo
   }
 }
 
+// sum_q p[q * stride] for q < nz, added in q order; the loads eight at a time in flight
+__device__ __forceinline__ float slice_sum(const float* __restrict__ p, size_t stride, int nz) {
+  float s = 0.f;
+  int q = 0;
+  for (; q + 8 <= nz; q += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = p[(size_t)(q + u) * stride];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s += v[u];
+  }
+  for (; q < nz; ++q) s += p[(size_t)q * stride];
+  return s;
+}
+
 // ---------------------------------------------------------------------------
 // B-splines. Knot vector of input i: t_0 .. t_{n_knots-1} (real), stored with
 // spline_k padding knots per side: kp[r] = t_{r - spline_k}.

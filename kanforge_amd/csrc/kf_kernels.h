@@ -1058,9 +1058,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_J * 64) void g_kernel(KBasis bs, int
 // threads reading consecutive floats of every split.
 static __global__ __launch_bounds__(kThreads) void g_split_sum(long n, int nz, size_t zstride, float* __restrict__ part) {
   for (long t = blockIdx.x * (long)kThreads + threadIdx.x; t < n; t += (long)gridDim.x * kThreads) {
-    float sum = 0.f;
-    for (int z = 0; z < nz; ++z) sum += part[(size_t)z * zstride + t];
-    part[t] = sum;
+    part[t] = slice_sum(part + t, zstride, nz);
   }
 }
 

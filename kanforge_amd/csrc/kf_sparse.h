@@ -463,21 +463,6 @@ __global__ __launch_bounds__(256) void g_sparse_kernel(KBasis bs, int B, int IN,
   }
 }
 
-// sum_q p[q * stride] for q < nz, added in q order; the loads eight at a time in flight
-__device__ __forceinline__ float slice_sum(const float* __restrict__ p, size_t stride, int nz) {
-  float s = 0.f;
-  int q = 0;
-  for (; q + 8 <= nz; q += 8) {
-    float v[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = p[(size_t)(q + u) * stride];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) s += v[u];
-  }
-  for (; q < nz; ++q) s += p[(size_t)q * stride];
-  return s;
-}
-
 // The base branch's G partials (K + 1 sums per (o, i), the last dW): dc[o][i][k] and dw[o][i] =
 // sum_z part[z][o][i][.], and with db, db[o] = sum_z bpart[z][o] (slice order: deterministic);
 // dc or dw may be NULL.
