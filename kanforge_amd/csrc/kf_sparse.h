@@ -313,15 +313,30 @@ __global__ __launch_bounds__(512) void p_small_kernel(KBasis bs, int B, int IN, 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int b0 = blockIdx.x * R, i0 = blockIdx.y * 64, i = i0 + lane;
   float cr[OPW][KM];
+  // whole float4s of each (o, i)'s K coefficients when K is a multiple of 4 and c is 16-byte
+  // aligned (a quarter of the load instructions; every lane reads its own run)
+  const bool vec4 = std::is_same<T, float>::value && (K & 3) == 0 && (reinterpret_cast<uintptr_t>(c) & 15) == 0;
   auto load_coef = [&](int o0) {
 #pragma unroll
     for (int j = 0; j < OPW; ++j) {
       const int o = o0 + wave * OPW + j;
       const bool in = i < IN && o < OUT;
       const size_t oi = (size_t)o * IN + i;
+      const float wv = (in && base) ? to_f32(bw[oi]) : 0.f;
+      if (vec4) {
 #pragma unroll
-      for (int k = 0; k < KM; ++k)
-        cr[j][k] = (in && k < K) ? to_f32(c[oi * K + k]) : ((in && base && k == K) ? to_f32(bw[oi]) : 0.f);
+        for (int k4 = 0; k4 < (KM + 3) / 4; ++k4) {
+          float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+          if (in && 4 * k4 < K) v = *reinterpret_cast<const float4*>(c + oi * K + 4 * k4);
+          const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            if (4 * k4 + u < KM) cr[j][4 * k4 + u] = 4 * k4 + u < K ? vv[u] : (4 * k4 + u == K ? wv : 0.f);
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < KM; ++k) cr[j][k] = (in && k < K) ? to_f32(c[oi * K + k]) : (k == K ? wv : 0.f);
+      }
     }
   };
   load_coef(0);  // in flight during the window pass
