@@ -567,7 +567,8 @@ int launch_g_sparse(const KBasis& kb, int kd, int64_t batch, int64_t n_in, int64
   const long n = (long)n_out * n_in * kb.K;
   long blocks = (n + 255) / 256;
   if (blocks > 4096) blocks = 4096;
-  hipLaunchKernelGGL(g_sparse_reduce<T>, dim3((unsigned)blocks), dim3(256), 0, s, sp.nz, n, (const float*)ws, (T*)dc);
+  hipLaunchKernelGGL(g_sparse_reduce<T>, dim3((unsigned)blocks), dim3(256), 0, s, sp.nz, (int)n_in, (int)n_out, kb.K,
+                     kb.K, (const float*)ws, (T*)dc, (T*)nullptr, (const float*)nullptr, (T*)nullptr);
   return check_launch("G sparse reduce");
 }
 
@@ -587,8 +588,8 @@ int launch_g_sparse_base(const KBasis& kb, int kd, int64_t batch, int64_t n_in, 
   const long n = (long)n_out * n_in * (kb.K + 1) + (db ? n_out : 0);
   long blocks = (n + 255) / 256;
   if (blocks > 4096) blocks = 4096;
-  hipLaunchKernelGGL(g_sparse_reduce_base<T>, dim3((unsigned)blocks), dim3(256), 0, s, sp.nz, (long)n_out * n_in, kb.K,
-                     (const float*)ws, (T*)dc, (T*)dw, (int)n_out, (const float*)bpart, (T*)db);
+  hipLaunchKernelGGL(g_sparse_reduce<T>, dim3((unsigned)blocks), dim3(256), 0, s, sp.nz, (int)n_in, (int)n_out, kb.K,
+                     kb.K + 1, (const float*)ws, (T*)dc, (T*)dw, (const float*)bpart, (T*)db);
   return check_launch("G sparse reduce");
 }
 

@@ -86,13 +86,27 @@ __global__ __launch_bounds__(512) void f_sparse_kernel(KBasis bs, int B, int IN,
   // staging map without divisions: output row ol = tid / 8 of the chunk, values r = tid % 8 + 8 u
   // of its contiguous run of ni K coefficients (and, with the base branch, W[ol][i0 + tid % 8])
   const int sol = threadIdx.x >> 3, sr = threadIdx.x & 7;
+  // with K a multiple of 4 (float c, 16-byte aligned) each thread moves whole float4s: values
+  // r = 4 sr + 32 (u / 4) + u % 4, a quarter of the load instructions; else r = sr + 8 u
+  const bool vec4 = std::is_same<T, float>::value && (K & 3) == 0 && (reinterpret_cast<uintptr_t>(c) & 15) == 0;
+  static_assert(PF % 4 == 0, "whole float4s per thread");
   auto fetch = [&](int i0) {
     const int ni = IN - i0 < kSpIC ? IN - i0 : kSpIC, per_o = ni * K;
     const T* src = c + ((size_t)(o0 + sol) * IN + i0) * K;
+    if (vec4) {
 #pragma unroll
-    for (int u = 0; u < PF; ++u) {
-      const int r = sr + 8 * u;
-      pre[u] = (sol < no && r < per_o) ? to_f32(src[r]) : 0.f;
+      for (int u4 = 0; u4 < PF / 4; ++u4) {
+        const int r = 4 * sr + 32 * u4;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (sol < no && r < per_o) v = *reinterpret_cast<const float4*>(src + r);
+        pre[4 * u4] = v.x, pre[4 * u4 + 1] = v.y, pre[4 * u4 + 2] = v.z, pre[4 * u4 + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < PF; ++u) {
+        const int r = sr + 8 * u;
+        pre[u] = (sol < no && r < per_o) ? to_f32(src[r]) : 0.f;
+      }
     }
     if (base) wpre = (sol < no && sr < ni) ? to_f32(bw[(size_t)(o0 + sol) * IN + i0 + sr]) : 0.f;
   };
@@ -127,7 +141,7 @@ __global__ __launch_bounds__(512) void f_sparse_kernel(KBasis bs, int B, int IN,
       __syncthreads();
 #pragma unroll
       for (int u = 0; u < PF; ++u) {
-        const int r = sr + 8 * u;
+        const int r = vec4 ? 4 * sr + 32 * (u >> 2) + (u & 3) : sr + 8 * u;
         // with the base branch, value r (input r / K, function r % K) goes to row r + r / K;
         // (r + 1/2) / K is at least 1 / (2 K) from an integer, so the float quotient is exact
         const int row = base ? r + (int)(((float)r + 0.5f) * inv_k) : r;
@@ -406,7 +420,7 @@ __global__ __launch_bounds__(512) void p_small_kernel(KBasis bs, int B, int IN, 
 }
 
 // G partial sums over a slice of rows: workgroup = 4 inputs (one per wave) x 64 outputs (lane)
-// x rows [z RS, (z + 1) RS); part[z][o][i][k] (float, K per (o, i)). For 64 rows at a time each
+// x rows [z RS, (z + 1) RS); part[z][i][k][o] (float, K per (i, o)). For 64 rows at a time each
 // lane turns its row's window into the row's KM features (zeros outside the window, all NaN for a
 // non-finite x) in the wave's LDS slot; every row then costs KM broadcast reads and KM FMAs per
 // lane, with the loads of sixteen rows' g in flight at once.
@@ -470,46 +484,40 @@ __global__ __launch_bounds__(256) void g_sparse_kernel(KBasis bs, int B, int IN,
     }
   }
   if (live) {
-    float* dst = part + (((size_t)z * OUT + o) * IN + i) * KO;
+    // part[z][i][k][o]: a wave's 64 lanes (outputs) store 256 contiguous bytes per k
+    float* dst = part + ((size_t)z * IN + i) * KO * OUT + o;
 #pragma unroll
     for (int k = 0; k < KM; ++k)
-      if (k < KO) dst[k] = acc[k];
+      if (k < KO) dst[(size_t)k * OUT] = acc[k];
     if (bsum) bpart[(size_t)z * OUT + o] = bacc;
   }
 }
 
-// The base branch's G partials (K + 1 sums per (o, i), the last dW): dc[o][i][k] and dw[o][i] =
-// sum_z part[z][o][i][.], and with db, db[o] = sum_z bpart[z][o] (slice order: deterministic);
-// dc or dw may be NULL.
+// G's slice partials part[z][i][k][o] (KO sums per (input, output), outputs contiguous) summed in
+// slice order (deterministic): dc[o][i][k] for k < K and, with KO = K + 1, dw[o][i] for k = K;
+// with db, db[o] = sum_z bpart[z][o]. dc or dw may be NULL. Reads run along the partials' layout;
+// each sum is written once, to its place in dc.
 template <typename T>
-__global__ __launch_bounds__(256) void g_sparse_reduce_base(int nz, long n_oi, int K, const float* __restrict__ part,
-                                                            T* __restrict__ dc, T* __restrict__ dw, int n_out,
-                                                            const float* __restrict__ bpart, T* __restrict__ db) {
-  const long n = n_oi * (K + 1), n_all = n + (db ? n_out : 0);
+__global__ __launch_bounds__(256) void g_sparse_reduce(int nz, int IN, int OUT, int K, int KO,
+                                                       const float* __restrict__ part, T* __restrict__ dc,
+                                                       T* __restrict__ dw, const float* __restrict__ bpart,
+                                                       T* __restrict__ db) {
+  const long n = (long)IN * KO * OUT, n_all = n + (db ? OUT : 0);
   for (long e = blockIdx.x * 256L + threadIdx.x; e < n_all; e += (long)gridDim.x * 256) {
     if (e >= n) {
       const int o = (int)(e - n);
-      const float s = slice_sum(bpart + o, (size_t)n_out, nz);
-      db[o] = from_f32<T>(s);
+      db[o] = from_f32<T>(slice_sum(bpart + o, (size_t)OUT, nz));
       continue;
     }
     const float s = slice_sum(part + e, (size_t)n, nz);
-    const long oi = e / (K + 1);
-    const int k = (int)(e - oi * (K + 1));
+    const long t = e / OUT;
+    const int o = (int)(e - t * OUT), i = (int)(t / KO), k = (int)(t - (long)i * KO);
+    const size_t oi = (size_t)o * IN + i;
     if (k < K) {
       if (dc) dc[oi * K + k] = from_f32<T>(s);
     } else if (dw) {
       dw[oi] = from_f32<T>(s);
     }
-  }
-}
-
-// dc[e] = sum_z part[z][e] over nz slices, e < n (float sums in slice order: deterministic).
-template <typename T>
-__global__ __launch_bounds__(256) void g_sparse_reduce(int nz, long n, const float* __restrict__ part,
-                                                       T* __restrict__ dc) {
-  for (long e = blockIdx.x * 256L + threadIdx.x; e < n; e += (long)gridDim.x * 256) {
-    dc[e] = from_f32<T>(slice_sum(part + e, (size_t)n, nz));
   }
 }
 
