@@ -464,7 +464,10 @@ inline WsGBias ws_g_bias(const kf_basis* b, int dtype, int64_t batch, int64_t n_
   WsGBias w;
   const WsG L = ws_g(b, dtype, batch, n_in, n_out, has_w);
   w.g = L.total;
-  w.part = align256((size_t)((L.BP + 63) / 64) * L.OUTP * sizeof(float));
+  // the transpose's 64-row block partials, or the sparse G's slice partials of sum_b g
+  w.part = bspline_sparse(b, dtype)
+               ? align256((size_t)sparse_g_plan(batch, n_in, n_out, b->size).nz * n_out * sizeof(float))
+               : align256((size_t)((L.BP + 63) / 64) * L.OUTP * sizeof(float));
   w.sums = align256((size_t)L.OUTP * sizeof(float));
   w.cws = align256(kf_column_sums_workspace_bytes(batch, n_out));
   w.total = w.g + w.part + w.sums + w.cws;
@@ -557,18 +560,21 @@ int launch_g_sparse_kernel(const KBasis& kb, int kd, dim3 grid, int64_t batch, i
   });
 }
 
+// The sparse G; with db, also the bias gradient db = sum_b g from the same pass (the lanes of
+// input 0 sum g per slice into bpart, nz x n_out floats, which the reduction totals).
 template <typename T>
 int launch_g_sparse(const KBasis& kb, int kd, int64_t batch, int64_t n_in, int64_t n_out, const void* x, const void* g,
-                    const void* w, void* dc, void* ws, hipStream_t s) {
+                    const void* w, void* dc, void* ws, hipStream_t s, void* db = nullptr, float* bpart = nullptr) {
   const SpG sp = sparse_g_plan(batch, n_in, n_out, kb.K);
   const dim3 grid((unsigned)((n_in + 3) / 4), (unsigned)((n_out + 63) / 64), (unsigned)sp.nz);
-  int rc = launch_g_sparse_kernel<T>(kb, kd, grid, batch, n_in, n_out, sp.RS, x, g, w, (float*)ws, kb.K, nullptr, s);
+  if (!db) bpart = nullptr;
+  int rc = launch_g_sparse_kernel<T>(kb, kd, grid, batch, n_in, n_out, sp.RS, x, g, w, (float*)ws, kb.K, bpart, s);
   if (rc) return rc;
-  const long n = (long)n_out * n_in * kb.K;
+  const long n = (long)n_out * n_in * kb.K + (bpart ? n_out : 0);
   long blocks = (n + 255) / 256;
   if (blocks > 4096) blocks = 4096;
   hipLaunchKernelGGL(g_sparse_reduce<T>, dim3((unsigned)blocks), dim3(256), 0, s, sp.nz, (int)n_in, (int)n_out, kb.K,
-                     kb.K, (const float*)ws, (T*)dc, (T*)nullptr, (const float*)nullptr, (T*)nullptr);
+                     kb.K, (const float*)ws, (T*)dc, (T*)nullptr, (const float*)bpart, (T*)(bpart ? db : nullptr));
   return check_launch("G sparse reduce");
 }
 

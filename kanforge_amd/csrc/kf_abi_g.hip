@@ -116,13 +116,17 @@ int launch_g_dma(const WsG& L, hipStream_t s, const KBasis& kb, int64_t n_in, in
 template <typename T>
 // dbias (dtype, n_out) or NULL: the column sums of g, taken from the transpose's block partials
 // (bias_part / bias_sums: (BP / 64, OUTP) and OUTP floats after G's own workspace, unless the
-// Chebyshev layout already has them), which sets *dbias_done; the sparse route leaves it to the
-// caller.
+// Chebyshev layout already has them), which sets *dbias_done; the sparse route sums g per row
+// slice beside its partials (bias_part: nz x n_out floats) and sets it too.
 int run_G(const KBasis& kb, const kf_basis* b, int dtype, int64_t batch, int64_t n_in, int64_t n_out, const void* x,
           const void* g, const void* w, void* dc, void* ws, hipStream_t s, void* dbias = nullptr,
           float* bias_part = nullptr, float* bias_sums = nullptr, bool* dbias_done = nullptr) {
   if constexpr (sizeof(T) == 4)
-    if (bspline_sparse(b, dtype)) return launch_g_sparse<T>(kb, b->spline_k, batch, n_in, n_out, x, g, w, dc, ws, s);
+    if (bspline_sparse(b, dtype)) {
+      const int rc = launch_g_sparse<T>(kb, b->spline_k, batch, n_in, n_out, x, g, w, dc, ws, s, dbias, bias_part);
+      if (!rc && dbias && bias_part && dbias_done) *dbias_done = true;
+      return rc;
+    }
   const bool cheb_kind = kb.kind == KF_KIND_CHEB;
   const bool weighted = features_weighted(b, w);
   WsG L = ws_g(b, dtype, batch, n_in, n_out, weighted);

@@ -266,7 +266,7 @@ G_BIAS_CASES = [
     ("bspline83", kf.BSpline(8, 3), torch.bfloat16, 257, 64, 130),  # GEMM core route
     ("rational", kf.Rational(5, 4), torch.bfloat16, 300, 128, 96),  # GEMM core route
     ("cheb8_f32", kf.Chebyshev(8), torch.float32, 333, 96, 200),
-    ("bspline53_f32", kf.BSpline(5, 3), torch.float32, 4096, 64, 64),  # sparse route: kf_column_sums
+    ("bspline53_f32", kf.BSpline(5, 3), torch.float32, 4096, 64, 64),  # sparse route: G's slice sums of g
 ]
 
 
